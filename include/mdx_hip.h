@@ -1,0 +1,164 @@
+/*
+ * mdx_hip.h — C ABI of the MI355X (gfx950) SOAP library.
+ *
+ * This is the drop-in boundary for MDescriptor's SOAP hot path.  It carries
+ * plain pointers and sizes only (no C++ or torch types), and no C++
+ * exception crosses it: every entry point returns a status code and
+ * mdx_hip_last_error() describes the last failure on a context.
+ *
+ * Each declaration names the reference interface it replaces
+ * (nicheal/MDescriptor, paths relative to the repository root).
+ *
+ * Threading: one call at a time per context (a mutex inside the context
+ * serialises callers); separate contexts are independent.  Ownership: the
+ * caller owns every host buffer it passes; a context owns its device
+ * buffers, its HIP stream and its pinned staging memory.
+ */
+#ifndef MDX_HIP_H
+#define MDX_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  The Python plugin maps them onto the reference's error
+ * families (src/mdescriptor/core/errors.py:215-248): OUT_OF_MEMORY ->
+ * MemoryError ("backend_out_of_memory"), DEVICE_UNAVAILABLE -> ImportError
+ * ("device_unavailable"), INVALID_ARGUMENT -> ValueError
+ * (DescriptorInputError at the adapter), CANCELLED -> the plugin's
+ * cancellation type (cpp/include/mdescriptor/detail/control.hpp:10-13). */
+enum {
+    MDX_OK = 0,
+    MDX_INVALID_ARGUMENT = 1,
+    MDX_OUT_OF_MEMORY = 2,
+    MDX_DEVICE_UNAVAILABLE = 3,
+    MDX_CANCELLED = 4,
+    MDX_INTERNAL = 5
+};
+
+/* Flattened structure batch, the same five arrays and two counts as
+ * StructureBatchView (cpp/include/mdescriptor/detail/batch.hpp:9-17):
+ * numbers i32[atoms], positions f64[atoms*3] (C order), cells
+ * f64[structures*9] (rows are lattice vectors), pbc i32[structures*3],
+ * offsets i64[structures+1].  Pointers are host pointers. */
+typedef struct mdx_batch_view {
+    const int32_t* numbers;
+    const double* positions;
+    const double* cells;
+    const int32_t* pbc;
+    const int64_t* offsets;
+    int64_t structures;
+    int64_t atoms;
+} mdx_batch_view;
+
+/* SOAP parameters: the GTO subset of SoapOptions
+ * (cpp/include/mdescriptor/descriptor.hpp:17-43).  alphas f64[(l_max+1)*n_max]
+ * and betas f64[(l_max+1)*n_max*n_max] (index (l*n_max + n)*n_max + k) are the
+ * orthonormalised radial basis computed by the caller, exactly as the
+ * reference passes them to C++ (src/mdescriptor/descriptors/_kernels/core.py:
+ * 237-240) and to its CUDA plugin (core.py:331-355).  They are copied. */
+typedef struct mdx_soap_params {
+    const int32_t* species; /* declared order, unique, positive */
+    int32_t n_species;
+    int32_t n_max;
+    int32_t l_max;
+    double r_cut;
+    double sigma;
+    const double* alphas;
+    const double* betas;
+    int32_t average;   /* 0 "off", 1 "inner", 2 "outer" */
+    int32_t out_dtype; /* bytes per output value: 4 (float32) or 8 (float64) */
+} mdx_soap_params;
+
+/* Per-stage device times of the last run, from HIP events recorded on the
+ * context's stream around each stage. */
+typedef struct mdx_timing {
+    double graph_ms;     /* cell binning + neighbour count/scan/fill (kernel 1) */
+    double expansion_ms; /* per-centre expansion + power spectrum + write (kernels 2-4) */
+    double finalize_ms;  /* structure-level average reductions (kernel 4), 0 if off */
+    double total_ms;     /* first to last event of the device pipeline */
+    double h2d_ms;       /* host-to-device copies (mdx_hip_soap_compute only) */
+    double d2h_ms;       /* device-to-host copy of the result (mdx_hip_soap_compute only) */
+    int64_t pairs;       /* neighbour pairs found at the padded SOAP cutoff */
+    int64_t binned;      /* periodic images binned into the cell grid */
+    int64_t expansion_launches; /* launches of the expansion kernel in the run */
+} mdx_timing;
+
+typedef struct mdx_hip_ctx mdx_hip_ctx;
+typedef struct mdx_soap_plan mdx_soap_plan;
+typedef struct mdx_device_batch mdx_device_batch;
+
+/* Context on one HIP device: stream, device arena, pinned staging.
+ * Replaces CudaExecutionContext (cpp/cuda/include/mdescriptor/cuda/context.hpp:27-78)
+ * and the lazy device selection of Backend (cpp/cuda/src/backend.cu:338-356). */
+int mdx_hip_create(int device, mdx_hip_ctx** out);
+void mdx_hip_destroy(mdx_hip_ctx* ctx);
+
+/* Last error message on this context ("" when none).  Replaces the
+ * exception text of check_cuda (cpp/cuda/include/mdescriptor/cuda/error.hpp:15-30). */
+const char* mdx_hip_last_error(const mdx_hip_ctx* ctx);
+
+/* Validated, device-resident SOAP plan (prefactors, beta, feature table).
+ * Replaces SoapCalculator(SoapOptions) + prepare_soap
+ * (cpp/src/standalone/soap.cpp:507-572, 1248) and the CUDA payload upload
+ * (cpp/cuda/src/extended_descriptors_soap.cuh:898-906).  *features receives
+ * the feature count (soap.cpp:373-387). */
+int mdx_hip_soap_plan_create(mdx_hip_ctx* ctx, const mdx_soap_params* params, mdx_soap_plan** out,
+                             int64_t* features);
+void mdx_hip_soap_plan_destroy(mdx_soap_plan* plan);
+
+/* Rows of the result for this plan and batch: structures when averaging,
+ * else atoms (soap.cpp:1216-1217, 1240-1243). */
+int64_t mdx_hip_soap_rows(const mdx_soap_plan* plan, const mdx_batch_view* batch);
+
+/* Full compute: validate, upload, run, download into out_host
+ * (rows x features values of out_dtype, row stride out_pitch_bytes).
+ * Replaces SoapCalculator::compute (soap.cpp:1254-1258) as called through
+ * compute_soap_array (cpp/src/bindings/module.cpp:431-452), and the CUDA
+ * Backend::compute SOAP path (cpp/cuda/src/backend.cu:338-631 ->
+ * extended_descriptors_soap.cuh:799-1125).  cancel_flag (nullable) is polled
+ * between stages and launches; a non-zero value returns MDX_CANCELLED.
+ * timing (nullable) receives the stage times. */
+int mdx_hip_soap_compute(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, const mdx_batch_view* batch,
+                         void* out_host, int64_t out_rows, int64_t out_pitch_bytes,
+                         const volatile int32_t* cancel_flag, mdx_timing* timing);
+
+/* Device-resident path: upload and prepare a batch once ...
+ * (the H2D part of Backend::compute, cpp/cuda/src/backend.cu:353-356) */
+int mdx_hip_batch_upload(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, const mdx_batch_view* batch,
+                         mdx_device_batch** out);
+void mdx_hip_batch_destroy(mdx_device_batch* batch);
+
+/* ... then run the SOAP pipeline on it, writing into device memory out_device
+ * (rows x features, row stride out_pitch_bytes).  No host copy of the result;
+ * the call returns after the stream has finished.  Same computation as
+ * mdx_hip_soap_compute. */
+int mdx_hip_soap_run(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, mdx_device_batch* batch,
+                     void* out_device, int64_t out_pitch_bytes, const volatile int32_t* cancel_flag,
+                     mdx_timing* timing);
+
+/* Neighbour graph on the device, for parity and the pair-level API.
+ * Replaces build_neighbor_graph (cpp/src/common/neighbor.cpp:703-768) as
+ * exported by _native.build_neighbor_graph (cpp/src/bindings/module.cpp:887-935):
+ * CSR over all atoms of the batch, rows in the reference's candidate order,
+ * atom indices global to the batch, self pair and periodic self-images
+ * included, boundary inclusive when include_boundary != 0.
+ * mdx_hip_neighbors_build computes and keeps the graph on the context and
+ * returns its pair count; mdx_hip_neighbors_fetch copies it out into caller
+ * buffers: offsets i64[atoms+1], neighbors i32[pairs], shifts i32[pairs*3],
+ * displacements f64[pairs*3], distance2 f64[pairs] (any may be NULL). */
+int mdx_hip_neighbors_build(mdx_hip_ctx* ctx, const mdx_batch_view* batch, double cutoff,
+                            int32_t include_boundary, int64_t* pairs);
+int mdx_hip_neighbors_fetch(mdx_hip_ctx* ctx, int64_t* offsets, int32_t* neighbors, int32_t* shifts,
+                            double* displacements, double* distance2);
+
+/* Library version and build target, for diagnostics. */
+const char* mdx_hip_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MDX_HIP_H */

@@ -1,0 +1,452 @@
+"""The HIP plugin: a ctypes binding of ``_lib/libmdx_hip.so``.
+
+It mirrors the reference's CUDA plugin contract (``cpp/cuda/src/bindings.cu:
+15-57``): ``create_backend(name, options) -> Backend`` with
+``Backend.compute(batch, control) -> dict`` (``values``, ``level``,
+``row_offsets``, ``labels``, ``metadata``, ``_mdescriptor_owned_values``),
+``Backend.feature_count``, ``Backend.metadata()`` and ``Backend.close()``,
+plus ``MODEL_SNAPSHOT_ABI``.  The library's C ABI is declared in
+``include/mdx_hip.h``; ctypes releases the GIL around every call.
+
+Errors map onto the reference's families (``src/mdescriptor/core/errors.py:
+215-248``): a missing library or device raises :class:`HipUnavailable`
+(an ``ImportError``), device allocation failure :class:`HipOutOfMemory`
+(a ``MemoryError``), invalid input ``ValueError``, cancellation
+:class:`HipCancelledError`.  There is no CPU fallback: without the built
+library nothing here computes.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from collections.abc import Mapping
+from pathlib import Path
+from typing import Any
+
+import numpy as np
+
+MODEL_SNAPSHOT_ABI = 1
+LIBRARY_PATH = Path(__file__).resolve().parent / "_lib" / "libmdx_hip.so"
+
+MDX_OK = 0
+MDX_INVALID_ARGUMENT = 1
+MDX_OUT_OF_MEMORY = 2
+MDX_DEVICE_UNAVAILABLE = 3
+MDX_CANCELLED = 4
+MDX_INTERNAL = 5
+
+
+class HipUnavailable(ImportError):
+    """The HIP library or a HIP device is not available."""
+
+
+class HipOutOfMemory(MemoryError):
+    """A device allocation failed."""
+
+
+class HipCancelledError(RuntimeError):
+    """The computation was cancelled through its control."""
+
+
+class HipError(RuntimeError):
+    """An internal failure of the HIP backend."""
+
+
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_i64p = ctypes.POINTER(ctypes.c_int64)
+_f64p = ctypes.POINTER(ctypes.c_double)
+
+
+class BatchView(ctypes.Structure):
+    _fields_ = [
+        ("numbers", _i32p),
+        ("positions", _f64p),
+        ("cells", _f64p),
+        ("pbc", _i32p),
+        ("offsets", _i64p),
+        ("structures", ctypes.c_int64),
+        ("atoms", ctypes.c_int64),
+    ]
+
+
+class SoapParams(ctypes.Structure):
+    _fields_ = [
+        ("species", _i32p),
+        ("n_species", ctypes.c_int32),
+        ("n_max", ctypes.c_int32),
+        ("l_max", ctypes.c_int32),
+        ("r_cut", ctypes.c_double),
+        ("sigma", ctypes.c_double),
+        ("alphas", _f64p),
+        ("betas", _f64p),
+        ("average", ctypes.c_int32),
+        ("out_dtype", ctypes.c_int32),
+    ]
+
+
+class Timing(ctypes.Structure):
+    _fields_ = [
+        ("graph_ms", ctypes.c_double),
+        ("expansion_ms", ctypes.c_double),
+        ("finalize_ms", ctypes.c_double),
+        ("total_ms", ctypes.c_double),
+        ("h2d_ms", ctypes.c_double),
+        ("d2h_ms", ctypes.c_double),
+        ("pairs", ctypes.c_int64),
+        ("binned", ctypes.c_int64),
+        ("expansion_launches", ctypes.c_int64),
+    ]
+
+    def as_dict(self) -> dict[str, float]:
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+# Every symbol include/mdx_hip.h declares, with its ctypes signature.
+SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
+    "mdx_hip_create": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_void_p)]),
+    "mdx_hip_destroy": (None, [ctypes.c_void_p]),
+    "mdx_hip_last_error": (ctypes.c_char_p, [ctypes.c_void_p]),
+    "mdx_hip_soap_plan_create": (
+        ctypes.c_int,
+        [ctypes.c_void_p, ctypes.POINTER(SoapParams), ctypes.POINTER(ctypes.c_void_p), _i64p],
+    ),
+    "mdx_hip_soap_plan_destroy": (None, [ctypes.c_void_p]),
+    "mdx_hip_soap_rows": (ctypes.c_int64, [ctypes.c_void_p, ctypes.POINTER(BatchView)]),
+    "mdx_hip_soap_compute": (
+        ctypes.c_int,
+        [ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(BatchView), ctypes.c_void_p, ctypes.c_int64,
+         ctypes.c_int64, _i32p, ctypes.POINTER(Timing)],
+    ),
+    "mdx_hip_batch_upload": (
+        ctypes.c_int,
+        [ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(BatchView), ctypes.POINTER(ctypes.c_void_p)],
+    ),
+    "mdx_hip_batch_destroy": (None, [ctypes.c_void_p]),
+    "mdx_hip_soap_run": (
+        ctypes.c_int,
+        [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, _i32p,
+         ctypes.POINTER(Timing)],
+    ),
+    "mdx_hip_neighbors_build": (
+        ctypes.c_int,
+        [ctypes.c_void_p, ctypes.POINTER(BatchView), ctypes.c_double, ctypes.c_int32, _i64p],
+    ),
+    "mdx_hip_neighbors_fetch": (
+        ctypes.c_int,
+        [ctypes.c_void_p, _i64p, _i32p, _i32p, _f64p, _f64p],
+    ),
+    "mdx_hip_version": (ctypes.c_char_p, []),
+}
+
+_lock = threading.Lock()
+_library: Any = None
+
+
+def load_library() -> Any:
+    """Load the in-tree HIP library, or raise :class:`HipUnavailable`."""
+
+    global _library
+    with _lock:
+        if _library is not None:
+            return _library
+        if not LIBRARY_PATH.is_file():
+            raise HipUnavailable(
+                f"the HIP SOAP library is not built ({LIBRARY_PATH}); run `python -m mdescriptor_amd.build`"
+            )
+        try:
+            lib = ctypes.CDLL(str(LIBRARY_PATH))
+        except OSError as exc:
+            raise HipUnavailable(f"cannot load {LIBRARY_PATH.name}: {exc}") from exc
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _library = lib
+        return lib
+
+
+def _raise_for(status: int, message: str) -> None:
+    if status == MDX_OK:
+        return
+    if status == MDX_INVALID_ARGUMENT:
+        raise ValueError(message or "invalid argument")
+    if status == MDX_OUT_OF_MEMORY:
+        raise HipOutOfMemory(message or "HIP backend ran out of memory")
+    if status == MDX_DEVICE_UNAVAILABLE:
+        raise HipUnavailable(message or "HIP device unavailable")
+    if status == MDX_CANCELLED:
+        raise HipCancelledError(message or "descriptor computation was cancelled")
+    raise HipError(message or f"HIP backend failed with status {status}")
+
+
+class _BatchArrays:
+    """C-contiguous copies of a batch's five arrays and the ctypes view on them."""
+
+    def __init__(self, batch: Any) -> None:
+        self.numbers = np.ascontiguousarray(batch.numbers, dtype=np.int32)
+        self.positions = np.ascontiguousarray(batch.positions, dtype=np.float64).reshape(-1, 3)
+        self.cells = np.ascontiguousarray(batch.cells, dtype=np.float64).reshape(-1, 3, 3)
+        self.pbc = np.ascontiguousarray(batch.pbc, dtype=np.int32).reshape(-1, 3)
+        self.offsets = np.ascontiguousarray(batch.offsets, dtype=np.int64)
+        self.view = BatchView(
+            self.numbers.ctypes.data_as(_i32p),
+            self.positions.ctypes.data_as(_f64p),
+            self.cells.ctypes.data_as(_f64p),
+            self.pbc.ctypes.data_as(_i32p),
+            self.offsets.ctypes.data_as(_i64p),
+            len(self.offsets) - 1,
+            len(self.numbers),
+        )
+
+
+class Context:
+    """One HIP device context (stream, device arena, pinned staging)."""
+
+    def __init__(self, device: int = 0) -> None:
+        self.lib = load_library()
+        handle = ctypes.c_void_p()
+        status = self.lib.mdx_hip_create(int(device), ctypes.byref(handle))
+        _raise_for(status, (self.lib.mdx_hip_last_error(None) or b"").decode())
+        self.handle = handle
+        self.device = int(device)
+
+    def check(self, status: int) -> None:
+        if status != MDX_OK:
+            _raise_for(status, (self.lib.mdx_hip_last_error(self.handle) or b"").decode())
+
+    def close(self) -> None:
+        if getattr(self, "handle", None) is not None and self.handle.value:
+            self.lib.mdx_hip_destroy(self.handle)
+        self.handle = None
+
+    def __del__(self) -> None:  # pragma: no cover - interpreter shutdown order
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class SoapPlan:
+    """Device-resident SOAP plan on a context."""
+
+    def __init__(self, context: Context, *, species: Any, n_max: int, l_max: int, r_cut: float, sigma: float,
+                 alphas: np.ndarray, betas: np.ndarray, average: str, dtype: str) -> None:
+        self.context = context
+        self._species = np.ascontiguousarray(species, dtype=np.int32)
+        self._alphas = np.ascontiguousarray(alphas, dtype=np.float64).ravel()
+        self._betas = np.ascontiguousarray(betas, dtype=np.float64).ravel()
+        self.average = str(average)
+        self.dtype = np.dtype(dtype)
+        params = SoapParams(
+            self._species.ctypes.data_as(_i32p), len(self._species), int(n_max), int(l_max), float(r_cut),
+            float(sigma), self._alphas.ctypes.data_as(_f64p), self._betas.ctypes.data_as(_f64p),
+            {"off": 0, "inner": 1, "outer": 2}[self.average], int(self.dtype.itemsize),
+        )
+        handle = ctypes.c_void_p()
+        features = ctypes.c_int64()
+        context.check(context.lib.mdx_hip_soap_plan_create(context.handle, ctypes.byref(params),
+                                                           ctypes.byref(handle), ctypes.byref(features)))
+        self.handle = handle
+        self.features = int(features.value)
+
+    def rows(self, batch: Any) -> int:
+        return (len(batch.offsets) - 1) if self.average != "off" else len(batch.numbers)
+
+    def compute(self, batch: Any, cancel: ctypes.c_int32 | None = None) -> tuple[np.ndarray, dict[str, float]]:
+        arrays = _BatchArrays(batch)
+        rows = self.rows(batch)
+        out = np.empty((rows, self.features), dtype=self.dtype)
+        timing = Timing()
+        flag = ctypes.pointer(cancel) if cancel is not None else None
+        lib = self.context.lib
+        self.context.check(lib.mdx_hip_soap_compute(
+            self.context.handle, self.handle, ctypes.byref(arrays.view), out.ctypes.data_as(ctypes.c_void_p),
+            rows, out.strides[0] if rows > 0 else self.features * self.dtype.itemsize, flag, ctypes.byref(timing)))
+        return out, timing.as_dict()
+
+    def close(self) -> None:
+        if getattr(self, "handle", None) is not None and self.handle.value:
+            self.context.lib.mdx_hip_soap_plan_destroy(self.handle)
+        self.handle = None
+
+    def __del__(self) -> None:  # pragma: no cover
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class DeviceBatch:
+    """A batch validated, prepared and resident in HBM for one plan."""
+
+    def __init__(self, plan: SoapPlan, batch: Any) -> None:
+        self.plan = plan
+        self.arrays = _BatchArrays(batch)
+        self.rows = plan.rows(batch)
+        ctx = plan.context
+        handle = ctypes.c_void_p()
+        ctx.check(ctx.lib.mdx_hip_batch_upload(ctx.handle, plan.handle, ctypes.byref(self.arrays.view),
+                                               ctypes.byref(handle)))
+        self.handle = handle
+
+    def run(self, out_device_ptr: int, pitch_bytes: int, cancel: ctypes.c_int32 | None = None) -> dict[str, float]:
+        ctx = self.plan.context
+        timing = Timing()
+        flag = ctypes.pointer(cancel) if cancel is not None else None
+        ctx.check(ctx.lib.mdx_hip_soap_run(ctx.handle, self.plan.handle, self.handle, ctypes.c_void_p(out_device_ptr),
+                                           int(pitch_bytes), flag, ctypes.byref(timing)))
+        return timing.as_dict()
+
+    def close(self) -> None:
+        if getattr(self, "handle", None) is not None and self.handle.value:
+            self.plan.context.lib.mdx_hip_batch_destroy(self.handle)
+        self.handle = None
+
+    def __del__(self) -> None:  # pragma: no cover
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def neighbor_graph(context: Context, batch: Any, cutoff: float, *, include_boundary: bool = True
+                   ) -> dict[str, np.ndarray]:
+    """Device neighbour graph in the layout of ``_native.build_neighbor_graph``
+    (``cpp/src/bindings/module.cpp:887-935``): offsets, atoms, shifts,
+    displacements, distance2 — over every structure of the batch."""
+
+    arrays = _BatchArrays(batch)
+    lib = context.lib
+    pairs = ctypes.c_int64()
+    context.check(lib.mdx_hip_neighbors_build(context.handle, ctypes.byref(arrays.view), float(cutoff),
+                                              1 if include_boundary else 0, ctypes.byref(pairs)))
+    p = int(pairs.value)
+    n = len(arrays.numbers)
+    offsets = np.zeros(n + 1, dtype=np.int64)
+    atoms = np.zeros(max(p, 1), dtype=np.int32)
+    shifts = np.zeros((max(p, 1), 3), dtype=np.int32)
+    disp = np.zeros((max(p, 1), 3), dtype=np.float64)
+    d2 = np.zeros(max(p, 1), dtype=np.float64)
+    context.check(lib.mdx_hip_neighbors_fetch(
+        context.handle, offsets.ctypes.data_as(_i64p), atoms.ctypes.data_as(_i32p), shifts.ctypes.data_as(_i32p),
+        disp.ctypes.data_as(_f64p), d2.ctypes.data_as(_f64p)))
+    return {
+        "offsets": offsets,
+        "atoms": atoms[:p],
+        "shifts": shifts[:p],
+        "displacements": disp[:p],
+        "distance2": d2[:p],
+    }
+
+
+_contexts: dict[int, Context] = {}
+
+
+def shared_context(device: int = 0) -> Context:
+    """Process-wide context per device, created on first use."""
+
+    with _lock:
+        ctx = _contexts.get(device)
+    if ctx is None:
+        ctx = Context(device)
+        with _lock:
+            _contexts.setdefault(device, ctx)
+            ctx = _contexts[device]
+    return ctx
+
+
+class Backend:
+    """SOAP on one HIP device, created lazily by :func:`create_backend`."""
+
+    def __init__(self, name: str, options: Mapping[str, Any]) -> None:
+        if name != "SOAP":
+            raise ValueError(f"the HIP backend implements SOAP only, not {name!r}")
+        payload = options.get("_hip_payload")
+        if not isinstance(payload, Mapping):
+            raise ValueError("SOAP HIP backend requires the private _hip_payload")
+        radial = payload["radial_basis"]
+        if "alphas" not in radial:
+            raise ValueError("the HIP backend implements the GTO radial basis only")
+        self.name = name
+        self.options = dict(options)
+        self._labels = tuple(options.get("_hip_labels") or payload.get("labels") or ())
+        output = options.get("output") or {}
+        self._dtype = output.get("dtype", "float64") if isinstance(output, Mapping) else getattr(output, "dtype", "float64")
+        execution = options.get("execution") or {}
+        num_threads = execution.get("num_threads") if isinstance(execution, Mapping) else getattr(execution, "num_threads", None)
+        self._num_threads = num_threads
+        self._average = str(options.get("average", "inner"))
+        self._context = shared_context(0)
+        self._plan = SoapPlan(
+            self._context, species=options["species"], n_max=int(options["n_max"]), l_max=int(options["l_max"]),
+            r_cut=float(options["r_cut"]), sigma=float(options.get("sigma", 1.0)),
+            alphas=np.asarray(radial["alphas"]), betas=np.asarray(radial["betas"]), average=self._average,
+            dtype=self._dtype,
+        )
+        self._lock = threading.Lock()
+        self._closed = False
+        self.last_timing: dict[str, float] = {}
+
+    @property
+    def feature_count(self) -> int:
+        return self._plan.features
+
+    def metadata(self) -> dict[str, Any]:
+        return {
+            "descriptor": self.name,
+            "backend": "mdescriptor-hip",
+            "execution": {"device": "hip", "num_threads": self._num_threads},
+        }
+
+    def compute(self, batch: Any, control: Any = None) -> dict[str, Any]:
+        with self._lock:
+            if self._closed:
+                raise RuntimeError("HIP backend is closed")
+            flag = getattr(control, "_hip_cancel_flag", None) if control is not None else None
+            values, timing = self._plan.compute(batch, flag)
+            self.last_timing = timing
+            level = "structure" if self._average in ("inner", "outer") else "atom"
+            result: dict[str, Any] = {
+                "values": values,
+                "level": level,
+                "labels": self._labels,
+                "metadata": self.metadata(),
+                "_mdescriptor_owned_values": True,
+            }
+            if level == "atom":
+                result["row_offsets"] = np.asarray(batch.offsets, dtype=np.int64).copy()
+            return result
+
+    def close(self) -> None:
+        with self._lock:
+            if not self._closed:
+                self._plan.close()
+            self._closed = True
+
+
+def create_backend(name: str, options: Mapping[str, Any]) -> Backend:
+    """Plugin factory, the counterpart of ``_cuda.create_backend`` (bindings.cu:30-40)."""
+
+    return Backend(name, options)
+
+
+def version() -> str:
+    return load_library().mdx_hip_version().decode()
+
+
+__all__ = [
+    "Backend",
+    "Context",
+    "DeviceBatch",
+    "HipCancelledError",
+    "HipError",
+    "HipOutOfMemory",
+    "HipUnavailable",
+    "MODEL_SNAPSHOT_ABI",
+    "SoapPlan",
+    "create_backend",
+    "load_library",
+    "neighbor_graph",
+    "shared_context",
+]

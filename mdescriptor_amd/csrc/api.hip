@@ -1,0 +1,490 @@
+// The extern "C" boundary of the SOAP library (declared in include/mdx_hip.h).
+//
+// Everything below the boundary throws mdx::Error; every entry point catches
+// and returns a status code, keeping the message on the context.  Calls on
+// one context are serialised by its mutex (the reference serialises a
+// calculator the same way, cpp/src/standalone/soap.cpp:1255 and
+// cpp/cuda/src/backend.cu:339-345).
+#include "mdx_internal.h"
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <unordered_set>
+
+namespace {
+
+thread_local std::string g_last_error;
+
+template <typename Fn>
+int guarded(mdx_hip_ctx* ctx, Fn&& fn) {
+    std::string message;
+    int status = MDX_OK;
+    try {
+        fn();
+    } catch (const mdx::Error& e) {
+        status = e.status;
+        message = e.what();
+    } catch (const std::bad_alloc&) {
+        status = MDX_OUT_OF_MEMORY;
+        message = "host out of memory";
+    } catch (const std::exception& e) {
+        status = MDX_INTERNAL;
+        message = e.what();
+    } catch (...) {
+        status = MDX_INTERNAL;
+        message = "unknown error";
+    }
+    if (ctx != nullptr) ctx->last_error = message;
+    g_last_error = message;
+    return status;
+}
+
+struct DeviceScope {
+    int previous = -1;
+    explicit DeviceScope(int device) {
+        if (hipGetDevice(&previous) != hipSuccess) previous = -1;
+        MDX_HIP(hipSetDevice(device));
+    }
+    ~DeviceScope() {
+        if (previous >= 0) (void)hipSetDevice(previous);
+    }
+};
+
+float elapsed(hipEvent_t a, hipEvent_t b) {
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, a, b) != hipSuccess) return 0.0f;
+    return ms;
+}
+
+void check_cancel(const volatile int32_t* cancel) {
+    if (cancel != nullptr && *cancel != 0) throw mdx::Error(MDX_CANCELLED, "descriptor computation was cancelled");
+}
+
+// Pair export for the neighbour API: one thread per pair.
+__global__ void k_export_pairs(const int64_t* pair_start, int64_t atoms, int64_t pairs, const uint32_t* pair_bin,
+                               const double* positions, const double* bx, const double* by, const double* bz,
+                               const int32_t* batom, const int32_t* bimage, const mdx::ImageDesc* images,
+                               int32_t* out_atoms, int32_t* out_shifts, double* out_disp, double* out_d2) {
+    for (int64_t p = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; p < pairs;
+         p += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        int64_t lo = 0, hi = atoms;
+        while (hi - lo > 1) {
+            const int64_t mid = (lo + hi) / 2;
+            if (pair_start[mid] <= p) lo = mid; else hi = mid;
+        }
+        while (lo + 1 < atoms && pair_start[lo + 1] <= p) ++lo;
+        const uint32_t b = pair_bin[p];
+        const double dx = bx[b] - positions[lo * 3 + 0];
+        const double dy = by[b] - positions[lo * 3 + 1];
+        const double dz = bz[b] - positions[lo * 3 + 2];
+        out_atoms[p] = batom[b];
+        const mdx::ImageDesc& im = images[bimage[b]];
+        out_shifts[p * 3 + 0] = im.n[0];
+        out_shifts[p * 3 + 1] = im.n[1];
+        out_shifts[p * 3 + 2] = im.n[2];
+        out_disp[p * 3 + 0] = dx;
+        out_disp[p * 3 + 1] = dy;
+        out_disp[p * 3 + 2] = dz;
+        out_d2[p] = dx * dx + dy * dy + dz * dz;
+    }
+}
+
+double soap_padding(double sigma) {
+    // graph cutoff padding, cpp/src/standalone/soap.cpp:1214
+    return sigma * std::sqrt(-2.0 * std::log(1e-3));
+}
+
+void validate_params(const mdx_soap_params& p) {
+    if (p.species == nullptr || p.n_species < 1) throw mdx::Error(MDX_INVALID_ARGUMENT, "species must not be empty");
+    if (p.n_species > mdx::kMaxSpecies) {
+        throw mdx::Error(MDX_INVALID_ARGUMENT, "the HIP SOAP backend supports at most 16 species");
+    }
+    std::unordered_set<int32_t> seen;
+    for (int t = 0; t < p.n_species; ++t) {
+        if (p.species[t] <= 0) throw mdx::Error(MDX_INVALID_ARGUMENT, "species must contain positive atomic numbers");
+        if (!seen.insert(p.species[t]).second) {
+            throw mdx::Error(MDX_INVALID_ARGUMENT, "species must contain unique atomic numbers");
+        }
+    }
+    // soap.cpp:1152-1158
+    if (!std::isfinite(p.r_cut) || !std::isfinite(p.sigma) || p.r_cut <= 0.0 || p.sigma <= 0.0 || p.n_max < 1
+        || p.l_max < 0 || p.l_max > mdx::kMaxLmax || p.average < 0 || p.average > 2
+        || (p.out_dtype != 4 && p.out_dtype != 8)) {
+        throw mdx::Error(MDX_INVALID_ARGUMENT, "invalid SOAP parameters");
+    }
+    if (p.n_max > mdx::kMaxNmax) {
+        throw mdx::Error(MDX_INVALID_ARGUMENT, "the HIP SOAP backend supports n_max <= 16");
+    }
+    if (p.alphas == nullptr || p.betas == nullptr) {
+        throw mdx::Error(MDX_INVALID_ARGUMENT, "invalid SOAP radial basis size");
+    }
+    const int L = p.l_max + 1;
+    for (int i = 0; i < L * p.n_max; ++i) {
+        if (!std::isfinite(p.alphas[i])) throw mdx::Error(MDX_INVALID_ARGUMENT, "SOAP radial basis must be finite");
+    }
+    for (int i = 0; i < L * p.n_max * p.n_max; ++i) {
+        if (!std::isfinite(p.betas[i])) throw mdx::Error(MDX_INVALID_ARGUMENT, "SOAP radial basis must be finite");
+    }
+    const int64_t coeff = static_cast<int64_t>(p.n_species) * p.n_max * L * L;
+    if (coeff * 8 > 96 * 1024) {
+        throw mdx::Error(MDX_INVALID_ARGUMENT,
+                         "SOAP shape exceeds the HIP backend coefficient budget (species*n_max*(l_max+1)^2 <= 12288)");
+    }
+}
+
+template <typename T>
+void upload(mdx::DeviceBuffer& buf, const std::vector<T>& host) {
+    buf.reserve(std::max<size_t>(1, host.size() * sizeof(T)));
+    if (!host.empty()) MDX_HIP(hipMemcpy(buf.ptr, host.data(), host.size() * sizeof(T), hipMemcpyHostToDevice));
+}
+
+void fill_timing(mdx_hip_ctx* ctx, mdx_timing* timing, bool with_copies) {
+    if (timing == nullptr) return;
+    hipEvent_t* ev = ctx->events;
+    timing->graph_ms = elapsed(ev[0], ev[1]);
+    timing->expansion_ms = elapsed(ev[2], ev[3]);
+    timing->finalize_ms = elapsed(ev[3], ev[4]);
+    timing->total_ms = elapsed(ev[0], ev[4]);
+    if (with_copies) {
+        timing->h2d_ms = elapsed(ev[5], ev[0]);
+        timing->d2h_ms = elapsed(ev[4], ev[6]);
+    } else {
+        timing->h2d_ms = 0.0;
+        timing->d2h_ms = 0.0;
+    }
+}
+
+void run_pipeline(mdx_hip_ctx* ctx, const mdx_soap_plan& plan, mdx::PreparedBatch& pb, mdx::DeviceGraph& graph,
+                  mdx::DeviceBuffer& partials, void* out_device, int64_t pitch, const volatile int32_t* cancel,
+                  mdx_timing* timing) {
+    hipStream_t s = ctx->stream;
+    MDX_HIP(hipEventRecord(ctx->events[0], s));
+    const int64_t pairs = mdx::build_graph(s, pb, graph, cancel);
+    MDX_HIP(hipEventRecord(ctx->events[1], s));
+    check_cancel(cancel);
+    mdx::run_soap(s, plan, pb, graph, out_device, pitch, partials, cancel, ctx->events, timing);
+    const int64_t rows = plan.average != 0 ? pb.structures : pb.atoms;
+    if (rows == 0 || plan.features == 0) {
+        MDX_HIP(hipEventRecord(ctx->events[2], s));
+        MDX_HIP(hipEventRecord(ctx->events[3], s));
+        MDX_HIP(hipEventRecord(ctx->events[4], s));
+    }
+    if (timing != nullptr) {
+        timing->pairs = pairs;
+        timing->binned = graph.binned;
+    }
+}
+
+} // namespace
+
+extern "C" {
+
+const char* mdx_hip_version(void) { return "mdx_hip 0.1.0 (gfx950)"; }
+
+const char* mdx_hip_last_error(const mdx_hip_ctx* ctx) {
+    return ctx != nullptr ? ctx->last_error.c_str() : g_last_error.c_str();
+}
+
+int mdx_hip_create(int device, mdx_hip_ctx** out) {
+    if (out == nullptr) return MDX_INVALID_ARGUMENT;
+    *out = nullptr;
+    return guarded(nullptr, [&] {
+        int count = 0;
+        const hipError_t rc = hipGetDeviceCount(&count);
+        if (rc != hipSuccess || count <= 0) {
+            throw mdx::Error(MDX_DEVICE_UNAVAILABLE, "no HIP device is available");
+        }
+        if (device < 0 || device >= count) throw mdx::Error(MDX_INVALID_ARGUMENT, "HIP device index out of range");
+        auto ctx = new mdx_hip_ctx();
+        try {
+            DeviceScope scope(device);
+            ctx->device = device;
+            MDX_HIP(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+            for (auto& ev : ctx->events) MDX_HIP(hipEventCreate(&ev));
+        } catch (...) {
+            mdx_hip_destroy(ctx);
+            throw;
+        }
+        *out = ctx;
+    });
+}
+
+void mdx_hip_destroy(mdx_hip_ctx* ctx) {
+    if (ctx == nullptr) return;
+    int previous = -1;
+    (void)hipGetDevice(&previous);
+    (void)hipSetDevice(ctx->device);
+    {
+        std::lock_guard<std::mutex> lock(ctx->mutex);
+        if (ctx->stream != nullptr) (void)hipStreamSynchronize(ctx->stream);
+        for (auto& ev : ctx->events) {
+            if (ev != nullptr) (void)hipEventDestroy(ev);
+            ev = nullptr;
+        }
+        if (ctx->pinned != nullptr) (void)hipHostFree(ctx->pinned);
+        ctx->pinned = nullptr;
+    }
+    hipStream_t stream = ctx->stream;
+    delete ctx; // device buffers are freed by their destructors
+    if (stream != nullptr) (void)hipStreamDestroy(stream);
+    if (previous >= 0) (void)hipSetDevice(previous);
+}
+
+int mdx_hip_soap_plan_create(mdx_hip_ctx* ctx, const mdx_soap_params* params, mdx_soap_plan** out,
+                             int64_t* features) {
+    if (ctx == nullptr || params == nullptr || out == nullptr) return MDX_INVALID_ARGUMENT;
+    *out = nullptr;
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    return guarded(ctx, [&] {
+        const mdx_soap_params& p = *params;
+        validate_params(p);
+        DeviceScope scope(ctx->device);
+        auto plan = new mdx_soap_plan();
+        try {
+            plan->device = ctx->device;
+            plan->S = p.n_species;
+            plan->n = p.n_max;
+            plan->l_max = p.l_max;
+            plan->L = p.l_max + 1;
+            plan->H = plan->L * plan->L;
+            plan->LN = plan->L * p.n_max;
+            plan->average = p.average;
+            plan->out_dtype = p.out_dtype;
+            plan->r_cut = p.r_cut;
+            plan->sigma = p.sigma;
+            plan->cutoff = p.r_cut + soap_padding(p.sigma);
+            plan->species.assign(p.species, p.species + p.n_species);
+            const int64_t w = static_cast<int64_t>(plan->S) * plan->n;
+            plan->features = w * (w + 1) / 2 * plan->L; // soap.cpp:382-385
+            plan->coeff_size = w * plan->H;
+            const int L = plan->L, n = plan->n, H = plan->H;
+            // prepare_soap, soap.cpp:507-534
+            const double pi = 3.141592653589793238462643383279502884;
+            const double eta = 1.0 / (2.0 * p.sigma * p.sigma);
+            const double soap_scale = pi * std::sqrt(pi);
+            std::vector<double> pref(static_cast<size_t>(L * n)), expo(static_cast<size_t>(L * n));
+            double eta_power = 1.0;
+            for (int l = 0; l < L; ++l) {
+                if (l > 0) eta_power *= eta;
+                for (int k = 0; k < n; ++k) {
+                    const int idx = l * n + k;
+                    const double alpha = p.alphas[idx];
+                    const double denominator = alpha + eta;
+                    pref[static_cast<size_t>(idx)] = eta_power * std::pow(denominator, -l - 1.5);
+                    expo[static_cast<size_t>(idx)] = alpha * eta / denominator;
+                }
+            }
+            std::vector<double> beta(static_cast<size_t>(L * n * n));
+            for (size_t i = 0; i < beta.size(); ++i) beta[i] = soap_scale * p.betas[i];
+            std::vector<double> ps_pref(static_cast<size_t>(L));
+            for (int l = 0; l < L; ++l) ps_pref[static_cast<size_t>(l)] = pi * std::sqrt(8.0 / (2.0 * l + 1.0));
+            // solid_harmonic_normalization (soap.cpp:26-38), sqrt(2) folded in for m > 0
+            std::vector<double> hnorm(static_cast<size_t>(L * L), 0.0);
+            const double sqrt2 = 1.414213562373095048801688724209698079;
+            for (int l = 0; l < L; ++l) {
+                for (int m = 0; m <= l; ++m) {
+                    const double norm = std::sqrt((2.0 * l + 1.0) / (4.0 * pi)
+                                                  * std::exp(std::lgamma(l - m + 1.0) - std::lgamma(l + m + 1.0)));
+                    hnorm[static_cast<size_t>(l * L + m)] = m == 0 ? norm : sqrt2 * norm;
+                }
+            }
+            // feature order of soap.cpp:997-1013 (labels core.py:321-329)
+            std::vector<int32_t> fa, fb;
+            fa.reserve(static_cast<size_t>(plan->features));
+            fb.reserve(static_cast<size_t>(plan->features));
+            for (int t1 = 0; t1 < plan->S; ++t1) {
+                for (int t2 = t1; t2 < plan->S; ++t2) {
+                    for (int l = 0; l < L; ++l) {
+                        for (int n1 = 0; n1 < n; ++n1) {
+                            for (int n2 = (t1 == t2 ? n1 : 0); n2 < n; ++n2) {
+                                fa.push_back(((t1 * n + n1) * H + l * l) | (l << 24));
+                                fb.push_back((t2 * n + n2) * H + l * l);
+                            }
+                        }
+                    }
+                }
+            }
+            upload(plan->d_pref, pref);
+            upload(plan->d_expo, expo);
+            upload(plan->d_beta, beta);
+            upload(plan->d_ps_pref, ps_pref);
+            upload(plan->d_hnorm, hnorm);
+            upload(plan->d_feat_a, fa);
+            upload(plan->d_feat_b, fb);
+        } catch (...) {
+            delete plan;
+            throw;
+        }
+        *out = plan;
+        if (features != nullptr) *features = plan->features;
+    });
+}
+
+void mdx_hip_soap_plan_destroy(mdx_soap_plan* plan) {
+    if (plan == nullptr) return;
+    int previous = -1;
+    (void)hipGetDevice(&previous);
+    (void)hipSetDevice(plan->device);
+    delete plan;
+    if (previous >= 0) (void)hipSetDevice(previous);
+}
+
+int64_t mdx_hip_soap_rows(const mdx_soap_plan* plan, const mdx_batch_view* batch) {
+    if (plan == nullptr || batch == nullptr) return -1;
+    return plan->average != 0 ? batch->structures : batch->atoms;
+}
+
+int mdx_hip_soap_compute(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, const mdx_batch_view* batch, void* out_host,
+                         int64_t out_rows, int64_t out_pitch_bytes, const volatile int32_t* cancel_flag,
+                         mdx_timing* timing) {
+    if (ctx == nullptr) return MDX_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    return guarded(ctx, [&] {
+        if (plan == nullptr || batch == nullptr) throw mdx::Error(MDX_INVALID_ARGUMENT, "null plan or batch");
+        if (plan->device != ctx->device) throw mdx::Error(MDX_INVALID_ARGUMENT, "plan belongs to another device");
+        check_cancel(cancel_flag);
+        DeviceScope scope(ctx->device);
+        const int64_t rows = plan->average != 0 ? batch->structures : batch->atoms;
+        const int64_t row_bytes = plan->features * plan->out_dtype;
+        if (out_rows != rows) throw mdx::Error(MDX_INVALID_ARGUMENT, "output rows do not match the batch");
+        if (out_pitch_bytes < row_bytes) throw mdx::Error(MDX_INVALID_ARGUMENT, "output pitch is too small");
+        if (rows > 0 && row_bytes > 0 && out_host == nullptr) throw mdx::Error(MDX_INVALID_ARGUMENT, "null output");
+        mdx::PreparedBatch& pb = ctx->scratch_batch;
+        pb.include_boundary = 1;
+        mdx::prepare_batch(*batch, plan->species.data(), plan->S, plan->cutoff, pb);
+        hipStream_t s = ctx->stream;
+        MDX_HIP(hipEventRecord(ctx->events[5], s));
+        mdx::upload_batch(s, *batch, pb);
+        ctx->out_dev.reserve(std::max<size_t>(1, static_cast<size_t>(rows) * static_cast<size_t>(row_bytes)));
+        run_pipeline(ctx, *plan, pb, ctx->graph, ctx->partials, ctx->out_dev.ptr, row_bytes, cancel_flag, timing);
+        if (rows > 0 && row_bytes > 0) {
+            MDX_HIP(hipMemcpy2DAsync(out_host, static_cast<size_t>(out_pitch_bytes), ctx->out_dev.ptr,
+                                     static_cast<size_t>(row_bytes), static_cast<size_t>(row_bytes),
+                                     static_cast<size_t>(rows), hipMemcpyDeviceToHost, s));
+        }
+        MDX_HIP(hipEventRecord(ctx->events[6], s));
+        MDX_HIP(hipStreamSynchronize(s));
+        fill_timing(ctx, timing, true);
+    });
+}
+
+int mdx_hip_batch_upload(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, const mdx_batch_view* batch,
+                         mdx_device_batch** out) {
+    if (ctx == nullptr || out == nullptr) return MDX_INVALID_ARGUMENT;
+    *out = nullptr;
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    return guarded(ctx, [&] {
+        if (plan == nullptr || batch == nullptr) throw mdx::Error(MDX_INVALID_ARGUMENT, "null plan or batch");
+        if (plan->device != ctx->device) throw mdx::Error(MDX_INVALID_ARGUMENT, "plan belongs to another device");
+        DeviceScope scope(ctx->device);
+        auto db = new mdx_device_batch();
+        try {
+            db->device = ctx->device;
+            db->pb.include_boundary = 1;
+            mdx::prepare_batch(*batch, plan->species.data(), plan->S, plan->cutoff, db->pb);
+            mdx::upload_batch(ctx->stream, *batch, db->pb);
+        } catch (...) {
+            delete db;
+            throw;
+        }
+        *out = db;
+    });
+}
+
+void mdx_hip_batch_destroy(mdx_device_batch* batch) {
+    if (batch == nullptr) return;
+    int previous = -1;
+    (void)hipGetDevice(&previous);
+    (void)hipSetDevice(batch->device);
+    delete batch;
+    if (previous >= 0) (void)hipSetDevice(previous);
+}
+
+int mdx_hip_soap_run(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, mdx_device_batch* batch, void* out_device,
+                     int64_t out_pitch_bytes, const volatile int32_t* cancel_flag, mdx_timing* timing) {
+    if (ctx == nullptr) return MDX_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    return guarded(ctx, [&] {
+        if (plan == nullptr || batch == nullptr) throw mdx::Error(MDX_INVALID_ARGUMENT, "null plan or batch");
+        if (plan->device != ctx->device || batch->device != ctx->device) {
+            throw mdx::Error(MDX_INVALID_ARGUMENT, "plan or batch belongs to another device");
+        }
+        if (batch->pb.n_species != plan->S || batch->pb.cutoff != plan->cutoff) {
+            throw mdx::Error(MDX_INVALID_ARGUMENT, "device batch was prepared for another plan");
+        }
+        check_cancel(cancel_flag);
+        const int64_t rows = plan->average != 0 ? batch->pb.structures : batch->pb.atoms;
+        const int64_t row_bytes = plan->features * plan->out_dtype;
+        if (out_pitch_bytes < row_bytes) throw mdx::Error(MDX_INVALID_ARGUMENT, "output pitch is too small");
+        if (rows > 0 && row_bytes > 0 && out_device == nullptr) throw mdx::Error(MDX_INVALID_ARGUMENT, "null output");
+        DeviceScope scope(ctx->device);
+        run_pipeline(ctx, *plan, batch->pb, batch->graph, batch->partials, out_device, out_pitch_bytes, cancel_flag,
+                     timing);
+        MDX_HIP(hipStreamSynchronize(ctx->stream));
+        fill_timing(ctx, timing, false);
+    });
+}
+
+int mdx_hip_neighbors_build(mdx_hip_ctx* ctx, const mdx_batch_view* batch, double cutoff, int32_t include_boundary,
+                            int64_t* pairs) {
+    if (ctx == nullptr) return MDX_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    return guarded(ctx, [&] {
+        if (batch == nullptr) throw mdx::Error(MDX_INVALID_ARGUMENT, "null batch");
+        DeviceScope scope(ctx->device);
+        mdx::PreparedBatch& pb = ctx->scratch_batch;
+        pb.include_boundary = include_boundary != 0 ? 1 : 0;
+        mdx::prepare_batch(*batch, nullptr, 1, cutoff, pb);
+        mdx::upload_batch(ctx->stream, *batch, pb);
+        const int64_t n = mdx::build_graph(ctx->stream, pb, ctx->graph, nullptr);
+        MDX_HIP(hipStreamSynchronize(ctx->stream));
+        if (pairs != nullptr) *pairs = n;
+    });
+}
+
+int mdx_hip_neighbors_fetch(mdx_hip_ctx* ctx, int64_t* offsets, int32_t* neighbors, int32_t* shifts,
+                            double* displacements, double* distance2) {
+    if (ctx == nullptr) return MDX_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    return guarded(ctx, [&] {
+        DeviceScope scope(ctx->device);
+        const mdx::PreparedBatch& pb = ctx->scratch_batch;
+        mdx::DeviceGraph& g = ctx->graph;
+        if (g.n_species != 1) throw mdx::Error(MDX_INVALID_ARGUMENT, "no neighbour graph has been built");
+        hipStream_t s = ctx->stream;
+        const int64_t atoms = pb.atoms, pairs = g.pairs;
+        if (offsets != nullptr) {
+            MDX_HIP(hipMemcpyAsync(offsets, g.pair_start.ptr, static_cast<size_t>(atoms + 1) * sizeof(int64_t),
+                                   hipMemcpyDeviceToHost, s));
+        }
+        if (pairs > 0) {
+            mdx::DeviceBuffer& tmp = ctx->out_dev;
+            const size_t p = static_cast<size_t>(pairs);
+            tmp.reserve(p * (4 + 12 + 24 + 8));
+            char* base = static_cast<char*>(tmp.ptr);
+            double* d_disp = reinterpret_cast<double*>(base);
+            double* d_d2 = d_disp + 3 * p;
+            int32_t* d_atoms = reinterpret_cast<int32_t*>(d_d2 + p);
+            int32_t* d_shifts = d_atoms + p;
+            const unsigned grid = static_cast<unsigned>(std::min<int64_t>((pairs + 255) / 256, 1 << 20));
+            hipLaunchKernelGGL(k_export_pairs, dim3(grid), dim3(256), 0, s, g.pair_start.as<int64_t>(), atoms, pairs,
+                               g.pair_bin.as<uint32_t>(), pb.d_positions.as<double>(), g.bin_x.as<double>(),
+                               g.bin_y.as<double>(), g.bin_z.as<double>(), g.bin_atom.as<int32_t>(),
+                               g.bin_image.as<int32_t>(), pb.d_images.as<mdx::ImageDesc>(), d_atoms, d_shifts, d_disp,
+                               d_d2);
+            MDX_HIP(hipGetLastError());
+            if (neighbors != nullptr) MDX_HIP(hipMemcpyAsync(neighbors, d_atoms, p * 4, hipMemcpyDeviceToHost, s));
+            if (shifts != nullptr) MDX_HIP(hipMemcpyAsync(shifts, d_shifts, p * 12, hipMemcpyDeviceToHost, s));
+            if (displacements != nullptr) {
+                MDX_HIP(hipMemcpyAsync(displacements, d_disp, p * 24, hipMemcpyDeviceToHost, s));
+            }
+            if (distance2 != nullptr) MDX_HIP(hipMemcpyAsync(distance2, d_d2, p * 8, hipMemcpyDeviceToHost, s));
+        }
+        MDX_HIP(hipStreamSynchronize(s));
+    });
+}
+
+} // extern "C"

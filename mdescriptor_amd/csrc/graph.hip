@@ -1,0 +1,786 @@
+// Kernel 1: periodic / isolated cell-list neighbour search on gfx950.
+//
+// The pair set is the reference's (build_structure_graph, image-extended
+// path, cpp/src/common/neighbor.cpp:423-679): every (atom j, image n) with
+// n in [-b, b]^3 and |r_j + n.cell - r_i|^2 <= cutoff^2, self pair and
+// self-images included, on raw (unwrapped) positions.  The cell grid is the
+// reference's own (build_grid, neighbor.cpp:135-194: bounding box of all
+// images, 1e-10 padding, cells at least `cutoff` wide), so each centre visits
+// the same 27 cells in the same z/y/x order and finds candidates in the same
+// order; rows therefore come out in the reference's order (grouped by
+// neighbour species for SOAP, a stable partition of that order).
+//
+// Device pipeline (all on one stream):
+//   bin_count  -> scan -> bin_fill -> bin_sort   images into ROI cells
+//   centre_cell -> scan -> centre_fill           centres grouped by home cell
+//   pair_pass<count> -> totals -> scan           per-centre, per-species counts
+//   pair_pass<fill>                              wave ballot / mbcnt compaction
+// Only cells within one cell of some centre (the region of interest) are
+// binned; the others are never visited.
+#include "mdx_internal.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <limits>
+#include <unordered_map>
+
+namespace mdx {
+
+void check_hip(hipError_t code, const char* what) {
+    if (code == hipSuccess) return;
+    const char* name = hipGetErrorString(code);
+    if (code == hipErrorOutOfMemory || code == hipErrorMemoryAllocation) {
+        throw Error(MDX_OUT_OF_MEMORY, std::string("HIP out of memory in ") + what);
+    }
+    if (code == hipErrorNoDevice || code == hipErrorInvalidDevice || code == hipErrorInsufficientDriver) {
+        throw Error(MDX_DEVICE_UNAVAILABLE, std::string("HIP device unavailable: ") + name);
+    }
+    throw Error(MDX_INTERNAL, std::string(what) + " failed: " + name);
+}
+
+void DeviceBuffer::reserve(size_t size) {
+    if (size <= bytes && ptr != nullptr) return;
+    release();
+    const size_t rounded = std::max<size_t>(256, (size + 255) & ~size_t(255));
+    MDX_HIP(hipMalloc(&ptr, rounded));
+    bytes = rounded;
+}
+
+void DeviceBuffer::release() {
+    if (ptr != nullptr) {
+        (void)hipFree(ptr);
+    }
+    ptr = nullptr;
+    bytes = 0;
+}
+
+namespace {
+
+// ---------------------------------------------------------------- host side
+
+double det3(const double* m) {
+    return m[0] * (m[4] * m[8] - m[5] * m[7]) - m[1] * (m[3] * m[8] - m[5] * m[6])
+        + m[2] * (m[3] * m[7] - m[4] * m[6]);
+}
+
+// inverse (math3.hpp:52-68), same cofactor order and division
+bool inverse3(const double* m, double* r) {
+    const double d = det3(m);
+    if (!std::isfinite(d) || std::abs(d) < 1e-14) return false;
+    r[0] = (m[4] * m[8] - m[5] * m[7]) / d;
+    r[1] = (m[2] * m[7] - m[1] * m[8]) / d;
+    r[2] = (m[1] * m[5] - m[2] * m[4]) / d;
+    r[3] = (m[5] * m[6] - m[3] * m[8]) / d;
+    r[4] = (m[0] * m[8] - m[2] * m[6]) / d;
+    r[5] = (m[2] * m[3] - m[0] * m[5]) / d;
+    r[6] = (m[3] * m[7] - m[4] * m[6]) / d;
+    r[7] = (m[1] * m[6] - m[0] * m[7]) / d;
+    r[8] = (m[0] * m[4] - m[1] * m[3]) / d;
+    return true;
+}
+
+// validate_batch (cpp/include/mdescriptor/detail/batch.hpp:19-80)
+void validate_batch(const mdx_batch_view& b) {
+    if (b.structures < 0 || b.atoms < 0 || b.offsets == nullptr) {
+        throw Error(MDX_INVALID_ARGUMENT, "invalid structure batch");
+    }
+    if (b.structures == 0) {
+        if (b.atoms != 0 || b.offsets[0] != 0) {
+            throw Error(MDX_INVALID_ARGUMENT, "empty structure batch has non-empty atom data");
+        }
+        return;
+    }
+    if (b.numbers == nullptr || b.positions == nullptr || b.cells == nullptr || b.pbc == nullptr) {
+        throw Error(MDX_INVALID_ARGUMENT, "structure batch contains null arrays");
+    }
+    if (b.offsets[0] != 0 || b.offsets[b.structures] != b.atoms) {
+        throw Error(MDX_INVALID_ARGUMENT, "offsets do not describe the flattened arrays");
+    }
+    for (int64_t s = 0; s < b.structures; ++s) {
+        if (b.offsets[s] < 0 || b.offsets[s] > b.offsets[s + 1] || b.offsets[s + 1] > b.atoms) {
+            throw Error(MDX_INVALID_ARGUMENT, "offsets must be monotonic");
+        }
+        bool periodic = true, isolated = true;
+        for (int a = 0; a < 3; ++a) {
+            const int32_t f = b.pbc[s * 3 + a];
+            if (f != 0 && f != 1) throw Error(MDX_INVALID_ARGUMENT, "pbc must contain only 0 or 1");
+            periodic = periodic && f == 1;
+            isolated = isolated && f == 0;
+        }
+        if (!periodic && !isolated) {
+            throw Error(MDX_INVALID_ARGUMENT, "mixed periodicity is not supported; use all-zero or all-one pbc");
+        }
+        const double* cell = b.cells + s * 9;
+        for (int i = 0; i < 9; ++i) {
+            if (!std::isfinite(cell[i])) throw Error(MDX_INVALID_ARGUMENT, "cells must be finite");
+        }
+        const double d = det3(cell);
+        if (periodic && (!std::isfinite(d) || std::abs(d) < 1e-14)) {
+            throw Error(MDX_INVALID_ARGUMENT, "cells must be nonsingular");
+        }
+    }
+    for (int64_t i = 0; i < b.atoms; ++i) {
+        if (b.numbers[i] <= 0) throw Error(MDX_INVALID_ARGUMENT, "atomic numbers must be positive");
+        for (int a = 0; a < 3; ++a) {
+            if (!std::isfinite(b.positions[i * 3 + a])) {
+                throw Error(MDX_INVALID_ARGUMENT, "positions must be finite");
+            }
+        }
+    }
+}
+
+// CellGrid::coordinate (neighbor.cpp:122-132); shared by host and device.
+__host__ __device__ inline int grid_coordinate(double value, double origin, double width, int dim) {
+    const double scaled = (value - origin) / width;
+    if (!(scaled > 0.0)) return 0;
+    if (!__builtin_isfinite(scaled) || scaled >= static_cast<double>(dim)) return dim - 1;
+    return static_cast<int>(scaled);
+}
+
+// ---------------------------------------------------------------- device side
+
+__device__ inline int64_t find_by_begin(const StructGeom* geom, int64_t n, int64_t value, int which) {
+    // last structure whose begin (ext/cell/atom by `which`) is <= value
+    int64_t lo = 0, hi = n;
+    while (hi - lo > 1) {
+        const int64_t mid = (lo + hi) / 2;
+        const int64_t b = which == 0 ? geom[mid].ext_begin : which == 1 ? geom[mid].cell_begin : geom[mid].atom_begin;
+        if (b <= value) lo = mid; else hi = mid;
+    }
+    // skip empty structures that share the same begin
+    return lo;
+}
+
+__device__ inline int64_t roi_cell(const StructGeom& g, double x, double y, double z, bool& inside) {
+    const int cx = grid_coordinate(x, g.minimum[0], g.spacing[0], g.dims[0]);
+    const int cy = grid_coordinate(y, g.minimum[1], g.spacing[1], g.dims[1]);
+    const int cz = grid_coordinate(z, g.minimum[2], g.spacing[2], g.dims[2]);
+    const int lx = cx - g.roi_lo[0], ly = cy - g.roi_lo[1], lz = cz - g.roi_lo[2];
+    inside = lx >= 0 && ly >= 0 && lz >= 0 && lx < g.roi_dim[0] && ly < g.roi_dim[1] && lz < g.roi_dim[2];
+    return g.cell_begin + lx + static_cast<int64_t>(g.roi_dim[0]) * (ly + static_cast<int64_t>(g.roi_dim[1]) * lz);
+}
+
+// Locate enumeration index e (image-major, atom-minor: the reference's
+// extended order, neighbor.cpp:519-528) and compute the image position.
+__device__ inline const StructGeom& ext_lookup(const StructGeom* geom, int64_t nstruct, int64_t e,
+                                              int64_t& key) {
+    int64_t s = find_by_begin(geom, nstruct, e, 0);
+    // structures with zero atoms share ext_begin with the next one; move forward
+    while (s + 1 < nstruct && geom[s + 1].ext_begin <= e) ++s;
+    const StructGeom& g = geom[s];
+    key = e - g.ext_begin;
+    return g;
+}
+
+__device__ inline void image_position(const StructGeom& g, const ImageDesc* images, const double* positions,
+                                      int64_t key, double& x, double& y, double& z, int64_t& atom,
+                                      int64_t& image) {
+    const int64_t q = key / g.natoms;
+    const int64_t j = key - q * g.natoms;
+    atom = g.atom_begin + j;
+    image = g.image_begin + q;
+    const ImageDesc& im = images[image];
+    x = positions[atom * 3 + 0] + im.shift[0];
+    y = positions[atom * 3 + 1] + im.shift[1];
+    z = positions[atom * 3 + 2] + im.shift[2];
+}
+
+__global__ void k_bin_count(const StructGeom* geom, int64_t nstruct, const ImageDesc* images,
+                            const double* positions, int64_t ext_total, int32_t* cell_count) {
+    for (int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; e < ext_total;
+         e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        int64_t key, atom, image;
+        const StructGeom& g = ext_lookup(geom, nstruct, e, key);
+        double x, y, z;
+        image_position(g, images, positions, key, x, y, z, atom, image);
+        bool inside;
+        const int64_t c = roi_cell(g, x, y, z, inside);
+        if (inside) atomicAdd(&cell_count[c], 1);
+    }
+}
+
+__global__ void k_bin_fill(const StructGeom* geom, int64_t nstruct, const ImageDesc* images,
+                           const double* positions, int64_t ext_total, const int64_t* cell_start,
+                           int32_t* cell_fill, uint32_t* keys) {
+    for (int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; e < ext_total;
+         e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        int64_t key, atom, image;
+        const StructGeom& g = ext_lookup(geom, nstruct, e, key);
+        double x, y, z;
+        image_position(g, images, positions, key, x, y, z, atom, image);
+        bool inside;
+        const int64_t c = roi_cell(g, x, y, z, inside);
+        if (inside) {
+            const int32_t slot = atomicAdd(&cell_fill[c], 1);
+            keys[cell_start[c] + slot] = static_cast<uint32_t>(key);
+        }
+    }
+}
+
+// Order each cell by extended index (the reference fills cells in extended
+// order, neighbor.cpp:184-192) by ranking, then materialise the binned
+// images as SoA.  Keys are unique inside a cell.
+__global__ void k_bin_sort(const StructGeom* geom, int64_t nstruct, const ImageDesc* images,
+                           const double* positions, const int32_t* types, const int64_t* cell_start,
+                           int64_t cells_total, const uint32_t* keys, double* bx, double* by, double* bz,
+                           int32_t* batom, int32_t* bimage, int32_t* btype) {
+    for (int64_t c = blockIdx.x; c < cells_total; c += gridDim.x) {
+        const int64_t start = cell_start[c];
+        const int64_t n = cell_start[c + 1] - start;
+        if (n == 0) continue;
+        int64_t s = find_by_begin(geom, nstruct, c, 1);
+        while (s + 1 < nstruct && geom[s + 1].cell_begin <= c) ++s;
+        const StructGeom& g = geom[s];
+        for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+            const uint32_t key = keys[start + i];
+            int64_t rank = 0;
+            for (int64_t j = 0; j < n; ++j) rank += keys[start + j] < key ? 1 : 0;
+            const int64_t dest = start + rank;
+            double x, y, z;
+            int64_t atom, image;
+            image_position(g, images, positions, key, x, y, z, atom, image);
+            bx[dest] = x;
+            by[dest] = y;
+            bz[dest] = z;
+            batom[dest] = static_cast<int32_t>(atom);
+            bimage[dest] = static_cast<int32_t>(image);
+            btype[dest] = types[atom];
+        }
+    }
+}
+
+__global__ void k_centre_cell(const StructGeom* geom, int64_t nstruct, const double* positions, int64_t atoms,
+                              int64_t* centre_cell, int32_t* cell_centre_count, int32_t* error_flag) {
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < atoms;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        int64_t s = find_by_begin(geom, nstruct, i, 2);
+        while (s + 1 < nstruct && geom[s + 1].atom_begin <= i) ++s;
+        const StructGeom& g = geom[s];
+        bool inside;
+        const int64_t c = roi_cell(g, positions[i * 3 + 0], positions[i * 3 + 1], positions[i * 3 + 2], inside);
+        if (!inside) {
+            // the host placed every centre inside the ROI with the same arithmetic
+            atomicOr(error_flag, 1);
+            centre_cell[i] = -1;
+            continue;
+        }
+        centre_cell[i] = c;
+        atomicAdd(&cell_centre_count[c], 1);
+    }
+}
+
+__global__ void k_centre_fill(const int64_t* centre_cell, int64_t atoms, const int64_t* cell_centre_start,
+                              int32_t* cell_centre_fill, int32_t* cell_centre_list) {
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < atoms;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t c = centre_cell[i];
+        if (c < 0) continue;
+        const int32_t slot = atomicAdd(&cell_centre_fill[c], 1);
+        cell_centre_list[cell_centre_start[c] + slot] = static_cast<int32_t>(i);
+    }
+}
+
+// One workgroup per home cell: stage the 27 neighbour cells' candidates in
+// LDS (visit order, chunks of kChunk), then each wave tests its centres
+// against them, 64 candidates per step.  Count pass: per-species counts.
+// Fill pass: wave ballot + popcount compaction into species-grouped rows.
+template <bool kFill>
+__global__ __launch_bounds__(kBlock) void k_pair_pass(
+    const StructGeom* geom, int64_t nstruct, const double* positions, const int64_t* cell_start,
+    const int64_t* cell_centre_start, const int32_t* cell_centre_list, int64_t cells_total,
+    const double* bx, const double* by, const double* bz, const int32_t* btype, int S, double cutoff2,
+    int include_boundary, int32_t* counts, const int64_t* pair_start, int64_t* cursor, uint32_t* pair_bin) {
+    __shared__ double sx[kChunk], sy[kChunk], sz[kChunk];
+    __shared__ int32_t st[kChunk];
+    __shared__ uint32_t sb[kChunk];
+    __shared__ int64_t seg_start[27];
+    __shared__ int32_t seg_prefix[28];
+    __shared__ int32_t nseg;
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    for (int64_t c = blockIdx.x; c < cells_total; c += gridDim.x) {
+        const int64_t cs = cell_centre_start[c];
+        const int64_t ce = cell_centre_start[c + 1];
+        if (cs == ce) continue;
+        if (threadIdx.x == 0) {
+            int64_t s = find_by_begin(geom, nstruct, c, 1);
+            while (s + 1 < nstruct && geom[s + 1].cell_begin <= c) ++s;
+            const StructGeom& g = geom[s];
+            const int64_t local = c - g.cell_begin;
+            const int lx = static_cast<int>(local % g.roi_dim[0]);
+            const int ly = static_cast<int>((local / g.roi_dim[0]) % g.roi_dim[1]);
+            const int lz = static_cast<int>(local / (static_cast<int64_t>(g.roi_dim[0]) * g.roi_dim[1]));
+            const int ix = g.roi_lo[0] + lx, iy = g.roi_lo[1] + ly, iz = g.roi_lo[2] + lz;
+            int k = 0;
+            seg_prefix[0] = 0;
+            // visit order of neighbor.cpp:562-564: z outer, y, x inner, clamped to the grid
+            for (int z = max(0, iz - 1); z <= min(g.dims[2] - 1, iz + 1); ++z) {
+                for (int y = max(0, iy - 1); y <= min(g.dims[1] - 1, iy + 1); ++y) {
+                    for (int x = max(0, ix - 1); x <= min(g.dims[0] - 1, ix + 1); ++x) {
+                        const int64_t id = g.cell_begin + (x - g.roi_lo[0])
+                            + static_cast<int64_t>(g.roi_dim[0])
+                                * ((y - g.roi_lo[1]) + static_cast<int64_t>(g.roi_dim[1]) * (z - g.roi_lo[2]));
+                        seg_start[k] = cell_start[id];
+                        seg_prefix[k + 1] = seg_prefix[k] + static_cast<int32_t>(cell_start[id + 1] - cell_start[id]);
+                        ++k;
+                    }
+                }
+            }
+            nseg = k;
+        }
+        __syncthreads();
+        const int total = seg_prefix[nseg];
+        __syncthreads();
+        for (int base = 0; base < total; base += kChunk) {
+            const int len = min(kChunk, total - base);
+            for (int i = threadIdx.x; i < len; i += kBlock) {
+                const int gi = base + i;
+                int k = 0;
+                while (seg_prefix[k + 1] <= gi) ++k;
+                const int64_t b = seg_start[k] + (gi - seg_prefix[k]);
+                sx[i] = bx[b];
+                sy[i] = by[b];
+                sz[i] = bz[b];
+                st[i] = btype[b];
+                sb[i] = static_cast<uint32_t>(b);
+            }
+            __syncthreads();
+            for (int64_t ci = cs + wave; ci < ce; ci += kBlock / kWave) {
+                const int32_t atom = cell_centre_list[ci];
+                const double px = positions[atom * 3 + 0];
+                const double py = positions[atom * 3 + 1];
+                const double pz = positions[atom * 3 + 2];
+                int64_t cur[kMaxSpecies];
+                int32_t cnt[kMaxSpecies];
+#pragma unroll
+                for (int t = 0; t < kMaxSpecies; ++t) {
+                    cnt[t] = 0;
+                    cur[t] = 0;
+                }
+                if (kFill) {
+                    if (base == 0) {
+                        int64_t run = pair_start[atom];
+#pragma unroll
+                        for (int t = 0; t < kMaxSpecies; ++t) {
+                            if (t < S) {
+                                cur[t] = run;
+                                run += counts[static_cast<int64_t>(atom) * S + t];
+                            }
+                        }
+                    } else {
+#pragma unroll
+                        for (int t = 0; t < kMaxSpecies; ++t) {
+                            if (t < S) cur[t] = cursor[static_cast<int64_t>(atom) * S + t];
+                        }
+                    }
+                }
+                for (int j0 = 0; j0 < len; j0 += kWave) {
+                    const int j = j0 + lane;
+                    bool accept = false;
+                    int type = 0;
+                    if (j < len) {
+                        // displacement = image - centre; d^2 = (dx*dx + dy*dy) + dz*dz
+                        // (neighbor.cpp:569, math3.hpp:31-35), no contraction
+                        const double dx = sx[j] - px;
+                        const double dy = sy[j] - py;
+                        const double dz = sz[j] - pz;
+                        const double d2 = dx * dx + dy * dy + dz * dz;
+                        accept = include_boundary ? d2 <= cutoff2 : d2 < cutoff2;
+                        type = st[j];
+                    }
+#pragma unroll
+                    for (int t = 0; t < kMaxSpecies; ++t) {
+                        if (t < S) {
+                            const bool mine = accept && type == t;
+                            const uint64_t mask = __ballot(mine);
+                            if (kFill) {
+                                if (mine) pair_bin[cur[t] + __popcll(mask & below)] = sb[j];
+                                cur[t] += __popcll(mask);
+                            } else {
+                                cnt[t] += __popcll(mask);
+                            }
+                        }
+                    }
+                }
+                if (lane == 0) {
+#pragma unroll
+                    for (int t = 0; t < kMaxSpecies; ++t) {
+                        if (t < S) {
+                            if (kFill) cursor[static_cast<int64_t>(atom) * S + t] = cur[t];
+                            else counts[static_cast<int64_t>(atom) * S + t] += cnt[t];
+                        }
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+__global__ void k_totals(const int32_t* counts, int S, int64_t atoms, int32_t* totals) {
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < atoms;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        int32_t sum = 0;
+        for (int t = 0; t < S; ++t) sum += counts[i * S + t];
+        totals[i] = sum;
+    }
+}
+
+// ------------------------------------------------------------------ scan
+constexpr int kScanItems = 8;
+constexpr int kScanTile = kBlock * kScanItems;
+
+__device__ int64_t block_exclusive_scan(int64_t value, int64_t* lds, int64_t& total) {
+    lds[threadIdx.x] = value;
+    __syncthreads();
+    for (int offset = 1; offset < kBlock; offset *= 2) {
+        const int64_t add = threadIdx.x >= offset ? lds[threadIdx.x - offset] : 0;
+        __syncthreads();
+        lds[threadIdx.x] += add;
+        __syncthreads();
+    }
+    const int64_t inclusive = lds[threadIdx.x];
+    total = lds[kBlock - 1];
+    __syncthreads();
+    return inclusive - value;
+}
+
+__global__ __launch_bounds__(kBlock) void k_scan_reduce(const int32_t* in, int64_t n, int64_t* sums) {
+    __shared__ int64_t lds[kBlock];
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile;
+    int64_t local = 0;
+    for (int i = 0; i < kScanItems; ++i) {
+        const int64_t idx = base + static_cast<int64_t>(threadIdx.x) * kScanItems + i;
+        if (idx < n) local += in[idx];
+    }
+    int64_t total;
+    (void)block_exclusive_scan(local, lds, total);
+    if (threadIdx.x == 0) sums[blockIdx.x] = total;
+}
+
+__global__ __launch_bounds__(kBlock) void k_scan_blocks(int64_t* sums, int64_t nb) {
+    __shared__ int64_t lds[kBlock];
+    int64_t carry = 0;
+    for (int64_t base = 0; base < nb; base += kBlock) {
+        const int64_t idx = base + threadIdx.x;
+        const int64_t v = idx < nb ? sums[idx] : 0;
+        int64_t total;
+        const int64_t ex = block_exclusive_scan(v, lds, total);
+        if (idx < nb) sums[idx] = carry + ex;
+        carry += total;
+    }
+    if (threadIdx.x == 0) sums[nb] = carry;
+}
+
+__global__ __launch_bounds__(kBlock) void k_scan_apply(const int32_t* in, int64_t n, const int64_t* sums,
+                                                       int64_t nb, int64_t* out) {
+    __shared__ int64_t lds[kBlock];
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile;
+    int64_t vals[kScanItems];
+    int64_t local = 0;
+    for (int i = 0; i < kScanItems; ++i) {
+        const int64_t idx = base + static_cast<int64_t>(threadIdx.x) * kScanItems + i;
+        vals[i] = idx < n ? in[idx] : 0;
+        local += vals[i];
+    }
+    int64_t total;
+    int64_t run = sums[blockIdx.x] + block_exclusive_scan(local, lds, total);
+    for (int i = 0; i < kScanItems; ++i) {
+        const int64_t idx = base + static_cast<int64_t>(threadIdx.x) * kScanItems + i;
+        if (idx < n) out[idx] = run;
+        run += vals[i];
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) out[n] = sums[nb];
+}
+
+unsigned grid_for(int64_t work, int block = kBlock) {
+    const int64_t blocks = (work + block - 1) / block;
+    return static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(blocks, 1 << 20)));
+}
+
+} // namespace
+
+void scan_counts(hipStream_t stream, const int32_t* in, int64_t* out, int64_t n, DeviceBuffer& tmp) {
+    const int64_t nb = std::max<int64_t>(1, (n + kScanTile - 1) / kScanTile);
+    tmp.reserve(static_cast<size_t>(nb + 1) * sizeof(int64_t));
+    int64_t* sums = tmp.as<int64_t>();
+    hipLaunchKernelGGL(k_scan_reduce, dim3(static_cast<unsigned>(nb)), dim3(kBlock), 0, stream, in, n, sums);
+    hipLaunchKernelGGL(k_scan_blocks, dim3(1), dim3(kBlock), 0, stream, sums, nb);
+    hipLaunchKernelGGL(k_scan_apply, dim3(static_cast<unsigned>(nb)), dim3(kBlock), 0, stream, in, n, sums, nb,
+                       out);
+    MDX_HIP(hipGetLastError());
+}
+
+void prepare_batch(const mdx_batch_view& batch, const int32_t* species, int n_species, double cutoff,
+                   PreparedBatch& out) {
+    if (!std::isfinite(cutoff) || cutoff <= 0.0) {
+        throw Error(MDX_INVALID_ARGUMENT, "neighbor cutoff must be finite and positive");
+    }
+    validate_batch(batch);
+    if (batch.atoms > std::numeric_limits<int32_t>::max()) {
+        throw Error(MDX_INVALID_ARGUMENT, "neighbor atom index exceeds int32 range");
+    }
+    out.structures = batch.structures;
+    out.atoms = batch.atoms;
+    out.cutoff = cutoff;
+    out.n_species = species != nullptr ? n_species : 1;
+    out.offsets.assign(batch.offsets, batch.offsets + batch.structures + 1);
+    out.types.assign(static_cast<size_t>(batch.atoms), 0);
+    if (species != nullptr) {
+        std::unordered_map<int32_t, int32_t> map;
+        for (int t = 0; t < n_species; ++t) map.emplace(species[t], t);
+        for (int64_t i = 0; i < batch.atoms; ++i) {
+            const auto it = map.find(batch.numbers[i]);
+            if (it == map.end()) {
+                throw Error(MDX_INVALID_ARGUMENT, "batch contains an atomic number outside calculator species");
+            }
+            out.types[static_cast<size_t>(i)] = it->second;
+        }
+    }
+    out.geom.assign(static_cast<size_t>(batch.structures), StructGeom{});
+    out.images.clear();
+    int64_t ext = 0, cells = 0;
+    for (int64_t s = 0; s < batch.structures; ++s) {
+        StructGeom& g = out.geom[static_cast<size_t>(s)];
+        std::memset(&g, 0, sizeof(g));
+        const int64_t begin = batch.offsets[s];
+        const int64_t natoms = batch.offsets[s + 1] - begin;
+        g.atom_begin = begin;
+        g.natoms = static_cast<int32_t>(natoms);
+        g.ext_begin = ext;
+        g.cell_begin = cells;
+        g.image_begin = static_cast<int64_t>(out.images.size());
+        const double* cell = batch.cells + s * 9;
+        const bool periodic = batch.pbc[s * 3] == 1;
+        int bounds[3] = {0, 0, 0};
+        if (periodic) {
+            double inv[9];
+            if (!inverse3(cell, inv)) throw Error(MDX_INVALID_ARGUMENT, "cell matrix is singular");
+            for (int a = 0; a < 3; ++a) {
+                // neighbor.cpp:459-467
+                const double bound = std::floor(
+                    cutoff * std::sqrt(inv[0 * 3 + a] * inv[0 * 3 + a] + inv[1 * 3 + a] * inv[1 * 3 + a]
+                                       + inv[2 * 3 + a] * inv[2 * 3 + a])
+                    + 1.0);
+                if (!std::isfinite(bound) || bound < 0.0 || bound > 1024.0) {
+                    throw Error(MDX_INVALID_ARGUMENT, "periodic image range exceeds the device graph capacity");
+                }
+                bounds[a] = static_cast<int>(bound);
+            }
+        }
+        const int64_t n_images = static_cast<int64_t>(2 * bounds[0] + 1) * (2 * bounds[1] + 1) * (2 * bounds[2] + 1);
+        if (natoms * n_images > std::numeric_limits<int32_t>::max()) {
+            throw Error(MDX_INVALID_ARGUMENT, "periodic images exceed the device graph capacity");
+        }
+        g.n_images = static_cast<int32_t>(n_images);
+        for (int n0 = -bounds[0]; n0 <= bounds[0]; ++n0) {
+            for (int n1 = -bounds[1]; n1 <= bounds[1]; ++n1) {
+                for (int n2 = -bounds[2]; n2 <= bounds[2]; ++n2) {
+                    ImageDesc im{};
+                    for (int a = 0; a < 3; ++a) {
+                        // Vec3 shift = n0*row0 + n1*row1 + n2*row2 (neighbor.cpp:472-474)
+                        im.shift[a] = periodic ? (static_cast<double>(n0) * cell[0 * 3 + a]
+                                                  + static_cast<double>(n1) * cell[1 * 3 + a])
+                                                     + static_cast<double>(n2) * cell[2 * 3 + a]
+                                               : 0.0;
+                    }
+                    im.n[0] = n0;
+                    im.n[1] = n1;
+                    im.n[2] = n2;
+                    out.images.push_back(im);
+                }
+            }
+        }
+        if (natoms == 0) {
+            g.dims[0] = g.dims[1] = g.dims[2] = 1;
+            g.spacing[0] = g.spacing[1] = g.spacing[2] = cutoff;
+            continue;
+        }
+        ext += natoms * n_images;
+        // bounding box of every image (build_grid, neighbor.cpp:143-158); rounding
+        // is monotonic, so min over images of fl(min_j r_j + s) equals the
+        // minimum over all image positions.
+        for (int a = 0; a < 3; ++a) {
+            double lo = batch.positions[begin * 3 + a], hi = lo;
+            for (int64_t i = begin; i < begin + natoms; ++i) {
+                lo = std::min(lo, batch.positions[i * 3 + a]);
+                hi = std::max(hi, batch.positions[i * 3 + a]);
+            }
+            double mn = 0.0, mx = 0.0;
+            for (int64_t q = 0; q < n_images; ++q) {
+                const double sh = out.images[static_cast<size_t>(g.image_begin + q)].shift[a];
+                const double l2 = lo + sh, h2 = hi + sh;
+                if (q == 0 || l2 < mn) mn = l2;
+                if (q == 0 || h2 > mx) mx = h2;
+            }
+            mn -= 1e-10;
+            mx += 1e-10;
+            g.minimum[a] = mn;
+            const double range = mx - mn;
+            const double ncell = range / cutoff;
+            if (!std::isfinite(range) || range < 0.0 || !std::isfinite(ncell) || ncell > 1.0e6) {
+                throw Error(MDX_INVALID_ARGUMENT, "neighbor cell-grid dimension exceeds the device graph capacity");
+            }
+            g.dims[a] = std::max(1, static_cast<int>(ncell));
+            g.spacing[a] = std::max(cutoff, range / g.dims[a]);
+        }
+        // region of interest: cells within one cell of a centre
+        int lo_c[3] = {std::numeric_limits<int>::max(), std::numeric_limits<int>::max(), std::numeric_limits<int>::max()};
+        int hi_c[3] = {-1, -1, -1};
+        for (int64_t i = begin; i < begin + natoms; ++i) {
+            for (int a = 0; a < 3; ++a) {
+                const int c = grid_coordinate(batch.positions[i * 3 + a], g.minimum[a], g.spacing[a], g.dims[a]);
+                lo_c[a] = std::min(lo_c[a], c);
+                hi_c[a] = std::max(hi_c[a], c);
+            }
+        }
+        int64_t volume = 1;
+        for (int a = 0; a < 3; ++a) {
+            g.roi_lo[a] = std::max(0, lo_c[a] - 1);
+            const int hi = std::min(g.dims[a] - 1, hi_c[a] + 1);
+            g.roi_dim[a] = hi - g.roi_lo[a] + 1;
+            volume *= g.roi_dim[a];
+        }
+        cells += volume;
+        if (cells > (int64_t(1) << 30)) {
+            throw Error(MDX_INVALID_ARGUMENT, "neighbor cell-grid exceeds the device graph capacity");
+        }
+    }
+    if (ext >= (int64_t(1) << 32) - 1) {
+        throw Error(MDX_INVALID_ARGUMENT, "periodic images exceed the device graph capacity");
+    }
+    out.ext_total = ext;
+    out.cells_total = cells;
+}
+
+void upload_batch(hipStream_t stream, const mdx_batch_view& batch, PreparedBatch& pb) {
+    const size_t atoms = static_cast<size_t>(pb.atoms);
+    pb.d_positions.reserve(std::max<size_t>(1, atoms * 3 * sizeof(double)));
+    pb.d_types.reserve(std::max<size_t>(1, atoms * sizeof(int32_t)));
+    pb.d_geom.reserve(std::max<size_t>(1, pb.geom.size() * sizeof(StructGeom)));
+    pb.d_images.reserve(std::max<size_t>(1, pb.images.size() * sizeof(ImageDesc)));
+    pb.d_offsets.reserve(pb.offsets.size() * sizeof(int64_t));
+    if (atoms > 0) {
+        MDX_HIP(hipMemcpyAsync(pb.d_positions.ptr, batch.positions, atoms * 3 * sizeof(double),
+                               hipMemcpyHostToDevice, stream));
+        MDX_HIP(hipMemcpyAsync(pb.d_types.ptr, pb.types.data(), atoms * sizeof(int32_t), hipMemcpyHostToDevice,
+                               stream));
+    }
+    if (!pb.geom.empty()) {
+        MDX_HIP(hipMemcpyAsync(pb.d_geom.ptr, pb.geom.data(), pb.geom.size() * sizeof(StructGeom),
+                               hipMemcpyHostToDevice, stream));
+    }
+    if (!pb.images.empty()) {
+        MDX_HIP(hipMemcpyAsync(pb.d_images.ptr, pb.images.data(), pb.images.size() * sizeof(ImageDesc),
+                               hipMemcpyHostToDevice, stream));
+    }
+    MDX_HIP(hipMemcpyAsync(pb.d_offsets.ptr, pb.offsets.data(), pb.offsets.size() * sizeof(int64_t),
+                           hipMemcpyHostToDevice, stream));
+    // pageable sources: the copies are staged synchronously by the runtime,
+    // but wait so the host vectors may change after return
+    MDX_HIP(hipStreamSynchronize(stream));
+}
+
+int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr, const volatile int32_t* cancel) {
+    const int S = pb.n_species;
+    gr.n_species = S;
+    const int64_t atoms = pb.atoms;
+    const int64_t cells = pb.cells_total;
+    const int64_t nstruct = pb.structures;
+    const size_t cells1 = static_cast<size_t>(cells + 1);
+    gr.pair_start.reserve(static_cast<size_t>(atoms + 1) * sizeof(int64_t));
+    if (atoms == 0 || cells == 0) {
+        MDX_HIP(hipMemsetAsync(gr.pair_start.ptr, 0, static_cast<size_t>(atoms + 1) * sizeof(int64_t), stream));
+        gr.counts.reserve(std::max<size_t>(1, static_cast<size_t>(atoms * S) * sizeof(int32_t)));
+        gr.pairs = 0;
+        gr.binned = 0;
+        return 0;
+    }
+    const StructGeom* geom = pb.d_geom.as<StructGeom>();
+    const ImageDesc* images = pb.d_images.as<ImageDesc>();
+    const double* pos = pb.d_positions.as<double>();
+    const int64_t ext = pb.ext_total;
+
+    gr.cell_count.reserve(cells1 * sizeof(int32_t));
+    gr.cell_fill.reserve(cells1 * sizeof(int32_t));
+    gr.cell_start.reserve(cells1 * sizeof(int64_t));
+    gr.cell_centre_count.reserve(cells1 * sizeof(int32_t));
+    gr.cell_centre_fill.reserve(cells1 * sizeof(int32_t));
+    gr.cell_centre_start.reserve(cells1 * sizeof(int64_t));
+    gr.cell_centre_list.reserve(static_cast<size_t>(atoms) * sizeof(int32_t));
+    gr.centre_cell.reserve(static_cast<size_t>(atoms) * sizeof(int64_t));
+    gr.bin_key.reserve(static_cast<size_t>(ext) * sizeof(uint32_t));
+    gr.bin_x.reserve(static_cast<size_t>(ext) * sizeof(double));
+    gr.bin_y.reserve(static_cast<size_t>(ext) * sizeof(double));
+    gr.bin_z.reserve(static_cast<size_t>(ext) * sizeof(double));
+    gr.bin_atom.reserve(static_cast<size_t>(ext) * sizeof(int32_t));
+    gr.bin_image.reserve(static_cast<size_t>(ext) * sizeof(int32_t));
+    gr.bin_type.reserve(static_cast<size_t>(ext) * sizeof(int32_t));
+    gr.counts.reserve(static_cast<size_t>(atoms * S) * sizeof(int32_t));
+    gr.cursor.reserve(static_cast<size_t>(atoms * S) * sizeof(int64_t));
+    gr.totals.reserve(static_cast<size_t>(atoms) * sizeof(int32_t));
+    gr.error_flag.reserve(sizeof(int32_t));
+    MDX_HIP(hipMemsetAsync(gr.error_flag.ptr, 0, sizeof(int32_t), stream));
+
+    MDX_HIP(hipMemsetAsync(gr.cell_count.ptr, 0, cells1 * sizeof(int32_t), stream));
+    MDX_HIP(hipMemsetAsync(gr.cell_fill.ptr, 0, cells1 * sizeof(int32_t), stream));
+    MDX_HIP(hipMemsetAsync(gr.cell_centre_count.ptr, 0, cells1 * sizeof(int32_t), stream));
+    MDX_HIP(hipMemsetAsync(gr.cell_centre_fill.ptr, 0, cells1 * sizeof(int32_t), stream));
+    MDX_HIP(hipMemsetAsync(gr.counts.ptr, 0, static_cast<size_t>(atoms * S) * sizeof(int32_t), stream));
+
+    hipLaunchKernelGGL(k_bin_count, dim3(grid_for(ext)), dim3(kBlock), 0, stream, geom, nstruct, images, pos, ext,
+                       gr.cell_count.as<int32_t>());
+    scan_counts(stream, gr.cell_count.as<int32_t>(), gr.cell_start.as<int64_t>(), cells, gr.scan_tmp);
+    hipLaunchKernelGGL(k_bin_fill, dim3(grid_for(ext)), dim3(kBlock), 0, stream, geom, nstruct, images, pos, ext,
+                       gr.cell_start.as<int64_t>(), gr.cell_fill.as<int32_t>(), gr.bin_key.as<uint32_t>());
+    const unsigned cell_grid = static_cast<unsigned>(std::min<int64_t>(cells, 1 << 20));
+    hipLaunchKernelGGL(k_bin_sort, dim3(cell_grid), dim3(kBlock), 0, stream, geom, nstruct, images, pos,
+                       pb.d_types.as<int32_t>(), gr.cell_start.as<int64_t>(), cells, gr.bin_key.as<uint32_t>(),
+                       gr.bin_x.as<double>(), gr.bin_y.as<double>(), gr.bin_z.as<double>(), gr.bin_atom.as<int32_t>(),
+                       gr.bin_image.as<int32_t>(), gr.bin_type.as<int32_t>());
+    hipLaunchKernelGGL(k_centre_cell, dim3(grid_for(atoms)), dim3(kBlock), 0, stream, geom, nstruct, pos, atoms,
+                       gr.centre_cell.as<int64_t>(), gr.cell_centre_count.as<int32_t>(), gr.error_flag.as<int32_t>());
+    scan_counts(stream, gr.cell_centre_count.as<int32_t>(), gr.cell_centre_start.as<int64_t>(), cells, gr.scan_tmp);
+    hipLaunchKernelGGL(k_centre_fill, dim3(grid_for(atoms)), dim3(kBlock), 0, stream, gr.centre_cell.as<int64_t>(),
+                       atoms, gr.cell_centre_start.as<int64_t>(), gr.cell_centre_fill.as<int32_t>(),
+                       gr.cell_centre_list.as<int32_t>());
+    MDX_HIP(hipGetLastError());
+    if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
+
+    const double cutoff2 = pb.cutoff * pb.cutoff;
+    hipLaunchKernelGGL(k_pair_pass<false>, dim3(cell_grid), dim3(kBlock), 0, stream, geom, nstruct, pos,
+                       gr.cell_start.as<int64_t>(), gr.cell_centre_start.as<int64_t>(), gr.cell_centre_list.as<int32_t>(),
+                       cells, gr.bin_x.as<double>(), gr.bin_y.as<double>(), gr.bin_z.as<double>(),
+                       gr.bin_type.as<int32_t>(), S, cutoff2, pb.include_boundary, gr.counts.as<int32_t>(), nullptr, nullptr,
+                       nullptr);
+    hipLaunchKernelGGL(k_totals, dim3(grid_for(atoms)), dim3(kBlock), 0, stream, gr.counts.as<int32_t>(), S, atoms,
+                       gr.totals.as<int32_t>());
+    scan_counts(stream, gr.totals.as<int32_t>(), gr.pair_start.as<int64_t>(), atoms, gr.scan_tmp);
+    MDX_HIP(hipGetLastError());
+    int64_t pairs = 0;
+    MDX_HIP(hipMemcpyAsync(&pairs, gr.pair_start.as<int64_t>() + atoms, sizeof(int64_t), hipMemcpyDeviceToHost,
+                           stream));
+    int64_t binned = 0;
+    MDX_HIP(hipMemcpyAsync(&binned, gr.cell_start.as<int64_t>() + cells, sizeof(int64_t), hipMemcpyDeviceToHost,
+                           stream));
+    int32_t flag = 0;
+    MDX_HIP(hipMemcpyAsync(&flag, gr.error_flag.ptr, sizeof(int32_t), hipMemcpyDeviceToHost, stream));
+    MDX_HIP(hipStreamSynchronize(stream));
+    if (flag != 0) throw Error(MDX_INTERNAL, "a centre fell outside its structure's cell grid");
+    if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
+    if (pairs >= (int64_t(1) << 40)) throw Error(MDX_INTERNAL, "implausible neighbour pair count");
+    gr.pair_bin.reserve(std::max<size_t>(1, static_cast<size_t>(pairs) * sizeof(uint32_t)));
+    hipLaunchKernelGGL(k_pair_pass<true>, dim3(cell_grid), dim3(kBlock), 0, stream, geom, nstruct, pos,
+                       gr.cell_start.as<int64_t>(), gr.cell_centre_start.as<int64_t>(), gr.cell_centre_list.as<int32_t>(),
+                       cells, gr.bin_x.as<double>(), gr.bin_y.as<double>(), gr.bin_z.as<double>(),
+                       gr.bin_type.as<int32_t>(), S, cutoff2, pb.include_boundary, gr.counts.as<int32_t>(), gr.pair_start.as<int64_t>(),
+                       gr.cursor.as<int64_t>(), gr.pair_bin.as<uint32_t>());
+    MDX_HIP(hipGetLastError());
+    gr.pairs = pairs;
+    gr.binned = binned;
+    return pairs;
+}
+
+} // namespace mdx

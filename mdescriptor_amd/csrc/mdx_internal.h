@@ -1,0 +1,178 @@
+// Internal declarations shared by the gfx950 translation units of the SOAP
+// library.  Compiled with -ffp-contract=off: every fused multiply-add in the
+// device code is written out with fma(), so the geometry arithmetic
+// (image shifts, displacements, squared distances) rounds exactly like the
+// reference's C++ (cpp/src/common/neighbor.cpp:471-478, 569;
+// cpp/include/mdescriptor/detail/math3.hpp:19-35).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/mdx_hip.h"
+
+namespace mdx {
+
+constexpr int kMaxSpecies = 16;   // species per SOAP plan handled on the device
+constexpr int kMaxNmax = 16;      // radial channels per (species, l)
+constexpr int kMaxLmax = 20;      // as the reference's parameter check (soap.cpp:1153-1154)
+constexpr int kBlock = 256;       // threads per workgroup of the graph and SOAP kernels
+constexpr int kWave = 64;         // CDNA wavefront width
+constexpr int kChunk = 1024;      // candidates staged in LDS per graph chunk
+
+// Error carrying one of the C-ABI status codes; thrown inside the library and
+// converted to a status at the extern "C" boundary.
+struct Error : std::runtime_error {
+    int status;
+    Error(int code, const std::string& message) : std::runtime_error(message), status(code) {}
+};
+
+void check_hip(hipError_t code, const char* what);
+#define MDX_HIP(call) ::mdx::check_hip((call), #call)
+
+// Grow-only device buffer.  Reallocated only when a larger size is asked for.
+struct DeviceBuffer {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    void reserve(size_t size);
+    void release();
+    template <typename T> T* as() const { return static_cast<T*>(ptr); }
+    ~DeviceBuffer() { release(); }
+    DeviceBuffer() = default;
+    DeviceBuffer(const DeviceBuffer&) = delete;
+    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+};
+
+// One structure's cell-grid geometry, as seen by the device.  The grid is the
+// reference's (build_grid, neighbor.cpp:135-194) over every periodic image of
+// the structure; only the box of cells within one cell of a centre (the
+// "region of interest") is materialised.
+struct StructGeom {
+    int64_t atom_begin;  // first atom of the structure in the batch
+    int64_t ext_begin;   // first index of the structure in image-major enumeration space
+    int64_t cell_begin;  // first global ROI cell of the structure
+    int64_t image_begin; // first entry of the structure in the image table
+    int32_t natoms;
+    int32_t n_images;
+    int32_t dims[3];     // full grid dimensions
+    int32_t roi_lo[3];   // ROI box origin (grid coordinates)
+    int32_t roi_dim[3];  // ROI box extent
+    int32_t pad;
+    double minimum[3];   // grid origin (bounding box minus padding)
+    double spacing[3];   // cell widths
+};
+
+// Periodic image: integer shift and its Cartesian vector, computed on the
+// host as ((n0*a + n1*b) + n2*c) per component (neighbor.cpp:472-474).
+struct ImageDesc {
+    double shift[3];
+    int32_t n[3];
+    int32_t pad;
+};
+
+// Host-side prepared batch: geometry plus device copies of the inputs.
+struct PreparedBatch {
+    int64_t structures = 0;
+    int64_t atoms = 0;
+    int64_t ext_total = 0;   // sum over structures of natoms * n_images
+    int64_t cells_total = 0; // ROI cells over all structures
+    double cutoff = 0.0;
+    int include_boundary = 1;  // d^2 <= cutoff^2 (1) or d^2 < cutoff^2 (0), neighbor.cpp:553-555
+    std::vector<StructGeom> geom;
+    std::vector<ImageDesc> images;
+    std::vector<int32_t> types; // species index per atom (0 when species are ignored)
+    std::vector<int64_t> offsets;
+    int n_species = 1;
+    DeviceBuffer d_positions; // f64[atoms*3]
+    DeviceBuffer d_types;     // i32[atoms]
+    DeviceBuffer d_geom;      // StructGeom[structures]
+    DeviceBuffer d_images;    // ImageDesc[...]
+    DeviceBuffer d_offsets;   // i64[structures+1]
+};
+
+// Device graph (kernel 1 output).  Pairs are indices into the cell-sorted
+// binned image arrays; rows are grouped by neighbour species when
+// n_species > 1 and keep the reference's candidate order inside a species.
+struct DeviceGraph {
+    int64_t binned = 0;
+    int64_t pairs = 0;
+    int n_species = 1;
+    DeviceBuffer cell_count, cell_start, cell_fill; // per ROI cell
+    DeviceBuffer bin_key;                           // unsorted keys, then scratch
+    DeviceBuffer bin_x, bin_y, bin_z;               // f64 positions of binned images (sorted)
+    DeviceBuffer bin_atom;                          // i32 global atom index
+    DeviceBuffer bin_image;                         // i32 global image index
+    DeviceBuffer bin_type;                          // i32 species index
+    DeviceBuffer centre_cell;                       // i64 per atom
+    DeviceBuffer cell_centre_count, cell_centre_start, cell_centre_fill, cell_centre_list;
+    DeviceBuffer counts;     // i32[atoms * n_species]
+    DeviceBuffer totals;     // i32[atoms]
+    DeviceBuffer pair_start; // i64[atoms + 1]
+    DeviceBuffer cursor;     // i64[atoms * n_species]
+    DeviceBuffer pair_bin;   // u32[pairs]
+    DeviceBuffer scan_tmp;   // block sums of the scans
+    DeviceBuffer error_flag; // i32, set by a kernel on an internal inconsistency
+};
+
+// Build (or rebuild) the device graph of a prepared batch at pb.cutoff.
+// Returns the pair count.  Polls cancel between launches.
+int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& graph,
+                    const volatile int32_t* cancel);
+
+// Exclusive scan of n int32 counts into n+1 int64 offsets (out[n] = total).
+void scan_counts(hipStream_t stream, const int32_t* in, int64_t* out, int64_t n, DeviceBuffer& tmp);
+
+// Prepare a batch on the host (validation, species map, image tables, grid
+// geometry) for cutoff; species may be null (all atoms one species).
+void prepare_batch(const mdx_batch_view& batch, const int32_t* species, int n_species, double cutoff,
+                   PreparedBatch& out);
+void upload_batch(hipStream_t stream, const mdx_batch_view& batch, PreparedBatch& pb);
+
+} // namespace mdx
+
+// Opaque C-ABI objects.
+struct mdx_hip_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::mutex mutex;
+    std::string last_error;
+    mdx::PreparedBatch scratch_batch; // used by mdx_hip_soap_compute / neighbors
+    mdx::DeviceGraph graph;
+    mdx::DeviceBuffer out_dev;        // device result of mdx_hip_soap_compute
+    mdx::DeviceBuffer partials;       // inner/outer partial sums
+    void* pinned = nullptr;           // pinned staging for the result download
+    size_t pinned_bytes = 0;
+    hipEvent_t events[8] = {};
+};
+
+struct mdx_soap_plan {
+    int device = 0;
+    int S = 0, n = 0, l_max = 0, L = 0, H = 0, LN = 0;
+    int average = 0, out_dtype = 8;
+    double r_cut = 0.0, sigma = 0.0, cutoff = 0.0;
+    int64_t features = 0, coeff_size = 0;
+    std::vector<int32_t> species;
+    mdx::DeviceBuffer d_pref, d_expo, d_beta, d_ps_pref; // radial prefactors/exponents, scaled beta, PS prefactors
+    mdx::DeviceBuffer d_feat_a, d_feat_b;                // feature table: (c row offsets, l)
+    mdx::DeviceBuffer d_hnorm;                           // harmonic normalisation N_lm (x sqrt(2) for m > 0)
+};
+
+struct mdx_device_batch {
+    int device = 0;
+    mdx::PreparedBatch pb;
+    mdx::DeviceGraph graph;
+    mdx::DeviceBuffer partials;
+};
+
+namespace mdx {
+// Run the SOAP kernels (2-4) of a plan over a prepared batch whose graph is
+// built; output rows x features in device memory with the given pitch.
+void run_soap(hipStream_t stream, const mdx_soap_plan& plan, const PreparedBatch& pb,
+              const DeviceGraph& graph, void* out_device, int64_t pitch_bytes, DeviceBuffer& partials,
+              const volatile int32_t* cancel, hipEvent_t* events, mdx_timing* timing);
+} // namespace mdx

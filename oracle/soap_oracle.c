@@ -1,0 +1,857 @@
+/*
+ * TEST INFRASTRUCTURE ONLY — the CPU oracle for the SOAP hot path.
+ *
+ * A plain-C restatement of the reference's neighbour graph and GTO SOAP
+ * (nicheal/MDescriptor, C++17/OpenMP).  Only tests/, __graft_entry__.smoke()
+ * and bench.py's cpu_baseline leg may load this library, and only as the
+ * checker or the timed CPU baseline.  The product path (mdescriptor_amd)
+ * never links, imports or calls it.
+ *
+ * Each function names the reference file:line it follows.  Parity status of
+ * every function is pinned by tests (see tests/test_oracle_*.py):
+ *   graph        : brute-force closed form over shifts, the reference's
+ *                  NeighborList golden (448 pairs), boundary KATs, and the
+ *                  reference C++ compiled in place (oracle/_ref)
+ *   harmonics    : scipy sph_harm x r^l, orthonormality on a quadrature grid
+ *   soap         : the reference's SOAP goldens (project + DScribe sidecar),
+ *                  single-atom closed form, and oracle/_ref
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define MDXO_PI 3.141592653589793238462643383279502884
+#define MDXO_SQRT2 1.414213562373095048801688724209698079
+
+/* status codes mirror the C-ABI of the product library */
+enum { MDXO_OK = 0, MDXO_INVALID = 1, MDXO_NOMEM = 2, MDXO_CANCELLED = 4 };
+
+static void set_error(char* err, int errlen, const char* message) {
+    if (err != NULL && errlen > 0) {
+        snprintf(err, (size_t)errlen, "%s", message);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* 3x3 helpers: cpp/include/mdescriptor/detail/math3.hpp:46-68              */
+/* ------------------------------------------------------------------------ */
+static double det3(const double* m) {
+    return m[0] * (m[4] * m[8] - m[5] * m[7])
+        - m[1] * (m[3] * m[8] - m[5] * m[6])
+        + m[2] * (m[3] * m[7] - m[4] * m[6]);
+}
+
+static int inverse3(const double* m, double* r) {
+    const double d = det3(m);
+    if (!isfinite(d) || fabs(d) < 1e-14) return 0;
+    r[0] = (m[4] * m[8] - m[5] * m[7]) / d;
+    r[1] = (m[2] * m[7] - m[1] * m[8]) / d;
+    r[2] = (m[1] * m[5] - m[2] * m[4]) / d;
+    r[3] = (m[5] * m[6] - m[3] * m[8]) / d;
+    r[4] = (m[0] * m[8] - m[2] * m[6]) / d;
+    r[5] = (m[2] * m[3] - m[0] * m[5]) / d;
+    r[6] = (m[3] * m[7] - m[4] * m[6]) / d;
+    r[7] = (m[1] * m[6] - m[0] * m[7]) / d;
+    r[8] = (m[0] * m[4] - m[1] * m[3]) / d;
+    return 1;
+}
+
+/* batch validation: cpp/include/mdescriptor/detail/batch.hpp:19-80 */
+static int validate_batch(const int32_t* numbers, const double* positions, const double* cells,
+                          const int32_t* pbc, const int64_t* offsets, int64_t structures,
+                          int64_t atoms, char* err, int errlen) {
+    if (structures < 0 || atoms < 0 || offsets == NULL) {
+        set_error(err, errlen, "invalid structure batch");
+        return 0;
+    }
+    if (structures == 0) {
+        if (atoms != 0 || offsets[0] != 0) {
+            set_error(err, errlen, "empty structure batch has non-empty atom data");
+            return 0;
+        }
+        return 1;
+    }
+    if (offsets[0] != 0 || offsets[structures] != atoms) {
+        set_error(err, errlen, "offsets do not describe the flattened arrays");
+        return 0;
+    }
+    for (int64_t s = 0; s < structures; ++s) {
+        if (offsets[s] < 0 || offsets[s] > offsets[s + 1] || offsets[s + 1] > atoms) {
+            set_error(err, errlen, "offsets must be monotonic");
+            return 0;
+        }
+        int periodic = 1, isolated = 1;
+        for (int a = 0; a < 3; ++a) {
+            const int32_t f = pbc[s * 3 + a];
+            if (f != 0 && f != 1) {
+                set_error(err, errlen, "pbc must contain only 0 or 1");
+                return 0;
+            }
+            periodic = periodic && f == 1;
+            isolated = isolated && f == 0;
+        }
+        if (!periodic && !isolated) {
+            set_error(err, errlen, "mixed periodicity is not supported; use all-zero or all-one pbc");
+            return 0;
+        }
+        const double* cell = cells + s * 9;
+        for (int i = 0; i < 9; ++i) {
+            if (!isfinite(cell[i])) {
+                set_error(err, errlen, "cells must be finite");
+                return 0;
+            }
+        }
+        const double d = det3(cell);
+        if (periodic && (!isfinite(d) || fabs(d) < 1e-14)) {
+            set_error(err, errlen, "cells must be nonsingular");
+            return 0;
+        }
+    }
+    for (int64_t i = 0; i < atoms; ++i) {
+        if (numbers[i] <= 0) {
+            set_error(err, errlen, "atomic numbers must be positive");
+            return 0;
+        }
+        for (int a = 0; a < 3; ++a) {
+            if (!isfinite(positions[i * 3 + a])) {
+                set_error(err, errlen, "positions must be finite");
+                return 0;
+            }
+        }
+    }
+    return 1;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Neighbour graph: cpp/src/common/neighbor.cpp:423-679 (image-extended     */
+/* path, store_shifts = true, use_scaled_periodic_images = false)           */
+/* ------------------------------------------------------------------------ */
+typedef struct {
+    int32_t atom;
+    int32_t shift[3];
+    double pos[3];
+} ext_atom;
+
+typedef struct {
+    double minimum[3];
+    double spacing[3];
+    int dims[3];
+    int64_t* offsets; /* cell_count + 1 */
+    int32_t* atoms;   /* extended indices, cell-major, extended order within a cell */
+} cell_grid;
+
+/* CellGrid::coordinate, neighbor.cpp:122-132 */
+static int grid_coordinate(const cell_grid* g, double value, int axis) {
+    const double scaled = (value - g->minimum[axis]) / g->spacing[axis];
+    if (!(scaled > 0.0)) return 0;
+    if (!isfinite(scaled) || scaled >= (double)g->dims[axis]) return g->dims[axis] - 1;
+    return (int)scaled;
+}
+
+static int64_t grid_index(const cell_grid* g, int x, int y, int z) {
+    return (int64_t)x + (int64_t)g->dims[0] * ((int64_t)y + (int64_t)g->dims[1] * (int64_t)z);
+}
+
+/* build_grid, neighbor.cpp:135-194 */
+static int build_grid(const ext_atom* ext, int64_t n_ext, double cutoff, cell_grid* g,
+                      char* err, int errlen) {
+    memset(g, 0, sizeof(*g));
+    g->dims[0] = g->dims[1] = g->dims[2] = 1;
+    if (n_ext == 0) {
+        g->offsets = (int64_t*)calloc(2, sizeof(int64_t));
+        return g->offsets != NULL;
+    }
+    double mn[3], mx[3];
+    for (int a = 0; a < 3; ++a) mn[a] = mx[a] = ext[0].pos[a];
+    for (int64_t i = 0; i < n_ext; ++i) {
+        for (int a = 0; a < 3; ++a) {
+            if (ext[i].pos[a] < mn[a]) mn[a] = ext[i].pos[a];
+            if (ext[i].pos[a] > mx[a]) mx[a] = ext[i].pos[a];
+        }
+    }
+    const double padding = 1e-10;
+    for (int a = 0; a < 3; ++a) {
+        mn[a] -= padding;
+        mx[a] += padding;
+        g->minimum[a] = mn[a];
+        const double range = mx[a] - mn[a];
+        const double cells = range / cutoff;
+        if (!isfinite(range) || range < 0.0 || !isfinite(cells) || cells > 2147483647.0) {
+            set_error(err, errlen, "neighbor cell-grid dimension exceeds integer range");
+            return 0;
+        }
+        g->dims[a] = (int)cells < 1 ? 1 : (int)cells;
+        const double even = range / g->dims[a];
+        g->spacing[a] = cutoff > even ? cutoff : even;
+    }
+    const int64_t cell_count = (int64_t)g->dims[0] * g->dims[1] * g->dims[2];
+    if (cell_count > ((int64_t)1 << 34)) {
+        set_error(err, errlen, "neighbor cell-grid is too large");
+        return 0;
+    }
+    int64_t* counts = (int64_t*)calloc((size_t)cell_count, sizeof(int64_t));
+    g->offsets = (int64_t*)calloc((size_t)cell_count + 1, sizeof(int64_t));
+    g->atoms = (int32_t*)malloc((size_t)n_ext * sizeof(int32_t));
+    int64_t* fill = (int64_t*)calloc((size_t)cell_count, sizeof(int64_t));
+    int64_t* cell_of = (int64_t*)malloc((size_t)n_ext * sizeof(int64_t));
+    if (!counts || !g->offsets || !g->atoms || !fill || !cell_of) {
+        free(counts); free(fill); free(cell_of);
+        set_error(err, errlen, "out of memory");
+        return 0;
+    }
+    for (int64_t i = 0; i < n_ext; ++i) {
+        cell_of[i] = grid_index(g, grid_coordinate(g, ext[i].pos[0], 0),
+                                grid_coordinate(g, ext[i].pos[1], 1),
+                                grid_coordinate(g, ext[i].pos[2], 2));
+        counts[cell_of[i]]++;
+    }
+    for (int64_t c = 0; c < cell_count; ++c) g->offsets[c + 1] = g->offsets[c] + counts[c];
+    for (int64_t i = 0; i < n_ext; ++i) {
+        const int64_t c = cell_of[i];
+        g->atoms[g->offsets[c] + fill[c]++] = (int32_t)i;
+    }
+    free(counts);
+    free(fill);
+    free(cell_of);
+    return 1;
+}
+
+static void free_grid(cell_grid* g) {
+    free(g->offsets);
+    free(g->atoms);
+    g->offsets = NULL;
+    g->atoms = NULL;
+}
+
+typedef struct {
+    int64_t count, capacity;
+    int32_t* atoms;
+    int32_t* shifts;
+    double* disp;
+    double* d2;
+} pair_buffer;
+
+static int pair_push(pair_buffer* b, int32_t atom, const int32_t* shift, const double* disp, double d2) {
+    if (b->count == b->capacity) {
+        const int64_t cap = b->capacity ? b->capacity * 2 : 256;
+        int32_t* na = (int32_t*)realloc(b->atoms, (size_t)cap * sizeof(int32_t));
+        if (na) b->atoms = na;
+        int32_t* ns = (int32_t*)realloc(b->shifts, (size_t)cap * 3 * sizeof(int32_t));
+        if (ns) b->shifts = ns;
+        double* nd = (double*)realloc(b->disp, (size_t)cap * 3 * sizeof(double));
+        if (nd) b->disp = nd;
+        double* n2 = (double*)realloc(b->d2, (size_t)cap * sizeof(double));
+        if (n2) b->d2 = n2;
+        if (!na || !ns || !nd || !n2) return 0;
+        b->capacity = cap;
+    }
+    const int64_t i = b->count++;
+    b->atoms[i] = atom;
+    b->shifts[i * 3 + 0] = shift[0];
+    b->shifts[i * 3 + 1] = shift[1];
+    b->shifts[i * 3 + 2] = shift[2];
+    b->disp[i * 3 + 0] = disp[0];
+    b->disp[i * 3 + 1] = disp[1];
+    b->disp[i * 3 + 2] = disp[2];
+    b->d2[i] = d2;
+    return 1;
+}
+
+static void pair_free(pair_buffer* b) {
+    free(b->atoms);
+    free(b->shifts);
+    free(b->disp);
+    free(b->d2);
+    memset(b, 0, sizeof(*b));
+}
+
+/*
+ * Graph of one structure.  Atom indices are those of the batch passed in
+ * (global indices for a multi-structure batch, neighbor.cpp:475-497).
+ * offsets[local] / offsets[local+1] delimit the rows of centre `local`.
+ * Candidates are visited in the reference order: 3x3x3 cells z-major, then y,
+ * then x, and extended order inside a cell (neighbor.cpp:558-574).
+ */
+static int build_structure_graph(const double* positions, const double* cell, const int32_t* pbc,
+                                 int64_t begin, int64_t end, double cutoff, int include_boundary,
+                                 int64_t* offsets_out, pair_buffer* pairs, char* err, int errlen) {
+    const int64_t n = end - begin;
+    const int periodic = pbc[0] == 1 && pbc[1] == 1 && pbc[2] == 1;
+    int bounds[3] = {0, 0, 0};
+    if (periodic) {
+        double inv[9];
+        if (!inverse3(cell, inv)) {
+            set_error(err, errlen, "cell matrix is singular");
+            return 0;
+        }
+        for (int a = 0; a < 3; ++a) {
+            const double norm = sqrt(inv[0 * 3 + a] * inv[0 * 3 + a] + inv[1 * 3 + a] * inv[1 * 3 + a]
+                                     + inv[2 * 3 + a] * inv[2 * 3 + a]);
+            const double bound = floor(cutoff * norm + 1.0);
+            if (!isfinite(bound) || bound < 0.0 || bound > 2147483647.0) {
+                set_error(err, errlen, "periodic image range exceeds integer range");
+                return 0;
+            }
+            bounds[a] = (int)bound;
+        }
+    }
+    const int64_t images = (int64_t)(2 * bounds[0] + 1) * (2 * bounds[1] + 1) * (2 * bounds[2] + 1);
+    const int64_t n_ext = images * n;
+    ext_atom* ext = (ext_atom*)malloc((size_t)(n_ext > 0 ? n_ext : 1) * sizeof(ext_atom));
+    if (!ext) {
+        set_error(err, errlen, "out of memory");
+        return 0;
+    }
+    int64_t e = 0;
+    /* extended list, neighbor.cpp:471-529: n0 outer, n2 inner, atoms innermost */
+    for (int n0 = -bounds[0]; n0 <= bounds[0]; ++n0) {
+        for (int n1 = -bounds[1]; n1 <= bounds[1]; ++n1) {
+            for (int n2 = -bounds[2]; n2 <= bounds[2]; ++n2) {
+                double shift[3];
+                for (int a = 0; a < 3; ++a) {
+                    shift[a] = ((double)n0 * cell[0 * 3 + a] + (double)n1 * cell[1 * 3 + a])
+                        + (double)n2 * cell[2 * 3 + a];
+                }
+                for (int64_t atom = begin; atom < end; ++atom) {
+                    ext[e].atom = (int32_t)atom;
+                    ext[e].shift[0] = n0;
+                    ext[e].shift[1] = n1;
+                    ext[e].shift[2] = n2;
+                    for (int a = 0; a < 3; ++a) ext[e].pos[a] = positions[atom * 3 + a] + shift[a];
+                    ++e;
+                }
+            }
+        }
+    }
+    cell_grid grid;
+    if (!build_grid(ext, n_ext, cutoff, &grid, err, errlen)) {
+        free(ext);
+        free_grid(&grid);
+        return 0;
+    }
+    const double cutoff2 = cutoff * cutoff;
+    for (int64_t local = 0; local < n; ++local) {
+        offsets_out[local] = pairs->count;
+        const double* c = positions + (begin + local) * 3;
+        const int ix = grid_coordinate(&grid, c[0], 0);
+        const int iy = grid_coordinate(&grid, c[1], 1);
+        const int iz = grid_coordinate(&grid, c[2], 2);
+        for (int z = iz - 1 < 0 ? 0 : iz - 1; z <= (iz + 1 < grid.dims[2] - 1 ? iz + 1 : grid.dims[2] - 1); ++z) {
+            for (int y = iy - 1 < 0 ? 0 : iy - 1; y <= (iy + 1 < grid.dims[1] - 1 ? iy + 1 : grid.dims[1] - 1); ++y) {
+                for (int x = ix - 1 < 0 ? 0 : ix - 1; x <= (ix + 1 < grid.dims[0] - 1 ? ix + 1 : grid.dims[0] - 1); ++x) {
+                    const int64_t cidx = grid_index(&grid, x, y, z);
+                    for (int64_t o = grid.offsets[cidx]; o < grid.offsets[cidx + 1]; ++o) {
+                        const ext_atom* nb = &ext[grid.atoms[o]];
+                        double d[3];
+                        d[0] = nb->pos[0] - c[0];
+                        d[1] = nb->pos[1] - c[1];
+                        d[2] = nb->pos[2] - c[2];
+                        const double dd = d[0] * d[0] + d[1] * d[1] + d[2] * d[2];
+                        const int keep = include_boundary ? dd <= cutoff2 : dd < cutoff2;
+                        if (!keep) continue;
+                        if (!pair_push(pairs, nb->atom, nb->shift, d, dd)) {
+                            free(ext);
+                            free_grid(&grid);
+                            set_error(err, errlen, "out of memory");
+                            return 0;
+                        }
+                    }
+                }
+            }
+        }
+    }
+    offsets_out[n] = pairs->count;
+    free(ext);
+    free_grid(&grid);
+    return 1;
+}
+
+/* Result of mdxo_graph_build; all arrays malloc'd and owned by the caller. */
+typedef struct {
+    int64_t atoms_count;
+    int64_t pairs;
+    int64_t* offsets;
+    int32_t* atoms;
+    int32_t* shifts;
+    double* disp;
+    double* d2;
+} mdxo_graph;
+
+/* build_neighbor_graph, neighbor.cpp:703-768: per-structure graphs
+ * concatenated in structure order, atom indices global to the batch. */
+int mdxo_graph_build(const int32_t* numbers, const double* positions, const double* cells,
+                     const int32_t* pbc, const int64_t* offsets, int64_t structures, int64_t atoms,
+                     double cutoff, int include_boundary, mdxo_graph* out, char* err, int errlen) {
+    memset(out, 0, sizeof(*out));
+    if (!isfinite(cutoff) || cutoff <= 0.0) {
+        set_error(err, errlen, "neighbor cutoff must be finite and positive");
+        return MDXO_INVALID;
+    }
+    if (!validate_batch(numbers, positions, cells, pbc, offsets, structures, atoms, err, errlen)) {
+        return MDXO_INVALID;
+    }
+    out->atoms_count = atoms;
+    out->offsets = (int64_t*)calloc((size_t)atoms + 1, sizeof(int64_t));
+    if (!out->offsets) return MDXO_NOMEM;
+    pair_buffer pairs;
+    memset(&pairs, 0, sizeof(pairs));
+    for (int64_t s = 0; s < structures; ++s) {
+        if (!build_structure_graph(positions, cells + s * 9, pbc + s * 3, offsets[s], offsets[s + 1],
+                                   cutoff, include_boundary, out->offsets + offsets[s], &pairs, err,
+                                   errlen)) {
+            pair_free(&pairs);
+            free(out->offsets);
+            out->offsets = NULL;
+            return MDXO_INVALID;
+        }
+    }
+    out->pairs = pairs.count;
+    out->atoms = pairs.atoms;
+    out->shifts = pairs.shifts;
+    out->disp = pairs.disp;
+    out->d2 = pairs.d2;
+    return MDXO_OK;
+}
+
+void mdxo_graph_free(mdxo_graph* g) {
+    free(g->offsets);
+    free(g->atoms);
+    free(g->shifts);
+    free(g->disp);
+    free(g->d2);
+    memset(g, 0, sizeof(*g));
+}
+
+/* ------------------------------------------------------------------------ */
+/* Real regular solid harmonics r^l Y_lm.                                   */
+/* Layout (soap.cpp:60-69): index l*l + l holds m = 0; l*l + (l-m) holds the */
+/* cos part and l*l + (l+m) the sin part, both scaled by sqrt(2).  Values    */
+/* follow the Cartesian recurrence of soap.cpp:166-216, which for every l is */
+/* the same polynomial as the literal (l<=4, l=6) and Legendre (l>6)         */
+/* branches of soap.cpp:101-370 (Condon-Shortley phase included).            */
+/* ------------------------------------------------------------------------ */
+#define MDXO_LMAX 20
+
+/* solid_harmonic_normalization, soap.cpp:26-38 */
+static void harmonic_normalization(int l_max, double* out /* (l_max+1)^2 */) {
+    const int width = l_max + 1;
+    for (int l = 0; l <= l_max; ++l) {
+        for (int m = 0; m <= l; ++m) {
+            out[l * width + m] = sqrt((2.0 * l + 1.0) / (4.0 * MDXO_PI)
+                                      * exp(lgamma(l - m + 1.0) - lgamma(l + m + 1.0)));
+        }
+        for (int m = l + 1; m < width; ++m) out[l * width + m] = 0.0;
+    }
+}
+
+void mdxo_solid_harmonics(double x, double y, double z, int l_max, double* result) {
+    double norm[(MDXO_LMAX + 1) * (MDXO_LMAX + 1)];
+    double re[MDXO_LMAX + 1][MDXO_LMAX + 1];
+    double im[MDXO_LMAX + 1][MDXO_LMAX + 1];
+    const int width = l_max + 1;
+    harmonic_normalization(l_max, norm);
+    const double r2 = x * x + y * y + z * z;
+    memset(re, 0, sizeof(re));
+    memset(im, 0, sizeof(im));
+    re[0][0] = 1.0;
+    for (int m = 0; m <= l_max; ++m) {
+        if (m > 0) {
+            const double f = -(2.0 * m - 1.0);
+            re[m][m] = f * (x * re[m - 1][m - 1] - y * im[m - 1][m - 1]);
+            im[m][m] = f * (x * im[m - 1][m - 1] + y * re[m - 1][m - 1]);
+        }
+        if (m < l_max) {
+            re[m + 1][m] = (2.0 * m + 1.0) * z * re[m][m];
+            im[m + 1][m] = (2.0 * m + 1.0) * z * im[m][m];
+        }
+        for (int l = m + 2; l <= l_max; ++l) {
+            re[l][m] = ((2.0 * l - 1.0) * z * re[l - 1][m] - (l + m - 1.0) * r2 * re[l - 2][m]) / (l - m);
+            im[l][m] = ((2.0 * l - 1.0) * z * im[l - 1][m] - (l + m - 1.0) * r2 * im[l - 2][m]) / (l - m);
+        }
+    }
+    for (int l = 0; l <= l_max; ++l) {
+        result[l * l + l] = norm[l * width] * re[l][0];
+        for (int m = 1; m <= l; ++m) {
+            const double f = MDXO_SQRT2 * norm[l * width + m];
+            result[l * l + (l - m)] = f * re[l][m];
+            result[l * l + (l + m)] = f * im[l][m];
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* SOAP, GTO radial basis, compression off, default weighting.              */
+/* Plan: prepare_soap, soap.cpp:507-534.  Expansion: calculate_coefficients */
+/* GTO branch, soap.cpp:701-760 + 864-931.  Power spectrum: compression off */
+/* branch, soap.cpp:997-1013.  Averaging: soap.cpp:1019-1142.  Driver:      */
+/* compute_soap, soap.cpp:1149-1246.                                        */
+/* ------------------------------------------------------------------------ */
+typedef struct {
+    int S, n, l_max, L, H;
+    int64_t coeff_size, features;
+    double eta, soap_scale;
+    double* power_prefactors; /* [L] */
+    double* radial_prefactors; /* [L*n] */
+    double* radial_exponents;  /* [L*n] */
+    const double* betas;       /* [L*n*n], index (l*n + n')*n + k */
+    int32_t species[256];
+} soap_plan;
+
+static int64_t soap_feature_count(int S, int n, int l_max) {
+    const int64_t w = (int64_t)S * n;
+    return w * (w + 1) / 2 * (l_max + 1);
+}
+
+int64_t mdxo_soap_feature_count(int S, int n, int l_max) { return soap_feature_count(S, n, l_max); }
+
+static void compute_centre_coefficients(const soap_plan* p, const int32_t* atom_type, int64_t centre,
+                                        const int64_t* graph_offsets, const int32_t* graph_atoms,
+                                        const double* graph_disp, const double* graph_d2,
+                                        int64_t atom_base, double* coeff, double* scratch_harm,
+                                        int64_t* scratch_order, double* hsum, double* ylm) {
+    const int64_t begin = graph_offsets[centre];
+    const int64_t count = graph_offsets[centre + 1] - begin;
+    memset(coeff, 0, (size_t)p->coeff_size * sizeof(double));
+    /* species counting sort (stable), soap.cpp:737-760; S == 1 keeps graph order */
+    int64_t type_offsets[257];
+    int64_t cursor[256];
+    memset(cursor, 0, sizeof(cursor));
+    for (int64_t i = 0; i < count; ++i) cursor[atom_type[graph_atoms[begin + i] - atom_base]]++;
+    type_offsets[0] = 0;
+    for (int t = 0; t < p->S; ++t) {
+        type_offsets[t + 1] = type_offsets[t] + cursor[t];
+        cursor[t] = type_offsets[t];
+    }
+    for (int64_t i = 0; i < count; ++i) {
+        const int t = atom_type[graph_atoms[begin + i] - atom_base];
+        scratch_order[cursor[t]++] = begin + i;
+    }
+    /* harmonics, SoA [h * count + j], soap.cpp:761-780 */
+    for (int64_t j = 0; j < count; ++j) {
+        const int64_t src = scratch_order[j];
+        mdxo_solid_harmonics(graph_disp[src * 3 + 0], graph_disp[src * 3 + 1], graph_disp[src * 3 + 2],
+                             p->l_max, ylm);
+        for (int h = 0; h < p->H; ++h) scratch_harm[(int64_t)h * count + j] = ylm[h];
+    }
+    /* accumulate per species, l, k then fold beta, soap.cpp:881-929 */
+    for (int t = 0; t < p->S; ++t) {
+        const int64_t tb = type_offsets[t];
+        const int64_t te = type_offsets[t + 1];
+        for (int l = 0; l <= p->l_max; ++l) {
+            const int mc = 2 * l + 1;
+            for (int k = 0; k < p->n; ++k) {
+                const int ri = l * p->n + k;
+                const double pref = p->radial_prefactors[ri];
+                const double expo = p->radial_exponents[ri];
+                for (int m = 0; m < mc; ++m) hsum[m] = 0.0;
+                for (int64_t j = tb; j < te; ++j) {
+                    const double radial = pref * exp(-expo * graph_d2[scratch_order[j]]);
+                    for (int m = 0; m < mc; ++m) {
+                        /* weight = 1.0 at the default weighting (soap.cpp:389-420) */
+                        hsum[m] += radial * scratch_harm[(int64_t)(l * l + m) * count + j] * 1.0;
+                    }
+                }
+                for (int nn = 0; nn < p->n; ++nn) {
+                    const double beta = p->betas[(l * p->n + nn) * p->n + k];
+                    double* dst = coeff + ((int64_t)t * p->n + nn) * p->H + l * l;
+                    for (int m = 0; m < mc; ++m) dst[m] += p->soap_scale * beta * hsum[m];
+                }
+            }
+        }
+    }
+}
+
+/* power_spectrum, compression "off", soap.cpp:933-1017 */
+static void power_spectrum(const soap_plan* p, const double* c, double* out) {
+    int64_t f = 0;
+    for (int t1 = 0; t1 < p->S; ++t1) {
+        for (int t2 = t1; t2 < p->S; ++t2) {
+            for (int l = 0; l <= p->l_max; ++l) {
+                const double pref = p->power_prefactors[l];
+                for (int n1 = 0; n1 < p->n; ++n1) {
+                    for (int n2 = (t1 == t2 ? n1 : 0); n2 < p->n; ++n2) {
+                        const double* a = c + ((int64_t)t1 * p->n + n1) * p->H + l * l;
+                        const double* b = c + ((int64_t)t2 * p->n + n2) * p->H + l * l;
+                        double sum = 0.0;
+                        for (int m = 0; m < 2 * l + 1; ++m) sum += a[m] * b[m];
+                        out[f++] = pref * sum;
+                    }
+                }
+            }
+        }
+    }
+}
+
+typedef struct {
+    double* coeff;
+    double* harm;
+    int64_t* order;
+    double* hsum;
+    double* ylm;
+    double* power;
+    int64_t capacity;
+} centre_workspace;
+
+static int workspace_reserve(centre_workspace* w, const soap_plan* p, int64_t count) {
+    if (w->coeff == NULL) {
+        w->coeff = (double*)malloc((size_t)p->coeff_size * sizeof(double));
+        w->hsum = (double*)malloc((size_t)(2 * p->l_max + 1) * sizeof(double));
+        w->ylm = (double*)malloc((size_t)p->H * sizeof(double));
+        w->power = (double*)malloc((size_t)p->features * sizeof(double));
+        if (!w->coeff || !w->hsum || !w->ylm || !w->power) return 0;
+    }
+    if (count > w->capacity) {
+        const int64_t cap = count * 2;
+        free(w->harm);
+        free(w->order);
+        w->harm = (double*)malloc((size_t)cap * p->H * sizeof(double));
+        w->order = (int64_t*)malloc((size_t)cap * sizeof(int64_t));
+        if (!w->harm || !w->order) return 0;
+        w->capacity = cap;
+    }
+    return 1;
+}
+
+static void workspace_free(centre_workspace* w) {
+    free(w->coeff);
+    free(w->harm);
+    free(w->order);
+    free(w->hsum);
+    free(w->ylm);
+    free(w->power);
+    memset(w, 0, sizeof(*w));
+}
+
+/* compute_soap_structure (soap.cpp:598-1146) for one structure whose graph is
+ * given with local atom indices.  parallel != 0 runs centres in an OpenMP
+ * loop with per-thread partial sums, as in soap.cpp:1022-1060, 1071-1112. */
+static int soap_structure(const soap_plan* p, const int32_t* atom_type, int64_t atom_count,
+                          const int64_t* g_off, const int32_t* g_atoms, const double* g_disp,
+                          const double* g_d2, int average, int parallel, int threads, double* out,
+                          const volatile int32_t* cancel) {
+    const int64_t F = p->features;
+    const int64_t C = p->coeff_size;
+    int failed = 0;
+    if (average == 1 || average == 2) {
+        const int64_t width = average == 1 ? C : F;
+        double* total = (double*)calloc((size_t)width, sizeof(double));
+        if (!total) return MDXO_NOMEM;
+        const int nt = parallel ? threads : 1;
+        double* partial = (double*)calloc((size_t)width * nt, sizeof(double));
+        if (!partial) {
+            free(total);
+            return MDXO_NOMEM;
+        }
+#pragma omp parallel num_threads(nt) if (parallel)
+        {
+            int tid = 0;
+#ifdef _OPENMP
+            tid = omp_get_thread_num();
+#endif
+            centre_workspace w;
+            memset(&w, 0, sizeof(w));
+#pragma omp for schedule(static)
+            for (int64_t c = 0; c < atom_count; ++c) {
+                if (failed || (cancel && *cancel)) continue;
+                if (!workspace_reserve(&w, p, g_off[c + 1] - g_off[c])) {
+                    failed = 1;
+                    continue;
+                }
+                compute_centre_coefficients(p, atom_type, c, g_off, g_atoms, g_disp, g_d2, 0, w.coeff,
+                                            w.harm, w.order, w.hsum, w.ylm);
+                double* dst = partial + (int64_t)tid * width;
+                if (average == 1) {
+                    for (int64_t i = 0; i < C; ++i) dst[i] += w.coeff[i];
+                } else {
+                    power_spectrum(p, w.coeff, w.power);
+                    for (int64_t i = 0; i < F; ++i) dst[i] += w.power[i];
+                }
+            }
+            workspace_free(&w);
+        }
+        if (failed) {
+            free(total);
+            free(partial);
+            return MDXO_NOMEM;
+        }
+        if (cancel && *cancel) {
+            free(total);
+            free(partial);
+            return MDXO_CANCELLED;
+        }
+        for (int t = 0; t < nt; ++t) {
+            for (int64_t i = 0; i < width; ++i) total[i] += partial[(int64_t)t * width + i];
+        }
+        if (average == 1) {
+            if (atom_count > 0) {
+                const double inv = 1.0 / (double)atom_count;
+                for (int64_t i = 0; i < C; ++i) total[i] *= inv;
+            }
+            power_spectrum(p, total, out);
+        } else {
+            if (atom_count > 0) {
+                const double inv = 1.0 / (double)atom_count;
+                for (int64_t i = 0; i < F; ++i) out[i] = total[i] * inv;
+            } else {
+                for (int64_t i = 0; i < F; ++i) out[i] = 0.0;
+            }
+        }
+        free(total);
+        free(partial);
+        return MDXO_OK;
+    }
+#pragma omp parallel num_threads(parallel ? threads : 1) if (parallel)
+    {
+        centre_workspace w;
+        memset(&w, 0, sizeof(w));
+#pragma omp for schedule(static)
+        for (int64_t c = 0; c < atom_count; ++c) {
+            if (failed || (cancel && *cancel)) continue;
+            if (!workspace_reserve(&w, p, g_off[c + 1] - g_off[c])) {
+                failed = 1;
+                continue;
+            }
+            compute_centre_coefficients(p, atom_type, c, g_off, g_atoms, g_disp, g_d2, 0, w.coeff,
+                                        w.harm, w.order, w.hsum, w.ylm);
+            power_spectrum(p, w.coeff, out + c * F);
+        }
+        workspace_free(&w);
+    }
+    if (failed) return MDXO_NOMEM;
+    if (cancel && *cancel) return MDXO_CANCELLED;
+    return MDXO_OK;
+}
+
+/*
+ * mdxo_soap: compute_soap (soap.cpp:1149-1246) for rbf = "gto", compression
+ * "off", default weighting.  average: 0 off, 1 inner, 2 outer.  `output` is
+ * caller-allocated C-order f64 [rows, features], rows = structures when
+ * averaging, else atoms.  alphas [L*n] and betas [L*n*n] are supplied by the
+ * caller exactly as the reference passes them (core.py:237-240).
+ * decomposition: 0 = the reference's (one structure: centre-parallel;
+ * several: structure-parallel with serial centres, soap.cpp:1218-1245);
+ * 1 = every structure centre-parallel over all threads.
+ */
+int mdxo_soap(const int32_t* numbers, const double* positions, const double* cells, const int32_t* pbc,
+              const int64_t* offsets, int64_t structures, int64_t atoms, const int32_t* species, int S,
+              int n_max, int l_max, double r_cut, double sigma, const double* alphas, const double* betas,
+              int average, int num_threads, int decomposition, double* output,
+              const volatile int32_t* cancel, char* err, int errlen) {
+    if (!validate_batch(numbers, positions, cells, pbc, offsets, structures, atoms, err, errlen)) {
+        return MDXO_INVALID;
+    }
+    if (S < 1 || S > 256 || !isfinite(r_cut) || !isfinite(sigma) || r_cut <= 0.0 || sigma <= 0.0
+        || n_max < 1 || l_max < 0 || l_max > MDXO_LMAX || average < 0 || average > 2) {
+        set_error(err, errlen, "invalid SOAP parameters");
+        return MDXO_INVALID;
+    }
+    soap_plan p;
+    memset(&p, 0, sizeof(p));
+    p.S = S;
+    p.n = n_max;
+    p.l_max = l_max;
+    p.L = l_max + 1;
+    p.H = p.L * p.L;
+    p.coeff_size = (int64_t)S * n_max * p.H;
+    p.features = soap_feature_count(S, n_max, l_max);
+    for (int t = 0; t < S; ++t) p.species[t] = species[t];
+    int32_t* atom_type = (int32_t*)malloc((size_t)(atoms > 0 ? atoms : 1) * sizeof(int32_t));
+    if (!atom_type) return MDXO_NOMEM;
+    for (int64_t i = 0; i < atoms; ++i) {
+        int found = -1;
+        for (int t = 0; t < S; ++t) {
+            if (species[t] == numbers[i]) found = t;
+        }
+        if (found < 0) {
+            free(atom_type);
+            set_error(err, errlen, "batch contains an atomic number outside calculator species");
+            return MDXO_INVALID;
+        }
+        atom_type[i] = found;
+    }
+    for (int i = 0; i < p.L * n_max; ++i) {
+        if (!isfinite(alphas[i])) {
+            free(atom_type);
+            set_error(err, errlen, "SOAP radial basis must be finite");
+            return MDXO_INVALID;
+        }
+    }
+    /* prepare_soap, soap.cpp:507-534 */
+    p.eta = 1.0 / (2.0 * sigma * sigma);
+    p.soap_scale = MDXO_PI * sqrt(MDXO_PI);
+    p.power_prefactors = (double*)malloc((size_t)p.L * sizeof(double));
+    p.radial_prefactors = (double*)malloc((size_t)p.L * n_max * sizeof(double));
+    p.radial_exponents = (double*)malloc((size_t)p.L * n_max * sizeof(double));
+    p.betas = betas;
+    for (int l = 0; l <= l_max; ++l) p.power_prefactors[l] = MDXO_PI * sqrt(8.0 / (2.0 * l + 1.0));
+    {
+        double eta_power = 1.0;
+        for (int l = 0; l <= l_max; ++l) {
+            if (l > 0) eta_power *= p.eta;
+            for (int k = 0; k < n_max; ++k) {
+                const int idx = l * n_max + k;
+                const double denominator = alphas[idx] + p.eta;
+                p.radial_prefactors[idx] = eta_power * pow(denominator, -l - 1.5);
+                p.radial_exponents[idx] = alphas[idx] * p.eta / denominator;
+            }
+        }
+    }
+    /* graph cutoff padding, soap.cpp:1214 */
+    const double padding = sigma * sqrt(-2.0 * log(1e-3));
+    const double cutoff = r_cut + padding;
+    int threads = num_threads;
+#ifdef _OPENMP
+    if (threads <= 0) threads = omp_get_max_threads();
+#else
+    threads = 1;
+#endif
+    const int64_t F = p.features;
+    int status = MDXO_OK;
+    const int averaged = average != 0;
+    const int structure_parallel = decomposition == 0 && structures > 1;
+    int st_threads = threads;
+    if (structure_parallel && st_threads > structures) st_threads = (int)structures; /* descriptor_common.hpp:34-38 */
+#pragma omp parallel for schedule(static) num_threads(st_threads) if (structure_parallel)
+    for (int64_t s = 0; s < structures; ++s) {
+        if (status != MDXO_OK || (cancel && *cancel)) continue;
+        const int64_t b = offsets[s], e = offsets[s + 1], n = e - b;
+        int64_t* g_off = (int64_t*)calloc((size_t)n + 1, sizeof(int64_t));
+        pair_buffer pairs;
+        memset(&pairs, 0, sizeof(pairs));
+        char local_err[256] = {0};
+        /* structure_view (extra_common.hpp:36-51): local atom indices */
+        int ok = g_off != NULL
+            && build_structure_graph(positions + b * 3, cells + s * 9, pbc + s * 3, 0, n, cutoff, 1, g_off,
+                                     &pairs, local_err, (int)sizeof(local_err));
+        if (!ok) {
+#pragma omp critical
+            {
+                status = MDXO_INVALID;
+                set_error(err, errlen, local_err[0] ? local_err : "graph construction failed");
+            }
+        } else {
+            double* dst = output + (averaged ? s : b) * F;
+            const int rc = soap_structure(&p, atom_type + b, n, g_off, pairs.atoms, pairs.disp, pairs.d2,
+                                          average, !structure_parallel, threads, dst, cancel);
+            if (rc != MDXO_OK) {
+#pragma omp critical
+                {
+                    status = rc;
+                }
+            }
+        }
+        free(g_off);
+        pair_free(&pairs);
+    }
+    if (status == MDXO_OK && cancel && *cancel) status = MDXO_CANCELLED;
+    free(atom_type);
+    free(p.power_prefactors);
+    free(p.radial_prefactors);
+    free(p.radial_exponents);
+    return status;
+}
