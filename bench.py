@@ -1,0 +1,185 @@
+#!/usr/bin/env python
+"""SOAP atom-environments per second on one MI355X (benchmark configuration 2).
+
+One step is one pass of the hot path over the batch resident in HBM:
+neighbour graph (kernel 1) + per-centre expansion, power spectrum and float32
+write (kernels 2-4), exactly what ``mdx_hip_soap_run`` does.  Inputs are
+uploaded once before timing; the output stays on the device.
+
+Prints one JSON line with the metric of BASELINE.json, a ``roofline`` object
+for the dominant kernel (the expansion kernel, FP64: its algorithmic flops
+per launch over its launch time from HIP events on the library's stream) and
+a ``cpu_baseline`` object (the reference's own C++ SOAP compiled in place,
+``oracle/_ref``, timed on this host's cores on a bounded sample).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "SOAP atom-envs/sec (4 spec, n8 l6, rc5) on 1 MI355X; % of FP64/HBM roofline"
+FP64_PEAK_TFLOPS = 78.6  # MI355X dense FP64 (vector and MFMA)
+HBM_PEAK_GBS = 8000.0
+
+
+def flops_per_env(kbar: float, S: int, n: int, l_max: int) -> float:
+    """Algorithmic FP64 flops per environment (FMA = 2): accumulation
+    2*K*n*H, beta contraction 2*S*n^2*H, power spectrum S*n*(S*n+1)*H."""
+
+    H = (l_max + 1) ** 2
+    return 2.0 * kbar * n * H + 2.0 * S * n * n * H + S * n * (S * n + 1) * H
+
+
+def cpu_baseline(workload, alphas, betas, threads: int, budget_s: float = 30.0) -> dict:
+    from oracle import oracle
+
+    kind = "reference" if oracle.reference_available() else "port"
+    p = workload.params
+    batch = workload.batch
+    times = []
+    while True:
+        t0 = time.perf_counter()
+        oracle.soap(batch, species=p["species"], n_max=p["n_max"], l_max=p["l_max"], r_cut=p["r_cut"],
+                    sigma=1.0, alphas=alphas, betas=betas, average=p["average"], num_threads=threads,
+                    kind="ref" if kind == "reference" else "oracle")
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 3 or sum(times) + times[-1] > budget_s:
+            break
+    seconds = statistics.median(times)
+    return {
+        "value": batch.atoms / seconds,
+        "unit": "atom-envs/s",
+        "cores": threads,
+        "kind": kind,
+        "sample": (f"full {workload.name} batch ({batch.atoms} envs, {batch.structures} structures), "
+                   f"reference decomposition (structure-parallel, threads capped at structures), "
+                   f"float64 compute, median of {len(times)} run(s) of {seconds:.2f}s"),
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--config", type=int, default=2, help="benchmark configuration 1-5 (default 2)")
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--cpu-threads", type=int, default=0)
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only; the SOAP path shards by structure or "
+                                   "centre range across GPUs (see DESIGN.md) but no multi-GPU run is provided",
+                          "n_gpus": args.gpus}))
+        return 2
+
+    from mdescriptor_amd import _hip, workloads
+    from mdescriptor_amd.descriptors.basis import basis_gto
+
+    workload = workloads.config(args.config)
+    p = workload.params
+    batch = workload.batch
+    alphas, betas = basis_gto(p["r_cut"], p["n_max"], p["l_max"])
+    ctx = _hip.Context(0)
+    plan = _hip.SoapPlan(ctx, species=p["species"], n_max=p["n_max"], l_max=p["l_max"], r_cut=p["r_cut"],
+                         sigma=1.0, alphas=alphas, betas=betas, average=p["average"], dtype=p["dtype"])
+    dbatch = _hip.DeviceBatch(plan, batch)
+    itemsize = np.dtype(p["dtype"]).itemsize
+    pitch = plan.features * itemsize
+    out = _hip.DeviceMemory(dbatch.rows * pitch)
+
+    for _ in range(args.warmup):
+        dbatch.run(out.address, pitch)
+    _hip.DeviceMemory.synchronize()
+    timings = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        timings.append(dbatch.run(out.address, pitch))
+    _hip.DeviceMemory.synchronize()
+    elapsed = time.perf_counter() - t0
+
+    envs = batch.atoms
+    ms_per_step = 1e3 * elapsed / args.steps
+    value = envs * args.steps / elapsed
+    pairs = timings[-1]["pairs"]
+    kbar = pairs / envs
+    S, n, l_max = len(p["species"]), p["n_max"], p["l_max"]
+    launches = max(1, int(timings[-1]["expansion_launches"]))
+    flops_launch = envs * flops_per_env(kbar, S, n, l_max) / launches
+    launch_ms = statistics.mean(t["expansion_ms"] for t in timings) / launches
+    achieved = flops_launch / (launch_ms * 1e-3) / 1e12
+    H = (l_max + 1) ** 2
+    result = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "atom-envs/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f64",
+        "data": "synthetic (seeded generator, mdescriptor_amd/workloads.py)",
+        "config": {
+            "workload": workload.name,
+            "structures": batch.structures,
+            "atoms": envs,
+            "species": p["species"],
+            "n_max": n,
+            "l_max": l_max,
+            "r_cut": p["r_cut"],
+            "sigma": 1.0,
+            "average": p["average"],
+            "output_dtype": p["dtype"],
+            "parallelism": "single-gpu",
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": achieved,
+            "peak": FP64_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": achieved / FP64_PEAK_TFLOPS,
+            "traffic": None,
+            "kernel": "k_soap_expand (expansion + beta + power spectrum + write)",
+            "flops_per_launch": flops_launch,
+            "launch_ms": launch_ms,
+        },
+        "breakdown": {
+            "graph_ms": statistics.mean(t["graph_ms"] for t in timings),
+            "expansion_ms": statistics.mean(t["expansion_ms"] for t in timings),
+            "device_total_ms": statistics.mean(t["total_ms"] for t in timings),
+            "pairs": pairs,
+            "kbar": kbar,
+            "output_bytes": dbatch.rows * pitch,
+            "output_gbs": dbatch.rows * pitch / (launch_ms * launches * 1e-3) / 1e9,
+            "features": plan.features,
+            "exps_per_env": kbar * (l_max + 1) * n,
+            "flops_per_env": flops_per_env(kbar, S, n, l_max),
+            "H": H,
+        },
+    }
+    if not args.no_cpu_baseline:
+        threads = args.cpu_threads or min(batch.structures if batch.structures > 1 else 10**9,
+                                          len(os.sched_getaffinity(0)), 16)
+        result["cpu_baseline"] = cpu_baseline(workload, alphas, betas, threads)
+    dbatch.close()
+    plan.close()
+    out.free()
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

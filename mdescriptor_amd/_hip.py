@@ -450,3 +450,65 @@ __all__ = [
     "neighbor_graph",
     "shared_context",
 ]
+
+
+class DeviceMemory:
+    """Raw device allocation through the HIP runtime (for device-resident
+    outputs in benchmarks and tests; the library itself never needs it)."""
+
+    _runtime: Any = None
+
+    @classmethod
+    def runtime(cls) -> Any:
+        if cls._runtime is None:
+            load_library()  # the runtime is a dependency of the library
+            rt = ctypes.CDLL("libamdhip64.so")
+            rt.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+            rt.hipMalloc.restype = ctypes.c_int
+            rt.hipFree.argtypes = [ctypes.c_void_p]
+            rt.hipFree.restype = ctypes.c_int
+            rt.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+            rt.hipMemcpy.restype = ctypes.c_int
+            rt.hipDeviceSynchronize.argtypes = []
+            rt.hipDeviceSynchronize.restype = ctypes.c_int
+            rt.hipSetDevice.argtypes = [ctypes.c_int]
+            rt.hipSetDevice.restype = ctypes.c_int
+            cls._runtime = rt
+        return cls._runtime
+
+    def __init__(self, nbytes: int, device: int = 0) -> None:
+        rt = self.runtime()
+        if rt.hipSetDevice(int(device)) != 0:
+            raise HipUnavailable("hipSetDevice failed")
+        ptr = ctypes.c_void_p()
+        if rt.hipMalloc(ctypes.byref(ptr), max(1, int(nbytes))) != 0:
+            raise HipOutOfMemory(f"hipMalloc of {nbytes} bytes failed")
+        self.ptr = ptr
+        self.nbytes = int(nbytes)
+
+    @property
+    def address(self) -> int:
+        return int(self.ptr.value or 0)
+
+    def to_host(self, out: np.ndarray) -> np.ndarray:
+        if out.nbytes > self.nbytes:
+            raise ValueError("host buffer larger than the device allocation")
+        if self.runtime().hipMemcpy(out.ctypes.data_as(ctypes.c_void_p), self.ptr, out.nbytes, 2) != 0:
+            raise HipError("hipMemcpy device-to-host failed")
+        return out
+
+    @classmethod
+    def synchronize(cls) -> None:
+        if cls.runtime().hipDeviceSynchronize() != 0:
+            raise HipError("hipDeviceSynchronize failed")
+
+    def free(self) -> None:
+        if getattr(self, "ptr", None) is not None and self.ptr.value:
+            self.runtime().hipFree(self.ptr)
+        self.ptr = None
+
+    def __del__(self) -> None:  # pragma: no cover
+        try:
+            self.free()
+        except Exception:
+            pass

@@ -6,10 +6,12 @@
 // calculator the same way, cpp/src/standalone/soap.cpp:1255 and
 // cpp/cuda/src/backend.cu:339-345).
 #include "mdx_internal.h"
+#include "soap_mfma.h"
 
 #include <algorithm>
 #include <chrono>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <unordered_set>
@@ -182,7 +184,7 @@ void run_pipeline(mdx_hip_ctx* ctx, const mdx_soap_plan& plan, mdx::PreparedBatc
 
 extern "C" {
 
-const char* mdx_hip_version(void) { return "mdx_hip 0.1.0 (gfx950)"; }
+const char* mdx_hip_version(void) { return "mdx_hip 0.2.0 (gfx950)"; }
 
 const char* mdx_hip_last_error(const mdx_hip_ctx* ctx) {
     return ctx != nullptr ? ctx->last_error.c_str() : g_last_error.c_str();
@@ -306,6 +308,42 @@ int mdx_hip_soap_plan_create(mdx_hip_ctx* ctx, const mdx_soap_params* params, md
                         }
                     }
                 }
+            }
+            // matrix-core path unless MDX_HIP_SOAP_KERNEL=generic; =mfma makes it mandatory
+            const char* env = std::getenv("MDX_HIP_SOAP_KERNEL");
+            const std::string choice = env != nullptr ? env : "auto";
+            if (choice != "auto" && choice != "generic" && choice != "mfma") {
+                throw mdx::Error(MDX_INVALID_ARGUMENT, "MDX_HIP_SOAP_KERNEL must be auto, generic or mfma");
+            }
+            const mdx::MfmaPlanHost mp = mdx::plan_mfma_tables(plan->S, n, p.l_max, beta);
+            mdx::MfmaDims md{};
+            md.S = plan->S;
+            md.n = n;
+            md.l_max = p.l_max;
+            md.L = L;
+            md.H = H;
+            md.tiles = mp.tiles;
+            md.mode = p.average;
+            md.out_dtype = p.out_dtype;
+            md.F = plan->features;
+            md.hpad = mdx::mfma_padded_row(p.l_max);
+            double max_expo = 0.0;
+            for (double e : expo) max_expo = std::max(max_expo, e);
+            md.clamp = max_expo * plan->cutoff * plan->cutoff > 700.0 ? 1 : 0;
+            plan->hpad = md.hpad;
+            plan->clamp = md.clamp;
+            const bool fits = mdx::mfma_template_tiles(mp.tiles) > 0 && mdx::mfma_lds_bytes(md) <= 64 * 1024;
+            plan->use_mfma = choice != "generic" && fits;
+            if (choice == "mfma" && !fits) {
+                throw mdx::Error(MDX_INVALID_ARGUMENT, "SOAP shape is outside the matrix-core kernel's limits");
+            }
+            plan->tiles = mp.tiles;
+            if (plan->use_mfma) {
+                upload(plan->d_row_channel, mp.row_channel);
+                upload(plan->d_col_harmonic, mp.col_harmonic);
+                upload(plan->d_beta_lane, mp.beta_lane);
+                upload(plan->d_fbase, mp.fbase);
+                upload(plan->d_fstride, mp.fstride);
             }
             upload(plan->d_pref, pref);
             upload(plan->d_expo, expo);

@@ -87,6 +87,8 @@ struct PreparedBatch {
     std::vector<ImageDesc> images;
     std::vector<int32_t> types; // species index per atom (0 when species are ignored)
     std::vector<int64_t> offsets;
+    // work items of the averaged SOAP modes (host copies outlive the async upload)
+    std::vector<int64_t> item_begin, struct_items;
     int n_species = 1;
     DeviceBuffer d_positions; // f64[atoms*3]
     DeviceBuffer d_types;     // i32[atoms]
@@ -160,6 +162,12 @@ struct mdx_soap_plan {
     mdx::DeviceBuffer d_pref, d_expo, d_beta, d_ps_pref; // radial prefactors/exponents, scaled beta, PS prefactors
     mdx::DeviceBuffer d_feat_a, d_feat_b;                // feature table: (c row offsets, l)
     mdx::DeviceBuffer d_hnorm;                           // harmonic normalisation N_lm (x sqrt(2) for m > 0)
+    // matrix-core path (soap_mfma.hip): tile maps, beta-fold operands, feature index tables
+    bool use_mfma = false;
+    int tiles = 0;
+    int hpad = 0;  // padded harmonic row of the matrix-core layout
+    int clamp = 0; // 1 when expo * cutoff^2 can exceed 700
+    mdx::DeviceBuffer d_row_channel, d_col_harmonic, d_beta_lane, d_fbase, d_fstride;
 };
 
 struct mdx_device_batch {
@@ -172,7 +180,7 @@ struct mdx_device_batch {
 namespace mdx {
 // Run the SOAP kernels (2-4) of a plan over a prepared batch whose graph is
 // built; output rows x features in device memory with the given pitch.
-void run_soap(hipStream_t stream, const mdx_soap_plan& plan, const PreparedBatch& pb,
+void run_soap(hipStream_t stream, const mdx_soap_plan& plan, PreparedBatch& pb,
               const DeviceGraph& graph, void* out_device, int64_t pitch_bytes, DeviceBuffer& partials,
               const volatile int32_t* cancel, hipEvent_t* events, mdx_timing* timing);
 } // namespace mdx

@@ -19,6 +19,7 @@
 // spectra go to a partial row, and a finalize kernel reduces the partial
 // rows of each structure in a fixed order.
 #include "mdx_internal.h"
+#include "soap_mfma.h"
 
 #include <algorithm>
 #include <cmath>
@@ -350,7 +351,7 @@ void dispatch_hpt(int hpt, hipStream_t stream, dim3 grid, size_t lds, const mdx_
 
 } // namespace
 
-void run_soap(hipStream_t stream, const mdx_soap_plan& p, const PreparedBatch& pb, const DeviceGraph& g,
+void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, const DeviceGraph& g,
               void* out_device, int64_t pitch_bytes, DeviceBuffer& partials, const volatile int32_t* cancel,
               hipEvent_t* events, mdx_timing* timing) {
     SoapDims d{};
@@ -368,8 +369,10 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, const PreparedBatch& p
     if (rows == 0 || d.F == 0) return;
 
     // work items
-    std::vector<int64_t> item_begin_h;
-    std::vector<int64_t> struct_items_h;
+    std::vector<int64_t>& item_begin_h = pb.item_begin;
+    std::vector<int64_t>& struct_items_h = pb.struct_items;
+    item_begin_h.clear();
+    struct_items_h.clear();
     int64_t items = pb.atoms;
     if (p.average != 0) {
         struct_items_h.resize(static_cast<size_t>(pb.structures) + 1);
@@ -384,22 +387,14 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, const PreparedBatch& p
         items = static_cast<int64_t>(item_begin_h.size());
         item_begin_h.push_back(pb.atoms);
     }
-    const int64_t acc_words = p.average == 1 ? d.C : p.average == 2 ? d.F : 0;
-    // chunk of neighbours staged per step: largest that keeps LDS within budget
-    const size_t budget = 64 * 1024;
-    int CH = 64;
-    while (CH > 8 && expand_lds_bytes(p, CH, 0) > budget) CH /= 2;
-    d.CH = CH;
-    d.acc_in_lds = acc_words > 0 && expand_lds_bytes(p, CH, static_cast<int>(acc_words)) <= 96 * 1024 ? 1 : 0;
-    const size_t lds = expand_lds_bytes(p, CH, d.acc_in_lds ? static_cast<int>(acc_words) : 0);
-    if (lds > 160 * 1024) throw Error(MDX_INVALID_ARGUMENT, "SOAP shape exceeds the device LDS budget");
-
     DeviceBuffer& scratch = partials;
     int64_t* d_item_begin = nullptr;
     int64_t* d_struct_items = nullptr;
     double* d_partial = nullptr;
     if (p.average != 0) {
-        const size_t width = static_cast<size_t>(p.average == 1 ? d.C : d.F);
+        const size_t inner_width = p.use_mfma ? static_cast<size_t>(p.S * p.n + 1) * static_cast<size_t>(p.hpad)
+                                              : static_cast<size_t>(d.C);
+        const size_t width = p.average == 1 ? inner_width : static_cast<size_t>(d.F);
         const size_t head = ((item_begin_h.size() + struct_items_h.size()) * sizeof(int64_t) + 255) & ~size_t(255);
         scratch.reserve(head + static_cast<size_t>(items) * width * sizeof(double));
         d_item_begin = scratch.as<int64_t>();
@@ -411,10 +406,60 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, const PreparedBatch& p
                                hipMemcpyHostToDevice, stream));
     }
 
-    const int hpt = p.H > kBlock ? 2 : 1;
     // launch in slices so cancellation is polled between launches
     const int64_t slice = 1 << 17;
     int64_t launches = 0;
+    if (p.use_mfma) {
+        MfmaDims md{};
+        md.S = p.S;
+        md.n = p.n;
+        md.l_max = p.l_max;
+        md.L = p.L;
+        md.H = p.H;
+        md.tiles = p.tiles;
+        md.mode = p.average;
+        md.out_dtype = p.out_dtype;
+        md.F = p.features;
+        md.hpad = p.hpad;
+        md.clamp = p.clamp;
+        MfmaTables tab{};
+        tab.row_channel = p.d_row_channel.as<int32_t>();
+        tab.col_harmonic = p.d_col_harmonic.as<int32_t>();
+        tab.beta_lane = p.d_beta_lane.as<double>();
+        tab.pref = p.d_pref.as<double>();
+        tab.expo = p.d_expo.as<double>();
+        tab.hnorm = p.d_hnorm.as<double>();
+        tab.ps_pref = p.d_ps_pref.as<double>();
+        tab.fbase = p.d_fbase.as<int32_t>();
+        tab.fstride = p.d_fstride.as<int32_t>();
+        const int tt = mfma_template_tiles(p.tiles);
+        if (events != nullptr) MDX_HIP(hipEventRecord(events[2], stream));
+        for (int64_t base = 0; base < items; base += slice) {
+            if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
+            const int64_t count = std::min(slice, items - base);
+            launch_mfma_expand(stream, tt, pb, g, tab, md, d_item_begin, base, count, out_device, pitch_bytes,
+                               d_partial);
+            ++launches;
+        }
+        if (events != nullptr) MDX_HIP(hipEventRecord(events[3], stream));
+        if (p.average != 0) {
+            launch_mfma_finalize(stream, pb, tab, md, d_partial, d_struct_items, out_device, pitch_bytes);
+        }
+        if (events != nullptr) MDX_HIP(hipEventRecord(events[4], stream));
+        if (timing != nullptr) timing->expansion_launches = launches;
+        return;
+    }
+    const int64_t acc_words = p.average == 1 ? d.C : p.average == 2 ? d.F : 0;
+    // chunk of neighbours staged per step: largest that keeps LDS within budget
+    const size_t budget = 64 * 1024;
+    int CH = 64;
+    while (CH > 8 && expand_lds_bytes(p, CH, 0) > budget) CH /= 2;
+    d.CH = CH;
+    d.acc_in_lds = acc_words > 0 && expand_lds_bytes(p, CH, static_cast<int>(acc_words)) <= 96 * 1024 ? 1 : 0;
+    const size_t lds = expand_lds_bytes(p, CH, d.acc_in_lds ? static_cast<int>(acc_words) : 0);
+    if (lds > 160 * 1024) throw Error(MDX_INVALID_ARGUMENT, "SOAP shape exceeds the device LDS budget");
+
+    const int hpt = p.H > kBlock ? 2 : 1;
     if (events != nullptr) MDX_HIP(hipEventRecord(events[2], stream));
     for (int64_t base = 0; base < items; base += slice) {
         if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");

@@ -1,0 +1,58 @@
+// Host/device interface of the matrix-core SOAP kernels (soap_mfma.hip).
+#pragma once
+
+#include "mdx_internal.h"
+
+namespace mdx {
+
+// Shape of one SOAP plan as the MFMA kernels see it.
+struct MfmaDims {
+    int S, n, l_max, L, H;
+    int tiles;     // 16x16 contraction tiles in use
+    int mode;      // 0 off, 1 inner, 2 outer
+    int out_dtype; // 4 or 8
+    int hpad;      // padded harmonic row: each l block rounded up to a multiple of 4
+    int clamp;     // 1 when some radial exponent argument can fall below -700
+    int64_t F;
+};
+
+// Device tables built once per plan.
+//   row_channel[t*16 + r]  radial channel l*n + k of row r of tile t, or -1
+//   col_harmonic[t*16 + c] harmonic index l*l + m' of column c, or -1
+//   beta_lane[(t*4 + s)*64 + lane]  A operand of beta-fold step s for a lane:
+//       pi^1.5 beta[l][n'][k] for row (l, n') = lane%16 and column (l, k) =
+//       4s + lane/16 of the same diagonal block, else 0
+//   fbase/fstride[i*W + j] feature index of channel pair (i, j), i <= j, at
+//       degree l is fbase + l * fstride (layout of soap.cpp:997-1013)
+struct MfmaTables {
+    const int32_t* row_channel;
+    const int32_t* col_harmonic;
+    const double* beta_lane;
+    const double* pref;
+    const double* expo;
+    const double* hnorm;
+    const double* ps_pref;
+    const int32_t* fbase;
+    const int32_t* fstride;
+};
+
+// Host-side tables of a plan: block-diagonal packing of the (l, k) x (l, m)
+// blocks into 16x16 tiles, the beta-fold operands and feature indices.
+// beta_scaled is pi^1.5 beta with index (l*n + n')*n + k.
+struct MfmaPlanHost {
+    int tiles = 0;
+    std::vector<int32_t> row_channel, col_harmonic, fbase, fstride;
+    std::vector<double> beta_lane;
+};
+MfmaPlanHost plan_mfma_tables(int S, int n, int l_max, const std::vector<double>& beta_scaled);
+
+int mfma_template_tiles(int tiles);
+int mfma_padded_row(int l_max);
+size_t mfma_lds_bytes(const MfmaDims& d);
+void launch_mfma_expand(hipStream_t stream, int template_tiles, const PreparedBatch& pb, const DeviceGraph& g,
+                        const MfmaTables& tab, const MfmaDims& d, const int64_t* item_begin, int64_t base,
+                        int64_t count, void* out, int64_t pitch, double* partial);
+void launch_mfma_finalize(hipStream_t stream, const PreparedBatch& pb, const MfmaTables& tab, const MfmaDims& d,
+                          const double* partial, const int64_t* struct_items, void* out, int64_t pitch);
+
+} // namespace mdx
