@@ -253,10 +253,19 @@ class SoapPlan:
     def rows(self, batch: Any) -> int:
         return (len(batch.offsets) - 1) if self.average != "off" else len(batch.numbers)
 
-    def compute(self, batch: Any, cancel: ctypes.c_int32 | None = None) -> tuple[np.ndarray, dict[str, float]]:
+    def compute(self, batch: Any, cancel: ctypes.c_int32 | None = None,
+                out: np.ndarray | None = None) -> tuple[np.ndarray, dict[str, float]]:
+        """Compute one batch into ``out`` (allocated when None), a C-contiguous
+        ``(rows, features)`` array of the plan's dtype."""
+
         arrays = _BatchArrays(batch)
         rows = self.rows(batch)
-        out = np.empty((rows, self.features), dtype=self.dtype)
+        if out is None:
+            out = np.empty((rows, self.features), dtype=self.dtype)
+        elif (out.shape != (rows, self.features) or out.dtype != self.dtype or not out.flags.c_contiguous
+              or not out.flags.writeable):
+            raise ValueError(f"output must be a writable C-contiguous {self.dtype} array of shape "
+                             f"({rows}, {self.features})")
         timing = Timing()
         flag = ctypes.pointer(cancel) if cancel is not None else None
         lib = self.context.lib
@@ -399,12 +408,12 @@ class Backend:
             "execution": {"device": "hip", "num_threads": self._num_threads},
         }
 
-    def compute(self, batch: Any, control: Any = None) -> dict[str, Any]:
+    def compute(self, batch: Any, control: Any = None, out: np.ndarray | None = None) -> dict[str, Any]:
         with self._lock:
             if self._closed:
                 raise RuntimeError("HIP backend is closed")
             flag = getattr(control, "_hip_cancel_flag", None) if control is not None else None
-            values, timing = self._plan.compute(batch, flag)
+            values, timing = self._plan.compute(batch, flag, out)
             self.last_timing = timing
             level = "structure" if self._average in ("inner", "outer") else "atom"
             result: dict[str, Any] = {

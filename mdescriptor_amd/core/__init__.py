@@ -1,0 +1,1 @@
+"""The public descriptor contract: batches, options, results, errors, control."""

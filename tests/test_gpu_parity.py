@@ -1,0 +1,307 @@
+"""Parity of the HIP library with the CPU oracle, through the C-ABI.
+
+Gates: the neighbour graph is identical to the oracle's in every field and
+order (d^2 bit-identical); float64 features satisfy
+|delta| <= 1e-10 (|ref| + max|row|) and float32 features the same form at
+2e-5 (the oracle's float64 result is the reference); samples, labels and
+row offsets are identical.  The reference goldens are also checked end to end
+through the public ``SOAP`` class.  Full-size configurations are checked
+through properties that do not need a CPU run of the whole batch: one
+structure against the oracle, translation invariance and periodic-supercell
+replication.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+
+import mdescriptor_amd as mdx
+from conftest import SOAP_PAD, load_golden, scaled_error
+from mdescriptor_amd import _hip, workloads
+from mdescriptor_amd.descriptors.basis import basis_gto
+
+pytestmark = pytest.mark.gpu
+
+F64_GATE = 1e-10
+F32_GATE = 2e-5
+
+
+def _plan(ctx, params, average=None, dtype=None):
+    p = dict(params)
+    alphas, betas = basis_gto(p["r_cut"], p["n_max"], p["l_max"])
+    return _hip.SoapPlan(ctx, species=p["species"], n_max=p["n_max"], l_max=p["l_max"], r_cut=p["r_cut"],
+                         sigma=p.get("sigma", 1.0), alphas=alphas, betas=betas,
+                         average=average or p["average"], dtype=dtype or p["dtype"]), (alphas, betas)
+
+
+def _oracle_soap(oracle, batch, params, basis, average):
+    return oracle.soap(batch, species=params["species"], n_max=params["n_max"], l_max=params["l_max"],
+                       r_cut=params["r_cut"], sigma=params.get("sigma", 1.0), alphas=basis[0], betas=basis[1],
+                       average=average, num_threads=0)
+
+
+def _check(ctx, oracle, batch, params, average, dtype):
+    plan, basis = _plan(ctx, params, average, dtype)
+    try:
+        values, timing = plan.compute(batch)
+    finally:
+        plan.close()
+    expected = _oracle_soap(oracle, batch, params, basis, average)
+    assert values.dtype == np.dtype(dtype)
+    assert values.shape == expected.shape
+    assert np.all(np.isfinite(values))
+    error = scaled_error(values, expected)
+    assert error <= (F64_GATE if dtype == "float64" else F32_GATE), f"scaled error {error:.3e}"
+    return values, timing
+
+
+@pytest.fixture(scope="module", params=[1, 2, 3, 4, 5])
+def workload(request):
+    return workloads.config(request.param, "small")
+
+
+def test_graph_identical_to_oracle(hip_context, oracle, workload):
+    cutoff = workload.params["r_cut"] + SOAP_PAD
+    ours = _hip.neighbor_graph(hip_context, workload.batch, cutoff)
+    theirs = oracle.graph(workload.batch, cutoff)
+    for key in theirs:
+        np.testing.assert_array_equal(ours[key], theirs[key], err_msg=key)
+
+
+@pytest.mark.parametrize("average", ["off", "inner", "outer"])
+@pytest.mark.parametrize("dtype", ["float64", "float32"])
+def test_soap_matches_oracle(hip_context, oracle, workload, average, dtype):
+    _check(hip_context, oracle, workload.batch, workload.params, average, dtype)
+
+
+@pytest.mark.parametrize("kernel", ["generic", "mfma"])
+def test_both_expansion_kernels_match(hip_context, oracle, monkeypatch, kernel):
+    """The plan picks the matrix-core kernel where its tiles fit; the generic
+    kernel is the fallback for other shapes.  Both stay parity-green."""
+
+    monkeypatch.setenv("MDX_HIP_SOAP_KERNEL", kernel)
+    work = workloads.config(2, "small")
+    for average in ("off", "inner", "outer"):
+        _check(hip_context, oracle, work.batch, work.params, average, "float64")
+
+
+@pytest.mark.parametrize("cutoff", [3.5, 3.5 + SOAP_PAD])
+def test_golden_graphs(hip_context, oracle, cutoff):
+    _, batch, _ = load_golden("reference_soap", "manifest.json")
+    ours = _hip.neighbor_graph(hip_context, batch, cutoff)
+    theirs = oracle.graph(batch, cutoff)
+    for key in theirs:
+        np.testing.assert_array_equal(ours[key], theirs[key], err_msg=key)
+
+
+@pytest.mark.parametrize("manifest", ["manifest.json", "external_manifest.json"])
+def test_neighbor_list_goldens(hip_context, manifest):
+    """The device graph reproduces the reference NeighborList pairs, in order."""
+
+    meta, batch, expected = load_golden("reference_neighborlist", manifest)
+    g = _hip.neighbor_graph(hip_context, batch, meta["configuration"]["parameters"]["cutoff"])
+    offsets = np.asarray(batch.offsets)
+    centre = np.repeat(np.arange(len(g["offsets"]) - 1), np.diff(g["offsets"]))
+    keep = ~((g["atoms"] == centre) & np.all(g["shifts"] == 0, axis=1))
+    structure = np.searchsorted(offsets, centre, side="right") - 1
+    samples = np.column_stack((structure, centre - offsets[structure], g["atoms"] - offsets[structure],
+                               g["shifts"]))[keep]
+    np.testing.assert_array_equal(samples, expected["samples"])
+    values = np.column_stack((g["displacements"], np.sqrt(g["distance2"])))[keep]
+    np.testing.assert_allclose(values, expected["values"], rtol=1e-9, atol=1e-11)
+
+
+def test_graph_boundary_inclusive_and_exclusive(hip_context):
+    batch = SimpleNamespace(numbers=np.array([1, 8], np.int32), positions=np.array([[0.0, 0, 0], [1.0, 0, 0]]),
+                            cells=np.zeros((1, 3, 3)), pbc=np.zeros((1, 3), np.int32), offsets=np.array([0, 2]))
+    inclusive = _hip.neighbor_graph(hip_context, batch, 1.0, include_boundary=True)
+    assert inclusive["offsets"].tolist() == [0, 2, 4] and 1.0 in inclusive["distance2"].tolist()
+    exclusive = _hip.neighbor_graph(hip_context, batch, 1.0, include_boundary=False)
+    assert exclusive["offsets"].tolist() == [0, 1, 2]
+
+
+@pytest.mark.parametrize("manifest", ["manifest.json", "external_manifest.json"])
+@pytest.mark.parametrize("dtype", ["float64", "float32"])
+def test_public_soap_reproduces_goldens(manifest, dtype):
+    meta, raw, expected = load_golden("reference_soap", manifest)
+    p = meta["configuration"]["parameters"]
+    ids = meta["result"]["structure_ids"]
+    batch = mdx.StructureBatch(raw.numbers, raw.positions, raw.cells, raw.pbc, raw.offsets, ids)
+    with mdx.SOAP(species=p["species"], r_cut=p["r_cut"], n_max=p["n_max"], l_max=p["l_max"],
+                  sigma=p.get("sigma", 1.0), average=p["average"],
+                  output=mdx.OutputOptions(dtype=dtype)) as soap:
+        result = soap.compute(batch)
+    tol = meta["tolerance"]
+    if dtype == "float64":
+        np.testing.assert_allclose(result.values, expected["values"], rtol=tol["rtol"], atol=tol["atol"])
+    else:
+        assert result.values.dtype == np.float32
+        assert scaled_error(result.values, expected["values"]) <= F32_GATE
+    assert list(result.labels) == meta["result"]["labels"]
+    assert result.level.value == meta["result"]["level"]
+    assert list(result.structure_ids) == ids
+    expected_offsets = meta["result"]["row_offsets"]
+    assert (result.row_offsets is None and expected_offsets is None) or \
+        result.row_offsets.tolist() == expected_offsets
+    if "samples" in expected:
+        np.testing.assert_array_equal(result.samples, expected["samples"])
+    assert result.metadata["backend"] == "mdescriptor-hip"
+    assert result.metadata["execution"]["device"] == "hip"
+    assert not result.values.flags.writeable
+
+
+def _edge_batch():
+    """Empty structure, single isolated atom, a tiny periodic cell that needs
+    several image shells, atoms outside the home cell, and an isolated
+    molecule, in one batch."""
+
+    rng = np.random.default_rng(5)
+    tiny = np.array([[1.9, 0.0, 0.0], [0.3, 2.1, 0.0], [0.2, -0.4, 2.3]])
+    big = np.diag([7.0, 7.5, 8.0])
+    parts = [
+        (np.array([], np.int32), np.zeros((0, 3)), np.zeros((3, 3)), [0, 0, 0]),
+        (np.array([8]), np.array([[0.1, 0.2, 0.3]]), np.zeros((3, 3)), [0, 0, 0]),
+        (np.array([1, 8]), rng.uniform(0, 1, (2, 3)) @ tiny, tiny, [1, 1, 1]),
+        (np.array([8, 1, 1, 6]), rng.uniform(-0.5, 1.5, (4, 3)) @ big, big, [1, 1, 1]),
+        (np.array([6, 1, 1, 1, 8]), rng.normal(size=(5, 3)) * 1.3, np.zeros((3, 3)), [0, 0, 0]),
+    ]
+    numbers = np.concatenate([p[0] for p in parts]).astype(np.int32)
+    positions = np.concatenate([p[1] for p in parts])
+    offsets = np.concatenate([[0], np.cumsum([len(p[0]) for p in parts])])
+    return mdx.StructureBatch(numbers, positions, np.stack([p[2] for p in parts]), np.array([p[3] for p in parts]),
+                              offsets, [f"edge{i}" for i in range(len(parts))])
+
+
+@pytest.mark.parametrize("average", ["off", "inner", "outer"])
+def test_edge_cases(hip_context, oracle, average):
+    params = dict(species=[1, 6, 8], r_cut=4.0, n_max=4, l_max=4, dtype="float64")
+    values, _ = _check(hip_context, oracle, _edge_batch(), params, average, "float64")
+    if average != "off":
+        assert np.all(values[0] == 0.0)
+
+
+def test_empty_batch(hip_context):
+    batch = mdx.StructureBatch(np.zeros(0, np.int32), np.zeros((0, 3)), np.zeros((0, 3, 3)), np.zeros((0, 3)), [0],
+                               [])
+    for average in ("off", "inner"):
+        plan, _ = _plan(hip_context, dict(species=[1, 8], r_cut=4.0, n_max=2, l_max=2, dtype="float64"), average)
+        values, _ = plan.compute(batch)
+        plan.close()
+        assert values.shape == (0, plan.features)
+
+
+def test_invalid_batch_is_rejected_on_the_host(hip_context):
+    batch = SimpleNamespace(numbers=np.array([1, 8], np.int32), positions=np.zeros((2, 3)),
+                            cells=np.zeros((1, 3, 3)), pbc=np.ones((1, 3), np.int32), offsets=np.array([0, 2]))
+    plan, _ = _plan(hip_context, dict(species=[1, 8], r_cut=4.0, n_max=2, l_max=2, dtype="float64"), "off")
+    with pytest.raises(ValueError):
+        plan.compute(batch)
+    undeclared = SimpleNamespace(numbers=np.array([1, 9], np.int32), positions=np.eye(2, 3),
+                                 cells=np.zeros((1, 3, 3)), pbc=np.zeros((1, 3), np.int32), offsets=np.array([0, 2]))
+    with pytest.raises(ValueError):
+        plan.compute(undeclared)
+    plan.close()
+
+
+def test_cancellation_flag(hip_context):
+    work = workloads.config(1, "small")
+    plan, _ = _plan(hip_context, work.params, "off")
+    flag = ctypes.c_int32(1)
+    with pytest.raises(_hip.HipCancelledError):
+        plan.compute(work.batch, flag)
+    flag.value = 0
+    values, _ = plan.compute(work.batch, flag)
+    plan.close()
+    assert np.all(np.isfinite(values))
+    control = mdx.ComputeControl()
+    control.cancel()
+    with pytest.raises(mdx.CancelledError):
+        mdx.SOAP(species=[1, 8], r_cut=4.5, n_max=4, l_max=3, average="off").compute(work.batch, control=control)
+
+
+def test_public_api_matches_c_abi_and_block_splitting(hip_context):
+    work = workloads.config(3, "small")
+    p = work.params
+    plan, _ = _plan(hip_context, p)
+    direct, _ = plan.compute(work.batch)
+    plan.close()
+    soap = mdx.SOAP(species=p["species"], r_cut=p["r_cut"], n_max=p["n_max"], l_max=p["l_max"],
+                    average=p["average"], output=mdx.OutputOptions(dtype=p["dtype"]))
+    control = mdx.ComputeControl()
+    result = soap.compute(work.batch, control=control)
+    np.testing.assert_array_equal(result.values, direct)
+    assert control.completed() == control.total() == work.batch.structures
+    soap._backend.atom_budget = 700
+    split = soap.compute(work.batch)
+    np.testing.assert_array_equal(split.values, direct)
+    soap.close()
+
+
+def test_device_resident_run_matches_compute(hip_context):
+    work = workloads.config(2, "small")
+    plan, _ = _plan(hip_context, work.params)
+    host, _ = plan.compute(work.batch)
+    device_batch = _hip.DeviceBatch(plan, work.batch)
+    pitch = plan.features * host.itemsize
+    memory = _hip.DeviceMemory(device_batch.rows * pitch)
+    device_batch.run(memory.address, pitch)
+    resident = memory.to_host(np.empty_like(host))
+    np.testing.assert_array_equal(resident, host)
+    memory.free()
+    device_batch.close()
+    plan.close()
+
+
+def test_full_config2_structure_against_oracle(hip_context, oracle):
+    """Headline configuration at full size: every row finite, and the rows of
+    one 4096-atom cell equal to the oracle's for that cell alone."""
+
+    work = workloads.config(2)
+    plan, basis = _plan(hip_context, work.params)
+    values, timing = plan.compute(work.batch)
+    plan.close()
+    assert values.shape == (65536, 3696) and values.dtype == np.float32
+    assert np.all(np.isfinite(values))
+    assert timing["pairs"] > 17_000_000
+    for s in (0, 15):
+        part = work.batch._slice_view(s, s + 1)
+        expected = _oracle_soap(oracle, part, work.params, basis, "off")
+        rows = values[work.batch.offsets[s]:work.batch.offsets[s + 1]]
+        assert scaled_error(rows, expected) <= F32_GATE
+
+
+def test_supercell_replication_at_full_size(hip_context):
+    """A periodic cell tiled 2x2x2 gives every image the same features as its
+    original atom (the 32000-atom HEA size, built from a 4000-atom cell)."""
+
+    base = workloads.hea_fcc(10)
+    p = base.params
+    cell = base.batch.cells[0]
+    shifts = np.array([[i, j, k] for i in range(2) for j in range(2) for k in range(2)], dtype=np.float64)
+    positions = np.concatenate([base.batch.positions + s @ cell for s in shifts])
+    numbers = np.tile(base.batch.numbers, 8)
+    big = mdx.StructureBatch(numbers, positions, (2 * cell)[None], [[1, 1, 1]], [0, len(numbers)], ["tiled"])
+    plan, _ = _plan(hip_context, p, "off", "float64")
+    small_values, _ = plan.compute(base.batch)
+    big_values, _ = plan.compute(big)
+    plan.close()
+    assert big_values.shape[0] == 32000
+    n = base.batch.atoms
+    for image in range(8):
+        assert scaled_error(big_values[image * n:(image + 1) * n], small_values) <= 1e-9
+
+
+def test_translation_invariance_full_config5(hip_context):
+    work = workloads.config(5)
+    plan, _ = _plan(hip_context, work.params, "off", "float32")
+    first, timing = plan.compute(work.batch)
+    moved = mdx.StructureBatch(work.batch.numbers, work.batch.positions + np.array([1.37, -2.11, 0.53]),
+                               work.batch.cells, work.batch.pbc, work.batch.offsets, work.batch.ids)
+    second, _ = plan.compute(moved)
+    plan.close()
+    assert first.shape == (216000, 780)
+    assert scaled_error(second, first.astype(np.float64)) <= F32_GATE

@@ -1,0 +1,287 @@
+"""Pins of the CPU oracle by mathematics, independent of any stored output.
+
+Each check is chosen so that a plausible slip in the restatement fails it:
+
+* solid harmonics against scipy's complex ``sph_harm`` times r^l (a sign,
+  phase or normalisation slip, a swapped cos/sin slot);
+* the radial basis: beta_l^T S_l beta_l = I for the analytic GTO overlap (a
+  wrong exponent or a transposed beta);
+* the whole expansion against a 3D quadrature of the Gaussian-smeared density
+  projected on r^l exp(-alpha r^2) Y_lm (a wrong prefactor, exponent, pi
+  power or harmonic);
+* the neighbour graph against a brute-force sum over images (the triclinic
+  test cell of the reference's tests/test_neighbor_graph.py:40-85) and the
+  reference's inclusive/exclusive boundary case
+  (cpp/tests/test_public_api.cpp:56-78);
+* SOAP invariances (rotation, translation, permutation of atoms) and the
+  averaging closed forms (outer = row mean of the atom rows; inner = off for
+  a one-atom structure; empty structures give zero rows).
+"""
+
+from __future__ import annotations
+
+import warnings
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+
+from mdescriptor_amd.descriptors.basis import basis_gto
+
+
+def _batch(numbers, positions, cells, pbc, offsets):
+    return SimpleNamespace(numbers=np.asarray(numbers, np.int32), positions=np.asarray(positions, np.float64),
+                           cells=np.asarray(cells, np.float64).reshape(-1, 3, 3),
+                           pbc=np.asarray(pbc, np.int32).reshape(-1, 3), offsets=np.asarray(offsets, np.int64))
+
+
+def _sph_harm(m, l, azimuth, polar):
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore", DeprecationWarning)
+        from scipy.special import sph_harm
+
+        return sph_harm(m, l, azimuth, polar)
+
+
+def _real_harmonic(l, m, polar, azimuth):
+    """Real spherical harmonic on the unit sphere with the Condon-Shortley
+    phase: Y_l0, sqrt(2) Re Y_lm (m > 0), sqrt(2) Im Y_l|m| (m < 0)."""
+
+    y = _sph_harm(abs(m), l, azimuth, polar)
+    if m == 0:
+        return y.real
+    return np.sqrt(2.0) * (y.real if m > 0 else y.imag)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_solid_harmonics_match_scipy(oracle, seed):
+    rng = np.random.default_rng(seed)
+    l_max = 12
+    for _ in range(20):
+        v = rng.normal(size=3) * rng.uniform(0.2, 3.0)
+        r = np.linalg.norm(v)
+        polar, azimuth = np.arccos(v[2] / r), np.arctan2(v[1], v[0])
+        values = oracle.solid_harmonics(v, l_max)
+        for l in range(l_max + 1):
+            for m in range(l + 1):
+                expected_cos = _real_harmonic(l, m, polar, azimuth) * r**l
+                scale = max(1.0, r**l)
+                assert abs(values[l * l + l - m] - expected_cos) <= 1e-12 * scale
+                if m > 0:
+                    expected_sin = _real_harmonic(l, -m, polar, azimuth) * r**l
+                    assert abs(values[l * l + l + m] - expected_sin) <= 1e-12 * scale
+
+
+def test_solid_harmonics_of_zero_vector(oracle):
+    values = oracle.solid_harmonics([0.0, 0.0, 0.0], 6)
+    assert values[0] == pytest.approx(0.5 / np.sqrt(np.pi), rel=1e-15)
+    assert np.all(values[1:] == 0.0)
+
+
+@pytest.mark.parametrize("r_cut,n_max,l_max", [(3.5, 2, 2), (4.5, 4, 3), (5.0, 8, 6), (5.0, 6, 4), (6.0, 8, 8),
+                                               (5.5, 12, 9)])
+def test_basis_is_loewdin_orthonormal(r_cut, n_max, l_max):
+    from math import gamma
+
+    alphas, betas = basis_gto(r_cut, n_max, l_max)
+    radii = np.linspace(1.0, r_cut, n_max)
+    for l in range(l_max + 1):
+        # alpha makes r^l exp(-alpha r^2) equal 1e-3 at its own radius
+        np.testing.assert_allclose(radii**l * np.exp(-alphas[l] * radii**2), 1e-3, rtol=1e-9)
+        overlap = 0.5 * gamma(l + 1.5) * (alphas[l][:, None] + alphas[l][None, :]) ** (-l - 1.5)
+        beta = betas[l]
+        np.testing.assert_allclose(beta, beta.T, rtol=0, atol=1e-10 * np.abs(beta).max())
+        identity = beta.T @ overlap @ beta
+        # the overlap is ill-conditioned (cond up to ~1e13), so the identity
+        # holds to about cond * eps
+        tol = max(1e-12, 100 * np.finfo(float).eps * np.linalg.cond(overlap))
+        np.testing.assert_allclose(identity, np.eye(n_max), atol=tol)
+
+
+def test_basis_rejects_unnormalisable():
+    with pytest.raises(ValueError):
+        basis_gto(5.0, 16, 20)
+
+
+def _quadrature_soap(positions, types, n_species, sigma, r_cut, n_max, l_max):
+    """SOAP row of centre 0 by direct 3D quadrature of
+    c[t][n][lm] = sum_k beta[l][n][k] * int rho_t(r) r^l exp(-alpha_lk r^2) Y_lm(r_hat) d^3r
+    with rho_t = sum_{j of type t} exp(-|r - r_j|^2 / (2 sigma^2)), then
+    p = pi sqrt(8 / (2l + 1)) sum_m c1 c2 (the DScribe power-spectrum scale)."""
+
+    alphas, betas = basis_gto(r_cut, n_max, l_max)
+    eta = 1.0 / (2.0 * sigma * sigma)
+    xr, wr = np.polynomial.legendre.leggauss(240)
+    radius = 14.0
+    r = (xr + 1.0) * radius / 2.0
+    wr = wr * radius / 2.0
+    xc, wc = np.polynomial.legendre.leggauss(48)
+    nphi = 96
+    phi = np.arange(nphi) * 2.0 * np.pi / nphi
+    polar, azimuth = np.meshgrid(np.arccos(xc), phi, indexing="ij")
+    wang = (wc[:, None] * (2.0 * np.pi / nphi) * np.ones(nphi)[None, :]).ravel()
+    dirs = np.stack([np.sin(polar) * np.cos(azimuth), np.sin(polar) * np.sin(azimuth), np.cos(polar)], -1)
+    dirs = dirs.reshape(-1, 3)
+    pts = r[:, None, None] * dirs[None, :, :]
+    centre = positions[0]
+    H = (l_max + 1) ** 2
+    coeff = np.zeros((n_species, n_max, H))
+    harmonics = {(l, m): _real_harmonic(l, m, polar, azimuth).ravel()
+                 for l in range(l_max + 1) for m in range(-l, l + 1)}
+    for t in range(n_species):
+        rho = np.zeros(pts.shape[:2])
+        for j in np.flatnonzero(types == t):
+            rho += np.exp(-eta * np.sum((pts - (positions[j] - centre)) ** 2, axis=-1))
+        for l in range(l_max + 1):
+            radial = np.stack([wr * r**2 * r**l * np.exp(-alphas[l, k] * r**2) for k in range(n_max)])
+            for m in range(-l, l + 1):
+                angular = rho @ (harmonics[(l, m)] * wang)
+                raw = radial @ angular
+                coeff[t, :, l * l + l + m] = betas[l] @ raw
+    out = []
+    for t1 in range(n_species):
+        for t2 in range(t1, n_species):
+            for l in range(l_max + 1):
+                block = slice(l * l, (l + 1) ** 2)
+                for n1 in range(n_max):
+                    for n2 in range(n1 if t1 == t2 else 0, n_max):
+                        out.append(np.pi * np.sqrt(8.0 / (2 * l + 1)) * coeff[t1, n1, block] @ coeff[t2, n2, block])
+    return np.array(out)
+
+
+@pytest.mark.parametrize("sigma,n_max,l_max", [(1.0, 3, 2), (0.7, 2, 3)])
+def test_expansion_matches_density_quadrature(oracle, sigma, n_max, l_max):
+    positions = np.array([[0.0, 0.0, 0.0], [0.6, -0.8, 1.2], [-1.1, 0.4, 0.3]])
+    types = np.array([0, 1, 0])
+    numbers = np.array([1, 8, 1])
+    r_cut = 3.5
+    alphas, betas = basis_gto(r_cut, n_max, l_max)
+    batch = _batch(numbers, positions, np.zeros((1, 3, 3)), np.zeros((1, 3)), [0, 3])
+    values = oracle.soap(batch, species=[1, 8], n_max=n_max, l_max=l_max, r_cut=r_cut, sigma=sigma,
+                         alphas=alphas, betas=betas, average="off")
+    expected = _quadrature_soap(positions, types, 2, sigma, r_cut, n_max, l_max)
+    np.testing.assert_allclose(values[0], expected, rtol=0, atol=1e-10 * np.abs(expected).max())
+
+
+def _brute_force_graph(positions, cell, periodic, cutoff, reach=4):
+    pairs = {}
+    shifts = [(0, 0, 0)]
+    if periodic:
+        span = range(-reach, reach + 1)
+        shifts = [(a, b, c) for a in span for b in span for c in span]
+    for i in range(len(positions)):
+        for j in range(len(positions)):
+            for a, b, c in shifts:
+                shift = (a * cell[0] + b * cell[1]) + c * cell[2]
+                d = (positions[j] + shift) - positions[i]
+                d2 = (d[0] * d[0] + d[1] * d[1]) + d[2] * d[2]
+                if d2 <= cutoff * cutoff:
+                    pairs[(i, j, a, b, c)] = d2
+    return pairs
+
+
+@pytest.mark.parametrize("case", ["triclinic", "random"])
+def test_graph_matches_brute_force_images(oracle, case):
+    if case == "triclinic":
+        cell = np.array([[1.8, 0.0, 0.0], [0.25, 1.7, 0.0], [0.1, 0.2, 1.9]])
+        positions = np.array([[0.18, 0.29, 0.41], [0.96, 0.85, 1.12]])
+        cutoff = 2.3
+    else:
+        rng = np.random.default_rng(7)
+        cell = np.diag([3.1, 2.7, 3.4]) + rng.uniform(-0.4, 0.4, (3, 3))
+        positions = rng.uniform(0, 1, (6, 3)) @ cell
+        cutoff = 3.9
+    batch = _batch(np.full(len(positions), 8), positions, cell, np.ones(3), [0, len(positions)])
+    g = oracle.graph(batch, cutoff)
+    expected = _brute_force_graph(positions, cell, True, cutoff)
+    centre = np.repeat(np.arange(len(positions)), np.diff(g["offsets"]))
+    actual = {(int(c), int(a), *map(int, s)): d2 for c, a, s, d2 in zip(centre, g["atoms"], g["shifts"],
+                                                                        g["distance2"])}
+    assert set(actual) == set(expected)
+    for key, d2 in actual.items():
+        assert d2 == expected[key]
+    assert (0, 0, 0, 0, 0) in actual
+
+
+def test_graph_boundary_is_inclusive_for_soap(oracle):
+    batch = _batch([1, 8], [[0, 0, 0], [1, 0, 0]], np.zeros((1, 3, 3)), np.zeros((1, 3)), [0, 2])
+    inclusive = oracle.graph(batch, 1.0, include_boundary=True)
+    assert inclusive["offsets"].tolist() == [0, 2, 4]
+    assert 1.0 in inclusive["distance2"].tolist()
+    exclusive = oracle.graph(batch, 1.0, include_boundary=False)
+    assert exclusive["offsets"].tolist() == [0, 1, 2]
+
+
+def _soap(oracle, batch, species, average="off", n_max=4, l_max=4, r_cut=4.0, sigma=1.0):
+    alphas, betas = basis_gto(r_cut, n_max, l_max)
+    return oracle.soap(batch, species=species, n_max=n_max, l_max=l_max, r_cut=r_cut, sigma=sigma, alphas=alphas,
+                       betas=betas, average=average)
+
+
+def _random_rotation(rng):
+    q, r = np.linalg.qr(rng.normal(size=(3, 3)))
+    q = q * np.sign(np.diag(r))
+    if np.linalg.det(q) < 0:
+        q[:, 0] = -q[:, 0]
+    return q
+
+
+def test_soap_invariances(oracle):
+    rng = np.random.default_rng(3)
+    cell = np.diag([5.0, 5.5, 6.0]) + rng.uniform(-0.5, 0.5, (3, 3))
+    positions = rng.uniform(0, 1, (10, 3)) @ cell
+    numbers = rng.choice([1, 6, 8], size=10)
+    species = [1, 6, 8]
+    base = _soap(oracle, _batch(numbers, positions, cell, np.ones(3), [0, 10]), species)
+    scale = np.abs(base).max()
+
+    shift = np.array([0.37, -1.21, 2.05])
+    moved = _soap(oracle, _batch(numbers, positions + shift, cell, np.ones(3), [0, 10]), species)
+    np.testing.assert_allclose(moved, base, atol=1e-10 * scale)
+
+    rot = _random_rotation(rng)
+    rotated = _soap(oracle, _batch(numbers, positions @ rot.T, cell @ rot.T, np.ones(3), [0, 10]), species)
+    np.testing.assert_allclose(rotated, base, atol=1e-9 * scale)
+
+    perm = rng.permutation(10)
+    permuted = _soap(oracle, _batch(numbers[perm], positions[perm], cell, np.ones(3), [0, 10]), species)
+    np.testing.assert_allclose(permuted, base[perm], atol=1e-10 * scale)
+
+
+def test_isolated_atom_has_only_l0_features(oracle):
+    batch = _batch([6], [[0.3, 0.2, 0.1]], np.zeros((1, 3, 3)), np.zeros((1, 3)), [0, 1])
+    values = _soap(oracle, batch, [1, 6], n_max=3, l_max=3)[0]
+    from mdescriptor_amd.descriptors.soap import SoapSettings
+
+    labels = SoapSettings(species=[1, 6], n_max=3, l_max=3, r_cut=4.0).labels()
+    for label, value in zip(labels, values):
+        if "z1=6,z2=6,l=0" in label:
+            assert value > 0
+        else:
+            assert value == 0.0
+
+
+def test_averaging_closed_forms(oracle):
+    rng = np.random.default_rng(11)
+    # structure 0: periodic, 5 atoms; structure 1: one isolated atom;
+    # structure 2: empty; structure 3: isolated molecule of 4 atoms
+    cell0 = np.diag([4.0, 4.2, 4.4])
+    pos = np.concatenate([rng.uniform(0, 1, (5, 3)) @ cell0, [[0.0, 0.0, 0.0]], rng.normal(size=(4, 3)) * 1.2])
+    numbers = np.array([1, 8, 8, 1, 6, 6, 1, 8, 6, 1])
+    cells = np.stack([cell0, np.zeros((3, 3)), np.zeros((3, 3)), np.zeros((3, 3))])
+    pbc = np.array([[1, 1, 1], [0, 0, 0], [0, 0, 0], [0, 0, 0]])
+    offsets = [0, 5, 6, 6, 10]
+    batch = _batch(numbers, pos, cells, pbc, offsets)
+    species = [1, 6, 8]
+    off = _soap(oracle, batch, species, "off")
+    outer = _soap(oracle, batch, species, "outer")
+    inner = _soap(oracle, batch, species, "inner")
+    scale = np.abs(off).max()
+    for s in range(4):
+        rows = off[offsets[s]:offsets[s + 1]]
+        expected = rows.mean(axis=0) if len(rows) else np.zeros(off.shape[1])
+        np.testing.assert_allclose(outer[s], expected, atol=1e-12 * scale)
+    np.testing.assert_allclose(inner[1], off[5], atol=1e-13 * scale)
+    assert np.all(inner[2] == 0.0) and np.all(outer[2] == 0.0)
+    # inner <= outer in the l = 0, same-channel diagonal (Jensen / Cauchy-Schwarz)
+    assert not np.allclose(inner[0], outer[0])
