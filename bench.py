@@ -11,6 +11,15 @@ for the dominant kernel (the expansion kernel, FP64: its algorithmic flops
 per launch over its launch time from HIP events on the library's stream) and
 a ``cpu_baseline`` object (the reference's own C++ SOAP compiled in place,
 ``oracle/_ref``, timed on this host's cores on a bounded sample).
+
+``roofline.traffic`` (HBM bytes per launch of that kernel) is read from the
+committed counter summary ``profiles/k_soap_mfma_<workload>_traffic.txt``
+when it exists for the benchmarked workload; it comes from two rocprofv3
+``--pmc`` runs (FETCH_SIZE, WRITE_SIZE) of this script, each scaled by the
+same counter on a device copy of known size (``--calibrate-copy``).
+
+``--calibrate-copy MIB`` only runs that copy: five launches of a plain
+device-to-device copy of MIB mebibytes, then exits.
 """
 
 from __future__ import annotations
@@ -39,6 +48,53 @@ def flops_per_env(kbar: float, S: int, n: int, l_max: int) -> float:
 
     H = (l_max + 1) ** 2
     return 2.0 * kbar * n * H + 2.0 * S * n * n * H + S * n * (S * n + 1) * H
+
+
+def traffic_from_profile(workload_name: str) -> tuple[float | None, str | None]:
+    """HBM bytes per launch recorded in the committed counter summary."""
+
+    path = ROOT / "profiles" / f"k_soap_mfma_{workload_name}_traffic.txt"
+    if not path.is_file():
+        return None, None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch="):
+            return float(line.split("=", 1)[1]), str(path.relative_to(ROOT))
+    return None, None
+
+
+def calibrate_copy(mib: int) -> int:
+    import torch
+
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4, "launches": 5}))
+    return 0
+
+
+def end_to_end(plan, batch, repeats: int = 3) -> dict:
+    """compute() from host arrays into a host matrix: upload, graph,
+    expansion and the device-to-host copy of the whole output -- into the
+    page-locked result the API returns by default, and into a caller's
+    pageable array (staged by the library)."""
+
+    report = {}
+    for name, make_out in (("pinned", lambda: None),
+                           ("pageable", lambda: np.empty((plan.rows(batch), plan.features), dtype=plan.dtype))):
+        seconds = []
+        for _ in range(repeats):
+            out = make_out()
+            t0 = time.perf_counter()
+            values, timing = plan.compute(batch, out=out)
+            seconds.append(time.perf_counter() - t0)
+            del values, out
+        best = min(seconds)
+        report[name] = {"envs_per_s": batch.atoms / best, "seconds": best, "d2h_ms": timing["d2h_ms"],
+                        "h2d_ms": timing["h2d_ms"], "device_ms": timing["total_ms"]}
+    return report
 
 
 def cpu_baseline(workload, alphas, betas, threads: int, budget_s: float = 30.0) -> dict:
@@ -76,7 +132,11 @@ def main() -> int:
     parser.add_argument("--config", type=int, default=2, help="benchmark configuration 1-5 (default 2)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-threads", type=int, default=0)
+    parser.add_argument("--no-end-to-end", action="store_true")
+    parser.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB")
     args = parser.parse_args()
+    if args.calibrate_copy:
+        return calibrate_copy(args.calibrate_copy)
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; the SOAP path shards by structure or "
                                    "centre range across GPUs (see DESIGN.md) but no multi-GPU run is provided",
@@ -119,6 +179,10 @@ def main() -> int:
     launch_ms = statistics.mean(t["expansion_ms"] for t in timings) / launches
     achieved = flops_launch / (launch_ms * 1e-3) / 1e12
     H = (l_max + 1) ** 2
+    traffic, traffic_source = traffic_from_profile(workload.name)
+    tiles = int(timings[-1]["expansion_tiles"])
+    kernel = (f"k_soap_mfma<{tiles}> (expansion + beta + power spectrum + write)"
+              if tiles else "k_soap_expand (expansion + beta + power spectrum + write)")
     result = {
         "metric": METRIC,
         "value": value,
@@ -151,10 +215,11 @@ def main() -> int:
             "peak": FP64_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": achieved / FP64_PEAK_TFLOPS,
-            "traffic": None,
-            "kernel": "k_soap_expand (expansion + beta + power spectrum + write)",
+            "traffic": traffic,
+            "kernel": kernel,
             "flops_per_launch": flops_launch,
             "launch_ms": launch_ms,
+            "traffic_source": traffic_source,
         },
         "breakdown": {
             "graph_ms": statistics.mean(t["graph_ms"] for t in timings),
@@ -170,6 +235,8 @@ def main() -> int:
             "H": H,
         },
     }
+    if not args.no_end_to_end:
+        result["end_to_end"] = end_to_end(plan, batch)
     if not args.no_cpu_baseline:
         threads = args.cpu_threads or min(batch.structures if batch.structures > 1 else 10**9,
                                           len(os.sched_getaffinity(0)), 16)

@@ -17,6 +17,7 @@
 #ifndef MDX_HIP_H
 #define MDX_HIP_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -84,6 +85,8 @@ typedef struct mdx_timing {
     int64_t pairs;       /* neighbour pairs found at the padded SOAP cutoff */
     int64_t binned;      /* periodic images binned into the cell grid */
     int64_t expansion_launches; /* launches of the expansion kernel in the run */
+    int64_t expansion_tiles;    /* 16x16 tiles of the matrix-core kernel's template,
+                                   0 when the generic kernel ran */
 } mdx_timing;
 
 typedef struct mdx_hip_ctx mdx_hip_ctx;
@@ -153,6 +156,16 @@ int mdx_hip_neighbors_build(mdx_hip_ctx* ctx, const mdx_batch_view* batch, doubl
                             int32_t include_boundary, int64_t* pairs);
 int mdx_hip_neighbors_fetch(mdx_hip_ctx* ctx, int64_t* offsets, int32_t* neighbors, int32_t* shifts,
                             double* displacements, double* distance2);
+
+/* Page-locked host memory for result matrices.  mdx_hip_soap_compute copies
+ * into such a buffer with one DMA at the full PCIe rate; into pageable memory
+ * it stages through the context's pinned ring and copies out on host threads.
+ * No reference counterpart: the reference's CUDA context copies straight into
+ * the caller's pageable buffer (download_output_slice_into,
+ * cpp/cuda/src/context.cu:115-137).  Returns MDX_OUT_OF_MEMORY when it cannot
+ * allocate. */
+int mdx_hip_host_alloc(size_t bytes, void** out);
+void mdx_hip_host_free(void* ptr);
 
 /* Library version and build target, for diagnostics. */
 const char* mdx_hip_version(void);

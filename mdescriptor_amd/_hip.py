@@ -19,6 +19,7 @@ library nothing here computes.
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from collections.abc import Mapping
 from pathlib import Path
@@ -96,6 +97,7 @@ class Timing(ctypes.Structure):
         ("pairs", ctypes.c_int64),
         ("binned", ctypes.c_int64),
         ("expansion_launches", ctypes.c_int64),
+        ("expansion_tiles", ctypes.c_int64),
     ]
 
     def as_dict(self) -> dict[str, float]:
@@ -136,6 +138,8 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         ctypes.c_int,
         [ctypes.c_void_p, _i64p, _i32p, _i32p, _f64p, _f64p],
     ),
+    "mdx_hip_host_alloc": (ctypes.c_int, [ctypes.c_size_t, ctypes.POINTER(ctypes.c_void_p)]),
+    "mdx_hip_host_free": (None, [ctypes.c_void_p]),
     "mdx_hip_version": (ctypes.c_char_p, []),
 }
 
@@ -227,6 +231,96 @@ class Context:
             pass
 
 
+class PinnedPool:
+    """Page-locked host blocks for result matrices, reused across calls.
+
+    A result written into pinned memory arrives with one DMA at the PCIe rate
+    (pageable destinations are staged by the library).  Pinning costs a few
+    milliseconds per gigabyte, so released blocks are kept, up to
+    ``cache_bytes`` in total, and handed out again to requests of at least
+    half their size.
+    """
+
+    GRAIN = 2 << 20
+
+    def __init__(self, cache_bytes: int = 4 << 30) -> None:
+        self.cache_bytes = int(cache_bytes)
+        self._free: list[tuple[int, int]] = []  # (size, address)
+        self._cached = 0
+        self._lock = threading.Lock()
+
+    def acquire(self, nbytes: int) -> tuple[int, int] | None:
+        size = max(self.GRAIN, -(-int(nbytes) // self.GRAIN) * self.GRAIN)
+        with self._lock:
+            best = None
+            for i, (have, address) in enumerate(self._free):
+                if size <= have <= 2 * size and (best is None or have < self._free[best][0]):
+                    best = i
+            if best is not None:
+                have, address = self._free.pop(best)
+                self._cached -= have
+                return address, have
+        lib = load_library()
+        pointer = ctypes.c_void_p()
+        if lib.mdx_hip_host_alloc(size, ctypes.byref(pointer)) != MDX_OK or not pointer.value:
+            return None
+        return int(pointer.value), size
+
+    def release(self, address: int, size: int) -> None:
+        with self._lock:
+            if self._cached + size <= self.cache_bytes:
+                self._free.append((size, address))
+                self._cached += size
+                return
+        load_library().mdx_hip_host_free(ctypes.c_void_p(address))
+
+    def clear(self) -> None:
+        with self._lock:
+            blocks, self._free, self._cached = self._free, [], 0
+        for _, address in blocks:
+            load_library().mdx_hip_host_free(ctypes.c_void_p(address))
+
+
+class _PinnedArrayBase:
+    """Owner of one pinned block, exposed to NumPy through the array interface;
+    the block returns to the pool when the last array viewing it is gone."""
+
+    def __init__(self, pool: PinnedPool, address: int, size: int, shape: tuple[int, ...], dtype: np.dtype) -> None:
+        self._pool, self._address, self._size = pool, address, size
+        self.__array_interface__ = {"shape": shape, "typestr": dtype.str, "data": (address, False), "version": 3}
+
+    def __del__(self) -> None:  # pragma: no cover - runs at garbage collection
+        try:
+            self._pool.release(self._address, self._size)
+        except Exception:
+            pass
+
+
+pinned_pool = PinnedPool(int(os.environ.get("MDX_HIP_PINNED_CACHE_MB", "4096")) << 20)
+
+
+def pinned_empty(shape: tuple[int, ...], dtype: Any) -> np.ndarray:
+    """Uninitialised C-contiguous array in page-locked host memory (pageable
+    memory when pinning fails or the array is empty)."""
+
+    dtype = np.dtype(dtype)
+    shape = tuple(int(v) for v in shape)
+    nbytes = int(np.prod(shape, dtype=np.int64)) * dtype.itemsize
+    if nbytes == 0:
+        return np.empty(shape, dtype=dtype)
+    block = pinned_pool.acquire(nbytes)
+    if block is None:
+        return np.empty(shape, dtype=dtype)
+    return np.asarray(_PinnedArrayBase(pinned_pool, block[0], block[1], shape, dtype))
+
+
+def is_pinned(array: np.ndarray) -> bool:
+    base = array
+    while isinstance(base, np.ndarray):
+        base = base.base
+    return isinstance(base, _PinnedArrayBase)
+
+
 class SoapPlan:
     """Device-resident SOAP plan on a context."""
 
@@ -261,7 +355,7 @@ class SoapPlan:
         arrays = _BatchArrays(batch)
         rows = self.rows(batch)
         if out is None:
-            out = np.empty((rows, self.features), dtype=self.dtype)
+            out = pinned_empty((rows, self.features), self.dtype)
         elif (out.shape != (rows, self.features) or out.dtype != self.dtype or not out.flags.c_contiguous
               or not out.flags.writeable):
             raise ValueError(f"output must be a writable C-contiguous {self.dtype} array of shape "

@@ -81,7 +81,7 @@ class HipBackend:
         dtype = np.dtype((self.options.get("output") or {}).get("dtype", "float64"))
         level = "atom" if average == "off" else "structure"
         rows = batch.atoms if level == "atom" else batch.structures
-        values = np.empty((rows, int(self._feature_count)), dtype=dtype)
+        values = _hip.pinned_empty((rows, int(self._feature_count)), dtype)
         blocks = structure_blocks(batch.offsets, self.atom_budget)
         if control is not None:
             control.reset(batch.structures)

@@ -33,14 +33,18 @@ class DescriptorLevel(str, Enum):
 
 
 class _OwnedValues:
-    """A fresh C-contiguous matrix that the result may keep without copying."""
+    """A fresh C-contiguous matrix that the result may keep without copying:
+    either an array owning its memory or a whole page-locked block from the
+    HIP plugin's pool (an array whose base is the block's owner)."""
 
     __slots__ = ("array",)
 
     def __init__(self, array: Any) -> None:
         if not isinstance(array, np.ndarray):
             raise TypeError("owned descriptor values must be a NumPy array")
-        if array.ndim != 2 or not array.flags.c_contiguous or not array.flags.owndata:
+        owner = array.flags.owndata or (array.base is not None and not isinstance(array.base, np.ndarray)
+                                        and hasattr(array.base, "__array_interface__"))
+        if array.ndim != 2 or not array.flags.c_contiguous or not owner:
             raise ValueError("owned descriptor values must be a C-contiguous owning matrix")
         array.setflags(write=False)
         self.array = array

@@ -14,6 +14,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <new>
+#include <thread>
 #include <unordered_set>
 
 namespace {
@@ -180,9 +181,120 @@ void run_pipeline(mdx_hip_ctx* ctx, const mdx_soap_plan& plan, mdx::PreparedBatc
     }
 }
 
+// True for memory from hipHostMalloc (page-locked, DMA-able at full PCIe
+// rate); pageable memory reports "unregistered" or an error, which is cleared.
+bool is_pinned_host(const void* p) {
+    hipPointerAttribute_t attr{};
+    const hipError_t rc = hipPointerGetAttributes(&attr, p);
+    if (rc != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return attr.type == hipMemoryTypeHost;
+}
+
+// Copy rows x row_bytes of device memory into the caller's host rows (row
+// stride pitch) and wait for it.  Pinned destinations take one DMA.  Pageable
+// ones go through the context's pinned staging ring in chunks of whole rows:
+// while the DMA fills one half of the ring, host threads copy the other half
+// out, so the transfer runs near the PCIe rate instead of the driver's
+// pageable path (which the reference's download_output_slice_into,
+// cpp/cuda/src/context.cu:115-137, takes with one plain copy).
+void download_result(mdx_hip_ctx* ctx, const void* src, int64_t rows, int64_t row_bytes, void* dst, int64_t pitch) {
+    hipStream_t s = ctx->stream;
+    if (rows <= 0 || row_bytes <= 0) return;
+    const size_t total = static_cast<size_t>(rows) * static_cast<size_t>(row_bytes);
+    if (is_pinned_host(dst)) {
+        if (pitch == row_bytes) {
+            MDX_HIP(hipMemcpyAsync(dst, src, total, hipMemcpyDeviceToHost, s));
+        } else {
+            MDX_HIP(hipMemcpy2DAsync(dst, static_cast<size_t>(pitch), src, static_cast<size_t>(row_bytes),
+                                     static_cast<size_t>(row_bytes), static_cast<size_t>(rows), hipMemcpyDeviceToHost,
+                                     s));
+        }
+        MDX_HIP(hipStreamSynchronize(s));
+        return;
+    }
+    constexpr size_t kStageHalf = size_t(64) << 20;
+    const int64_t chunk_rows = std::max<int64_t>(1, static_cast<int64_t>(kStageHalf / static_cast<size_t>(row_bytes)));
+    const size_t half = static_cast<size_t>(chunk_rows) * static_cast<size_t>(row_bytes);
+    if (ctx->pinned == nullptr || ctx->pinned_bytes < 2 * half) {
+        if (ctx->pinned != nullptr) (void)hipHostFree(ctx->pinned);
+        ctx->pinned = nullptr;
+        ctx->pinned_bytes = 0;
+        const hipError_t rc = hipHostMalloc(&ctx->pinned, 2 * half, hipHostMallocDefault);
+        if (rc != hipSuccess || ctx->pinned == nullptr) {
+            (void)hipGetLastError();
+            ctx->pinned = nullptr;
+            throw mdx::Error(MDX_OUT_OF_MEMORY, "cannot allocate pinned staging for the result download");
+        }
+        ctx->pinned_bytes = 2 * half;
+    }
+    char* ring[2] = {static_cast<char*>(ctx->pinned), static_cast<char*>(ctx->pinned) + half};
+    const int64_t chunks = (rows + chunk_rows - 1) / chunk_rows;
+    auto enqueue = [&](int64_t c) {
+        const int64_t r0 = c * chunk_rows;
+        const int64_t nr = std::min(chunk_rows, rows - r0);
+        MDX_HIP(hipMemcpyAsync(ring[c & 1], static_cast<const char*>(src) + r0 * row_bytes,
+                               static_cast<size_t>(nr) * static_cast<size_t>(row_bytes), hipMemcpyDeviceToHost, s));
+        MDX_HIP(hipEventRecord(ctx->stage_events[c & 1], s));
+    };
+    const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+    const int threads = static_cast<int>(std::min(8u, hw));
+    enqueue(0);
+    for (int64_t c = 0; c < chunks; ++c) {
+        // the other half was copied out in the previous iteration, so it can take the next DMA
+        if (c + 1 < chunks) enqueue(c + 1);
+        MDX_HIP(hipEventSynchronize(ctx->stage_events[c & 1]));
+        const int64_t r0 = c * chunk_rows;
+        const int64_t nr = std::min(chunk_rows, rows - r0);
+        const char* from = ring[c & 1];
+        char* to = static_cast<char*>(dst) + r0 * pitch;
+        auto copy_rows = [&](int64_t a, int64_t b) {
+            if (pitch == row_bytes) {
+                std::memcpy(to + a * row_bytes, from + a * row_bytes, static_cast<size_t>((b - a) * row_bytes));
+            } else {
+                for (int64_t r = a; r < b; ++r) {
+                    std::memcpy(to + r * pitch, from + r * row_bytes, static_cast<size_t>(row_bytes));
+                }
+            }
+        };
+        const int parts = static_cast<int>(std::min<int64_t>(threads, nr));
+        if (parts <= 1) {
+            copy_rows(0, nr);
+            continue;
+        }
+        std::vector<std::thread> pool;
+        pool.reserve(static_cast<size_t>(parts - 1));
+        for (int t = 1; t < parts; ++t) {
+            pool.emplace_back(copy_rows, nr * t / parts, nr * (t + 1) / parts);
+        }
+        copy_rows(0, nr / parts);
+        for (auto& th : pool) th.join();
+    }
+}
+
 } // namespace
 
 extern "C" {
+
+int mdx_hip_host_alloc(size_t bytes, void** out) {
+    if (out == nullptr) return MDX_INVALID_ARGUMENT;
+    *out = nullptr;
+    return guarded(nullptr, [&] {
+        void* p = nullptr;
+        const hipError_t rc = hipHostMalloc(&p, std::max<size_t>(1, bytes), hipHostMallocDefault);
+        if (rc != hipSuccess || p == nullptr) {
+            (void)hipGetLastError();
+            throw mdx::Error(MDX_OUT_OF_MEMORY, "cannot allocate pinned host memory");
+        }
+        *out = p;
+    });
+}
+
+void mdx_hip_host_free(void* p) {
+    if (p != nullptr) (void)hipHostFree(p);
+}
 
 const char* mdx_hip_version(void) { return "mdx_hip 0.2.0 (gfx950)"; }
 
@@ -206,6 +318,7 @@ int mdx_hip_create(int device, mdx_hip_ctx** out) {
             ctx->device = device;
             MDX_HIP(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
             for (auto& ev : ctx->events) MDX_HIP(hipEventCreate(&ev));
+            for (auto& ev : ctx->stage_events) MDX_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
         } catch (...) {
             mdx_hip_destroy(ctx);
             throw;
@@ -223,6 +336,10 @@ void mdx_hip_destroy(mdx_hip_ctx* ctx) {
         std::lock_guard<std::mutex> lock(ctx->mutex);
         if (ctx->stream != nullptr) (void)hipStreamSynchronize(ctx->stream);
         for (auto& ev : ctx->events) {
+            if (ev != nullptr) (void)hipEventDestroy(ev);
+            ev = nullptr;
+        }
+        for (auto& ev : ctx->stage_events) {
             if (ev != nullptr) (void)hipEventDestroy(ev);
             ev = nullptr;
         }
@@ -398,14 +515,15 @@ int mdx_hip_soap_compute(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, const mdx_
         mdx::upload_batch(s, *batch, pb);
         ctx->out_dev.reserve(std::max<size_t>(1, static_cast<size_t>(rows) * static_cast<size_t>(row_bytes)));
         run_pipeline(ctx, *plan, pb, ctx->graph, ctx->partials, ctx->out_dev.ptr, row_bytes, cancel_flag, timing);
-        if (rows > 0 && row_bytes > 0) {
-            MDX_HIP(hipMemcpy2DAsync(out_host, static_cast<size_t>(out_pitch_bytes), ctx->out_dev.ptr,
-                                     static_cast<size_t>(row_bytes), static_cast<size_t>(row_bytes),
-                                     static_cast<size_t>(rows), hipMemcpyDeviceToHost, s));
-        }
+        MDX_HIP(hipStreamSynchronize(s));
+        check_cancel(cancel_flag);
+        const auto t0 = std::chrono::steady_clock::now();
+        download_result(ctx, ctx->out_dev.ptr, rows, row_bytes, out_host, out_pitch_bytes);
+        const auto t1 = std::chrono::steady_clock::now();
         MDX_HIP(hipEventRecord(ctx->events[6], s));
         MDX_HIP(hipStreamSynchronize(s));
         fill_timing(ctx, timing, true);
+        if (timing != nullptr) timing->d2h_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
     });
 }
 

@@ -147,9 +147,10 @@ struct mdx_hip_ctx {
     mdx::DeviceGraph graph;
     mdx::DeviceBuffer out_dev;        // device result of mdx_hip_soap_compute
     mdx::DeviceBuffer partials;       // inner/outer partial sums
-    void* pinned = nullptr;           // pinned staging for the result download
+    void* pinned = nullptr;           // pinned staging ring (two halves) for pageable result downloads
     size_t pinned_bytes = 0;
     hipEvent_t events[8] = {};
+    hipEvent_t stage_events[2] = {};  // completion of the DMA into each staging half
 };
 
 struct mdx_soap_plan {

@@ -446,7 +446,10 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
             launch_mfma_finalize(stream, pb, tab, md, d_partial, d_struct_items, out_device, pitch_bytes);
         }
         if (events != nullptr) MDX_HIP(hipEventRecord(events[4], stream));
-        if (timing != nullptr) timing->expansion_launches = launches;
+        if (timing != nullptr) {
+            timing->expansion_launches = launches;
+            timing->expansion_tiles = tt;
+        }
         return;
     }
     const int64_t acc_words = p.average == 1 ? d.C : p.average == 2 ? d.F : 0;
@@ -490,7 +493,10 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
         MDX_HIP(hipGetLastError());
     }
     if (events != nullptr) MDX_HIP(hipEventRecord(events[4], stream));
-    if (timing != nullptr) timing->expansion_launches = launches;
+    if (timing != nullptr) {
+        timing->expansion_launches = launches;
+        timing->expansion_tiles = 0;
+    }
 }
 
 } // namespace mdx

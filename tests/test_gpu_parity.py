@@ -256,6 +256,29 @@ def test_device_resident_run_matches_compute(hip_context):
     plan.close()
 
 
+def test_download_paths_agree(hip_context):
+    """Pinned destinations take one DMA; pageable ones go through the pinned
+    staging ring (several 64 MB chunks here) and host threads; a pitched
+    pageable destination is written row by row and its padding left alone."""
+
+    work = workloads.config(4, "small")
+    plan, _ = _plan(hip_context, dict(work.params, dtype="float64"), "off")
+    pinned, _ = plan.compute(work.batch)
+    assert _hip.is_pinned(pinned)
+    pageable = np.empty_like(np.asarray(pinned))
+    plan.compute(work.batch, out=pageable)
+    np.testing.assert_array_equal(pageable, pinned)
+    rows, features = pinned.shape
+    pitched = np.full((rows, features + 5), -7.0)
+    arrays = _hip._BatchArrays(work.batch)
+    hip_context.check(hip_context.lib.mdx_hip_soap_compute(
+        hip_context.handle, plan.handle, ctypes.byref(arrays.view), pitched.ctypes.data_as(ctypes.c_void_p), rows,
+        pitched.strides[0], None, None))
+    np.testing.assert_array_equal(pitched[:, :features], pinned)
+    assert np.all(pitched[:, features:] == -7.0)
+    plan.close()
+
+
 def test_full_config2_structure_against_oracle(hip_context, oracle):
     """Headline configuration at full size: every row finite, and the rows of
     one 4096-atom cell equal to the oracle's for that cell alone."""
@@ -263,8 +286,11 @@ def test_full_config2_structure_against_oracle(hip_context, oracle):
     work = workloads.config(2)
     plan, basis = _plan(hip_context, work.params)
     values, timing = plan.compute(work.batch)
+    staged = np.empty((65536, 3696), dtype=np.float32)
+    plan.compute(work.batch, out=staged)
     plan.close()
     assert values.shape == (65536, 3696) and values.dtype == np.float32
+    np.testing.assert_array_equal(staged, values)
     assert np.all(np.isfinite(values))
     assert timing["pairs"] > 17_000_000
     for s in (0, 15):
