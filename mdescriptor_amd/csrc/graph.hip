@@ -201,8 +201,8 @@ __global__ void k_bin_count(const StructGeom* geom, int64_t nstruct, const Image
 }
 
 __global__ void k_bin_fill(const StructGeom* geom, int64_t nstruct, const ImageDesc* images,
-                           const double* positions, int64_t ext_total, const int64_t* cell_start,
-                           int32_t* cell_fill, uint32_t* keys) {
+                           const double* positions, const int32_t* types, int species_major, int64_t ext_total,
+                           const int64_t* cell_start, int32_t* cell_fill, uint64_t* keys) {
     for (int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; e < ext_total;
          e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
         int64_t key, atom, image;
@@ -213,17 +213,18 @@ __global__ void k_bin_fill(const StructGeom* geom, int64_t nstruct, const ImageD
         const int64_t c = roi_cell(g, x, y, z, inside);
         if (inside) {
             const int32_t slot = atomicAdd(&cell_fill[c], 1);
-            keys[cell_start[c] + slot] = static_cast<uint32_t>(key);
+            const uint64_t major = species_major ? static_cast<uint64_t>(types[atom]) << 32 : 0;
+            keys[cell_start[c] + slot] = major | static_cast<uint64_t>(static_cast<uint32_t>(key));
         }
     }
 }
 
 // Order each cell by extended index (the reference fills cells in extended
-// order, neighbor.cpp:184-192) by ranking, then materialise the binned
-// images as SoA.  Keys are unique inside a cell.
+// order, neighbor.cpp:184-192) -- species first in Bins mode -- by ranking,
+// then materialise the binned images as SoA.  Keys are unique inside a cell.
 __global__ void k_bin_sort(const StructGeom* geom, int64_t nstruct, const ImageDesc* images,
                            const double* positions, const int32_t* types, const int64_t* cell_start,
-                           int64_t cells_total, const uint32_t* keys, double* bx, double* by, double* bz,
+                           int64_t cells_total, const uint64_t* keys, double* bx, double* by, double* bz,
                            int32_t* batom, int32_t* bimage, int32_t* btype) {
     for (int64_t c = blockIdx.x; c < cells_total; c += gridDim.x) {
         const int64_t start = cell_start[c];
@@ -233,10 +234,11 @@ __global__ void k_bin_sort(const StructGeom* geom, int64_t nstruct, const ImageD
         while (s + 1 < nstruct && geom[s + 1].cell_begin <= c) ++s;
         const StructGeom& g = geom[s];
         for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
-            const uint32_t key = keys[start + i];
+            const uint64_t full = keys[start + i];
             int64_t rank = 0;
-            for (int64_t j = 0; j < n; ++j) rank += keys[start + j] < key ? 1 : 0;
+            for (int64_t j = 0; j < n; ++j) rank += keys[start + j] < full ? 1 : 0;
             const int64_t dest = start + rank;
+            const int64_t key = static_cast<int64_t>(static_cast<uint32_t>(full));
             double x, y, z;
             int64_t atom, image;
             image_position(g, images, positions, key, x, y, z, atom, image);
@@ -250,13 +252,15 @@ __global__ void k_bin_sort(const StructGeom* geom, int64_t nstruct, const ImageD
     }
 }
 
+// Home ROI cell and structure of every atom (the centres).
 __global__ void k_centre_cell(const StructGeom* geom, int64_t nstruct, const double* positions, int64_t atoms,
-                              int64_t* centre_cell, int32_t* cell_centre_count, int32_t* error_flag) {
+                              int64_t* centre_cell, int32_t* centre_struct, int32_t* error_flag) {
     for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < atoms;
          i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
         int64_t s = find_by_begin(geom, nstruct, i, 2);
         while (s + 1 < nstruct && geom[s + 1].atom_begin <= i) ++s;
         const StructGeom& g = geom[s];
+        centre_struct[i] = static_cast<int32_t>(s);
         bool inside;
         const int64_t c = roi_cell(g, positions[i * 3 + 0], positions[i * 3 + 1], positions[i * 3 + 2], inside);
         if (!inside) {
@@ -266,165 +270,128 @@ __global__ void k_centre_cell(const StructGeom* geom, int64_t nstruct, const dou
             continue;
         }
         centre_cell[i] = c;
-        atomicAdd(&cell_centre_count[c], 1);
     }
 }
 
-__global__ void k_centre_fill(const int64_t* centre_cell, int64_t atoms, const int64_t* cell_centre_start,
-                              int32_t* cell_centre_fill, int32_t* cell_centre_list) {
-    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < atoms;
-         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        const int64_t c = centre_cell[i];
-        if (c < 0) continue;
-        const int32_t slot = atomicAdd(&cell_centre_fill[c], 1);
-        cell_centre_list[cell_centre_start[c] + slot] = static_cast<int32_t>(i);
+// First bin of each species in each cell (Bins mode: cells are sorted by
+// species); species t of cell c spans [start[c*S + t], start[c*S + t + 1])
+// with the cell's end after the last species.
+__global__ void k_cell_species(const int64_t* cell_start, int64_t cells_total, const int32_t* btype, int S,
+                               int64_t* cell_species_start) {
+    for (int64_t c = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; c < cells_total;
+         c += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t begin = cell_start[c], end = cell_start[c + 1];
+        int64_t i = begin;
+        for (int t = 0; t < S; ++t) {
+            while (i < end && btype[i] < t) ++i;
+            cell_species_start[c * S + t] = i;
+        }
     }
 }
 
-// One workgroup per home cell: stage the 27 neighbour cells' candidates in
-// LDS (visit order, chunks of kChunk), then each wave tests its centres
-// against them, 64 candidates per step.  Count pass: per-species counts.
-// Fill pass: wave ballot + popcount compaction into species-grouped rows.
+
+// Kernel 1: the neighbour rows of each centre, one wavefront per centre.
+// The 27 cells around the centre's home cell are visited in the reference's
+// order (z outer, y, x inner, cells outside the grid skipped;
+// neighbor.cpp:558-566) and the binned images of a cell in extended order.
+// With several species the bins of a cell are sorted by species first and the
+// walk is repeated per species, so a centre's rows come out grouped by species
+// and, inside a species, in the reference's candidate order; with one species
+// they are exactly the reference's rows.  Count pass: per-species counts and
+// row totals.  Fill pass: the same walk writes the bin index of every accepted
+// image at pair_start[centre] onwards (wave ballot + popcount compaction).
+// A block holds four independent waves with a few hundred bytes of LDS each,
+// so many centres are in flight per SIMD to hide the gather latency.
 template <bool kFill>
-__global__ __launch_bounds__(kBlock) void k_pair_pass(
-    const StructGeom* geom, int64_t nstruct, const double* positions, const int64_t* cell_start,
-    const int64_t* cell_centre_start, const int32_t* cell_centre_list, int64_t cells_total,
-    const double* bx, const double* by, const double* bz, const int32_t* btype, int S, double cutoff2,
-    int include_boundary, int32_t* counts, const int64_t* pair_start, int64_t* cursor, uint32_t* pair_bin) {
-    __shared__ double sx[kChunk], sy[kChunk], sz[kChunk];
-    __shared__ int32_t st[kChunk];
-    __shared__ uint32_t sb[kChunk];
-    __shared__ int64_t seg_start[27];
-    __shared__ int32_t seg_prefix[28];
-    __shared__ int32_t nseg;
+__global__ __launch_bounds__(kBlock) void k_neighbors(
+    const StructGeom* geom, const double* positions, int64_t atoms, const int64_t* centre_cell,
+    const int32_t* centre_struct, const int64_t* cell_start, const int64_t* cell_species_start, const double* bx,
+    const double* by, const double* bz, int S, double cutoff2, int include_boundary, int32_t* counts,
+    int32_t* totals, const int64_t* pair_start, uint32_t* pair_bin) {
+    constexpr int kWaves = kBlock / kWave;
+    __shared__ int64_t s_start[kWaves][27];
+    __shared__ int32_t s_pre[kWaves][28];
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
     const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-    for (int64_t c = blockIdx.x; c < cells_total; c += gridDim.x) {
-        const int64_t cs = cell_centre_start[c];
-        const int64_t ce = cell_centre_start[c + 1];
-        if (cs == ce) continue;
-        if (threadIdx.x == 0) {
-            int64_t s = find_by_begin(geom, nstruct, c, 1);
-            while (s + 1 < nstruct && geom[s + 1].cell_begin <= c) ++s;
-            const StructGeom& g = geom[s];
-            const int64_t local = c - g.cell_begin;
-            const int lx = static_cast<int>(local % g.roi_dim[0]);
-            const int ly = static_cast<int>((local / g.roi_dim[0]) % g.roi_dim[1]);
-            const int lz = static_cast<int>(local / (static_cast<int64_t>(g.roi_dim[0]) * g.roi_dim[1]));
-            const int ix = g.roi_lo[0] + lx, iy = g.roi_lo[1] + ly, iz = g.roi_lo[2] + lz;
-            int k = 0;
-            seg_prefix[0] = 0;
-            // visit order of neighbor.cpp:562-564: z outer, y, x inner, clamped to the grid
-            for (int z = max(0, iz - 1); z <= min(g.dims[2] - 1, iz + 1); ++z) {
-                for (int y = max(0, iy - 1); y <= min(g.dims[1] - 1, iy + 1); ++y) {
-                    for (int x = max(0, ix - 1); x <= min(g.dims[0] - 1, ix + 1); ++x) {
-                        const int64_t id = g.cell_begin + (x - g.roi_lo[0])
-                            + static_cast<int64_t>(g.roi_dim[0])
-                                * ((y - g.roi_lo[1]) + static_cast<int64_t>(g.roi_dim[1]) * (z - g.roi_lo[2]));
-                        seg_start[k] = cell_start[id];
-                        seg_prefix[k + 1] = seg_prefix[k] + static_cast<int32_t>(cell_start[id + 1] - cell_start[id]);
-                        ++k;
-                    }
-                }
+    for (int64_t centre = static_cast<int64_t>(blockIdx.x) * kWaves + wave; centre < atoms;
+         centre += static_cast<int64_t>(gridDim.x) * kWaves) {
+        const double px = positions[centre * 3 + 0];
+        const double py = positions[centre * 3 + 1];
+        const double pz = positions[centre * 3 + 2];
+        const int64_t home = centre_cell[centre];
+        int64_t cell = -1;
+        if (lane < 27 && home >= 0) {
+            const StructGeom& g = geom[centre_struct[centre]];
+            const int64_t local = home - g.cell_begin;
+            const int ix = g.roi_lo[0] + static_cast<int>(local % g.roi_dim[0]) + lane % 3 - 1;
+            const int iy = g.roi_lo[1] + static_cast<int>((local / g.roi_dim[0]) % g.roi_dim[1]) + (lane / 3) % 3 - 1;
+            const int iz = g.roi_lo[2] + static_cast<int>(local / (static_cast<int64_t>(g.roi_dim[0]) * g.roi_dim[1]))
+                + lane / 9 - 1;
+            if (ix >= 0 && iy >= 0 && iz >= 0 && ix < g.dims[0] && iy < g.dims[1] && iz < g.dims[2]) {
+                cell = g.cell_begin + (ix - g.roi_lo[0])
+                    + static_cast<int64_t>(g.roi_dim[0])
+                        * ((iy - g.roi_lo[1]) + static_cast<int64_t>(g.roi_dim[1]) * (iz - g.roi_lo[2]));
             }
-            nseg = k;
         }
-        __syncthreads();
-        const int total = seg_prefix[nseg];
-        __syncthreads();
-        for (int base = 0; base < total; base += kChunk) {
-            const int len = min(kChunk, total - base);
-            for (int i = threadIdx.x; i < len; i += kBlock) {
-                const int gi = base + i;
-                int k = 0;
-                while (seg_prefix[k + 1] <= gi) ++k;
-                const int64_t b = seg_start[k] + (gi - seg_prefix[k]);
-                sx[i] = bx[b];
-                sy[i] = by[b];
-                sz[i] = bz[b];
-                st[i] = btype[b];
-                sb[i] = static_cast<uint32_t>(b);
+        int64_t cursor = kFill ? pair_start[centre] : 0;
+        int32_t rows = 0;
+        for (int sp = 0; sp < S; ++sp) {
+            int64_t start = 0;
+            int32_t len = 0;
+            if (cell >= 0) {
+                start = S == 1 ? cell_start[cell] : cell_species_start[cell * S + sp];
+                const int64_t end = S == 1 || sp + 1 == S ? cell_start[cell + 1] : cell_species_start[cell * S + sp + 1];
+                len = static_cast<int32_t>(end - start);
             }
-            __syncthreads();
-            for (int64_t ci = cs + wave; ci < ce; ci += kBlock / kWave) {
-                const int32_t atom = cell_centre_list[ci];
-                const double px = positions[atom * 3 + 0];
-                const double py = positions[atom * 3 + 1];
-                const double pz = positions[atom * 3 + 2];
-                int64_t cur[kMaxSpecies];
-                int32_t cnt[kMaxSpecies];
+            int32_t incl = len;
 #pragma unroll
-                for (int t = 0; t < kMaxSpecies; ++t) {
-                    cnt[t] = 0;
-                    cur[t] = 0;
-                }
-                if (kFill) {
-                    if (base == 0) {
-                        int64_t run = pair_start[atom];
-#pragma unroll
-                        for (int t = 0; t < kMaxSpecies; ++t) {
-                            if (t < S) {
-                                cur[t] = run;
-                                run += counts[static_cast<int64_t>(atom) * S + t];
-                            }
-                        }
-                    } else {
-#pragma unroll
-                        for (int t = 0; t < kMaxSpecies; ++t) {
-                            if (t < S) cur[t] = cursor[static_cast<int64_t>(atom) * S + t];
-                        }
-                    }
-                }
-                for (int j0 = 0; j0 < len; j0 += kWave) {
-                    const int j = j0 + lane;
-                    bool accept = false;
-                    int type = 0;
-                    if (j < len) {
-                        // displacement = image - centre; d^2 = (dx*dx + dy*dy) + dz*dz
-                        // (neighbor.cpp:569, math3.hpp:31-35), no contraction
-                        const double dx = sx[j] - px;
-                        const double dy = sy[j] - py;
-                        const double dz = sz[j] - pz;
-                        const double d2 = dx * dx + dy * dy + dz * dz;
-                        accept = include_boundary ? d2 <= cutoff2 : d2 < cutoff2;
-                        type = st[j];
-                    }
-#pragma unroll
-                    for (int t = 0; t < kMaxSpecies; ++t) {
-                        if (t < S) {
-                            const bool mine = accept && type == t;
-                            const uint64_t mask = __ballot(mine);
-                            if (kFill) {
-                                if (mine) pair_bin[cur[t] + __popcll(mask & below)] = sb[j];
-                                cur[t] += __popcll(mask);
-                            } else {
-                                cnt[t] += __popcll(mask);
-                            }
-                        }
-                    }
-                }
-                if (lane == 0) {
-#pragma unroll
-                    for (int t = 0; t < kMaxSpecies; ++t) {
-                        if (t < S) {
-                            if (kFill) cursor[static_cast<int64_t>(atom) * S + t] = cur[t];
-                            else counts[static_cast<int64_t>(atom) * S + t] += cnt[t];
-                        }
-                    }
-                }
+            for (int off = 1; off < 32; off *= 2) {
+                const int32_t v = __shfl_up(incl, off, 32);
+                if ((lane & 31) >= off) incl += v;
             }
-            __syncthreads();
+            const int32_t total = __shfl(incl, 26);
+            if (lane < 27) {
+                s_start[wave][lane] = start;
+                s_pre[wave][lane + 1] = incl;
+            }
+            if (lane == 0) s_pre[wave][0] = 0;
+            // hand-off inside one wavefront: its LDS operations complete in order
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            int32_t found = 0;
+            for (int32_t v0 = 0; v0 < total; v0 += kWave) {
+                const int32_t v = v0 + lane;
+                bool accept = false;
+                uint32_t b = 0;
+                if (v < total) {
+                    int lo = 0;
+#pragma unroll
+                    for (int step = 16; step > 0; step /= 2) {
+                        if (lo + step < 27 && s_pre[wave][lo + step] <= v) lo += step;
+                    }
+                    b = static_cast<uint32_t>(s_start[wave][lo] + (v - s_pre[wave][lo]));
+                    // displacement = image - centre; d^2 = (dx*dx + dy*dy) + dz*dz
+                    // (neighbor.cpp:569, math3.hpp:31-35), no contraction
+                    const double dx = bx[b] - px;
+                    const double dy = by[b] - py;
+                    const double dz = bz[b] - pz;
+                    const double d2 = dx * dx + dy * dy + dz * dz;
+                    accept = include_boundary ? d2 <= cutoff2 : d2 < cutoff2;
+                }
+                const uint64_t mask = __ballot(accept);
+                if (kFill && accept) pair_bin[cursor + found + __popcll(mask & below)] = b;
+                found += static_cast<int32_t>(__popcll(mask));
+            }
+            if (!kFill && lane == 0) counts[centre * S + sp] = found;
+            cursor += found;
+            rows += found;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
-    }
-}
-
-__global__ void k_totals(const int32_t* counts, int S, int64_t atoms, int32_t* totals) {
-    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < atoms;
-         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        int32_t sum = 0;
-        for (int t = 0; t < S; ++t) sum += counts[i * S + t];
-        totals[i] = sum;
+        if (!kFill && lane == 0) totals[centre] = rows;
     }
 }
 
@@ -702,16 +669,19 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     const ImageDesc* images = pb.d_images.as<ImageDesc>();
     const double* pos = pb.d_positions.as<double>();
     const int64_t ext = pb.ext_total;
+    if (ext >= (int64_t(1) << 31)) {
+        // a centre's candidates are counted in 32-bit integers
+        throw Error(MDX_INVALID_ARGUMENT, "periodic images exceed the device graph capacity");
+    }
 
     gr.cell_count.reserve(cells1 * sizeof(int32_t));
     gr.cell_fill.reserve(cells1 * sizeof(int32_t));
     gr.cell_start.reserve(cells1 * sizeof(int64_t));
-    gr.cell_centre_count.reserve(cells1 * sizeof(int32_t));
-    gr.cell_centre_fill.reserve(cells1 * sizeof(int32_t));
-    gr.cell_centre_start.reserve(cells1 * sizeof(int64_t));
-    gr.cell_centre_list.reserve(static_cast<size_t>(atoms) * sizeof(int32_t));
+    gr.cell_species_start.reserve(std::max<size_t>(1, static_cast<size_t>(cells) * static_cast<size_t>(S)) *
+                                  sizeof(int64_t));
     gr.centre_cell.reserve(static_cast<size_t>(atoms) * sizeof(int64_t));
-    gr.bin_key.reserve(static_cast<size_t>(ext) * sizeof(uint32_t));
+    gr.centre_struct.reserve(static_cast<size_t>(atoms) * sizeof(int32_t));
+    gr.bin_key.reserve(static_cast<size_t>(ext) * sizeof(uint64_t));
     gr.bin_x.reserve(static_cast<size_t>(ext) * sizeof(double));
     gr.bin_y.reserve(static_cast<size_t>(ext) * sizeof(double));
     gr.bin_z.reserve(static_cast<size_t>(ext) * sizeof(double));
@@ -719,44 +689,40 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     gr.bin_image.reserve(static_cast<size_t>(ext) * sizeof(int32_t));
     gr.bin_type.reserve(static_cast<size_t>(ext) * sizeof(int32_t));
     gr.counts.reserve(static_cast<size_t>(atoms * S) * sizeof(int32_t));
-    gr.cursor.reserve(static_cast<size_t>(atoms * S) * sizeof(int64_t));
     gr.totals.reserve(static_cast<size_t>(atoms) * sizeof(int32_t));
     gr.error_flag.reserve(sizeof(int32_t));
     MDX_HIP(hipMemsetAsync(gr.error_flag.ptr, 0, sizeof(int32_t), stream));
-
     MDX_HIP(hipMemsetAsync(gr.cell_count.ptr, 0, cells1 * sizeof(int32_t), stream));
     MDX_HIP(hipMemsetAsync(gr.cell_fill.ptr, 0, cells1 * sizeof(int32_t), stream));
-    MDX_HIP(hipMemsetAsync(gr.cell_centre_count.ptr, 0, cells1 * sizeof(int32_t), stream));
-    MDX_HIP(hipMemsetAsync(gr.cell_centre_fill.ptr, 0, cells1 * sizeof(int32_t), stream));
-    MDX_HIP(hipMemsetAsync(gr.counts.ptr, 0, static_cast<size_t>(atoms * S) * sizeof(int32_t), stream));
 
+    // bin every periodic image into its ROI cell, sorted by (species, extended index)
     hipLaunchKernelGGL(k_bin_count, dim3(grid_for(ext)), dim3(kBlock), 0, stream, geom, nstruct, images, pos, ext,
                        gr.cell_count.as<int32_t>());
     scan_counts(stream, gr.cell_count.as<int32_t>(), gr.cell_start.as<int64_t>(), cells, gr.scan_tmp);
-    hipLaunchKernelGGL(k_bin_fill, dim3(grid_for(ext)), dim3(kBlock), 0, stream, geom, nstruct, images, pos, ext,
-                       gr.cell_start.as<int64_t>(), gr.cell_fill.as<int32_t>(), gr.bin_key.as<uint32_t>());
+    hipLaunchKernelGGL(k_bin_fill, dim3(grid_for(ext)), dim3(kBlock), 0, stream, geom, nstruct, images, pos,
+                       pb.d_types.as<int32_t>(), S > 1 ? 1 : 0, ext, gr.cell_start.as<int64_t>(),
+                       gr.cell_fill.as<int32_t>(), gr.bin_key.as<uint64_t>());
     const unsigned cell_grid = static_cast<unsigned>(std::min<int64_t>(cells, 1 << 20));
     hipLaunchKernelGGL(k_bin_sort, dim3(cell_grid), dim3(kBlock), 0, stream, geom, nstruct, images, pos,
-                       pb.d_types.as<int32_t>(), gr.cell_start.as<int64_t>(), cells, gr.bin_key.as<uint32_t>(),
+                       pb.d_types.as<int32_t>(), gr.cell_start.as<int64_t>(), cells, gr.bin_key.as<uint64_t>(),
                        gr.bin_x.as<double>(), gr.bin_y.as<double>(), gr.bin_z.as<double>(), gr.bin_atom.as<int32_t>(),
                        gr.bin_image.as<int32_t>(), gr.bin_type.as<int32_t>());
+    if (S > 1) {
+        hipLaunchKernelGGL(k_cell_species, dim3(grid_for(cells)), dim3(kBlock), 0, stream, gr.cell_start.as<int64_t>(),
+                           cells, gr.bin_type.as<int32_t>(), S, gr.cell_species_start.as<int64_t>());
+    }
     hipLaunchKernelGGL(k_centre_cell, dim3(grid_for(atoms)), dim3(kBlock), 0, stream, geom, nstruct, pos, atoms,
-                       gr.centre_cell.as<int64_t>(), gr.cell_centre_count.as<int32_t>(), gr.error_flag.as<int32_t>());
-    scan_counts(stream, gr.cell_centre_count.as<int32_t>(), gr.cell_centre_start.as<int64_t>(), cells, gr.scan_tmp);
-    hipLaunchKernelGGL(k_centre_fill, dim3(grid_for(atoms)), dim3(kBlock), 0, stream, gr.centre_cell.as<int64_t>(),
-                       atoms, gr.cell_centre_start.as<int64_t>(), gr.cell_centre_fill.as<int32_t>(),
-                       gr.cell_centre_list.as<int32_t>());
+                       gr.centre_cell.as<int64_t>(), gr.centre_struct.as<int32_t>(), gr.error_flag.as<int32_t>());
     MDX_HIP(hipGetLastError());
     if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
 
     const double cutoff2 = pb.cutoff * pb.cutoff;
-    hipLaunchKernelGGL(k_pair_pass<false>, dim3(cell_grid), dim3(kBlock), 0, stream, geom, nstruct, pos,
-                       gr.cell_start.as<int64_t>(), gr.cell_centre_start.as<int64_t>(), gr.cell_centre_list.as<int32_t>(),
-                       cells, gr.bin_x.as<double>(), gr.bin_y.as<double>(), gr.bin_z.as<double>(),
-                       gr.bin_type.as<int32_t>(), S, cutoff2, pb.include_boundary, gr.counts.as<int32_t>(), nullptr, nullptr,
-                       nullptr);
-    hipLaunchKernelGGL(k_totals, dim3(grid_for(atoms)), dim3(kBlock), 0, stream, gr.counts.as<int32_t>(), S, atoms,
-                       gr.totals.as<int32_t>());
+    const unsigned centre_grid = static_cast<unsigned>(std::min<int64_t>((atoms + 3) / 4, 1 << 20));
+    hipLaunchKernelGGL(k_neighbors<false>, dim3(centre_grid), dim3(kBlock), 0, stream, geom, pos, atoms,
+                       gr.centre_cell.as<int64_t>(), gr.centre_struct.as<int32_t>(), gr.cell_start.as<int64_t>(),
+                       gr.cell_species_start.as<int64_t>(), gr.bin_x.as<double>(), gr.bin_y.as<double>(),
+                       gr.bin_z.as<double>(), S, cutoff2, pb.include_boundary, gr.counts.as<int32_t>(),
+                       gr.totals.as<int32_t>(), static_cast<const int64_t*>(nullptr), static_cast<uint32_t*>(nullptr));
     scan_counts(stream, gr.totals.as<int32_t>(), gr.pair_start.as<int64_t>(), atoms, gr.scan_tmp);
     MDX_HIP(hipGetLastError());
     int64_t pairs = 0;
@@ -772,11 +738,11 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
     if (pairs >= (int64_t(1) << 40)) throw Error(MDX_INTERNAL, "implausible neighbour pair count");
     gr.pair_bin.reserve(std::max<size_t>(1, static_cast<size_t>(pairs) * sizeof(uint32_t)));
-    hipLaunchKernelGGL(k_pair_pass<true>, dim3(cell_grid), dim3(kBlock), 0, stream, geom, nstruct, pos,
-                       gr.cell_start.as<int64_t>(), gr.cell_centre_start.as<int64_t>(), gr.cell_centre_list.as<int32_t>(),
-                       cells, gr.bin_x.as<double>(), gr.bin_y.as<double>(), gr.bin_z.as<double>(),
-                       gr.bin_type.as<int32_t>(), S, cutoff2, pb.include_boundary, gr.counts.as<int32_t>(), gr.pair_start.as<int64_t>(),
-                       gr.cursor.as<int64_t>(), gr.pair_bin.as<uint32_t>());
+    hipLaunchKernelGGL(k_neighbors<true>, dim3(centre_grid), dim3(kBlock), 0, stream, geom, pos, atoms,
+                       gr.centre_cell.as<int64_t>(), gr.centre_struct.as<int32_t>(), gr.cell_start.as<int64_t>(),
+                       gr.cell_species_start.as<int64_t>(), gr.bin_x.as<double>(), gr.bin_y.as<double>(),
+                       gr.bin_z.as<double>(), S, cutoff2, pb.include_boundary, static_cast<int32_t*>(nullptr),
+                       static_cast<int32_t*>(nullptr), gr.pair_start.as<int64_t>(), gr.pair_bin.as<uint32_t>());
     MDX_HIP(hipGetLastError());
     gr.pairs = pairs;
     gr.binned = binned;

@@ -105,17 +105,17 @@ struct DeviceGraph {
     int64_t pairs = 0;
     int n_species = 1;
     DeviceBuffer cell_count, cell_start, cell_fill; // per ROI cell
-    DeviceBuffer bin_key;                           // unsorted keys, then scratch
+    DeviceBuffer bin_key;                           // unsorted u64 keys, (species << 32) | extended index
+    DeviceBuffer cell_species_start;                // i64[cells * n_species]: first bin of each species in a cell
+    DeviceBuffer centre_struct;                     // i32 structure of each atom
     DeviceBuffer bin_x, bin_y, bin_z;               // f64 positions of binned images (sorted)
     DeviceBuffer bin_atom;                          // i32 global atom index
     DeviceBuffer bin_image;                         // i32 global image index
     DeviceBuffer bin_type;                          // i32 species index
-    DeviceBuffer centre_cell;                       // i64 per atom
-    DeviceBuffer cell_centre_count, cell_centre_start, cell_centre_fill, cell_centre_list;
+    DeviceBuffer centre_cell;                       // i64 home ROI cell per atom
     DeviceBuffer counts;     // i32[atoms * n_species]
     DeviceBuffer totals;     // i32[atoms]
     DeviceBuffer pair_start; // i64[atoms + 1]
-    DeviceBuffer cursor;     // i64[atoms * n_species]
     DeviceBuffer pair_bin;   // u32[pairs]
     DeviceBuffer scan_tmp;   // block sums of the scans
     DeviceBuffer error_flag; // i32, set by a kernel on an internal inconsistency

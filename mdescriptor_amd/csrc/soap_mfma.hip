@@ -150,17 +150,39 @@ __device__ inline void store_out(void* out, int64_t pitch, int64_t row, int64_t 
     }
 }
 
+// Feature index of channel pair (i, j), i <= j, at l = 0, and its stride
+// per degree l, in the layout of soap.cpp:997-1013: species pairs t1 <= t2 in
+// order, each a block of L x (n(n+1)/2) (t1 == t2, n2 >= n1) or L x n^2
+// values ordered l, n1, n2.  Channel i is species i / n, radial i % n.
+__device__ inline int feature_index(int i, int j, int S, int n, int L, int& stride) {
+    const int t1 = i / n, n1 = i - t1 * n;
+    const int t2 = j / n, n2 = j - t2 * n;
+    const int same = n * (n + 1) / 2, cross = n * n;
+    // blocks of the species rows a < t1, then (t1, t1 .. t2-1)
+    int before = t1 * same + cross * (t1 * (S - 1) - t1 * (t1 - 1) / 2);
+    if (t2 > t1) before += same + (t2 - t1 - 1) * cross;
+    int inner;
+    if (t1 == t2) {
+        inner = n1 * n - n1 * (n1 - 1) / 2 + (n2 - n1);
+        stride = same;
+    } else {
+        inner = n1 * n + n2;
+        stride = cross;
+    }
+    return L * before + inner;
+}
+
 // Power spectrum of the coefficients in LDS on 16x16 Gram tiles.  s_c holds
 // W + 1 rows of d.hpad values (row W and every pad entry are zero), entry
 // (row, l, m') at row*hpad + loff[l] + m'.  mode 0: write row `row` of out;
 // mode 2: add into the partial row `acc`.
-__device__ void power_spectrum_tiles(const double* s_c, const int* loff, const MfmaDims& d, const int32_t* fbase,
-                                     const int32_t* fstride, const double* ps_pref, int mode, void* out,
-                                     int64_t pitch, int64_t row, double* acc) {
+__device__ void power_spectrum_tiles(const double* s_c, const int* loff, const MfmaDims& d, const double* ps_pref,
+                                     int mode, void* out, int64_t pitch, int64_t row, double* acc) {
     const int lane = threadIdx.x;
     const int W = d.S * d.n;
     const int RT = (W + 15) / 16;
     const int hp = d.hpad;
+    char* out_row = static_cast<char*>(out) + row * pitch;
     for (int bi = 0; bi < RT; ++bi) {
         for (int bj = bi; bj < RT; ++bj) {
             const int ia = min(16 * bi + lane % 16, W);
@@ -168,15 +190,13 @@ __device__ void power_spectrum_tiles(const double* s_c, const int* loff, const M
             const double* arow = s_c + ia * hp + lane / 16;
             const double* brow = s_c + jb * hp + lane / 16;
             const int j = 16 * bj + lane % 16;
-            int64_t fb[4];
-            int fs[4];
-            bool ok[4];
+            int fb[4], fs[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int i = 16 * bi + lane / 16 + 4 * r;
-                ok[r] = i < W && j < W && i <= j;
-                fb[r] = ok[r] ? fbase[i * W + j] : 0;
-                fs[r] = ok[r] ? fstride[i * W + j] : 0;
+                const bool ok = i < W && j < W && i <= j;
+                fs[r] = 0;
+                fb[r] = ok ? feature_index(i, j, d.S, d.n, d.L, fs[r]) : -1;
             }
             for (int l = 0; l <= d.l_max; ++l) {
                 const int steps = (2 * l + 4) / 4;
@@ -186,13 +206,15 @@ __device__ void power_spectrum_tiles(const double* s_c, const int* loff, const M
                 const double pref = ps_pref[l];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    if (ok[r]) {
-                        const int64_t f = fb[r] + static_cast<int64_t>(l) * fs[r];
+                    if (fb[r] >= 0) {
+                        const int f = fb[r] + l * fs[r];
                         const double v = pref * acc4[r];
-                        if (mode == 0) {
-                            store_out(out, pitch, row, f, v, d.out_dtype);
-                        } else {
+                        if (mode != 0) {
                             acc[f] += v;
+                        } else if (d.out_dtype == 4) {
+                            reinterpret_cast<float*>(out_row)[f] = static_cast<float>(v);
+                        } else {
+                            reinterpret_cast<double*>(out_row)[f] = v;
                         }
                     }
                 }
@@ -206,7 +228,7 @@ __global__ __launch_bounds__(kWaveThreads) void k_soap_mfma(
     const double* __restrict__ positions, const int64_t* __restrict__ pair_start, const int32_t* __restrict__ counts,
     const uint32_t* __restrict__ pair_bin, const double* __restrict__ bx, const double* __restrict__ by,
     const double* __restrict__ bz, const MfmaTables tab, MfmaDims d, const int64_t* __restrict__ item_begin,
-    int64_t item_base, int64_t items, void* out, int64_t pitch, double* partial) {
+    int64_t item_base, int64_t items, int64_t per_block, void* out, int64_t pitch, double* partial) {
     extern __shared__ double lds[];
     const int lane = threadIdx.x;
     const int H = d.H, L = d.L, S = d.S, n = d.n;
@@ -221,6 +243,7 @@ __global__ __launch_bounds__(kWaveThreads) void k_soap_mfma(
     double* s_c = s_tab + 64;             // cw (coefficients of the current centre, padded)
     double* s_csum = s_c + cw;            // cw (inner average only)
     int* s_loff = reinterpret_cast<int*>(s_csum + (d.mode == 1 ? cw : 0)); // L + 1
+    int* s_seg = s_loff + (L + 1);        // S + 1: first row of each species segment of the centre
 
     for (int i = lane; i < L * L; i += kWaveThreads) s_norm[i] = tab.hnorm[i];
     s_tab[lane] = exp2(static_cast<double>(lane) / 64.0);
@@ -260,8 +283,17 @@ __global__ __launch_bounds__(kWaveThreads) void k_soap_mfma(
             dst[t][r] = diag ? (och % n) * hp + s_loff[lh] + (ch - lh * lh) : -1;
         }
     }
+    // A operands of the beta fold, the same for every species and centre
+    double bfold[T][4];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) bfold[t][r] = tab.beta_lane[(t * 4 + r) * kWaveThreads + lane];
+    }
 
-    for (int64_t item = item_base + blockIdx.x; item < item_base + items; item += gridDim.x) {
+    const int64_t item_first = item_base + static_cast<int64_t>(blockIdx.x) * per_block;
+    const int64_t item_last = min(item_first + per_block, item_base + items);
+    for (int64_t item = item_first; item < item_last; ++item) {
         const int64_t first = item_begin ? item_begin[item] : item;
         const int64_t last = item_begin ? item_begin[item + 1] : item + 1;
         double* part_row = partial != nullptr ? partial + item * (d.mode == 1 ? static_cast<int64_t>(cw) : d.F) : nullptr;
@@ -275,29 +307,42 @@ __global__ __launch_bounds__(kWaveThreads) void k_soap_mfma(
             const double cy = positions[centre * 3 + 1];
             const double cz = positions[centre * 3 + 2];
             const int64_t centre_pairs = pair_start[centre];
-            // prefetch: lane (jj = lane/4) holds the image position of neighbour jj of the next chunk
+            // species segments of this centre's rows (kernel 1 groups them by species)
+            if (lane == 0) {
+                int rows = 0;
+                for (int q = 0; q < S; ++q) {
+                    s_seg[q] = rows;
+                    rows += counts[centre * S + q];
+                }
+                s_seg[S] = rows;
+            }
+            wave_sync();
+            // prefetch: lane (jj = lane/4) holds the image position of neighbour jj of the next chunk;
+            // the first chunk starts at the centre's first row whatever its species
             double px = 0.0, py = 0.0, pz = 0.0;
             {
-                // the first chunk belongs to the first species with neighbours; empty
-                // species own no rows, so it starts at the centre's first row
-                int64_t k0 = 0;
-                for (int q = 0; q < S && k0 == 0; ++q) k0 = counts[centre * S + q];
                 const int jj = lane / 4;
-                if (jj < min<int64_t>(kNb, k0)) {
+                if (jj < min(kNb, s_seg[S])) {
                     const uint32_t b = pair_bin[centre_pairs + jj];
                     px = bx[b];
                     py = by[b];
                     pz = bz[b];
                 }
             }
-            int64_t seg = centre_pairs;
             for (int sp = 0; sp < S; ++sp) {
-                const int64_t kt = counts[centre * S + sp];
+                const int seg0 = s_seg[sp];
+                const int kt = s_seg[sp + 1] - seg0;
+                if (kt == 0) {
+                    // an empty species leaves its coefficients at zero
+                    double* cdst = s_c + sp * n * hp;
+                    for (int i = lane; i < n * hp; i += kWaveThreads) cdst[i] = 0.0;
+                    continue;
+                }
                 d4 acc[T];
 #pragma unroll
                 for (int t = 0; t < T; ++t) acc[t] = d4{0.0, 0.0, 0.0, 0.0};
-                for (int64_t j0 = 0; j0 < kt; j0 += kNb) {
-                    const int cnt = static_cast<int>(min<int64_t>(kNb, kt - j0));
+                for (int j0 = 0; j0 < kt; j0 += kNb) {
+                    const int cnt = min(kNb, kt - j0);
                     wave_sync();
                     {
                         // four lanes per neighbour: geometry and m-columns of the harmonics;
@@ -319,16 +364,24 @@ __global__ __launch_bounds__(kWaveThreads) void k_soap_mfma(
                     }
                     wave_sync();
                     {
-                        // issue the loads of the next chunk (this species or the next) now
-                        int64_t next = seg + j0 + kNb;
-                        int64_t avail = kt - j0 - kNb;
-                        for (int q = sp + 1; avail <= 0 && q < S; ++q) {
-                            next = seg + kt;
-                            avail = counts[centre * S + q];
+                        // issue the loads of the next chunk now: rows are contiguous across
+                        // species, so the next chunk starts right after this one, but a chunk
+                        // never runs past its species' end
+                        const int next = seg0 + j0 + kNb < s_seg[sp + 1] ? seg0 + j0 + kNb : s_seg[sp + 1];
+                        int end = s_seg[sp + 1];
+                        if (next == end) {
+                            // first non-empty species after this one (empty ones own no rows)
+                            for (int q = sp + 1; q < S; ++q) {
+                                if (s_seg[q + 1] > next) {
+                                    end = s_seg[q + 1];
+                                    break;
+                                }
+                            }
                         }
+                        const int avail = end - next;
                         const int jj = lane / 4;
-                        if (avail > 0 && jj < min<int64_t>(kNb, avail)) {
-                            const uint32_t b = pair_bin[next + jj];
+                        if (avail > 0 && jj < min(kNb, avail)) {
+                            const uint32_t b = pair_bin[centre_pairs + next + jj];
                             px = bx[b];
                             py = by[b];
                             pz = bz[b];
@@ -352,25 +405,20 @@ __global__ __launch_bounds__(kWaveThreads) void k_soap_mfma(
                 for (int t = 0; t < T; ++t) {
                     d4 c = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const double bb = tab.beta_lane[(t * 4 + r) * kWaveThreads + lane];
-                        c = mfma(bb, acc[t][r], c);
-                    }
+                    for (int r = 0; r < 4; ++r) c = mfma(bfold[t][r], acc[t][r], c);
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         if (dst[t][r] >= 0) cdst[dst[t][r]] = c[r];
                     }
                 }
-                seg += kt;
             }
             wave_sync();
             if (d.mode == 0) {
-                power_spectrum_tiles(s_c, s_loff, d, tab.fbase, tab.fstride, tab.ps_pref, 0, out, pitch, centre, nullptr);
+                power_spectrum_tiles(s_c, s_loff, d, tab.ps_pref, 0, out, pitch, centre, nullptr);
             } else if (d.mode == 1) {
                 for (int i = lane; i < cw; i += kWaveThreads) s_csum[i] += s_c[i];
             } else {
-                power_spectrum_tiles(s_c, s_loff, d, tab.fbase, tab.fstride, tab.ps_pref, 2, out, pitch, centre,
-                                     part_row);
+                power_spectrum_tiles(s_c, s_loff, d, tab.ps_pref, 2, out, pitch, centre, part_row);
             }
             wave_sync();
         }
@@ -408,7 +456,7 @@ __global__ __launch_bounds__(kWaveThreads) void k_mfma_finalize_inner(const doub
             s_c[i] = natoms > 0 ? sum * inv : 0.0;
         }
         __syncthreads();
-        power_spectrum_tiles(s_c, s_loff, d, tab.fbase, tab.fstride, tab.ps_pref, 0, out, pitch, s, nullptr);
+        power_spectrum_tiles(s_c, s_loff, d, tab.ps_pref, 0, out, pitch, s, nullptr);
         __syncthreads();
     }
 }
@@ -428,12 +476,27 @@ __global__ void k_mfma_finalize_outer(const double* partial, const int64_t* stru
 }
 
 template <int T>
-void launch(hipStream_t stream, unsigned grid, size_t lds, const PreparedBatch& pb, const DeviceGraph& g,
-            const MfmaTables& tab, const MfmaDims& d, const int64_t* item_begin, int64_t base, int64_t count, void* out,
-            int64_t pitch, double* partial) {
+void launch(hipStream_t stream, unsigned grid, int64_t per_block, size_t lds, const PreparedBatch& pb,
+            const DeviceGraph& g, const MfmaTables& tab, const MfmaDims& d, const int64_t* item_begin, int64_t base,
+            int64_t count, void* out, int64_t pitch, double* partial) {
     hipLaunchKernelGGL((k_soap_mfma<T>), dim3(grid), dim3(kWaveThreads), lds, stream, pb.d_positions.as<double>(),
                        g.pair_start.as<int64_t>(), g.counts.as<int32_t>(), g.pair_bin.as<uint32_t>(), g.bin_x.as<double>(),
-                       g.bin_y.as<double>(), g.bin_z.as<double>(), tab, d, item_begin, base, count, out, pitch, partial);
+                       g.bin_y.as<double>(), g.bin_z.as<double>(), tab, d, item_begin, base, count, per_block, out, pitch,
+                       partial);
+}
+
+// Compute units of the current device (queried once per process and device).
+int device_compute_units() {
+    static int cached[64] = {};
+    int dev = 0;
+    MDX_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int cus = 0;
+        MDX_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        cached[dev] = cus > 0 ? cus : 256;
+    }
+    return cached[dev];
 }
 
 } // namespace
@@ -544,23 +607,31 @@ size_t mfma_lds_bytes(const MfmaDims& d) {
     const size_t cw = (W + 1) * static_cast<size_t>(d.hpad);
     size_t words = static_cast<size_t>(kNb) * (d.H + 1) + kNb + static_cast<size_t>(d.L) * d.L + 64 + cw;
     if (d.mode == 1) words += cw;
-    return words * sizeof(double) + static_cast<size_t>(d.L + 2) * sizeof(int);
+    return words * sizeof(double) + static_cast<size_t>(d.L + 1 + kMaxSpecies + 1) * sizeof(int);
 }
 
 void launch_mfma_expand(hipStream_t stream, int template_tiles, const PreparedBatch& pb, const DeviceGraph& g,
                         const MfmaTables& tab, const MfmaDims& d, const int64_t* item_begin, int64_t base,
                         int64_t count, void* out, int64_t pitch, double* partial) {
     const size_t lds = mfma_lds_bytes(d);
-    const unsigned grid = static_cast<unsigned>(count);
+    // persistent blocks: about two per wave slot the LDS footprint allows on
+    // every CU, each walking a contiguous range of items
+    const int64_t resident = std::max<int64_t>(1, std::min<int64_t>(32, (160 * 1024) / std::max<size_t>(lds, 1)));
+    // a few centres per block: enough to amortise the block's table set-up,
+    // few enough that the last blocks do not leave CUs idle
+    const int64_t target = std::max<int64_t>(1, 8 * resident * device_compute_units());
+    const int64_t per_block = std::max<int64_t>(1, (count + target - 1) / target);
+    const unsigned grid = static_cast<unsigned>((count + per_block - 1) / per_block);
+    if (count <= 0) return;
     switch (template_tiles) {
-    case 1: launch<1>(stream, grid, lds, pb, g, tab, d, item_begin, base, count, out, pitch, partial); break;
-    case 2: launch<2>(stream, grid, lds, pb, g, tab, d, item_begin, base, count, out, pitch, partial); break;
-    case 3: launch<3>(stream, grid, lds, pb, g, tab, d, item_begin, base, count, out, pitch, partial); break;
-    case 4: launch<4>(stream, grid, lds, pb, g, tab, d, item_begin, base, count, out, pitch, partial); break;
-    case 6: launch<6>(stream, grid, lds, pb, g, tab, d, item_begin, base, count, out, pitch, partial); break;
-    case 8: launch<8>(stream, grid, lds, pb, g, tab, d, item_begin, base, count, out, pitch, partial); break;
-    case 12: launch<12>(stream, grid, lds, pb, g, tab, d, item_begin, base, count, out, pitch, partial); break;
-    case 16: launch<16>(stream, grid, lds, pb, g, tab, d, item_begin, base, count, out, pitch, partial); break;
+    case 1: launch<1>(stream, grid, per_block, lds, pb, g, tab, d, item_begin, base, count, out, pitch, partial); break;
+    case 2: launch<2>(stream, grid, per_block, lds, pb, g, tab, d, item_begin, base, count, out, pitch, partial); break;
+    case 3: launch<3>(stream, grid, per_block, lds, pb, g, tab, d, item_begin, base, count, out, pitch, partial); break;
+    case 4: launch<4>(stream, grid, per_block, lds, pb, g, tab, d, item_begin, base, count, out, pitch, partial); break;
+    case 6: launch<6>(stream, grid, per_block, lds, pb, g, tab, d, item_begin, base, count, out, pitch, partial); break;
+    case 8: launch<8>(stream, grid, per_block, lds, pb, g, tab, d, item_begin, base, count, out, pitch, partial); break;
+    case 12: launch<12>(stream, grid, per_block, lds, pb, g, tab, d, item_begin, base, count, out, pitch, partial); break;
+    case 16: launch<16>(stream, grid, per_block, lds, pb, g, tab, d, item_begin, base, count, out, pitch, partial); break;
     default: throw Error(MDX_INTERNAL, "unsupported MFMA tile count");
     }
     MDX_HIP(hipGetLastError());
