@@ -64,3 +64,43 @@ def test_reference_harness_reproduces_goldens(reference, manifest):
                             sigma=p.get("sigma", 1.0), alphas=alphas, betas=betas, average=p["average"], kind="ref")
     np.testing.assert_allclose(values, expected["values"], rtol=meta["tolerance"]["rtol"],
                                atol=meta["tolerance"]["atol"])
+
+
+def _invalid_batches():
+    """Batches the reference's validate_batch (batch.hpp:19-80) and SOAP
+    options reject, each with the field it breaks."""
+
+    from types import SimpleNamespace
+
+    def batch(**overrides):
+        base = dict(numbers=np.array([1, 8], np.int32), positions=np.array([[0.0, 0.0, 0.0], [0.9, 0.1, 0.2]]),
+                    cells=np.eye(3)[None] * 6.0, pbc=np.ones((1, 3), np.int32), offsets=np.array([0, 2]))
+        base.update(overrides)
+        return SimpleNamespace(**base)
+
+    return {
+        "mixed_pbc": batch(pbc=np.array([[1, 0, 1]], np.int32)),
+        "pbc_value": batch(pbc=np.array([[2, 2, 2]], np.int32)),
+        "singular_cell": batch(cells=np.zeros((1, 3, 3))),
+        "nonfinite_cell": batch(cells=np.full((1, 3, 3), np.nan)),
+        "nonfinite_position": batch(positions=np.array([[0.0, 0.0, np.inf], [0.9, 0.1, 0.2]])),
+        "bad_number": batch(numbers=np.array([1, 0], np.int32)),
+        "offsets_end": batch(offsets=np.array([0, 1])),
+        "offsets_order": SimpleNamespace(numbers=np.array([1, 8, 1], np.int32), positions=np.zeros((3, 3)),
+                                         cells=np.zeros((2, 3, 3)), pbc=np.zeros((2, 3), np.int32),
+                                         offsets=np.array([0, 3, 2])),
+        "undeclared_species": batch(numbers=np.array([1, 6], np.int32)),
+    }
+
+
+@pytest.mark.parametrize("case", sorted(_invalid_batches()))
+def test_oracle_rejects_what_the_reference_rejects(reference, case):
+    batch = _invalid_batches()[case]
+    alphas, betas = basis_gto(4.0, 2, 2)
+    kwargs = dict(species=[1, 8], n_max=2, l_max=2, r_cut=4.0, sigma=1.0, alphas=alphas, betas=betas,
+                  average="off")
+    with pytest.raises(ValueError) as ours:
+        reference.soap(batch, **kwargs)
+    with pytest.raises(ValueError) as theirs:
+        reference.soap(batch, kind="ref", **kwargs)
+    assert str(ours.value) == str(theirs.value)
