@@ -14,6 +14,9 @@ struct MfmaDims {
     int hpad;      // padded harmonic row: each l block rounded up to a multiple of 4
     int clamp;     // 1 when some radial exponent argument can fall below -700
     int64_t F;
+    // harmonic m-columns computed by each wavefront of a workgroup (bit m of
+    // harm_mask[w]), balanced by recurrence length
+    uint32_t harm_mask[16];
 };
 
 // Device tables built once per plan.
@@ -31,6 +34,7 @@ struct MfmaTables {
     const double* pref;
     const double* expo;
     const double* hnorm;
+    const double* hcoef;  // normalised harmonic recurrence (kHc* layout)
     const double* ps_pref;
     const int32_t* fbase;
     const int32_t* fstride;

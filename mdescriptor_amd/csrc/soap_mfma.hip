@@ -1,16 +1,18 @@
 // Kernels 2-4 on the FP64 matrix cores of gfx950 (v_mfma_f64_16x16x4f64).
 //
-// One wavefront owns one centre (or one run of centres of a structure for
-// the "inner"/"outer" averages).  Per species segment of the centre's
-// neighbour list (rows of kernel 1 are grouped by species):
+// One workgroup owns one centre (or one run of centres of a structure for
+// the "inner"/"outer" averages), with one wavefront per contraction tile.
+// Per species segment of the centre's neighbour list (rows of kernel 1 are
+// grouped by species):
 //
 //   contraction  A[(l,k)][(l,m)] = sum_j R_lk(j) Y_lm(j)      (soap.cpp:902-914)
 //     The (l,k) x (l,m) products are packed block-diagonally into 16x16
 //     tiles (rows = radial channels, columns = harmonics, several l per
-//     tile); each MFMA adds 4 neighbours (K = 4).  A lane feeds the radial
-//     value of its own tile row for every tile, so every exp(-a d^2) is
-//     evaluated once, in the lane that consumes it; harmonics are computed
-//     four lanes per neighbour by m-columns and staged in LDS.
+//     tile); each MFMA adds 4 neighbours (K = 4).  Wavefront t owns tile t:
+//     a lane feeds the radial value of its tile row, so every exp(-a d^2)
+//     is evaluated once, in the lane that consumes it.  The harmonics of a
+//     chunk of 32 neighbours are computed two lanes per neighbour (cos/sin
+//     parts), the m-columns split across the wavefronts, and staged in LDS.
 //   beta fold    c = blockdiag(pi^1.5 beta_l) A               (soap.cpp:915-926)
 //     The accumulator layout of the MFMA (lane L, register r holds row
 //     L/16 + 4r, column L%16) is exactly the B-operand layout of step r, so
@@ -35,7 +37,7 @@ namespace {
 
 typedef double d4 __attribute__((ext_vector_type(4)));
 
-constexpr int kNb = 16;        // neighbours staged per chunk (4 MFMA steps)
+constexpr int kNb = 32;        // neighbours staged per chunk (8 MFMA steps)
 constexpr int kWaveThreads = 64;
 
 // Workgroups of the expansion kernel are a single wavefront: LDS operations
@@ -52,11 +54,6 @@ __device__ inline d4 mfma(double a, double b, d4 c) {
     return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
 }
 
-__constant__ double c_inv_small[32] = {
-    0.0, 1.0, 1.0 / 2, 1.0 / 3, 1.0 / 4, 1.0 / 5, 1.0 / 6, 1.0 / 7, 1.0 / 8, 1.0 / 9, 1.0 / 10,
-    1.0 / 11, 1.0 / 12, 1.0 / 13, 1.0 / 14, 1.0 / 15, 1.0 / 16, 1.0 / 17, 1.0 / 18, 1.0 / 19, 1.0 / 20,
-    1.0 / 21, 1.0 / 22, 1.0 / 23, 1.0 / 24, 1.0 / 25, 1.0 / 26, 1.0 / 27, 1.0 / 28, 1.0 / 29, 1.0 / 30,
-    1.0 / 31};
 
 // exp(x) for the radial Gaussians, x = -a d^2 <= 0, by the table-driven
 // method of P. T. P. Tang (ACM TOMS 15(2), 1989): x = (64k + j) ln2/64 + r
@@ -85,52 +82,48 @@ __device__ inline double exp_neg(double x, const double* tab64) {
     return ldexp(fma(t, em1, t), ki >> 6);
 }
 
-// Harmonics of one neighbour for the m-columns m = m0, m0 + 4, ... (one of
-// four cooperating lanes), written to a row of H values (entry (l, m') at
-// l*l + m', m' = l -/+ m for cos/sin, the layout of soap.cpp:60-69).  Same
-// recurrence as the generic kernel:
-// (l-m) R_l^m = (2l-1) z R_{l-1}^m - (l+m-1) r^2 R_{l-2}^m, seeded by the
-// Condon-Shortley diagonal (x + iy)^m (2m-1)!! (-1)^m.
-__device__ void harmonic_columns(double x, double y, double z, int l_max, int L, int m0, const double* norm,
-                                 double* out) {
+// Normalised real solid harmonics Q_l^m = N_lm R_l^m of one neighbour, one
+// component per lane: comp 0 writes the cos parts (entry l*l + l - m), comp 1
+// the sin parts (l*l + l + m, m > 0), the layout of soap.cpp:60-69.  The
+// recurrences carry the normalisation in their coefficients (hc, kHc*
+// layout, built with the plan):
+//   Q_0^0 = N_00,  Q_m^m = D_m (x + iy) Q_{m-1}^{m-1},  Q_{m+1}^m = E_m z Q_m^m,
+//   Q_l^m = A_lm z Q_{l-1}^m - B_lm r^2 Q_{l-2}^m.
+// Only the m-columns set in `mask` are computed (the workgroup's wavefronts
+// split them).  The l-loop is unrolled to kMaxLmax behind wave-uniform
+// guards, so each coefficient is a scalar load at a wave-uniform offset and
+// every store has a constant LDS offset from the lane's column base.
+__device__ __forceinline__ void harmonics_q(double x, double y, double z, int l_max, uint32_t mask, int comp,
+                                           const double* __restrict__ hc, double* out) {
     const double r2 = x * x + y * y + z * z;
-    double re_mm = 1.0, im_mm = 0.0;
-    int m_done = 0;
-    for (int m = m0; m <= l_max; m += 4) {
-        for (int q = m_done + 1; q <= m; ++q) {
-            const double f = -(2.0 * q - 1.0);
-            const double nr = f * (x * re_mm - y * im_mm);
-            const double ni = f * (x * im_mm + y * re_mm);
-            re_mm = nr;
-            im_mm = ni;
+    double sre = hc[0], sim = 0.0;
+    // highest m-column of this wavefront (the seed chain stops there)
+    const int m_top = mask == 0 ? -1 : min(l_max, 31 - __builtin_clz(mask));
+    for (int m = 0; m <= m_top; ++m) {
+        if (m > 0) {
+            const double dm = hc[kHcD + m];
+            const double nr = dm * fma(x, sre, -(y * sim));
+            const double ni = dm * fma(x, sim, y * sre);
+            sre = nr;
+            sim = ni;
         }
-        m_done = m;
-        double re2 = 0.0, im2 = 0.0, re1 = re_mm, im1 = im_mm;
-        for (int l = m; l <= l_max; ++l) {
-            double re0, im0;
-            if (l == m) {
-                re0 = re_mm;
-                im0 = im_mm;
-            } else if (l == m + 1) {
-                re0 = (2.0 * m + 1.0) * z * re_mm;
-                im0 = (2.0 * m + 1.0) * z * im_mm;
-            } else {
-                const double a = 2.0 * l - 1.0;
-                const double b = (l + m - 1.0) * r2;
-                const double inv = c_inv_small[l - m];
-                re0 = (a * z * re1 - b * re2) * inv;
-                im0 = (a * z * im1 - b * im2) * inv;
-            }
-            if (l > m) {
-                re2 = re1;
-                im2 = im1;
-                re1 = re0;
-                im1 = im0;
-            }
-            const double nf = norm[l * L + m];
-            double* row = out + l * l;
-            row[l - m] = nf * re0;
-            if (m > 0) row[l + m] = nf * im0;
+        if (((mask >> m) & 1u) == 0) continue;
+        double* col = out + (comp == 0 ? -m : m);  // entry (l, m) of this lane's part at col[l*l + l]
+        double q1 = comp == 0 ? sre : sim;
+        if (m > 0 || comp == 0) col[m * m + m] = q1;
+        if (m + 1 > l_max) continue;
+        double q2 = q1;
+        q1 = hc[kHcE + m] * (z * q2);
+        if (m > 0 || comp == 0) col[(m + 1) * (m + 1) + (m + 1)] = q1;
+#pragma unroll
+        for (int l = 2; l <= kMaxLmax; ++l) {
+            if (l < m + 2) continue;
+            if (l > l_max) break;
+            const int at = kHcAB + 2 * (l * (l + 1) / 2 + m);
+            const double q = fma(hc[at] * z, q1, -(hc[at + 1] * r2) * q2);
+            if (m > 0 || comp == 0) col[l * l + l] = q;
+            q2 = q1;
+            q1 = q;
         }
     }
 }
@@ -174,23 +167,44 @@ __device__ inline int feature_index(int i, int j, int S, int n, int L, int& stri
 
 // Power spectrum of the coefficients in LDS on 16x16 Gram tiles.  s_c holds
 // W + 1 rows of d.hpad values (row W and every pad entry are zero), entry
-// (row, l, m') at row*hpad + loff[l] + m'.  mode 0: write row `row` of out;
-// mode 2: add into the partial row `acc`.
-__device__ void power_spectrum_tiles(const double* s_c, const int* loff, const MfmaDims& d, const double* ps_pref,
-                                     int mode, void* out, int64_t pitch, int64_t row, double* acc) {
-    const int lane = threadIdx.x;
+// (row, l, m') at row*hpad + loff[l] + m'.  The units (tile pair, l) are
+// split into contiguous ranges over the `waves` wavefronts of the workgroup
+// (wavefront `wave` takes its range); units write disjoint features, and a
+// given feature always comes from the same wavefront.
+// mode 0: write row `row` of out; mode 2: add into the partial row `acc`;
+// mode 3: store into `acc` (the first centre of a run).
+__device__ void power_spectrum_tiles(const double* s_c, const int* loff, const MfmaDims& d,
+                                     const double* __restrict__ ps_pref, int mode, void* out, int64_t pitch,
+                                     int64_t row, double* acc, int wave, int waves) {
+    const int lane = threadIdx.x % kWaveThreads;
     const int W = d.S * d.n;
     const int RT = (W + 15) / 16;
+    const int L = d.L;
     const int hp = d.hpad;
+    const int units = RT * (RT + 1) / 2 * L;
+    const int u_begin = wave * units / waves;
+    const int u_end = (wave + 1) * units / waves;
     char* out_row = static_cast<char*>(out) + row * pitch;
-    for (int bi = 0; bi < RT; ++bi) {
-        for (int bj = bi; bj < RT; ++bj) {
+    int pair = -1;
+    const double* arow = s_c;
+    const double* brow = s_c;
+    int fb[4] = {-1, -1, -1, -1}, fs[4] = {0, 0, 0, 0};
+    for (int u = u_begin; u < u_end; ++u) {
+        const int p = u / L;
+        const int l = u - p * L;
+        if (p != pair) {
+            pair = p;
+            int bi = 0, rest = p;
+            while (rest >= RT - bi) {
+                rest -= RT - bi;
+                ++bi;
+            }
+            const int bj = bi + rest;
             const int ia = min(16 * bi + lane % 16, W);
             const int jb = min(16 * bj + lane % 16, W);
-            const double* arow = s_c + ia * hp + lane / 16;
-            const double* brow = s_c + jb * hp + lane / 16;
+            arow = s_c + ia * hp + lane / 16;
+            brow = s_c + jb * hp + lane / 16;
             const int j = 16 * bj + lane % 16;
-            int fb[4], fs[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int i = 16 * bi + lane / 16 + 4 * r;
@@ -198,25 +212,25 @@ __device__ void power_spectrum_tiles(const double* s_c, const int* loff, const M
                 fs[r] = 0;
                 fb[r] = ok ? feature_index(i, j, d.S, d.n, d.L, fs[r]) : -1;
             }
-            for (int l = 0; l <= d.l_max; ++l) {
-                const int steps = (2 * l + 4) / 4;
-                const int base = loff[l];
-                d4 acc4 = {0.0, 0.0, 0.0, 0.0};
-                for (int s = 0; s < steps; ++s) acc4 = mfma(arow[base + 4 * s], brow[base + 4 * s], acc4);
-                const double pref = ps_pref[l];
+        }
+        const int steps = (2 * l + 4) / 4;
+        const int base = loff[l];
+        d4 acc4 = {0.0, 0.0, 0.0, 0.0};
+        for (int s = 0; s < steps; ++s) acc4 = mfma(arow[base + 4 * s], brow[base + 4 * s], acc4);
+        const double pref = ps_pref[l];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    if (fb[r] >= 0) {
-                        const int f = fb[r] + l * fs[r];
-                        const double v = pref * acc4[r];
-                        if (mode != 0) {
-                            acc[f] += v;
-                        } else if (d.out_dtype == 4) {
-                            reinterpret_cast<float*>(out_row)[f] = static_cast<float>(v);
-                        } else {
-                            reinterpret_cast<double*>(out_row)[f] = v;
-                        }
-                    }
+        for (int r = 0; r < 4; ++r) {
+            if (fb[r] >= 0) {
+                const int f = fb[r] + l * fs[r];
+                const double v = pref * acc4[r];
+                if (mode == 2) {
+                    acc[f] += v;
+                } else if (mode == 3) {
+                    acc[f] = v;
+                } else if (d.out_dtype == 4) {
+                    reinterpret_cast<float*>(out_row)[f] = static_cast<float>(v);
+                } else {
+                    reinterpret_cast<double*>(out_row)[f] = v;
                 }
             }
         }
@@ -224,72 +238,66 @@ __device__ void power_spectrum_tiles(const double* s_c, const int* loff, const M
 }
 
 template <int T>
-__global__ __launch_bounds__(kWaveThreads) void k_soap_mfma(
+__global__ __launch_bounds__(T * kWaveThreads) void k_soap_mfma(
     const double* __restrict__ positions, const int64_t* __restrict__ pair_start, const int32_t* __restrict__ counts,
     const uint32_t* __restrict__ pair_bin, const double* __restrict__ bx, const double* __restrict__ by,
-    const double* __restrict__ bz, const MfmaTables tab, MfmaDims d, const int64_t* __restrict__ item_begin,
-    int64_t item_base, int64_t items, int64_t per_block, void* out, int64_t pitch, double* partial) {
+    const double* __restrict__ bz, const MfmaTables tab, const double* __restrict__ hcoef,
+    const double* __restrict__ ps_pref, MfmaDims d, const int64_t* __restrict__ item_begin, int64_t item_base,
+    int64_t items, int64_t per_block, void* out, int64_t pitch, double* partial) {
+    // hcoef and ps_pref are separate read-only, unaliased arguments so that
+    // their wave-uniform reads compile to scalar loads
     extern __shared__ double lds[];
-    const int lane = threadIdx.x;
+    const int tid = threadIdx.x;
+    const int lane = tid % kWaveThreads;
+    const int wave = tid / kWaveThreads;  // the tile this wavefront contracts
+    constexpr int kThreads = T * kWaveThreads;
     const int H = d.H, L = d.L, S = d.S, n = d.n;
     const int W = S * n;
     const int HP = H + 1;                 // Y row stride; entry H stays zero
     const int hp = d.hpad;                // padded c row
     const int cw = (W + 1) * hp;          // c words, including the zero row W
     double* s_y = lds;                    // kNb * HP
-    double* s_d2 = s_y + kNb * HP;        // kNb
-    double* s_norm = s_d2 + kNb;          // L * L
-    double* s_tab = s_norm + L * L;       // 64: 2^(j/64) for exp_neg
+    double* s_d2 = s_y + kNb * HP;        // kNb (-1 marks an empty slot)
+    double* s_tab = s_d2 + kNb;           // 64: 2^(j/64) for exp_neg
     double* s_c = s_tab + 64;             // cw (coefficients of the current centre, padded)
     double* s_csum = s_c + cw;            // cw (inner average only)
     int* s_loff = reinterpret_cast<int*>(s_csum + (d.mode == 1 ? cw : 0)); // L + 1
     int* s_seg = s_loff + (L + 1);        // S + 1: first row of each species segment of the centre
 
-    for (int i = lane; i < L * L; i += kWaveThreads) s_norm[i] = tab.hnorm[i];
-    s_tab[lane] = exp2(static_cast<double>(lane) / 64.0);
-    for (int i = lane; i < kNb * HP; i += kWaveThreads) s_y[i] = 0.0;
-    for (int i = lane; i < cw; i += kWaveThreads) s_c[i] = 0.0;
-    if (lane == 0) {
+    if (tid < 64) s_tab[tid] = exp2(static_cast<double>(tid) / 64.0);
+    for (int i = tid; i < kNb * HP; i += kThreads) s_y[i] = 0.0;
+    for (int i = tid; i < cw; i += kThreads) s_c[i] = 0.0;
+    if (tid == 0) {
         int off = 0;
         for (int l = 0; l <= L; ++l) {
             s_loff[l] = off;
             off += 4 * ((2 * l + 4) / 4);
         }
     }
-    // per-lane tile constants: radial parameters of row lane%16 (zero for pad
-    // rows, so their operand is 0 * e^0), Y column of lane%16 (the zero entry
-    // H for pad columns), and the beta-fold destination of result row
-    // lane/16 + 4r (or -1 off the diagonal blocks)
-    int ycol[T];
-    double pref[T], expo[T];
-#pragma unroll
-    for (int t = 0; t < T; ++t) {
-        const int rc = tab.row_channel[t * 16 + lane % 16];
-        const int ch = tab.col_harmonic[t * 16 + lane % 16];
-        ycol[t] = ch >= 0 ? ch : H;
-        pref[t] = rc >= 0 ? tab.pref[rc] : 0.0;
-        expo[t] = rc >= 0 ? tab.expo[rc] : 0.0;
-    }
-    wave_sync();
-    int dst[T][4];
-#pragma unroll
-    for (int t = 0; t < T; ++t) {
-        const int ch = tab.col_harmonic[t * 16 + lane % 16];
+    __syncthreads();
+    // per-lane constants of this wavefront's tile: radial parameters of row
+    // lane%16 (zero for pad rows, so their operand is 0 * e^0), Y column of
+    // lane%16 (the zero entry H for pad columns), the beta-fold operands and
+    // the destination of result row lane/16 + 4r (or -1 off the diagonal)
+    const bool has_tile = wave < d.tiles;
+    int ycol = H, dst[4] = {-1, -1, -1, -1};
+    double pref = 0.0, expo = 0.0, bfold[4] = {0.0, 0.0, 0.0, 0.0};
+    if (has_tile) {
+        const int rc = tab.row_channel[wave * 16 + lane % 16];
+        const int ch = tab.col_harmonic[wave * 16 + lane % 16];
+        ycol = ch >= 0 ? ch : H;
+        pref = rc >= 0 ? tab.pref[rc] : 0.0;
+        expo = rc >= 0 ? tab.expo[rc] : 0.0;
         const int lh = ch >= 0 ? degree_of_harmonic(ch) : -1;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int och = tab.row_channel[t * 16 + lane / 16 + 4 * r];
+            const int och = tab.row_channel[wave * 16 + lane / 16 + 4 * r];
             const bool diag = och >= 0 && ch >= 0 && och / n == lh;
-            dst[t][r] = diag ? (och % n) * hp + s_loff[lh] + (ch - lh * lh) : -1;
+            dst[r] = diag ? (och % n) * hp + s_loff[lh] + (ch - lh * lh) : -1;
+            bfold[r] = tab.beta_lane[(wave * 4 + r) * kWaveThreads + lane];
         }
     }
-    // A operands of the beta fold, the same for every species and centre
-    double bfold[T][4];
-#pragma unroll
-    for (int t = 0; t < T; ++t) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) bfold[t][r] = tab.beta_lane[(t * 4 + r) * kWaveThreads + lane];
-    }
+    const uint32_t hmask = d.harm_mask[wave];
 
     const int64_t item_first = item_base + static_cast<int64_t>(blockIdx.x) * per_block;
     const int64_t item_last = min(item_first + per_block, item_base + items);
@@ -298,9 +306,7 @@ __global__ __launch_bounds__(kWaveThreads) void k_soap_mfma(
         const int64_t last = item_begin ? item_begin[item + 1] : item + 1;
         double* part_row = partial != nullptr ? partial + item * (d.mode == 1 ? static_cast<int64_t>(cw) : d.F) : nullptr;
         if (d.mode == 1) {
-            for (int i = lane; i < cw; i += kWaveThreads) s_csum[i] = 0.0;
-        } else if (d.mode == 2) {
-            for (int64_t i = lane; i < d.F; i += kWaveThreads) part_row[i] = 0.0;
+            for (int i = tid; i < cw; i += kThreads) s_csum[i] = 0.0;
         }
         for (int64_t centre = first; centre < last; ++centre) {
             const double cx = positions[centre * 3 + 0];
@@ -308,7 +314,7 @@ __global__ __launch_bounds__(kWaveThreads) void k_soap_mfma(
             const double cz = positions[centre * 3 + 2];
             const int64_t centre_pairs = pair_start[centre];
             // species segments of this centre's rows (kernel 1 groups them by species)
-            if (lane == 0) {
+            if (tid == 0) {
                 int rows = 0;
                 for (int q = 0; q < S; ++q) {
                     s_seg[q] = rows;
@@ -316,12 +322,12 @@ __global__ __launch_bounds__(kWaveThreads) void k_soap_mfma(
                 }
                 s_seg[S] = rows;
             }
-            wave_sync();
-            // prefetch: lane (jj = lane/4) holds the image position of neighbour jj of the next chunk;
-            // the first chunk starts at the centre's first row whatever its species
+            __syncthreads();
+            // prefetch: lane pair (jj = lane/2) holds the image position of neighbour jj of the
+            // next chunk; the first chunk starts at the centre's first row whatever its species
             double px = 0.0, py = 0.0, pz = 0.0;
             {
-                const int jj = lane / 4;
+                const int jj = lane / 2;
                 if (jj < min(kNb, s_seg[S])) {
                     const uint32_t b = pair_bin[centre_pairs + jj];
                     px = bx[b];
@@ -335,34 +341,29 @@ __global__ __launch_bounds__(kWaveThreads) void k_soap_mfma(
                 if (kt == 0) {
                     // an empty species leaves its coefficients at zero
                     double* cdst = s_c + sp * n * hp;
-                    for (int i = lane; i < n * hp; i += kWaveThreads) cdst[i] = 0.0;
+                    for (int i = tid; i < n * hp; i += kThreads) cdst[i] = 0.0;
                     continue;
                 }
-                d4 acc[T];
-#pragma unroll
-                for (int t = 0; t < T; ++t) acc[t] = d4{0.0, 0.0, 0.0, 0.0};
+                // two accumulators (even and odd steps) halve the MFMA dependency chain
+                d4 acc0 = {0.0, 0.0, 0.0, 0.0}, acc1 = {0.0, 0.0, 0.0, 0.0};
                 for (int j0 = 0; j0 < kt; j0 += kNb) {
                     const int cnt = min(kNb, kt - j0);
-                    wave_sync();
                     {
-                        // four lanes per neighbour: geometry and m-columns of the harmonics;
-                        // rows past the chunk's end are zeroed so they add nothing
-                        const int jj = lane / 4;
-                        const int sub = lane % 4;
-                        double* yrow = s_y + jj * HP;
-                        if (jj < cnt) {
-                            // same arithmetic as kernel 1: image - centre, then d^2
-                            const double dx = px - cx;
-                            const double dy = py - cy;
-                            const double dz = pz - cz;
-                            if (sub == 0) s_d2[jj] = dx * dx + dy * dy + dz * dz;
-                            harmonic_columns(dx, dy, dz, d.l_max, L, sub, s_norm, yrow);
-                        } else {
-                            if (sub == 0) s_d2[jj] = 0.0;
-                            for (int h = sub; h < H; h += 4) yrow[h] = 0.0;
-                        }
+                        // two lanes per neighbour (cos / sin parts), this wavefront's
+                        // m-columns.  Every lane runs the recurrence so that control flow
+                        // and coefficient loads stay wave-uniform; slots past the chunk's
+                        // end hold harmonics of a stale (finite) position and get d^2 = -1,
+                        // which zeroes their radial operand
+                        const int jj = lane / 2;
+                        const int comp = lane % 2;
+                        // same arithmetic as kernel 1: image - centre, then d^2
+                        const double dx = px - cx;
+                        const double dy = py - cy;
+                        const double dz = pz - cz;
+                        if (wave == 0 && comp == 0) s_d2[jj] = jj < cnt ? dx * dx + dy * dy + dz * dz : -1.0;
+                        harmonics_q(dx, dy, dz, d.l_max, hmask, comp, hcoef, s_y + jj * HP);
                     }
-                    wave_sync();
+                    __syncthreads();
                     {
                         // issue the loads of the next chunk now: rows are contiguous across
                         // species, so the next chunk starts right after this one, but a chunk
@@ -379,7 +380,7 @@ __global__ __launch_bounds__(kWaveThreads) void k_soap_mfma(
                             }
                         }
                         const int avail = end - next;
-                        const int jj = lane / 4;
+                        const int jj = lane / 2;
                         if (avail > 0 && jj < min(kNb, avail)) {
                             const uint32_t b = pair_bin[centre_pairs + next + jj];
                             px = bx[b];
@@ -387,45 +388,49 @@ __global__ __launch_bounds__(kWaveThreads) void k_soap_mfma(
                             pz = bz[b];
                         }
                     }
+                    if (has_tile) {
 #pragma unroll
-                    for (int s = 0; s < kNb / 4; ++s) {
-                        const int jj = 4 * s + lane / 16;
-                        const double d2 = s_d2[jj];
-                        const double* yrow = s_y + jj * HP;
-#pragma unroll
-                        for (int t = 0; t < T; ++t) {
-                            const double a = pref[t] * exp_neg(-expo[t] * d2, s_tab);
-                            acc[t] = mfma(a, yrow[ycol[t]], acc[t]);
+                        for (int s = 0; s < kNb / 4; ++s) {
+                            const int jj = 4 * s + lane / 16;
+                            const double d2 = s_d2[jj];
+                            const double a = d2 >= 0.0 ? pref * exp_neg(-expo * d2, s_tab) : 0.0;
+                            const double y = s_y[jj * HP + ycol];
+                            if (s % 2 == 0) {
+                                acc0 = mfma(a, y, acc0);
+                            } else {
+                                acc1 = mfma(a, y, acc1);
+                            }
                         }
                     }
+                    __syncthreads();
                 }
-                // fold beta: c_T = Bbeta_T x A_T; step r uses the accumulator register r as B
-                double* cdst = s_c + sp * n * hp;
-#pragma unroll
-                for (int t = 0; t < T; ++t) {
+                if (has_tile) {
+                    // fold beta: c = Bbeta x A; step r uses accumulator register r as B
+                    double* cdst = s_c + sp * n * hp;
                     d4 c = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) c = mfma(bfold[t][r], acc[t][r], c);
+                    for (int r = 0; r < 4; ++r) c = mfma(bfold[r], acc0[r] + acc1[r], c);
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        if (dst[t][r] >= 0) cdst[dst[t][r]] = c[r];
+                        if (dst[r] >= 0) cdst[dst[r]] = c[r];
                     }
                 }
             }
-            wave_sync();
+            __syncthreads();
             if (d.mode == 0) {
-                power_spectrum_tiles(s_c, s_loff, d, tab.ps_pref, 0, out, pitch, centre, nullptr);
+                power_spectrum_tiles(s_c, s_loff, d, ps_pref, 0, out, pitch, centre, nullptr, wave, T);
             } else if (d.mode == 1) {
-                for (int i = lane; i < cw; i += kWaveThreads) s_csum[i] += s_c[i];
+                for (int i = tid; i < cw; i += kThreads) s_csum[i] += s_c[i];
             } else {
-                power_spectrum_tiles(s_c, s_loff, d, tab.ps_pref, 2, out, pitch, centre, part_row);
+                power_spectrum_tiles(s_c, s_loff, d, ps_pref, centre == first ? 3 : 2, out, pitch, centre, part_row,
+                                     wave, T);
             }
-            wave_sync();
+            __syncthreads();
         }
         if (d.mode == 1) {
-            for (int i = lane; i < cw; i += kWaveThreads) part_row[i] = s_csum[i];
+            for (int i = tid; i < cw; i += kThreads) part_row[i] = s_csum[i];
         }
-        wave_sync();
+        __syncthreads();
     }
 }
 
@@ -456,7 +461,7 @@ __global__ __launch_bounds__(kWaveThreads) void k_mfma_finalize_inner(const doub
             s_c[i] = natoms > 0 ? sum * inv : 0.0;
         }
         __syncthreads();
-        power_spectrum_tiles(s_c, s_loff, d, tab.ps_pref, 0, out, pitch, s, nullptr);
+        power_spectrum_tiles(s_c, s_loff, d, tab.ps_pref, 0, out, pitch, s, nullptr, 0, 1);
         __syncthreads();
     }
 }
@@ -479,10 +484,10 @@ template <int T>
 void launch(hipStream_t stream, unsigned grid, int64_t per_block, size_t lds, const PreparedBatch& pb,
             const DeviceGraph& g, const MfmaTables& tab, const MfmaDims& d, const int64_t* item_begin, int64_t base,
             int64_t count, void* out, int64_t pitch, double* partial) {
-    hipLaunchKernelGGL((k_soap_mfma<T>), dim3(grid), dim3(kWaveThreads), lds, stream, pb.d_positions.as<double>(),
+    hipLaunchKernelGGL((k_soap_mfma<T>), dim3(grid), dim3(T * kWaveThreads), lds, stream, pb.d_positions.as<double>(),
                        g.pair_start.as<int64_t>(), g.counts.as<int32_t>(), g.pair_bin.as<uint32_t>(), g.bin_x.as<double>(),
-                       g.bin_y.as<double>(), g.bin_z.as<double>(), tab, d, item_begin, base, count, per_block, out, pitch,
-                       partial);
+                       g.bin_y.as<double>(), g.bin_z.as<double>(), tab, tab.hcoef, tab.ps_pref, d, item_begin, base,
+                       count, per_block, out, pitch, partial);
 }
 
 // Compute units of the current device (queried once per process and device).
@@ -605,7 +610,7 @@ int mfma_padded_row(int l_max) {
 size_t mfma_lds_bytes(const MfmaDims& d) {
     const size_t W = static_cast<size_t>(d.S) * d.n;
     const size_t cw = (W + 1) * static_cast<size_t>(d.hpad);
-    size_t words = static_cast<size_t>(kNb) * (d.H + 1) + kNb + static_cast<size_t>(d.L) * d.L + 64 + cw;
+    size_t words = static_cast<size_t>(kNb) * (d.H + 1) + kNb + 64 + cw;
     if (d.mode == 1) words += cw;
     return words * sizeof(double) + static_cast<size_t>(d.L + 1 + kMaxSpecies + 1) * sizeof(int);
 }
@@ -614,6 +619,21 @@ void launch_mfma_expand(hipStream_t stream, int template_tiles, const PreparedBa
                         const MfmaTables& tab, const MfmaDims& d, const int64_t* item_begin, int64_t base,
                         int64_t count, void* out, int64_t pitch, double* partial) {
     const size_t lds = mfma_lds_bytes(d);
+    // split the harmonic m-columns over the workgroup's wavefronts, longest
+    // recurrence (l_max - m + 1 values) first onto the least-loaded one
+    MfmaDims dm = d;
+    {
+        int load[16] = {};
+        for (int w = 0; w < 16; ++w) dm.harm_mask[w] = 0;
+        for (int m = 0; m <= d.l_max; ++m) {
+            int best = 0;
+            for (int w = 1; w < template_tiles; ++w) {
+                if (load[w] < load[best]) best = w;
+            }
+            dm.harm_mask[best] |= 1u << m;
+            load[best] += d.l_max - m + 1;
+        }
+    }
     // persistent blocks: about two per wave slot the LDS footprint allows on
     // every CU, each walking a contiguous range of items
     const int64_t resident = std::max<int64_t>(1, std::min<int64_t>(32, (160 * 1024) / std::max<size_t>(lds, 1)));
@@ -624,14 +644,14 @@ void launch_mfma_expand(hipStream_t stream, int template_tiles, const PreparedBa
     const unsigned grid = static_cast<unsigned>((count + per_block - 1) / per_block);
     if (count <= 0) return;
     switch (template_tiles) {
-    case 1: launch<1>(stream, grid, per_block, lds, pb, g, tab, d, item_begin, base, count, out, pitch, partial); break;
-    case 2: launch<2>(stream, grid, per_block, lds, pb, g, tab, d, item_begin, base, count, out, pitch, partial); break;
-    case 3: launch<3>(stream, grid, per_block, lds, pb, g, tab, d, item_begin, base, count, out, pitch, partial); break;
-    case 4: launch<4>(stream, grid, per_block, lds, pb, g, tab, d, item_begin, base, count, out, pitch, partial); break;
-    case 6: launch<6>(stream, grid, per_block, lds, pb, g, tab, d, item_begin, base, count, out, pitch, partial); break;
-    case 8: launch<8>(stream, grid, per_block, lds, pb, g, tab, d, item_begin, base, count, out, pitch, partial); break;
-    case 12: launch<12>(stream, grid, per_block, lds, pb, g, tab, d, item_begin, base, count, out, pitch, partial); break;
-    case 16: launch<16>(stream, grid, per_block, lds, pb, g, tab, d, item_begin, base, count, out, pitch, partial); break;
+    case 1: launch<1>(stream, grid, per_block, lds, pb, g, tab, dm, item_begin, base, count, out, pitch, partial); break;
+    case 2: launch<2>(stream, grid, per_block, lds, pb, g, tab, dm, item_begin, base, count, out, pitch, partial); break;
+    case 3: launch<3>(stream, grid, per_block, lds, pb, g, tab, dm, item_begin, base, count, out, pitch, partial); break;
+    case 4: launch<4>(stream, grid, per_block, lds, pb, g, tab, dm, item_begin, base, count, out, pitch, partial); break;
+    case 6: launch<6>(stream, grid, per_block, lds, pb, g, tab, dm, item_begin, base, count, out, pitch, partial); break;
+    case 8: launch<8>(stream, grid, per_block, lds, pb, g, tab, dm, item_begin, base, count, out, pitch, partial); break;
+    case 12: launch<12>(stream, grid, per_block, lds, pb, g, tab, dm, item_begin, base, count, out, pitch, partial); break;
+    case 16: launch<16>(stream, grid, per_block, lds, pb, g, tab, dm, item_begin, base, count, out, pitch, partial); break;
     default: throw Error(MDX_INTERNAL, "unsupported MFMA tile count");
     }
     MDX_HIP(hipGetLastError());
