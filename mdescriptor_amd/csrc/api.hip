@@ -410,29 +410,6 @@ int mdx_hip_soap_plan_create(mdx_hip_ctx* ctx, const mdx_soap_params* params, md
                     hnorm[static_cast<size_t>(l * L + m)] = m == 0 ? norm : sqrt2 * norm;
                 }
             }
-            // normalised recurrence of the same harmonics, Q_l^m = N_lm R_l^m:
-            //   Q_m^m = D_m (x + iy) Q_{m-1}^{m-1},  Q_{m+1}^m = E_m z Q_m^m,
-            //   Q_l^m = A_lm z Q_{l-1}^m - B_lm r^2 Q_{l-2}^m,
-            // whose coefficients are ratios of the N_lm above times the
-            // recurrence factors, in closed form:
-            //   D_m = -sqrt((2m+1)/(2m)) (times sqrt(2) at m = 1), E_m = sqrt(2m+3),
-            //   A_lm = sqrt((2l-1)(2l+1)/((l-m)(l+m))),
-            //   B_lm = sqrt((2l+1)(l+m-1)(l-m-1)/((2l-3)(l-m)(l+m)))
-            std::vector<double> hcoef(static_cast<size_t>(mdx::kHcSize), 0.0);
-            hcoef[0] = 0.5 / std::sqrt(pi);
-            for (int m = 1; m <= mdx::kMaxLmax; ++m) {
-                const double dm = -std::sqrt((2.0 * m + 1.0) / (2.0 * m));
-                hcoef[static_cast<size_t>(mdx::kHcD + m)] = m == 1 ? dm * sqrt2 : dm;
-            }
-            for (int m = 0; m < mdx::kMaxLmax; ++m) hcoef[static_cast<size_t>(mdx::kHcE + m)] = std::sqrt(2.0 * m + 3.0);
-            for (int l = 2; l <= mdx::kMaxLmax; ++l) {
-                for (int m = 0; m + 2 <= l; ++m) {
-                    const size_t at = static_cast<size_t>(mdx::kHcAB + 2 * (l * (l + 1) / 2 + m));
-                    const double lm = static_cast<double>(l - m), lp = static_cast<double>(l + m);
-                    hcoef[at] = std::sqrt((2.0 * l - 1.0) * (2.0 * l + 1.0) / (lm * lp));
-                    hcoef[at + 1] = std::sqrt((2.0 * l + 1.0) * (lp - 1.0) * (lm - 1.0) / ((2.0 * l - 3.0) * lm * lp));
-                }
-            }
             // feature order of soap.cpp:997-1013 (labels core.py:321-329)
             std::vector<int32_t> fa, fb;
             fa.reserve(static_cast<size_t>(plan->features));
@@ -490,7 +467,6 @@ int mdx_hip_soap_plan_create(mdx_hip_ctx* ctx, const mdx_soap_params* params, md
             upload(plan->d_beta, beta);
             upload(plan->d_ps_pref, ps_pref);
             upload(plan->d_hnorm, hnorm);
-            upload(plan->d_hcoef, hcoef);
             upload(plan->d_feat_a, fa);
             upload(plan->d_feat_b, fb);
         } catch (...) {

@@ -25,14 +25,6 @@ constexpr int kBlock = 256;       // threads per workgroup of the graph and SOAP
 constexpr int kWave = 64;         // CDNA wavefront width
 constexpr int kChunk = 1024;      // candidates staged in LDS per graph chunk
 
-// Layout of the normalised solid-harmonic recurrence table (one per plan):
-// [0] N_00; [kHcD + m] D_m; [kHcE + m] E_m; [kHcAB + 2p], [kHcAB + 2p + 1]
-// A_lm, B_lm with p = l(l+1)/2 + m (l >= m + 2).
-constexpr int kHcD = 1;
-constexpr int kHcE = 24;
-constexpr int kHcAB = 48;
-constexpr int kHcSize = kHcAB + 2 * ((kMaxLmax + 1) * (kMaxLmax + 2) / 2);
-
 // Error carrying one of the C-ABI status codes; thrown inside the library and
 // converted to a status at the extern "C" boundary.
 struct Error : std::runtime_error {
@@ -171,7 +163,6 @@ struct mdx_soap_plan {
     mdx::DeviceBuffer d_pref, d_expo, d_beta, d_ps_pref; // radial prefactors/exponents, scaled beta, PS prefactors
     mdx::DeviceBuffer d_feat_a, d_feat_b;                // feature table: (c row offsets, l)
     mdx::DeviceBuffer d_hnorm;                           // harmonic normalisation N_lm (x sqrt(2) for m > 0)
-    mdx::DeviceBuffer d_hcoef;                           // normalised harmonic recurrence coefficients (kHc*)
     // matrix-core path (soap_mfma.hip): tile maps, beta-fold operands, feature index tables
     bool use_mfma = false;
     int tiles = 0;

@@ -429,7 +429,6 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
         tab.pref = p.d_pref.as<double>();
         tab.expo = p.d_expo.as<double>();
         tab.hnorm = p.d_hnorm.as<double>();
-        tab.hcoef = p.d_hcoef.as<double>();
         tab.ps_pref = p.d_ps_pref.as<double>();
         tab.fbase = p.d_fbase.as<int32_t>();
         tab.fstride = p.d_fstride.as<int32_t>();

@@ -34,7 +34,6 @@ struct MfmaTables {
     const double* pref;
     const double* expo;
     const double* hnorm;
-    const double* hcoef;  // normalised harmonic recurrence (kHc* layout)
     const double* ps_pref;
     const int32_t* fbase;
     const int32_t* fstride;

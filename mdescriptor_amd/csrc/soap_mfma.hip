@@ -2,8 +2,9 @@
 //
 // One workgroup owns one centre (or one run of centres of a structure for
 // the "inner"/"outer" averages), with one wavefront per contraction tile.
-// Per species segment of the centre's neighbour list (rows of kernel 1 are
-// grouped by species):
+// Rows of kernel 1 are grouped by species; each species segment of the
+// centre's list is padded to a multiple of 4 slots and the slots are walked
+// in chunks of 32 that may span segments:
 //
 //   contraction  A[(l,k)][(l,m)] = sum_j R_lk(j) Y_lm(j)      (soap.cpp:902-914)
 //     The (l,k) x (l,m) products are packed block-diagonally into 16x16
@@ -24,6 +25,7 @@
 // MFMA lane layouts (measured on gfx950): A operand lane L = A[L%16][L/16],
 // B operand lane L = B[L/16][L%16], result lane L register r =
 // D[L/16 + 4r][L%16].
+#include "harmonic_table.h"
 #include "mdx_internal.h"
 #include "soap_mfma.h"
 
@@ -33,22 +35,14 @@
 
 namespace mdx {
 
+static_assert(kHarmonicLmax == kMaxLmax, "harmonic table must cover every supported l_max");
+
 namespace {
 
 typedef double d4 __attribute__((ext_vector_type(4)));
 
 constexpr int kNb = 32;        // neighbours staged per chunk (8 MFMA steps)
 constexpr int kWaveThreads = 64;
-
-// Workgroups of the expansion kernel are a single wavefront: LDS operations
-// of one wave complete in issue order, so cross-lane LDS hand-offs need only
-// a compiler barrier and a wavefront-scope fence -- unlike __syncthreads(),
-// which would also wait for the outstanding global prefetch.
-__device__ inline void wave_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 __device__ inline d4 mfma(double a, double b, d4 c) {
     return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
@@ -84,24 +78,22 @@ __device__ inline double exp_neg(double x, const double* tab64) {
 
 // Normalised real solid harmonics Q_l^m = N_lm R_l^m of one neighbour, one
 // component per lane: comp 0 writes the cos parts (entry l*l + l - m), comp 1
-// the sin parts (l*l + l + m, m > 0), the layout of soap.cpp:60-69.  The
-// recurrences carry the normalisation in their coefficients (hc, kHc*
-// layout, built with the plan):
-//   Q_0^0 = N_00,  Q_m^m = D_m (x + iy) Q_{m-1}^{m-1},  Q_{m+1}^m = E_m z Q_m^m,
-//   Q_l^m = A_lm z Q_{l-1}^m - B_lm r^2 Q_{l-2}^m.
-// Only the m-columns set in `mask` are computed (the workgroup's wavefronts
-// split them).  The l-loop is unrolled to kMaxLmax behind wave-uniform
-// guards, so each coefficient is a scalar load at a wave-uniform offset and
-// every store has a constant LDS offset from the lane's column base.
-__device__ __forceinline__ void harmonics_q(double x, double y, double z, int l_max, uint32_t mask, int comp,
-                                           const double* __restrict__ hc, double* out) {
+// the sin parts (l*l + l + m, m > 0), the layout of soap.cpp:60-69, by the
+// recurrences of harmonic_table.h.  Only the m-columns set in `mask` are
+// computed (the workgroup's wavefronts split them).  With l_max = LM fixed at
+// compile time both loops unroll completely: every coefficient is an
+// immediate constant and every store a constant LDS offset from the lane's
+// column base.
+template <int LM>
+__device__ __forceinline__ void harmonics_fixed(double x, double y, double z, uint32_t mask, int comp,
+                                               const HarmonicRecurrence* __restrict__ hr, double* out) {
     const double r2 = x * x + y * y + z * z;
-    double sre = hc[0], sim = 0.0;
-    // highest m-column of this wavefront (the seed chain stops there)
-    const int m_top = mask == 0 ? -1 : min(l_max, 31 - __builtin_clz(mask));
-    for (int m = 0; m <= m_top; ++m) {
+    double sre = hr->n00, sim = 0.0;
+#pragma unroll
+    for (int m = 0; m <= LM; ++m) {
+        if ((mask >> m) == 0) break;  // no column of this wavefront from here on
         if (m > 0) {
-            const double dm = hc[kHcD + m];
+            const double dm = hr->d[m];
             const double nr = dm * fma(x, sre, -(y * sim));
             const double ni = dm * fma(x, sim, y * sre);
             sre = nr;
@@ -111,20 +103,28 @@ __device__ __forceinline__ void harmonics_q(double x, double y, double z, int l_
         double* col = out + (comp == 0 ? -m : m);  // entry (l, m) of this lane's part at col[l*l + l]
         double q1 = comp == 0 ? sre : sim;
         if (m > 0 || comp == 0) col[m * m + m] = q1;
-        if (m + 1 > l_max) continue;
+        if (m + 1 > LM) continue;
         double q2 = q1;
-        q1 = hc[kHcE + m] * (z * q2);
+        q1 = hr->e[m] * (z * q2);
         if (m > 0 || comp == 0) col[(m + 1) * (m + 1) + (m + 1)] = q1;
 #pragma unroll
-        for (int l = 2; l <= kMaxLmax; ++l) {
-            if (l < m + 2) continue;
-            if (l > l_max) break;
-            const int at = kHcAB + 2 * (l * (l + 1) / 2 + m);
-            const double q = fma(hc[at] * z, q1, -(hc[at + 1] * r2) * q2);
+        for (int l = m + 2; l <= LM; ++l) {
+            const double q = fma(hr->a[l][m] * z, q1, -(hr->b[l][m] * r2) * q2);
             if (m > 0 || comp == 0) col[l * l + l] = q;
             q2 = q1;
             q1 = q;
         }
+    }
+}
+
+// harmonics_fixed<l_max> for a run-time l_max (a wave-uniform branch chain)
+template <int LM = 0>
+__device__ __forceinline__ void harmonics_q(double x, double y, double z, int l_max, uint32_t mask, int comp,
+                                           const HarmonicRecurrence* __restrict__ hr, double* out) {
+    if (l_max == LM) {
+        harmonics_fixed<LM>(x, y, z, mask, comp, hr, out);
+    } else if constexpr (LM < kHarmonicLmax) {
+        harmonics_q<LM + 1>(x, y, z, l_max, mask, comp, hr, out);
     }
 }
 
@@ -241,15 +241,16 @@ template <int T>
 __global__ __launch_bounds__(T * kWaveThreads) void k_soap_mfma(
     const double* __restrict__ positions, const int64_t* __restrict__ pair_start, const int32_t* __restrict__ counts,
     const uint32_t* __restrict__ pair_bin, const double* __restrict__ bx, const double* __restrict__ by,
-    const double* __restrict__ bz, const MfmaTables tab, const double* __restrict__ hcoef,
-    const double* __restrict__ ps_pref, MfmaDims d, const int64_t* __restrict__ item_begin, int64_t item_base,
+    const double* __restrict__ bz, const MfmaTables tab, const double* __restrict__ ps_pref, MfmaDims d, const int64_t* __restrict__ item_begin, int64_t item_base,
     int64_t items, int64_t per_block, void* out, int64_t pitch, double* partial) {
-    // hcoef and ps_pref are separate read-only, unaliased arguments so that
-    // their wave-uniform reads compile to scalar loads
+    // ps_pref is a separate read-only, unaliased argument so that its
+    // wave-uniform reads compile to scalar loads
     extern __shared__ double lds[];
     const int tid = threadIdx.x;
     const int lane = tid % kWaveThreads;
-    const int wave = tid / kWaveThreads;  // the tile this wavefront contracts
+    // the tile this wavefront contracts (wave-uniform: keeps tile constants and
+    // branches on it in scalar registers)
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWaveThreads);
     constexpr int kThreads = T * kWaveThreads;
     const int H = d.H, L = d.L, S = d.S, n = d.n;
     const int W = S * n;
@@ -263,6 +264,8 @@ __global__ __launch_bounds__(T * kWaveThreads) void k_soap_mfma(
     double* s_csum = s_c + cw;            // cw (inner average only)
     int* s_loff = reinterpret_cast<int*>(s_csum + (d.mode == 1 ? cw : 0)); // L + 1
     int* s_seg = s_loff + (L + 1);        // S + 1: first row of each species segment of the centre
+    int* s_pseg = s_seg + (S + 1);        // S + 1: first slot of each segment (padded to 4)
+    int* s_step = s_pseg + (S + 1);       // kNb / 4: species of each MFMA step of the chunk
 
     if (tid < 64) s_tab[tid] = exp2(static_cast<double>(tid) / 64.0);
     for (int i = tid; i < kNb * HP; i += kThreads) s_y[i] = 0.0;
@@ -313,109 +316,130 @@ __global__ __launch_bounds__(T * kWaveThreads) void k_soap_mfma(
             const double cy = positions[centre * 3 + 1];
             const double cz = positions[centre * 3 + 2];
             const int64_t centre_pairs = pair_start[centre];
-            // species segments of this centre's rows (kernel 1 groups them by species)
+            // species segments of this centre's rows (kernel 1 groups them by
+            // species) and their slots: each segment is padded to a multiple of
+            // 4 slots, so one MFMA step (4 slots) never mixes species while a
+            // chunk of kNb slots may span several segments
             if (tid == 0) {
-                int rows = 0;
+                int rows = 0, slots = 0;
                 for (int q = 0; q < S; ++q) {
+                    const int c = counts[centre * S + q];
                     s_seg[q] = rows;
-                    rows += counts[centre * S + q];
+                    s_pseg[q] = slots;
+                    rows += c;
+                    slots += (c + 3) & ~3;
                 }
                 s_seg[S] = rows;
+                s_pseg[S] = slots;
             }
             __syncthreads();
-            // prefetch: lane pair (jj = lane/2) holds the image position of neighbour jj of the
-            // next chunk; the first chunk starts at the centre's first row whatever its species
+            // an empty species leaves its coefficients at zero
+            for (int q = 0; q < S; ++q) {
+                if (s_seg[q + 1] == s_seg[q]) {
+                    double* cdst = s_c + q * n * hp;
+                    for (int i = tid; i < n * hp; i += kThreads) cdst[i] = 0.0;
+                }
+            }
+            const int slots = s_pseg[S];
+            // row of slot p (-1 for a pad slot or p >= slots) and its species
+            auto slot_row = [&](int p, int& q) -> int {
+                q = 0;
+                while (q < S - 1 && p >= s_pseg[q + 1]) ++q;
+                const int off = p - s_pseg[q];
+                return off < s_seg[q + 1] - s_seg[q] ? s_seg[q] + off : -1;
+            };
+            // prefetch: lane pair jj = lane/2 holds the image position of slot jj
+            // of the next chunk (stale, finite values in pad slots)
             double px = 0.0, py = 0.0, pz = 0.0;
+            int prow, pq;
             {
-                const int jj = lane / 2;
-                if (jj < min(kNb, s_seg[S])) {
-                    const uint32_t b = pair_bin[centre_pairs + jj];
+                prow = slot_row(lane / 2, pq);
+                if (prow >= 0) {
+                    const uint32_t b = pair_bin[centre_pairs + prow];
                     px = bx[b];
                     py = by[b];
                     pz = bz[b];
                 }
             }
-            for (int sp = 0; sp < S; ++sp) {
-                const int seg0 = s_seg[sp];
-                const int kt = s_seg[sp + 1] - seg0;
-                if (kt == 0) {
-                    // an empty species leaves its coefficients at zero
-                    double* cdst = s_c + sp * n * hp;
-                    for (int i = tid; i < n * hp; i += kThreads) cdst[i] = 0.0;
-                    continue;
-                }
-                // two accumulators (even and odd steps) halve the MFMA dependency chain
-                d4 acc0 = {0.0, 0.0, 0.0, 0.0}, acc1 = {0.0, 0.0, 0.0, 0.0};
-                for (int j0 = 0; j0 < kt; j0 += kNb) {
-                    const int cnt = min(kNb, kt - j0);
-                    {
-                        // two lanes per neighbour (cos / sin parts), this wavefront's
-                        // m-columns.  Every lane runs the recurrence so that control flow
-                        // and coefficient loads stay wave-uniform; slots past the chunk's
-                        // end hold harmonics of a stale (finite) position and get d^2 = -1,
-                        // which zeroes their radial operand
-                        const int jj = lane / 2;
-                        const int comp = lane % 2;
-                        // same arithmetic as kernel 1: image - centre, then d^2
-                        const double dx = px - cx;
-                        const double dy = py - cy;
-                        const double dz = pz - cz;
-                        if (wave == 0 && comp == 0) s_d2[jj] = jj < cnt ? dx * dx + dy * dy + dz * dz : -1.0;
-                        harmonics_q(dx, dy, dz, d.l_max, hmask, comp, hcoef, s_y + jj * HP);
-                    }
-                    __syncthreads();
-                    {
-                        // issue the loads of the next chunk now: rows are contiguous across
-                        // species, so the next chunk starts right after this one, but a chunk
-                        // never runs past its species' end
-                        const int next = seg0 + j0 + kNb < s_seg[sp + 1] ? seg0 + j0 + kNb : s_seg[sp + 1];
-                        int end = s_seg[sp + 1];
-                        if (next == end) {
-                            // first non-empty species after this one (empty ones own no rows)
-                            for (int q = sp + 1; q < S; ++q) {
-                                if (s_seg[q + 1] > next) {
-                                    end = s_seg[q + 1];
-                                    break;
-                                }
-                            }
-                        }
-                        const int avail = end - next;
-                        const int jj = lane / 2;
-                        if (avail > 0 && jj < min(kNb, avail)) {
-                            const uint32_t b = pair_bin[centre_pairs + next + jj];
-                            px = bx[b];
-                            py = by[b];
-                            pz = bz[b];
-                        }
-                    }
-                    if (has_tile) {
+            // the accumulators hold the partial contraction of species `cur`;
+            // they are folded into s_c when the species changes and at the end.
+            // Two accumulators (even and odd steps) halve the MFMA dependency chain
+            int cur = -1;
+            d4 acc0 = {0.0, 0.0, 0.0, 0.0}, acc1 = {0.0, 0.0, 0.0, 0.0};
+            auto fold = [&](int q) {
+                // c = Bbeta x A; step r uses accumulator register r as B
+                double* cdst = s_c + q * n * hp;
+                d4 c = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-                        for (int s = 0; s < kNb / 4; ++s) {
-                            const int jj = 4 * s + lane / 16;
-                            const double d2 = s_d2[jj];
-                            const double a = d2 >= 0.0 ? pref * exp_neg(-expo * d2, s_tab) : 0.0;
-                            const double y = s_y[jj * HP + ycol];
-                            if (s % 2 == 0) {
-                                acc0 = mfma(a, y, acc0);
-                            } else {
-                                acc1 = mfma(a, y, acc1);
-                            }
-                        }
+                for (int r = 0; r < 4; ++r) c = mfma(bfold[r], acc0[r] + acc1[r], c);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if (dst[r] >= 0) cdst[dst[r]] = c[r];
+                }
+            };
+            for (int j0 = 0; j0 < slots; j0 += kNb) {
+                {
+                    // two lanes per slot (cos / sin parts), this wavefront's
+                    // m-columns.  Every lane runs the recurrence so that control flow
+                    // and coefficient loads stay wave-uniform; pad slots hold
+                    // harmonics of a stale position and get d^2 = -1, which zeroes
+                    // their radial operand
+                    const int jj = lane / 2;
+                    const int comp = lane % 2;
+                    // same arithmetic as kernel 1: image - centre, then d^2
+                    const double dx = px - cx;
+                    const double dy = py - cy;
+                    const double dz = pz - cz;
+                    if (wave == 0 && comp == 0) {
+                        s_d2[jj] = prow >= 0 ? dx * dx + dy * dy + dz * dz : -1.0;
+                        if (jj % 4 == 0) s_step[jj / 4] = pq;
                     }
-                    __syncthreads();
+                    // l_max, the column mask and an offset of zero into the table are
+                    // re-read from opaque scalar registers every chunk, so that the
+                    // compiler keeps the coefficient loads and the branches on them
+                    // inside the loop instead of holding their results in (spilled)
+                    // scalar registers across it
+                    int lm = d.l_max, zero = 0;
+                    uint32_t mk = hmask;
+                    asm volatile("" : "+s"(lm), "+s"(mk), "+s"(zero));
+                    harmonics_q(dx, dy, dz, lm, mk, comp, &kHarmonic + zero, s_y + jj * HP);
+                }
+                __syncthreads();
+                {
+                    // issue the loads of the next chunk now
+                    prow = slot_row(j0 + kNb + lane / 2, pq);
+                    if (prow >= 0) {
+                        const uint32_t b = pair_bin[centre_pairs + prow];
+                        px = bx[b];
+                        py = by[b];
+                        pz = bz[b];
+                    }
                 }
                 if (has_tile) {
-                    // fold beta: c = Bbeta x A; step r uses accumulator register r as B
-                    double* cdst = s_c + sp * n * hp;
-                    d4 c = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) c = mfma(bfold[r], acc0[r] + acc1[r], c);
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        if (dst[r] >= 0) cdst[dst[r]] = c[r];
+                    for (int s = 0; s < kNb / 4; ++s) {
+                        if (j0 + 4 * s >= slots) break;
+                        const int q = __builtin_amdgcn_readfirstlane(s_step[s]);
+                        if (q != cur) {
+                            if (cur >= 0) fold(cur);
+                            cur = q;
+                            acc0 = d4{0.0, 0.0, 0.0, 0.0};
+                            acc1 = d4{0.0, 0.0, 0.0, 0.0};
+                        }
+                        const int jj = 4 * s + lane / 16;
+                        const double d2 = s_d2[jj];
+                        const double a = d2 >= 0.0 ? pref * exp_neg(-expo * d2, s_tab) : 0.0;
+                        const double y = s_y[jj * HP + ycol];
+                        if (s % 2 == 0) {
+                            acc0 = mfma(a, y, acc0);
+                        } else {
+                            acc1 = mfma(a, y, acc1);
+                        }
                     }
                 }
+                __syncthreads();
             }
+            if (has_tile && cur >= 0) fold(cur);
             __syncthreads();
             if (d.mode == 0) {
                 power_spectrum_tiles(s_c, s_loff, d, ps_pref, 0, out, pitch, centre, nullptr, wave, T);
@@ -486,7 +510,7 @@ void launch(hipStream_t stream, unsigned grid, int64_t per_block, size_t lds, co
             int64_t count, void* out, int64_t pitch, double* partial) {
     hipLaunchKernelGGL((k_soap_mfma<T>), dim3(grid), dim3(T * kWaveThreads), lds, stream, pb.d_positions.as<double>(),
                        g.pair_start.as<int64_t>(), g.counts.as<int32_t>(), g.pair_bin.as<uint32_t>(), g.bin_x.as<double>(),
-                       g.bin_y.as<double>(), g.bin_z.as<double>(), tab, tab.hcoef, tab.ps_pref, d, item_begin, base,
+                       g.bin_y.as<double>(), g.bin_z.as<double>(), tab, tab.ps_pref, d, item_begin, base,
                        count, per_block, out, pitch, partial);
 }
 
@@ -612,7 +636,7 @@ size_t mfma_lds_bytes(const MfmaDims& d) {
     const size_t cw = (W + 1) * static_cast<size_t>(d.hpad);
     size_t words = static_cast<size_t>(kNb) * (d.H + 1) + kNb + 64 + cw;
     if (d.mode == 1) words += cw;
-    return words * sizeof(double) + static_cast<size_t>(d.L + 1 + kMaxSpecies + 1) * sizeof(int);
+    return words * sizeof(double) + static_cast<size_t>(d.L + 1 + 2 * (d.S + 1) + kNb / 4) * sizeof(int);
 }
 
 void launch_mfma_expand(hipStream_t stream, int template_tiles, const PreparedBatch& pb, const DeviceGraph& g,
