@@ -30,6 +30,9 @@ HIPCC_FLAGS = [
     "-fPIC",
     "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # matrix-core accumulators in ordinary VGPRs (gfx950 allows both forms):
+    # avoids copies between AGPRs and VGPRs around every MFMA step
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wall",
     "-Wno-unused-function",
     "-Wno-unused-result",

@@ -432,7 +432,7 @@ int mdx_hip_soap_plan_create(mdx_hip_ctx* ctx, const mdx_soap_params* params, md
             if (choice != "auto" && choice != "generic" && choice != "mfma") {
                 throw mdx::Error(MDX_INVALID_ARGUMENT, "MDX_HIP_SOAP_KERNEL must be auto, generic or mfma");
             }
-            const mdx::MfmaPlanHost mp = mdx::plan_mfma_tables(plan->S, n, p.l_max, beta);
+            const mdx::MfmaPlanHost mp = mdx::plan_mfma_tables(plan->S, n, p.l_max, beta, pref);
             mdx::MfmaDims md{};
             md.S = plan->S;
             md.n = n;

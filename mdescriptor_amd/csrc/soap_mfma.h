@@ -23,8 +23,9 @@ struct MfmaDims {
 //   row_channel[t*16 + r]  radial channel l*n + k of row r of tile t, or -1
 //   col_harmonic[t*16 + c] harmonic index l*l + m' of column c, or -1
 //   beta_lane[(t*4 + s)*64 + lane]  A operand of beta-fold step s for a lane:
-//       pi^1.5 beta[l][n'][k] for row (l, n') = lane%16 and column (l, k) =
-//       4s + lane/16 of the same diagonal block, else 0
+//       pi^1.5 beta[l][n'][k] pref[l][k] for row (l, n') = lane%16 and column
+//       (l, k) = 4s + lane/16 of the same diagonal block, else 0 (the radial
+//       prefactor is applied here, once per centre, instead of per neighbour)
 //   fbase/fstride[i*W + j] feature index of channel pair (i, j), i <= j, at
 //       degree l is fbase + l * fstride (layout of soap.cpp:997-1013)
 struct MfmaTables {
@@ -41,13 +42,15 @@ struct MfmaTables {
 
 // Host-side tables of a plan: block-diagonal packing of the (l, k) x (l, m)
 // blocks into 16x16 tiles, the beta-fold operands and feature indices.
-// beta_scaled is pi^1.5 beta with index (l*n + n')*n + k.
+// beta_scaled is pi^1.5 beta with index (l*n + n')*n + k; pref is the radial
+// prefactor of channel l*n + k.
 struct MfmaPlanHost {
     int tiles = 0;
     std::vector<int32_t> row_channel, col_harmonic, fbase, fstride;
     std::vector<double> beta_lane;
 };
-MfmaPlanHost plan_mfma_tables(int S, int n, int l_max, const std::vector<double>& beta_scaled);
+MfmaPlanHost plan_mfma_tables(int S, int n, int l_max, const std::vector<double>& beta_scaled,
+                              const std::vector<double>& pref);
 
 int mfma_template_tiles(int tiles);
 int mfma_padded_row(int l_max);

@@ -85,10 +85,11 @@ __device__ inline double exp_neg(double x, const double* tab64) {
 // immediate constant and every store a constant LDS offset from the lane's
 // column base.
 template <int LM>
-__device__ __forceinline__ void harmonics_fixed(double x, double y, double z, uint32_t mask, int comp,
+__device__ __forceinline__ void harmonics_fixed(double x, double y, double z, bool valid, uint32_t mask, int comp,
                                                const HarmonicRecurrence* __restrict__ hr, double* out) {
     const double r2 = x * x + y * y + z * z;
-    double sre = hr->n00, sim = 0.0;
+    // an invalid (pad) slot gets all-zero harmonics from a zero seed
+    double sre = valid ? hr->n00 : 0.0, sim = 0.0;
 #pragma unroll
     for (int m = 0; m <= LM; ++m) {
         if ((mask >> m) == 0) break;  // no column of this wavefront from here on
@@ -119,12 +120,12 @@ __device__ __forceinline__ void harmonics_fixed(double x, double y, double z, ui
 
 // harmonics_fixed<l_max> for a run-time l_max (a wave-uniform branch chain)
 template <int LM = 0>
-__device__ __forceinline__ void harmonics_q(double x, double y, double z, int l_max, uint32_t mask, int comp,
-                                           const HarmonicRecurrence* __restrict__ hr, double* out) {
+__device__ __forceinline__ void harmonics_q(double x, double y, double z, bool valid, int l_max, uint32_t mask,
+                                           int comp, const HarmonicRecurrence* __restrict__ hr, double* out) {
     if (l_max == LM) {
-        harmonics_fixed<LM>(x, y, z, mask, comp, hr, out);
+        harmonics_fixed<LM>(x, y, z, valid, mask, comp, hr, out);
     } else if constexpr (LM < kHarmonicLmax) {
-        harmonics_q<LM + 1>(x, y, z, l_max, mask, comp, hr, out);
+        harmonics_q<LM + 1>(x, y, z, valid, l_max, mask, comp, hr, out);
     }
 }
 
@@ -237,11 +238,14 @@ __device__ void power_spectrum_tiles(const double* s_c, const int* loff, const M
     }
 }
 
+// At least 4 wavefronts per SIMD: the register budget (128 VGPRs) the
+// compiler must fit.
 template <int T>
-__global__ __launch_bounds__(T * kWaveThreads) void k_soap_mfma(
+__global__ __launch_bounds__(T * kWaveThreads, 4) void k_soap_mfma(
     const double* __restrict__ positions, const int64_t* __restrict__ pair_start, const int32_t* __restrict__ counts,
     const uint32_t* __restrict__ pair_bin, const double* __restrict__ bx, const double* __restrict__ by,
-    const double* __restrict__ bz, const MfmaTables tab, const double* __restrict__ ps_pref, MfmaDims d, const int64_t* __restrict__ item_begin, int64_t item_base,
+    const double* __restrict__ bz, const MfmaTables tab, const double* __restrict__ ps_pref, MfmaDims d,
+    const int64_t* __restrict__ item_begin, int64_t item_base,
     int64_t items, int64_t per_block, void* out, int64_t pitch, double* partial) {
     // ps_pref is a separate read-only, unaliased argument so that its
     // wave-uniform reads compile to scalar loads
@@ -265,7 +269,7 @@ __global__ __launch_bounds__(T * kWaveThreads) void k_soap_mfma(
     int* s_loff = reinterpret_cast<int*>(s_csum + (d.mode == 1 ? cw : 0)); // L + 1
     int* s_seg = s_loff + (L + 1);        // S + 1: first row of each species segment of the centre
     int* s_pseg = s_seg + (S + 1);        // S + 1: first slot of each segment (padded to 4)
-    int* s_step = s_pseg + (S + 1);       // kNb / 4: species of each MFMA step of the chunk
+    int* s_step = s_pseg + (S + 1);       // 1: species of the chunk's MFMA steps, 4 bits each
 
     if (tid < 64) s_tab[tid] = exp2(static_cast<double>(tid) / 64.0);
     for (int i = tid; i < kNb * HP; i += kThreads) s_y[i] = 0.0;
@@ -278,18 +282,18 @@ __global__ __launch_bounds__(T * kWaveThreads) void k_soap_mfma(
         }
     }
     __syncthreads();
-    // per-lane constants of this wavefront's tile: radial parameters of row
-    // lane%16 (zero for pad rows, so their operand is 0 * e^0), Y column of
-    // lane%16 (the zero entry H for pad columns), the beta-fold operands and
-    // the destination of result row lane/16 + 4r (or -1 off the diagonal)
+    // per-lane constants of this wavefront's tile: radial exponent of row
+    // lane%16 (zero for pad rows, whose sums the fold multiplies by zero), Y
+    // column of lane%16 (the zero entry H for pad columns), the beta-fold
+    // operands (which carry the radial prefactors) and the destination of
+    // result row lane/16 + 4r (or -1 off the diagonal)
     const bool has_tile = wave < d.tiles;
     int ycol = H, dst[4] = {-1, -1, -1, -1};
-    double pref = 0.0, expo = 0.0, bfold[4] = {0.0, 0.0, 0.0, 0.0};
+    double expo = 0.0, bfold[4] = {0.0, 0.0, 0.0, 0.0};
     if (has_tile) {
         const int rc = tab.row_channel[wave * 16 + lane % 16];
         const int ch = tab.col_harmonic[wave * 16 + lane % 16];
         ycol = ch >= 0 ? ch : H;
-        pref = rc >= 0 ? tab.pref[rc] : 0.0;
         expo = rc >= 0 ? tab.expo[rc] : 0.0;
         const int lh = ch >= 0 ? degree_of_harmonic(ch) : -1;
 #pragma unroll
@@ -361,17 +365,16 @@ __global__ __launch_bounds__(T * kWaveThreads) void k_soap_mfma(
                     pz = bz[b];
                 }
             }
-            // the accumulators hold the partial contraction of species `cur`;
-            // they are folded into s_c when the species changes and at the end.
-            // Two accumulators (even and odd steps) halve the MFMA dependency chain
+            // the accumulator holds the partial contraction of species `cur`; it
+            // is folded into s_c when the species changes and at the end
             int cur = -1;
-            d4 acc0 = {0.0, 0.0, 0.0, 0.0}, acc1 = {0.0, 0.0, 0.0, 0.0};
+            d4 acc = {0.0, 0.0, 0.0, 0.0};
             auto fold = [&](int q) {
                 // c = Bbeta x A; step r uses accumulator register r as B
                 double* cdst = s_c + q * n * hp;
                 d4 c = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-                for (int r = 0; r < 4; ++r) c = mfma(bfold[r], acc0[r] + acc1[r], c);
+                for (int r = 0; r < 4; ++r) c = mfma(bfold[r], acc[r], c);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     if (dst[r] >= 0) cdst[dst[r]] = c[r];
@@ -381,18 +384,24 @@ __global__ __launch_bounds__(T * kWaveThreads) void k_soap_mfma(
                 {
                     // two lanes per slot (cos / sin parts), this wavefront's
                     // m-columns.  Every lane runs the recurrence so that control flow
-                    // and coefficient loads stay wave-uniform; pad slots hold
-                    // harmonics of a stale position and get d^2 = -1, which zeroes
-                    // their radial operand
+                    // and coefficient loads stay wave-uniform; pad slots (and slots
+                    // past the end) get all-zero harmonics, so whatever finite radial
+                    // value meets them adds nothing
                     const int jj = lane / 2;
                     const int comp = lane % 2;
                     // same arithmetic as kernel 1: image - centre, then d^2
                     const double dx = px - cx;
                     const double dy = py - cy;
                     const double dz = pz - cz;
-                    if (wave == 0 && comp == 0) {
-                        s_d2[jj] = prow >= 0 ? dx * dx + dy * dy + dz * dz : -1.0;
-                        if (jj % 4 == 0) s_step[jj / 4] = pq;
+                    if (wave == 0) {
+                        if (comp == 0) s_d2[jj] = dx * dx + dy * dy + dz * dz;
+                        // species of the 8 MFMA steps, 4 bits each, from the lanes
+                        // holding slots 0, 4, .., 28 (lanes 0, 8, .., 56)
+                        uint32_t bits = lane % 8 == 0 ? static_cast<uint32_t>(pq) << (4 * (lane / 8)) : 0u;
+                        bits |= __shfl_xor(bits, 8);
+                        bits |= __shfl_xor(bits, 16);
+                        bits |= __shfl_xor(bits, 32);
+                        if (lane == 0) s_step[0] = static_cast<int>(bits);
                     }
                     // l_max, the column mask and an offset of zero into the table are
                     // re-read from opaque scalar registers every chunk, so that the
@@ -402,7 +411,7 @@ __global__ __launch_bounds__(T * kWaveThreads) void k_soap_mfma(
                     int lm = d.l_max, zero = 0;
                     uint32_t mk = hmask;
                     asm volatile("" : "+s"(lm), "+s"(mk), "+s"(zero));
-                    harmonics_q(dx, dy, dz, lm, mk, comp, &kHarmonic + zero, s_y + jj * HP);
+                    harmonics_q(dx, dy, dz, prow >= 0, lm, mk, comp, &kHarmonic + zero, s_y + jj * HP);
                 }
                 __syncthreads();
                 {
@@ -416,24 +425,30 @@ __global__ __launch_bounds__(T * kWaveThreads) void k_soap_mfma(
                     }
                 }
                 if (has_tile) {
+                    // per half chunk: operands of 4 steps first (independent LDS
+                    // reads and exps the compiler can overlap), then their MFMAs
+                    const uint32_t species = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(s_step[0]));
+                    const int nst = min(kNb / 4, (slots - j0) / 4);
 #pragma unroll
-                    for (int s = 0; s < kNb / 4; ++s) {
-                        if (j0 + 4 * s >= slots) break;
-                        const int q = __builtin_amdgcn_readfirstlane(s_step[s]);
-                        if (q != cur) {
-                            if (cur >= 0) fold(cur);
-                            cur = q;
-                            acc0 = d4{0.0, 0.0, 0.0, 0.0};
-                            acc1 = d4{0.0, 0.0, 0.0, 0.0};
+                    for (int h = 0; h < kNb / 4; h += 4) {
+                        double av[4], yv[4];
+#pragma unroll
+                        for (int s = 0; s < 4; ++s) {
+                            const int jj = 4 * (h + s) + lane / 16;
+                            av[s] = exp_neg(-expo * s_d2[jj], s_tab);
+                            yv[s] = s_y[jj * HP + ycol];
                         }
-                        const int jj = 4 * s + lane / 16;
-                        const double d2 = s_d2[jj];
-                        const double a = d2 >= 0.0 ? pref * exp_neg(-expo * d2, s_tab) : 0.0;
-                        const double y = s_y[jj * HP + ycol];
-                        if (s % 2 == 0) {
-                            acc0 = mfma(a, y, acc0);
-                        } else {
-                            acc1 = mfma(a, y, acc1);
+#pragma unroll
+                        for (int s = 0; s < 4; ++s) {
+                            if (h + s < nst) {
+                                const int q = static_cast<int>((species >> (4 * (h + s))) & 15u);
+                                if (q != cur) {
+                                    if (cur >= 0) fold(cur);
+                                    cur = q;
+                                    acc = d4{0.0, 0.0, 0.0, 0.0};
+                                }
+                                acc = mfma(av[s], yv[s], acc);
+                            }
                         }
                     }
                 }
@@ -530,7 +545,8 @@ int device_compute_units() {
 
 } // namespace
 
-MfmaPlanHost plan_mfma_tables(int S, int n, int l_max, const std::vector<double>& beta_scaled) {
+MfmaPlanHost plan_mfma_tables(int S, int n, int l_max, const std::vector<double>& beta_scaled,
+                              const std::vector<double>& pref) {
     struct Block {
         int l, m_start, width;
     };
@@ -589,7 +605,7 @@ MfmaPlanHost plan_mfma_tables(int S, int n, int l_max, const std::vector<double>
                 if (cr >= 0 && ck >= 0 && cr / n == ck / n) {
                     const int l = cr / n, np = cr % n, k = ck % n;
                     out.beta_lane[static_cast<size_t>((t * 4 + s) * 64 + lane)] =
-                        beta_scaled[static_cast<size_t>((l * n + np) * n + k)];
+                        beta_scaled[static_cast<size_t>((l * n + np) * n + k)] * pref[static_cast<size_t>(ck)];
                 }
             }
         }
@@ -636,7 +652,7 @@ size_t mfma_lds_bytes(const MfmaDims& d) {
     const size_t cw = (W + 1) * static_cast<size_t>(d.hpad);
     size_t words = static_cast<size_t>(kNb) * (d.H + 1) + kNb + 64 + cw;
     if (d.mode == 1) words += cw;
-    return words * sizeof(double) + static_cast<size_t>(d.L + 1 + 2 * (d.S + 1) + kNb / 4) * sizeof(int);
+    return words * sizeof(double) + static_cast<size_t>(d.L + 1 + 2 * (d.S + 1) + 1) * sizeof(int);
 }
 
 void launch_mfma_expand(hipStream_t stream, int template_tiles, const PreparedBatch& pb, const DeviceGraph& g,
