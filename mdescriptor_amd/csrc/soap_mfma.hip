@@ -258,11 +258,13 @@ __global__ __launch_bounds__(T * kWaveThreads, 4) void k_soap_mfma(
     constexpr int kThreads = T * kWaveThreads;
     const int H = d.H, L = d.L, S = d.S, n = d.n;
     const int W = S * n;
-    const int HP = H + 1;                 // Y row stride; entry H stays zero
+    // Y row stride, odd so that the 32 slots of one harmonic store hit distinct
+    // bank pairs; entry H stays zero
+    const int HP = (H + 1) | 1;
     const int hp = d.hpad;                // padded c row
     const int cw = (W + 1) * hp;          // c words, including the zero row W
     double* s_y = lds;                    // kNb * HP
-    double* s_d2 = s_y + kNb * HP;        // kNb (-1 marks an empty slot)
+    double* s_d2 = s_y + kNb * HP;        // kNb: d^2 of the chunk's slots
     double* s_tab = s_d2 + kNb;           // 64: 2^(j/64) for exp_neg
     double* s_c = s_tab + 64;             // cw (coefficients of the current centre, padded)
     double* s_csum = s_c + cw;            // cw (inner average only)
@@ -345,10 +347,11 @@ __global__ __launch_bounds__(T * kWaveThreads, 4) void k_soap_mfma(
                 }
             }
             const int slots = s_pseg[S];
-            // row of slot p (-1 for a pad slot or p >= slots) and its species
+            // row of slot p (-1 for a pad slot or p >= slots) and its species;
+            // the species count runs over wave-uniform bounds (no divergence)
             auto slot_row = [&](int p, int& q) -> int {
                 q = 0;
-                while (q < S - 1 && p >= s_pseg[q + 1]) ++q;
+                for (int t = 1; t < S; ++t) q += p >= s_pseg[t] ? 1 : 0;
                 const int off = p - s_pseg[q];
                 return off < s_seg[q + 1] - s_seg[q] ? s_seg[q] + off : -1;
             };
@@ -644,13 +647,16 @@ int mfma_template_tiles(int tiles) {
 int mfma_padded_row(int l_max) {
     int off = 0;
     for (int l = 0; l <= l_max; ++l) off += 4 * ((2 * l + 4) / 4);
-    return off;
+    // row stride = 4 (mod 32) doubles: the 16 rows x 4 columns that one
+    // Gram-tile MFMA operand reads (and the 4 x 16 of the fold's stores) then
+    // fall on distinct LDS banks in the fewest passes, for 32 or 64 banks
+    return off + ((4 - off) % 32 + 32) % 32;
 }
 
 size_t mfma_lds_bytes(const MfmaDims& d) {
     const size_t W = static_cast<size_t>(d.S) * d.n;
     const size_t cw = (W + 1) * static_cast<size_t>(d.hpad);
-    size_t words = static_cast<size_t>(kNb) * (d.H + 1) + kNb + 64 + cw;
+    size_t words = static_cast<size_t>(kNb) * ((d.H + 1) | 1) + kNb + 64 + cw;
     if (d.mode == 1) words += cw;
     return words * sizeof(double) + static_cast<size_t>(d.L + 1 + 2 * (d.S + 1) + 1) * sizeof(int);
 }
