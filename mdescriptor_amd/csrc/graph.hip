@@ -11,12 +11,15 @@
 // neighbour species for SOAP, a stable partition of that order).
 //
 // Device pipeline (all on one stream):
-//   bin_count  -> scan -> bin_fill -> bin_sort   images into ROI cells
+//   bin_count -> scan -> bin_fill -> bin_sort   images into ROI cells, sorted
+//   cell_species                                 first bin of each species per cell
 //   centre_cell -> scan -> centre_fill           centres grouped by home cell
-//   pair_pass<count> -> totals -> scan           per-centre, per-species counts
-//   pair_pass<fill>                              wave ballot / mbcnt compaction
+//   neighbors<count> -> scan of totals           per-centre, per-species counts
+//   neighbors<fill>                              wave ballot compaction
 // Only cells within one cell of some centre (the region of interest) are
-// binned; the others are never visited.
+// binned; the others are never visited.  The neighbour passes run one
+// workgroup per home cell: its 27-cell candidate set is the same for every
+// centre of the cell, so it is staged in LDS once and scanned by all of them.
 #include "mdx_internal.h"
 
 #include <algorithm>
@@ -45,6 +48,20 @@ void DeviceBuffer::reserve(size_t size) {
     const size_t rounded = std::max<size_t>(256, (size + 255) & ~size_t(255));
     MDX_HIP(hipMalloc(&ptr, rounded));
     bytes = rounded;
+}
+
+// Compute units of the current device (queried once per process and device).
+int device_compute_units() {
+    static int cached[64] = {};
+    int dev = 0;
+    MDX_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int cus = 0;
+        MDX_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        cached[dev] = cus > 0 ? cus : 256;
+    }
+    return cached[dev];
 }
 
 void DeviceBuffer::release() {
@@ -254,7 +271,8 @@ __global__ void k_bin_sort(const StructGeom* geom, int64_t nstruct, const ImageD
 
 // Home ROI cell and structure of every atom (the centres).
 __global__ void k_centre_cell(const StructGeom* geom, int64_t nstruct, const double* positions, int64_t atoms,
-                              int64_t* centre_cell, int32_t* centre_struct, int32_t* error_flag) {
+                              int64_t* centre_cell, int32_t* centre_struct, int32_t* cell_ncentre,
+                              int32_t* centre_slot, int32_t* error_flag) {
     for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < atoms;
          i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
         int64_t s = find_by_begin(geom, nstruct, i, 2);
@@ -270,128 +288,272 @@ __global__ void k_centre_cell(const StructGeom* geom, int64_t nstruct, const dou
             continue;
         }
         centre_cell[i] = c;
+        centre_slot[i] = atomicAdd(&cell_ncentre[c], 1);
     }
 }
 
 // First bin of each species in each cell (Bins mode: cells are sorted by
 // species); species t of cell c spans [start[c*S + t], start[c*S + t + 1])
-// with the cell's end after the last species.
+// with the cell's end after the last species.  One thread per (cell, t):
+// a lower-bound search for t in the cell's sorted species column.
 __global__ void k_cell_species(const int64_t* cell_start, int64_t cells_total, const int32_t* btype, int S,
                                int64_t* cell_species_start) {
-    for (int64_t c = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; c < cells_total;
-         c += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        const int64_t begin = cell_start[c], end = cell_start[c + 1];
-        int64_t i = begin;
-        for (int t = 0; t < S; ++t) {
-            while (i < end && btype[i] < t) ++i;
-            cell_species_start[c * S + t] = i;
+    const int64_t work = cells_total * S;
+    for (int64_t w = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; w < work;
+         w += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t c = w / S;
+        const int t = static_cast<int>(w - c * S);
+        int64_t lo = cell_start[c], hi = cell_start[c + 1];
+        while (lo < hi) {
+            const int64_t mid = lo + (hi - lo) / 2;
+            if (btype[mid] < t) lo = mid + 1; else hi = mid;
         }
+        cell_species_start[w] = lo;
     }
 }
 
+// Centres of each ROI cell in one list: centre_slot (from k_centre_cell) is
+// the centre's place among its cell's centres.
+__global__ void k_centre_fill(const int64_t* centre_cell, const int32_t* centre_slot, int64_t atoms,
+                              const int64_t* cell_centre_start, int32_t* cell_centres) {
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < atoms;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t c = centre_cell[i];
+        if (c >= 0) cell_centres[cell_centre_start[c] + centre_slot[i]] = static_cast<int32_t>(i);
+    }
+}
 
-// Kernel 1: the neighbour rows of each centre, one wavefront per centre.
-// The 27 cells around the centre's home cell are visited in the reference's
-// order (z outer, y, x inner, cells outside the grid skipped;
+// Kernel 1: the neighbour rows of the centres of one home cell per
+// workgroup.  The 27 cells around the home cell are visited in the
+// reference's order (z outer, y, x inner, cells outside the grid skipped;
 // neighbor.cpp:558-566) and the binned images of a cell in extended order.
-// With several species the bins of a cell are sorted by species first and the
-// walk is repeated per species, so a centre's rows come out grouped by species
-// and, inside a species, in the reference's candidate order; with one species
-// they are exactly the reference's rows.  Count pass: per-species counts and
-// row totals.  Fill pass: the same walk writes the bin index of every accepted
-// image at pair_start[centre] onwards (wave ballot + popcount compaction).
-// A block holds four independent waves with a few hundred bytes of LDS each,
-// so many centres are in flight per SIMD to hide the gather latency.
+// With several species the bins of a cell are sorted by species first and
+// the walk is species-major (species, then the 27 cells), so a centre's rows
+// come out grouped by species and, inside a species, in the reference's
+// candidate order; with one species they are exactly the reference's rows.
+// That candidate sequence is the same for every centre of the cell: the
+// workgroup stages it in LDS (kStage candidates at a time) and each
+// wavefront scans it for one centre after another.  Count pass: per-species
+// counts and row totals.  Fill pass: the bin index of every accepted image at
+// pair_start[centre] onwards (wave ballot + popcount compaction).
+constexpr int kNbrThreads = 512;
+constexpr int kNbrWaves = kNbrThreads / kWave;
+constexpr int kStage = 1024;        // candidates staged in LDS per pass over a cell's centres
+constexpr int kCentreBatch = 128;   // centres whose running counts live in LDS at once
+constexpr int kSegments = kMaxSpecies * 27;
+constexpr int kNoBoundary = 0x7fffffff;
+
+__device__ inline uint64_t lane_range(int lo, int hi) {
+    // bits lo .. hi-1 of a 64-lane mask, 0 <= lo <= hi <= 64
+    const uint64_t upto_hi = hi >= 64 ? ~0ull : ((1ull << hi) - 1ull);
+    const uint64_t upto_lo = lo >= 64 ? ~0ull : ((1ull << lo) - 1ull);
+    return upto_hi & ~upto_lo;
+}
+
 template <bool kFill>
-__global__ __launch_bounds__(kBlock) void k_neighbors(
-    const StructGeom* geom, const double* positions, int64_t atoms, const int64_t* centre_cell,
-    const int32_t* centre_struct, const int64_t* cell_start, const int64_t* cell_species_start, const double* bx,
-    const double* by, const double* bz, int S, double cutoff2, int include_boundary, int32_t* counts,
-    int32_t* totals, const int64_t* pair_start, uint32_t* pair_bin) {
-    constexpr int kWaves = kBlock / kWave;
-    __shared__ int64_t s_start[kWaves][27];
-    __shared__ int32_t s_pre[kWaves][28];
-    const int lane = threadIdx.x % kWave;
-    const int wave = threadIdx.x / kWave;
+__global__ __launch_bounds__(kNbrThreads) void k_neighbors(
+    const StructGeom* geom, int64_t nstruct, const double* positions, int64_t cells_total,
+    const int64_t* cell_centre_start, const int32_t* cell_centres, const int64_t* cell_start,
+    const int64_t* cell_species_start, const double* bx, const double* by, const double* bz, int S,
+    double accept_max, int32_t* counts, int32_t* totals, const int64_t* pair_start, uint32_t* pair_bin) {
+    __shared__ double2 s_xy[kStage];          // candidate x, y
+    __shared__ double2 s_zb[kStage];          // candidate z, bin index (bit pattern)
+    __shared__ int64_t s_segstart[kSegments]; // first bin of segment (species, cell k)
+    __shared__ int32_t s_segpre[kSegments + 1];
+    __shared__ int32_t s_centre[kCentreBatch];
+    __shared__ double s_cpos[kCentreBatch * 3]; // centre positions of the batch
+    __shared__ int64_t s_first[kCentreBatch];   // first output row of each centre (fill pass)
+    __shared__ int32_t s_found[kCentreBatch];
+    // rows of a centre before species boundary t (count pass)
+    __shared__ int32_t s_bfound[kCentreBatch * kMaxSpecies];
+    const int tid = threadIdx.x;
+    const int lane = tid % kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-    for (int64_t centre = static_cast<int64_t>(blockIdx.x) * kWaves + wave; centre < atoms;
-         centre += static_cast<int64_t>(gridDim.x) * kWaves) {
-        const double px = positions[centre * 3 + 0];
-        const double py = positions[centre * 3 + 1];
-        const double pz = positions[centre * 3 + 2];
-        const int64_t home = centre_cell[centre];
-        int64_t cell = -1;
-        if (lane < 27 && home >= 0) {
-            const StructGeom& g = geom[centre_struct[centre]];
-            const int64_t local = home - g.cell_begin;
-            const int ix = g.roi_lo[0] + static_cast<int>(local % g.roi_dim[0]) + lane % 3 - 1;
-            const int iy = g.roi_lo[1] + static_cast<int>((local / g.roi_dim[0]) % g.roi_dim[1]) + (lane / 3) % 3 - 1;
+    const int nseg = S * 27;
+    for (int64_t c = blockIdx.x; c < cells_total; c += gridDim.x) {
+        const int64_t c0 = cell_centre_start[c], c1 = cell_centre_start[c + 1];
+        if (c0 == c1) continue;
+        int64_t sidx = 0;
+        {
+            int64_t lo = 0, hi = nstruct;
+            while (hi - lo > 1) {
+                const int64_t mid = (lo + hi) / 2;
+                if (geom[mid].cell_begin <= c) lo = mid; else hi = mid;
+            }
+            sidx = lo;
+            while (sidx + 1 < nstruct && geom[sidx + 1].cell_begin <= c) ++sidx;
+        }
+        const StructGeom& g = geom[sidx];
+        // segments in walk order: index sp * 27 + k, k = the z/y/x cell offset
+        for (int t = tid; t < nseg; t += kNbrThreads) {
+            const int sp = t / 27, k = t - sp * 27;
+            const int64_t local = c - g.cell_begin;
+            const int ix = g.roi_lo[0] + static_cast<int>(local % g.roi_dim[0]) + k % 3 - 1;
+            const int iy = g.roi_lo[1] + static_cast<int>((local / g.roi_dim[0]) % g.roi_dim[1]) + (k / 3) % 3 - 1;
             const int iz = g.roi_lo[2] + static_cast<int>(local / (static_cast<int64_t>(g.roi_dim[0]) * g.roi_dim[1]))
-                + lane / 9 - 1;
+                + k / 9 - 1;
+            int64_t start = 0, len = 0;
             if (ix >= 0 && iy >= 0 && iz >= 0 && ix < g.dims[0] && iy < g.dims[1] && iz < g.dims[2]) {
-                cell = g.cell_begin + (ix - g.roi_lo[0])
+                const int64_t nc = g.cell_begin + (ix - g.roi_lo[0])
                     + static_cast<int64_t>(g.roi_dim[0])
                         * ((iy - g.roi_lo[1]) + static_cast<int64_t>(g.roi_dim[1]) * (iz - g.roi_lo[2]));
+                start = S == 1 ? cell_start[nc] : cell_species_start[nc * S + sp];
+                const int64_t end = S == 1 || sp + 1 == S ? cell_start[nc + 1] : cell_species_start[nc * S + sp + 1];
+                len = end - start;
             }
+            s_segstart[t] = start;
+            s_segpre[t + 1] = static_cast<int32_t>(len);
         }
-        int64_t cursor = kFill ? pair_start[centre] : 0;
-        int32_t rows = 0;
-        for (int sp = 0; sp < S; ++sp) {
-            int64_t start = 0;
-            int32_t len = 0;
-            if (cell >= 0) {
-                start = S == 1 ? cell_start[cell] : cell_species_start[cell * S + sp];
-                const int64_t end = S == 1 || sp + 1 == S ? cell_start[cell + 1] : cell_species_start[cell * S + sp + 1];
-                len = static_cast<int32_t>(end - start);
-            }
-            int32_t incl = len;
+        __syncthreads();
+        if (wave == 0) {
+            // inclusive scan of the segment lengths, 64 at a time
+            int32_t carry = 0;
+            for (int t0 = 0; t0 < nseg; t0 += kWave) {
+                const int t = t0 + lane;
+                int32_t v = t < nseg ? s_segpre[t + 1] : 0;
 #pragma unroll
-            for (int off = 1; off < 32; off *= 2) {
-                const int32_t v = __shfl_up(incl, off, 32);
-                if ((lane & 31) >= off) incl += v;
-            }
-            const int32_t total = __shfl(incl, 26);
-            if (lane < 27) {
-                s_start[wave][lane] = start;
-                s_pre[wave][lane + 1] = incl;
-            }
-            if (lane == 0) s_pre[wave][0] = 0;
-            // hand-off inside one wavefront: its LDS operations complete in order
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            int32_t found = 0;
-            for (int32_t v0 = 0; v0 < total; v0 += kWave) {
-                const int32_t v = v0 + lane;
-                bool accept = false;
-                uint32_t b = 0;
-                if (v < total) {
-                    int lo = 0;
-#pragma unroll
-                    for (int step = 16; step > 0; step /= 2) {
-                        if (lo + step < 27 && s_pre[wave][lo + step] <= v) lo += step;
-                    }
-                    b = static_cast<uint32_t>(s_start[wave][lo] + (v - s_pre[wave][lo]));
-                    // displacement = image - centre; d^2 = (dx*dx + dy*dy) + dz*dz
-                    // (neighbor.cpp:569, math3.hpp:31-35), no contraction
-                    const double dx = bx[b] - px;
-                    const double dy = by[b] - py;
-                    const double dz = bz[b] - pz;
-                    const double d2 = dx * dx + dy * dy + dz * dz;
-                    accept = include_boundary ? d2 <= cutoff2 : d2 < cutoff2;
+                for (int off = 1; off < kWave; off *= 2) {
+                    const int32_t u = __shfl_up(v, off);
+                    if (lane >= off) v += u;
                 }
-                const uint64_t mask = __ballot(accept);
-                if (kFill && accept) pair_bin[cursor + found + __popcll(mask & below)] = b;
-                found += static_cast<int32_t>(__popcll(mask));
+                if (t < nseg) s_segpre[t + 1] = carry + v;
+                carry += __shfl(v, kWave - 1);
             }
-            if (!kFill && lane == 0) counts[centre * S + sp] = found;
-            cursor += found;
-            rows += found;
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (lane == 0) s_segpre[0] = 0;
         }
-        if (!kFill && lane == 0) totals[centre] = rows;
+        __syncthreads();
+        const int total = s_segpre[nseg];
+        for (int64_t b0 = c0; b0 < c1; b0 += kCentreBatch) {
+            const int nb = static_cast<int>(min<int64_t>(kCentreBatch, c1 - b0));
+            for (int i = tid; i < nb; i += kNbrThreads) {
+                const int32_t centre = cell_centres[b0 + i];
+                s_centre[i] = centre;
+                s_cpos[i * 3 + 0] = positions[static_cast<int64_t>(centre) * 3 + 0];
+                s_cpos[i * 3 + 1] = positions[static_cast<int64_t>(centre) * 3 + 1];
+                s_cpos[i * 3 + 2] = positions[static_cast<int64_t>(centre) * 3 + 2];
+                s_first[i] = kFill ? pair_start[centre] : 0;
+                s_found[i] = 0;
+            }
+            for (int i = tid; i < nb * S; i += kNbrThreads) s_bfound[i] = 0;
+            __syncthreads();
+            for (int v0 = 0; v0 < total; v0 += kStage) {
+                const int len = min(kStage, total - v0);
+                const int glen = (len + kWave - 1) / kWave * kWave;
+                // each thread stages up to kStage / kNbrThreads candidates, all
+                // bin lookups first so that their global loads are in flight together
+                constexpr int kPer = kStage / kNbrThreads;
+                int64_t bins[kPer];
+#pragma unroll
+                for (int r = 0; r < kPer; ++r) {
+                    const int i = tid + r * kNbrThreads;
+                    const int v = v0 + min(i, len - 1);
+                    // last segment starting at or before v (empty segments repeat a start)
+                    int lo = 0, hi = nseg;
+                    while (hi - lo > 1) {
+                        const int mid = (lo + hi) / 2;
+                        if (s_segpre[mid] <= v) lo = mid; else hi = mid;
+                    }
+                    bins[r] = s_segstart[lo] + (v - s_segpre[lo]);
+                }
+                double cx[kPer], cy[kPer], cz[kPer];
+#pragma unroll
+                for (int r = 0; r < kPer; ++r) {
+                    cx[r] = bx[bins[r]];
+                    cy[r] = by[bins[r]];
+                    cz[r] = bz[bins[r]];
+                }
+#pragma unroll
+                for (int r = 0; r < kPer; ++r) {
+                    const int i = tid + r * kNbrThreads;
+                    if (i < len) {
+                        s_xy[i] = make_double2(cx[r], cy[r]);
+                        s_zb[i] = make_double2(cz[r], __longlong_as_double(bins[r]));
+                    } else if (i < glen) {
+                        // pad to whole wavefronts with candidates at infinity (d^2 = inf)
+                        s_xy[i] = make_double2(__builtin_huge_val(), 0.0);
+                        s_zb[i] = make_double2(0.0, 0.0);
+                    }
+                }
+                __syncthreads();
+                for (int ci = wave; ci < nb; ci += kNbrWaves) {
+                    const double px = s_cpos[ci * 3 + 0];
+                    const double py = s_cpos[ci * 3 + 1];
+                    const double pz = s_cpos[ci * 3 + 2];
+                    int32_t found = s_found[ci];
+                    const int64_t first_row = s_first[ci];
+                    // next species boundary of the walk at or after v0 (count pass)
+                    int t_next = 1;
+                    int bnext = kNoBoundary;
+                    if (!kFill) {
+                        while (t_next < S && __builtin_amdgcn_readfirstlane(s_segpre[t_next * 27]) < v0) ++t_next;
+                        bnext = t_next < S ? __builtin_amdgcn_readfirstlane(s_segpre[t_next * 27]) : kNoBoundary;
+                    }
+                    // bookkeeping of one wavefront-wide group of candidates at i0
+                    auto account = [&](int i0, bool accept, uint64_t mask, uint32_t b) {
+                        if (kFill) {
+                            if (accept) pair_bin[first_row + found + __popcll(mask & below)] = b;
+                        } else {
+                            while (bnext < v0 + i0 + kWave) {
+                                // rows before the boundary: earlier groups plus this group's lanes below it
+                                const int k = bnext - (v0 + i0);
+                                if (lane == 0) {
+                                    s_bfound[ci * S + t_next] =
+                                        found + static_cast<int32_t>(__popcll(mask & lane_range(0, k)));
+                                }
+                                ++t_next;
+                                bnext = t_next < S ? __builtin_amdgcn_readfirstlane(s_segpre[t_next * 27]) : kNoBoundary;
+                            }
+                        }
+                        found += static_cast<int32_t>(__popcll(mask));
+                    };
+                    // displacement = image - centre; d^2 = (dx*dx + dy*dy) + dz*dz
+                    // (neighbor.cpp:569, math3.hpp:31-35), no contraction; accepted
+                    // when d^2 <= accept_max (the host folds the boundary rule into it)
+                    auto test = [&](int i, bool& accept, uint32_t& b) {
+                        const double2 xy = s_xy[i];
+                        const double2 zb = s_zb[i];
+                        const double dx = xy.x - px;
+                        const double dy = xy.y - py;
+                        const double dz = zb.x - pz;
+                        const double d2 = dx * dx + dy * dy + dz * dz;
+                        accept = d2 <= accept_max;
+                        b = static_cast<uint32_t>(__double_as_longlong(zb.y));
+                    };
+                    int i0 = 0;
+                    for (; i0 + 2 * kWave <= glen; i0 += 2 * kWave) {
+                        bool a0, a1;
+                        uint32_t b0, b1;
+                        test(i0 + lane, a0, b0);
+                        test(i0 + kWave + lane, a1, b1);
+                        const uint64_t m0 = __ballot(a0);
+                        const uint64_t m1 = __ballot(a1);
+                        account(i0, a0, m0, b0);
+                        account(i0 + kWave, a1, m1, b1);
+                    }
+                    if (i0 < glen) {
+                        bool a0;
+                        uint32_t b0;
+                        test(i0 + lane, a0, b0);
+                        account(i0, a0, __ballot(a0), b0);
+                    }
+                    if (lane == 0) s_found[ci] = found;
+                }
+                __syncthreads();
+            }
+            if (!kFill) {
+                for (int i = tid; i < nb; i += kNbrThreads) totals[s_centre[i]] = s_found[i];
+                for (int i = tid; i < nb * S; i += kNbrThreads) {
+                    const int ci = i / S, t = i - ci * S;
+                    // rows before boundaries t and t + 1 (boundary 0 is the start; a
+                    // boundary at or past the end of the walk is the centre's total)
+                    const int32_t lo = t == 0 ? 0 : s_segpre[t * 27] >= total ? s_found[ci] : s_bfound[i];
+                    const int32_t hi = t + 1 == S || s_segpre[(t + 1) * 27] >= total ? s_found[ci] : s_bfound[i + 1];
+                    counts[static_cast<int64_t>(s_centre[ci]) * S + t] = hi - lo;
+                }
+            }
+            __syncthreads();
+        }
     }
 }
 
@@ -681,6 +843,10 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
                                   sizeof(int64_t));
     gr.centre_cell.reserve(static_cast<size_t>(atoms) * sizeof(int64_t));
     gr.centre_struct.reserve(static_cast<size_t>(atoms) * sizeof(int32_t));
+    gr.centre_slot.reserve(static_cast<size_t>(atoms) * sizeof(int32_t));
+    gr.cell_centres.reserve(static_cast<size_t>(atoms) * sizeof(int32_t));
+    gr.cell_ncentre.reserve(cells1 * sizeof(int32_t));
+    gr.cell_centre_start.reserve(cells1 * sizeof(int64_t));
     gr.bin_key.reserve(static_cast<size_t>(ext) * sizeof(uint64_t));
     gr.bin_x.reserve(static_cast<size_t>(ext) * sizeof(double));
     gr.bin_y.reserve(static_cast<size_t>(ext) * sizeof(double));
@@ -694,6 +860,7 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     MDX_HIP(hipMemsetAsync(gr.error_flag.ptr, 0, sizeof(int32_t), stream));
     MDX_HIP(hipMemsetAsync(gr.cell_count.ptr, 0, cells1 * sizeof(int32_t), stream));
     MDX_HIP(hipMemsetAsync(gr.cell_fill.ptr, 0, cells1 * sizeof(int32_t), stream));
+    MDX_HIP(hipMemsetAsync(gr.cell_ncentre.ptr, 0, cells1 * sizeof(int32_t), stream));
 
     // bin every periodic image into its ROI cell, sorted by (species, extended index)
     hipLaunchKernelGGL(k_bin_count, dim3(grid_for(ext)), dim3(kBlock), 0, stream, geom, nstruct, images, pos, ext,
@@ -708,21 +875,31 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
                        gr.bin_x.as<double>(), gr.bin_y.as<double>(), gr.bin_z.as<double>(), gr.bin_atom.as<int32_t>(),
                        gr.bin_image.as<int32_t>(), gr.bin_type.as<int32_t>());
     if (S > 1) {
-        hipLaunchKernelGGL(k_cell_species, dim3(grid_for(cells)), dim3(kBlock), 0, stream, gr.cell_start.as<int64_t>(),
-                           cells, gr.bin_type.as<int32_t>(), S, gr.cell_species_start.as<int64_t>());
+        hipLaunchKernelGGL(k_cell_species, dim3(grid_for(cells * S)), dim3(kBlock), 0, stream,
+                           gr.cell_start.as<int64_t>(), cells, gr.bin_type.as<int32_t>(), S,
+                           gr.cell_species_start.as<int64_t>());
     }
+    // centres grouped by home cell
     hipLaunchKernelGGL(k_centre_cell, dim3(grid_for(atoms)), dim3(kBlock), 0, stream, geom, nstruct, pos, atoms,
-                       gr.centre_cell.as<int64_t>(), gr.centre_struct.as<int32_t>(), gr.error_flag.as<int32_t>());
+                       gr.centre_cell.as<int64_t>(), gr.centre_struct.as<int32_t>(), gr.cell_ncentre.as<int32_t>(),
+                       gr.centre_slot.as<int32_t>(), gr.error_flag.as<int32_t>());
+    scan_counts(stream, gr.cell_ncentre.as<int32_t>(), gr.cell_centre_start.as<int64_t>(), cells, gr.scan_tmp);
+    hipLaunchKernelGGL(k_centre_fill, dim3(grid_for(atoms)), dim3(kBlock), 0, stream, gr.centre_cell.as<int64_t>(),
+                       gr.centre_slot.as<int32_t>(), atoms, gr.cell_centre_start.as<int64_t>(),
+                       gr.cell_centres.as<int32_t>());
     MDX_HIP(hipGetLastError());
     if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
 
+    // d^2 < c^2 is d^2 <= the largest double below c^2
     const double cutoff2 = pb.cutoff * pb.cutoff;
-    const unsigned centre_grid = static_cast<unsigned>(std::min<int64_t>((atoms + 3) / 4, 1 << 20));
-    hipLaunchKernelGGL(k_neighbors<false>, dim3(centre_grid), dim3(kBlock), 0, stream, geom, pos, atoms,
-                       gr.centre_cell.as<int64_t>(), gr.centre_struct.as<int32_t>(), gr.cell_start.as<int64_t>(),
-                       gr.cell_species_start.as<int64_t>(), gr.bin_x.as<double>(), gr.bin_y.as<double>(),
-                       gr.bin_z.as<double>(), S, cutoff2, pb.include_boundary, gr.counts.as<int32_t>(),
-                       gr.totals.as<int32_t>(), static_cast<const int64_t*>(nullptr), static_cast<uint32_t*>(nullptr));
+    const double accept_max = pb.include_boundary ? cutoff2 : std::nextafter(cutoff2, 0.0);
+    const unsigned cell_blocks = static_cast<unsigned>(std::min<int64_t>(cells, 1 << 20));
+    hipLaunchKernelGGL(k_neighbors<false>, dim3(cell_blocks), dim3(kNbrThreads), 0, stream, geom, nstruct, pos,
+                       cells, gr.cell_centre_start.as<int64_t>(), gr.cell_centres.as<int32_t>(),
+                       gr.cell_start.as<int64_t>(), gr.cell_species_start.as<int64_t>(), gr.bin_x.as<double>(),
+                       gr.bin_y.as<double>(), gr.bin_z.as<double>(), S, accept_max,
+                       gr.counts.as<int32_t>(), gr.totals.as<int32_t>(), static_cast<const int64_t*>(nullptr),
+                       static_cast<uint32_t*>(nullptr));
     scan_counts(stream, gr.totals.as<int32_t>(), gr.pair_start.as<int64_t>(), atoms, gr.scan_tmp);
     MDX_HIP(hipGetLastError());
     int64_t pairs = 0;
@@ -738,11 +915,12 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
     if (pairs >= (int64_t(1) << 40)) throw Error(MDX_INTERNAL, "implausible neighbour pair count");
     gr.pair_bin.reserve(std::max<size_t>(1, static_cast<size_t>(pairs) * sizeof(uint32_t)));
-    hipLaunchKernelGGL(k_neighbors<true>, dim3(centre_grid), dim3(kBlock), 0, stream, geom, pos, atoms,
-                       gr.centre_cell.as<int64_t>(), gr.centre_struct.as<int32_t>(), gr.cell_start.as<int64_t>(),
-                       gr.cell_species_start.as<int64_t>(), gr.bin_x.as<double>(), gr.bin_y.as<double>(),
-                       gr.bin_z.as<double>(), S, cutoff2, pb.include_boundary, static_cast<int32_t*>(nullptr),
-                       static_cast<int32_t*>(nullptr), gr.pair_start.as<int64_t>(), gr.pair_bin.as<uint32_t>());
+    hipLaunchKernelGGL(k_neighbors<true>, dim3(cell_blocks), dim3(kNbrThreads), 0, stream, geom, nstruct, pos,
+                       cells, gr.cell_centre_start.as<int64_t>(), gr.cell_centres.as<int32_t>(),
+                       gr.cell_start.as<int64_t>(), gr.cell_species_start.as<int64_t>(), gr.bin_x.as<double>(),
+                       gr.bin_y.as<double>(), gr.bin_z.as<double>(), S, accept_max,
+                       static_cast<int32_t*>(nullptr), static_cast<int32_t*>(nullptr), gr.pair_start.as<int64_t>(),
+                       gr.pair_bin.as<uint32_t>());
     MDX_HIP(hipGetLastError());
     gr.pairs = pairs;
     gr.binned = binned;

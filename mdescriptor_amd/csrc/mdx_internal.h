@@ -23,7 +23,6 @@ constexpr int kMaxNmax = 16;      // radial channels per (species, l)
 constexpr int kMaxLmax = 20;      // as the reference's parameter check (soap.cpp:1153-1154)
 constexpr int kBlock = 256;       // threads per workgroup of the graph and SOAP kernels
 constexpr int kWave = 64;         // CDNA wavefront width
-constexpr int kChunk = 1024;      // candidates staged in LDS per graph chunk
 
 // Error carrying one of the C-ABI status codes; thrown inside the library and
 // converted to a status at the extern "C" boundary.
@@ -113,6 +112,10 @@ struct DeviceGraph {
     DeviceBuffer bin_image;                         // i32 global image index
     DeviceBuffer bin_type;                          // i32 species index
     DeviceBuffer centre_cell;                       // i64 home ROI cell per atom
+    DeviceBuffer centre_slot;                       // i32 place of the atom among its cell's centres
+    DeviceBuffer cell_ncentre;                      // i32[cells + 1] centres per ROI cell
+    DeviceBuffer cell_centre_start;                 // i64[cells + 1] first entry of a cell in cell_centres
+    DeviceBuffer cell_centres;                      // i32[atoms] centres grouped by home cell
     DeviceBuffer counts;     // i32[atoms * n_species]
     DeviceBuffer totals;     // i32[atoms]
     DeviceBuffer pair_start; // i64[atoms + 1]
@@ -125,6 +128,9 @@ struct DeviceGraph {
 // Returns the pair count.  Polls cancel between launches.
 int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& graph,
                     const volatile int32_t* cancel);
+
+// Compute units of the current device (queried once per process and device).
+int device_compute_units();
 
 // Exclusive scan of n int32 counts into n+1 int64 offsets (out[n] = total).
 void scan_counts(hipStream_t stream, const int32_t* in, int64_t* out, int64_t n, DeviceBuffer& tmp);

@@ -532,20 +532,6 @@ void launch(hipStream_t stream, unsigned grid, int64_t per_block, size_t lds, co
                        count, per_block, out, pitch, partial);
 }
 
-// Compute units of the current device (queried once per process and device).
-int device_compute_units() {
-    static int cached[64] = {};
-    int dev = 0;
-    MDX_HIP(hipGetDevice(&dev));
-    if (dev < 0 || dev >= 64) return 256;
-    if (cached[dev] == 0) {
-        int cus = 0;
-        MDX_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-        cached[dev] = cus > 0 ? cus : 256;
-    }
-    return cached[dev];
-}
-
 } // namespace
 
 MfmaPlanHost plan_mfma_tables(int S, int n, int l_max, const std::vector<double>& beta_scaled,
