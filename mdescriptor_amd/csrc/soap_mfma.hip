@@ -44,6 +44,13 @@ typedef double d4 __attribute__((ext_vector_type(4)));
 constexpr int kNb = 32;        // neighbours staged per chunk (8 MFMA steps)
 constexpr int kWaveThreads = 64;
 
+// 64-bit value of lane `src` (a compile-time lane) in scalar registers.
+__device__ inline int64_t lane_value(int64_t v, int src) {
+    const int lo = __builtin_amdgcn_readlane(static_cast<int>(v), src);
+    const int hi = __builtin_amdgcn_readlane(static_cast<int>(v >> 32), src);
+    return static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | static_cast<uint32_t>(lo));
+}
+
 __device__ inline d4 mfma(double a, double b, d4 c) {
     return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
 }
@@ -144,13 +151,20 @@ __device__ inline void store_out(void* out, int64_t pitch, int64_t row, int64_t 
     }
 }
 
+// i / n for 0 <= i < 256, 1 <= n <= 16 without an integer division:
+// (i + 1/2) / n sits at least 1/32 away from an integer, far beyond the
+// float rounding of the product.
+__device__ inline int div_small(int i, float inv_n) {
+    return static_cast<int>((static_cast<float>(i) + 0.5f) * inv_n);
+}
+
 // Feature index of channel pair (i, j), i <= j, at l = 0, and its stride
 // per degree l, in the layout of soap.cpp:997-1013: species pairs t1 <= t2 in
 // order, each a block of L x (n(n+1)/2) (t1 == t2, n2 >= n1) or L x n^2
 // values ordered l, n1, n2.  Channel i is species i / n, radial i % n.
-__device__ inline int feature_index(int i, int j, int S, int n, int L, int& stride) {
-    const int t1 = i / n, n1 = i - t1 * n;
-    const int t2 = j / n, n2 = j - t2 * n;
+__device__ inline int feature_index(int i, int j, int S, int n, float inv_n, int L, int& stride) {
+    const int t1 = div_small(i, inv_n), n1 = i - t1 * n;
+    const int t2 = div_small(j, inv_n), n2 = j - t2 * n;
     const int same = n * (n + 1) / 2, cross = n * n;
     // blocks of the species rows a < t1, then (t1, t1 .. t2-1)
     int before = t1 * same + cross * (t1 * (S - 1) - t1 * (t1 - 1) / 2);
@@ -168,10 +182,10 @@ __device__ inline int feature_index(int i, int j, int S, int n, int L, int& stri
 
 // Power spectrum of the coefficients in LDS on 16x16 Gram tiles.  s_c holds
 // W + 1 rows of d.hpad values (row W and every pad entry are zero), entry
-// (row, l, m') at row*hpad + loff[l] + m'.  The units (tile pair, l) are
-// split into contiguous ranges over the `waves` wavefronts of the workgroup
-// (wavefront `wave` takes its range); units write disjoint features, and a
-// given feature always comes from the same wavefront.
+// (row, l, m') at row*hpad + loff[l] + m'.  The units (tile pair, l), pair-
+// major, are split into contiguous ranges over the `waves` wavefronts of the
+// workgroup (wavefront `wave` takes its range); units write disjoint
+// features, and a given feature always comes from the same wavefront.
 // mode 0: write row `row` of out; mode 2: add into the partial row `acc`;
 // mode 3: store into `acc` (the first centre of a run).
 __device__ void power_spectrum_tiles(const double* s_c, const int* loff, const MfmaDims& d,
@@ -182,25 +196,29 @@ __device__ void power_spectrum_tiles(const double* s_c, const int* loff, const M
     const int RT = (W + 15) / 16;
     const int L = d.L;
     const int hp = d.hpad;
+    const float inv_n = 1.0f / static_cast<float>(d.n);
     const int units = RT * (RT + 1) / 2 * L;
     const int u_begin = wave * units / waves;
     const int u_end = (wave + 1) * units / waves;
+    if (u_begin >= u_end) return;
     char* out_row = static_cast<char*>(out) + row * pitch;
-    int pair = -1;
+    // first unit of the range: pair p = (bi, bj), bi <= bj, row-major over the
+    // upper triangle of tile pairs, and degree l; later units step l, then bj, then bi
+    int p = u_begin / L;
+    int l = u_begin - p * L;
+    int bi = 0;
+    while (p >= RT - bi) {
+        p -= RT - bi;
+        ++bi;
+    }
+    int bj = bi + p;
     const double* arow = s_c;
     const double* brow = s_c;
     int fb[4] = {-1, -1, -1, -1}, fs[4] = {0, 0, 0, 0};
+    bool new_pair = true;
     for (int u = u_begin; u < u_end; ++u) {
-        const int p = u / L;
-        const int l = u - p * L;
-        if (p != pair) {
-            pair = p;
-            int bi = 0, rest = p;
-            while (rest >= RT - bi) {
-                rest -= RT - bi;
-                ++bi;
-            }
-            const int bj = bi + rest;
+        if (new_pair) {
+            new_pair = false;
             const int ia = min(16 * bi + lane % 16, W);
             const int jb = min(16 * bj + lane % 16, W);
             arow = s_c + ia * hp + lane / 16;
@@ -211,7 +229,7 @@ __device__ void power_spectrum_tiles(const double* s_c, const int* loff, const M
                 const int i = 16 * bi + lane / 16 + 4 * r;
                 const bool ok = i < W && j < W && i <= j;
                 fs[r] = 0;
-                fb[r] = ok ? feature_index(i, j, d.S, d.n, d.L, fs[r]) : -1;
+                fb[r] = ok ? feature_index(i, j, d.S, d.n, inv_n, d.L, fs[r]) : -1;
             }
         }
         const int steps = (2 * l + 4) / 4;
@@ -233,6 +251,14 @@ __device__ void power_spectrum_tiles(const double* s_c, const int* loff, const M
                 } else {
                     reinterpret_cast<double*>(out_row)[f] = v;
                 }
+            }
+        }
+        if (++l == L) {
+            l = 0;
+            new_pair = true;
+            if (++bj == RT) {
+                ++bi;
+                bj = bi;
             }
         }
     }
@@ -310,6 +336,24 @@ __global__ __launch_bounds__(T * kWaveThreads, 4) void k_soap_mfma(
 
     const int64_t item_first = item_base + static_cast<int64_t>(blockIdx.x) * per_block;
     const int64_t item_last = min(item_first + per_block, item_base + items);
+    // centres of this workgroup: [first of item_first, end of item_last - 1)
+    const int64_t range_end = item_first >= item_last ? 0 : item_begin ? item_begin[item_last] : item_last;
+    // The per-centre metadata (species counts, first row, position) of the
+    // next centre is loaded one centre ahead into registers with vector loads:
+    // lane q < S holds count q, lanes 0-2 the position bits, lane 3 the first row.
+    int pre_count = 0;
+    int64_t pre_bits = 0;
+    auto prefetch_centre = [&](int64_t c) {
+        if (c < range_end) {
+            if (lane < S) pre_count = counts[c * S + lane];
+            if (lane < 3) {
+                pre_bits = __double_as_longlong(positions[c * 3 + lane]);
+            } else if (lane == 3) {
+                pre_bits = pair_start[c];
+            }
+        }
+    };
+    if (item_first < item_last) prefetch_centre(item_begin ? item_begin[item_first] : item_first);
     for (int64_t item = item_first; item < item_last; ++item) {
         const int64_t first = item_begin ? item_begin[item] : item;
         const int64_t last = item_begin ? item_begin[item + 1] : item + 1;
@@ -318,25 +362,37 @@ __global__ __launch_bounds__(T * kWaveThreads, 4) void k_soap_mfma(
             for (int i = tid; i < cw; i += kThreads) s_csum[i] = 0.0;
         }
         for (int64_t centre = first; centre < last; ++centre) {
-            const double cx = positions[centre * 3 + 0];
-            const double cy = positions[centre * 3 + 1];
-            const double cz = positions[centre * 3 + 2];
-            const int64_t centre_pairs = pair_start[centre];
+            // scalar copies (readlane): these stay live across the whole centre
+            const double cx = __longlong_as_double(lane_value(pre_bits, 0));
+            const double cy = __longlong_as_double(lane_value(pre_bits, 1));
+            const double cz = __longlong_as_double(lane_value(pre_bits, 2));
+            const int64_t centre_pairs = lane_value(pre_bits, 3);
             // species segments of this centre's rows (kernel 1 groups them by
             // species) and their slots: each segment is padded to a multiple of
             // 4 slots, so one MFMA step (4 slots) never mixes species while a
-            // chunk of kNb slots may span several segments
-            if (tid == 0) {
-                int rows = 0, slots = 0;
-                for (int q = 0; q < S; ++q) {
-                    const int c = counts[centre * S + q];
-                    s_seg[q] = rows;
-                    s_pseg[q] = slots;
-                    rows += c;
-                    slots += (c + 3) & ~3;
+            // chunk of kNb slots may span several segments.  Exclusive prefix
+            // sums over lanes q < S.
+            {
+                int rows = lane < S ? pre_count : 0;
+                int pad = (rows + 3) & ~3;
+#pragma unroll
+                for (int off = 1; off < kMaxSpecies; off *= 2) {
+                    const int r_up = __shfl_up(rows, off, kMaxSpecies);
+                    const int p_up = __shfl_up(pad, off, kMaxSpecies);
+                    if ((lane % kMaxSpecies) >= off) {
+                        rows += r_up;
+                        pad += p_up;
+                    }
                 }
-                s_seg[S] = rows;
-                s_pseg[S] = slots;
+                if (wave == 0 && lane < S) {
+                    // inclusive sums: entry q + 1
+                    s_seg[lane + 1] = rows;
+                    s_pseg[lane + 1] = pad;
+                    if (lane == 0) {
+                        s_seg[0] = 0;
+                        s_pseg[0] = 0;
+                    }
+                }
             }
             __syncthreads();
             // an empty species leaves its coefficients at zero
@@ -414,7 +470,11 @@ __global__ __launch_bounds__(T * kWaveThreads, 4) void k_soap_mfma(
                     int lm = d.l_max, zero = 0;
                     uint32_t mk = hmask;
                     asm volatile("" : "+s"(lm), "+s"(mk), "+s"(zero));
-                    harmonics_q(dx, dy, dz, prow >= 0, lm, mk, comp, &kHarmonic + zero, s_y + jj * HP);
+                    // likewise the lane's component, so that the per-column LDS
+                    // addresses derived from it are not held across the loop
+                    int part = comp;
+                    asm volatile("" : "+v"(part));
+                    harmonics_q(dx, dy, dz, prow >= 0, lm, mk, part, &kHarmonic + zero, s_y + jj * HP);
                 }
                 __syncthreads();
                 {
@@ -458,6 +518,8 @@ __global__ __launch_bounds__(T * kWaveThreads, 4) void k_soap_mfma(
                 __syncthreads();
             }
             if (has_tile && cur >= 0) fold(cur);
+            // the next centre's metadata arrives while this one's power spectrum runs
+            prefetch_centre(centre + 1);
             __syncthreads();
             if (d.mode == 0) {
                 power_spectrum_tiles(s_c, s_loff, d, ps_pref, 0, out, pitch, centre, nullptr, wave, T);
