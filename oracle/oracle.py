@@ -44,6 +44,81 @@ class _Graph(ctypes.Structure):
     ]
 
 
+class _Options(ctypes.Structure):
+    """mdxo_soap_options / mdxr_soap_options (the SoapOptions fields beyond
+    the GTO, uncompressed, unweighted default; descriptor.hpp:17-43)."""
+
+    _fields_ = [
+        ("weighting_function", ctypes.c_int32),
+        ("weighting_has_w0", ctypes.c_int32),
+        ("weighting_r0", ctypes.c_double),
+        ("weighting_c", ctypes.c_double),
+        ("weighting_d", ctypes.c_double),
+        ("weighting_m", ctypes.c_double),
+        ("weighting_w0", ctypes.c_double),
+        ("species_weights", _f64p),
+        ("compression", ctypes.c_int32),
+        ("radial_basis", ctypes.c_int32),
+        ("grid_size", ctypes.c_int32),
+        ("radial_grid", _f64p),
+        ("radial_weights", _f64p),
+        ("radial_values", _f64p),
+    ]
+
+
+_COMPRESSION = {"off": 0, "mu2": 1, "mu1nu1": 2, "crossover": 3}
+_WEIGHTING = {"poly": 1, "pow": 2, "exp": 3}
+
+
+def feature_count(S: int, n: int, l_max: int, compression: str = "off") -> int:
+    """soap_features (soap.cpp:373-387)."""
+
+    L = l_max + 1
+    if compression == "mu2":
+        return n * (n + 1) // 2 * L
+    if compression == "mu1nu1":
+        return S * n * n * L
+    if compression == "crossover":
+        return S * n * (n + 1) // 2 * L
+    w = S * n
+    return w * (w + 1) // 2 * L
+
+
+def _options(options: dict | None, S: int, keep: list) -> Any:
+    """A ctypes options struct (or None) from
+    {"weighting": {...}, "species_weights": [...], "compression": str,
+     "polynomial": (grid, weights, values)}; `keep` holds the arrays alive."""
+
+    if not options:
+        return None
+    o = _Options()
+    weighting = dict(options.get("weighting") or {})
+    if "function" in weighting:
+        o.weighting_function = _WEIGHTING[weighting["function"]]
+    o.weighting_has_w0 = 1 if "w0" in weighting else 0
+    o.weighting_r0 = float(weighting.get("r0", 1.0))
+    o.weighting_c = float(weighting.get("c", 1.0))
+    o.weighting_d = float(weighting.get("d", 0.0))
+    o.weighting_m = float(weighting.get("m", 1.0))
+    o.weighting_w0 = float(weighting.get("w0", 1.0))
+    if options.get("species_weights") is not None:
+        sw = np.ascontiguousarray(options["species_weights"], dtype=np.float64)
+        if sw.shape != (S,):
+            raise ValueError("species_weights needs one value per species")
+        keep.append(sw)
+        o.species_weights = _ptr(sw, _f64p)
+    o.compression = _COMPRESSION[options.get("compression", "off")]
+    if options.get("polynomial") is not None:
+        grid, weights, values = (np.ascontiguousarray(a, dtype=np.float64) for a in options["polynomial"])
+        keep.extend([grid, weights, values])
+        o.radial_basis = 1
+        o.grid_size = len(grid)
+        o.radial_grid = _ptr(grid, _f64p)
+        o.radial_weights = _ptr(weights, _f64p)
+        o.radial_values = _ptr(values.ravel(), _f64p)
+    return ctypes.pointer(o)
+
+
 _loaded: dict[str, Any] = {}
 
 
@@ -79,7 +154,7 @@ def _load(kind: str) -> Any:
         lib.mdxo_soap.argtypes = [
             _i32p, _f64p, _f64p, _i32p, _i64p, ctypes.c_int64, ctypes.c_int64,
             _i32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_double, ctypes.c_double,
-            _f64p, _f64p, ctypes.c_int, ctypes.c_int, ctypes.c_int, _f64p,
+            _f64p, _f64p, ctypes.POINTER(_Options), ctypes.c_int, ctypes.c_int, ctypes.c_int, _f64p,
             ctypes.POINTER(ctypes.c_int32), ctypes.c_char_p, ctypes.c_int,
         ]
         lib.mdxo_solid_harmonics.restype = None
@@ -100,7 +175,8 @@ def _load(kind: str) -> Any:
         lib.mdxr_soap.argtypes = [
             _i32p, _f64p, _f64p, _i32p, _i64p, ctypes.c_int64, ctypes.c_int64,
             _i32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_double, ctypes.c_double,
-            _f64p, _f64p, ctypes.c_int, ctypes.c_int, _f64p, ctypes.c_char_p, ctypes.c_int,
+            _f64p, _f64p, ctypes.POINTER(_Options), ctypes.c_int, ctypes.c_int, _f64p, ctypes.c_char_p,
+            ctypes.c_int,
         ]
     _loaded[kind] = lib
     return lib
@@ -164,20 +240,25 @@ _AVERAGE = {"off": 0, "inner": 1, "outer": 2}
 
 
 def soap(batch: Any, *, species: Any, n_max: int, l_max: int, r_cut: float, sigma: float,
-         alphas: np.ndarray, betas: np.ndarray, average: str = "off", num_threads: int = 0,
-         decomposition: int = 0, kind: str = "oracle", cancel: Any = None) -> np.ndarray:
-    """SOAP features (float64, rows x features) from the oracle or the reference."""
+         alphas: np.ndarray | None = None, betas: np.ndarray | None = None, average: str = "off",
+         num_threads: int = 0, decomposition: int = 0, kind: str = "oracle", cancel: Any = None,
+         options: dict | None = None) -> np.ndarray:
+    """SOAP features (float64, rows x features) from the oracle or the reference.
+
+    ``options`` (see ``_options``) selects weighting, species weights,
+    compression and the polynomial basis; None is the GTO default."""
 
     lib = _load(kind)
     if lib is None:
         raise FileNotFoundError("reference harness is not built")
     numbers, positions, cells, pbc, offsets = _batch_arrays(batch)
     species_arr = np.ascontiguousarray(species, dtype=np.int32)
-    alphas = np.ascontiguousarray(alphas, dtype=np.float64).ravel()
-    betas = np.ascontiguousarray(betas, dtype=np.float64).ravel()
+    alphas = np.ascontiguousarray(alphas if alphas is not None else np.zeros(1), dtype=np.float64).ravel()
+    betas = np.ascontiguousarray(betas if betas is not None else np.zeros(1), dtype=np.float64).ravel()
     S = len(species_arr)
-    w = S * n_max
-    features = w * (w + 1) // 2 * (l_max + 1)
+    keep: list = []
+    opt = _options(options, S, keep)
+    features = feature_count(S, n_max, l_max, (options or {}).get("compression", "off"))
     structures = len(offsets) - 1
     rows = structures if average in ("inner", "outer") else len(numbers)
     output = np.zeros((rows, features), dtype=np.float64)
@@ -186,7 +267,7 @@ def soap(batch: Any, *, species: Any, n_max: int, l_max: int, r_cut: float, sigm
         _ptr(numbers, _i32p), _ptr(positions, _f64p), _ptr(cells, _f64p), _ptr(pbc, _i32p),
         _ptr(offsets, _i64p), structures, len(numbers), _ptr(species_arr, _i32p), S,
         int(n_max), int(l_max), float(r_cut), float(sigma), _ptr(alphas, _f64p), _ptr(betas, _f64p),
-        _AVERAGE[average], int(num_threads),
+        opt, _AVERAGE[average], int(num_threads),
     )
     if kind == "oracle":
         flag = cancel if cancel is not None else None

@@ -45,14 +45,30 @@ mdescriptor::StructureBatchView view(const std::int32_t* numbers, const double* 
 
 extern "C" {
 
-// SOAP with rbf = "gto", compression "off", default weighting; the same
-// option mapping as SoapKernel._ensure_native (core.py:229-270).
+// The SoapOptions fields beyond the GTO, uncompressed, unweighted default
+// (same layout as the oracle's mdxo_soap_options).
+struct mdxr_soap_options {
+    std::int32_t weighting_function; // 0 none, 1 poly, 2 pow, 3 exp
+    std::int32_t weighting_has_w0;
+    double weighting_r0, weighting_c, weighting_d, weighting_m, weighting_w0;
+    const double* species_weights; // n_species values or null (all 1)
+    std::int32_t compression;      // 0 off, 1 mu2, 2 mu1nu1, 3 crossover
+    std::int32_t radial_basis;     // 0 GTO, 1 polynomial
+    std::int32_t grid_size;
+    const double* radial_grid;
+    const double* radial_weights;
+    const double* radial_values;   // n_max x grid_size
+};
+
+// SOAP with the option mapping of SoapKernel._ensure_native (core.py:229-270);
+// opt may be null (rbf = "gto", compression "off", default weighting).
 // average: 0 off, 1 inner, 2 outer.  Returns 0, 1 (invalid) or 4 (cancelled).
 int mdxr_soap(const std::int32_t* numbers, const double* positions, const double* cells,
               const std::int32_t* pbc, const std::int64_t* offsets, std::int64_t structures,
               std::int64_t atoms, const std::int32_t* species, int n_species, int n_max, int l_max,
-              double r_cut, double sigma, const double* alphas, const double* betas, int average,
-              int num_threads, double* output, char* err, int errlen) {
+              double r_cut, double sigma, const double* alphas, const double* betas,
+              const mdxr_soap_options* opt, int average, int num_threads, double* output, char* err,
+              int errlen) {
     try {
         mdescriptor::SoapOptions options;
         options.species.assign(species, species + n_species);
@@ -60,12 +76,35 @@ int mdxr_soap(const std::int32_t* numbers, const double* positions, const double
         options.n_max = n_max;
         options.l_max = l_max;
         options.sigma = sigma;
-        options.radial_basis = 0;
-        const std::size_t radial = static_cast<std::size_t>(l_max + 1) * static_cast<std::size_t>(n_max);
-        options.alphas.assign(alphas, alphas + radial);
-        options.betas.assign(betas, betas + radial * static_cast<std::size_t>(n_max));
-        options.species_weights.assign(static_cast<std::size_t>(n_species), 1.0);
-        options.compression = 0;
+        const bool polynomial = opt != nullptr && opt->radial_basis == 1;
+        options.radial_basis = polynomial ? 1 : 0;
+        if (polynomial) {
+            const std::size_t q = static_cast<std::size_t>(opt->grid_size);
+            options.radial_grid.assign(opt->radial_grid, opt->radial_grid + q);
+            options.radial_weights.assign(opt->radial_weights, opt->radial_weights + q);
+            options.radial_values.assign(opt->radial_values,
+                                         opt->radial_values + q * static_cast<std::size_t>(n_max));
+        } else {
+            const std::size_t radial = static_cast<std::size_t>(l_max + 1) * static_cast<std::size_t>(n_max);
+            options.alphas.assign(alphas, alphas + radial);
+            options.betas.assign(betas, betas + radial * static_cast<std::size_t>(n_max));
+        }
+        if (opt != nullptr && opt->species_weights != nullptr) {
+            options.species_weights.assign(opt->species_weights, opt->species_weights + n_species);
+        } else {
+            options.species_weights.assign(static_cast<std::size_t>(n_species), 1.0);
+        }
+        if (opt != nullptr) {
+            options.weighting_has_function = opt->weighting_function != 0;
+            options.weighting_function = opt->weighting_function;
+            options.weighting_has_w0 = opt->weighting_has_w0 != 0;
+            options.weighting_r0 = opt->weighting_r0;
+            options.weighting_c = opt->weighting_c;
+            options.weighting_d = opt->weighting_d;
+            options.weighting_m = opt->weighting_m;
+            options.weighting_w0 = opt->weighting_w0;
+        }
+        options.compression = opt != nullptr ? opt->compression : 0;
         options.inner_average = average == 1;
         options.outer_average = average == 2;
         options.num_threads = num_threads;

@@ -485,133 +485,325 @@ void mdxo_solid_harmonics(double x, double y, double z, int l_max, double* resul
 }
 
 /* ------------------------------------------------------------------------ */
-/* SOAP, GTO radial basis, compression off, default weighting.              */
-/* Plan: prepare_soap, soap.cpp:507-534.  Expansion: calculate_coefficients */
-/* GTO branch, soap.cpp:701-760 + 864-931.  Power spectrum: compression off */
-/* branch, soap.cpp:997-1013.  Averaging: soap.cpp:1019-1142.  Driver:      */
-/* compute_soap, soap.cpp:1149-1246.                                        */
+/* SOAP: both radial bases, every compression mode and distance weighting.  */
+/* Plan: prepare_soap, soap.cpp:507-572.  Expansion: calculate_coefficients */
+/* soap.cpp:701-931 (weights :799-812, polynomial :813-863, GTO :864-930).  */
+/* Power spectrum: soap.cpp:933-1017.  Averaging: soap.cpp:1019-1142.       */
+/* Driver: compute_soap, soap.cpp:1149-1246.                                */
 /* ------------------------------------------------------------------------ */
+
+/* Options beyond the GTO/off/unweighted default, the fields of SoapOptions
+ * (cpp/include/mdescriptor/descriptor.hpp:17-43) as SoapKernel._ensure_native
+ * fills them (core.py:229-270).  A NULL pointer means the defaults. */
 typedef struct {
-    int S, n, l_max, L, H;
+    int32_t weighting_function; /* 0 none, 1 poly, 2 pow, 3 exp */
+    int32_t weighting_has_w0;
+    double weighting_r0, weighting_c, weighting_d, weighting_m, weighting_w0;
+    const double* species_weights; /* [S], NULL = all 1 */
+    int32_t compression;           /* 0 off, 1 mu2, 2 mu1nu1, 3 crossover */
+    int32_t radial_basis;          /* 0 GTO (alphas, betas), 1 polynomial */
+    int32_t grid_size;
+    const double* radial_grid;     /* [grid_size] */
+    const double* radial_weights;  /* [grid_size] */
+    const double* radial_values;   /* [n * grid_size] */
+} mdxo_soap_options;
+
+typedef struct {
+    int S, n, l_max, L, H, types; /* types: coefficient species (1 for mu2) */
     int64_t coeff_size, features;
     double eta, soap_scale;
-    double* power_prefactors; /* [L] */
+    double* power_prefactors;  /* [L] */
     double* radial_prefactors; /* [L*n] */
     double* radial_exponents;  /* [L*n] */
     const double* betas;       /* [L*n*n], index (l*n + n')*n + k */
-    int32_t species[256];
+    double* weighted_qn;       /* polynomial: [Q*n] = w_q r_q^2 values[n][q] */
+    mdxo_soap_options opt;
+    double species_weights[256];
 } soap_plan;
 
-static int64_t soap_feature_count(int S, int n, int l_max) {
-    const int64_t w = (int64_t)S * n;
-    return w * (w + 1) / 2 * (l_max + 1);
+/* soap_features, soap.cpp:373-387 */
+static int64_t soap_feature_count(int S, int n, int l_max, int compression) {
+    const int64_t L = l_max + 1;
+    switch (compression) {
+    case 1:
+        return (int64_t)n * (n + 1) / 2 * L;
+    case 2:
+        return (int64_t)S * n * n * L;
+    case 3:
+        return (int64_t)S * n * (n + 1) / 2 * L;
+    default: {
+        const int64_t w = (int64_t)S * n;
+        return w * (w + 1) / 2 * L;
+    }
+    }
 }
 
-int64_t mdxo_soap_feature_count(int S, int n, int l_max) { return soap_feature_count(S, n, l_max); }
+int64_t mdxo_soap_feature_count(int S, int n, int l_max) { return soap_feature_count(S, n, l_max, 0); }
 
-static void compute_centre_coefficients(const soap_plan* p, const int32_t* atom_type, int64_t centre,
-                                        const int64_t* graph_offsets, const int32_t* graph_atoms,
-                                        const double* graph_disp, const double* graph_d2,
-                                        int64_t atom_base, double* coeff, double* scratch_harm,
-                                        int64_t* scratch_order, double* hsum, double* ylm) {
-    const int64_t begin = graph_offsets[centre];
-    const int64_t count = graph_offsets[centre + 1] - begin;
-    memset(coeff, 0, (size_t)p->coeff_size * sizeof(double));
-    /* species counting sort (stable), soap.cpp:737-760; S == 1 keeps graph order */
-    int64_t type_offsets[257];
-    int64_t cursor[256];
-    memset(cursor, 0, sizeof(cursor));
-    for (int64_t i = 0; i < count; ++i) cursor[atom_type[graph_atoms[begin + i] - atom_base]]++;
-    type_offsets[0] = 0;
-    for (int t = 0; t < p->S; ++t) {
-        type_offsets[t + 1] = type_offsets[t] + cursor[t];
-        cursor[t] = type_offsets[t];
-    }
-    for (int64_t i = 0; i < count; ++i) {
-        const int t = atom_type[graph_atoms[begin + i] - atom_base];
-        scratch_order[cursor[t]++] = begin + i;
-    }
-    /* harmonics, SoA [h * count + j], soap.cpp:761-780 */
-    for (int64_t j = 0; j < count; ++j) {
-        const int64_t src = scratch_order[j];
-        mdxo_solid_harmonics(graph_disp[src * 3 + 0], graph_disp[src * 3 + 1], graph_disp[src * 3 + 2],
-                             p->l_max, ylm);
-        for (int h = 0; h < p->H; ++h) scratch_harm[(int64_t)h * count + j] = ylm[h];
-    }
-    /* accumulate per species, l, k then fold beta, soap.cpp:881-929 */
-    for (int t = 0; t < p->S; ++t) {
-        const int64_t tb = type_offsets[t];
-        const int64_t te = type_offsets[t + 1];
-        for (int l = 0; l <= p->l_max; ++l) {
-            const int mc = 2 * l + 1;
-            for (int k = 0; k < p->n; ++k) {
-                const int ri = l * p->n + k;
-                const double pref = p->radial_prefactors[ri];
-                const double expo = p->radial_exponents[ri];
-                for (int m = 0; m < mc; ++m) hsum[m] = 0.0;
-                for (int64_t j = tb; j < te; ++j) {
-                    const double radial = pref * exp(-expo * graph_d2[scratch_order[j]]);
-                    for (int m = 0; m < mc; ++m) {
-                        /* weight = 1.0 at the default weighting (soap.cpp:389-420) */
-                        hsum[m] += radial * scratch_harm[(int64_t)(l * l + m) * count + j] * 1.0;
-                    }
-                }
-                for (int nn = 0; nn < p->n; ++nn) {
-                    const double beta = p->betas[(l * p->n + nn) * p->n + k];
-                    double* dst = coeff + ((int64_t)t * p->n + nn) * p->H + l * l;
-                    for (int m = 0; m < mc; ++m) dst[m] += p->soap_scale * beta * hsum[m];
-                }
-            }
+int64_t mdxo_soap_feature_count_ex(int S, int n, int l_max, int compression) {
+    return soap_feature_count(S, n, l_max, compression);
+}
+
+/* soap_weight, soap.cpp:389-420 */
+static double soap_weight(const soap_plan* p, double distance, int exact_self, int type) {
+    const mdxo_soap_options* o = &p->opt;
+    double value = 1.0;
+    if (o->weighting_function != 0) {
+        const double ratio = distance / o->weighting_r0;
+        switch (o->weighting_function) {
+        case 1:
+            value = distance > o->weighting_r0
+                ? 0.0
+                : o->weighting_c * pow(1.0 + 2.0 * ratio * ratio * ratio - 3.0 * ratio * ratio, o->weighting_m);
+            break;
+        case 2:
+            value = o->weighting_c / (o->weighting_d + pow(ratio, o->weighting_m));
+            break;
+        default:
+            value = o->weighting_c / (o->weighting_d + exp(-ratio));
+            break;
         }
     }
+    if (exact_self && o->weighting_has_w0) value = o->weighting_w0;
+    return value * p->species_weights[type];
 }
 
-/* power_spectrum, compression "off", soap.cpp:933-1017 */
-static void power_spectrum(const soap_plan* p, const double* c, double* out) {
-    int64_t f = 0;
-    for (int t1 = 0; t1 < p->S; ++t1) {
-        for (int t2 = t1; t2 < p->S; ++t2) {
-            for (int l = 0; l <= p->l_max; ++l) {
-                const double pref = p->power_prefactors[l];
-                for (int n1 = 0; n1 < p->n; ++n1) {
-                    for (int n2 = (t1 == t2 ? n1 : 0); n2 < p->n; ++n2) {
-                        const double* a = c + ((int64_t)t1 * p->n + n1) * p->H + l * l;
-                        const double* b = c + ((int64_t)t2 * p->n + n2) * p->H + l * l;
-                        double sum = 0.0;
-                        for (int m = 0; m < 2 * l + 1; ++m) sum += a[m] * b[m];
-                        out[f++] = pref * sum;
-                    }
-                }
-            }
+/* polynomial_flir, soap.cpp:450-492 (without the reference's distance cache,
+ * which returns the same values) */
+static void polynomial_flir(const soap_plan* p, double radius, double* values /* [L*Q] */) {
+    const int Q = p->opt.grid_size;
+    memset(values, 0, (size_t)p->L * Q * sizeof(double));
+    for (int q = 0; q < Q; ++q) {
+        const double radial = p->opt.radial_grid[q];
+        const double radial2 = radial * radial;
+        if (radius <= 1e-14) {
+            values[q] = exp(-p->eta * radial2);
+            continue;
+        }
+        const double prefactor = 0.25 / (p->eta * radius * radial);
+        const double minus = exp(-p->eta * (radial - radius) * (radial - radius));
+        const double plus = exp(-p->eta * (radial + radius) * (radial + radius));
+        values[q] = prefactor * (minus - plus);
+        if (p->l_max >= 1) values[Q + q] = prefactor * (minus + plus - 2.0 * values[q]);
+        for (int l = 2; l <= p->l_max; ++l) {
+            const double v = values[(l - 2) * Q + q] - prefactor * (4.0 * l - 2.0) * values[(l - 1) * Q + q];
+            values[l * Q + q] = v > 0.0 ? v : 0.0;
         }
     }
 }
 
 typedef struct {
     double* coeff;
-    double* harm;
-    int64_t* order;
-    double* hsum;
-    double* ylm;
-    double* power;
+    double* harm;    /* [H * count] */
+    int64_t* order;  /* [count] graph index in species order */
+    double* hsum;    /* [2 l_max + 1] */
+    double* ylm;     /* [H] */
+    double* power;   /* [F] */
+    double* weight;  /* [count] */
+    double* flir;    /* polynomial: [L * Q] */
+    double* integrand; /* polynomial: [types * H * Q] */
+    double* summed;  /* mu1nu1: [n * H] */
     int64_t capacity;
 } centre_workspace;
 
+static void compute_centre_coefficients(const soap_plan* p, const int32_t* atom_type, int64_t centre,
+                                        const int64_t* graph_offsets, const int32_t* graph_atoms,
+                                        const int32_t* graph_shifts, const double* graph_disp,
+                                        const double* graph_d2, centre_workspace* w) {
+    const int64_t begin = graph_offsets[centre];
+    const int64_t count = graph_offsets[centre + 1] - begin;
+    double* coeff = w->coeff;
+    memset(coeff, 0, (size_t)p->coeff_size * sizeof(double));
+    /* neighbour order: mu2 and one species keep the graph order, otherwise a
+     * stable counting sort by species (soap.cpp:727-760) */
+    int64_t type_offsets[257];
+    int64_t cursor[256];
+    if (p->opt.compression == 1 || p->S == 1) {
+        type_offsets[0] = 0;
+        type_offsets[1] = count;
+        for (int64_t i = 0; i < count; ++i) w->order[i] = begin + i;
+    } else {
+        memset(cursor, 0, sizeof(cursor));
+        for (int64_t i = 0; i < count; ++i) cursor[atom_type[graph_atoms[begin + i]]]++;
+        type_offsets[0] = 0;
+        for (int t = 0; t < p->S; ++t) {
+            type_offsets[t + 1] = type_offsets[t] + cursor[t];
+            cursor[t] = type_offsets[t];
+        }
+        for (int64_t i = 0; i < count; ++i) {
+            const int t = atom_type[graph_atoms[begin + i]];
+            w->order[cursor[t]++] = begin + i;
+        }
+    }
+    /* harmonics, SoA [h * count + j], soap.cpp:761-780 */
+    for (int64_t j = 0; j < count; ++j) {
+        const int64_t src = w->order[j];
+        mdxo_solid_harmonics(graph_disp[src * 3 + 0], graph_disp[src * 3 + 1], graph_disp[src * 3 + 2],
+                             p->l_max, w->ylm);
+        for (int h = 0; h < p->H; ++h) w->harm[(int64_t)h * count + j] = w->ylm[h];
+    }
+    /* weights, soap.cpp:781-812: the neighbour's own species under mu2, the
+     * species run otherwise (the same thing once sorted) */
+    for (int64_t j = 0; j < count; ++j) {
+        const int64_t src = w->order[j];
+        const int32_t atom = graph_atoms[src];
+        const int exact_self = atom == centre && graph_shifts[src * 3] == 0 && graph_shifts[src * 3 + 1] == 0
+            && graph_shifts[src * 3 + 2] == 0;
+        const int type = (p->opt.compression == 1 || p->S > 1) ? atom_type[atom] : 0;
+        w->weight[j] = soap_weight(p, sqrt(graph_d2[src]), exact_self, type);
+    }
+    if (p->opt.radial_basis == 1) {
+        /* polynomial basis, soap.cpp:813-863 */
+        const int Q = p->opt.grid_size;
+        const int64_t stride = (int64_t)p->H * Q;
+        memset(w->integrand, 0, (size_t)(p->types * stride) * sizeof(double));
+        for (int t = 0; t < p->types; ++t) {
+            const int64_t tb = p->opt.compression == 1 ? 0 : type_offsets[t];
+            const int64_t te = p->opt.compression == 1 ? count : type_offsets[t + 1];
+            for (int64_t j = tb; j < te; ++j) {
+                const double radius = sqrt(graph_d2[w->order[j]]);
+                polynomial_flir(p, radius, w->flir);
+                const double inverse_radius = radius <= 1e-14 ? 0.0 : 1.0 / radius;
+                double inverse_radius_power = 1.0;
+                for (int l = 0; l <= p->l_max; ++l) {
+                    const double scale = radius <= 1e-14 ? (l == 0 ? 4.0 * MDXO_PI * w->weight[j] : 0.0)
+                                                         : 4.0 * MDXO_PI * inverse_radius_power * w->weight[j];
+                    const double* source = w->flir + (int64_t)l * Q;
+                    for (int m = 0; m < 2 * l + 1; ++m) {
+                        const double factor = scale * w->harm[(int64_t)(l * l + m) * count + j];
+                        double* target = w->integrand + t * stride + (int64_t)(l * l + m) * Q;
+                        for (int q = 0; q < Q; ++q) target[q] += factor * source[q];
+                    }
+                    inverse_radius_power *= inverse_radius;
+                }
+            }
+        }
+        for (int t = 0; t < p->types; ++t) {
+            for (int l = 0; l <= p->l_max; ++l) {
+                for (int nn = 0; nn < p->n; ++nn) {
+                    double* dst = coeff + ((int64_t)t * p->n + nn) * p->H + l * l;
+                    for (int m = 0; m < 2 * l + 1; ++m) {
+                        const double* integrand = w->integrand + t * stride + (int64_t)(l * l + m) * Q;
+                        double sum = 0.0;
+                        for (int q = 0; q < Q; ++q) sum += integrand[q] * p->weighted_qn[(int64_t)q * p->n + nn];
+                        dst[m] += sum;
+                    }
+                }
+            }
+        }
+        return;
+    }
+    /* GTO: accumulate per species, l, k then fold beta, soap.cpp:864-929 */
+    for (int t = 0; t < p->types; ++t) {
+        const int64_t tb = p->opt.compression == 1 ? 0 : type_offsets[t];
+        const int64_t te = p->opt.compression == 1 ? count : type_offsets[t + 1];
+        for (int l = 0; l <= p->l_max; ++l) {
+            const int mc = 2 * l + 1;
+            for (int k = 0; k < p->n; ++k) {
+                const int ri = l * p->n + k;
+                const double pref = p->radial_prefactors[ri];
+                const double expo = p->radial_exponents[ri];
+                for (int m = 0; m < mc; ++m) w->hsum[m] = 0.0;
+                for (int64_t j = tb; j < te; ++j) {
+                    const double radial = pref * exp(-expo * graph_d2[w->order[j]]);
+                    for (int m = 0; m < mc; ++m) {
+                        w->hsum[m] += radial * w->harm[(int64_t)(l * l + m) * count + j] * w->weight[j];
+                    }
+                }
+                for (int nn = 0; nn < p->n; ++nn) {
+                    const double beta = p->betas[(l * p->n + nn) * p->n + k];
+                    double* dst = coeff + ((int64_t)t * p->n + nn) * p->H + l * l;
+                    for (int m = 0; m < mc; ++m) dst[m] += p->soap_scale * beta * w->hsum[m];
+                }
+            }
+        }
+    }
+}
+
+static double dot_channels(const double* a, const double* b, int l) {
+    double sum = 0.0;
+    for (int m = 0; m < 2 * l + 1; ++m) sum += a[l * l + m] * b[l * l + m];
+    return sum;
+}
+
+/* power_spectrum, soap.cpp:933-1017; summed [n * H] is scratch for mu1nu1 */
+static void power_spectrum(const soap_plan* p, const double* c, double* summed, double* out) {
+    int64_t f = 0;
+    const int64_t H = p->H;
+    const int n = p->n;
+    if (p->opt.compression == 1) {
+        for (int l = 0; l <= p->l_max; ++l) {
+            for (int n1 = 0; n1 < n; ++n1) {
+                for (int n2 = n1; n2 < n; ++n2) {
+                    out[f++] = p->power_prefactors[l] * dot_channels(c + n1 * H, c + n2 * H, l);
+                }
+            }
+        }
+    } else if (p->opt.compression == 2) {
+        memset(summed, 0, (size_t)(n * H) * sizeof(double));
+        for (int t = 0; t < p->S; ++t) {
+            for (int nn = 0; nn < n; ++nn) {
+                for (int64_t i = 0; i < H; ++i) summed[nn * H + i] += c[((int64_t)t * n + nn) * H + i];
+            }
+        }
+        for (int t = 0; t < p->S; ++t) {
+            for (int l = 0; l <= p->l_max; ++l) {
+                for (int n1 = 0; n1 < n; ++n1) {
+                    for (int n2 = 0; n2 < n; ++n2) {
+                        out[f++] = p->power_prefactors[l]
+                            * dot_channels(c + ((int64_t)t * n + n1) * H, summed + n2 * H, l);
+                    }
+                }
+            }
+        }
+    } else if (p->opt.compression == 3) {
+        for (int t = 0; t < p->S; ++t) {
+            for (int l = 0; l <= p->l_max; ++l) {
+                for (int n1 = 0; n1 < n; ++n1) {
+                    for (int n2 = n1; n2 < n; ++n2) {
+                        out[f++] = p->power_prefactors[l]
+                            * dot_channels(c + ((int64_t)t * n + n1) * H, c + ((int64_t)t * n + n2) * H, l);
+                    }
+                }
+            }
+        }
+    } else {
+        for (int t1 = 0; t1 < p->S; ++t1) {
+            for (int t2 = t1; t2 < p->S; ++t2) {
+                for (int l = 0; l <= p->l_max; ++l) {
+                    for (int n1 = 0; n1 < n; ++n1) {
+                        for (int n2 = (t1 == t2 ? n1 : 0); n2 < n; ++n2) {
+                            out[f++] = p->power_prefactors[l]
+                                * dot_channels(c + ((int64_t)t1 * n + n1) * H, c + ((int64_t)t2 * n + n2) * H, l);
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
 static int workspace_reserve(centre_workspace* w, const soap_plan* p, int64_t count) {
     if (w->coeff == NULL) {
+        const int Q = p->opt.radial_basis == 1 ? p->opt.grid_size : 0;
         w->coeff = (double*)malloc((size_t)p->coeff_size * sizeof(double));
         w->hsum = (double*)malloc((size_t)(2 * p->l_max + 1) * sizeof(double));
         w->ylm = (double*)malloc((size_t)p->H * sizeof(double));
         w->power = (double*)malloc((size_t)p->features * sizeof(double));
-        if (!w->coeff || !w->hsum || !w->ylm || !w->power) return 0;
+        w->summed = (double*)malloc((size_t)p->n * p->H * sizeof(double));
+        w->flir = (double*)malloc((size_t)(p->L * Q + 1) * sizeof(double));
+        w->integrand = (double*)malloc((size_t)((int64_t)p->types * p->H * Q + 1) * sizeof(double));
+        if (!w->coeff || !w->hsum || !w->ylm || !w->power || !w->summed || !w->flir || !w->integrand) return 0;
     }
     if (count > w->capacity) {
         const int64_t cap = count * 2;
         free(w->harm);
         free(w->order);
+        free(w->weight);
         w->harm = (double*)malloc((size_t)cap * p->H * sizeof(double));
         w->order = (int64_t*)malloc((size_t)cap * sizeof(int64_t));
-        if (!w->harm || !w->order) return 0;
+        w->weight = (double*)malloc((size_t)cap * sizeof(double));
+        if (!w->harm || !w->order || !w->weight) return 0;
         w->capacity = cap;
     }
     return 1;
@@ -624,6 +816,10 @@ static void workspace_free(centre_workspace* w) {
     free(w->hsum);
     free(w->ylm);
     free(w->power);
+    free(w->weight);
+    free(w->flir);
+    free(w->integrand);
+    free(w->summed);
     memset(w, 0, sizeof(*w));
 }
 
@@ -631,9 +827,9 @@ static void workspace_free(centre_workspace* w) {
  * given with local atom indices.  parallel != 0 runs centres in an OpenMP
  * loop with per-thread partial sums, as in soap.cpp:1022-1060, 1071-1112. */
 static int soap_structure(const soap_plan* p, const int32_t* atom_type, int64_t atom_count,
-                          const int64_t* g_off, const int32_t* g_atoms, const double* g_disp,
-                          const double* g_d2, int average, int parallel, int threads, double* out,
-                          const volatile int32_t* cancel) {
+                          const int64_t* g_off, const int32_t* g_atoms, const int32_t* g_shifts,
+                          const double* g_disp, const double* g_d2, int average, int parallel, int threads,
+                          double* out, const volatile int32_t* cancel) {
     const int64_t F = p->features;
     const int64_t C = p->coeff_size;
     int failed = 0;
@@ -662,13 +858,12 @@ static int soap_structure(const soap_plan* p, const int32_t* atom_type, int64_t 
                     failed = 1;
                     continue;
                 }
-                compute_centre_coefficients(p, atom_type, c, g_off, g_atoms, g_disp, g_d2, 0, w.coeff,
-                                            w.harm, w.order, w.hsum, w.ylm);
+                compute_centre_coefficients(p, atom_type, c, g_off, g_atoms, g_shifts, g_disp, g_d2, &w);
                 double* dst = partial + (int64_t)tid * width;
                 if (average == 1) {
                     for (int64_t i = 0; i < C; ++i) dst[i] += w.coeff[i];
                 } else {
-                    power_spectrum(p, w.coeff, w.power);
+                    power_spectrum(p, w.coeff, w.summed, w.power);
                     for (int64_t i = 0; i < F; ++i) dst[i] += w.power[i];
                 }
             }
@@ -692,7 +887,14 @@ static int soap_structure(const soap_plan* p, const int32_t* atom_type, int64_t 
                 const double inv = 1.0 / (double)atom_count;
                 for (int64_t i = 0; i < C; ++i) total[i] *= inv;
             }
-            power_spectrum(p, total, out);
+            double* summed = (double*)malloc((size_t)p->n * p->H * sizeof(double));
+            if (!summed) {
+                free(total);
+                free(partial);
+                return MDXO_NOMEM;
+            }
+            power_spectrum(p, total, summed, out);
+            free(summed);
         } else {
             if (atom_count > 0) {
                 const double inv = 1.0 / (double)atom_count;
@@ -716,9 +918,8 @@ static int soap_structure(const soap_plan* p, const int32_t* atom_type, int64_t 
                 failed = 1;
                 continue;
             }
-            compute_centre_coefficients(p, atom_type, c, g_off, g_atoms, g_disp, g_d2, 0, w.coeff,
-                                        w.harm, w.order, w.hsum, w.ylm);
-            power_spectrum(p, w.coeff, out + c * F);
+            compute_centre_coefficients(p, atom_type, c, g_off, g_atoms, g_shifts, g_disp, g_d2, &w);
+            power_spectrum(p, w.coeff, w.summed, out + c * F);
         }
         workspace_free(&w);
     }
@@ -728,38 +929,105 @@ static int soap_structure(const soap_plan* p, const int32_t* atom_type, int64_t 
 }
 
 /*
- * mdxo_soap: compute_soap (soap.cpp:1149-1246) for rbf = "gto", compression
- * "off", default weighting.  average: 0 off, 1 inner, 2 outer.  `output` is
- * caller-allocated C-order f64 [rows, features], rows = structures when
- * averaging, else atoms.  alphas [L*n] and betas [L*n*n] are supplied by the
- * caller exactly as the reference passes them (core.py:237-240).
+ * mdxo_soap: compute_soap (soap.cpp:1149-1246).  average: 0 off, 1 inner,
+ * 2 outer.  `output` is caller-allocated C-order f64 [rows, features], rows =
+ * structures when averaging, else atoms.  alphas [L*n] and betas [L*n*n] (GTO)
+ * or the polynomial grid/weights/values in `options` are supplied by the
+ * caller exactly as the reference passes them (core.py:237-245).  options may
+ * be NULL (GTO, compression off, no weighting, unit species weights).
  * decomposition: 0 = the reference's (one structure: centre-parallel;
  * several: structure-parallel with serial centres, soap.cpp:1218-1245);
  * 1 = every structure centre-parallel over all threads.
  */
+static int all_finite(const double* v, int64_t count) {
+    for (int64_t i = 0; i < count; ++i) {
+        if (!isfinite(v[i])) return 0;
+    }
+    return 1;
+}
+
 int mdxo_soap(const int32_t* numbers, const double* positions, const double* cells, const int32_t* pbc,
               const int64_t* offsets, int64_t structures, int64_t atoms, const int32_t* species, int S,
               int n_max, int l_max, double r_cut, double sigma, const double* alphas, const double* betas,
-              int average, int num_threads, int decomposition, double* output,
-              const volatile int32_t* cancel, char* err, int errlen) {
+              const mdxo_soap_options* options, int average, int num_threads, int decomposition,
+              double* output, const volatile int32_t* cancel, char* err, int errlen) {
     if (!validate_batch(numbers, positions, cells, pbc, offsets, structures, atoms, err, errlen)) {
-        return MDXO_INVALID;
-    }
-    if (S < 1 || S > 256 || !isfinite(r_cut) || !isfinite(sigma) || r_cut <= 0.0 || sigma <= 0.0
-        || n_max < 1 || l_max < 0 || l_max > MDXO_LMAX || average < 0 || average > 2) {
-        set_error(err, errlen, "invalid SOAP parameters");
         return MDXO_INVALID;
     }
     soap_plan p;
     memset(&p, 0, sizeof(p));
+    if (options != NULL) p.opt = *options;
+    /* parameter checks of compute_soap, soap.cpp:1150-1210, in its order */
+    if (S < 1 || S > 256 || !isfinite(r_cut) || !isfinite(sigma) || r_cut <= 0.0 || sigma <= 0.0
+        || n_max < 1 || l_max < 0 || l_max > MDXO_LMAX || average < 0 || average > 2 || p.opt.radial_basis < 0
+        || p.opt.radial_basis > 1 || p.opt.compression < 0 || p.opt.compression > 3) {
+        set_error(err, errlen, "invalid SOAP parameters");
+        return MDXO_INVALID;
+    }
+    if (p.opt.radial_basis == 0) {
+        if (alphas == NULL || betas == NULL) {
+            set_error(err, errlen, "invalid SOAP radial basis size");
+            return MDXO_INVALID;
+        }
+    } else if (p.opt.grid_size < 2 || p.opt.radial_grid == NULL || p.opt.radial_weights == NULL
+               || p.opt.radial_values == NULL) {
+        set_error(err, errlen, "invalid SOAP polynomial radial basis size");
+        return MDXO_INVALID;
+    }
+    if (p.opt.radial_basis == 0
+        && (!all_finite(alphas, (int64_t)(l_max + 1) * n_max)
+            || !all_finite(betas, (int64_t)(l_max + 1) * n_max * n_max))) {
+        set_error(err, errlen, "SOAP radial basis must be finite");
+        return MDXO_INVALID;
+    }
+    if (p.opt.radial_basis == 1) {
+        for (int q = 0; q < p.opt.grid_size; ++q) {
+            const double v = p.opt.radial_grid[q];
+            if (!isfinite(v) || v < 0.0 || v > r_cut) {
+                set_error(err, errlen, "SOAP polynomial radial grid must be finite and in range");
+                return MDXO_INVALID;
+            }
+        }
+        for (int q = 0; q < p.opt.grid_size; ++q) {
+            const double v = p.opt.radial_weights[q];
+            if (!isfinite(v) || v <= 0.0) {
+                set_error(err, errlen, "SOAP polynomial radial weights must be positive and finite");
+                return MDXO_INVALID;
+            }
+        }
+        if (!all_finite(p.opt.radial_values, (int64_t)n_max * p.opt.grid_size)) {
+            set_error(err, errlen, "SOAP polynomial radial basis must be finite");
+            return MDXO_INVALID;
+        }
+    }
+    for (int t = 0; t < S; ++t) {
+        p.species_weights[t] = p.opt.species_weights != NULL ? p.opt.species_weights[t] : 1.0;
+    }
+    if (!all_finite(p.species_weights, S)) {
+        set_error(err, errlen, "SOAP species weights must be finite");
+        return MDXO_INVALID;
+    }
+    if (p.opt.weighting_function != 0) {
+        if (p.opt.weighting_function < 1 || p.opt.weighting_function > 3 || !isfinite(p.opt.weighting_r0)
+            || p.opt.weighting_r0 <= 0.0 || !isfinite(p.opt.weighting_c) || p.opt.weighting_c < 0.0
+            || !isfinite(p.opt.weighting_d) || p.opt.weighting_d < 0.0 || !isfinite(p.opt.weighting_m)
+            || p.opt.weighting_m < 0.0) {
+            set_error(err, errlen, "invalid SOAP weighting parameters");
+            return MDXO_INVALID;
+        }
+    }
+    if (p.opt.weighting_has_w0 && (!isfinite(p.opt.weighting_w0) || p.opt.weighting_w0 < 0.0)) {
+        set_error(err, errlen, "invalid SOAP w0 weighting");
+        return MDXO_INVALID;
+    }
     p.S = S;
     p.n = n_max;
     p.l_max = l_max;
     p.L = l_max + 1;
     p.H = p.L * p.L;
-    p.coeff_size = (int64_t)S * n_max * p.H;
-    p.features = soap_feature_count(S, n_max, l_max);
-    for (int t = 0; t < S; ++t) p.species[t] = species[t];
+    p.types = p.opt.compression == 1 ? 1 : S;
+    p.coeff_size = (int64_t)p.types * n_max * p.H;
+    p.features = soap_feature_count(S, n_max, l_max, p.opt.compression);
     int32_t* atom_type = (int32_t*)malloc((size_t)(atoms > 0 ? atoms : 1) * sizeof(int32_t));
     if (!atom_type) return MDXO_NOMEM;
     for (int64_t i = 0; i < atoms; ++i) {
@@ -774,22 +1042,16 @@ int mdxo_soap(const int32_t* numbers, const double* positions, const double* cel
         }
         atom_type[i] = found;
     }
-    for (int i = 0; i < p.L * n_max; ++i) {
-        if (!isfinite(alphas[i])) {
-            free(atom_type);
-            set_error(err, errlen, "SOAP radial basis must be finite");
-            return MDXO_INVALID;
-        }
-    }
-    /* prepare_soap, soap.cpp:507-534 */
+    /* prepare_soap, soap.cpp:507-572 */
     p.eta = 1.0 / (2.0 * sigma * sigma);
     p.soap_scale = MDXO_PI * sqrt(MDXO_PI);
     p.power_prefactors = (double*)malloc((size_t)p.L * sizeof(double));
-    p.radial_prefactors = (double*)malloc((size_t)p.L * n_max * sizeof(double));
-    p.radial_exponents = (double*)malloc((size_t)p.L * n_max * sizeof(double));
+    p.radial_prefactors = (double*)calloc((size_t)p.L * n_max, sizeof(double));
+    p.radial_exponents = (double*)calloc((size_t)p.L * n_max, sizeof(double));
+    p.weighted_qn = (double*)calloc((size_t)(p.opt.radial_basis == 1 ? p.opt.grid_size : 1) * n_max, sizeof(double));
     p.betas = betas;
     for (int l = 0; l <= l_max; ++l) p.power_prefactors[l] = MDXO_PI * sqrt(8.0 / (2.0 * l + 1.0));
-    {
+    if (p.opt.radial_basis == 0) {
         double eta_power = 1.0;
         for (int l = 0; l <= l_max; ++l) {
             if (l > 0) eta_power *= p.eta;
@@ -798,6 +1060,14 @@ int mdxo_soap(const int32_t* numbers, const double* positions, const double* cel
                 const double denominator = alphas[idx] + p.eta;
                 p.radial_prefactors[idx] = eta_power * pow(denominator, -l - 1.5);
                 p.radial_exponents[idx] = alphas[idx] * p.eta / denominator;
+            }
+        }
+    } else {
+        for (int q = 0; q < p.opt.grid_size; ++q) {
+            const double radial = p.opt.radial_grid[q];
+            const double quadrature = p.opt.radial_weights[q] * radial * radial;
+            for (int nn = 0; nn < n_max; ++nn) {
+                p.weighted_qn[(int64_t)q * n_max + nn] = quadrature * p.opt.radial_values[(int64_t)nn * p.opt.grid_size + q];
             }
         }
     }
@@ -836,8 +1106,8 @@ int mdxo_soap(const int32_t* numbers, const double* positions, const double* cel
             }
         } else {
             double* dst = output + (averaged ? s : b) * F;
-            const int rc = soap_structure(&p, atom_type + b, n, g_off, pairs.atoms, pairs.disp, pairs.d2,
-                                          average, !structure_parallel, threads, dst, cancel);
+            const int rc = soap_structure(&p, atom_type + b, n, g_off, pairs.atoms, pairs.shifts, pairs.disp,
+                                          pairs.d2, average, !structure_parallel, threads, dst, cancel);
             if (rc != MDXO_OK) {
 #pragma omp critical
                 {
@@ -853,5 +1123,6 @@ int mdxo_soap(const int32_t* numbers, const double* positions, const double* cel
     free(p.power_prefactors);
     free(p.radial_prefactors);
     free(p.radial_exponents);
+    free(p.weighted_qn);
     return status;
 }

@@ -285,3 +285,184 @@ def test_averaging_closed_forms(oracle):
     assert np.all(inner[2] == 0.0) and np.all(outer[2] == 0.0)
     # inner <= outer in the l = 0, same-channel diagonal (Jensen / Cauchy-Schwarz)
     assert not np.allclose(inner[0], outer[0])
+
+
+# ---------------------------------------------------------------- SOAP options
+# Distance weighting, species weights, compression and the polynomial basis
+# (soap.cpp:373-492, 799-863, 933-1017), pinned independently of the
+# reference: weights enter the smeared density, compression modes are fixed
+# linear combinations of the uncompressed spectrum, and the polynomial basis
+# is a quadrature of the continuous projection.
+
+def _coefficient_quadrature(positions, types, weights, n_species, sigma, radial, n_radial, l_max, radius=14.0):
+    """c[t][n][lm] = int rho_t(r) g_n(|r|) Y_lm(r_hat) d^3r around centre 0 by
+    direct 3D quadrature, rho_t = sum_{j of type t} w_j exp(-|r - r_j|^2 / (2 sigma^2));
+    radial(l, r) -> [n_radial, len(r)] values of g_n (times r^l for the GTO)."""
+
+    eta = 1.0 / (2.0 * sigma * sigma)
+    xr, wr = np.polynomial.legendre.leggauss(240)
+    r = (xr + 1.0) * radius / 2.0
+    wr = wr * radius / 2.0
+    xc, wc = np.polynomial.legendre.leggauss(48)
+    nphi = 96
+    phi = np.arange(nphi) * 2.0 * np.pi / nphi
+    polar, azimuth = np.meshgrid(np.arccos(xc), phi, indexing="ij")
+    wang = (wc[:, None] * (2.0 * np.pi / nphi) * np.ones(nphi)[None, :]).ravel()
+    dirs = np.stack([np.sin(polar) * np.cos(azimuth), np.sin(polar) * np.sin(azimuth), np.cos(polar)], -1)
+    pts = r[:, None, None] * dirs.reshape(-1, 3)[None, :, :]
+    centre = positions[0]
+    H = (l_max + 1) ** 2
+    coeff = np.zeros((n_species, n_radial, H))
+    for t in range(n_species):
+        rho = np.zeros(pts.shape[:2])
+        for j in np.flatnonzero(types == t):
+            rho += weights[j] * np.exp(-eta * np.sum((pts - (positions[j] - centre)) ** 2, axis=-1))
+        for l in range(l_max + 1):
+            radial_w = radial(l, r) * (wr * r**2)[None, :]
+            for m in range(-l, l + 1):
+                angular = rho @ (_real_harmonic(l, m, polar, azimuth).ravel() * wang)
+                coeff[t, :, l * l + l + m] = radial_w @ angular
+    return coeff
+
+
+def _uncompressed(coeff, l_max):
+    out = []
+    S, n = coeff.shape[:2]
+    for t1 in range(S):
+        for t2 in range(t1, S):
+            for l in range(l_max + 1):
+                block = slice(l * l, (l + 1) ** 2)
+                for n1 in range(n):
+                    for n2 in range(n1 if t1 == t2 else 0, n):
+                        out.append(np.pi * np.sqrt(8.0 / (2 * l + 1)) * coeff[t1, n1, block] @ coeff[t2, n2, block])
+    return np.array(out)
+
+
+def _molecule():
+    positions = np.array([[0.0, 0.0, 0.0], [0.6, -0.8, 1.2], [-1.1, 0.4, 0.3], [0.9, 1.0, -0.7]])
+    return positions, np.array([1, 8, 1, 6]), np.array([0, 2, 0, 1])
+
+
+def test_polynomial_basis_orthonormal_on_its_quadrature():
+    from mdescriptor_amd.descriptors.basis import basis_polynomial
+
+    # The (r_cut - r)^(n+3) are nearly collinear: the Loewdin transform is
+    # only as accurate as cond(S) * eps, so the identity is checked to that.
+    for r_cut, n_max in [(3.5, 3), (5.0, 5), (6.0, 8)]:
+        grid, weights, values = basis_polynomial(r_cut, n_max)
+        assert grid.shape == (100,) and weights.shape == (100,) and values.shape == (n_max, 100)
+        assert np.all((grid > 0) & (grid < r_cut)) and np.isclose(weights.sum(), r_cut)
+        k = np.arange(1, n_max + 1)[:, None] + np.arange(1, n_max + 1)[None, :]
+        overlap = 2.0 * r_cut ** (7.0 + k) / ((5.0 + k) * (6.0 + k) * (7.0 + k))
+        cond = np.linalg.cond(overlap)
+        gram = (values * (weights * grid**2)[None, :]) @ values.T
+        np.testing.assert_allclose(gram, np.eye(n_max), atol=max(1e-12, 50 * cond * np.finfo(float).eps))
+
+
+@pytest.mark.parametrize("sigma,n_max,l_max", [(0.7, 3, 3), (1.0, 2, 2)])
+def test_polynomial_expansion_matches_density_quadrature(oracle, sigma, n_max, l_max):
+    """The polynomial basis (flir kernel + 100-point radial rule, soap.cpp:
+    450-492, 813-863) against the continuous projection onto the
+    orthonormalised (r_cut - r)^(n+3) functions, cut at r_cut."""
+
+    from mdescriptor_amd.descriptors.basis import basis_polynomial
+
+    r_cut = 3.5
+    positions, numbers, types = _molecule()
+    grid, weights, values = basis_polynomial(r_cut, n_max)
+    # the same orthonormal functions evaluated anywhere: S^(-1/2) g(r), zero beyond r_cut
+    _, _, at_grid = basis_polynomial(r_cut, n_max)
+    powers = np.asarray([(r_cut - np.clip(grid, 0.0, r_cut)) ** (n + 3) for n in range(n_max)])
+    transform = at_grid @ np.linalg.pinv(powers)
+
+    def radial(l, r):
+        g = np.asarray([(r_cut - np.clip(r, 0.0, r_cut)) ** (n + 3) for n in range(n_max)])
+        return transform @ g
+
+    batch = _batch(numbers, positions, np.zeros((1, 3, 3)), np.zeros((1, 3)), [0, 4])
+    got = oracle.soap(batch, species=[1, 6, 8], n_max=n_max, l_max=l_max, r_cut=r_cut, sigma=sigma,
+                      average="off", options={"polynomial": (grid, weights, values)})
+    coeff = _coefficient_quadrature(positions, types, np.ones(4), 3, sigma, radial, n_max, l_max, radius=r_cut)
+    expected = _uncompressed(coeff, l_max)
+    np.testing.assert_allclose(got[0], expected, rtol=0, atol=1e-9 * np.abs(expected).max())
+
+
+def test_weights_enter_the_density(oracle):
+    """Distance weighting, w0 on the centre's own image and species weights
+    multiply each atom's Gaussian (soap.cpp:389-420, 881-914)."""
+
+    r_cut, sigma, n_max, l_max = 3.5, 0.8, 3, 2
+    positions, numbers, types = _molecule()
+    alphas, betas = basis_gto(r_cut, n_max, l_max)
+    species_weights = np.array([1.5, 0.5, 2.0])
+    r0, c, m = 3.0, 1.2, 2.0
+    d = np.linalg.norm(positions - positions[0], axis=1)
+    ratio = d / r0
+    weights = np.where(d > r0, 0.0, c * (1.0 + 2.0 * ratio**3 - 3.0 * ratio**2) ** m)
+    weights[0] = 0.25  # w0
+    weights = weights * species_weights[types]
+
+    def radial(l, r):
+        return np.stack([r**l * np.exp(-alphas[l, k] * r**2) for k in range(n_max)])
+
+    coeff = _coefficient_quadrature(positions, types, weights, 3, sigma, radial, n_max, l_max)
+    folded = np.zeros_like(coeff)
+    for l in range(l_max + 1):
+        block = slice(l * l, (l + 1) ** 2)
+        folded[:, :, block] = np.einsum("nk,tkh->tnh", betas[l], coeff[:, :, block])
+    expected = _uncompressed(folded, l_max)
+    batch = _batch(numbers, positions, np.zeros((1, 3, 3)), np.zeros((1, 3)), [0, 4])
+    got = oracle.soap(batch, species=[1, 6, 8], n_max=n_max, l_max=l_max, r_cut=r_cut, sigma=sigma, alphas=alphas,
+                      betas=betas, average="off",
+                      options={"weighting": {"function": "poly", "r0": r0, "c": c, "m": m, "w0": 0.25},
+                               "species_weights": species_weights})
+    np.testing.assert_allclose(got[0], expected, rtol=0, atol=1e-10 * np.abs(expected).max())
+
+
+def _full_spectrum(flat, S, n, L):
+    """P[l][(t1 n1), (t2 n2)] (symmetric) from the uncompressed feature row."""
+
+    P = np.zeros((L, S * n, S * n))
+    f = 0
+    for t1 in range(S):
+        for t2 in range(t1, S):
+            for l in range(L):
+                for n1 in range(n):
+                    for n2 in range(n1 if t1 == t2 else 0, n):
+                        P[l, t1 * n + n1, t2 * n + n2] = P[l, t2 * n + n2, t1 * n + n1] = flat[f]
+                        f += 1
+    assert f == len(flat)
+    return P
+
+
+@pytest.mark.parametrize("average", ["off", "inner"])
+def test_compression_modes_are_sums_of_the_full_spectrum(oracle, average):
+    """mu2 is the spectrum of the species-summed density, mu1nu1 pairs each
+    species with that sum, crossover keeps the species-diagonal blocks
+    (soap.cpp:948-996): fixed linear combinations of the uncompressed one."""
+
+    rng = np.random.default_rng(5)
+    cell = np.diag([5.0, 5.4, 5.8])
+    positions = rng.uniform(0, 1, (9, 3)) @ cell
+    numbers = rng.choice([1, 6, 8], size=9)
+    batch = _batch(numbers, positions, cell, np.ones(3), [0, 9])
+    S, n, l_max = 3, 3, 3
+    L = l_max + 1
+    alphas, betas = basis_gto(4.0, n, l_max)
+    weights = {"species_weights": [1.0, 0.6, 1.7]}
+    kwargs = dict(species=[1, 6, 8], n_max=n, l_max=l_max, r_cut=4.0, sigma=1.0, alphas=alphas, betas=betas,
+                  average=average)
+    full = oracle.soap(batch, options=weights, **kwargs)
+    mu2 = oracle.soap(batch, options={**weights, "compression": "mu2"}, **kwargs)
+    mu1nu1 = oracle.soap(batch, options={**weights, "compression": "mu1nu1"}, **kwargs)
+    cross = oracle.soap(batch, options={**weights, "compression": "crossover"}, **kwargs)
+    iu = np.triu_indices(n)
+    for row in range(full.shape[0]):
+        P = _full_spectrum(full[row], S, n, L).reshape(L, S, n, S, n)
+        scale = np.abs(full[row]).max()
+        expect_mu2 = np.concatenate([P[l].sum(axis=(0, 2))[iu] for l in range(L)])
+        np.testing.assert_allclose(mu2[row], expect_mu2, atol=1e-12 * scale)
+        expect_mu1nu1 = np.concatenate([P[l, t].sum(axis=1).ravel() for t in range(S) for l in range(L)])
+        np.testing.assert_allclose(mu1nu1[row], expect_mu1nu1, atol=1e-12 * scale)
+        expect_cross = np.concatenate([P[l, t, :, t, :][iu] for t in range(S) for l in range(L)])
+        np.testing.assert_allclose(cross[row], expect_cross, atol=1e-12 * scale)

@@ -104,3 +104,76 @@ def test_oracle_rejects_what_the_reference_rejects(reference, case):
     with pytest.raises(ValueError) as theirs:
         reference.soap(batch, kind="ref", **kwargs)
     assert str(ours.value) == str(theirs.value)
+
+
+# Options beyond the GTO/uncompressed/unweighted default: the oracle's
+# weighting, species weights, compression modes and polynomial basis against
+# the reference build, on the water boxes (periodic) and the isolated
+# molecules of the small configurations.
+OPTION_CASES = {
+    "poly": {"weighting": {"function": "poly", "r0": 4.0, "c": 1.0, "m": 2.0}},
+    "pow_w0": {"weighting": {"function": "pow", "r0": 2.0, "c": 2.0, "d": 1.0, "m": 3.0, "w0": 0.5}},
+    "exp": {"weighting": {"function": "exp", "r0": 1.5, "c": 1.0, "d": 0.5}},
+    "w0_only": {"weighting": {"w0": 0.0}},
+    "species_weights": {"species_weights": "ramp"},
+    "mu2": {"compression": "mu2", "species_weights": "ramp"},
+    "mu1nu1": {"compression": "mu1nu1"},
+    "crossover": {"compression": "crossover", "weighting": {"function": "exp", "r0": 2.0, "c": 1.0, "d": 0.2}},
+    "polynomial": {"polynomial": True},
+    "polynomial_mu1nu1": {"polynomial": True, "compression": "mu1nu1",
+                          "weighting": {"function": "poly", "r0": 3.5, "c": 1.0, "m": 1.0}},
+}
+
+
+def option_arguments(name, species, r_cut, n_max):
+    from mdescriptor_amd.descriptors.basis import basis_polynomial
+
+    options = dict(OPTION_CASES[name])
+    if options.get("species_weights") == "ramp":
+        options["species_weights"] = list(np.linspace(0.5, 2.0, len(species)))
+    if options.get("polynomial"):
+        options["polynomial"] = basis_polynomial(r_cut, n_max)
+    return options
+
+
+@pytest.mark.parametrize("config", [1, 3])
+@pytest.mark.parametrize("name", sorted(OPTION_CASES))
+@pytest.mark.parametrize("average", ["off", "inner", "outer"])
+def test_soap_options_match_reference(reference, config, name, average):
+    w = workloads.config(config, "small")
+    p = w.params
+    n_max, l_max = min(p["n_max"], 4), min(p["l_max"], 4)
+    alphas, betas = basis_gto(p["r_cut"], n_max, l_max)
+    kwargs = dict(species=p["species"], n_max=n_max, l_max=l_max, r_cut=p["r_cut"], sigma=1.0, alphas=alphas,
+                  betas=betas, average=average, num_threads=8,
+                  options=option_arguments(name, p["species"], p["r_cut"], n_max))
+    ours = reference.soap(w.batch, **kwargs)
+    theirs = reference.soap(w.batch, kind="ref", **kwargs)
+    assert ours.shape == theirs.shape
+    assert scaled_error(ours, theirs) <= 1e-10
+
+
+@pytest.mark.parametrize("case", ["weighting_r0", "weighting_m", "w0", "species_weight", "grid_range", "grid_weight"])
+def test_oracle_rejects_options_as_the_reference_does(reference, case):
+    from types import SimpleNamespace
+    from mdescriptor_amd.descriptors.basis import basis_polynomial
+
+    batch = SimpleNamespace(numbers=np.array([1, 8], np.int32), positions=np.array([[0.0, 0.0, 0.0], [0.9, 0.1, 0.2]]),
+                            cells=np.eye(3)[None] * 6.0, pbc=np.ones((1, 3), np.int32), offsets=np.array([0, 2]))
+    alphas, betas = basis_gto(4.0, 2, 2)
+    grid, weights, values = basis_polynomial(4.0, 2)
+    options = {
+        "weighting_r0": {"weighting": {"function": "poly", "r0": 0.0, "c": 1.0, "m": 1.0}},
+        "weighting_m": {"weighting": {"function": "pow", "r0": 1.0, "c": 1.0, "d": 0.0, "m": -1.0}},
+        "w0": {"weighting": {"w0": -1.0}},
+        "species_weight": {"species_weights": [1.0, float("nan")]},
+        "grid_range": {"polynomial": (grid * 2.0, weights, values)},
+        "grid_weight": {"polynomial": (grid, -weights, values)},
+    }[case]
+    kwargs = dict(species=[1, 8], n_max=2, l_max=2, r_cut=4.0, sigma=1.0, alphas=alphas, betas=betas,
+                  average="off", options=options)
+    with pytest.raises(ValueError) as ours:
+        reference.soap(batch, **kwargs)
+    with pytest.raises(ValueError) as theirs:
+        reference.soap(batch, kind="ref", **kwargs)
+    assert str(ours.value) == str(theirs.value)
