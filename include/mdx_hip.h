@@ -54,12 +54,44 @@ typedef struct mdx_batch_view {
     int64_t atoms;
 } mdx_batch_view;
 
-/* SOAP parameters: the GTO subset of SoapOptions
- * (cpp/include/mdescriptor/descriptor.hpp:17-43).  alphas f64[(l_max+1)*n_max]
- * and betas f64[(l_max+1)*n_max*n_max] (index (l*n_max + n)*n_max + k) are the
- * orthonormalised radial basis computed by the caller, exactly as the
- * reference passes them to C++ (src/mdescriptor/descriptors/_kernels/core.py:
- * 237-240) and to its CUDA plugin (core.py:331-355).  They are copied. */
+/* The SoapOptions fields beyond the GTO, uncompressed, unweighted default
+ * (cpp/include/mdescriptor/descriptor.hpp:17-43), filled the way
+ * SoapKernel._ensure_native fills them (src/mdescriptor/descriptors/
+ * _kernels/core.py:241-270).  Arrays are copied at plan creation.
+ *   weighting_function: 0 none, 1 "poly", 2 "pow", 3 "exp" (soap.cpp:389-420)
+ *     with r0, c, d, m; weighting_has_w0 / weighting_w0: weight of the
+ *     centre's own image.
+ *   species_weights: n_species values in declared order, or NULL for 1.0.
+ *   compression: 0 "off", 1 "mu2", 2 "mu1nu1", 3 "crossover" (soap.cpp:373-387,
+ *     933-1017).
+ *   radial_basis: 0 GTO (mdx_soap_params.alphas/betas), 1 polynomial with
+ *     radial_grid / radial_weights f64[grid_size] and radial_values
+ *     f64[n_max * grid_size] (core.py:79-95, soap.cpp:450-492). */
+typedef struct mdx_soap_options {
+    int32_t weighting_function;
+    int32_t weighting_has_w0;
+    double weighting_r0;
+    double weighting_c;
+    double weighting_d;
+    double weighting_m;
+    double weighting_w0;
+    const double* species_weights;
+    int32_t compression;
+    int32_t radial_basis;
+    int32_t grid_size;
+    const double* radial_grid;
+    const double* radial_weights;
+    const double* radial_values;
+} mdx_soap_options;
+
+/* SOAP parameters: SoapOptions (cpp/include/mdescriptor/descriptor.hpp:17-43).
+ * alphas f64[(l_max+1)*n_max] and betas f64[(l_max+1)*n_max*n_max] (index
+ * (l*n_max + n)*n_max + k) are the orthonormalised GTO basis computed by the
+ * caller, exactly as the reference passes them to C++ (src/mdescriptor/
+ * descriptors/_kernels/core.py:237-240) and to its CUDA plugin
+ * (core.py:331-355); unused (may be NULL) with the polynomial basis.  They are
+ * copied.  options may be NULL: GTO basis, compression off, no weighting,
+ * unit species weights. */
 typedef struct mdx_soap_params {
     const int32_t* species; /* declared order, unique, positive */
     int32_t n_species;
@@ -71,6 +103,7 @@ typedef struct mdx_soap_params {
     const double* betas;
     int32_t average;   /* 0 "off", 1 "inner", 2 "outer" */
     int32_t out_dtype; /* bytes per output value: 4 (float32) or 8 (float64) */
+    const mdx_soap_options* options;
 } mdx_soap_params;
 
 /* Per-stage device times of the last run, from HIP events recorded on the

@@ -71,6 +71,25 @@ class BatchView(ctypes.Structure):
     ]
 
 
+class SoapOptions(ctypes.Structure):
+    _fields_ = [
+        ("weighting_function", ctypes.c_int32),
+        ("weighting_has_w0", ctypes.c_int32),
+        ("weighting_r0", ctypes.c_double),
+        ("weighting_c", ctypes.c_double),
+        ("weighting_d", ctypes.c_double),
+        ("weighting_m", ctypes.c_double),
+        ("weighting_w0", ctypes.c_double),
+        ("species_weights", _f64p),
+        ("compression", ctypes.c_int32),
+        ("radial_basis", ctypes.c_int32),
+        ("grid_size", ctypes.c_int32),
+        ("radial_grid", _f64p),
+        ("radial_weights", _f64p),
+        ("radial_values", _f64p),
+    ]
+
+
 class SoapParams(ctypes.Structure):
     _fields_ = [
         ("species", _i32p),
@@ -83,7 +102,50 @@ class SoapParams(ctypes.Structure):
         ("betas", _f64p),
         ("average", ctypes.c_int32),
         ("out_dtype", ctypes.c_int32),
+        ("options", ctypes.POINTER(SoapOptions)),
     ]
+
+
+COMPRESSION_MODES = {"off": 0, "mu2": 1, "mu1nu1": 2, "crossover": 3}
+WEIGHTING_FUNCTIONS = {"poly": 1, "pow": 2, "exp": 3}
+
+
+def soap_options(options: dict | None, n_species: int, keep: list) -> Any:
+    """A SoapOptions pointer (None for the defaults) from
+    ``{"weighting": {function, r0, c, d, m, w0}, "species_weights": [...],
+    "compression": "off"|"mu2"|"mu1nu1"|"crossover",
+    "polynomial": (grid, weights, values)}``, the fields SoapKernel fills
+    (core.py:241-270).  ``keep`` receives the arrays the struct points to."""
+
+    if not options:
+        return None
+    o = SoapOptions()
+    weighting = dict(options.get("weighting") or {})
+    if weighting.get("function") is not None:
+        o.weighting_function = WEIGHTING_FUNCTIONS[str(weighting["function"])]
+    o.weighting_has_w0 = 1 if "w0" in weighting else 0
+    o.weighting_r0 = float(weighting.get("r0", 1.0))
+    o.weighting_c = float(weighting.get("c", 1.0))
+    o.weighting_d = float(weighting.get("d", 0.0))
+    o.weighting_m = float(weighting.get("m", 1.0))
+    o.weighting_w0 = float(weighting.get("w0", 1.0))
+    if options.get("species_weights") is not None:
+        weights = np.ascontiguousarray(options["species_weights"], dtype=np.float64)
+        if weights.shape != (n_species,):
+            raise ValueError("species_weights needs one value per species")
+        keep.append(weights)
+        o.species_weights = weights.ctypes.data_as(_f64p)
+    o.compression = COMPRESSION_MODES[str(options.get("compression", "off"))]
+    if options.get("polynomial") is not None:
+        grid, weights, values = (np.ascontiguousarray(a, dtype=np.float64) for a in options["polynomial"])
+        keep.extend([grid, weights, values])
+        o.radial_basis = 1
+        o.grid_size = int(grid.shape[0])
+        o.radial_grid = grid.ctypes.data_as(_f64p)
+        o.radial_weights = weights.ctypes.data_as(_f64p)
+        o.radial_values = values.ctypes.data_as(_f64p)
+    keep.append(o)
+    return ctypes.pointer(o)
 
 
 class Timing(ctypes.Structure):
@@ -325,17 +387,21 @@ class SoapPlan:
     """Device-resident SOAP plan on a context."""
 
     def __init__(self, context: Context, *, species: Any, n_max: int, l_max: int, r_cut: float, sigma: float,
-                 alphas: np.ndarray, betas: np.ndarray, average: str, dtype: str) -> None:
+                 alphas: np.ndarray | None, betas: np.ndarray | None, average: str, dtype: str,
+                 options: dict | None = None) -> None:
         self.context = context
         self._species = np.ascontiguousarray(species, dtype=np.int32)
-        self._alphas = np.ascontiguousarray(alphas, dtype=np.float64).ravel()
-        self._betas = np.ascontiguousarray(betas, dtype=np.float64).ravel()
+        self._alphas = np.ascontiguousarray(alphas if alphas is not None else np.zeros(1), dtype=np.float64).ravel()
+        self._betas = np.ascontiguousarray(betas if betas is not None else np.zeros(1), dtype=np.float64).ravel()
         self.average = str(average)
         self.dtype = np.dtype(dtype)
+        self._keep: list = []
+        opt = soap_options(options, len(self._species), self._keep)
         params = SoapParams(
             self._species.ctypes.data_as(_i32p), len(self._species), int(n_max), int(l_max), float(r_cut),
-            float(sigma), self._alphas.ctypes.data_as(_f64p), self._betas.ctypes.data_as(_f64p),
-            {"off": 0, "inner": 1, "outer": 2}[self.average], int(self.dtype.itemsize),
+            float(sigma), self._alphas.ctypes.data_as(_f64p) if alphas is not None else None,
+            self._betas.ctypes.data_as(_f64p) if betas is not None else None,
+            {"off": 0, "inner": 1, "outer": 2}[self.average], int(self.dtype.itemsize), opt,
         )
         handle = ctypes.c_void_p()
         features = ctypes.c_int64()
@@ -469,8 +535,8 @@ class Backend:
         if not isinstance(payload, Mapping):
             raise ValueError("SOAP HIP backend requires the private _hip_payload")
         radial = payload["radial_basis"]
-        if "alphas" not in radial:
-            raise ValueError("the HIP backend implements the GTO radial basis only")
+        if "alphas" not in radial and "radial_grid" not in radial:
+            raise ValueError("the SOAP payload carries neither a GTO nor a polynomial radial basis")
         self.name = name
         self.options = dict(options)
         self._labels = tuple(options.get("_hip_labels") or payload.get("labels") or ())
@@ -481,11 +547,13 @@ class Backend:
         self._num_threads = num_threads
         self._average = str(options.get("average", "inner"))
         self._context = shared_context(0)
+        species = [int(z) for z in options["species"]]
         self._plan = SoapPlan(
-            self._context, species=options["species"], n_max=int(options["n_max"]), l_max=int(options["l_max"]),
+            self._context, species=species, n_max=int(options["n_max"]), l_max=int(options["l_max"]),
             r_cut=float(options["r_cut"]), sigma=float(options.get("sigma", 1.0)),
-            alphas=np.asarray(radial["alphas"]), betas=np.asarray(radial["betas"]), average=self._average,
-            dtype=self._dtype,
+            alphas=np.asarray(radial["alphas"]) if "alphas" in radial else None,
+            betas=np.asarray(radial["betas"]) if "betas" in radial else None, average=self._average,
+            dtype=self._dtype, options=plan_options(options, species, radial),
         )
         self._lock = threading.Lock()
         self._closed = False
@@ -526,6 +594,37 @@ class Backend:
             if not self._closed:
                 self._plan.close()
             self._closed = True
+
+
+def plan_options(options: Mapping[str, Any], species: list[int], radial: Mapping[str, Any]) -> dict | None:
+    """The SoapPlan options of a backend configuration: the canonical
+    ``weighting`` mapping, ``compression`` (mode and ``species_weighting``,
+    a mapping from atomic number to weight) and the polynomial basis arrays of
+    the payload, mapped as SoapKernel._ensure_native maps them
+    (core.py:241-270).  None for the GTO / uncompressed / unweighted default."""
+
+    weighting = dict(options.get("weighting") or {})
+    compression = dict(options.get("compression") or {})
+    mode = str(compression.get("mode", "off"))
+    species_weighting = compression.get("species_weighting")
+    species_weights = None
+    if species_weighting is not None:
+        keys = {int(k) for k in species_weighting}
+        if keys != set(species):
+            raise ValueError("species_weighting must contain exactly the configured species")
+        by_number = {int(k): float(v) for k, v in species_weighting.items()}
+        species_weights = [by_number[z] for z in species]
+    result: dict[str, Any] = {}
+    if weighting:
+        result["weighting"] = weighting
+    if species_weights is not None:
+        result["species_weights"] = species_weights
+    if mode != "off":
+        result["compression"] = mode
+    if "radial_grid" in radial:
+        result["polynomial"] = (np.asarray(radial["radial_grid"]), np.asarray(radial["radial_weights"]),
+                                np.asarray(radial["radial_values"]))
+    return result or None
 
 
 def create_backend(name: str, options: Mapping[str, Any]) -> Backend:

@@ -121,15 +121,64 @@ void validate_params(const mdx_soap_params& p) {
     if (p.n_max > mdx::kMaxNmax) {
         throw mdx::Error(MDX_INVALID_ARGUMENT, "the HIP SOAP backend supports n_max <= 16");
     }
-    if (p.alphas == nullptr || p.betas == nullptr) {
-        throw mdx::Error(MDX_INVALID_ARGUMENT, "invalid SOAP radial basis size");
+    const mdx_soap_options* o = p.options;
+    if (o != nullptr && (o->radial_basis < 0 || o->radial_basis > 1 || o->compression < 0 || o->compression > 3)) {
+        throw mdx::Error(MDX_INVALID_ARGUMENT, "invalid SOAP parameters");
     }
+    const bool polynomial = o != nullptr && o->radial_basis == 1;
     const int L = p.l_max + 1;
-    for (int i = 0; i < L * p.n_max; ++i) {
-        if (!std::isfinite(p.alphas[i])) throw mdx::Error(MDX_INVALID_ARGUMENT, "SOAP radial basis must be finite");
+    // soap.cpp:1160-1209, in its order
+    if (!polynomial) {
+        if (p.alphas == nullptr || p.betas == nullptr) {
+            throw mdx::Error(MDX_INVALID_ARGUMENT, "invalid SOAP radial basis size");
+        }
+        for (int i = 0; i < L * p.n_max; ++i) {
+            if (!std::isfinite(p.alphas[i])) throw mdx::Error(MDX_INVALID_ARGUMENT, "SOAP radial basis must be finite");
+        }
+        for (int i = 0; i < L * p.n_max * p.n_max; ++i) {
+            if (!std::isfinite(p.betas[i])) throw mdx::Error(MDX_INVALID_ARGUMENT, "SOAP radial basis must be finite");
+        }
+    } else {
+        if (o->grid_size < 2 || o->radial_grid == nullptr || o->radial_weights == nullptr
+            || o->radial_values == nullptr) {
+            throw mdx::Error(MDX_INVALID_ARGUMENT, "invalid SOAP polynomial radial basis size");
+        }
+        if (o->grid_size > 4096) {
+            throw mdx::Error(MDX_INVALID_ARGUMENT, "the HIP SOAP backend supports at most 4096 radial grid points");
+        }
+        for (int q = 0; q < o->grid_size; ++q) {
+            if (!std::isfinite(o->radial_grid[q]) || o->radial_grid[q] < 0.0 || o->radial_grid[q] > p.r_cut) {
+                throw mdx::Error(MDX_INVALID_ARGUMENT, "SOAP polynomial radial grid must be finite and in range");
+            }
+        }
+        for (int q = 0; q < o->grid_size; ++q) {
+            if (!std::isfinite(o->radial_weights[q]) || o->radial_weights[q] <= 0.0) {
+                throw mdx::Error(MDX_INVALID_ARGUMENT, "SOAP polynomial radial weights must be positive and finite");
+            }
+        }
+        for (int64_t i = 0; i < static_cast<int64_t>(o->grid_size) * p.n_max; ++i) {
+            if (!std::isfinite(o->radial_values[i])) {
+                throw mdx::Error(MDX_INVALID_ARGUMENT, "SOAP polynomial radial basis must be finite");
+            }
+        }
     }
-    for (int i = 0; i < L * p.n_max * p.n_max; ++i) {
-        if (!std::isfinite(p.betas[i])) throw mdx::Error(MDX_INVALID_ARGUMENT, "SOAP radial basis must be finite");
+    if (o != nullptr && o->species_weights != nullptr) {
+        for (int t = 0; t < p.n_species; ++t) {
+            if (!std::isfinite(o->species_weights[t])) {
+                throw mdx::Error(MDX_INVALID_ARGUMENT, "SOAP species weights must be finite");
+            }
+        }
+    }
+    if (o != nullptr && o->weighting_function != 0) {
+        if (o->weighting_function < 1 || o->weighting_function > 3 || !std::isfinite(o->weighting_r0)
+            || o->weighting_r0 <= 0.0 || !std::isfinite(o->weighting_c) || o->weighting_c < 0.0
+            || !std::isfinite(o->weighting_d) || o->weighting_d < 0.0 || !std::isfinite(o->weighting_m)
+            || o->weighting_m < 0.0) {
+            throw mdx::Error(MDX_INVALID_ARGUMENT, "invalid SOAP weighting parameters");
+        }
+    }
+    if (o != nullptr && o->weighting_has_w0 && (!std::isfinite(o->weighting_w0) || o->weighting_w0 < 0.0)) {
+        throw mdx::Error(MDX_INVALID_ARGUMENT, "invalid SOAP w0 weighting");
     }
     const int64_t coeff = static_cast<int64_t>(p.n_species) * p.n_max * L * L;
     if (coeff * 8 > 96 * 1024) {
@@ -376,28 +425,80 @@ int mdx_hip_soap_plan_create(mdx_hip_ctx* ctx, const mdx_soap_params* params, md
             plan->sigma = p.sigma;
             plan->cutoff = p.r_cut + soap_padding(p.sigma);
             plan->species.assign(p.species, p.species + p.n_species);
+            const mdx_soap_options* o = p.options;
+            plan->compression = o != nullptr ? o->compression : 0;
+            plan->radial_basis = o != nullptr ? o->radial_basis : 0;
+            plan->weighting = o != nullptr ? o->weighting_function : 0;
+            plan->has_w0 = o != nullptr && o->weighting_has_w0 ? 1 : 0;
+            if (o != nullptr) {
+                plan->w_r0 = o->weighting_r0;
+                plan->w_c = o->weighting_c;
+                plan->w_d = o->weighting_d;
+                plan->w_m = o->weighting_m;
+                plan->w_w0 = o->weighting_w0;
+            }
+            plan->species_weights.assign(static_cast<size_t>(plan->S), 1.0);
+            if (o != nullptr && o->species_weights != nullptr) {
+                plan->species_weights.assign(o->species_weights, o->species_weights + plan->S);
+            }
+            bool unit_species = true;
+            for (double v : plan->species_weights) unit_species = unit_species && v == 1.0;
+            plan->weighted = plan->weighting != 0 || plan->has_w0 || !unit_species ? 1 : 0;
+            // coefficient species: mu2 sums every neighbour into one density (soap.cpp:710)
+            plan->Sc = plan->compression == 1 ? 1 : plan->S;
+            {
+                // soap_features, soap.cpp:373-387
+                const int64_t S = plan->S, n = plan->n, Lw = plan->L;
+                switch (plan->compression) {
+                case 1: plan->features = n * (n + 1) / 2 * Lw; break;
+                case 2: plan->features = S * n * n * Lw; break;
+                case 3: plan->features = S * n * (n + 1) / 2 * Lw; break;
+                default: plan->features = S * n * (S * n + 1) / 2 * Lw; break;
+                }
+            }
             const int64_t w = static_cast<int64_t>(plan->S) * plan->n;
-            plan->features = w * (w + 1) / 2 * plan->L; // soap.cpp:382-385
             plan->coeff_size = w * plan->H;
             const int L = plan->L, n = plan->n, H = plan->H;
             // prepare_soap, soap.cpp:507-534
             const double pi = 3.141592653589793238462643383279502884;
             const double eta = 1.0 / (2.0 * p.sigma * p.sigma);
             const double soap_scale = pi * std::sqrt(pi);
-            std::vector<double> pref(static_cast<size_t>(L * n)), expo(static_cast<size_t>(L * n));
-            double eta_power = 1.0;
-            for (int l = 0; l < L; ++l) {
-                if (l > 0) eta_power *= eta;
-                for (int k = 0; k < n; ++k) {
-                    const int idx = l * n + k;
-                    const double alpha = p.alphas[idx];
-                    const double denominator = alpha + eta;
-                    pref[static_cast<size_t>(idx)] = eta_power * std::pow(denominator, -l - 1.5);
-                    expo[static_cast<size_t>(idx)] = alpha * eta / denominator;
+            plan->eta = eta;
+            std::vector<double> pref(static_cast<size_t>(L * n), 1.0), expo(static_cast<size_t>(L * n), 0.0);
+            std::vector<double> beta(static_cast<size_t>(L * n * n), 0.0);
+            if (plan->radial_basis == 0) {
+                double eta_power = 1.0;
+                for (int l = 0; l < L; ++l) {
+                    if (l > 0) eta_power *= eta;
+                    for (int k = 0; k < n; ++k) {
+                        const int idx = l * n + k;
+                        const double alpha = p.alphas[idx];
+                        const double denominator = alpha + eta;
+                        pref[static_cast<size_t>(idx)] = eta_power * std::pow(denominator, -l - 1.5);
+                        expo[static_cast<size_t>(idx)] = alpha * eta / denominator;
+                    }
                 }
+                for (size_t i = 0; i < beta.size(); ++i) beta[i] = soap_scale * p.betas[i];
+            } else {
+                // polynomial: the per-neighbour radial functions G_lk come out
+                // already projected (no fold), so the fold is the identity
+                for (int l = 0; l < L; ++l) {
+                    for (int k = 0; k < n; ++k) beta[static_cast<size_t>((l * n + k) * n + k)] = 1.0;
+                }
+                // quadrature-weighted basis values w_q r_q^2 g_k(r_q), [q * n + k] (soap.cpp:551-565)
+                const int Q = o->grid_size;
+                plan->grid_size = Q;
+                std::vector<double> bw(static_cast<size_t>(Q) * n), grid(o->radial_grid, o->radial_grid + Q);
+                for (int q = 0; q < Q; ++q) {
+                    const double radial = o->radial_grid[q];
+                    const double quadrature = o->radial_weights[q] * radial * radial;
+                    for (int k = 0; k < n; ++k) {
+                        bw[static_cast<size_t>(q) * n + k] = quadrature * o->radial_values[static_cast<size_t>(k) * Q + q];
+                    }
+                }
+                upload(plan->d_poly_bw, bw);
+                upload(plan->d_poly_grid, grid);
             }
-            std::vector<double> beta(static_cast<size_t>(L * n * n));
-            for (size_t i = 0; i < beta.size(); ++i) beta[i] = soap_scale * p.betas[i];
             std::vector<double> ps_pref(static_cast<size_t>(L));
             for (int l = 0; l < L; ++l) ps_pref[static_cast<size_t>(l)] = pi * std::sqrt(8.0 / (2.0 * l + 1.0));
             // solid_harmonic_normalization (soap.cpp:26-38), sqrt(2) folded in for m > 0
@@ -432,9 +533,14 @@ int mdx_hip_soap_plan_create(mdx_hip_ctx* ctx, const mdx_soap_params* params, md
             if (choice != "auto" && choice != "generic" && choice != "mfma") {
                 throw mdx::Error(MDX_INVALID_ARGUMENT, "MDX_HIP_SOAP_KERNEL must be auto, generic or mfma");
             }
-            const mdx::MfmaPlanHost mp = mdx::plan_mfma_tables(plan->S, n, p.l_max, beta, pref);
+            const mdx::MfmaPlanHost mp = mdx::plan_mfma_tables(plan->Sc, n, p.l_max, beta, pref);
             mdx::MfmaDims md{};
             md.S = plan->S;
+            md.Sc = plan->Sc;
+            md.compression = plan->compression;
+            md.radial = plan->radial_basis;
+            md.grid = plan->grid_size;
+            md.crow = mdx::mfma_coefficient_rows(plan->Sc, n, plan->compression);
             md.n = n;
             md.l_max = p.l_max;
             md.L = L;
@@ -450,9 +556,14 @@ int mdx_hip_soap_plan_create(mdx_hip_ctx* ctx, const mdx_soap_params* params, md
             plan->hpad = md.hpad;
             plan->clamp = md.clamp;
             const bool fits = mdx::mfma_template_tiles(mp.tiles) > 0 && mdx::mfma_lds_bytes(md) <= 64 * 1024;
-            plan->use_mfma = choice != "generic" && fits;
-            if (choice == "mfma" && !fits) {
-                throw mdx::Error(MDX_INVALID_ARGUMENT, "SOAP shape is outside the matrix-core kernel's limits");
+            // only the matrix-core kernel implements weighting, compression and the polynomial basis
+            const bool defaults = plan->compression == 0 && plan->radial_basis == 0 && plan->weighted == 0;
+            plan->use_mfma = fits && (choice != "generic" || !defaults);
+            if ((choice == "mfma" || !defaults) && !fits) {
+                throw mdx::Error(MDX_INVALID_ARGUMENT, defaults
+                    ? "SOAP shape is outside the matrix-core kernel's limits"
+                    : "SOAP shape is outside the matrix-core kernel's limits, which weighting, compression and the "
+                      "polynomial basis need");
             }
             plan->tiles = mp.tiles;
             if (plan->use_mfma) {
@@ -469,6 +580,7 @@ int mdx_hip_soap_plan_create(mdx_hip_ctx* ctx, const mdx_soap_params* params, md
             upload(plan->d_hnorm, hnorm);
             upload(plan->d_feat_a, fa);
             upload(plan->d_feat_b, fb);
+            upload(plan->d_species_w, plan->species_weights);
         } catch (...) {
             delete plan;
             throw;

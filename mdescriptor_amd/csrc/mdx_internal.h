@@ -175,6 +175,17 @@ struct mdx_soap_plan {
     int hpad = 0;  // padded harmonic row of the matrix-core layout
     int clamp = 0; // 1 when expo * cutoff^2 can exceed 700
     mdx::DeviceBuffer d_row_channel, d_col_harmonic, d_beta_lane, d_fbase, d_fstride;
+    // options beyond the GTO / uncompressed / unweighted default (mdx_soap_options)
+    int Sc = 0;              // coefficient species: 1 for mu2, else S
+    int compression = 0;     // 0 off, 1 mu2, 2 mu1nu1, 3 crossover
+    int radial_basis = 0;    // 0 GTO, 1 polynomial
+    int grid_size = 0;       // polynomial radial grid points
+    int weighting = 0;       // 0 none, 1 poly, 2 pow, 3 exp
+    int has_w0 = 0;
+    int weighted = 0;        // any weighting function, w0 or species weight != 1
+    double w_r0 = 1.0, w_c = 1.0, w_d = 0.0, w_m = 1.0, w_w0 = 1.0, eta = 0.5;
+    std::vector<double> species_weights;
+    mdx::DeviceBuffer d_species_w, d_poly_bw, d_poly_grid;
 };
 
 struct mdx_device_batch {

@@ -392,7 +392,7 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
     int64_t* d_struct_items = nullptr;
     double* d_partial = nullptr;
     if (p.average != 0) {
-        const size_t inner_width = p.use_mfma ? static_cast<size_t>(p.S * p.n + 1) * static_cast<size_t>(p.hpad)
+        const size_t inner_width = p.use_mfma ? static_cast<size_t>(mfma_coefficient_rows(p.Sc, p.n, p.compression)) * static_cast<size_t>(p.hpad)
                                               : static_cast<size_t>(d.C);
         const size_t width = p.average == 1 ? inner_width : static_cast<size_t>(d.F);
         const size_t head = ((item_begin_h.size() + struct_items_h.size()) * sizeof(int64_t) + 255) & ~size_t(255);
@@ -422,6 +422,20 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
         md.F = p.features;
         md.hpad = p.hpad;
         md.clamp = p.clamp;
+        md.Sc = p.Sc;
+        md.compression = p.compression;
+        md.crow = mfma_coefficient_rows(p.Sc, p.n, p.compression);
+        md.radial = p.radial_basis;
+        md.grid = p.grid_size;
+        md.weighted = p.weighted;
+        md.weighting = p.weighting;
+        md.has_w0 = p.has_w0;
+        md.w_r0 = p.w_r0;
+        md.w_c = p.w_c;
+        md.w_d = p.w_d;
+        md.w_m = p.w_m;
+        md.w_w0 = p.w_w0;
+        md.eta = p.eta;
         MfmaTables tab{};
         tab.row_channel = p.d_row_channel.as<int32_t>();
         tab.col_harmonic = p.d_col_harmonic.as<int32_t>();
@@ -432,6 +446,12 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
         tab.ps_pref = p.d_ps_pref.as<double>();
         tab.fbase = p.d_fbase.as<int32_t>();
         tab.fstride = p.d_fstride.as<int32_t>();
+        tab.species_w = p.d_species_w.as<double>();
+        tab.poly_bw = p.d_poly_bw.as<double>();
+        tab.poly_grid = p.d_poly_grid.as<double>();
+        tab.bin_atom = g.bin_atom.as<int32_t>();
+        tab.bin_image = g.bin_image.as<int32_t>();
+        tab.images = pb.d_images.as<ImageDesc>();
         const int tt = mfma_template_tiles(p.tiles);
         if (events != nullptr) MDX_HIP(hipEventRecord(events[2], stream));
         for (int64_t base = 0; base < items; base += slice) {

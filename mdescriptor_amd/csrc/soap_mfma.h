@@ -17,6 +17,18 @@ struct MfmaDims {
     // harmonic m-columns computed by each wavefront of a workgroup (bit m of
     // harm_mask[w]), balanced by recurrence length
     uint32_t harm_mask[16];
+    // options (mdx_soap_options): S above is the graph's species; Sc the
+    // coefficient species (1 for mu2); crow the LDS coefficient rows: Sc*n
+    // channels, then n species-summed rows for mu1nu1, then one zero row
+    int Sc;
+    int compression; // 0 off, 1 mu2, 2 mu1nu1, 3 crossover
+    int crow;
+    int radial;      // 0 GTO, 1 polynomial
+    int grid;        // polynomial radial grid points
+    int weighted;    // 1 when any neighbour weight can differ from 1
+    int weighting;   // 0 none, 1 poly, 2 pow, 3 exp
+    int has_w0;
+    double w_r0, w_c, w_d, w_m, w_w0, eta;
 };
 
 // Device tables built once per plan.
@@ -38,6 +50,12 @@ struct MfmaTables {
     const double* ps_pref;
     const int32_t* fbase;
     const int32_t* fstride;
+    const double* species_w;  // species weights [S]
+    const double* poly_bw;    // polynomial: w_q r_q^2 g_k(r_q), [q * n + k]
+    const double* poly_grid;  // polynomial: r_q
+    const int32_t* bin_atom;  // atom of each binned image (exact-self test for w0)
+    const int32_t* bin_image; // image of each binned image
+    const ImageDesc* images;  // image table (integer shifts)
 };
 
 // Host-side tables of a plan: block-diagonal packing of the (l, k) x (l, m)
@@ -53,6 +71,8 @@ MfmaPlanHost plan_mfma_tables(int S, int n, int l_max, const std::vector<double>
                               const std::vector<double>& pref);
 
 int mfma_template_tiles(int tiles);
+// LDS coefficient rows of a plan: Sc*n channels, n summed rows for mu1nu1, one zero row
+inline int mfma_coefficient_rows(int Sc, int n, int compression) { return Sc * n + (compression == 2 ? n : 0) + 1; }
 int mfma_padded_row(int l_max);
 size_t mfma_lds_bytes(const MfmaDims& d);
 void launch_mfma_expand(hipStream_t stream, int template_tiles, const PreparedBatch& pb, const DeviceGraph& g,

@@ -92,11 +92,12 @@ __device__ inline double exp_neg(double x, const double* tab64) {
 // immediate constant and every store a constant LDS offset from the lane's
 // column base.
 template <int LM>
-__device__ __forceinline__ void harmonics_fixed(double x, double y, double z, bool valid, uint32_t mask, int comp,
+__device__ __forceinline__ void harmonics_fixed(double x, double y, double z, double scale, uint32_t mask, int comp,
                                                const HarmonicRecurrence* __restrict__ hr, double* out) {
     const double r2 = x * x + y * y + z * z;
-    // an invalid (pad) slot gets all-zero harmonics from a zero seed
-    double sre = valid ? hr->n00 : 0.0, sim = 0.0;
+    // the seed carries the neighbour's weight: every harmonic is linear in it,
+    // and a pad slot (scale 0) gets all-zero harmonics
+    double sre = scale * hr->n00, sim = 0.0;
 #pragma unroll
     for (int m = 0; m <= LM; ++m) {
         if ((mask >> m) == 0) break;  // no column of this wavefront from here on
@@ -127,13 +128,31 @@ __device__ __forceinline__ void harmonics_fixed(double x, double y, double z, bo
 
 // harmonics_fixed<l_max> for a run-time l_max (a wave-uniform branch chain)
 template <int LM = 0>
-__device__ __forceinline__ void harmonics_q(double x, double y, double z, bool valid, int l_max, uint32_t mask,
+__device__ __forceinline__ void harmonics_q(double x, double y, double z, double scale, int l_max, uint32_t mask,
                                            int comp, const HarmonicRecurrence* __restrict__ hr, double* out) {
     if (l_max == LM) {
-        harmonics_fixed<LM>(x, y, z, valid, mask, comp, hr, out);
+        harmonics_fixed<LM>(x, y, z, scale, mask, comp, hr, out);
     } else if constexpr (LM < kHarmonicLmax) {
-        harmonics_q<LM + 1>(x, y, z, valid, l_max, mask, comp, hr, out);
+        harmonics_q<LM + 1>(x, y, z, scale, l_max, mask, comp, hr, out);
     }
+}
+
+// Weight of one neighbour (soap_weight, soap.cpp:389-420): the distance
+// function, w0 for the centre's own image, times the species weight.
+__device__ inline double neighbour_weight(const MfmaDims& d, double distance, bool exact_self, double species_w) {
+    double value = 1.0;
+    if (d.weighting != 0) {
+        const double ratio = distance / d.w_r0;
+        if (d.weighting == 1) {
+            value = distance > d.w_r0 ? 0.0 : d.w_c * pow(1.0 + 2.0 * ratio * ratio * ratio - 3.0 * ratio * ratio, d.w_m);
+        } else if (d.weighting == 2) {
+            value = d.w_c / (d.w_d + pow(ratio, d.w_m));
+        } else {
+            value = d.w_c / (d.w_d + exp(-ratio));
+        }
+    }
+    if (exact_self && d.has_w0) value = d.w_w0;
+    return value * species_w;
 }
 
 __device__ inline int degree_of_harmonic(int h) {
@@ -180,6 +199,19 @@ __device__ inline int feature_index(int i, int j, int S, int n, float inv_n, int
     return L * before + inner;
 }
 
+// mu1nu1: rows W + n2 of s_c = sum over species of rows t n + n2 (the
+// summed density of soap.cpp:955-967).  All threads of the workgroup; the
+// caller synchronises before the power spectrum reads them.
+__device__ void species_sums(double* s_c, const MfmaDims& d, int tid, int threads) {
+    const int n = d.n, hp = d.hpad, W = d.Sc * n;
+    for (int i = tid; i < n * hp; i += threads) {
+        const int n2 = i / hp, e = i - n2 * hp;
+        double sum = 0.0;
+        for (int t = 0; t < d.Sc; ++t) sum += s_c[(t * n + n2) * hp + e];
+        s_c[(W + n2) * hp + e] = sum;
+    }
+}
+
 // Power spectrum of the coefficients in LDS on 16x16 Gram tiles.  s_c holds
 // W + 1 rows of d.hpad values (row W and every pad entry are zero), entry
 // (row, l, m') at row*hpad + loff[l] + m'.  The units (tile pair, l), pair-
@@ -188,16 +220,25 @@ __device__ inline int feature_index(int i, int j, int S, int n, float inv_n, int
 // features, and a given feature always comes from the same wavefront.
 // mode 0: write row `row` of out; mode 2: add into the partial row `acc`;
 // mode 3: store into `acc` (the first centre of a run).
+//
+// Compression (soap.cpp:948-996): "mu2" has one coefficient species, so it is
+// the plain layout with Sc = 1; "crossover" keeps the pairs inside a species;
+// "mu1nu1" pairs every channel (t, n1) with the species-summed row n2 (rows W
+// .. W+n-1 of s_c, filled by species_sums), over all (n1, n2).
 __device__ void power_spectrum_tiles(const double* s_c, const int* loff, const MfmaDims& d,
                                      const double* __restrict__ ps_pref, int mode, void* out, int64_t pitch,
                                      int64_t row, double* acc, int wave, int waves) {
     const int lane = threadIdx.x % kWaveThreads;
-    const int W = d.S * d.n;
+    const int W = d.Sc * d.n;
+    const int zero_row = d.crow - 1;
     const int RT = (W + 15) / 16;
+    const bool rect = d.compression == 2;          // A = channels, B = summed rows
+    const int RB = rect ? (d.n + 15) / 16 : RT;
     const int L = d.L;
     const int hp = d.hpad;
-    const float inv_n = 1.0f / static_cast<float>(d.n);
-    const int units = RT * (RT + 1) / 2 * L;
+    const int n = d.n;
+    const float inv_n = 1.0f / static_cast<float>(n);
+    const int units = (rect ? RT * RB : RT * (RT + 1) / 2) * L;
     const int u_begin = wave * units / waves;
     const int u_end = (wave + 1) * units / waves;
     if (u_begin >= u_end) return;
@@ -206,12 +247,17 @@ __device__ void power_spectrum_tiles(const double* s_c, const int* loff, const M
     // upper triangle of tile pairs, and degree l; later units step l, then bj, then bi
     int p = u_begin / L;
     int l = u_begin - p * L;
-    int bi = 0;
-    while (p >= RT - bi) {
-        p -= RT - bi;
-        ++bi;
+    int bi = 0, bj = 0;
+    if (rect) {
+        bi = p / RB;
+        bj = p - bi * RB;
+    } else {
+        while (p >= RT - bi) {
+            p -= RT - bi;
+            ++bi;
+        }
+        bj = bi + p;
     }
-    int bj = bi + p;
     const double* arow = s_c;
     const double* brow = s_c;
     int fb[4] = {-1, -1, -1, -1}, fs[4] = {0, 0, 0, 0};
@@ -219,17 +265,39 @@ __device__ void power_spectrum_tiles(const double* s_c, const int* loff, const M
     for (int u = u_begin; u < u_end; ++u) {
         if (new_pair) {
             new_pair = false;
-            const int ia = min(16 * bi + lane % 16, W);
-            const int jb = min(16 * bj + lane % 16, W);
+            const int ia = 16 * bi + lane % 16 < W ? 16 * bi + lane % 16 : zero_row;
+            const int jrow = rect ? W + 16 * bj + lane % 16 : 16 * bj + lane % 16;
+            const int jlim = rect ? W + n : W;
+            const int jb = jrow < jlim ? jrow : zero_row;
             arow = s_c + ia * hp + lane / 16;
             brow = s_c + jb * hp + lane / 16;
             const int j = 16 * bj + lane % 16;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int i = 16 * bi + lane / 16 + 4 * r;
-                const bool ok = i < W && j < W && i <= j;
                 fs[r] = 0;
-                fb[r] = ok ? feature_index(i, j, d.S, d.n, inv_n, d.L, fs[r]) : -1;
+                fb[r] = -1;
+                if (rect) {
+                    // mu1nu1: i = t n + n1 against summed row j = n2 (soap.cpp:969-981)
+                    if (i < W && j < n) {
+                        const int t = div_small(i, inv_n);
+                        fs[r] = n * n;
+                        fb[r] = t * L * n * n + (i - t * n) * n + j;
+                    }
+                } else if (i < W && j < W && i <= j) {
+                    if (d.compression == 3) {
+                        // crossover: same species only (soap.cpp:983-995)
+                        const int t1 = div_small(i, inv_n), t2 = div_small(j, inv_n);
+                        if (t1 == t2) {
+                            const int n1 = i - t1 * n, n2 = j - t2 * n;
+                            const int same = n * (n + 1) / 2;
+                            fs[r] = same;
+                            fb[r] = t1 * L * same + n1 * n - n1 * (n1 - 1) / 2 + (n2 - n1);
+                        }
+                    } else {
+                        fb[r] = feature_index(i, j, d.Sc, n, inv_n, L, fs[r]);
+                    }
+                }
             }
         }
         const int steps = (2 * l + 4) / 4;
@@ -256,7 +324,12 @@ __device__ void power_spectrum_tiles(const double* s_c, const int* loff, const M
         if (++l == L) {
             l = 0;
             new_pair = true;
-            if (++bj == RT) {
+            if (rect) {
+                if (++bj == RB) {
+                    ++bi;
+                    bj = 0;
+                }
+            } else if (++bj == RT) {
                 ++bi;
                 bj = bi;
             }
@@ -264,10 +337,79 @@ __device__ void power_spectrum_tiles(const double* s_c, const int* loff, const M
     }
 }
 
-// At least 4 wavefronts per SIMD: the register budget (128 VGPRs) the
-// compiler must fit.
-template <int T>
-__global__ __launch_bounds__(T * kWaveThreads, 4) void k_soap_mfma(
+constexpr double kPi = 3.141592653589793238462643383279502884;
+
+// Radial functions of the polynomial basis for the chunk's slots:
+//   G[slot][l*n + k] = sum_q K_l(q; r_slot) w_q r_q^2 g_k(r_q),
+// K_l the Gaussian-smeared radial kernel of polynomial_flir
+// (soap.cpp:450-492) with its l = 0 special case at r <= 1e-14.  Four grid
+// points at a time: one thread per (slot, point) evaluates K_0..K_lmax into
+// s_f, then each (l, 16-slot tile) unit -- one wavefront's -- adds its
+// 16 slots x 4 points x n product, computed on the matrix cores, into s_g.
+// All threads take part (barriers inside).
+__device__ void polynomial_radial(const double* s_r, double* s_f, double* s_g, const MfmaTables& tab,
+                                  const MfmaDims& d, int tid, int wave, int threads, int waves) {
+    const int lane = tid % kWaveThreads;
+    const int L = d.L, n = d.n, Q = d.grid;
+    const int GP = L * n + 1;
+    constexpr int kF = kNb * 4;  // entries of one l in s_f
+    for (int i = tid; i < kNb * GP; i += threads) s_g[i] = 0.0;
+    for (int q0 = 0; q0 < Q; q0 += 4) {
+        // (a workgroup of one wavefront takes two items per thread)
+        for (int item = tid; item < kF; item += threads) {
+            const int slot = item / 4, qq = item - slot * 4, q = q0 + qq;
+            double* f = s_f + slot * 4 + qq;
+            if (q < Q) {
+                const double radius = s_r[slot];
+                const double radial = tab.poly_grid[q];
+                const double eta = d.eta;
+                if (radius <= 1e-14) {
+                    const double radial2 = radial * radial;
+                    f[0] = exp(-eta * radial2);
+                    for (int l = 1; l < L; ++l) f[l * kF] = 0.0;
+                } else {
+                    const double prefactor = 0.25 / (eta * radius * radial);
+                    const double minus = exp(-eta * (radial - radius) * (radial - radius));
+                    const double plus = exp(-eta * (radial + radius) * (radial + radius));
+                    double before = prefactor * (minus - plus);
+                    f[0] = before;
+                    if (L > 1) {
+                        double last = prefactor * (minus + plus - 2.0 * before);
+                        f[kF] = last;
+                        for (int l = 2; l < L; ++l) {
+                            const double value = before - prefactor * (4.0 * l - 2.0) * last;
+                            const double kept = value > 0.0 ? value : 0.0;
+                            f[l * kF] = kept;
+                            before = last;
+                            last = kept;
+                        }
+                    }
+                }
+            } else {
+                for (int l = 0; l < L; ++l) f[l * kF] = 0.0;
+            }
+        }
+        __syncthreads();
+        for (int u = wave; u < 2 * L; u += waves) {
+            const int l = u >> 1, tile = u & 1;
+            const double a = s_f[l * kF + (16 * tile + lane % 16) * 4 + lane / 16];
+            const int q = q0 + lane / 16;
+            const double b = q < Q && lane % 16 < n ? tab.poly_bw[q * n + lane % 16] : 0.0;
+            const d4 g = mfma(a, b, d4{0.0, 0.0, 0.0, 0.0});
+            if (lane % 16 < n) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) s_g[(16 * tile + lane / 16 + 4 * r) * GP + l * n + lane % 16] += g[r];
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// kGeneral adds neighbour weights and the polynomial basis; without them the
+// kernel keeps at least 4 wavefronts per SIMD (a 128-VGPR budget the
+// compiler must fit), with them 2.
+template <int T, bool kGeneral>
+__global__ __launch_bounds__(T * kWaveThreads, kGeneral ? 2 : 4) void k_soap_mfma(
     const double* __restrict__ positions, const int64_t* __restrict__ pair_start, const int32_t* __restrict__ counts,
     const uint32_t* __restrict__ pair_bin, const double* __restrict__ bx, const double* __restrict__ by,
     const double* __restrict__ bz, const MfmaTables tab, const double* __restrict__ ps_pref, MfmaDims d,
@@ -283,18 +425,20 @@ __global__ __launch_bounds__(T * kWaveThreads, 4) void k_soap_mfma(
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWaveThreads);
     constexpr int kThreads = T * kWaveThreads;
     const int H = d.H, L = d.L, S = d.S, n = d.n;
-    const int W = S * n;
     // Y row stride, odd so that the 32 slots of one harmonic store hit distinct
     // bank pairs; entry H stays zero
     const int HP = (H + 1) | 1;
     const int hp = d.hpad;                // padded c row
-    const int cw = (W + 1) * hp;          // c words, including the zero row W
+    const int cw = d.crow * hp;           // c words, including the zero row
+    const int GP = L * n + 1;             // polynomial radial row; entry L*n stays zero
     double* s_y = lds;                    // kNb * HP
-    double* s_d2 = s_y + kNb * HP;        // kNb: d^2 of the chunk's slots
+    double* s_d2 = s_y + kNb * HP;        // kNb: d^2 (GTO) or distance (polynomial) of the chunk's slots
     double* s_tab = s_d2 + kNb;           // 64: 2^(j/64) for exp_neg
     double* s_c = s_tab + 64;             // cw (coefficients of the current centre, padded)
     double* s_csum = s_c + cw;            // cw (inner average only)
-    int* s_loff = reinterpret_cast<int*>(s_csum + (d.mode == 1 ? cw : 0)); // L + 1
+    double* s_g = s_csum + (d.mode == 1 ? cw : 0);     // polynomial: kNb * GP radial functions
+    double* s_f = s_g + (d.radial == 1 ? kNb * GP : 0); // polynomial: L * kNb * 4 radial kernels
+    int* s_loff = reinterpret_cast<int*>(s_f + (d.radial == 1 ? L * kNb * 4 : 0)); // L + 1
     int* s_seg = s_loff + (L + 1);        // S + 1: first row of each species segment of the centre
     int* s_pseg = s_seg + (S + 1);        // S + 1: first slot of each segment (padded to 4)
     int* s_step = s_pseg + (S + 1);       // 1: species of the chunk's MFMA steps, 4 bits each
@@ -316,12 +460,13 @@ __global__ __launch_bounds__(T * kWaveThreads, 4) void k_soap_mfma(
     // operands (which carry the radial prefactors) and the destination of
     // result row lane/16 + 4r (or -1 off the diagonal)
     const bool has_tile = wave < d.tiles;
-    int ycol = H, dst[4] = {-1, -1, -1, -1};
+    int ycol = H, gcol = GP - 1, dst[4] = {-1, -1, -1, -1};
     double expo = 0.0, bfold[4] = {0.0, 0.0, 0.0, 0.0};
     if (has_tile) {
         const int rc = tab.row_channel[wave * 16 + lane % 16];
         const int ch = tab.col_harmonic[wave * 16 + lane % 16];
         ycol = ch >= 0 ? ch : H;
+        gcol = rc >= 0 ? rc : GP - 1;
         expo = rc >= 0 ? tab.expo[rc] : 0.0;
         const int lh = ch >= 0 ? degree_of_harmonic(ch) : -1;
 #pragma unroll
@@ -395,9 +540,11 @@ __global__ __launch_bounds__(T * kWaveThreads, 4) void k_soap_mfma(
                 }
             }
             __syncthreads();
-            // an empty species leaves its coefficients at zero
-            for (int q = 0; q < S; ++q) {
-                if (s_seg[q + 1] == s_seg[q]) {
+            // an empty species leaves its coefficients at zero (mu2: one block
+            // for every species, empty only without neighbours)
+            for (int q = 0; q < d.Sc; ++q) {
+                const bool empty = d.Sc == S ? s_seg[q + 1] == s_seg[q] : s_seg[S] == 0;
+                if (empty) {
                     double* cdst = s_c + q * n * hp;
                     for (int i = tid; i < n * hp; i += kThreads) cdst[i] = 0.0;
                 }
@@ -415,6 +562,14 @@ __global__ __launch_bounds__(T * kWaveThreads, 4) void k_soap_mfma(
             // of the next chunk (stale, finite values in pad slots)
             double px = 0.0, py = 0.0, pz = 0.0;
             int prow, pq;
+            bool pself = false;
+            // exact self image (NeighborView::exact_self, neighbor.cpp:683-689):
+            // the centre's own atom under the zero shift; only w0 needs it
+            auto exact_self = [&](uint32_t b) {
+                if (tab.bin_atom[b] != static_cast<int32_t>(centre)) return false;
+                const ImageDesc& image = tab.images[tab.bin_image[b]];
+                return image.n[0] == 0 && image.n[1] == 0 && image.n[2] == 0;
+            };
             {
                 prow = slot_row(lane / 2, pq);
                 if (prow >= 0) {
@@ -422,6 +577,7 @@ __global__ __launch_bounds__(T * kWaveThreads, 4) void k_soap_mfma(
                     px = bx[b];
                     py = by[b];
                     pz = bz[b];
+                    if (kGeneral && d.has_w0) pself = exact_self(b);
                 }
             }
             // the accumulator holds the partial contraction of species `cur`; it
@@ -452,11 +608,31 @@ __global__ __launch_bounds__(T * kWaveThreads, 4) void k_soap_mfma(
                     const double dx = px - cx;
                     const double dy = py - cy;
                     const double dz = pz - cz;
+                    const double d2 = dx * dx + dy * dy + dz * dz;
+                    // seed scale: 0 for pad slots, else the neighbour's weight
+                    double scale = prow >= 0 ? 1.0 : 0.0;
+                    if (kGeneral && d.weighted && prow >= 0) {
+                        scale = neighbour_weight(d, sqrt(d2), pself, tab.species_w[pq]);
+                    }
+                    double hx = dx, hy = dy, hz = dz, slot_value = d2;
+                    if (kGeneral && d.radial == 1) {
+                        // polynomial: harmonics of the direction, times 4 pi w (soap.cpp:833-836);
+                        // the radial functions need the distance
+                        const double radius = sqrt(d2);
+                        const double inverse = radius <= 1e-14 ? 0.0 : 1.0 / radius;
+                        hx = dx * inverse;
+                        hy = dy * inverse;
+                        hz = dz * inverse;
+                        scale *= 4.0 * kPi;
+                        slot_value = radius;
+                    }
                     if (wave == 0) {
-                        if (comp == 0) s_d2[jj] = dx * dx + dy * dy + dz * dz;
-                        // species of the 8 MFMA steps, 4 bits each, from the lanes
-                        // holding slots 0, 4, .., 28 (lanes 0, 8, .., 56)
-                        uint32_t bits = lane % 8 == 0 ? static_cast<uint32_t>(pq) << (4 * (lane / 8)) : 0u;
+                        if (comp == 0) s_d2[jj] = slot_value;
+                        // coefficient species of the 8 MFMA steps, 4 bits each, from the
+                        // lanes holding slots 0, 4, .., 28 (lanes 0, 8, .., 56); mu2
+                        // sums every species into block 0
+                        const int qc = d.Sc == S ? pq : 0;
+                        uint32_t bits = lane % 8 == 0 ? static_cast<uint32_t>(qc) << (4 * (lane / 8)) : 0u;
                         bits |= __shfl_xor(bits, 8);
                         bits |= __shfl_xor(bits, 16);
                         bits |= __shfl_xor(bits, 32);
@@ -474,9 +650,12 @@ __global__ __launch_bounds__(T * kWaveThreads, 4) void k_soap_mfma(
                     // addresses derived from it are not held across the loop
                     int part = comp;
                     asm volatile("" : "+v"(part));
-                    harmonics_q(dx, dy, dz, prow >= 0, lm, mk, part, &kHarmonic + zero, s_y + jj * HP);
+                    harmonics_q(hx, hy, hz, scale, lm, mk, part, &kHarmonic + zero, s_y + jj * HP);
                 }
                 __syncthreads();
+                if (kGeneral && d.radial == 1) {
+                    polynomial_radial(s_d2, s_f, s_g, tab, d, tid, wave, kThreads, T);
+                }
                 {
                     // issue the loads of the next chunk now
                     prow = slot_row(j0 + kNb + lane / 2, pq);
@@ -485,6 +664,7 @@ __global__ __launch_bounds__(T * kWaveThreads, 4) void k_soap_mfma(
                         px = bx[b];
                         py = by[b];
                         pz = bz[b];
+                        if (kGeneral && d.has_w0) pself = exact_self(b);
                     }
                 }
                 if (has_tile) {
@@ -498,7 +678,7 @@ __global__ __launch_bounds__(T * kWaveThreads, 4) void k_soap_mfma(
 #pragma unroll
                         for (int s = 0; s < 4; ++s) {
                             const int jj = 4 * (h + s) + lane / 16;
-                            av[s] = exp_neg(-expo * s_d2[jj], s_tab);
+                            av[s] = !kGeneral || d.radial == 0 ? exp_neg(-expo * s_d2[jj], s_tab) : s_g[jj * GP + gcol];
                             yv[s] = s_y[jj * HP + ycol];
                         }
 #pragma unroll
@@ -521,6 +701,10 @@ __global__ __launch_bounds__(T * kWaveThreads, 4) void k_soap_mfma(
             // the next centre's metadata arrives while this one's power spectrum runs
             prefetch_centre(centre + 1);
             __syncthreads();
+            if (d.compression == 2 && d.mode != 1) {
+                species_sums(s_c, d, tid, kThreads);
+                __syncthreads();
+            }
             if (d.mode == 0) {
                 power_spectrum_tiles(s_c, s_loff, d, ps_pref, 0, out, pitch, centre, nullptr, wave, T);
             } else if (d.mode == 1) {
@@ -544,8 +728,7 @@ __global__ __launch_bounds__(kWaveThreads) void k_mfma_finalize_inner(const doub
                                                                      const MfmaTables tab, MfmaDims d, void* out,
                                                                      int64_t pitch) {
     extern __shared__ double lds[];
-    const int W = d.S * d.n;
-    const int cw = (W + 1) * d.hpad;
+    const int cw = d.crow * d.hpad;
     double* s_c = lds;
     int* s_loff = reinterpret_cast<int*>(s_c + cw);
     if (threadIdx.x == 0) {
@@ -565,6 +748,10 @@ __global__ __launch_bounds__(kWaveThreads) void k_mfma_finalize_inner(const doub
             s_c[i] = natoms > 0 ? sum * inv : 0.0;
         }
         __syncthreads();
+        if (d.compression == 2) {
+            species_sums(s_c, d, threadIdx.x, kWaveThreads);
+            __syncthreads();
+        }
         power_spectrum_tiles(s_c, s_loff, d, tab.ps_pref, 0, out, pitch, s, nullptr, 0, 1);
         __syncthreads();
     }
@@ -588,7 +775,9 @@ template <int T>
 void launch(hipStream_t stream, unsigned grid, int64_t per_block, size_t lds, const PreparedBatch& pb,
             const DeviceGraph& g, const MfmaTables& tab, const MfmaDims& d, const int64_t* item_begin, int64_t base,
             int64_t count, void* out, int64_t pitch, double* partial) {
-    hipLaunchKernelGGL((k_soap_mfma<T>), dim3(grid), dim3(T * kWaveThreads), lds, stream, pb.d_positions.as<double>(),
+    const bool general = d.weighted != 0 || d.radial != 0;
+    auto kernel = general ? k_soap_mfma<T, true> : k_soap_mfma<T, false>;
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(T * kWaveThreads), lds, stream, pb.d_positions.as<double>(),
                        g.pair_start.as<int64_t>(), g.counts.as<int32_t>(), g.pair_bin.as<uint32_t>(), g.bin_x.as<double>(),
                        g.bin_y.as<double>(), g.bin_z.as<double>(), tab, tab.ps_pref, d, item_begin, base,
                        count, per_block, out, pitch, partial);
@@ -702,10 +891,10 @@ int mfma_padded_row(int l_max) {
 }
 
 size_t mfma_lds_bytes(const MfmaDims& d) {
-    const size_t W = static_cast<size_t>(d.S) * d.n;
-    const size_t cw = (W + 1) * static_cast<size_t>(d.hpad);
+    const size_t cw = static_cast<size_t>(d.crow) * static_cast<size_t>(d.hpad);
     size_t words = static_cast<size_t>(kNb) * ((d.H + 1) | 1) + kNb + 64 + cw;
     if (d.mode == 1) words += cw;
+    if (d.radial == 1) words += static_cast<size_t>(kNb) * (d.L * d.n + 1) + static_cast<size_t>(d.L) * kNb * 4;
     return words * sizeof(double) + static_cast<size_t>(d.L + 1 + 2 * (d.S + 1) + 1) * sizeof(int);
 }
 
@@ -755,7 +944,7 @@ void launch_mfma_finalize(hipStream_t stream, const PreparedBatch& pb, const Mfm
                           const double* partial, const int64_t* struct_items, void* out, int64_t pitch) {
     const unsigned grid = static_cast<unsigned>(std::min<int64_t>(pb.structures, 1 << 20));
     if (d.mode == 1) {
-        const size_t lds = (static_cast<size_t>(d.S) * d.n + 1) * d.hpad * sizeof(double)
+        const size_t lds = static_cast<size_t>(d.crow) * d.hpad * sizeof(double)
             + static_cast<size_t>(d.L + 2) * sizeof(int);
         hipLaunchKernelGGL(k_mfma_finalize_inner, dim3(grid), dim3(kWaveThreads), lds, stream, partial, struct_items,
                            pb.d_offsets.as<int64_t>(), pb.structures, tab, d, out, pitch);

@@ -12,11 +12,9 @@ Mirrors the reference's public class and its validation kernel:
   the device plugin exactly as ``_cuda_payload`` is (``core.py:331-355``,
   ``adapter.py:528-603``), keyed ``_hip_*`` here.
 
-The GPU library implements the options the SOAP hot path uses: the GTO radial
-basis, no distance weighting, no compression and unit species weights.  Other
-values are valid SOAP options that this device does not run; they are rejected
-at construction with ``code="unsupported_option"``, as the reference does for
-options a device lacks.
+Every SOAP option of the reference runs on the GPU: both radial bases (GTO
+and polynomial), distance weighting (poly, pow, exp, w0), species weights and
+the four compression modes, on the matrix-core kernel.
 """
 
 from __future__ import annotations
@@ -33,7 +31,7 @@ from ..core.errors import DescriptorConfigError, DescriptorInputError
 from ..core.options import CONFIGURATION_SCHEMA_VERSION, ExecutionOptions, OutputOptions, coerce_options
 from ..core.result import DescriptorResult, format_values, metadata_envelope, owned_values
 from ..core.species import require_species, validate_batch_species
-from .basis import basis_gto
+from .basis import basis_gto, basis_polynomial
 
 # Limits of the HIP library (mdx_hip_soap_plan_create): species, radial
 # channels and coefficient storage per centre.
@@ -210,27 +208,25 @@ class SoapSettings:
     def hip_payload(self) -> dict[str, Any]:
         """Radial basis, labels and width for the device plugin (core.py:331-355)."""
 
-        alphas, betas = basis_gto(self.r_cut, self.n_max, self.l_max)
+        if self.rbf == "gto":
+            alphas, betas = basis_gto(self.r_cut, self.n_max, self.l_max)
+            radial = {"alphas": alphas, "betas": betas}
+        else:
+            grid, weights, values = basis_polynomial(self.r_cut, self.n_max)
+            radial = {"radial_grid": grid, "radial_weights": weights, "radial_values": values}
         return {
-            "radial_basis": {"alphas": alphas, "betas": betas},
+            "radial_basis": radial,
             "feature_count": self.feature_count,
             "labels": self.labels(),
         }
 
     def hip_unsupported(self) -> tuple[str, str] | None:
-        """First option the HIP library does not implement, as (path, reason)."""
+        """First option the HIP library does not implement, as (path, reason):
+        none since every option runs on the device.  The species weighting
+        must name exactly the configured species (core.py:262-265)."""
 
-        if self.rbf != "gto":
-            return "rbf", "the HIP SOAP kernels implement the GTO radial basis"
-        if self.weighting:
-            return "weighting", "the HIP SOAP kernels implement unweighted densities"
-        if self.compression_mode != "off":
-            return "compression", "the HIP SOAP kernels implement the uncompressed power spectrum"
-        if self.species_weighting is not None:
-            if set(self.species_weighting) != set(self.species):
-                raise ValueError("species_weighting must contain exactly the configured species")
-            if any(float(v) != 1.0 for v in self.species_weighting.values()):
-                return "compression", "the HIP SOAP kernels implement unit species weights"
+        if self.species_weighting is not None and {int(k) for k in self.species_weighting} != set(self.species):
+            raise ValueError("species_weighting must contain exactly the configured species")
         return None
 
 
@@ -288,6 +284,7 @@ class SOAP(Descriptor):
         backend_options: dict[str, Any] = {
             "species": list(settings.species), "n_max": settings.n_max, "l_max": settings.l_max,
             "r_cut": settings.r_cut, "sigma": settings.sigma, "average": settings.average,
+            "rbf": settings.rbf, "weighting": dict(settings.weighting), "compression": dict(settings.compression),
             "output": self._output_options.to_dict(), "execution": self._execution_options.to_dict(),
             "_hip_payload": payload, "_hip_labels": payload["labels"], "_hip_feature_count": settings.feature_count,
         }

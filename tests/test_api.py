@@ -91,18 +91,28 @@ def test_unknown_device_is_invalid():
     assert info.value.code == "invalid_device"
 
 
-@pytest.mark.parametrize("kwargs,path", [
-    (dict(rbf="polynomial"), "rbf"),
-    (dict(weighting={"function": "poly", "r0": 4.0, "c": 1.0, "m": 2.0}), "weighting"),
-    (dict(weighting={"w0": 0.5}), "weighting"),
-    (dict(compression={"mode": "mu2"}), "compression"),
-    (dict(compression={"mode": "off", "species_weighting": {1: 2.0, 8: 1.0}}), "compression"),
+@pytest.mark.parametrize("kwargs,features", [
+    (dict(rbf="polynomial"), (2 * 8) * (2 * 8 + 1) // 2 * 7),
+    (dict(weighting={"function": "poly", "r0": 4.0, "c": 1.0, "m": 2.0}), (2 * 8) * (2 * 8 + 1) // 2 * 7),
+    (dict(weighting={"w0": 0.5}), (2 * 8) * (2 * 8 + 1) // 2 * 7),
+    (dict(compression={"mode": "mu2"}), 8 * 9 // 2 * 7),
+    (dict(compression={"mode": "mu1nu1"}), 2 * 8 * 8 * 7),
+    (dict(compression={"mode": "crossover"}), 2 * 8 * 9 // 2 * 7),
+    (dict(compression={"mode": "off", "species_weighting": {1: 2.0, 8: 1.0}}), (2 * 8) * (2 * 8 + 1) // 2 * 7),
 ])
-def test_options_outside_the_hip_kernels_are_rejected(kwargs, path):
+def test_every_soap_option_is_accepted(kwargs, features):
+    """Weighting, compression, species weights and the polynomial basis run on
+    the device; the width follows soap_features (soap.cpp:373-387)."""
+
+    soap = mdx.SOAP(species=[1, 8], r_cut=5.0, **kwargs)
+    assert soap.feature_count == features
+    assert len(soap.settings.labels()) == features
+
+
+def test_species_weighting_must_name_the_species():
     with pytest.raises(mdx.DescriptorConfigError) as info:
-        mdx.SOAP(species=[1, 8], r_cut=5.0, **kwargs)
-    assert info.value.code == "unsupported_option"
-    assert list(info.value.path) == ["parameters", path]
+        mdx.SOAP(species=[1, 8], r_cut=5.0, compression={"mode": "off", "species_weighting": {1: 2.0}})
+    assert info.value.code == "invalid_configuration"
 
 
 def test_unit_species_weights_are_accepted():
