@@ -225,14 +225,17 @@ __device__ void species_sums(double* s_c, const MfmaDims& d, int tid, int thread
 // the plain layout with Sc = 1; "crossover" keeps the pairs inside a species;
 // "mu1nu1" pairs every channel (t, n1) with the species-summed row n2 (rows W
 // .. W+n-1 of s_c, filled by species_sums), over all (n1, n2).
-__device__ void power_spectrum_tiles(const double* s_c, const int* loff, const MfmaDims& d,
-                                     const double* __restrict__ ps_pref, int mode, void* out, int64_t pitch,
-                                     int64_t row, double* acc, int wave, int waves) {
+// kPaired: mu1nu1 or crossover; the plain walk (off, mu2) is compiled without
+// their branches.
+template <bool kPaired>
+__device__ void power_spectrum_walk(const double* s_c, const int* loff, const MfmaDims& d,
+                                    const double* __restrict__ ps_pref, int mode, void* out, int64_t pitch,
+                                    int64_t row, double* acc, int wave, int waves) {
     const int lane = threadIdx.x % kWaveThreads;
     const int W = d.Sc * d.n;
     const int zero_row = d.crow - 1;
     const int RT = (W + 15) / 16;
-    const bool rect = d.compression == 2;          // A = channels, B = summed rows
+    const bool rect = kPaired && d.compression == 2; // A = channels, B = summed rows
     const int RB = rect ? (d.n + 15) / 16 : RT;
     const int L = d.L;
     const int hp = d.hpad;
@@ -285,7 +288,7 @@ __device__ void power_spectrum_tiles(const double* s_c, const int* loff, const M
                         fb[r] = t * L * n * n + (i - t * n) * n + j;
                     }
                 } else if (i < W && j < W && i <= j) {
-                    if (d.compression == 3) {
+                    if (kPaired && d.compression == 3) {
                         // crossover: same species only (soap.cpp:983-995)
                         const int t1 = div_small(i, inv_n), t2 = div_small(j, inv_n);
                         if (t1 == t2) {
@@ -334,6 +337,16 @@ __device__ void power_spectrum_tiles(const double* s_c, const int* loff, const M
                 bj = bi;
             }
         }
+    }
+}
+
+__device__ inline void power_spectrum_tiles(const double* s_c, const int* loff, const MfmaDims& d,
+                                            const double* __restrict__ ps_pref, int mode, void* out, int64_t pitch,
+                                            int64_t row, double* acc, int wave, int waves) {
+    if (d.compression >= 2) {
+        power_spectrum_walk<true>(s_c, loff, d, ps_pref, mode, out, pitch, row, acc, wave, waves);
+    } else {
+        power_spectrum_walk<false>(s_c, loff, d, ps_pref, mode, out, pitch, row, acc, wave, waves);
     }
 }
 
