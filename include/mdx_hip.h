@@ -190,6 +190,38 @@ int mdx_hip_neighbors_build(mdx_hip_ctx* ctx, const mdx_batch_view* batch, doubl
 int mdx_hip_neighbors_fetch(mdx_hip_ctx* ctx, int64_t* offsets, int32_t* neighbors, int32_t* shifts,
                             double* displacements, double* distance2);
 
+/* NeighborList descriptor on the device.  Replaces compute_neighbor_list
+ * (cpp/src/standalone/neighbor_list.cpp:15-78; declared in
+ * cpp/include/mdescriptor/local_descriptors.hpp:54-60) as bound by
+ * _cpp.compute_neighbor_list (cpp/src/bindings/module.cpp:772-798, 1012) and
+ * the CUDA plugin's NeighborList branch (cpp/cuda/src/backend.cu:358-471).
+ * Every centre's pairs within cutoff (boundary inclusive), in the
+ * reference's order, centre-major over the batch; the exact self pair (same
+ * atom, zero shift) is dropped unless self_pairs != 0, and with
+ * full_neighbor_list == 0 only the orientation kept by keep_half_neighbor
+ * (cpp/include/mdescriptor/detail/neighbor_filter.hpp:18-38) remains.
+ * mdx_hip_neighbor_list computes the list on the device, keeps it on the
+ * context and returns its pair count in *pairs; cancel_flag as for
+ * mdx_hip_soap_compute.  A non-finite or non-positive cutoff is rejected with
+ * the reference's message. */
+int mdx_hip_neighbor_list(mdx_hip_ctx* ctx, const mdx_batch_view* batch, double cutoff, int32_t full_neighbor_list,
+                          int32_t self_pairs, const volatile int32_t* cancel_flag, int64_t* pairs);
+
+/* Writes the last neighbour list of the context.  Any pointer may be NULL
+ * (that output is skipped) and each may be host or device memory (device
+ * memory is written in place by the kernel):
+ *   table   f64[pairs*9]  DescriptorPairTable rows (local_descriptors.hpp:29-34):
+ *                         centre, neighbour (global atom indices), cell
+ *                         shifts a b c, dx dy dz, distance
+ *   values  f64[pairs*4]  dx dy dz distance, the public result's values
+ *                         (src/mdescriptor/descriptors/_kernels/local.py:98-110)
+ *   samples i64[pairs*6]  structure, local centre, local neighbour, shifts
+ *                         a b c (pair_samples, src/mdescriptor/core/result.py:257-300)
+ *   offsets i64[structures+1]  first pair of each structure
+ *                         (DescriptorPairTable::offsets). */
+int mdx_hip_neighbor_list_fetch(mdx_hip_ctx* ctx, double* table, double* values, int64_t* samples,
+                                int64_t* offsets);
+
 /* Page-locked host memory for result matrices.  mdx_hip_soap_compute copies
  * into such a buffer with one DMA at the full PCIe rate; into pageable memory
  * it stages through the context's pinned ring and copies out on host threads.

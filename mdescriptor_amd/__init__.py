@@ -3,7 +3,8 @@
 The public names match the reference package (``src/mdescriptor/__init__.py``)
 for the SOAP path: build a :class:`StructureBatch`, construct
 ``SOAP(species=..., r_cut=..., execution=ExecutionOptions(device="hip"))`` and
-call ``compute``.  All numerical work runs in the HIP library
+call ``compute``.  ``NeighborList`` gives the same device graph as a
+pair-level result.  All numerical work runs in the HIP library
 ``mdescriptor_amd/_lib/libmdx_hip.so`` (C-ABI declared in
 ``include/mdx_hip.h``); there is no CPU execution path.
 """
@@ -22,6 +23,7 @@ from .core.errors import (
 from .core.input import StructureBatch
 from .core.options import ExecutionOptions, OutputOptions
 from .core.result import DescriptorLevel, DescriptorResult
+from .descriptors.neighbor_list import NeighborList
 from .descriptors.soap import SOAP
 
 __version__ = "0.1.0"
@@ -36,6 +38,7 @@ __all__ = [
     "DescriptorResult",
     "ExecutionOptions",
     "MDescriptorError",
+    "NeighborList",
     "OutputOptions",
     "SOAP",
     "StructureBatch",

@@ -200,6 +200,14 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         ctypes.c_int,
         [ctypes.c_void_p, _i64p, _i32p, _i32p, _f64p, _f64p],
     ),
+    "mdx_hip_neighbor_list": (
+        ctypes.c_int,
+        [ctypes.c_void_p, ctypes.POINTER(BatchView), ctypes.c_double, ctypes.c_int32, ctypes.c_int32, _i32p, _i64p],
+    ),
+    "mdx_hip_neighbor_list_fetch": (
+        ctypes.c_int,
+        [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p],
+    ),
     "mdx_hip_host_alloc": (ctypes.c_int, [ctypes.c_size_t, ctypes.POINTER(ctypes.c_void_p)]),
     "mdx_hip_host_free": (None, [ctypes.c_void_p]),
     "mdx_hip_version": (ctypes.c_char_p, []),
@@ -509,6 +517,42 @@ def neighbor_graph(context: Context, batch: Any, cutoff: float, *, include_bound
     }
 
 
+def neighbor_list(context: Context, batch: Any, cutoff: float, *, full_neighbor_list: bool = True,
+                  self_pairs: bool = False, cancel: ctypes.c_int32 | None = None, table: bool = False,
+                  values: bool = True, samples: bool = True) -> dict[str, np.ndarray]:
+    """NeighborList of a batch on the device (``mdx_hip_neighbor_list``).
+
+    Returns ``offsets`` (first pair of each structure) and, as asked,
+    ``table`` (rows x 9, the layout of ``_cpp.compute_neighbor_list``,
+    ``cpp/src/bindings/module.cpp:772-798``), ``values`` (rows x 4: dx, dy,
+    dz, distance) and ``samples`` (rows x 6: structure, local centre, local
+    neighbour, cell shifts), the last two in page-locked memory."""
+
+    arrays = _BatchArrays(batch)
+    lib = context.lib
+    rows = ctypes.c_int64()
+    flag = ctypes.pointer(cancel) if cancel is not None else None
+    context.check(lib.mdx_hip_neighbor_list(context.handle, ctypes.byref(arrays.view), float(cutoff),
+                                            1 if full_neighbor_list else 0, 1 if self_pairs else 0, flag,
+                                            ctypes.byref(rows)))
+    n = int(rows.value)
+    result: dict[str, np.ndarray] = {"offsets": np.zeros(len(arrays.offsets), dtype=np.int64)}
+    if table:
+        result["table"] = pinned_empty((n, 9), np.float64)
+    if values:
+        result["values"] = pinned_empty((n, 4), np.float64)
+    if samples:
+        result["samples"] = pinned_empty((n, 6), np.int64)
+
+    def address(key: str) -> Any:
+        array = result.get(key)
+        return None if array is None or array.size == 0 else array.ctypes.data_as(ctypes.c_void_p)
+
+    context.check(lib.mdx_hip_neighbor_list_fetch(context.handle, address("table"), address("values"),
+                                                  address("samples"), address("offsets")))
+    return result
+
+
 _contexts: dict[int, Context] = {}
 
 
@@ -596,6 +640,61 @@ class Backend:
             self._closed = True
 
 
+class NeighborListBackend:
+    """NeighborList on one HIP device, the counterpart of the CUDA plugin's
+    NeighborList branch (``cpp/cuda/src/backend.cu:358-471``): pair-level
+    values (dx, dy, dz, distance), per-structure row offsets and, instead of
+    the raw pair records, the pair samples already in the public
+    ``[structure, local_i, local_j, sa, sb, sc]`` form."""
+
+    feature_count = 4
+    labels = ("dx", "dy", "dz", "distance")
+
+    def __init__(self, name: str, options: Mapping[str, Any]) -> None:
+        self.name = name
+        self.options = dict(options)
+        self.cutoff = float(options.get("cutoff", 6.0))
+        self.full_neighbor_list = bool(options.get("full_neighbor_list", True))
+        self.self_pairs = bool(options.get("self_pairs", False))
+        execution = options.get("execution") or {}
+        self._num_threads = (execution.get("num_threads") if isinstance(execution, Mapping)
+                             else getattr(execution, "num_threads", None))
+        self._context = shared_context(0)
+        self._lock = threading.Lock()
+        self._closed = False
+        self.last_timing: dict[str, float] = {}
+
+    def metadata(self) -> dict[str, Any]:
+        return {
+            "descriptor": self.name,
+            "backend": "mdescriptor-hip",
+            "execution": {"device": "hip", "num_threads": self._num_threads},
+        }
+
+    def compute(self, batch: Any, control: Any = None, out: np.ndarray | None = None) -> dict[str, Any]:
+        if out is not None:
+            raise ValueError("the NeighborList backend allocates its own pair-level output")
+        with self._lock:
+            if self._closed:
+                raise RuntimeError("HIP backend is closed")
+            flag = getattr(control, "_hip_cancel_flag", None) if control is not None else None
+            raw = neighbor_list(self._context, batch, self.cutoff, full_neighbor_list=self.full_neighbor_list,
+                                self_pairs=self.self_pairs, cancel=flag)
+            return {
+                "values": raw["values"],
+                "level": "pair",
+                "row_offsets": raw["offsets"],
+                "samples": raw["samples"],
+                "labels": self.labels,
+                "metadata": self.metadata(),
+                "_mdescriptor_owned_values": True,
+            }
+
+    def close(self) -> None:
+        with self._lock:
+            self._closed = True
+
+
 def plan_options(options: Mapping[str, Any], species: list[int], radial: Mapping[str, Any]) -> dict | None:
     """The SoapPlan options of a backend configuration: the canonical
     ``weighting`` mapping, ``compression`` (mode and ``species_weighting``,
@@ -627,9 +726,11 @@ def plan_options(options: Mapping[str, Any], species: list[int], radial: Mapping
     return result or None
 
 
-def create_backend(name: str, options: Mapping[str, Any]) -> Backend:
+def create_backend(name: str, options: Mapping[str, Any]) -> Backend | NeighborListBackend:
     """Plugin factory, the counterpart of ``_cuda.create_backend`` (bindings.cu:30-40)."""
 
+    if name == "NeighborList":
+        return NeighborListBackend(name, options)
     return Backend(name, options)
 
 
@@ -646,10 +747,12 @@ __all__ = [
     "HipOutOfMemory",
     "HipUnavailable",
     "MODEL_SNAPSHOT_ABI",
+    "NeighborListBackend",
     "SoapPlan",
     "create_backend",
     "load_library",
     "neighbor_graph",
+    "neighbor_list",
     "shared_context",
 ]
 

@@ -16,7 +16,8 @@ writes its rows straight into one preallocated output matrix.
 
 from __future__ import annotations
 
-from collections.abc import Mapping
+from collections.abc import Iterator, Mapping
+from contextlib import contextmanager
 from typing import Any
 
 import numpy as np
@@ -48,17 +49,37 @@ def structure_blocks(offsets: np.ndarray, budget: int = ATOM_BUDGET) -> list[tup
     return blocks
 
 
+@contextmanager
+def _plugin_errors() -> Iterator[None]:
+    """Map plugin failures onto the public error schema (errors.py:83-145)."""
+
+    try:
+        yield
+    except MDescriptorError:
+        raise
+    except Exception as exc:
+        if isinstance(exc, _hip.HipCancelledError):
+            raise CancelledError("descriptor computation was cancelled") from exc
+        if isinstance(exc, ValueError):
+            raise
+        raise translate_backend_error(exc, unavailable_message="HIP backend is unavailable",
+                                      failure_message="HIP backend failed") from exc
+
+
 class HipBackend:
-    """Lazy proxy for the HIP plugin."""
+    """Lazy proxy for the HIP plugin.  ``level="pair"`` selects the pair-level
+    contract (NeighborList): per-block results are concatenated, since the
+    row count is known only after the device has filtered the pairs."""
 
     def __init__(self, name: str, options: Mapping[str, Any], feature_count: int | None = None,
-                 atom_budget: int = ATOM_BUDGET) -> None:
+                 atom_budget: int = ATOM_BUDGET, level: str | None = None) -> None:
         self.name = name
         self.options = dict(options)
         self._feature_count = feature_count
         self._implementation: Any = None
         self._closed = False
         self.atom_budget = int(atom_budget)
+        self.level = level
         self.last_timing: dict[str, float] = {}
 
     @property
@@ -77,6 +98,8 @@ class HipBackend:
 
     def compute(self, batch: Any, control: Any = None) -> dict[str, Any]:
         implementation = self._ensure_implementation()
+        if self.level == "pair":
+            return self._compute_pairs(implementation, batch, control)
         average = str(self.options.get("average", "inner"))
         dtype = np.dtype((self.options.get("output") or {}).get("dtype", "float64"))
         level = "atom" if average == "off" else "structure"
@@ -86,7 +109,7 @@ class HipBackend:
         if control is not None:
             control.reset(batch.structures)
         timing: dict[str, float] = {}
-        try:
+        with _plugin_errors():
             for start, stop in blocks:
                 if control is not None and control.cancelled():
                     raise CancelledError("descriptor computation was cancelled")
@@ -102,15 +125,6 @@ class HipBackend:
                 if control is not None:
                     for _ in range(stop - start):
                         control.mark_completed()
-        except MDescriptorError:
-            raise
-        except Exception as exc:
-            if isinstance(exc, _hip.HipCancelledError):
-                raise CancelledError("descriptor computation was cancelled") from exc
-            if isinstance(exc, ValueError):
-                raise
-            raise translate_backend_error(exc, unavailable_message="HIP backend is unavailable",
-                                          failure_message="HIP backend failed") from exc
         self.last_timing = timing
         result: dict[str, Any] = {
             "values": values,
@@ -121,6 +135,50 @@ class HipBackend:
         if level == "atom":
             result["row_offsets"] = np.asarray(batch.offsets, dtype=np.int64).copy()
         return result
+
+    def _compute_pairs(self, implementation: Any, batch: Any, control: Any) -> dict[str, Any]:
+        """Pair-level rows of every block, in structure order; block samples
+        count structures from the block's first one and are shifted here,
+        as the reference shifts its chunks' pair records (backends.py:230-241,
+        460-462)."""
+
+        width = int(self._feature_count or 0)
+        if control is not None:
+            control.reset(batch.structures)
+        parts: list[dict[str, Any]] = []
+        starts: list[int] = []
+        with _plugin_errors():
+            for start, stop in structure_blocks(batch.offsets, self.atom_budget):
+                if control is not None and control.cancelled():
+                    raise CancelledError("descriptor computation was cancelled")
+                block = batch if (start, stop) == (0, batch.structures) else batch._slice_view(start, stop)
+                parts.append(implementation.compute(block, control))
+                starts.append(start)
+                if control is not None:
+                    for _ in range(stop - start):
+                        control.mark_completed()
+        if len(parts) == 1:
+            values, samples, row_offsets = parts[0]["values"], parts[0]["samples"], parts[0]["row_offsets"]
+        else:
+            values = np.concatenate([p["values"] for p in parts]) if parts else np.empty((0, width))
+            shifted = []
+            for part, start in zip(parts, starts):
+                block_samples = np.array(part["samples"], dtype=np.int64, copy=True)
+                block_samples[:, 0] += start
+                shifted.append(block_samples)
+            samples = np.concatenate(shifted) if shifted else np.empty((0, 6), dtype=np.int64)
+            row_offsets = np.zeros(batch.structures + 1, dtype=np.int64)
+            for part, start in zip(parts, starts):
+                local = np.asarray(part["row_offsets"], dtype=np.int64)
+                row_offsets[start + 1:start + len(local)] = local[1:] + row_offsets[start]
+        return {
+            "values": values,
+            "level": "pair",
+            "labels": tuple(getattr(implementation, "labels", ()) or ()),
+            "row_offsets": np.asarray(row_offsets, dtype=np.int64),
+            "samples": samples,
+            "metadata": implementation.metadata(),
+        }
 
     def metadata(self) -> Mapping[str, Any]:
         if self._implementation is None:

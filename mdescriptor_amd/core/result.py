@@ -136,7 +136,8 @@ def _json_safe(value: Any) -> Any:
 
 def metadata_envelope(raw: Mapping[str, Any], level: str, feature_count: int | None) -> dict[str, Any]:
     """The fixed metadata envelope of a result (result.py:504-560): descriptor,
-    backend, output, execution, level, feature_count and backend ``details``."""
+    backend, output, execution, level, feature_count and, when there are
+    any, the backend ``details``."""
 
     data = _json_safe(dict(raw))
     descriptor = data.pop("descriptor", "unknown")
@@ -148,9 +149,10 @@ def metadata_envelope(raw: Mapping[str, Any], level: str, feature_count: int | N
     flat_execution = {"device": data.pop("device", "hip"), "num_threads": data.pop("num_threads", None)}
     output = data.pop("output", None) or flat_output
     execution = data.pop("execution", None) or flat_execution
+    data.pop("pair_records", None)  # pair identity lives in the samples only
     merged = dict(details or {})
     merged.update(data)
-    return {
+    envelope = {
         "schema_version": RESULT_SCHEMA_VERSION,
         "descriptor": descriptor,
         "backend": backend,
@@ -158,8 +160,10 @@ def metadata_envelope(raw: Mapping[str, Any], level: str, feature_count: int | N
         "feature_count": feature_count,
         "output": {"dtype": output.get("dtype", "float64"), "sparse": bool(output.get("sparse", False))},
         "execution": {"device": execution.get("device", "hip"), "num_threads": execution.get("num_threads")},
-        "details": merged,
     }
+    if merged:
+        envelope["details"] = merged
+    return envelope
 
 
 @dataclass(frozen=True, slots=True)
@@ -174,6 +178,9 @@ class DescriptorResult:
     metadata: Mapping[str, Any] = field(default_factory=dict)
     samples: Any = None
     feature_count: int | None = None
+    # Atom offsets of the batch, needed to validate the local atom indices of
+    # pair samples; construction context only, never serialised (result.py:320-327).
+    _atom_row_offsets: np.ndarray | None = field(default=None, repr=False, compare=False, kw_only=True)
 
     def __post_init__(self) -> None:
         level = DescriptorLevel(self.level)
@@ -204,13 +211,25 @@ class DescriptorResult:
                 raise ValueError("structure-level results cannot have row offsets")
             if rows != len(self.structure_ids):
                 raise ValueError("structure-level results need one row per structure")
-        elif level is DescriptorLevel.ATOM:
+        else:
             if offsets is None:
-                raise ValueError("atom-level results require row offsets")
+                raise ValueError(f"{level.value}-level results require row offsets")
             if len(offsets) != len(self.structure_ids) + 1 or offsets[0] != 0 or int(offsets[-1]) != rows:
-                raise ValueError("atom row offsets must cover every row, one entry per structure boundary")
+                raise ValueError(f"{level.value} row offsets must cover every row, one entry per structure boundary")
             if np.any(np.diff(offsets) < 0):
+                raise ValueError(f"{level.value} row offsets must be non-decreasing")
+        atom_offsets = self._atom_row_offsets
+        if atom_offsets is not None:
+            raw = np.asarray(atom_offsets)
+            if raw.ndim != 1 or not np.issubdtype(raw.dtype, np.integer):
+                raise ValueError("atom row offsets must be a one-dimensional integer array")
+            atom_offsets = np.array(raw, dtype=np.int64, order="C", copy=True)
+            if len(atom_offsets) != len(self.structure_ids) + 1 or atom_offsets[0] != 0:
+                raise ValueError("atom row offsets must start at zero, one entry per structure boundary")
+            if np.any(np.diff(atom_offsets) < 0):
                 raise ValueError("atom row offsets must be non-decreasing")
+            atom_offsets.setflags(write=False)
+            object.__setattr__(self, "_atom_row_offsets", atom_offsets)
 
         samples = self.samples
         if samples is None:
@@ -220,10 +239,23 @@ class DescriptorResult:
                 samples = atom_samples(offsets)
             else:
                 raise ValueError("pair-level results require explicit pair samples")
+        samples = np.asarray(samples)
+        if samples.size and not np.issubdtype(samples.dtype, np.integer):
+            raise ValueError("samples must contain integer indices")
         samples = np.array(samples, dtype=np.int64, order="C", copy=True)
         expected = {DescriptorLevel.STRUCTURE: 1, DescriptorLevel.ATOM: 2, DescriptorLevel.PAIR: 6}[level]
         if samples.ndim != 2 or samples.shape != (rows, expected):
             raise ValueError(f"{level.value}-level samples must have shape (rows, {expected})")
+        if level is DescriptorLevel.PAIR:
+            # result.py:399-410: structure and both local atom indices in range
+            if atom_offsets is None:
+                raise ValueError("pair-level results require atom row offsets for sample validation")
+            if rows and (np.any(samples[:, :3] < 0) or np.any(samples[:, 0] >= len(offsets) - 1)):
+                raise ValueError("pair samples contain an invalid structure or atom index")
+            counts = np.diff(atom_offsets)
+            if rows and (np.any(samples[:, 1] >= counts[samples[:, 0]])
+                         or np.any(samples[:, 2] >= counts[samples[:, 0]])):
+                raise ValueError("pair samples contain an invalid local atom index")
         samples.setflags(write=False)
         object.__setattr__(self, "samples", samples)
         object.__setattr__(self, "metadata", json.loads(json.dumps(_json_safe(self.metadata))))

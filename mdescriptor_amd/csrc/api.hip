@@ -242,6 +242,18 @@ bool is_pinned_host(const void* p) {
     return attr.type == hipMemoryTypeHost;
 }
 
+// True for device memory (hipMalloc and the like), which kernels may write
+// directly.
+bool is_device_memory(const void* p) {
+    hipPointerAttribute_t attr{};
+    const hipError_t rc = hipPointerGetAttributes(&attr, p);
+    if (rc != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return attr.type == hipMemoryTypeDevice;
+}
+
 // Copy rows x row_bytes of device memory into the caller's host rows (row
 // stride pitch) and wait for it.  Pinned destinations take one DMA.  Pageable
 // ones go through the context's pinned staging ring in chunks of whole rows:
@@ -620,6 +632,7 @@ int mdx_hip_soap_compute(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, const mdx_
         if (out_pitch_bytes < row_bytes) throw mdx::Error(MDX_INVALID_ARGUMENT, "output pitch is too small");
         if (rows > 0 && row_bytes > 0 && out_host == nullptr) throw mdx::Error(MDX_INVALID_ARGUMENT, "null output");
         mdx::PreparedBatch& pb = ctx->scratch_batch;
+        ctx->graph_kind = 0;
         pb.include_boundary = 1;
         mdx::prepare_batch(*batch, plan->species.data(), plan->S, plan->cutoff, pb);
         hipStream_t s = ctx->stream;
@@ -627,6 +640,7 @@ int mdx_hip_soap_compute(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, const mdx_
         mdx::upload_batch(s, *batch, pb);
         ctx->out_dev.reserve(std::max<size_t>(1, static_cast<size_t>(rows) * static_cast<size_t>(row_bytes)));
         run_pipeline(ctx, *plan, pb, ctx->graph, ctx->partials, ctx->out_dev.ptr, row_bytes, cancel_flag, timing);
+        ctx->graph_kind = 1;
         MDX_HIP(hipStreamSynchronize(s));
         check_cancel(cancel_flag);
         const auto t0 = std::chrono::steady_clock::now();
@@ -704,11 +718,13 @@ int mdx_hip_neighbors_build(mdx_hip_ctx* ctx, const mdx_batch_view* batch, doubl
         if (batch == nullptr) throw mdx::Error(MDX_INVALID_ARGUMENT, "null batch");
         DeviceScope scope(ctx->device);
         mdx::PreparedBatch& pb = ctx->scratch_batch;
+        ctx->graph_kind = 0;
         pb.include_boundary = include_boundary != 0 ? 1 : 0;
         mdx::prepare_batch(*batch, nullptr, 1, cutoff, pb);
         mdx::upload_batch(ctx->stream, *batch, pb);
         const int64_t n = mdx::build_graph(ctx->stream, pb, ctx->graph, nullptr);
         MDX_HIP(hipStreamSynchronize(ctx->stream));
+        ctx->graph_kind = 2;
         if (pairs != nullptr) *pairs = n;
     });
 }
@@ -721,7 +737,7 @@ int mdx_hip_neighbors_fetch(mdx_hip_ctx* ctx, int64_t* offsets, int32_t* neighbo
         DeviceScope scope(ctx->device);
         const mdx::PreparedBatch& pb = ctx->scratch_batch;
         mdx::DeviceGraph& g = ctx->graph;
-        if (g.n_species != 1) throw mdx::Error(MDX_INVALID_ARGUMENT, "no neighbour graph has been built");
+        if (ctx->graph_kind != 2) throw mdx::Error(MDX_INVALID_ARGUMENT, "no neighbour graph has been built");
         hipStream_t s = ctx->stream;
         const int64_t atoms = pb.atoms, pairs = g.pairs;
         if (offsets != nullptr) {
@@ -750,6 +766,79 @@ int mdx_hip_neighbors_fetch(mdx_hip_ctx* ctx, int64_t* offsets, int32_t* neighbo
                 MDX_HIP(hipMemcpyAsync(displacements, d_disp, p * 24, hipMemcpyDeviceToHost, s));
             }
             if (distance2 != nullptr) MDX_HIP(hipMemcpyAsync(distance2, d_d2, p * 8, hipMemcpyDeviceToHost, s));
+        }
+        MDX_HIP(hipStreamSynchronize(s));
+    });
+}
+
+int mdx_hip_neighbor_list(mdx_hip_ctx* ctx, const mdx_batch_view* batch, double cutoff, int32_t full_neighbor_list,
+                          int32_t self_pairs, const volatile int32_t* cancel_flag, int64_t* pairs) {
+    if (ctx == nullptr) return MDX_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    return guarded(ctx, [&] {
+        if (batch == nullptr) throw mdx::Error(MDX_INVALID_ARGUMENT, "null batch");
+        check_cancel(cancel_flag);
+        DeviceScope scope(ctx->device);
+        mdx::PreparedBatch& pb = ctx->scratch_batch;
+        ctx->graph_kind = 0;
+        pb.include_boundary = 1; // build_neighbor_graph's default (cpp/include/mdescriptor/neighbor.hpp:50-57)
+        mdx::prepare_batch(*batch, nullptr, 1, cutoff, pb);
+        mdx::upload_batch(ctx->stream, *batch, pb);
+        mdx::build_graph(ctx->stream, pb, ctx->graph, cancel_flag);
+        check_cancel(cancel_flag);
+        const int64_t rows = mdx::count_neighbor_list(ctx->stream, pb, ctx->graph, full_neighbor_list != 0 ? 1 : 0,
+                                                      self_pairs != 0 ? 1 : 0, ctx->list);
+        ctx->graph_kind = 3;
+        if (pairs != nullptr) *pairs = rows;
+    });
+}
+
+int mdx_hip_neighbor_list_fetch(mdx_hip_ctx* ctx, double* table, double* values, int64_t* samples,
+                                int64_t* offsets) {
+    if (ctx == nullptr) return MDX_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    return guarded(ctx, [&] {
+        if (ctx->graph_kind != 3) throw mdx::Error(MDX_INVALID_ARGUMENT, "no neighbour list has been computed");
+        DeviceScope scope(ctx->device);
+        const mdx::PreparedBatch& pb = ctx->scratch_batch;
+        const int64_t rows = ctx->list.rows;
+        hipStream_t s = ctx->stream;
+        // device destinations are written in place; host ones through a
+        // device staging area, one region per output
+        struct Target {
+            void* user;
+            int64_t count;     // records
+            int64_t width;     // bytes per record
+            void* device = nullptr;
+            size_t bytes() const { return static_cast<size_t>(count) * static_cast<size_t>(width); }
+        };
+        Target t[4] = {{table, rows, 72}, {values, rows, 32}, {samples, rows, 48},
+                       {offsets, pb.structures + 1, static_cast<int64_t>(sizeof(int64_t))}};
+        size_t staged = 0;
+        for (Target& x : t) {
+            if (x.user == nullptr || x.bytes() == 0) continue;
+            if (is_device_memory(x.user)) {
+                x.device = x.user;
+            } else {
+                x.device = reinterpret_cast<void*>(staged); // offset, rebased below
+                staged += (x.bytes() + 255) & ~size_t(255);
+            }
+        }
+        if (staged > 0) {
+            ctx->out_dev.reserve(staged);
+            for (Target& x : t) {
+                if (x.user != nullptr && x.bytes() != 0 && x.device != x.user) {
+                    x.device = static_cast<char*>(ctx->out_dev.ptr) + reinterpret_cast<size_t>(x.device);
+                }
+            }
+        }
+        mdx::fill_neighbor_list(s, pb, ctx->graph, ctx->list, static_cast<double*>(t[0].device),
+                                static_cast<double*>(t[1].device), static_cast<int64_t*>(t[2].device),
+                                static_cast<int64_t*>(t[3].device));
+        for (Target& x : t) {
+            if (x.device != nullptr && x.device != x.user) {
+                download_result(ctx, x.device, x.count, x.width, x.user, x.width);
+            }
         }
         MDX_HIP(hipStreamSynchronize(s));
     });

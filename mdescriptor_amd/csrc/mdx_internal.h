@@ -141,6 +141,27 @@ void prepare_batch(const mdx_batch_view& batch, const int32_t* species, int n_sp
                    PreparedBatch& out);
 void upload_batch(hipStream_t stream, const mdx_batch_view& batch, PreparedBatch& pb);
 
+// NeighborList descriptor over a one-species device graph (neighbor_list.hip).
+struct NeighborListState {
+    int64_t rows = -1;       // kept pairs of the last count, -1 before any
+    int full = 1, self_pairs = 0;
+    DeviceBuffer kept;       // i32[atoms]: kept pairs per centre
+    DeviceBuffer kept_start; // i64[atoms + 1]: first output row per centre
+    DeviceBuffer scan_tmp;
+};
+
+// Count the pairs each centre keeps under (full, self_pairs) and scan them;
+// returns the total (waits for the stream).
+int64_t count_neighbor_list(hipStream_t stream, const PreparedBatch& pb, const DeviceGraph& graph, int full,
+                            int self_pairs, NeighborListState& list);
+
+// Write the counted list into device memory: table f64[rows*9], values
+// f64[rows*4], samples i64[rows*6], offsets i64[structures+1]; null pointers
+// are skipped.  Enqueued on stream, not waited for.
+void fill_neighbor_list(hipStream_t stream, const PreparedBatch& pb, const DeviceGraph& graph,
+                        const NeighborListState& list, double* table, double* values, int64_t* samples,
+                        int64_t* offsets);
+
 } // namespace mdx
 
 // Opaque C-ABI objects.
@@ -149,8 +170,10 @@ struct mdx_hip_ctx {
     hipStream_t stream = nullptr;
     std::mutex mutex;
     std::string last_error;
-    mdx::PreparedBatch scratch_batch; // used by mdx_hip_soap_compute / neighbors
+    mdx::PreparedBatch scratch_batch; // used by mdx_hip_soap_compute / neighbors / neighbor_list
     mdx::DeviceGraph graph;
+    int graph_kind = 0;               // what last built `graph`: 0 none, 1 SOAP, 2 neighbors, 3 neighbor list
+    mdx::NeighborListState list;
     mdx::DeviceBuffer out_dev;        // device result of mdx_hip_soap_compute
     mdx::DeviceBuffer partials;       // inner/outer partial sums
     void* pinned = nullptr;           // pinned staging ring (two halves) for pageable result downloads

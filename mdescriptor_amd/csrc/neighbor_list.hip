@@ -1,0 +1,270 @@
+// NeighborList descriptor on the device graph.
+//
+// Kernel 1 (graph.hip) built for one species already is the reference's
+// build_neighbor_graph output (cpp/src/common/neighbor.cpp:703-768): every
+// centre's pairs within the cutoff, boundary inclusive, in the reference's
+// order.  The NeighborList descriptor (compute_neighbor_list,
+// cpp/src/standalone/neighbor_list.cpp:15-78) keeps a subset of those pairs
+// and writes each kept pair as one record.  Two passes over the graph, one
+// wave per centre:
+//
+//   count: a ballot of the keep predicate over the centre's pairs, 64 at a
+//          time, gives the centre's kept count;
+//   fill:  the same ballot gives each kept pair its rank among the kept ones;
+//          the wave stages its records in LDS and stores them as one
+//          contiguous run per output, so every store instruction covers
+//          consecutive addresses (a record is 9, 4 or 6 words wide, and
+//          per-lane rows would scatter each instruction over dozens of
+//          cache lines).
+//
+// An exclusive scan of the counts between the passes gives every centre its
+// first output row.  Rows are centre-major over the batch, which is the
+// reference's concatenation of per-structure tables (neighbor_list.cpp:62-76).
+//
+// The pass is HBM-bound integer and copy work: per graph pair it reads the
+// pair's bin (4 B), the bin's atom and image (8 B), the image's shift (from
+// a table that stays in cache) and, when kept, the bin position (24 B); per
+// kept pair it writes the requested outputs (72, 32 and 48 B).
+#include "mdx_internal.h"
+
+#include <algorithm>
+
+namespace mdx {
+namespace {
+
+constexpr int kListThreads = 64; // one wave per workgroup: the LDS staging needs only a wave barrier
+
+// neighbor_list.cpp:40-47: the exact self pair (same atom, zero shift;
+// NeighborView::exact_self, neighbor.cpp:683-689) unless self_pairs, then,
+// for a half list, the orientation keep_half_neighbor keeps
+// (cpp/include/mdescriptor/detail/neighbor_filter.hpp:18-38): the larger atom
+// index, or for an image of the centre itself the first non-zero shift
+// component positive; the zero shift is its own representative.
+__device__ inline bool keep_record(int64_t centre, int64_t atom, int32_t sa, int32_t sb, int32_t sc, int full,
+                                   int self_pairs) {
+    const bool same = atom == centre;
+    if (!self_pairs && same && sa == 0 && sb == 0 && sc == 0) return false;
+    if (full) return true;
+    if (!same) return atom > centre;
+    if (sa != 0) return sa > 0;
+    if (sb != 0) return sb > 0;
+    if (sc != 0) return sc > 0;
+    return true;
+}
+
+struct ListGraph {
+    const int64_t* pair_start; // i64[atoms + 1]
+    const uint32_t* pair_bin;  // u32[pairs]
+    const int32_t* bin_atom;
+    const int32_t* bin_image;
+    const ImageDesc* images;
+    int64_t atoms;
+    int full;
+    int self_pairs;
+};
+
+__device__ inline bool lane_keeps(const ListGraph& g, int64_t centre, int64_t p, int64_t end, uint32_t& bin,
+                                  int32_t& atom, int32_t (&shift)[3]) {
+    if (p >= end) return false;
+    bin = g.pair_bin[p];
+    atom = g.bin_atom[bin];
+    const ImageDesc& im = g.images[g.bin_image[bin]];
+    shift[0] = im.n[0];
+    shift[1] = im.n[1];
+    shift[2] = im.n[2];
+    return keep_record(centre, atom, shift[0], shift[1], shift[2], g.full, g.self_pairs);
+}
+
+__device__ inline int64_t wave_centre(int64_t c) {
+    // the centre is the same on every lane; keeping it in scalar registers
+    // keeps its loads and loop bounds scalar
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(c));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(c) >> 32));
+    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+__global__ __launch_bounds__(kListThreads) void k_list_count(ListGraph g, int32_t* kept) {
+    const int lane = threadIdx.x;
+    for (int64_t c0 = blockIdx.x; c0 < g.atoms; c0 += gridDim.x) {
+        const int64_t c = wave_centre(c0);
+        const int64_t begin = g.pair_start[c], end = g.pair_start[c + 1];
+        int count = 0;
+        for (int64_t base = begin; base < end; base += kListThreads) {
+            uint32_t bin;
+            int32_t atom, shift[3];
+            const bool keep = lane_keeps(g, c, base + lane, end, bin, atom, shift);
+            count += __popcll(__ballot(keep));
+        }
+        if (lane == 0) kept[c] = count;
+    }
+}
+
+// Outputs of the fill pass; a null pointer skips that output.
+struct ListOut {
+    double* table;    // f64[rows * 9]: centre, atom, shift a b c, dx dy dz, distance (neighbor_list.cpp:50-58)
+    double* values;   // f64[rows * 4]: dx dy dz distance
+    int64_t* samples; // i64[rows * 6]: structure, local centre, local atom, shift a b c (pair_samples,
+                      // src/mdescriptor/core/result.py:257-300)
+};
+
+// Write the wave's staged records (n rows of `width` words from LDS) to
+// out[row0 * width ...] as one contiguous run.
+__device__ inline void flush_rows(const int64_t* stage, int n, int width, int64_t row0, int64_t* out, int lane) {
+    const int words = n * width;
+    int64_t* dst = out + row0 * width;
+    for (int i = lane; i < words; i += kListThreads) dst[i] = stage[i];
+}
+
+__global__ __launch_bounds__(kListThreads) void k_list_fill(ListGraph g, const int64_t* kept_start,
+                                                            const double* positions, const double* bx,
+                                                            const double* by, const double* bz,
+                                                            const int32_t* centre_struct, const int64_t* atom_offsets,
+                                                            ListOut out) {
+    __shared__ int64_t stage[kListThreads * 9];
+    const int lane = threadIdx.x;
+    const uint64_t below = (uint64_t(1) << lane) - 1;
+    for (int64_t c0 = blockIdx.x; c0 < g.atoms; c0 += gridDim.x) {
+        const int64_t c = wave_centre(c0);
+        const int64_t begin = g.pair_start[c], end = g.pair_start[c + 1];
+        if (begin == end) continue;
+        int64_t row0 = kept_start[c];
+        const double cx = positions[c * 3 + 0], cy = positions[c * 3 + 1], cz = positions[c * 3 + 2];
+        const int64_t first = out.samples != nullptr ? atom_offsets[centre_struct[c]] : 0;
+        for (int64_t base = begin; base < end; base += kListThreads) {
+            uint32_t bin = 0;
+            int32_t atom = 0, shift[3] = {0, 0, 0};
+            const bool keep = lane_keeps(g, c, base + lane, end, bin, atom, shift);
+            const uint64_t mask = __ballot(keep);
+            const int n = __popcll(mask);
+            if (n == 0) continue;
+            const int rank = __popcll(mask & below);
+            double dx = 0.0, dy = 0.0, dz = 0.0, distance = 0.0;
+            if (keep) {
+                // displacement and squared distance as neighbor.cpp:569-577
+                // (image position minus centre, products summed left to right
+                // without contraction), distance as neighbor_list.cpp:58
+                dx = bx[bin] - cx;
+                dy = by[bin] - cy;
+                dz = bz[bin] - cz;
+                const double d2 = dx * dx + dy * dy + dz * dz;
+                distance = sqrt(fmax(0.0, d2));
+            }
+            if (out.table != nullptr) {
+                if (keep) {
+                    int64_t* r = stage + rank * 9;
+                    r[0] = __double_as_longlong(static_cast<double>(c));
+                    r[1] = __double_as_longlong(static_cast<double>(atom));
+                    r[2] = __double_as_longlong(static_cast<double>(shift[0]));
+                    r[3] = __double_as_longlong(static_cast<double>(shift[1]));
+                    r[4] = __double_as_longlong(static_cast<double>(shift[2]));
+                    r[5] = __double_as_longlong(dx);
+                    r[6] = __double_as_longlong(dy);
+                    r[7] = __double_as_longlong(dz);
+                    r[8] = __double_as_longlong(distance);
+                }
+                __syncthreads();
+                flush_rows(stage, n, 9, row0, reinterpret_cast<int64_t*>(out.table), lane);
+                __syncthreads();
+            }
+            if (out.values != nullptr) {
+                if (keep) {
+                    int64_t* r = stage + rank * 4;
+                    r[0] = __double_as_longlong(dx);
+                    r[1] = __double_as_longlong(dy);
+                    r[2] = __double_as_longlong(dz);
+                    r[3] = __double_as_longlong(distance);
+                }
+                __syncthreads();
+                flush_rows(stage, n, 4, row0, reinterpret_cast<int64_t*>(out.values), lane);
+                __syncthreads();
+            }
+            if (out.samples != nullptr) {
+                if (keep) {
+                    int64_t* r = stage + rank * 6;
+                    r[0] = centre_struct[c];
+                    r[1] = c - first;
+                    r[2] = atom - first;
+                    r[3] = shift[0];
+                    r[4] = shift[1];
+                    r[5] = shift[2];
+                }
+                __syncthreads();
+                flush_rows(stage, n, 6, row0, out.samples, lane);
+                __syncthreads();
+            }
+            row0 += n;
+        }
+    }
+}
+
+// Per-structure first rows: kept_start at every structure's first atom.
+__global__ void k_list_offsets(const int64_t* kept_start, const int64_t* atom_offsets, int64_t structures,
+                               int64_t* offsets) {
+    for (int64_t s = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; s <= structures;
+         s += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        offsets[s] = kept_start[atom_offsets[s]];
+    }
+}
+
+ListGraph list_graph(const PreparedBatch& pb, const DeviceGraph& g, int full, int self_pairs) {
+    ListGraph lg;
+    lg.pair_start = g.pair_start.as<int64_t>();
+    lg.pair_bin = g.pair_bin.as<uint32_t>();
+    lg.bin_atom = g.bin_atom.as<int32_t>();
+    lg.bin_image = g.bin_image.as<int32_t>();
+    lg.images = pb.d_images.as<ImageDesc>();
+    lg.atoms = pb.atoms;
+    lg.full = full;
+    lg.self_pairs = self_pairs;
+    return lg;
+}
+
+unsigned list_grid(int64_t atoms) {
+    return static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(atoms, int64_t(1) << 20)));
+}
+
+} // namespace
+
+int64_t count_neighbor_list(hipStream_t stream, const PreparedBatch& pb, const DeviceGraph& graph, int full,
+                            int self_pairs, NeighborListState& list) {
+    const int64_t atoms = pb.atoms;
+    list.kept.reserve(static_cast<size_t>(std::max<int64_t>(atoms, 1)) * sizeof(int32_t));
+    list.kept_start.reserve(static_cast<size_t>(atoms + 1) * sizeof(int64_t));
+    list.full = full;
+    list.self_pairs = self_pairs;
+    if (atoms == 0 || graph.pairs == 0) {
+        MDX_HIP(hipMemsetAsync(list.kept_start.ptr, 0, static_cast<size_t>(atoms + 1) * sizeof(int64_t), stream));
+        list.rows = 0;
+        return 0;
+    }
+    hipLaunchKernelGGL(k_list_count, dim3(list_grid(atoms)), dim3(kListThreads), 0, stream,
+                       list_graph(pb, graph, full, self_pairs), list.kept.as<int32_t>());
+    MDX_HIP(hipGetLastError());
+    scan_counts(stream, list.kept.as<int32_t>(), list.kept_start.as<int64_t>(), atoms, list.scan_tmp);
+    int64_t rows = 0;
+    MDX_HIP(hipMemcpyAsync(&rows, list.kept_start.as<int64_t>() + atoms, sizeof(int64_t), hipMemcpyDeviceToHost,
+                           stream));
+    MDX_HIP(hipStreamSynchronize(stream));
+    list.rows = rows;
+    return rows;
+}
+
+void fill_neighbor_list(hipStream_t stream, const PreparedBatch& pb, const DeviceGraph& graph,
+                        const NeighborListState& list, double* table, double* values, int64_t* samples,
+                        int64_t* offsets) {
+    if (offsets != nullptr) {
+        hipLaunchKernelGGL(k_list_offsets, dim3(static_cast<unsigned>((pb.structures + 1 + 255) / 256)), dim3(256),
+                           0, stream, list.kept_start.as<int64_t>(), pb.d_offsets.as<int64_t>(), pb.structures,
+                           offsets);
+        MDX_HIP(hipGetLastError());
+    }
+    if (list.rows == 0 || (table == nullptr && values == nullptr && samples == nullptr)) return;
+    ListOut out{table, values, samples};
+    hipLaunchKernelGGL(k_list_fill, dim3(list_grid(pb.atoms)), dim3(kListThreads), 0, stream,
+                       list_graph(pb, graph, list.full, list.self_pairs), list.kept_start.as<int64_t>(),
+                       pb.d_positions.as<double>(), graph.bin_x.as<double>(), graph.bin_y.as<double>(),
+                       graph.bin_z.as<double>(), graph.centre_struct.as<int32_t>(), pb.d_offsets.as<int64_t>(), out);
+    MDX_HIP(hipGetLastError());
+}
+
+} // namespace mdx

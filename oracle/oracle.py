@@ -3,8 +3,9 @@
 Two libraries are reachable from here:
 
 * ``oracle/_bin/libmdx_oracle.so``: the C restatement in ``soap_oracle.c``
-  of the reference's neighbour graph (cpp/src/common/neighbor.cpp:423-768)
-  and GTO SOAP (cpp/src/standalone/soap.cpp:494-1246);
+  of the reference's neighbour graph (cpp/src/common/neighbor.cpp:423-768),
+  NeighborList descriptor (cpp/src/standalone/neighbor_list.cpp:15-78) and
+  SOAP (cpp/src/standalone/soap.cpp:494-1246);
 * ``oracle/_ref/libmdx_ref.so``: the reference's own C++ compiled in place
   (``oracle/Makefile``), present only where it was built.
 
@@ -41,6 +42,18 @@ class _Graph(ctypes.Structure):
         ("shifts", _i32p),
         ("disp", _f64p),
         ("d2", _f64p),
+    ]
+
+
+class _PairTable(ctypes.Structure):
+    """mdxo_pair_table / mdxr_pair_table: DescriptorPairTable
+    (cpp/include/mdescriptor/local_descriptors.hpp:29-34)."""
+
+    _fields_ = [
+        ("rows", ctypes.c_int64),
+        ("structures", ctypes.c_int64),
+        ("values", _f64p),
+        ("offsets", _i64p),
     ]
 
 
@@ -150,6 +163,12 @@ def _load(kind: str) -> Any:
             ctypes.c_double, ctypes.c_int, ctypes.POINTER(_Graph), ctypes.c_char_p, ctypes.c_int,
         ]
         lib.mdxo_graph_free.argtypes = [ctypes.POINTER(_Graph)]
+        lib.mdxo_neighbor_list.restype = ctypes.c_int
+        lib.mdxo_neighbor_list.argtypes = [
+            _i32p, _f64p, _f64p, _i32p, _i64p, ctypes.c_int64, ctypes.c_int64,
+            ctypes.c_double, ctypes.c_int, ctypes.c_int, ctypes.POINTER(_PairTable), ctypes.c_char_p, ctypes.c_int,
+        ]
+        lib.mdxo_pair_table_free.argtypes = [ctypes.POINTER(_PairTable)]
         lib.mdxo_soap.restype = ctypes.c_int
         lib.mdxo_soap.argtypes = [
             _i32p, _f64p, _f64p, _i32p, _i64p, ctypes.c_int64, ctypes.c_int64,
@@ -171,6 +190,13 @@ def _load(kind: str) -> Any:
             ctypes.c_char_p, ctypes.c_int,
         ]
         lib.mdxr_graph_free.argtypes = [ctypes.POINTER(_Graph)]
+        lib.mdxr_neighbor_list.restype = ctypes.c_int
+        lib.mdxr_neighbor_list.argtypes = [
+            _i32p, _f64p, _f64p, _i32p, _i64p, ctypes.c_int64, ctypes.c_int64,
+            ctypes.c_double, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(_PairTable),
+            ctypes.c_char_p, ctypes.c_int,
+        ]
+        lib.mdxr_pair_table_free.argtypes = [ctypes.POINTER(_PairTable)]
         lib.mdxr_soap.restype = ctypes.c_int
         lib.mdxr_soap.argtypes = [
             _i32p, _f64p, _f64p, _i32p, _i64p, ctypes.c_int64, ctypes.c_int64,
@@ -234,6 +260,39 @@ def graph(batch: Any, cutoff: float, *, include_boundary: bool = True, kind: str
     finally:
         free(ctypes.byref(out))
     return result
+
+
+def neighbor_list(batch: Any, cutoff: float, *, full_neighbor_list: bool = True, self_pairs: bool = False,
+                  kind: str = "oracle", num_threads: int = 1) -> tuple[np.ndarray, np.ndarray]:
+    """NeighborList table of the batch: ``(values[rows, 9], offsets[structures + 1])``
+    as ``_cpp.compute_neighbor_list`` returns it (cpp/src/bindings/module.cpp:772-798)."""
+
+    lib = _load(kind)
+    if lib is None:
+        raise FileNotFoundError("reference harness is not built")
+    numbers, positions, cells, pbc, offsets = _batch_arrays(batch)
+    out = _PairTable()
+    err = ctypes.create_string_buffer(512)
+    args = (
+        _ptr(numbers, _i32p), _ptr(positions, _f64p), _ptr(cells, _f64p), _ptr(pbc, _i32p),
+        _ptr(offsets, _i64p), len(offsets) - 1, len(numbers), float(cutoff), int(bool(full_neighbor_list)),
+        int(bool(self_pairs)),
+    )
+    if kind == "oracle":
+        rc = lib.mdxo_neighbor_list(*args, ctypes.byref(out), err, 512)
+        free = lib.mdxo_pair_table_free
+    else:
+        rc = lib.mdxr_neighbor_list(*args, int(num_threads), ctypes.byref(out), err, 512)
+        free = lib.mdxr_pair_table_free
+    if rc != 0:
+        raise ValueError(err.value.decode())
+    try:
+        rows, structures = int(out.rows), int(out.structures)
+        values = np.ctypeslib.as_array(out.values, shape=(rows * 9 + 1,))[: rows * 9].reshape(rows, 9).copy()
+        table_offsets = np.ctypeslib.as_array(out.offsets, shape=(structures + 1,)).copy()
+    finally:
+        free(ctypes.byref(out))
+    return values, table_offsets
 
 
 _AVERAGE = {"off": 0, "inner": 1, "outer": 2}

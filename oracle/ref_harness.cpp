@@ -1,14 +1,17 @@
 // TEST INFRASTRUCTURE ONLY — a C-ABI shim around the reference's own C++.
 //
 // This file is compiled together with the reference sources where they lie
-// under /root/reference/cpp (soap.cpp, neighbor.cpp, control.cpp; see
+// under /root/reference/cpp (soap.cpp, neighbor_list.cpp, neighbor.cpp,
+// control.cpp; see
 // oracle/Makefile).  It only forwards flat arrays to
 //   mdescriptor::SoapCalculator::compute   (cpp/src/standalone/soap.cpp:1254-1258)
 //   mdescriptor::build_neighbor_graph      (cpp/src/common/neighbor.cpp:703-768)
+//   mdescriptor::compute_neighbor_list     (cpp/src/standalone/neighbor_list.cpp:15-78)
 // so that tests can check the oracle restatement, and bench.py can time the
 // reference CPU path ("cpu_baseline.kind = reference").  The built library
 // lands in oracle/_ref/ and is never part of the product.
 #include "mdescriptor/descriptor.hpp"
+#include "mdescriptor/local_descriptors.hpp"
 #include "mdescriptor/neighbor.hpp"
 
 #include <cstdint>
@@ -171,6 +174,42 @@ void mdxr_graph_free(mdxr_graph* graph) {
     delete[] graph->displacements;
     delete[] graph->distance2;
     std::memset(graph, 0, sizeof(*graph));
+}
+
+struct mdxr_pair_table {
+    std::int64_t rows;
+    std::int64_t structures;
+    double* values;         // rows x 9
+    std::int64_t* offsets;  // structures + 1
+};
+
+// compute_neighbor_list(batch, cutoff, full_neighbor_list, self_pairs, num_threads, nullptr).
+int mdxr_neighbor_list(const std::int32_t* numbers, const double* positions, const double* cells,
+                       const std::int32_t* pbc, const std::int64_t* offsets, std::int64_t structures,
+                       std::int64_t atoms, double cutoff, int full_neighbor_list, int self_pairs,
+                       int num_threads, mdxr_pair_table* out, char* err, int errlen) {
+    std::memset(out, 0, sizeof(*out));
+    try {
+        const mdescriptor::DescriptorPairTable table = mdescriptor::compute_neighbor_list(
+            view(numbers, positions, cells, pbc, offsets, structures, atoms), cutoff,
+            full_neighbor_list != 0, self_pairs != 0, num_threads, nullptr);
+        out->rows = static_cast<std::int64_t>(table.values.size() / 9);
+        out->structures = static_cast<std::int64_t>(table.offsets.size()) - 1;
+        out->values = new double[table.values.size() + 1];
+        out->offsets = new std::int64_t[table.offsets.size() + 1];
+        std::memcpy(out->values, table.values.data(), table.values.size() * sizeof(double));
+        std::memcpy(out->offsets, table.offsets.data(), table.offsets.size() * sizeof(std::int64_t));
+        return 0;
+    } catch (const std::exception& exc) {
+        copy_error(err, errlen, exc.what());
+        return 1;
+    }
+}
+
+void mdxr_pair_table_free(mdxr_pair_table* table) {
+    delete[] table->values;
+    delete[] table->offsets;
+    std::memset(table, 0, sizeof(*table));
 }
 
 } // extern "C"

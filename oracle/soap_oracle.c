@@ -15,6 +15,9 @@
  *   harmonics    : scipy sph_harm x r^l, orthonormality on a quadrature grid
  *   soap         : the reference's SOAP goldens (project + DScribe sidecar),
  *                  single-atom closed form, and oracle/_ref
+ *   neighbor list: the reference's NeighborList goldens, the half/full
+ *                  identity (full = half + its reversal, self pairs apart),
+ *                  and oracle/_ref over every (full, self_pairs) setting
  */
 #include <math.h>
 #include <stdint.h>
@@ -425,6 +428,94 @@ void mdxo_graph_free(mdxo_graph* g) {
     free(g->disp);
     free(g->d2);
     memset(g, 0, sizeof(*g));
+}
+
+/* ------------------------------------------------------------------------ */
+/* NeighborList descriptor, compute_neighbor_list                           */
+/* (cpp/src/standalone/neighbor_list.cpp:15-78).                            */
+/* ------------------------------------------------------------------------ */
+
+typedef struct {
+    int64_t rows;
+    int64_t structures;
+    double* values;   /* rows x 9: centre, atom, shift a b c, dx dy dz, distance */
+    int64_t* offsets; /* structures + 1 */
+} mdxo_pair_table;
+
+/* keep_half_neighbor, cpp/include/mdescriptor/detail/neighbor_filter.hpp:18-38 */
+static int keep_half_neighbor(int64_t centre, int64_t atom, const int32_t* shift) {
+    if (atom != centre) return atom > centre;
+    for (int k = 0; k < 3; ++k) {
+        if (shift[k] != 0) return shift[k] > 0;
+    }
+    return 1;
+}
+
+/* neighbor_list.cpp:40-47 (exact_self: neighbor.cpp:683-689) */
+static int keep_pair(const mdxo_graph* g, int64_t centre, int64_t p, int full, int self_pairs) {
+    const int32_t* shift = g->shifts + 3 * p;
+    const int64_t atom = g->atoms[p];
+    if (!self_pairs && atom == centre && shift[0] == 0 && shift[1] == 0 && shift[2] == 0) return 0;
+    if (!full && !keep_half_neighbor(centre, atom, shift)) return 0;
+    return 1;
+}
+
+int mdxo_neighbor_list(const int32_t* numbers, const double* positions, const double* cells,
+                       const int32_t* pbc, const int64_t* offsets, int64_t structures, int64_t atoms,
+                       double cutoff, int full_neighbor_list, int self_pairs, mdxo_pair_table* out,
+                       char* err, int errlen) {
+    memset(out, 0, sizeof(*out));
+    mdxo_graph g;
+    /* build_neighbor_graph with its defaults: boundary inclusive, shifts stored */
+    const int rc = mdxo_graph_build(numbers, positions, cells, pbc, offsets, structures, atoms, cutoff, 1,
+                                    &g, err, errlen);
+    if (rc != MDXO_OK) return rc;
+    int64_t rows = 0;
+    for (int64_t c = 0; c < atoms; ++c) {
+        for (int64_t p = g.offsets[c]; p < g.offsets[c + 1]; ++p) {
+            rows += keep_pair(&g, c, p, full_neighbor_list, self_pairs);
+        }
+    }
+    out->values = (double*)malloc((size_t)(rows * 9 + 1) * sizeof(double));
+    out->offsets = (int64_t*)calloc((size_t)structures + 1, sizeof(int64_t));
+    if (!out->values || !out->offsets) {
+        free(out->values);
+        free(out->offsets);
+        memset(out, 0, sizeof(*out));
+        mdxo_graph_free(&g);
+        return MDXO_NOMEM;
+    }
+    int64_t row = 0;
+    for (int64_t s = 0; s < structures; ++s) {
+        out->offsets[s] = row;
+        for (int64_t c = offsets[s]; c < offsets[s + 1]; ++c) {
+            for (int64_t p = g.offsets[c]; p < g.offsets[c + 1]; ++p) {
+                if (!keep_pair(&g, c, p, full_neighbor_list, self_pairs)) continue;
+                double* r = out->values + 9 * row;
+                r[0] = (double)c;
+                r[1] = (double)g.atoms[p];
+                r[2] = (double)g.shifts[3 * p + 0];
+                r[3] = (double)g.shifts[3 * p + 1];
+                r[4] = (double)g.shifts[3 * p + 2];
+                r[5] = g.disp[3 * p + 0];
+                r[6] = g.disp[3 * p + 1];
+                r[7] = g.disp[3 * p + 2];
+                r[8] = sqrt(fmax(0.0, g.d2[p]));
+                ++row;
+            }
+        }
+    }
+    out->offsets[structures] = row;
+    out->rows = rows;
+    out->structures = structures;
+    mdxo_graph_free(&g);
+    return MDXO_OK;
+}
+
+void mdxo_pair_table_free(mdxo_pair_table* t) {
+    free(t->values);
+    free(t->offsets);
+    memset(t, 0, sizeof(*t));
 }
 
 /* ------------------------------------------------------------------------ */

@@ -65,6 +65,42 @@ def hip_context():
     ctx.close()
 
 
+def edge_batch() -> SimpleNamespace:
+    """Empty structure, single isolated atom, a tiny periodic cell that needs
+    several image shells, atoms outside the home cell, and an isolated
+    molecule, in one batch."""
+
+    rng = np.random.default_rng(5)
+    tiny = np.array([[1.9, 0.0, 0.0], [0.3, 2.1, 0.0], [0.2, -0.4, 2.3]])
+    big = np.diag([7.0, 7.5, 8.0])
+    parts = [
+        (np.array([], np.int32), np.zeros((0, 3)), np.zeros((3, 3)), [0, 0, 0]),
+        (np.array([8]), np.array([[0.1, 0.2, 0.3]]), np.zeros((3, 3)), [0, 0, 0]),
+        (np.array([1, 8]), rng.uniform(0, 1, (2, 3)) @ tiny, tiny, [1, 1, 1]),
+        (np.array([8, 1, 1, 6]), rng.uniform(-0.5, 1.5, (4, 3)) @ big, big, [1, 1, 1]),
+        (np.array([6, 1, 1, 1, 8]), rng.normal(size=(5, 3)) * 1.3, np.zeros((3, 3)), [0, 0, 0]),
+    ]
+    numbers = np.concatenate([p[0] for p in parts]).astype(np.int32)
+    positions = np.concatenate([p[1] for p in parts])
+    offsets = np.concatenate([[0], np.cumsum([len(p[0]) for p in parts])])
+    return SimpleNamespace(numbers=numbers, positions=positions, cells=np.stack([p[2] for p in parts]),
+                           pbc=np.array([p[3] for p in parts]), offsets=offsets,
+                           ids=tuple(f"edge{i}" for i in range(len(parts))))
+
+
+def table_samples(table: np.ndarray, row_offsets: np.ndarray, atom_offsets: np.ndarray) -> np.ndarray:
+    """``[structure, local_i, local_j, sa, sb, sc]`` of DescriptorPairTable
+    rows, the conversion of the reference's pair_samples
+    (src/mdescriptor/core/result.py:257-300)."""
+
+    row_offsets = np.asarray(row_offsets, dtype=np.int64)
+    atom_offsets = np.asarray(atom_offsets, dtype=np.int64)
+    structure = np.repeat(np.arange(len(row_offsets) - 1, dtype=np.int64), np.diff(row_offsets))
+    first = atom_offsets[structure]
+    records = np.asarray(table[:, :5], dtype=np.int64)
+    return np.column_stack((structure, records[:, 0] - first, records[:, 1] - first, records[:, 2:5]))
+
+
 def scaled_error(values: np.ndarray, reference: np.ndarray) -> float:
     """max |v - r| / (|r| + max|row of r|): a relative error with an atol
     floor of one row maximum, since near-zero high-l features make a purely

@@ -20,7 +20,7 @@ import numpy as np
 import pytest
 
 import mdescriptor_amd as mdx
-from conftest import SOAP_PAD, load_golden, scaled_error
+from conftest import SOAP_PAD, edge_batch, load_golden, scaled_error
 from mdescriptor_amd import _hip, workloads
 from mdescriptor_amd.descriptors.basis import basis_gto
 
@@ -155,25 +155,8 @@ def test_public_soap_reproduces_goldens(manifest, dtype):
 
 
 def _edge_batch():
-    """Empty structure, single isolated atom, a tiny periodic cell that needs
-    several image shells, atoms outside the home cell, and an isolated
-    molecule, in one batch."""
-
-    rng = np.random.default_rng(5)
-    tiny = np.array([[1.9, 0.0, 0.0], [0.3, 2.1, 0.0], [0.2, -0.4, 2.3]])
-    big = np.diag([7.0, 7.5, 8.0])
-    parts = [
-        (np.array([], np.int32), np.zeros((0, 3)), np.zeros((3, 3)), [0, 0, 0]),
-        (np.array([8]), np.array([[0.1, 0.2, 0.3]]), np.zeros((3, 3)), [0, 0, 0]),
-        (np.array([1, 8]), rng.uniform(0, 1, (2, 3)) @ tiny, tiny, [1, 1, 1]),
-        (np.array([8, 1, 1, 6]), rng.uniform(-0.5, 1.5, (4, 3)) @ big, big, [1, 1, 1]),
-        (np.array([6, 1, 1, 1, 8]), rng.normal(size=(5, 3)) * 1.3, np.zeros((3, 3)), [0, 0, 0]),
-    ]
-    numbers = np.concatenate([p[0] for p in parts]).astype(np.int32)
-    positions = np.concatenate([p[1] for p in parts])
-    offsets = np.concatenate([[0], np.cumsum([len(p[0]) for p in parts])])
-    return mdx.StructureBatch(numbers, positions, np.stack([p[2] for p in parts]), np.array([p[3] for p in parts]),
-                              offsets, [f"edge{i}" for i in range(len(parts))])
+    raw = edge_batch()
+    return mdx.StructureBatch(raw.numbers, raw.positions, raw.cells, raw.pbc, raw.offsets, list(raw.ids))
 
 
 @pytest.mark.parametrize("average", ["off", "inner", "outer"])
