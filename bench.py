@@ -20,6 +20,14 @@ same counter on a device copy of known size (``--calibrate-copy``).
 
 ``--calibrate-copy MIB`` only runs that copy: five launches of a plain
 device-to-device copy of MIB mebibytes, then exits.
+
+``--path neighbor-list`` measures the NeighborList descriptor instead, on the
+same configuration's structures at ``--nl-cutoff`` (default 6, the
+descriptor's default): one step is ``mdx_hip_neighbor_list`` + a fetch of the
+public values and samples into device memory.  Its ``value`` is kept pairs
+per second of device time (graph + keep-count + fill, HIP events); the
+roofline object covers the fill kernel (``k_list_fill``, HBM-bound) and the
+CPU baseline is the reference's ``compute_neighbor_list`` (``oracle/_ref``).
 """
 
 from __future__ import annotations
@@ -50,10 +58,10 @@ def flops_per_env(kbar: float, S: int, n: int, l_max: int) -> float:
     return 2.0 * kbar * n * H + 2.0 * S * n * n * H + S * n * (S * n + 1) * H
 
 
-def traffic_from_profile(workload_name: str) -> tuple[float | None, str | None]:
+def traffic_from_profile(workload_name: str, kernel: str = "k_soap_mfma") -> tuple[float | None, str | None]:
     """HBM bytes per launch recorded in the committed counter summary."""
 
-    path = ROOT / "profiles" / f"k_soap_mfma_{workload_name}_traffic.txt"
+    path = ROOT / "profiles" / f"{kernel}_{workload_name}_traffic.txt"
     if not path.is_file():
         return None, None
     for line in path.read_text().splitlines():
@@ -124,6 +132,135 @@ def cpu_baseline(workload, alphas, betas, threads: int, budget_s: float = 30.0) 
     }
 
 
+def list_fill_bytes(graph_pairs: int, pairs: int, atoms: int, binned: int) -> int:
+    """Algorithmic HBM bytes of one k_list_fill launch writing values and
+    samples, each datum counted once: per graph pair its bin index (4 B); per
+    binned image its atom, image index and position (32 B); per centre its
+    pair range, first row, position, structure and atom offset (52 B); per
+    kept pair its records (32 + 48 B)."""
+
+    return 4 * graph_pairs + 32 * binned + 52 * atoms + 80 * pairs
+
+
+def neighbor_list_bench(args, workload) -> dict:
+    import ctypes
+
+    from mdescriptor_amd import _hip
+
+    batch = workload.batch
+    ctx = _hip.Context(0)
+    arrays = _hip._BatchArrays(batch)
+    lib = ctx.lib
+    rows = ctypes.c_int64()
+    full = not args.half
+
+    def build() -> int:
+        ctx.check(lib.mdx_hip_neighbor_list(ctx.handle, ctypes.byref(arrays.view), float(args.nl_cutoff),
+                                            1 if full else 0, 0, None, ctypes.byref(rows)))
+        return int(rows.value)
+
+    n = build()
+    values = _hip.DeviceMemory(max(1, n) * 32)
+    samples = _hip.DeviceMemory(max(1, n) * 48)
+    offsets = _hip.DeviceMemory((batch.structures + 1) * 8)
+
+    def fetch() -> None:
+        ctx.check(lib.mdx_hip_neighbor_list_fetch(ctx.handle, None, ctypes.c_void_p(values.address),
+                                                  ctypes.c_void_p(samples.address), ctypes.c_void_p(offsets.address)))
+
+    for _ in range(args.warmup):
+        build()
+        fetch()
+    timings = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        build()
+        fetch()
+        timings.append(_hip.neighbor_list_timing(ctx))
+    _hip.DeviceMemory.synchronize()
+    wall = time.perf_counter() - t0
+    graph_ms = statistics.mean(t["graph_ms"] for t in timings)
+    count_ms = statistics.mean(t["count_ms"] for t in timings)
+    fill_ms = statistics.mean(t["fill_ms"] for t in timings)
+    device_ms = graph_ms + count_ms + fill_ms
+    graph_pairs = int(timings[-1]["graph_pairs"])
+    fill_bytes = list_fill_bytes(graph_pairs, n, batch.atoms, int(timings[-1]["binned"]))
+    achieved = fill_bytes / (fill_ms * 1e-3) / 1e9
+    traffic, traffic_source = traffic_from_profile(f"{workload.name}_rc{args.nl_cutoff:g}", "k_list_fill")
+    result = {
+        "metric": f"NeighborList pairs/sec (rc {args.nl_cutoff:g}, {'full' if full else 'half'} list) on 1 MI355X",
+        "value": n / (device_ms * 1e-3),
+        "unit": "pairs/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": device_ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f64",
+        "data": "synthetic (seeded generator, mdescriptor_amd/workloads.py)",
+        "config": {
+            "workload": workload.name,
+            "structures": batch.structures,
+            "atoms": batch.atoms,
+            "cutoff": args.nl_cutoff,
+            "full_neighbor_list": full,
+            "self_pairs": False,
+            "outputs": "values (f64 x4) + samples (i64 x6), device memory",
+            "parallelism": "single-gpu",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": traffic,
+            "kernel": "k_list_fill (keep filter + record fill)",
+            "bytes_per_launch": fill_bytes,
+            "launch_ms": fill_ms,
+            "traffic_source": traffic_source,
+        },
+        "breakdown": {
+            "graph_ms": graph_ms,
+            "count_ms": count_ms,
+            "fill_ms": fill_ms,
+            "graph_pairs": graph_pairs,
+            "binned": int(timings[-1]["binned"]),
+            "pairs": n,
+            "wall_ms_per_step": 1e3 * wall / args.steps,
+        },
+    }
+    if not args.no_cpu_baseline:
+        from oracle import oracle
+
+        kind = "reference" if oracle.reference_available() else "port"
+        threads = args.cpu_threads or min(len(os.sched_getaffinity(0)), 16)
+        times = []
+        while True:
+            t1 = time.perf_counter()
+            table, _ = oracle.neighbor_list(batch, args.nl_cutoff, full_neighbor_list=full,
+                                            kind="ref" if kind == "reference" else "oracle", num_threads=threads)
+            times.append(time.perf_counter() - t1)
+            if len(times) >= 3 or sum(times) + times[-1] > 30.0:
+                break
+        seconds = statistics.median(times)
+        result["cpu_baseline"] = {
+            "value": len(table) / seconds,
+            "unit": "pairs/s",
+            "cores": threads if kind == "reference" else 1,
+            "kind": kind,
+            "sample": f"full {workload.name} batch ({len(table)} pairs), median of {len(times)} run(s) of "
+                      f"{seconds:.3f}s",
+        }
+    values.free()
+    samples.free()
+    offsets.free()
+    ctx.close()
+    return result
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
@@ -134,6 +271,9 @@ def main() -> int:
     parser.add_argument("--cpu-threads", type=int, default=0)
     parser.add_argument("--no-end-to-end", action="store_true")
     parser.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB")
+    parser.add_argument("--path", choices=("soap", "neighbor-list"), default="soap")
+    parser.add_argument("--nl-cutoff", type=float, default=6.0)
+    parser.add_argument("--half", action="store_true", help="neighbor-list path: half list")
     args = parser.parse_args()
     if args.calibrate_copy:
         return calibrate_copy(args.calibrate_copy)
@@ -147,6 +287,9 @@ def main() -> int:
     from mdescriptor_amd.descriptors.basis import basis_gto
 
     workload = workloads.config(args.config)
+    if args.path == "neighbor-list":
+        print(json.dumps(neighbor_list_bench(args, workload)))
+        return 0
     p = workload.params
     batch = workload.batch
     alphas, betas = basis_gto(p["r_cut"], p["n_max"], p["l_max"])

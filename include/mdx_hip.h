@@ -209,7 +209,8 @@ int mdx_hip_neighbor_list(mdx_hip_ctx* ctx, const mdx_batch_view* batch, double 
 
 /* Writes the last neighbour list of the context.  Any pointer may be NULL
  * (that output is skipped) and each may be host or device memory (device
- * memory is written in place by the kernel):
+ * memory aligned to 8 bytes is written in place by the kernel; other
+ * destinations receive a copy):
  *   table   f64[pairs*9]  DescriptorPairTable rows (local_descriptors.hpp:29-34):
  *                         centre, neighbour (global atom indices), cell
  *                         shifts a b c, dx dy dz, distance
@@ -221,6 +222,20 @@ int mdx_hip_neighbor_list(mdx_hip_ctx* ctx, const mdx_batch_view* batch, double 
  *                         (DescriptorPairTable::offsets). */
 int mdx_hip_neighbor_list_fetch(mdx_hip_ctx* ctx, double* table, double* values, int64_t* samples,
                                 int64_t* offsets);
+
+/* Device stage times of the last neighbour list on the context, from HIP
+ * events on its stream: the graph (kernel 1), the keep-count and its scan,
+ * and the record fill of the last fetch (0 before a fetch).  A diagnostic
+ * without reference counterpart, like mdx_timing. */
+typedef struct mdx_list_timing {
+    double graph_ms;
+    double count_ms;
+    double fill_ms;
+    int64_t graph_pairs; /* pairs of the graph before the filter */
+    int64_t pairs;       /* kept pairs */
+    int64_t binned;      /* periodic images binned into the cell grid */
+} mdx_list_timing;
+int mdx_hip_neighbor_list_timing(mdx_hip_ctx* ctx, mdx_list_timing* timing);
 
 /* Page-locked host memory for result matrices.  mdx_hip_soap_compute copies
  * into such a buffer with one DMA at the full PCIe rate; into pageable memory

@@ -167,6 +167,22 @@ class Timing(ctypes.Structure):
 
 
 # Every symbol include/mdx_hip.h declares, with its ctypes signature.
+class ListTiming(ctypes.Structure):
+    """mdx_list_timing: device stage times of the last neighbour list."""
+
+    _fields_ = [
+        ("graph_ms", ctypes.c_double),
+        ("count_ms", ctypes.c_double),
+        ("fill_ms", ctypes.c_double),
+        ("graph_pairs", ctypes.c_int64),
+        ("pairs", ctypes.c_int64),
+        ("binned", ctypes.c_int64),
+    ]
+
+    def as_dict(self) -> dict[str, float]:
+        return {name: float(getattr(self, name)) for name, _ in self._fields_}
+
+
 SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "mdx_hip_create": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_void_p)]),
     "mdx_hip_destroy": (None, [ctypes.c_void_p]),
@@ -208,6 +224,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         ctypes.c_int,
         [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p],
     ),
+    "mdx_hip_neighbor_list_timing": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ListTiming)]),
     "mdx_hip_host_alloc": (ctypes.c_int, [ctypes.c_size_t, ctypes.POINTER(ctypes.c_void_p)]),
     "mdx_hip_host_free": (None, [ctypes.c_void_p]),
     "mdx_hip_version": (ctypes.c_char_p, []),
@@ -553,6 +570,14 @@ def neighbor_list(context: Context, batch: Any, cutoff: float, *, full_neighbor_
     return result
 
 
+def neighbor_list_timing(context: Context) -> dict[str, float]:
+    """Stage times of the context's last neighbour list (``mdx_hip_neighbor_list_timing``)."""
+
+    timing = ListTiming()
+    context.check(context.lib.mdx_hip_neighbor_list_timing(context.handle, ctypes.byref(timing)))
+    return timing.as_dict()
+
+
 _contexts: dict[int, Context] = {}
 
 
@@ -753,6 +778,7 @@ __all__ = [
     "load_library",
     "neighbor_graph",
     "neighbor_list",
+    "neighbor_list_timing",
     "shared_context",
 ]
 

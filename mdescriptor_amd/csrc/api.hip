@@ -380,6 +380,7 @@ int mdx_hip_create(int device, mdx_hip_ctx** out) {
             MDX_HIP(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
             for (auto& ev : ctx->events) MDX_HIP(hipEventCreate(&ev));
             for (auto& ev : ctx->stage_events) MDX_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+            for (auto& ev : ctx->list_events) MDX_HIP(hipEventCreate(&ev));
         } catch (...) {
             mdx_hip_destroy(ctx);
             throw;
@@ -401,6 +402,10 @@ void mdx_hip_destroy(mdx_hip_ctx* ctx) {
             ev = nullptr;
         }
         for (auto& ev : ctx->stage_events) {
+            if (ev != nullptr) (void)hipEventDestroy(ev);
+            ev = nullptr;
+        }
+        for (auto& ev : ctx->list_events) {
             if (ev != nullptr) (void)hipEventDestroy(ev);
             ev = nullptr;
         }
@@ -784,10 +789,13 @@ int mdx_hip_neighbor_list(mdx_hip_ctx* ctx, const mdx_batch_view* batch, double 
         pb.include_boundary = 1; // build_neighbor_graph's default (cpp/include/mdescriptor/neighbor.hpp:50-57)
         mdx::prepare_batch(*batch, nullptr, 1, cutoff, pb);
         mdx::upload_batch(ctx->stream, *batch, pb);
+        ctx->list_filled = false;
+        MDX_HIP(hipEventRecord(ctx->list_events[0], ctx->stream));
         mdx::build_graph(ctx->stream, pb, ctx->graph, cancel_flag);
+        MDX_HIP(hipEventRecord(ctx->list_events[1], ctx->stream));
         check_cancel(cancel_flag);
         const int64_t rows = mdx::count_neighbor_list(ctx->stream, pb, ctx->graph, full_neighbor_list != 0 ? 1 : 0,
-                                                      self_pairs != 0 ? 1 : 0, ctx->list);
+                                                      self_pairs != 0 ? 1 : 0, ctx->list, ctx->list_events[2]);
         ctx->graph_kind = 3;
         if (pairs != nullptr) *pairs = rows;
     });
@@ -803,21 +811,25 @@ int mdx_hip_neighbor_list_fetch(mdx_hip_ctx* ctx, double* table, double* values,
         const mdx::PreparedBatch& pb = ctx->scratch_batch;
         const int64_t rows = ctx->list.rows;
         hipStream_t s = ctx->stream;
-        // device destinations are written in place; host ones through a
-        // device staging area, one region per output
+        // device destinations with the alignment of the fill kernel's 8-byte
+        // stores are written in place; host ones (and misaligned device
+        // ones) through a device staging area, one region per output
         struct Target {
             void* user;
             int64_t count;     // records
             int64_t width;     // bytes per record
+            uintptr_t align;   // alignment of the kernel's stores
             void* device = nullptr;
+            bool on_device = false;
             size_t bytes() const { return static_cast<size_t>(count) * static_cast<size_t>(width); }
         };
-        Target t[4] = {{table, rows, 72}, {values, rows, 32}, {samples, rows, 48},
-                       {offsets, pb.structures + 1, static_cast<int64_t>(sizeof(int64_t))}};
+        Target t[4] = {{table, rows, 72, 8}, {values, rows, 32, 8}, {samples, rows, 48, 8},
+                       {offsets, pb.structures + 1, static_cast<int64_t>(sizeof(int64_t)), 8}};
         size_t staged = 0;
         for (Target& x : t) {
             if (x.user == nullptr || x.bytes() == 0) continue;
-            if (is_device_memory(x.user)) {
+            x.on_device = is_device_memory(x.user);
+            if (x.on_device && reinterpret_cast<uintptr_t>(x.user) % x.align == 0) {
                 x.device = x.user;
             } else {
                 x.device = reinterpret_cast<void*>(staged); // offset, rebased below
@@ -832,15 +844,38 @@ int mdx_hip_neighbor_list_fetch(mdx_hip_ctx* ctx, double* table, double* values,
                 }
             }
         }
+        MDX_HIP(hipEventRecord(ctx->list_events[3], s));
         mdx::fill_neighbor_list(s, pb, ctx->graph, ctx->list, static_cast<double*>(t[0].device),
                                 static_cast<double*>(t[1].device), static_cast<int64_t*>(t[2].device),
                                 static_cast<int64_t*>(t[3].device));
+        MDX_HIP(hipEventRecord(ctx->list_events[4], s));
+        ctx->list_filled = true;
         for (Target& x : t) {
-            if (x.device != nullptr && x.device != x.user) {
+            if (x.device == nullptr || x.device == x.user) continue;
+            if (x.on_device) {
+                MDX_HIP(hipMemcpyAsync(x.user, x.device, x.bytes(), hipMemcpyDeviceToDevice, s));
+            } else {
                 download_result(ctx, x.device, x.count, x.width, x.user, x.width);
             }
         }
         MDX_HIP(hipStreamSynchronize(s));
+    });
+}
+
+int mdx_hip_neighbor_list_timing(mdx_hip_ctx* ctx, mdx_list_timing* timing) {
+    if (ctx == nullptr || timing == nullptr) return MDX_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    return guarded(ctx, [&] {
+        if (ctx->graph_kind != 3) throw mdx::Error(MDX_INVALID_ARGUMENT, "no neighbour list has been computed");
+        DeviceScope scope(ctx->device);
+        MDX_HIP(hipStreamSynchronize(ctx->stream));
+        *timing = mdx_list_timing{};
+        timing->graph_ms = elapsed(ctx->list_events[0], ctx->list_events[1]);
+        timing->count_ms = elapsed(ctx->list_events[1], ctx->list_events[2]);
+        timing->fill_ms = ctx->list_filled ? elapsed(ctx->list_events[3], ctx->list_events[4]) : 0.0;
+        timing->graph_pairs = ctx->graph.pairs;
+        timing->pairs = ctx->list.rows;
+        timing->binned = ctx->graph.binned;
     });
 }
 

@@ -151,9 +151,9 @@ struct NeighborListState {
 };
 
 // Count the pairs each centre keeps under (full, self_pairs) and scan them;
-// returns the total (waits for the stream).
+// records `done` after the scan and returns the total (waits for the stream).
 int64_t count_neighbor_list(hipStream_t stream, const PreparedBatch& pb, const DeviceGraph& graph, int full,
-                            int self_pairs, NeighborListState& list);
+                            int self_pairs, NeighborListState& list, hipEvent_t done);
 
 // Write the counted list into device memory: table f64[rows*9], values
 // f64[rows*4], samples i64[rows*6], offsets i64[structures+1]; null pointers
@@ -174,6 +174,8 @@ struct mdx_hip_ctx {
     mdx::DeviceGraph graph;
     int graph_kind = 0;               // what last built `graph`: 0 none, 1 SOAP, 2 neighbors, 3 neighbor list
     mdx::NeighborListState list;
+    hipEvent_t list_events[5] = {};   // neighbour list: graph start / graph end / count end, fill start / end
+    bool list_filled = false;         // a fetch since the last list wrote records
     mdx::DeviceBuffer out_dev;        // device result of mdx_hip_soap_compute
     mdx::DeviceBuffer partials;       // inner/outer partial sums
     void* pinned = nullptr;           // pinned staging ring (two halves) for pageable result downloads

@@ -20,6 +20,11 @@
 // An exclusive scan of the counts between the passes gives every centre its
 // first output row.  Rows are centre-major over the batch, which is the
 // reference's concatenation of per-structure tables (neighbor_list.cpp:62-76).
+// Workgroups take centres in atom order, so consecutive waves write
+// consecutive output runs: on config 2 that measured faster than walking
+// the centres in home-cell order for gather locality (0.109 against
+// 0.119 ms), and faster than per-lane 16-byte row stores without the LDS
+// staging (0.141 ms).
 //
 // The pass is HBM-bound integer and copy work: per graph pair it reads the
 // pair's bin (4 B), the bin's atom and image (8 B), the image's shift (from
@@ -226,7 +231,7 @@ unsigned list_grid(int64_t atoms) {
 } // namespace
 
 int64_t count_neighbor_list(hipStream_t stream, const PreparedBatch& pb, const DeviceGraph& graph, int full,
-                            int self_pairs, NeighborListState& list) {
+                            int self_pairs, NeighborListState& list, hipEvent_t done) {
     const int64_t atoms = pb.atoms;
     list.kept.reserve(static_cast<size_t>(std::max<int64_t>(atoms, 1)) * sizeof(int32_t));
     list.kept_start.reserve(static_cast<size_t>(atoms + 1) * sizeof(int64_t));
@@ -234,6 +239,7 @@ int64_t count_neighbor_list(hipStream_t stream, const PreparedBatch& pb, const D
     list.self_pairs = self_pairs;
     if (atoms == 0 || graph.pairs == 0) {
         MDX_HIP(hipMemsetAsync(list.kept_start.ptr, 0, static_cast<size_t>(atoms + 1) * sizeof(int64_t), stream));
+        MDX_HIP(hipEventRecord(done, stream));
         list.rows = 0;
         return 0;
     }
@@ -241,6 +247,7 @@ int64_t count_neighbor_list(hipStream_t stream, const PreparedBatch& pb, const D
                        list_graph(pb, graph, full, self_pairs), list.kept.as<int32_t>());
     MDX_HIP(hipGetLastError());
     scan_counts(stream, list.kept.as<int32_t>(), list.kept_start.as<int64_t>(), atoms, list.scan_tmp);
+    MDX_HIP(hipEventRecord(done, stream));
     int64_t rows = 0;
     MDX_HIP(hipMemcpyAsync(&rows, list.kept_start.as<int64_t>() + atoms, sizeof(int64_t), hipMemcpyDeviceToHost,
                            stream));

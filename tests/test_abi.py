@@ -58,11 +58,11 @@ def test_status_codes_match_header(hip):
 
 
 def test_struct_layout_matches_c(hip, tmp_path):
-    """sizeof/offsetof of the four public structs, compiled by gcc from the
+    """sizeof/offsetof of the five public structs, compiled by gcc from the
     header, against the ctypes mirror."""
 
     structs = {"mdx_batch_view": hip.BatchView, "mdx_soap_params": hip.SoapParams, "mdx_timing": hip.Timing,
-               "mdx_soap_options": hip.SoapOptions}
+               "mdx_soap_options": hip.SoapOptions, "mdx_list_timing": hip.ListTiming}
     lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "mdx_hip.h"', "int main(void) {"]
     for cname, ctype in structs.items():
         lines.append(f'printf("{cname} %zu\\n", sizeof({cname}));')

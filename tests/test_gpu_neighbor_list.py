@@ -107,6 +107,14 @@ def test_device_outputs_match_host_outputs(hip_context):
                       ("offsets", host["offsets"])):
         np.testing.assert_array_equal(memory[key].to_host(np.empty_like(like)), like, err_msg=key)
         memory[key].free()
+    # a device destination the 8-byte stores cannot take in place receives a copy
+    shifted = _hip.DeviceMemory(rows * 32 + 8)
+    hip_context.check(lib.mdx_hip_neighbor_list_fetch(hip_context.handle, None,
+                                                      ctypes.c_void_p(shifted.address + 4), None, None))
+    _hip.DeviceMemory.synchronize()
+    raw = shifted.to_host(np.empty(rows * 32 + 8, dtype=np.uint8))
+    np.testing.assert_array_equal(raw[4:4 + rows * 32].view(np.float64).reshape(rows, 4), host["values"])
+    shifted.free()
     # pageable host destinations take the staged download
     table = np.empty((rows, 9))
     hip_context.check(lib.mdx_hip_neighbor_list_fetch(hip_context.handle, table.ctypes.data_as(ctypes.c_void_p),
