@@ -114,7 +114,9 @@ typedef struct mdx_timing {
     double finalize_ms;  /* structure-level average reductions (kernel 4), 0 if off */
     double total_ms;     /* first to last event of the device pipeline */
     double h2d_ms;       /* host-to-device copies (mdx_hip_soap_compute only) */
-    double d2h_ms;       /* device-to-host copy of the result (mdx_hip_soap_compute only) */
+    double d2h_ms;       /* device-to-host copy of the result (mdx_hip_soap_compute only); for
+                            atom-level rows into page-locked memory, whose copy overlaps the
+                            expansion launches, only the part left after the last kernel */
     int64_t pairs;       /* neighbour pairs found at the padded SOAP cutoff */
     int64_t binned;      /* periodic images binned into the cell grid */
     int64_t expansion_launches; /* launches of the expansion kernel in the run */
@@ -151,6 +153,9 @@ int64_t mdx_hip_soap_rows(const mdx_soap_plan* plan, const mdx_batch_view* batch
 
 /* Full compute: validate, upload, run, download into out_host
  * (rows x features values of out_dtype, row stride out_pitch_bytes).
+ * With average "off" and out_host in page-locked memory (mdx_hip_host_alloc)
+ * the expansion runs in about eight launches and each launch's rows are
+ * copied out on a second stream while the next ones compute.
  * Replaces SoapCalculator::compute (soap.cpp:1254-1258) as called through
  * compute_soap_array (cpp/src/bindings/module.cpp:431-452), and the CUDA
  * Backend::compute SOAP path (cpp/cuda/src/backend.cu:338-631 ->

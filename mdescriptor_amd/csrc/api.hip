@@ -211,13 +211,13 @@ void fill_timing(mdx_hip_ctx* ctx, mdx_timing* timing, bool with_copies) {
 
 void run_pipeline(mdx_hip_ctx* ctx, const mdx_soap_plan& plan, mdx::PreparedBatch& pb, mdx::DeviceGraph& graph,
                   mdx::DeviceBuffer& partials, void* out_device, int64_t pitch, const volatile int32_t* cancel,
-                  mdx_timing* timing) {
+                  mdx_timing* timing, int64_t slice = 0, const mdx::SliceHook* on_slice = nullptr) {
     hipStream_t s = ctx->stream;
     MDX_HIP(hipEventRecord(ctx->events[0], s));
     const int64_t pairs = mdx::build_graph(s, pb, graph, cancel);
     MDX_HIP(hipEventRecord(ctx->events[1], s));
     check_cancel(cancel);
-    mdx::run_soap(s, plan, pb, graph, out_device, pitch, partials, cancel, ctx->events, timing);
+    mdx::run_soap(s, plan, pb, graph, out_device, pitch, partials, cancel, ctx->events, timing, slice, on_slice);
     const int64_t rows = plan.average != 0 ? pb.structures : pb.atoms;
     if (rows == 0 || plan.features == 0) {
         MDX_HIP(hipEventRecord(ctx->events[2], s));
@@ -378,6 +378,7 @@ int mdx_hip_create(int device, mdx_hip_ctx** out) {
             DeviceScope scope(device);
             ctx->device = device;
             MDX_HIP(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+            MDX_HIP(hipStreamCreateWithFlags(&ctx->copy_stream, hipStreamNonBlocking));
             for (auto& ev : ctx->events) MDX_HIP(hipEventCreate(&ev));
             for (auto& ev : ctx->stage_events) MDX_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
             for (auto& ev : ctx->list_events) MDX_HIP(hipEventCreate(&ev));
@@ -397,6 +398,11 @@ void mdx_hip_destroy(mdx_hip_ctx* ctx) {
     {
         std::lock_guard<std::mutex> lock(ctx->mutex);
         if (ctx->stream != nullptr) (void)hipStreamSynchronize(ctx->stream);
+        if (ctx->copy_stream != nullptr) (void)hipStreamSynchronize(ctx->copy_stream);
+        for (auto& ev : ctx->slice_events) {
+            if (ev != nullptr) (void)hipEventDestroy(ev);
+        }
+        ctx->slice_events.clear();
         for (auto& ev : ctx->events) {
             if (ev != nullptr) (void)hipEventDestroy(ev);
             ev = nullptr;
@@ -413,8 +419,10 @@ void mdx_hip_destroy(mdx_hip_ctx* ctx) {
         ctx->pinned = nullptr;
     }
     hipStream_t stream = ctx->stream;
+    hipStream_t copy_stream = ctx->copy_stream;
     delete ctx; // device buffers are freed by their destructors
     if (stream != nullptr) (void)hipStreamDestroy(stream);
+    if (copy_stream != nullptr) (void)hipStreamDestroy(copy_stream);
     if (previous >= 0) (void)hipSetDevice(previous);
 }
 
@@ -644,6 +652,46 @@ int mdx_hip_soap_compute(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, const mdx_
         MDX_HIP(hipEventRecord(ctx->events[5], s));
         mdx::upload_batch(s, *batch, pb);
         ctx->out_dev.reserve(std::max<size_t>(1, static_cast<size_t>(rows) * static_cast<size_t>(row_bytes)));
+        if (plan->average == 0 && rows > 0 && row_bytes > 0 && is_pinned_host(out_host)) {
+            // Atom-level rows into page-locked memory: the expansion runs in
+            // about kOverlapSlices launches and each launch's rows go out on
+            // the copy stream as soon as it finishes, so the PCIe transfer
+            // (the longer part) overlaps the rest of the computation.
+            constexpr int64_t kOverlapSlices = 8;
+            const int64_t slice = std::max<int64_t>(4096, (rows + kOverlapSlices - 1) / kOverlapSlices);
+            size_t next_event = 0;
+            char* src = static_cast<char*>(ctx->out_dev.ptr);
+            char* dst = static_cast<char*>(out_host);
+            const mdx::SliceHook copy_rows = [&](int64_t first, int64_t count) {
+                if (next_event == ctx->slice_events.size()) {
+                    hipEvent_t ev = nullptr;
+                    MDX_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+                    ctx->slice_events.push_back(ev);
+                }
+                hipEvent_t ev = ctx->slice_events[next_event++];
+                MDX_HIP(hipEventRecord(ev, s));
+                MDX_HIP(hipStreamWaitEvent(ctx->copy_stream, ev, 0));
+                MDX_HIP(hipMemcpy2DAsync(dst + first * out_pitch_bytes, static_cast<size_t>(out_pitch_bytes),
+                                         src + first * row_bytes, static_cast<size_t>(row_bytes),
+                                         static_cast<size_t>(row_bytes), static_cast<size_t>(count),
+                                         hipMemcpyDeviceToHost, ctx->copy_stream));
+            };
+            try {
+                run_pipeline(ctx, *plan, pb, ctx->graph, ctx->partials, ctx->out_dev.ptr, row_bytes, cancel_flag,
+                             timing, slice, &copy_rows);
+            } catch (...) {
+                (void)hipStreamSynchronize(ctx->copy_stream);
+                throw;
+            }
+            ctx->graph_kind = 1;
+            MDX_HIP(hipEventRecord(ctx->events[6], ctx->copy_stream));
+            MDX_HIP(hipStreamSynchronize(ctx->copy_stream));
+            MDX_HIP(hipStreamSynchronize(s));
+            check_cancel(cancel_flag);
+            // d2h_ms: the part of the transfer left after the last kernel
+            fill_timing(ctx, timing, true);
+            return;
+        }
         run_pipeline(ctx, *plan, pb, ctx->graph, ctx->partials, ctx->out_dev.ptr, row_bytes, cancel_flag, timing);
         ctx->graph_kind = 1;
         MDX_HIP(hipStreamSynchronize(s));

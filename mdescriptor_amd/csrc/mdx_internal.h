@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <functional>
 #include <mutex>
 #include <stdexcept>
 #include <string>
@@ -182,6 +183,8 @@ struct mdx_hip_ctx {
     size_t pinned_bytes = 0;
     hipEvent_t events[8] = {};
     hipEvent_t stage_events[2] = {};  // completion of the DMA into each staging half
+    hipStream_t copy_stream = nullptr; // result downloads overlapped with the expansion launches
+    std::vector<hipEvent_t> slice_events; // end of each expansion launch, waited on by copy_stream
 };
 
 struct mdx_soap_plan {
@@ -221,9 +224,16 @@ struct mdx_device_batch {
 };
 
 namespace mdx {
+// Called after each expansion launch of an atom-level run (average off) with
+// the launch's first output row and row count; the rows are written once the
+// stream reaches this point.
+using SliceHook = std::function<void(int64_t first_row, int64_t rows)>;
+
 // Run the SOAP kernels (2-4) of a plan over a prepared batch whose graph is
 // built; output rows x features in device memory with the given pitch.
+// slice (0: the default) bounds the centres per expansion launch.
 void run_soap(hipStream_t stream, const mdx_soap_plan& plan, PreparedBatch& pb,
               const DeviceGraph& graph, void* out_device, int64_t pitch_bytes, DeviceBuffer& partials,
-              const volatile int32_t* cancel, hipEvent_t* events, mdx_timing* timing);
+              const volatile int32_t* cancel, hipEvent_t* events, mdx_timing* timing, int64_t slice = 0,
+              const SliceHook* on_slice = nullptr);
 } // namespace mdx

@@ -353,7 +353,7 @@ void dispatch_hpt(int hpt, hipStream_t stream, dim3 grid, size_t lds, const mdx_
 
 void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, const DeviceGraph& g,
               void* out_device, int64_t pitch_bytes, DeviceBuffer& partials, const volatile int32_t* cancel,
-              hipEvent_t* events, mdx_timing* timing) {
+              hipEvent_t* events, mdx_timing* timing, int64_t slice_items, const SliceHook* on_slice) {
     SoapDims d{};
     d.S = p.S;
     d.n = p.n;
@@ -406,8 +406,10 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
                                hipMemcpyHostToDevice, stream));
     }
 
-    // launch in slices so cancellation is polled between launches
-    const int64_t slice = 1 << 17;
+    // launch in slices so cancellation is polled between launches (and, for
+    // an atom-level run, so the caller can copy finished rows out meanwhile)
+    const int64_t slice = slice_items > 0 ? slice_items : int64_t(1) << 17;
+    const bool hook = on_slice != nullptr && *on_slice && p.average == 0;
     int64_t launches = 0;
     if (p.use_mfma) {
         MfmaDims md{};
@@ -460,6 +462,7 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
             launch_mfma_expand(stream, tt, pb, g, tab, md, d_item_begin, base, count, out_device, pitch_bytes,
                                d_partial);
             ++launches;
+            if (hook) (*on_slice)(base, count);
         }
         if (events != nullptr) MDX_HIP(hipEventRecord(events[3], stream));
         if (p.average != 0) {
@@ -497,6 +500,7 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
         }
         MDX_HIP(hipGetLastError());
         ++launches;
+        if (hook) (*on_slice)(base, count);
     }
     if (events != nullptr) MDX_HIP(hipEventRecord(events[3], stream));
     if (p.average != 0) {

@@ -262,6 +262,37 @@ def test_download_paths_agree(hip_context):
     plan.close()
 
 
+def test_overlapped_download_matches(hip_context):
+    """Atom-level rows into page-locked memory leave in several launches'
+    worth of slices on the copy stream while later launches compute (12288
+    rows: three slices of 4096); a pitched page-locked destination keeps
+    its padding.  Both equal the staged pageable download."""
+
+    work = workloads.config(1)
+    plan, _ = _plan(hip_context, work.params, "off", "float64")
+    pageable = np.empty((work.batch.atoms, plan.features))
+    plan.compute(work.batch, out=pageable)
+    pinned, timing = plan.compute(work.batch)
+    assert _hip.is_pinned(pinned) and timing["expansion_launches"] == 3
+    np.testing.assert_array_equal(pinned, pageable)
+    rows, features = pageable.shape
+    pitch = (features + 3) * 8
+    block = ctypes.c_void_p()
+    assert hip_context.lib.mdx_hip_host_alloc(rows * pitch, ctypes.byref(block)) == 0
+    try:
+        pitched = np.ctypeslib.as_array(ctypes.cast(block, ctypes.POINTER(ctypes.c_double)),
+                                        shape=(rows, features + 3))
+        pitched[:] = -7.0
+        arrays = _hip._BatchArrays(work.batch)
+        hip_context.check(hip_context.lib.mdx_hip_soap_compute(
+            hip_context.handle, plan.handle, ctypes.byref(arrays.view), block, rows, pitch, None, None))
+        np.testing.assert_array_equal(pitched[:, :features], pageable)
+        assert np.all(pitched[:, features:] == -7.0)
+    finally:
+        hip_context.lib.mdx_hip_host_free(block)
+    plan.close()
+
+
 def test_full_config2_structure_against_oracle(hip_context, oracle):
     """Headline configuration at full size: every row finite, and the rows of
     one 4096-atom cell equal to the oracle's for that cell alone."""
