@@ -504,6 +504,71 @@ class DeviceBatch:
             pass
 
 
+class DeviceArray:
+    """Address, shape, dtype, row pitch and device of a caller's 2-D device
+    array: a torch tensor on a HIP device, or any object exposing
+    ``__cuda_array_interface__`` (taken to live on device 0).  Rows may be
+    pitched; elements inside a row must be contiguous."""
+
+    def __init__(self, out: Any) -> None:
+        module = type(out).__module__
+        if module.startswith("torch"):
+            if not getattr(out, "is_cuda", False):
+                raise ValueError("the output tensor must live on a HIP device")
+            if out.dim() != 2 or (out.shape[0] > 0 and out.shape[1] > 1 and out.stride(1) != 1):
+                raise ValueError("the output tensor must be two-dimensional with contiguous rows")
+            names = {"torch.float32": "float32", "torch.float64": "float64"}
+            if str(out.dtype) not in names:
+                raise ValueError(f"unsupported output tensor dtype {out.dtype}")
+            self.dtype = np.dtype(names[str(out.dtype)])
+            self.shape = (int(out.shape[0]), int(out.shape[1]))
+            self.address = int(out.data_ptr())
+            self.pitch = int(out.stride(0)) * self.dtype.itemsize if self.shape[0] > 1 else \
+                self.shape[1] * self.dtype.itemsize
+            self.device = int(out.device.index or 0)
+            self.torch_stream_owner = out
+            return
+        interface = getattr(out, "__cuda_array_interface__", None)
+        if interface is None:
+            raise ValueError("the output must be a torch tensor on a HIP device or expose __cuda_array_interface__")
+        shape = tuple(int(v) for v in interface["shape"])
+        if len(shape) != 2:
+            raise ValueError("the output array must be two-dimensional")
+        address, readonly = interface["data"]
+        if readonly:
+            raise ValueError("the output array is read-only")
+        self.dtype = np.dtype(interface["typestr"])
+        self.shape = shape
+        self.address = int(address)
+        strides = interface.get("strides")
+        if strides is None:
+            self.pitch = shape[1] * self.dtype.itemsize
+        else:
+            if shape[0] > 0 and shape[1] > 1 and int(strides[1]) != self.dtype.itemsize:
+                raise ValueError("the output array's rows must be contiguous")
+            self.pitch = int(strides[0]) if shape[0] > 1 else shape[1] * self.dtype.itemsize
+        self.device = 0
+        self.torch_stream_owner = None
+
+    def check(self, rows: int, features: int, dtype: Any) -> None:
+        if self.shape != (rows, features):
+            raise ValueError(f"the output array must have shape ({rows}, {features}), not {self.shape}")
+        if self.dtype != np.dtype(dtype):
+            raise ValueError(f"the output array must be {np.dtype(dtype)}, not {self.dtype}")
+        if rows > 0 and self.pitch < features * self.dtype.itemsize:
+            raise ValueError("the output array's rows overlap")
+        if self.device != 0:
+            raise ValueError("the HIP backend computes on device 0")
+
+    def settle(self) -> None:
+        """Wait for work a torch stream may still have queued on the array."""
+
+        if self.torch_stream_owner is not None:
+            import torch
+
+            torch.cuda.current_stream(self.torch_stream_owner.device).synchronize()
+
+
 def neighbor_graph(context: Context, batch: Any, cutoff: float, *, include_boundary: bool = True
                    ) -> dict[str, np.ndarray]:
     """Device neighbour graph in the layout of ``_native.build_neighbor_graph``
@@ -658,6 +723,23 @@ class Backend:
                 result["row_offsets"] = np.asarray(batch.offsets, dtype=np.int64).copy()
             return result
 
+    def compute_into(self, batch: Any, address: int, pitch: int, control: Any = None) -> dict[str, float]:
+        """Compute one batch into device memory at ``address`` (rows of
+        ``pitch`` bytes) through the device-resident path: no host copy of
+        the values."""
+
+        with self._lock:
+            if self._closed:
+                raise RuntimeError("HIP backend is closed")
+            flag = getattr(control, "_hip_cancel_flag", None) if control is not None else None
+            device_batch = DeviceBatch(self._plan, batch)
+            try:
+                timing = device_batch.run(address, pitch, flag)
+            finally:
+                device_batch.close()
+            self.last_timing = timing
+            return timing
+
     def close(self) -> None:
         with self._lock:
             if not self._closed:
@@ -766,6 +848,7 @@ def version() -> str:
 __all__ = [
     "Backend",
     "Context",
+    "DeviceArray",
     "DeviceBatch",
     "HipCancelledError",
     "HipError",

@@ -136,6 +136,25 @@ class HipBackend:
             result["row_offsets"] = np.asarray(batch.offsets, dtype=np.int64).copy()
         return result
 
+    def compute_into(self, batch: Any, address: int, pitch: int, control: Any = None) -> None:
+        """Write the rows of every block straight into a caller's device
+        matrix (``pitch`` bytes per row) through the device-resident path."""
+
+        implementation = self._ensure_implementation()
+        average = str(self.options.get("average", "inner"))
+        if control is not None:
+            control.reset(batch.structures)
+        with _plugin_errors():
+            for start, stop in structure_blocks(batch.offsets, self.atom_budget):
+                if control is not None and control.cancelled():
+                    raise CancelledError("descriptor computation was cancelled")
+                block = batch if (start, stop) == (0, batch.structures) else batch._slice_view(start, stop)
+                first_row = int(batch.offsets[start]) if average == "off" else start
+                implementation.compute_into(block, address + first_row * pitch, pitch, control)
+                if control is not None:
+                    for _ in range(stop - start):
+                        control.mark_completed()
+
     def _compute_pairs(self, implementation: Any, batch: Any, control: Any) -> dict[str, Any]:
         """Pair-level rows of every block, in structure order; block samples
         count structures from the block's first one and are shifted here,

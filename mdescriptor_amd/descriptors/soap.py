@@ -26,8 +26,9 @@ from typing import Any
 import numpy as np
 
 from ..core.backends import HipBackend
-from ..core.descriptor import Descriptor
-from ..core.errors import DescriptorConfigError, DescriptorInputError
+from ..core.descriptor import Descriptor, _is_cancelled
+from ..core.errors import CancelledError, DescriptorConfigError, DescriptorInputError
+from ..core.input import coerce_batch
 from ..core.options import CONFIGURATION_SCHEMA_VERSION, ExecutionOptions, OutputOptions, coerce_options
 from ..core.result import DescriptorResult, format_values, metadata_envelope, owned_values
 from ..core.species import require_species, validate_batch_species
@@ -342,6 +343,46 @@ class SOAP(Descriptor):
                                   feature_count=self.feature_count)
         self._metadata_snapshot = metadata
         return result
+
+    def compute_into(self, value: Any, out: Any, *, control: Any = None) -> Any:
+        """Compute one batch straight into device memory and return ``out``.
+
+        ``out`` is a writable two-dimensional device array of shape
+        ``(rows, feature_count)`` and the output dtype: a torch tensor on a
+        HIP device, or any object exposing ``__cuda_array_interface__``.
+        Rows are those of :meth:`compute` (atoms in batch order, or one per
+        structure when averaging); rows may be pitched.  The values never
+        touch host memory.  This entry has no counterpart in the reference,
+        whose results are always host arrays."""
+
+        from .. import _hip
+
+        self._ensure_open()
+        if _is_cancelled(control):
+            raise CancelledError("descriptor computation was cancelled")
+        try:
+            batch = coerce_batch(value)
+            self._validate_batch(batch)
+        except DescriptorInputError:
+            raise
+        except (TypeError, ValueError) as exc:
+            raise DescriptorInputError(str(exc), path=["input"]) from exc
+        try:
+            target = _hip.DeviceArray(out)
+            rows = batch.atoms if self._settings.average == "off" else batch.structures
+            target.check(rows, self.feature_count, self._output_options.dtype)
+        except ValueError as exc:
+            raise DescriptorInputError(str(exc), path=["out"]) from exc
+        target.settle()
+        try:
+            self._backend.compute_into(batch, target.address, target.pitch, control)
+        except DescriptorInputError:
+            raise
+        except ValueError as exc:
+            raise DescriptorInputError(str(exc), path=["input"]) from exc
+        if _is_cancelled(control):
+            raise CancelledError("descriptor computation was cancelled")
+        return out
 
     def close(self) -> None:
         if not self.closed:

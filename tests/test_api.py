@@ -162,6 +162,31 @@ def test_compute_validates_before_touching_the_device():
         mdx.SOAP(species=[1, 8], r_cut=4.0, n_max=2, l_max=2).compute(_water(), control=control)
 
 
+class _DeviceArrayStub:
+    """An object exposing __cuda_array_interface__ at address 0: enough for
+    the output checks, which run before any device work."""
+
+    def __init__(self, shape, typestr="<f8", readonly=False, strides=None):
+        self.__cuda_array_interface__ = {"shape": shape, "typestr": typestr, "data": (0, readonly),
+                                         "strides": strides, "version": 3}
+
+
+def test_compute_into_checks_the_output_before_touching_the_device():
+    soap = mdx.SOAP(species=[1, 8], r_cut=4.0, n_max=2, l_max=2, average="off")
+    batch = _water()
+    rows, features = batch.atoms, soap.feature_count
+    for bad in (_DeviceArrayStub((rows - 1, features)), _DeviceArrayStub((rows, features), "<f4"),
+                _DeviceArrayStub((rows, features), readonly=True),
+                _DeviceArrayStub((rows, features), strides=(8, rows * 8)), _DeviceArrayStub((rows * features,)),
+                np.zeros((rows, features))):
+        with pytest.raises(mdx.DescriptorInputError) as info:
+            soap.compute_into(batch, bad)
+        assert list(info.value.path) == ["out"]
+    inner = mdx.SOAP(species=[1, 8], r_cut=4.0, n_max=2, l_max=2, output=mdx.OutputOptions(dtype="float32"))
+    with pytest.raises(mdx.DescriptorInputError, match=r"shape \(1, "):
+        inner.compute_into(batch, _DeviceArrayStub((rows, features), "<f4"))
+
+
 def test_closed_descriptor_and_pickling():
     soap = mdx.SOAP(species=[1, 8], r_cut=4.0, n_max=2, l_max=2)
     with pytest.raises(TypeError):

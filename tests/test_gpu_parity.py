@@ -262,6 +262,32 @@ def test_download_paths_agree(hip_context):
     plan.close()
 
 
+def test_compute_into_a_torch_tensor():
+    """Device-resident public output: SOAP.compute_into writes the rows of
+    compute() into a torch tensor on the GPU (also a pitched view, and block
+    by block when the batch is split), bit for bit."""
+
+    torch = pytest.importorskip("torch")
+    work = workloads.config(3, "small")
+    p = work.params
+    for average, dtype in (("off", "float32"), ("inner", "float64"), ("outer", "float64")):
+        soap = mdx.SOAP(species=p["species"], r_cut=p["r_cut"], n_max=p["n_max"], l_max=p["l_max"],
+                        average=average, output=mdx.OutputOptions(dtype=dtype))
+        host = soap.compute(work.batch).values
+        tdtype = torch.float32 if dtype == "float32" else torch.float64
+        out = torch.full(host.shape, -1.0, dtype=tdtype, device="cuda:0")
+        assert soap.compute_into(work.batch, out) is out
+        np.testing.assert_array_equal(out.cpu().numpy(), host)
+        wide = torch.full((host.shape[0], host.shape[1] + 7), -3.0, dtype=tdtype, device="cuda:0")
+        soap._backend.atom_budget = 700
+        control = mdx.ComputeControl()
+        soap.compute_into(work.batch, wide[:, :host.shape[1]], control=control)
+        assert control.completed() == work.batch.structures
+        np.testing.assert_array_equal(wide[:, :host.shape[1]].cpu().numpy(), host)
+        assert bool(torch.all(wide[:, host.shape[1]:] == -3.0))
+        soap.close()
+
+
 def test_overlapped_download_matches(hip_context):
     """Atom-level rows into page-locked memory leave in several launches'
     worth of slices on the copy stream while later launches compute (12288
