@@ -322,10 +322,15 @@ def main() -> int:
     launch_ms = statistics.mean(t["expansion_ms"] for t in timings) / launches
     achieved = flops_launch / (launch_ms * 1e-3) / 1e12
     H = (l_max + 1) ** 2
-    traffic, traffic_source = traffic_from_profile(workload.name)
     tiles = int(timings[-1]["expansion_tiles"])
-    kernel = (f"k_soap_mfma<{tiles}> (expansion + beta + power spectrum + write)"
-              if tiles else "k_soap_expand (expansion + beta + power spectrum + write)")
+    family = "k_soap_quad" if tiles < 0 else "k_soap_mfma" if tiles > 0 else "k_soap_expand"
+    traffic, traffic_source = traffic_from_profile(workload.name, family)
+    if tiles < 0:
+        kernel = f"k_soap_quad ({-tiles} wavefronts of 4x4x4 FP64 MFMA; expansion + beta + power spectrum + write)"
+    elif tiles > 0:
+        kernel = f"k_soap_mfma<{tiles}> (expansion + beta + power spectrum + write)"
+    else:
+        kernel = "k_soap_expand (expansion + beta + power spectrum + write)"
     result = {
         "metric": METRIC,
         "value": value,

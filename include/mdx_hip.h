@@ -120,8 +120,9 @@ typedef struct mdx_timing {
     int64_t pairs;       /* neighbour pairs found at the padded SOAP cutoff */
     int64_t binned;      /* periodic images binned into the cell grid */
     int64_t expansion_launches; /* launches of the expansion kernel in the run */
-    int64_t expansion_tiles;    /* 16x16 tiles of the matrix-core kernel's template,
-                                   0 when the generic kernel ran */
+    int64_t expansion_tiles;    /* 16x16 tiles of the matrix-core kernel's template;
+                                   minus the wavefronts of the 4x4-block kernel
+                                   when that ran; 0 when the generic kernel ran */
 } mdx_timing;
 
 typedef struct mdx_hip_ctx mdx_hip_ctx;

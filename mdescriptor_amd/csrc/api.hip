@@ -552,11 +552,13 @@ int mdx_hip_soap_plan_create(mdx_hip_ctx* ctx, const mdx_soap_params* params, md
                     }
                 }
             }
-            // matrix-core path unless MDX_HIP_SOAP_KERNEL=generic; =mfma makes it mandatory
+            // matrix-core paths unless MDX_HIP_SOAP_KERNEL=generic: the 4x4-block
+            // kernel where the plan fits it, else the 16x16-tile kernel; =mfma
+            // makes the 16x16-tile kernel mandatory, =quad the 4x4-block kernel
             const char* env = std::getenv("MDX_HIP_SOAP_KERNEL");
             const std::string choice = env != nullptr ? env : "auto";
-            if (choice != "auto" && choice != "generic" && choice != "mfma") {
-                throw mdx::Error(MDX_INVALID_ARGUMENT, "MDX_HIP_SOAP_KERNEL must be auto, generic or mfma");
+            if (choice != "auto" && choice != "generic" && choice != "mfma" && choice != "quad") {
+                throw mdx::Error(MDX_INVALID_ARGUMENT, "MDX_HIP_SOAP_KERNEL must be auto, generic, mfma or quad");
             }
             const mdx::MfmaPlanHost mp = mdx::plan_mfma_tables(plan->Sc, n, p.l_max, beta, pref);
             mdx::MfmaDims md{};
@@ -591,6 +593,19 @@ int mdx_hip_soap_plan_create(mdx_hip_ctx* ctx, const mdx_soap_params* params, md
                       "polynomial basis need");
             }
             plan->tiles = mp.tiles;
+            const bool quad_range = -max_expo * plan->cutoff * plan->cutoff >= mdx::kQuadMinArgument;
+            if (plan->use_mfma && defaults && quad_range && (choice == "auto" || choice == "quad")) {
+                const mdx::QuadPlanHost qp = mdx::plan_quad_tables(n, p.l_max, md.hpad, beta, pref, expo);
+                if (qp.waves > 0 && mdx::quad_lds_bytes(md) <= 64 * 1024) {
+                    plan->quad_waves = qp.waves;
+                    plan->quad_kg = qp.kg;
+                    plan->quad_instr = qp.instr;
+                    upload(plan->d_quad_lanes, qp.lanes);
+                }
+            }
+            if (choice == "quad" && plan->quad_waves == 0) {
+                throw mdx::Error(MDX_INVALID_ARGUMENT, "SOAP plan is outside the 4x4-block kernel's limits");
+            }
             if (plan->use_mfma) {
                 upload(plan->d_row_channel, mp.row_channel);
                 upload(plan->d_col_harmonic, mp.col_harmonic);

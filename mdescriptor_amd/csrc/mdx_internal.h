@@ -203,6 +203,10 @@ struct mdx_soap_plan {
     int hpad = 0;  // padded harmonic row of the matrix-core layout
     int clamp = 0; // 1 when expo * cutoff^2 can exceed 700
     mdx::DeviceBuffer d_row_channel, d_col_harmonic, d_beta_lane, d_fbase, d_fstride;
+    // 4x4-block kernel (soap_quad.hip), default options only: wavefronts (0:
+    // not used), radial groups, MFMA instructions per step, lane constants
+    int quad_waves = 0, quad_kg = 0, quad_instr = 0;
+    mdx::DeviceBuffer d_quad_lanes;
     // options beyond the GTO / uncompressed / unweighted default (mdx_soap_options)
     int Sc = 0;              // coefficient species: 1 for mu2, else S
     int compression = 0;     // 0 off, 1 mu2, 2 mu1nu1, 3 crossover

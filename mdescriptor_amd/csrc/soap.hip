@@ -459,8 +459,13 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
         for (int64_t base = 0; base < items; base += slice) {
             if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
             const int64_t count = std::min(slice, items - base);
-            launch_mfma_expand(stream, tt, pb, g, tab, md, d_item_begin, base, count, out_device, pitch_bytes,
-                               d_partial);
+            if (p.quad_waves > 0) {
+                launch_quad_expand(stream, p.quad_waves, p.quad_kg, p.quad_instr, pb, g, p.d_quad_lanes.as<QuadLane>(),
+                                   tab.ps_pref, md, d_item_begin, base, count, out_device, pitch_bytes, d_partial);
+            } else {
+                launch_mfma_expand(stream, tt, pb, g, tab, md, d_item_begin, base, count, out_device, pitch_bytes,
+                                   d_partial);
+            }
             ++launches;
             if (hook) (*on_slice)(base, count);
         }
@@ -471,7 +476,7 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
         if (events != nullptr) MDX_HIP(hipEventRecord(events[4], stream));
         if (timing != nullptr) {
             timing->expansion_launches = launches;
-            timing->expansion_tiles = tt;
+            timing->expansion_tiles = p.quad_waves > 0 ? -p.quad_waves : tt;
         }
         return;
     }

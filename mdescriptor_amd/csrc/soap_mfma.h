@@ -71,6 +71,47 @@ MfmaPlanHost plan_mfma_tables(int S, int n, int l_max, const std::vector<double>
                               const std::vector<double>& pref);
 
 int mfma_template_tiles(int tiles);
+
+// 4x4-block kernel (soap_quad.hip) for the default options.  Limits: n <= 8
+// (at most two radial groups of 4 channels), l_max <= kQuadLmax, at most
+// kQuadMaxWaves wavefronts and kQuadG MFMA instructions per wavefront and step.
+constexpr int kQuadG = 4;
+// smallest radial exponent argument -a d^2 the kernel's exp accepts
+constexpr double kQuadMinArgument = -5.0e6;
+constexpr int kQuadLmax = 10;
+constexpr int kQuadMaxWaves = 8;
+
+// Constants of one lane of one wavefront of the 4x4-block kernel.
+//   expo     radial exponent a_lk of the lane's A-operand row (k = 4 group +
+//            lane % 4 of its block's unit), 0 for pad rows and idle blocks
+//   beta_r   beta-fold A operand for the block's own accumulator:
+//            pi^1.5 beta[l][n'][k] pref[l][k], n' = 4 group + lane % 4,
+//            k = 4 group + lane / 16
+//   beta_s   the same for the partner block's accumulator (k of the other
+//            radial group; KG = 2 only)
+//   ycol[g]  harmonic read by the lane for instruction g (H: the zero entry)
+//   cdst     LDS offset (within a species block of c) of the lane's fold
+//            output for g = 0, + 4 g for instruction g; -1: not stored
+//   cnt      instructions in which the lane's block is active
+struct QuadLane {
+    double expo = 0.0, beta_r = 0.0, beta_s = 0.0;
+    int32_t ycol[kQuadG] = {};
+    int32_t cdst = -1, cnt = 0;
+};
+
+struct QuadPlanHost {
+    int waves = 0;               // 0: the shape is outside the kernel's limits
+    int kg = 0;                  // radial groups of 4 channels (1 or 2)
+    int instr = 0;               // MFMA instructions per step, every wavefront (the largest unit)
+    std::vector<int> units;      // column groups of each wavefront's largest unit
+    std::vector<QuadLane> lanes; // [waves * 64]
+};
+QuadPlanHost plan_quad_tables(int n, int l_max, int hpad, const std::vector<double>& beta_scaled,
+                              const std::vector<double>& pref, const std::vector<double>& expo);
+size_t quad_lds_bytes(const MfmaDims& d);
+void launch_quad_expand(hipStream_t stream, int waves, int kg, int instr, const PreparedBatch& pb, const DeviceGraph& g,
+                        const QuadLane* lanes, const double* ps_pref, const MfmaDims& d, const int64_t* item_begin,
+                        int64_t base, int64_t count, void* out, int64_t pitch, double* partial);
 // LDS coefficient rows of a plan: Sc*n channels, n summed rows for mu1nu1, one zero row
 inline int mfma_coefficient_rows(int Sc, int n, int compression) { return Sc * n + (compression == 2 ? n : 0) + 1; }
 int mfma_padded_row(int l_max);

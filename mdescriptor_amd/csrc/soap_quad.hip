@@ -1,0 +1,510 @@
+// Kernels 2-4 on 4x4x4 FP64 matrix-core blocks (v_mfma_f64_4x4x4f64) for the
+// default SOAP options: GTO basis, no neighbour weighting, no compression, any
+// average (soap.cpp:701-931, 997-1013, 1019-1142).
+//
+// The contraction A[(l,k)][(l,m)] = sum_j R_lk(j) Y_lm(j) (soap.cpp:893-914)
+// is block-diagonal in l.  A 16x16 tile wastes most of its products on the
+// zero blocks; 4x4 blocks fit the (l,k) x (l,m) blocks closely.  One
+// v_mfma_f64_4x4x4f64 computes four independent 4x4 blocks, each over the
+// same 4 neighbours (K = 4).  The lane layouts (measured on gfx950), with the
+// block index (L/4) % 4:
+//   A operand  lane L = A_b[row L % 4][k L / 16]
+//   B operand  lane L = B_b[k L / 16][col L % 4]
+//   result     lane L = D_b[row L / 16][col L % 4]
+// so a result register is, lane for lane, a B operand: the beta fold
+// c = beta A (soap.cpp:915-926) reads the contraction accumulators directly.
+//
+// Plan (host, plan_quad_tables): every degree l has KG = ceil(n/4) radial
+// groups of 4 channels and ceil((2l+1)/4) column groups of 4 harmonics.  A
+// "unit" is (l, first column group, column-group count); it occupies KG
+// blocks of a register (KG = 2: blocks {0,1} or {2,3}, channel group = block
+// parity; KG = 1: one block).  Each wavefront owns one register of units: its
+// lanes evaluate exp(-a_lk d^2) for their block's row and the step's 4
+// neighbours (one exp per lane and step), then run one MFMA per column group.
+// With KG = 2 the two channel groups of a unit are summed in the fold: block
+// b and b^1 exchange accumulators with one DPP row_half_mirror (lane i <->
+// 7 - i inside each 8 lanes), which also reverses the column order, so the
+// odd block of every unit keeps its harmonic columns reversed.  The fold of
+// block b produces radial group b % 2 of the unit's c, written to LDS in the
+// layout the Gram-tile power spectrum of soap_device.h reads.
+#include "soap_device.h"
+
+#include <algorithm>
+#include <cmath>
+
+namespace mdx {
+namespace {
+
+constexpr int kQuadTab = 256; // 2^(j/256) table entries
+
+__device__ inline double mfma4(double a, double b, double c) {
+    return __builtin_amdgcn_mfma_f64_4x4x4f64(a, b, c, 0, 0, 0);
+}
+
+// value of lane 8*(L/8) + 7 - L%8 (DPP row_half_mirror), as a double
+__device__ inline double half_mirror(double v) {
+    const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(v), 0x141, 0xF, 0xF, true);
+    const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(v), 0x141, 0xF, 0xF, true);
+    return __hiloint2double(hi, lo);
+}
+
+// exp(x) for x <= 0 by the table-driven method of P. T. P. Tang (ACM TOMS
+// 15(2), 1989) with 256 table entries: x = (256k + j) ln2/256 + r,
+// |r| <= ln2/512, exp(x) = 2^k 2^(j/256) e^r, e^r - 1 by its degree-4 Taylor
+// polynomial (truncation below 4e-17 relative).  Measured within 1 ulp of
+// libm over [-760, 0], subnormal results included; exact 0 below.  The
+// integer k must fit 32 bits: x >= -5.8e6, which the host checks for every
+// plan that runs this kernel (kQuadMinArgument).  tab[j] = 2^(j/256).
+__device__ inline double exp_neg256(double x, const double* tab) {
+    constexpr double kInvLn2x256 = 369.32993046757463228414071833648; // 256 / ln 2
+    constexpr double kHi = 0.010830417275428772 / 4.0;                 // ln2/256, 32 trailing zero bits
+    constexpr double kLo = 7.420820373486988e-09 / 4.0;                // ln2/256 - kHi
+    constexpr double kShifter = 6755399441055744.0;                    // 1.5 * 2^52
+    const double s = fma(x, kInvLn2x256, kShifter);
+    const double kf = s - kShifter;
+    double r = fma(kf, -kHi, x);
+    r = fma(kf, -kLo, r);
+    const int ki = __double2loint(s);
+    double q = fma(r, 1.0 / 24.0, 1.0 / 6.0);
+    q = fma(q, r, 0.5);
+    q = fma(q, r, 1.0);
+    const double em1 = r * q; // e^r - 1
+    const double t = tab[ki & (kQuadTab - 1)];
+    return ldexp(fma(t, em1, t), ki >> 8);
+}
+
+// KG radial groups, G MFMA instructions per step for every wavefront; the
+// workgroup has blockDim.x / 64 wavefronts (one per register of the plan), at
+// most kQuadMaxWaves, and keeps 4 wavefronts per SIMD (128 VGPRs)
+template <int KG, int G>
+__global__ __launch_bounds__(kQuadMaxWaves * kWaveThreads) __attribute__((amdgpu_waves_per_eu(4)))
+void k_soap_quad(
+    const double* __restrict__ positions, const int64_t* __restrict__ pair_start, const int32_t* __restrict__ counts,
+    const uint32_t* __restrict__ pair_bin, const double* __restrict__ bx, const double* __restrict__ by,
+    const double* __restrict__ bz, const QuadLane* __restrict__ lanes, const double* __restrict__ ps_pref,
+    MfmaDims d, const int64_t* __restrict__ item_begin, int64_t item_base, int64_t items, int64_t per_block,
+    void* out, int64_t pitch, double* partial) {
+    extern __shared__ double lds[];
+    const int tid = threadIdx.x;
+    const int lane = tid % kWaveThreads;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWaveThreads);
+    const int kThreads = static_cast<int>(blockDim.x);
+    const int T = kThreads / kWaveThreads;
+    const int H = d.H, L = d.L, S = d.S, n = d.n;
+    const int HP = (H + 1) | 1;     // Y row stride (odd); entry H stays zero
+    const int hp = d.hpad;          // padded c row
+    const int cw = d.crow * hp;     // c words, including the zero row
+    double* s_y = lds;              // kNb * HP
+    double* s_d2 = s_y + kNb * HP;  // kNb
+    double* s_tab = s_d2 + kNb;     // kQuadTab
+    double* s_c = s_tab + kQuadTab; // cw
+    double* s_csum = s_c + cw;      // cw (inner average only)
+    int* s_loff = reinterpret_cast<int*>(s_csum + (d.mode == 1 ? cw : 0)); // L + 1
+    int* s_seg = s_loff + (L + 1);  // S + 1
+    int* s_pseg = s_seg + (S + 1);  // S + 1
+    int* s_step = s_pseg + (S + 1); // 1
+
+    for (int i = tid; i < kQuadTab; i += kThreads) s_tab[i] = exp2(static_cast<double>(i) / kQuadTab);
+    for (int i = tid; i < kNb * HP; i += kThreads) s_y[i] = 0.0;
+    for (int i = tid; i < cw; i += kThreads) s_c[i] = 0.0;
+    if (tid == 0) {
+        int off = 0;
+        for (int l = 0; l <= L; ++l) {
+            s_loff[l] = off;
+            off += 4 * ((2 * l + 4) / 4);
+        }
+    }
+    __syncthreads();
+    // this lane's constants (see QuadLane)
+    const QuadLane& ql = lanes[wave * kWaveThreads + lane];
+    const double expo = ql.expo;
+    const double beta_r = ql.beta_r;
+    const double beta_s = KG == 2 ? ql.beta_s : 0.0;
+    int ycol[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) ycol[g] = ql.ycol[g];
+    const int cdst = ql.cdst;
+    const int ccount = ql.cnt;
+    const uint32_t hmask = d.harm_mask[wave];
+    const int krow = lane / 16; // neighbour of the step this lane feeds (K index)
+
+    const int64_t item_first = item_base + static_cast<int64_t>(blockIdx.x) * per_block;
+    const int64_t item_last = min(item_first + per_block, item_base + items);
+    const int64_t range_end = item_first >= item_last ? 0 : item_begin ? item_begin[item_last] : item_last;
+    // next centre's species counts (lanes < S), position bits (lanes 0-2) and
+    // first row (lane 3), loaded one centre ahead
+    int pre_count = 0;
+    int64_t pre_bits = 0;
+    auto prefetch_centre = [&](int64_t c) {
+        if (c < range_end) {
+            if (lane < S) pre_count = counts[c * S + lane];
+            if (lane < 3) {
+                pre_bits = __double_as_longlong(positions[c * 3 + lane]);
+            } else if (lane == 3) {
+                pre_bits = pair_start[c];
+            }
+        }
+    };
+    if (item_first < item_last) prefetch_centre(item_begin ? item_begin[item_first] : item_first);
+    for (int64_t item = item_first; item < item_last; ++item) {
+        const int64_t first = item_begin ? item_begin[item] : item;
+        const int64_t last = item_begin ? item_begin[item + 1] : item + 1;
+        double* part_row = partial != nullptr ? partial + item * (d.mode == 1 ? static_cast<int64_t>(cw) : d.F) : nullptr;
+        if (d.mode == 1) {
+            for (int i = tid; i < cw; i += kThreads) s_csum[i] = 0.0;
+        }
+        for (int64_t centre = first; centre < last; ++centre) {
+            const double cx = __longlong_as_double(lane_value(pre_bits, 0));
+            const double cy = __longlong_as_double(lane_value(pre_bits, 1));
+            const double cz = __longlong_as_double(lane_value(pre_bits, 2));
+            const int64_t centre_pairs = lane_value(pre_bits, 3);
+            // species segments of the centre's rows and their slots (each
+            // segment padded to a multiple of 4): exclusive sums over lanes < S
+            {
+                int rows = lane < S ? pre_count : 0;
+                int pad = (rows + 3) & ~3;
+#pragma unroll
+                for (int off = 1; off < kMaxSpecies; off *= 2) {
+                    const int r_up = __shfl_up(rows, off, kMaxSpecies);
+                    const int p_up = __shfl_up(pad, off, kMaxSpecies);
+                    if ((lane % kMaxSpecies) >= off) {
+                        rows += r_up;
+                        pad += p_up;
+                    }
+                }
+                if (wave == 0 && lane < S) {
+                    s_seg[lane + 1] = rows;
+                    s_pseg[lane + 1] = pad;
+                    if (lane == 0) {
+                        s_seg[0] = 0;
+                        s_pseg[0] = 0;
+                    }
+                }
+            }
+            __syncthreads();
+            // an empty species leaves its coefficients at zero
+            for (int q = 0; q < S; ++q) {
+                if (s_seg[q + 1] == s_seg[q]) {
+                    double* cdst_q = s_c + q * n * hp;
+                    for (int i = tid; i < n * hp; i += kThreads) cdst_q[i] = 0.0;
+                }
+            }
+            const int slots = s_pseg[S];
+            auto slot_row = [&](int p, int& q) -> int {
+                q = 0;
+                for (int t = 1; t < S; ++t) q += p >= s_pseg[t] ? 1 : 0;
+                const int off = p - s_pseg[q];
+                return off < s_seg[q + 1] - s_seg[q] ? s_seg[q] + off : -1;
+            };
+            // lane pair jj = lane/2 holds the image position of slot jj of the
+            // next chunk (stale, finite values in pad slots)
+            double px = 0.0, py = 0.0, pz = 0.0;
+            int prow, pq;
+            {
+                prow = slot_row(lane / 2, pq);
+                if (prow >= 0) {
+                    const uint32_t b = pair_bin[centre_pairs + prow];
+                    px = bx[b];
+                    py = by[b];
+                    pz = bz[b];
+                }
+            }
+            // species of the first rows (the accumulators start there)
+            int cur = 0;
+            while (cur < S - 1 && s_seg[cur + 1] == 0) ++cur;
+            double acc[G];
+#pragma unroll
+            for (int g = 0; g < G; ++g) acc[g] = 0.0;
+            // c of species q from the accumulators: c = beta A per column
+            // group, the two radial groups of a unit summed through the
+            // half-mirror exchange (KG = 2); instructions past a block's own
+            // count summed zeros and are not stored
+            auto fold = [&](int q) {
+                double* cdst_q = s_c + q * n * hp + cdst;
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    double c = mfma4(beta_r, acc[g], 0.0);
+                    if (KG == 2) c = mfma4(beta_s, half_mirror(acc[g]), c);
+                    if (cdst >= 0 && g < ccount) cdst_q[4 * g] = c;
+                }
+            };
+            // operands of steps h and h + 1 of the chunk: exps and harmonic reads
+            auto operands = [&](int h, double(&ev)[2], double(&yv)[2][G]) {
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    const int jj = 4 * (h + s) + krow;
+                    ev[s] = exp_neg256(-expo * s_d2[jj], s_tab);
+                    const double* yrow = s_y + jj * HP;
+#pragma unroll
+                    for (int g = 0; g < G; ++g) yv[s][g] = yrow[ycol[g]];
+                }
+            };
+            // A chunk whose 8 steps all continue the current species (the common
+            // case: one species' rows span several chunks) runs without per-step
+            // checks; any other chunk checks each step for the end of the rows
+            // and for a change of species.
+            auto contract = [&](int j0) {
+                const uint32_t species = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(s_step[0]));
+                const int nst = min(kNb / 4, (slots - j0) / 4);
+                if (nst == kNb / 4 && species == static_cast<uint32_t>(cur) * 0x11111111u) {
+#pragma unroll
+                    for (int h = 0; h < kNb / 4; h += 2) {
+                        double ev[2], yv[2][G];
+                        operands(h, ev, yv);
+#pragma unroll
+                        for (int s = 0; s < 2; ++s) {
+#pragma unroll
+                            for (int g = 0; g < G; ++g) acc[g] = mfma4(ev[s], yv[s][g], acc[g]);
+                        }
+                    }
+                    return;
+                }
+#pragma unroll
+                for (int h = 0; h < kNb / 4; h += 2) {
+                    if (h >= nst) break;
+                    double ev[2], yv[2][G];
+                    operands(h, ev, yv);
+#pragma unroll
+                    for (int s = 0; s < 2; ++s) {
+                        if (h + s < nst) {
+                            const int qs = static_cast<int>((species >> (4 * (h + s))) & 15u);
+                            if (qs != cur) {
+                                fold(cur);
+                                cur = qs;
+#pragma unroll
+                                for (int g = 0; g < G; ++g) acc[g] = 0.0;
+                            }
+#pragma unroll
+                            for (int g = 0; g < G; ++g) acc[g] = mfma4(ev[s], yv[s][g], acc[g]);
+                        }
+                    }
+                }
+            };
+            for (int j0 = 0; j0 < slots; j0 += kNb) {
+                {
+                    // harmonics: two lanes per slot (cos / sin parts), this
+                    // wavefront's m-columns; pad slots get all-zero harmonics
+                    const int jj = lane / 2;
+                    const int comp = lane % 2;
+                    const double dx = px - cx;
+                    const double dy = py - cy;
+                    const double dz = pz - cz;
+                    const double d2 = dx * dx + dy * dy + dz * dz;
+                    const double scale = prow >= 0 ? 1.0 : 0.0;
+                    if (wave == 0) {
+                        if (comp == 0) s_d2[jj] = d2;
+                        // species of the 8 steps, 4 bits each, from lanes 0, 8, .., 56
+                        uint32_t bits = lane % 8 == 0 ? static_cast<uint32_t>(pq) << (4 * (lane / 8)) : 0u;
+                        bits |= __shfl_xor(bits, 8);
+                        bits |= __shfl_xor(bits, 16);
+                        bits |= __shfl_xor(bits, 32);
+                        if (lane == 0) s_step[0] = static_cast<int>(bits);
+                    }
+                    int lm = d.l_max, zero = 0;
+                    uint32_t mk = hmask;
+                    asm volatile("" : "+s"(lm), "+s"(mk), "+s"(zero));
+                    int part = comp;
+                    asm volatile("" : "+v"(part));
+                    harmonics_q<0, kQuadLmax>(dx, dy, dz, scale, lm, mk, part, &kHarmonic + zero, s_y + jj * HP);
+                }
+                __syncthreads();
+                {
+                    // loads of the next chunk
+                    prow = slot_row(j0 + kNb + lane / 2, pq);
+                    if (prow >= 0) {
+                        const uint32_t b = pair_bin[centre_pairs + prow];
+                        px = bx[b];
+                        py = by[b];
+                        pz = bz[b];
+                    }
+                }
+                contract(j0);
+                __syncthreads();
+            }
+            if (slots > 0) fold(cur);
+            prefetch_centre(centre + 1);
+            __syncthreads();
+            if (d.mode == 0) {
+                power_spectrum_tiles(s_c, s_loff, d, ps_pref, 0, out, pitch, centre, nullptr, wave, T);
+            } else if (d.mode == 1) {
+                for (int i = tid; i < cw; i += kThreads) s_csum[i] += s_c[i];
+            } else {
+                power_spectrum_tiles(s_c, s_loff, d, ps_pref, centre == first ? 3 : 2, out, pitch, centre, part_row,
+                                     wave, T);
+            }
+            __syncthreads();
+        }
+        if (d.mode == 1) {
+            for (int i = tid; i < cw; i += kThreads) part_row[i] = s_csum[i];
+        }
+        __syncthreads();
+    }
+}
+
+template <int KG, int G>
+void launch(hipStream_t stream, int waves, unsigned grid, int64_t per_block, size_t lds, const PreparedBatch& pb,
+            const DeviceGraph& g, const QuadLane* lanes, const double* ps_pref, const MfmaDims& d,
+            const int64_t* item_begin, int64_t base, int64_t count, void* out, int64_t pitch, double* partial) {
+    hipLaunchKernelGGL((k_soap_quad<KG, G>), dim3(grid), dim3(waves * kWaveThreads), lds, stream,
+                       pb.d_positions.as<double>(), g.pair_start.as<int64_t>(), g.counts.as<int32_t>(),
+                       g.pair_bin.as<uint32_t>(), g.bin_x.as<double>(), g.bin_y.as<double>(), g.bin_z.as<double>(),
+                       lanes, ps_pref, d, item_begin, base, count, per_block, out, pitch, partial);
+}
+
+template <int KG>
+void launch_instr(int instr, hipStream_t stream, int waves, unsigned grid, int64_t per_block, size_t lds,
+                  const PreparedBatch& pb, const DeviceGraph& g, const QuadLane* lanes, const double* ps_pref,
+                  const MfmaDims& d, const int64_t* item_begin, int64_t base, int64_t count, void* out, int64_t pitch,
+                  double* partial) {
+    switch (instr) {
+    case 1: launch<KG, 1>(stream, waves, grid, per_block, lds, pb, g, lanes, ps_pref, d, item_begin, base, count, out, pitch, partial); break;
+    case 2: launch<KG, 2>(stream, waves, grid, per_block, lds, pb, g, lanes, ps_pref, d, item_begin, base, count, out, pitch, partial); break;
+    case 3: launch<KG, 3>(stream, waves, grid, per_block, lds, pb, g, lanes, ps_pref, d, item_begin, base, count, out, pitch, partial); break;
+    case 4: launch<KG, 4>(stream, waves, grid, per_block, lds, pb, g, lanes, ps_pref, d, item_begin, base, count, out, pitch, partial); break;
+    default: throw Error(MDX_INTERNAL, "unsupported instruction count for the 4x4-block kernel");
+    }
+}
+
+} // namespace
+
+QuadPlanHost plan_quad_tables(int n, int l_max, int hpad, const std::vector<double>& beta_scaled,
+                              const std::vector<double>& pref, const std::vector<double>& expo) {
+    QuadPlanHost out;
+    const int KG = (n + 3) / 4;
+    if (KG > 2 || l_max > kQuadLmax || n < 1) return out;
+    const int P = 4 / KG; // units per register
+    const int L = l_max + 1;
+    struct Unit {
+        int l, g0, cnt;
+    };
+    // choose the largest column-group count per unit c (splitting degrees with
+    // more groups into balanced pieces) that minimises the estimated cost of a
+    // step: every wavefront evaluates one exp per lane and runs as many MFMAs
+    // as the largest unit of the plan has column groups
+    constexpr double kExpCost = 3.0, kMfmaCost = 1.0;
+    double best_cost = 0.0;
+    std::vector<std::vector<Unit>> best;
+    for (int c = 1; c <= kQuadG; ++c) {
+        std::vector<Unit> units;
+        for (int l = 0; l < L; ++l) {
+            const int groups = (2 * l + 1 + 3) / 4;
+            const int pieces = (groups + c - 1) / c;
+            int g0 = 0;
+            for (int p = 0; p < pieces; ++p) {
+                const int cnt = groups / pieces + (p < groups % pieces ? 1 : 0);
+                units.push_back({l, g0, cnt});
+                g0 += cnt;
+            }
+        }
+        // pack P units per register, largest first
+        std::stable_sort(units.begin(), units.end(), [](const Unit& a, const Unit& b) { return a.cnt > b.cnt; });
+        std::vector<std::vector<Unit>> regs;
+        for (size_t i = 0; i < units.size(); i += static_cast<size_t>(P)) {
+            regs.emplace_back(units.begin() + static_cast<std::ptrdiff_t>(i),
+                              units.begin() + static_cast<std::ptrdiff_t>(std::min(units.size(), i + P)));
+        }
+        if (regs.size() > static_cast<size_t>(kQuadMaxWaves)) continue;
+        int gmax = 0;
+        for (const auto& r : regs) gmax = std::max(gmax, r.front().cnt);
+        const double cost = static_cast<double>(regs.size()) * (kExpCost + kMfmaCost * gmax);
+        if (best.empty() || cost < best_cost) {
+            best_cost = cost;
+            best = regs;
+        }
+    }
+    if (best.empty()) return out;
+    const int T = static_cast<int>(best.size());
+    out.waves = T;
+    out.kg = KG;
+    out.units.assign(static_cast<size_t>(T), 0);
+    out.lanes.assign(static_cast<size_t>(T) * 64, QuadLane{});
+    std::vector<int> loff(static_cast<size_t>(L) + 1, 0);
+    for (int l = 0; l < L; ++l) loff[static_cast<size_t>(l) + 1] = loff[static_cast<size_t>(l)] + 4 * ((2 * l + 4) / 4);
+    const int H = L * L;
+    auto beta = [&](int l, int np, int k) -> double {
+        if (np >= n || k >= n) return 0.0;
+        return beta_scaled[static_cast<size_t>((l * n + np) * n + k)] * pref[static_cast<size_t>(l * n + k)];
+    };
+    for (int w = 0; w < T; ++w) {
+        const auto& reg = best[static_cast<size_t>(w)];
+        out.units[static_cast<size_t>(w)] = reg.front().cnt;
+        out.instr = std::max(out.instr, reg.front().cnt);
+        for (int lane = 0; lane < 64; ++lane) {
+            QuadLane& q = out.lanes[static_cast<size_t>(w) * 64 + static_cast<size_t>(lane)];
+            const int b = (lane / 4) % 4;
+            const int slot = b / KG; // unit slot of this block
+            for (int g = 0; g < kQuadG; ++g) q.ycol[g] = H;
+            q.cdst = -1;
+            q.cnt = 0;
+            if (slot >= static_cast<int>(reg.size())) continue; // idle block
+            const Unit& u = reg[static_cast<size_t>(slot)];
+            const int grp = KG == 2 ? b % 2 : 0;    // radial group of the block's A rows
+            const bool reversed = KG == 2 && (b % 2) == 1;
+            // A operand (exp): row lane % 4 of radial group grp
+            const int k = 4 * grp + lane % 4;
+            q.expo = k < n ? expo[static_cast<size_t>(u.l * n + k)] : 0.0;
+            // B operand (harmonics): column lane % 4 of column group g0 + g
+            const int col = lane % 4;
+            const int mcol = reversed ? 3 - col : col;
+            for (int g = 0; g < u.cnt; ++g) {
+                const int m = 4 * (u.g0 + g) + mcol;
+                q.ycol[g] = m <= 2 * u.l ? u.l * u.l + m : H;
+            }
+            // fold: A operand = beta (row n' = lane % 4 of radial group grp,
+            // k = lane / 16 of the block's own group, or of the partner's for
+            // the exchanged accumulator); result row n' = lane / 16
+            const int np_a = 4 * grp + lane % 4;
+            q.beta_r = beta(u.l, np_a, 4 * grp + lane / 16);
+            q.beta_s = KG == 2 ? beta(u.l, np_a, 4 * (1 - grp) + lane / 16) : 0.0;
+            const int np_out = 4 * grp + lane / 16;
+            if (np_out < n) {
+                q.cdst = np_out * hpad + loff[static_cast<size_t>(u.l)] + 4 * u.g0 + mcol;
+                q.cnt = u.cnt;
+            }
+        }
+    }
+    return out;
+}
+
+size_t quad_lds_bytes(const MfmaDims& d) {
+    const size_t cw = static_cast<size_t>(d.crow) * static_cast<size_t>(d.hpad);
+    size_t words = static_cast<size_t>(kNb) * ((d.H + 1) | 1) + kNb + kQuadTab + cw;
+    if (d.mode == 1) words += cw;
+    return words * sizeof(double) + static_cast<size_t>(d.L + 1 + 2 * (d.S + 1) + 1) * sizeof(int);
+}
+
+void launch_quad_expand(hipStream_t stream, int waves, int kg, int instr, const PreparedBatch& pb, const DeviceGraph& g,
+                        const QuadLane* lanes, const double* ps_pref, const MfmaDims& d, const int64_t* item_begin,
+                        int64_t base, int64_t count, void* out, int64_t pitch, double* partial) {
+    if (count <= 0) return;
+    const size_t lds = quad_lds_bytes(d);
+    MfmaDims dm = d;
+    {
+        // harmonic m-columns over the wavefronts, longest recurrence first
+        int load[16] = {};
+        for (int w = 0; w < 16; ++w) dm.harm_mask[w] = 0;
+        for (int m = 0; m <= d.l_max; ++m) {
+            int best = 0;
+            for (int w = 1; w < waves; ++w) {
+                if (load[w] < load[best]) best = w;
+            }
+            dm.harm_mask[best] |= 1u << m;
+            load[best] += d.l_max - m + 1;
+        }
+    }
+    const int64_t resident = std::max<int64_t>(1, std::min<int64_t>(32, (160 * 1024) / std::max<size_t>(lds, 1)));
+    const int64_t target = std::max<int64_t>(1, 8 * resident * device_compute_units());
+    const int64_t per_block = std::max<int64_t>(1, (count + target - 1) / target);
+    const unsigned grid = static_cast<unsigned>((count + per_block - 1) / per_block);
+    if (waves < 1 || waves > kQuadMaxWaves) throw Error(MDX_INTERNAL, "unsupported wave count for the 4x4-block kernel");
+    if (kg == 1) {
+        launch_instr<1>(instr, stream, waves, grid, per_block, lds, pb, g, lanes, ps_pref, dm, item_begin, base, count,
+                        out, pitch, partial);
+    } else {
+        launch_instr<2>(instr, stream, waves, grid, per_block, lds, pb, g, lanes, ps_pref, dm, item_begin, base, count,
+                        out, pitch, partial);
+    }
+    MDX_HIP(hipGetLastError());
+}
+
+} // namespace mdx

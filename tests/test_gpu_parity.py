@@ -78,15 +78,55 @@ def test_soap_matches_oracle(hip_context, oracle, workload, average, dtype):
     _check(hip_context, oracle, workload.batch, workload.params, average, dtype)
 
 
-@pytest.mark.parametrize("kernel", ["generic", "mfma"])
-def test_both_expansion_kernels_match(hip_context, oracle, monkeypatch, kernel):
-    """The plan picks the matrix-core kernel where its tiles fit; the generic
-    kernel is the fallback for other shapes.  Both stay parity-green."""
+@pytest.mark.parametrize("kernel", ["generic", "mfma", "quad"])
+def test_every_expansion_kernel_matches(hip_context, oracle, monkeypatch, kernel):
+    """The plan picks the 4x4-block kernel for the default options where it
+    fits (n_max <= 8), else the 16x16-tile kernel, with the generic kernel as
+    the last fallback.  Each stays parity-green when forced."""
 
     monkeypatch.setenv("MDX_HIP_SOAP_KERNEL", kernel)
     work = workloads.config(2, "small")
     for average in ("off", "inner", "outer"):
-        _check(hip_context, oracle, work.batch, work.params, average, "float64")
+        _, timing = _check(hip_context, oracle, work.batch, work.params, average, "float64")
+        tiles = timing["expansion_tiles"]
+        assert (tiles < 0) if kernel == "quad" else (tiles > 0) if kernel == "mfma" else tiles == 0
+
+
+def test_default_plan_runs_the_quad_kernel(hip_context, oracle):
+    work = workloads.config(2, "small")
+    _, timing = _check(hip_context, oracle, work.batch, work.params, "off", "float32")
+    assert timing["expansion_tiles"] == -4  # four wavefronts of 4x4x4 blocks for n_max 8, l_max 6
+
+
+def _random_cluster(seed, atoms, species):
+    """A dense periodic box and an isolated cluster, both with every species."""
+
+    rng = np.random.default_rng(seed)
+    numbers = np.array([species[i % len(species)] for i in range(2 * atoms)], np.int32)
+    box = 6.0
+    positions = np.concatenate([rng.uniform(0.0, box, (atoms, 3)), rng.uniform(0.0, 4.0, (atoms, 3))])
+    cells = np.stack([np.eye(3) * box, np.zeros((3, 3))])
+    pbc = np.array([[1, 1, 1], [0, 0, 0]], np.int32)
+    return SimpleNamespace(numbers=numbers, positions=positions, cells=cells, pbc=pbc,
+                           offsets=np.array([0, atoms, 2 * atoms]))
+
+
+@pytest.mark.parametrize("n_max,l_max", [(1, 0), (2, 1), (3, 2), (4, 3), (4, 7), (5, 4), (6, 5), (7, 9),
+                                         (8, 6), (8, 8), (8, 10)])
+def test_quad_kernel_shapes(hip_context, oracle, monkeypatch, n_max, l_max):
+    """Every radial-group count (n_max <= 4: one group, 5-8: two) and a range
+    of degrees, so that plans with 1-7 wavefronts, split degrees and idle
+    blocks all run against the oracle."""
+
+    monkeypatch.setenv("MDX_HIP_SOAP_KERNEL", "quad")
+    species = [1, 8]
+    batch = _random_cluster(100 * n_max + l_max, 24, species)
+    params = {"species": species, "n_max": n_max, "l_max": l_max, "r_cut": 3.0}
+    # the inner average keeps a second coefficient block in LDS: beyond 64 KB
+    # at l_max 10 the plan leaves the matrix-core kernels
+    for average in ("off", "outer") + (("inner",) if l_max < 10 else ()):
+        _, timing = _check(hip_context, oracle, batch, params, average, "float64")
+        assert timing["expansion_tiles"] < 0
 
 
 @pytest.mark.parametrize("cutoff", [3.5, 3.5 + SOAP_PAD])
