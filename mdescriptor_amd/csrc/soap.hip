@@ -461,7 +461,8 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
             const int64_t count = std::min(slice, items - base);
             if (p.quad_waves > 0) {
                 launch_quad_expand(stream, p.quad_waves, p.quad_kg, p.quad_instr, pb, g, p.d_quad_lanes.as<QuadLane>(),
-                                   tab.ps_pref, md, d_item_begin, base, count, out_device, pitch_bytes, d_partial);
+                                   tab.ps_pref, tab.fbase, tab.fstride, md, d_item_begin, base, count, out_device,
+                                   pitch_bytes, d_partial);
             } else {
                 launch_mfma_expand(stream, tt, pb, g, tab, md, d_item_begin, base, count, out_device, pitch_bytes,
                                    d_partial);

@@ -34,8 +34,8 @@ __device__ inline d4 mfma(double a, double b, d4 c) {
 // computed (the workgroup's wavefronts split them).  With l_max = LM fixed at
 // compile time both loops unroll completely: every coefficient is an
 // immediate constant and every store a constant LDS offset from the lane's
-// column base.
-template <int LM>
+// column base.  Entry h of the lane's slot sits at out[h * kStride].
+template <int LM, int kStride = 1>
 __device__ __forceinline__ void harmonics_fixed(double x, double y, double z, double scale, uint32_t mask, int comp,
                                                const HarmonicRecurrence* __restrict__ hr, double* out) {
     const double r2 = x * x + y * y + z * z;
@@ -53,32 +53,32 @@ __device__ __forceinline__ void harmonics_fixed(double x, double y, double z, do
             sim = ni;
         }
         if (((mask >> m) & 1u) == 0) continue;
-        double* col = out + (comp == 0 ? -m : m);  // entry (l, m) of this lane's part at col[l*l + l]
+        double* col = out + (comp == 0 ? -m : m) * kStride; // entry (l, m) of this lane's part at col[(l*l + l) * kStride]
         double q1 = comp == 0 ? sre : sim;
-        if (m > 0 || comp == 0) col[m * m + m] = q1;
+        if (m > 0 || comp == 0) col[(m * m + m) * kStride] = q1;
         if (m + 1 > LM) continue;
         double q2 = q1;
         q1 = hr->e[m] * (z * q2);
-        if (m > 0 || comp == 0) col[(m + 1) * (m + 1) + (m + 1)] = q1;
+        if (m > 0 || comp == 0) col[((m + 1) * (m + 1) + (m + 1)) * kStride] = q1;
 #pragma unroll
         for (int l = m + 2; l <= LM; ++l) {
             const double q = fma(hr->a[l][m] * z, q1, -(hr->b[l][m] * r2) * q2);
-            if (m > 0 || comp == 0) col[l * l + l] = q;
+            if (m > 0 || comp == 0) col[(l * l + l) * kStride] = q;
             q2 = q1;
             q1 = q;
         }
     }
 }
 
-// harmonics_fixed<l_max> for a run-time l_max <= kTop (a wave-uniform branch
-// chain)
-template <int LM = 0, int kTop = kHarmonicLmax>
+// harmonics_fixed<l_max, kStride> for a run-time l_max <= kTop (a wave-uniform
+// branch chain)
+template <int LM = 0, int kTop = kHarmonicLmax, int kStride = 1>
 __device__ __forceinline__ void harmonics_q(double x, double y, double z, double scale, int l_max, uint32_t mask,
                                            int comp, const HarmonicRecurrence* __restrict__ hr, double* out) {
     if (l_max == LM) {
-        harmonics_fixed<LM>(x, y, z, scale, mask, comp, hr, out);
+        harmonics_fixed<LM, kStride>(x, y, z, scale, mask, comp, hr, out);
     } else if constexpr (LM < kTop) {
-        harmonics_q<LM + 1, kTop>(x, y, z, scale, l_max, mask, comp, hr, out);
+        harmonics_q<LM + 1, kTop, kStride>(x, y, z, scale, l_max, mask, comp, hr, out);
     }
 }
 

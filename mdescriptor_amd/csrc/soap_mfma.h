@@ -110,8 +110,9 @@ QuadPlanHost plan_quad_tables(int n, int l_max, int hpad, const std::vector<doub
                               const std::vector<double>& pref, const std::vector<double>& expo);
 size_t quad_lds_bytes(const MfmaDims& d);
 void launch_quad_expand(hipStream_t stream, int waves, int kg, int instr, const PreparedBatch& pb, const DeviceGraph& g,
-                        const QuadLane* lanes, const double* ps_pref, const MfmaDims& d, const int64_t* item_begin,
-                        int64_t base, int64_t count, void* out, int64_t pitch, double* partial);
+                        const QuadLane* lanes, const double* ps_pref, const int32_t* fbase, const int32_t* fstride,
+                        const MfmaDims& d, const int64_t* item_begin, int64_t base, int64_t count, void* out,
+                        int64_t pitch, double* partial);
 // LDS coefficient rows of a plan: Sc*n channels, n summed rows for mu1nu1, one zero row
 inline int mfma_coefficient_rows(int Sc, int n, int compression) { return Sc * n + (compression == 2 ? n : 0) + 1; }
 int mfma_padded_row(int l_max);

@@ -35,7 +35,8 @@
 namespace mdx {
 namespace {
 
-constexpr int kQuadTab = 256; // 2^(j/256) table entries
+constexpr int kQuadTab = 64;  // 2^(j/64) table entries
+constexpr int kYStride = kNb + 1; // harmonic staging: entry h of slot j at h * kYStride + j
 
 __device__ inline double mfma4(double a, double b, double c) {
     return __builtin_amdgcn_mfma_f64_4x4x4f64(a, b, c, 0, 0, 0);
@@ -49,41 +50,129 @@ __device__ inline double half_mirror(double v) {
 }
 
 // exp(x) for x <= 0 by the table-driven method of P. T. P. Tang (ACM TOMS
-// 15(2), 1989) with 256 table entries: x = (256k + j) ln2/256 + r,
-// |r| <= ln2/512, exp(x) = 2^k 2^(j/256) e^r, e^r - 1 by its degree-4 Taylor
-// polynomial (truncation below 4e-17 relative).  Measured within 1 ulp of
-// libm over [-760, 0], subnormal results included; exact 0 below.  The
-// integer k must fit 32 bits: x >= -5.8e6, which the host checks for every
-// plan that runs this kernel (kQuadMinArgument).  tab[j] = 2^(j/256).
-__device__ inline double exp_neg256(double x, const double* tab) {
-    constexpr double kInvLn2x256 = 369.32993046757463228414071833648; // 256 / ln 2
-    constexpr double kHi = 0.010830417275428772 / 4.0;                 // ln2/256, 32 trailing zero bits
-    constexpr double kLo = 7.420820373486988e-09 / 4.0;                // ln2/256 - kHi
-    constexpr double kShifter = 6755399441055744.0;                    // 1.5 * 2^52
-    const double s = fma(x, kInvLn2x256, kShifter);
+// 15(2), 1989): x = (64k + j) ln2/64 + r, |r| <= ln2/128,
+// exp(x) = 2^k 2^(j/64) e^r, e^r - 1 by its degree-5 Taylor polynomial
+// (truncation below 4e-17 relative).  Within 2 ulp of libm over [-745, 0],
+// subnormal results included; exact 0 below.  The integer 64k must fit 32
+// bits: x >= -5.8e6, which the host checks for every plan that runs this
+// kernel (kQuadMinArgument).  tab[j] = 2^(j/64).
+__device__ inline double exp_neg64(double x, const double* tab) {
+    constexpr double kInvLn2x64 = 92.332482616893658071035179584121; // 64 / ln 2
+    constexpr double kHi = 0.010830417275428772;                      // ln2/64, 32 trailing zero bits
+    constexpr double kLo = 7.420820373486988e-09;                     // ln2/64 - kHi
+    constexpr double kShifter = 6755399441055744.0;                   // 1.5 * 2^52
+    const double s = fma(x, kInvLn2x64, kShifter);
     const double kf = s - kShifter;
     double r = fma(kf, -kHi, x);
     r = fma(kf, -kLo, r);
     const int ki = __double2loint(s);
-    double q = fma(r, 1.0 / 24.0, 1.0 / 6.0);
+    double q = fma(r, 1.0 / 120.0, 1.0 / 24.0);
+    q = fma(q, r, 1.0 / 6.0);
     q = fma(q, r, 0.5);
     q = fma(q, r, 1.0);
     const double em1 = r * q; // e^r - 1
     const double t = tab[ki & (kQuadTab - 1)];
-    return ldexp(fma(t, em1, t), ki >> 8);
+    return ldexp(fma(t, em1, t), ki >> 6);
+}
+
+// Byte offset that no output row reaches: a buffer store there is dropped by
+// the buffer's range check.
+constexpr int kDroppedOffset = 0x40000000;
+
+typedef int i2 __attribute__((ext_vector_type(2)));
+
+// Power spectrum of the coefficients in LDS (16x16 Gram tiles; units (tile
+// pair, l) split over the wavefronts in contiguous ranges, as in
+// power_spectrum_walk) written to one output row of F values of d.out_dtype
+// bytes with raw buffer stores.  A lane's feature offsets for a tile pair come
+// from the plan's fbase/fstride tables (layout of soap.cpp:997-1013); channel
+// pairs i > j and pad channels get an offset past the row, which the buffer's
+// range check drops, so the stores need no branches.
+__device__ void power_spectrum_row(const double* s_c, const int* loff, const MfmaDims& d,
+                                   const double* __restrict__ ps_pref, const int32_t* __restrict__ fbase,
+                                   const int32_t* __restrict__ fstride, void* out_row, int wave, int waves) {
+    const int lane = threadIdx.x % kWaveThreads;
+    const int W = d.S * d.n;
+    const int zero_row = d.crow - 1;
+    const int RT = (W + 15) / 16;
+    const int L = d.L;
+    const int hp = d.hpad;
+    const int units = RT * (RT + 1) / 2 * L;
+    const int u_begin = wave * units / waves;
+    const int u_end = (wave + 1) * units / waves;
+    if (u_begin >= u_end) return;
+    const int esize = d.out_dtype;
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(out_row, 0, static_cast<int>(d.F * esize), 0x00020000);
+    int p = u_begin / L;
+    int l = u_begin - p * L;
+    int bi = 0;
+    while (p >= RT - bi) {
+        p -= RT - bi;
+        ++bi;
+    }
+    int bj = bi + p;
+    const double* arow = s_c;
+    const double* brow = s_c;
+    int fb[4] = {kDroppedOffset, kDroppedOffset, kDroppedOffset, kDroppedOffset}, fs[4] = {0, 0, 0, 0};
+    bool new_pair = true;
+    for (int u = u_begin; u < u_end; ++u) {
+        if (new_pair) {
+            new_pair = false;
+            const int ia = 16 * bi + lane % 16 < W ? 16 * bi + lane % 16 : zero_row;
+            const int jb = 16 * bj + lane % 16 < W ? 16 * bj + lane % 16 : zero_row;
+            arow = s_c + ia * hp + lane / 16;
+            brow = s_c + jb * hp + lane / 16;
+            const int j = 16 * bj + lane % 16;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int i = 16 * bi + lane / 16 + 4 * r;
+                const int idx = i < W && j < W ? i * W + j : -1;
+                const int base = idx >= 0 ? fbase[idx] : -1;
+                fb[r] = base >= 0 ? base * esize : kDroppedOffset;
+                fs[r] = base >= 0 ? fstride[idx] * esize : 0;
+            }
+        }
+        const int steps = (2 * l + 4) / 4;
+        const int base = loff[l];
+        d4 acc4 = {0.0, 0.0, 0.0, 0.0};
+        for (int s = 0; s < steps; ++s) acc4 = mfma(arow[base + 4 * s], brow[base + 4 * s], acc4);
+        const double pref = ps_pref[l];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const double v = pref * acc4[r];
+            const int off = fb[r] + l * fs[r];
+            if (esize == 4) {
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(static_cast<float>(v)), rsrc, off, 0, 0);
+            } else {
+                const i2 bits = {__double2loint(v), __double2hiint(v)};
+                __builtin_amdgcn_raw_buffer_store_b64(bits, rsrc, off, 0, 0);
+            }
+        }
+        if (++l == L) {
+            l = 0;
+            new_pair = true;
+            if (++bj == RT) {
+                ++bi;
+                bj = bi;
+            }
+        }
+    }
 }
 
 // KG radial groups, G MFMA instructions per step for every wavefront; the
 // workgroup has blockDim.x / 64 wavefronts (one per register of the plan), at
-// most kQuadMaxWaves, and keeps 4 wavefronts per SIMD (128 VGPRs)
+// most kQuadMaxWaves, and keeps 5 wavefronts per SIMD (96 VGPRs): with its
+// LDS footprint under 32 KB, five 4-wavefront workgroups share a CU
 template <int KG, int G>
-__global__ __launch_bounds__(kQuadMaxWaves * kWaveThreads) __attribute__((amdgpu_waves_per_eu(4)))
+__global__ __launch_bounds__(kQuadMaxWaves * kWaveThreads) __attribute__((amdgpu_waves_per_eu(5)))
 void k_soap_quad(
     const double* __restrict__ positions, const int64_t* __restrict__ pair_start, const int32_t* __restrict__ counts,
     const uint32_t* __restrict__ pair_bin, const double* __restrict__ bx, const double* __restrict__ by,
     const double* __restrict__ bz, const QuadLane* __restrict__ lanes, const double* __restrict__ ps_pref,
-    MfmaDims d, const int64_t* __restrict__ item_begin, int64_t item_base, int64_t items, int64_t per_block,
-    void* out, int64_t pitch, double* partial) {
+    const int32_t* __restrict__ fbase, const int32_t* __restrict__ fstride, MfmaDims d,
+    const int64_t* __restrict__ item_begin, int64_t item_base, int64_t items, int64_t per_block, void* out,
+    int64_t pitch, double* partial) {
     extern __shared__ double lds[];
     const int tid = threadIdx.x;
     const int lane = tid % kWaveThreads;
@@ -91,11 +180,10 @@ void k_soap_quad(
     const int kThreads = static_cast<int>(blockDim.x);
     const int T = kThreads / kWaveThreads;
     const int H = d.H, L = d.L, S = d.S, n = d.n;
-    const int HP = (H + 1) | 1;     // Y row stride (odd); entry H stays zero
     const int hp = d.hpad;          // padded c row
     const int cw = d.crow * hp;     // c words, including the zero row
-    double* s_y = lds;              // kNb * HP
-    double* s_d2 = s_y + kNb * HP;  // kNb
+    double* s_y = lds;              // (H + 1) * kYStride, harmonic-major; row H stays zero
+    double* s_d2 = s_y + (H + 1) * kYStride; // kNb
     double* s_tab = s_d2 + kNb;     // kQuadTab
     double* s_c = s_tab + kQuadTab; // cw
     double* s_csum = s_c + cw;      // cw (inner average only)
@@ -105,7 +193,7 @@ void k_soap_quad(
     int* s_step = s_pseg + (S + 1); // 1
 
     for (int i = tid; i < kQuadTab; i += kThreads) s_tab[i] = exp2(static_cast<double>(i) / kQuadTab);
-    for (int i = tid; i < kNb * HP; i += kThreads) s_y[i] = 0.0;
+    for (int i = tid; i < (H + 1) * kYStride; i += kThreads) s_y[i] = 0.0;
     for (int i = tid; i < cw; i += kThreads) s_c[i] = 0.0;
     if (tid == 0) {
         int off = 0;
@@ -120,9 +208,10 @@ void k_soap_quad(
     const double expo = ql.expo;
     const double beta_r = ql.beta_r;
     const double beta_s = KG == 2 ? ql.beta_s : 0.0;
-    int ycol[G];
+    // the lane's harmonic row of each instruction at its step's first slot
+    const double* yrow[G];
 #pragma unroll
-    for (int g = 0; g < G; ++g) ycol[g] = ql.ycol[g];
+    for (int g = 0; g < G; ++g) yrow[g] = s_y + ql.ycol[g] * kYStride + lane / 16;
     const int cdst = ql.cdst;
     const int ccount = ql.cnt;
     const uint32_t hmask = d.harm_mask[wave];
@@ -233,10 +322,9 @@ void k_soap_quad(
 #pragma unroll
                 for (int s = 0; s < 2; ++s) {
                     const int jj = 4 * (h + s) + krow;
-                    ev[s] = exp_neg256(-expo * s_d2[jj], s_tab);
-                    const double* yrow = s_y + jj * HP;
+                    ev[s] = exp_neg64(-expo * s_d2[jj], s_tab);
 #pragma unroll
-                    for (int g = 0; g < G; ++g) yv[s][g] = yrow[ycol[g]];
+                    for (int g = 0; g < G; ++g) yv[s][g] = yrow[g][4 * (h + s)];
                 }
             };
             // A chunk whose 8 steps all continue the current species (the common
@@ -305,7 +393,7 @@ void k_soap_quad(
                     asm volatile("" : "+s"(lm), "+s"(mk), "+s"(zero));
                     int part = comp;
                     asm volatile("" : "+v"(part));
-                    harmonics_q<0, kQuadLmax>(dx, dy, dz, scale, lm, mk, part, &kHarmonic + zero, s_y + jj * HP);
+                    harmonics_q<0, kQuadLmax, kYStride>(dx, dy, dz, scale, lm, mk, part, &kHarmonic + zero, s_y + jj);
                 }
                 __syncthreads();
                 {
@@ -325,7 +413,8 @@ void k_soap_quad(
             prefetch_centre(centre + 1);
             __syncthreads();
             if (d.mode == 0) {
-                power_spectrum_tiles(s_c, s_loff, d, ps_pref, 0, out, pitch, centre, nullptr, wave, T);
+                power_spectrum_row(s_c, s_loff, d, ps_pref, fbase, fstride, static_cast<char*>(out) + centre * pitch,
+                                   wave, T);
             } else if (d.mode == 1) {
                 for (int i = tid; i < cw; i += kThreads) s_csum[i] += s_c[i];
             } else {
@@ -343,24 +432,25 @@ void k_soap_quad(
 
 template <int KG, int G>
 void launch(hipStream_t stream, int waves, unsigned grid, int64_t per_block, size_t lds, const PreparedBatch& pb,
-            const DeviceGraph& g, const QuadLane* lanes, const double* ps_pref, const MfmaDims& d,
-            const int64_t* item_begin, int64_t base, int64_t count, void* out, int64_t pitch, double* partial) {
+            const DeviceGraph& g, const QuadLane* lanes, const double* ps_pref, const int32_t* fbase,
+            const int32_t* fstride, const MfmaDims& d, const int64_t* item_begin, int64_t base, int64_t count,
+            void* out, int64_t pitch, double* partial) {
     hipLaunchKernelGGL((k_soap_quad<KG, G>), dim3(grid), dim3(waves * kWaveThreads), lds, stream,
                        pb.d_positions.as<double>(), g.pair_start.as<int64_t>(), g.counts.as<int32_t>(),
                        g.pair_bin.as<uint32_t>(), g.bin_x.as<double>(), g.bin_y.as<double>(), g.bin_z.as<double>(),
-                       lanes, ps_pref, d, item_begin, base, count, per_block, out, pitch, partial);
+                       lanes, ps_pref, fbase, fstride, d, item_begin, base, count, per_block, out, pitch, partial);
 }
 
 template <int KG>
 void launch_instr(int instr, hipStream_t stream, int waves, unsigned grid, int64_t per_block, size_t lds,
                   const PreparedBatch& pb, const DeviceGraph& g, const QuadLane* lanes, const double* ps_pref,
-                  const MfmaDims& d, const int64_t* item_begin, int64_t base, int64_t count, void* out, int64_t pitch,
+                  const int32_t* fbase, const int32_t* fstride, const MfmaDims& d, const int64_t* item_begin, int64_t base, int64_t count, void* out, int64_t pitch,
                   double* partial) {
     switch (instr) {
-    case 1: launch<KG, 1>(stream, waves, grid, per_block, lds, pb, g, lanes, ps_pref, d, item_begin, base, count, out, pitch, partial); break;
-    case 2: launch<KG, 2>(stream, waves, grid, per_block, lds, pb, g, lanes, ps_pref, d, item_begin, base, count, out, pitch, partial); break;
-    case 3: launch<KG, 3>(stream, waves, grid, per_block, lds, pb, g, lanes, ps_pref, d, item_begin, base, count, out, pitch, partial); break;
-    case 4: launch<KG, 4>(stream, waves, grid, per_block, lds, pb, g, lanes, ps_pref, d, item_begin, base, count, out, pitch, partial); break;
+    case 1: launch<KG, 1>(stream, waves, grid, per_block, lds, pb, g, lanes, ps_pref, fbase, fstride, d, item_begin, base, count, out, pitch, partial); break;
+    case 2: launch<KG, 2>(stream, waves, grid, per_block, lds, pb, g, lanes, ps_pref, fbase, fstride, d, item_begin, base, count, out, pitch, partial); break;
+    case 3: launch<KG, 3>(stream, waves, grid, per_block, lds, pb, g, lanes, ps_pref, fbase, fstride, d, item_begin, base, count, out, pitch, partial); break;
+    case 4: launch<KG, 4>(stream, waves, grid, per_block, lds, pb, g, lanes, ps_pref, fbase, fstride, d, item_begin, base, count, out, pitch, partial); break;
     default: throw Error(MDX_INTERNAL, "unsupported instruction count for the 4x4-block kernel");
     }
 }
@@ -468,14 +558,15 @@ QuadPlanHost plan_quad_tables(int n, int l_max, int hpad, const std::vector<doub
 
 size_t quad_lds_bytes(const MfmaDims& d) {
     const size_t cw = static_cast<size_t>(d.crow) * static_cast<size_t>(d.hpad);
-    size_t words = static_cast<size_t>(kNb) * ((d.H + 1) | 1) + kNb + kQuadTab + cw;
+    size_t words = static_cast<size_t>(d.H + 1) * kYStride + kNb + kQuadTab + cw;
     if (d.mode == 1) words += cw;
     return words * sizeof(double) + static_cast<size_t>(d.L + 1 + 2 * (d.S + 1) + 1) * sizeof(int);
 }
 
 void launch_quad_expand(hipStream_t stream, int waves, int kg, int instr, const PreparedBatch& pb, const DeviceGraph& g,
-                        const QuadLane* lanes, const double* ps_pref, const MfmaDims& d, const int64_t* item_begin,
-                        int64_t base, int64_t count, void* out, int64_t pitch, double* partial) {
+                        const QuadLane* lanes, const double* ps_pref, const int32_t* fbase, const int32_t* fstride,
+                        const MfmaDims& d, const int64_t* item_begin, int64_t base, int64_t count, void* out,
+                        int64_t pitch, double* partial) {
     if (count <= 0) return;
     const size_t lds = quad_lds_bytes(d);
     MfmaDims dm = d;
@@ -498,11 +589,11 @@ void launch_quad_expand(hipStream_t stream, int waves, int kg, int instr, const 
     const unsigned grid = static_cast<unsigned>((count + per_block - 1) / per_block);
     if (waves < 1 || waves > kQuadMaxWaves) throw Error(MDX_INTERNAL, "unsupported wave count for the 4x4-block kernel");
     if (kg == 1) {
-        launch_instr<1>(instr, stream, waves, grid, per_block, lds, pb, g, lanes, ps_pref, dm, item_begin, base, count,
-                        out, pitch, partial);
+        launch_instr<1>(instr, stream, waves, grid, per_block, lds, pb, g, lanes, ps_pref, fbase, fstride, dm, item_begin,
+                        base, count, out, pitch, partial);
     } else {
-        launch_instr<2>(instr, stream, waves, grid, per_block, lds, pb, g, lanes, ps_pref, dm, item_begin, base, count,
-                        out, pitch, partial);
+        launch_instr<2>(instr, stream, waves, grid, per_block, lds, pb, g, lanes, ps_pref, fbase, fstride, dm, item_begin,
+                        base, count, out, pitch, partial);
     }
     MDX_HIP(hipGetLastError());
 }
