@@ -214,7 +214,7 @@ void run_pipeline(mdx_hip_ctx* ctx, const mdx_soap_plan& plan, mdx::PreparedBatc
                   mdx_timing* timing, int64_t slice = 0, const mdx::SliceHook* on_slice = nullptr) {
     hipStream_t s = ctx->stream;
     MDX_HIP(hipEventRecord(ctx->events[0], s));
-    const int64_t pairs = mdx::build_graph(s, pb, graph, cancel);
+    const int64_t pairs = mdx::build_graph(s, pb, graph, cancel, true);
     MDX_HIP(hipEventRecord(ctx->events[1], s));
     check_cancel(cancel);
     mdx::run_soap(s, plan, pb, graph, out_device, pitch, partials, cancel, ctx->events, timing, slice, on_slice);

@@ -22,6 +22,8 @@
 // centre of the cell, so it is staged in LDS once and scanned by all of them.
 #include "mdx_internal.h"
 
+#include <type_traits>
+
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -178,18 +180,6 @@ __device__ inline int64_t roi_cell(const StructGeom& g, double x, double y, doub
     return g.cell_begin + lx + static_cast<int64_t>(g.roi_dim[0]) * (ly + static_cast<int64_t>(g.roi_dim[1]) * lz);
 }
 
-// Locate enumeration index e (image-major, atom-minor: the reference's
-// extended order, neighbor.cpp:519-528) and compute the image position.
-__device__ inline const StructGeom& ext_lookup(const StructGeom* geom, int64_t nstruct, int64_t e,
-                                              int64_t& key) {
-    int64_t s = find_by_begin(geom, nstruct, e, 0);
-    // structures with zero atoms share ext_begin with the next one; move forward
-    while (s + 1 < nstruct && geom[s + 1].ext_begin <= e) ++s;
-    const StructGeom& g = geom[s];
-    key = e - g.ext_begin;
-    return g;
-}
-
 __device__ inline void image_position(const StructGeom& g, const ImageDesc* images, const double* positions,
                                       int64_t key, double& x, double& y, double& z, int64_t& atom,
                                       int64_t& image) {
@@ -203,35 +193,32 @@ __device__ inline void image_position(const StructGeom& g, const ImageDesc* imag
     z = positions[atom * 3 + 2] + im.shift[2];
 }
 
-__global__ void k_bin_count(const StructGeom* geom, int64_t nstruct, const ImageDesc* images,
-                            const double* positions, int64_t ext_total, int32_t* cell_count) {
-    for (int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; e < ext_total;
-         e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        int64_t key, atom, image;
-        const StructGeom& g = ext_lookup(geom, nstruct, e, key);
-        double x, y, z;
-        image_position(g, images, positions, key, x, y, z, atom, image);
-        bool inside;
-        const int64_t c = roi_cell(g, x, y, z, inside);
-        if (inside) atomicAdd(&cell_count[c], 1);
-    }
-}
-
-__global__ void k_bin_fill(const StructGeom* geom, int64_t nstruct, const ImageDesc* images,
-                           const double* positions, const int32_t* types, int species_major, int64_t ext_total,
-                           const int64_t* cell_start, int32_t* cell_fill, uint64_t* keys) {
-    for (int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; e < ext_total;
-         e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        int64_t key, atom, image;
-        const StructGeom& g = ext_lookup(geom, nstruct, e, key);
-        double x, y, z;
-        image_position(g, images, positions, key, x, y, z, atom, image);
-        bool inside;
-        const int64_t c = roi_cell(g, x, y, z, inside);
-        if (inside) {
-            const int32_t slot = atomicAdd(&cell_fill[c], 1);
-            const uint64_t major = species_major ? static_cast<uint64_t>(types[atom]) << 32 : 0;
-            keys[cell_start[c] + slot] = major | static_cast<uint64_t>(static_cast<uint32_t>(key));
+// Binning walks (image, atom) pairs on a 2-D grid (y: image, x: atom), so no
+// index division is needed.  The extended index of (image q, local atom j) is
+// q * natoms + j (neighbor.cpp:519-528).  Count pass: cell_count[c] += 1;
+// fill pass: keys at cell_start[c] + a slot taken from cell_count.
+template <bool kFill>
+__global__ void k_bin_atoms(const StructGeom* geom, const ImageDesc* images, const double* positions,
+                            const int32_t* centre_struct, const int32_t* types, int species_major, int64_t atoms,
+                            int max_images, int32_t* cell_count, const int64_t* cell_start, uint64_t* keys) {
+    for (int q = blockIdx.y; q < max_images; q += gridDim.y) {
+        for (int64_t a = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; a < atoms;
+             a += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+            const StructGeom& g = geom[centre_struct[a]];
+            if (q >= g.n_images) continue;
+            const ImageDesc& im = images[g.image_begin + q];
+            bool inside;
+            const int64_t c = roi_cell(g, positions[a * 3 + 0] + im.shift[0], positions[a * 3 + 1] + im.shift[1],
+                                       positions[a * 3 + 2] + im.shift[2], inside);
+            if (!inside) continue;
+            if (kFill) {
+                const int32_t slot = atomicAdd(&cell_count[c], 1);
+                const uint64_t major = species_major ? static_cast<uint64_t>(types[a]) << 32 : 0;
+                const uint32_t j = static_cast<uint32_t>(a - g.atom_begin);
+                keys[cell_start[c] + slot] = major | (static_cast<uint32_t>(q) * static_cast<uint32_t>(g.natoms) + j);
+            } else {
+                atomicAdd(&cell_count[c], 1);
+            }
         }
     }
 }
@@ -315,7 +302,10 @@ __global__ void k_cell_species(const int64_t* cell_start, int64_t cells_total, c
 // Centres of each ROI cell in one list: centre_slot (from k_centre_cell) is
 // the centre's place among its cell's centres.
 __global__ void k_centre_fill(const int64_t* centre_cell, const int32_t* centre_slot, int64_t atoms,
-                              const int64_t* cell_centre_start, int32_t* cell_centres) {
+                              const int64_t* cell_centre_start, int32_t* cell_centres, const int64_t* cell_start,
+                              int64_t cells, unsigned long long* stats) {
+    // the binned image total, read back with the search statistics
+    if (blockIdx.x == 0 && threadIdx.x == 0) stats[kStatBinned] = static_cast<unsigned long long>(cell_start[cells]);
     for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < atoms;
          i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
         const int64_t c = centre_cell[i];
@@ -333,15 +323,20 @@ __global__ void k_centre_fill(const int64_t* centre_cell, const int32_t* centre_
 // candidate order; with one species they are exactly the reference's rows.
 // That candidate sequence is the same for every centre of the cell: the
 // workgroup stages it in LDS (kStage candidates at a time) and each
-// wavefront scans it for one centre after another.  Count pass: per-species
-// counts and row totals.  Fill pass: the bin index of every accepted image at
-// pair_start[centre] onwards (wave ballot + popcount compaction).
+// wavefront scans it for one centre after another.  Count pass
+// (kNbrCount): per-species counts and row totals.  Fill pass (kNbrFill): the
+// bin index of every accepted image at pair_start[centre] onwards (wave
+// ballot + popcount compaction).  Slotted pass (kNbrSlotted, the SOAP
+// expansion's layout): both at once, each centre's rows at centre * cap
+// onwards (rows past cap are dropped and reported through stats: [0] the
+// total rows, [1] the largest row count of a centre).
 constexpr int kNbrThreads = 512;
 constexpr int kNbrWaves = kNbrThreads / kWave;
 constexpr int kStage = 1024;        // candidates staged in LDS per pass over a cell's centres
 constexpr int kCentreBatch = 128;   // centres whose running counts live in LDS at once
 constexpr int kSegments = kMaxSpecies * 27;
 constexpr int kNoBoundary = 0x7fffffff;
+constexpr int kNbrCount = 0, kNbrFill = 1, kNbrSlotted = 2;
 
 __device__ inline uint64_t lane_range(int lo, int hi) {
     // bits lo .. hi-1 of a 64-lane mask, 0 <= lo <= hi <= 64
@@ -350,12 +345,16 @@ __device__ inline uint64_t lane_range(int lo, int hi) {
     return upto_hi & ~upto_lo;
 }
 
-template <bool kFill>
+template <int kMode>
 __global__ __launch_bounds__(kNbrThreads) void k_neighbors(
     const StructGeom* geom, int64_t nstruct, const double* positions, int64_t cells_total,
     const int64_t* cell_centre_start, const int32_t* cell_centres, const int64_t* cell_start,
     const int64_t* cell_species_start, const double* bx, const double* by, const double* bz, int S,
-    double accept_max, int32_t* counts, int32_t* totals, const int64_t* pair_start, uint32_t* pair_bin) {
+    double accept_max, int32_t* counts, int32_t* totals, int64_t* pair_start, uint32_t* pair_bin, int64_t cap,
+    unsigned long long* stats) {
+    constexpr bool kFill = kMode == kNbrFill;
+    constexpr bool kCount = kMode != kNbrFill;
+    constexpr bool kWrite = kMode != kNbrCount;
     __shared__ double2 s_xy[kStage];          // candidate x, y
     __shared__ double2 s_zb[kStage];          // candidate z, bin index (bit pattern)
     __shared__ int64_t s_segstart[kSegments]; // first bin of segment (species, cell k)
@@ -432,7 +431,7 @@ __global__ __launch_bounds__(kNbrThreads) void k_neighbors(
                 s_cpos[i * 3 + 0] = positions[static_cast<int64_t>(centre) * 3 + 0];
                 s_cpos[i * 3 + 1] = positions[static_cast<int64_t>(centre) * 3 + 1];
                 s_cpos[i * 3 + 2] = positions[static_cast<int64_t>(centre) * 3 + 2];
-                s_first[i] = kFill ? pair_start[centre] : 0;
+                s_first[i] = kFill ? pair_start[centre] : kMode == kNbrSlotted ? centre * cap : 0;
                 s_found[i] = 0;
             }
             for (int i = tid; i < nb * S; i += kNbrThreads) s_bfound[i] = 0;
@@ -485,15 +484,17 @@ __global__ __launch_bounds__(kNbrThreads) void k_neighbors(
                     // next species boundary of the walk at or after v0 (count pass)
                     int t_next = 1;
                     int bnext = kNoBoundary;
-                    if (!kFill) {
+                    if (kCount) {
                         while (t_next < S && __builtin_amdgcn_readfirstlane(s_segpre[t_next * 27]) < v0) ++t_next;
                         bnext = t_next < S ? __builtin_amdgcn_readfirstlane(s_segpre[t_next * 27]) : kNoBoundary;
                     }
                     // bookkeeping of one wavefront-wide group of candidates at i0
                     auto account = [&](int i0, bool accept, uint64_t mask, uint32_t b) {
-                        if (kFill) {
-                            if (accept) pair_bin[first_row + found + __popcll(mask & below)] = b;
-                        } else {
+                        if (kWrite && accept) {
+                            const int32_t k = found + static_cast<int32_t>(__popcll(mask & below));
+                            if (kFill || k < cap) pair_bin[first_row + k] = b;
+                        }
+                        if (kCount) {
                             while (bnext < v0 + i0 + kWave) {
                                 // rows before the boundary: earlier groups plus this group's lanes below it
                                 const int k = bnext - (v0 + i0);
@@ -541,8 +542,15 @@ __global__ __launch_bounds__(kNbrThreads) void k_neighbors(
                 }
                 __syncthreads();
             }
-            if (!kFill) {
-                for (int i = tid; i < nb; i += kNbrThreads) totals[s_centre[i]] = s_found[i];
+            if (kCount) {
+                for (int i = tid; i < nb; i += kNbrThreads) {
+                    totals[s_centre[i]] = s_found[i];
+                    if (kMode == kNbrSlotted) {
+                        pair_start[s_centre[i]] = s_first[i];
+                        atomicAdd(&stats[kStatRows], static_cast<unsigned long long>(s_found[i]));
+                        atomicMax(&stats[kStatMostRows], static_cast<unsigned long long>(s_found[i]));
+                    }
+                }
                 for (int i = tid; i < nb * S; i += kNbrThreads) {
                     const int ci = i / S, t = i - ci * S;
                     // rows before boundaries t and t + 1 (boundary 0 is the start; a
@@ -812,7 +820,8 @@ void upload_batch(hipStream_t stream, const mdx_batch_view& batch, PreparedBatch
     MDX_HIP(hipStreamSynchronize(stream));
 }
 
-int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr, const volatile int32_t* cancel) {
+int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr, const volatile int32_t* cancel,
+                    bool slotted) {
     const int S = pb.n_species;
     gr.n_species = S;
     const int64_t atoms = pb.atoms;
@@ -820,6 +829,7 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     const int64_t nstruct = pb.structures;
     const size_t cells1 = static_cast<size_t>(cells + 1);
     gr.pair_start.reserve(static_cast<size_t>(atoms + 1) * sizeof(int64_t));
+    gr.slots = 0;
     if (atoms == 0 || cells == 0) {
         MDX_HIP(hipMemsetAsync(gr.pair_start.ptr, 0, static_cast<size_t>(atoms + 1) * sizeof(int64_t), stream));
         gr.counts.reserve(std::max<size_t>(1, static_cast<size_t>(atoms * S) * sizeof(int32_t)));
@@ -836,8 +846,15 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
         throw Error(MDX_INVALID_ARGUMENT, "periodic images exceed the device graph capacity");
     }
 
-    gr.cell_count.reserve(cells1 * sizeof(int32_t));
-    gr.cell_fill.reserve(cells1 * sizeof(int32_t));
+    // one zero-filled block: search statistics (error flag among them), then
+    // the cell counters of binning (count, fill) and of the centres
+    const size_t counter_bytes = kStatWords * sizeof(unsigned long long) + 3 * cells1 * sizeof(int32_t);
+    gr.counters.reserve(counter_bytes);
+    unsigned long long* stats = gr.counters.as<unsigned long long>();
+    int32_t* error_flag = reinterpret_cast<int32_t*>(stats + kStatError);
+    int32_t* cell_count = reinterpret_cast<int32_t*>(stats + kStatWords);
+    int32_t* cell_fill = cell_count + cells1;
+    int32_t* cell_ncentre = cell_fill + cells1;
     gr.cell_start.reserve(cells1 * sizeof(int64_t));
     gr.cell_species_start.reserve(std::max<size_t>(1, static_cast<size_t>(cells) * static_cast<size_t>(S)) *
                                   sizeof(int64_t));
@@ -845,7 +862,6 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     gr.centre_struct.reserve(static_cast<size_t>(atoms) * sizeof(int32_t));
     gr.centre_slot.reserve(static_cast<size_t>(atoms) * sizeof(int32_t));
     gr.cell_centres.reserve(static_cast<size_t>(atoms) * sizeof(int32_t));
-    gr.cell_ncentre.reserve(cells1 * sizeof(int32_t));
     gr.cell_centre_start.reserve(cells1 * sizeof(int64_t));
     gr.bin_key.reserve(static_cast<size_t>(ext) * sizeof(uint64_t));
     gr.bin_x.reserve(static_cast<size_t>(ext) * sizeof(double));
@@ -856,19 +872,24 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     gr.bin_type.reserve(static_cast<size_t>(ext) * sizeof(int32_t));
     gr.counts.reserve(static_cast<size_t>(atoms * S) * sizeof(int32_t));
     gr.totals.reserve(static_cast<size_t>(atoms) * sizeof(int32_t));
-    gr.error_flag.reserve(sizeof(int32_t));
-    MDX_HIP(hipMemsetAsync(gr.error_flag.ptr, 0, sizeof(int32_t), stream));
-    MDX_HIP(hipMemsetAsync(gr.cell_count.ptr, 0, cells1 * sizeof(int32_t), stream));
-    MDX_HIP(hipMemsetAsync(gr.cell_fill.ptr, 0, cells1 * sizeof(int32_t), stream));
-    MDX_HIP(hipMemsetAsync(gr.cell_ncentre.ptr, 0, cells1 * sizeof(int32_t), stream));
+    MDX_HIP(hipMemsetAsync(gr.counters.ptr, 0, counter_bytes, stream));
 
+    // home cell and structure of every atom (the centres)
+    hipLaunchKernelGGL(k_centre_cell, dim3(grid_for(atoms)), dim3(kBlock), 0, stream, geom, nstruct, pos, atoms,
+                       gr.centre_cell.as<int64_t>(), gr.centre_struct.as<int32_t>(), cell_ncentre,
+                       gr.centre_slot.as<int32_t>(), error_flag);
     // bin every periodic image into its ROI cell, sorted by (species, extended index)
-    hipLaunchKernelGGL(k_bin_count, dim3(grid_for(ext)), dim3(kBlock), 0, stream, geom, nstruct, images, pos, ext,
-                       gr.cell_count.as<int32_t>());
-    scan_counts(stream, gr.cell_count.as<int32_t>(), gr.cell_start.as<int64_t>(), cells, gr.scan_tmp);
-    hipLaunchKernelGGL(k_bin_fill, dim3(grid_for(ext)), dim3(kBlock), 0, stream, geom, nstruct, images, pos,
-                       pb.d_types.as<int32_t>(), S > 1 ? 1 : 0, ext, gr.cell_start.as<int64_t>(),
-                       gr.cell_fill.as<int32_t>(), gr.bin_key.as<uint64_t>());
+    int max_images = 1;
+    for (const StructGeom& sg : pb.geom) max_images = std::max(max_images, static_cast<int>(sg.n_images));
+    const dim3 bin_grid(static_cast<unsigned>(std::min<int64_t>((atoms + kBlock - 1) / kBlock, 1 << 16)),
+                        static_cast<unsigned>(std::min(max_images, 65535)));
+    hipLaunchKernelGGL(k_bin_atoms<false>, bin_grid, dim3(kBlock), 0, stream, geom, images, pos,
+                       gr.centre_struct.as<int32_t>(), pb.d_types.as<int32_t>(), 0, atoms, max_images, cell_count,
+                       static_cast<const int64_t*>(nullptr), static_cast<uint64_t*>(nullptr));
+    scan_counts(stream, cell_count, gr.cell_start.as<int64_t>(), cells, gr.scan_tmp);
+    hipLaunchKernelGGL(k_bin_atoms<true>, bin_grid, dim3(kBlock), 0, stream, geom, images, pos,
+                       gr.centre_struct.as<int32_t>(), pb.d_types.as<int32_t>(), S > 1 ? 1 : 0, atoms, max_images,
+                       cell_fill, gr.cell_start.as<int64_t>(), gr.bin_key.as<uint64_t>());
     const unsigned cell_grid = static_cast<unsigned>(std::min<int64_t>(cells, 1 << 20));
     hipLaunchKernelGGL(k_bin_sort, dim3(cell_grid), dim3(kBlock), 0, stream, geom, nstruct, images, pos,
                        pb.d_types.as<int32_t>(), gr.cell_start.as<int64_t>(), cells, gr.bin_key.as<uint64_t>(),
@@ -880,13 +901,10 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
                            gr.cell_species_start.as<int64_t>());
     }
     // centres grouped by home cell
-    hipLaunchKernelGGL(k_centre_cell, dim3(grid_for(atoms)), dim3(kBlock), 0, stream, geom, nstruct, pos, atoms,
-                       gr.centre_cell.as<int64_t>(), gr.centre_struct.as<int32_t>(), gr.cell_ncentre.as<int32_t>(),
-                       gr.centre_slot.as<int32_t>(), gr.error_flag.as<int32_t>());
-    scan_counts(stream, gr.cell_ncentre.as<int32_t>(), gr.cell_centre_start.as<int64_t>(), cells, gr.scan_tmp);
+    scan_counts(stream, cell_ncentre, gr.cell_centre_start.as<int64_t>(), cells, gr.scan_tmp);
     hipLaunchKernelGGL(k_centre_fill, dim3(grid_for(atoms)), dim3(kBlock), 0, stream, gr.centre_cell.as<int64_t>(),
                        gr.centre_slot.as<int32_t>(), atoms, gr.cell_centre_start.as<int64_t>(),
-                       gr.cell_centres.as<int32_t>());
+                       gr.cell_centres.as<int32_t>(), gr.cell_start.as<int64_t>(), cells, stats);
     MDX_HIP(hipGetLastError());
     if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
 
@@ -894,34 +912,66 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     const double cutoff2 = pb.cutoff * pb.cutoff;
     const double accept_max = pb.include_boundary ? cutoff2 : std::nextafter(cutoff2, 0.0);
     const unsigned cell_blocks = static_cast<unsigned>(std::min<int64_t>(cells, 1 << 20));
-    hipLaunchKernelGGL(k_neighbors<false>, dim3(cell_blocks), dim3(kNbrThreads), 0, stream, geom, nstruct, pos,
-                       cells, gr.cell_centre_start.as<int64_t>(), gr.cell_centres.as<int32_t>(),
-                       gr.cell_start.as<int64_t>(), gr.cell_species_start.as<int64_t>(), gr.bin_x.as<double>(),
-                       gr.bin_y.as<double>(), gr.bin_z.as<double>(), S, accept_max,
-                       gr.counts.as<int32_t>(), gr.totals.as<int32_t>(), static_cast<const int64_t*>(nullptr),
-                       static_cast<uint32_t*>(nullptr));
+    auto neighbors = [&](auto mode, int64_t cap) {
+        hipLaunchKernelGGL(k_neighbors<decltype(mode)::value>, dim3(cell_blocks), dim3(kNbrThreads), 0, stream, geom,
+                           nstruct, pos, cells, gr.cell_centre_start.as<int64_t>(), gr.cell_centres.as<int32_t>(),
+                           gr.cell_start.as<int64_t>(), gr.cell_species_start.as<int64_t>(), gr.bin_x.as<double>(),
+                           gr.bin_y.as<double>(), gr.bin_z.as<double>(), S, accept_max, gr.counts.as<int32_t>(),
+                           gr.totals.as<int32_t>(), gr.pair_start.as<int64_t>(), gr.pair_bin.as<uint32_t>(), cap,
+                           stats);
+        MDX_HIP(hipGetLastError());
+    };
+    using Count = std::integral_constant<int, kNbrCount>;
+    using Fill = std::integral_constant<int, kNbrFill>;
+    using Slotted = std::integral_constant<int, kNbrSlotted>;
+    const int64_t cap = slotted ? gr.slot_cap : 0;
+    const bool use_slots = cap > 0 && atoms * cap * static_cast<int64_t>(sizeof(uint32_t)) <= kMaxSlottedBytes;
+    gr.slots = 0;
+    if (use_slots) {
+        // one pass: counts and rows at centre * cap
+        gr.pair_bin.reserve(static_cast<size_t>(atoms * cap) * sizeof(uint32_t));
+        neighbors(Slotted{}, cap);
+        unsigned long long st[kStatWords] = {};
+        MDX_HIP(hipMemcpyAsync(st, stats, sizeof(st), hipMemcpyDeviceToHost, stream));
+        MDX_HIP(hipStreamSynchronize(stream));
+        if (st[kStatError] != 0) throw Error(MDX_INTERNAL, "a centre fell outside its structure's cell grid");
+        if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
+        const int64_t pairs = static_cast<int64_t>(st[kStatRows]);
+        const int64_t most = static_cast<int64_t>(st[kStatMostRows]);
+        const int64_t binned = static_cast<int64_t>(st[kStatBinned]);
+        if (most <= cap) {
+            gr.slots = cap;
+            gr.pairs = pairs;
+            gr.binned = binned;
+            return pairs;
+        }
+        // a centre overflowed its slot: later calls use a larger one (or the
+        // compact layout), this one lays the counted rows out compactly
+        int64_t grown = kMinSlotCap;
+        while (grown < most) grown *= 2;
+        gr.slot_cap = grown <= kMaxSlotCap ? grown : 0;
+        scan_counts(stream, gr.totals.as<int32_t>(), gr.pair_start.as<int64_t>(), atoms, gr.scan_tmp);
+        gr.pair_bin.reserve(std::max<size_t>(1, static_cast<size_t>(pairs) * sizeof(uint32_t)));
+        neighbors(Fill{}, 0);
+        gr.pairs = pairs;
+        gr.binned = binned;
+        return pairs;
+    }
+    neighbors(Count{}, 0);
     scan_counts(stream, gr.totals.as<int32_t>(), gr.pair_start.as<int64_t>(), atoms, gr.scan_tmp);
     MDX_HIP(hipGetLastError());
     int64_t pairs = 0;
     MDX_HIP(hipMemcpyAsync(&pairs, gr.pair_start.as<int64_t>() + atoms, sizeof(int64_t), hipMemcpyDeviceToHost,
                            stream));
-    int64_t binned = 0;
-    MDX_HIP(hipMemcpyAsync(&binned, gr.cell_start.as<int64_t>() + cells, sizeof(int64_t), hipMemcpyDeviceToHost,
-                           stream));
-    int32_t flag = 0;
-    MDX_HIP(hipMemcpyAsync(&flag, gr.error_flag.ptr, sizeof(int32_t), hipMemcpyDeviceToHost, stream));
+    unsigned long long st[kStatWords] = {};
+    MDX_HIP(hipMemcpyAsync(st, stats, sizeof(st), hipMemcpyDeviceToHost, stream));
     MDX_HIP(hipStreamSynchronize(stream));
-    if (flag != 0) throw Error(MDX_INTERNAL, "a centre fell outside its structure's cell grid");
+    const int64_t binned = static_cast<int64_t>(st[kStatBinned]);
+    if (st[kStatError] != 0) throw Error(MDX_INTERNAL, "a centre fell outside its structure's cell grid");
     if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
     if (pairs >= (int64_t(1) << 40)) throw Error(MDX_INTERNAL, "implausible neighbour pair count");
     gr.pair_bin.reserve(std::max<size_t>(1, static_cast<size_t>(pairs) * sizeof(uint32_t)));
-    hipLaunchKernelGGL(k_neighbors<true>, dim3(cell_blocks), dim3(kNbrThreads), 0, stream, geom, nstruct, pos,
-                       cells, gr.cell_centre_start.as<int64_t>(), gr.cell_centres.as<int32_t>(),
-                       gr.cell_start.as<int64_t>(), gr.cell_species_start.as<int64_t>(), gr.bin_x.as<double>(),
-                       gr.bin_y.as<double>(), gr.bin_z.as<double>(), S, accept_max,
-                       static_cast<int32_t*>(nullptr), static_cast<int32_t*>(nullptr), gr.pair_start.as<int64_t>(),
-                       gr.pair_bin.as<uint32_t>());
-    MDX_HIP(hipGetLastError());
+    neighbors(Fill{}, 0);
     gr.pairs = pairs;
     gr.binned = binned;
     return pairs;

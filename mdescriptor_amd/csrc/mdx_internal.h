@@ -104,7 +104,9 @@ struct DeviceGraph {
     int64_t binned = 0;
     int64_t pairs = 0;
     int n_species = 1;
-    DeviceBuffer cell_count, cell_start, cell_fill; // per ROI cell
+    DeviceBuffer counters;   // zero-filled per build: u64 statistics[kStatWords], then i32 cell
+                             // counts of binning (count, fill) and of the centres, [cells + 1] each
+    DeviceBuffer cell_start; // i64[cells + 1] first bin of each ROI cell
     DeviceBuffer bin_key;                           // unsorted u64 keys, (species << 32) | extended index
     DeviceBuffer cell_species_start;                // i64[cells * n_species]: first bin of each species in a cell
     DeviceBuffer centre_struct;                     // i32 structure of each atom
@@ -114,21 +116,33 @@ struct DeviceGraph {
     DeviceBuffer bin_type;                          // i32 species index
     DeviceBuffer centre_cell;                       // i64 home ROI cell per atom
     DeviceBuffer centre_slot;                       // i32 place of the atom among its cell's centres
-    DeviceBuffer cell_ncentre;                      // i32[cells + 1] centres per ROI cell
     DeviceBuffer cell_centre_start;                 // i64[cells + 1] first entry of a cell in cell_centres
     DeviceBuffer cell_centres;                      // i32[atoms] centres grouped by home cell
     DeviceBuffer counts;     // i32[atoms * n_species]
     DeviceBuffer totals;     // i32[atoms]
-    DeviceBuffer pair_start; // i64[atoms + 1]
-    DeviceBuffer pair_bin;   // u32[pairs]
+    DeviceBuffer pair_start; // i64[atoms + 1]: first row of each centre (compact: the
+                             // prefix sum of totals, pair_start[atoms] = pairs; slotted: centre * slots)
+    DeviceBuffer pair_bin;   // u32 rows: [pairs] compact, [atoms * slots] slotted
+    int64_t slots = 0;       // layout of the last build: 0 compact, else rows reserved per centre
+    int64_t slot_cap = 512;  // rows per centre for the next slotted build (0: compact only)
     DeviceBuffer scan_tmp;   // block sums of the scans
-    DeviceBuffer error_flag; // i32, set by a kernel on an internal inconsistency
 };
 
 // Build (or rebuild) the device graph of a prepared batch at pb.cutoff.
-// Returns the pair count.  Polls cancel between launches.
+// Returns the pair count.  Polls cancel between launches.  slotted: the rows
+// may be laid out at centre * graph.slot_cap (one search pass instead of a
+// count and a fill pass) when every centre fits; graph.slots records the
+// layout built.  Only consumers that read rows through pair_start[centre] and
+// the per-species counts may ask for it (the SOAP expansion).
+// graph statistics words, read back once per build: rows of the search pass,
+// the largest row count of a centre, binned images, and an error flag (set by a
+// kernel on an internal inconsistency)
+constexpr int kStatRows = 0, kStatMostRows = 1, kStatBinned = 2, kStatError = 3, kStatWords = 4;
+constexpr int64_t kMinSlotCap = 512;
+constexpr int64_t kMaxSlotCap = 8192;
+constexpr int64_t kMaxSlottedBytes = int64_t(4) << 30;
 int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& graph,
-                    const volatile int32_t* cancel);
+                    const volatile int32_t* cancel, bool slotted = false);
 
 // Compute units of the current device (queried once per process and device).
 int device_compute_units();

@@ -111,6 +111,32 @@ def _random_cluster(seed, atoms, species):
                            offsets=np.array([0, atoms, 2 * atoms]))
 
 
+def test_slot_overflow_falls_back_to_the_compact_layout(hip_context, oracle):
+    """The SOAP graph keeps 512 rows per centre in one search pass; a centre
+    with more neighbours makes that call lay the rows out compactly and the
+    next call use larger slots.  Both calls, and a normal batch after them,
+    must match the oracle."""
+
+    rng = np.random.default_rng(7)
+    atoms = 640
+    dense = SimpleNamespace(numbers=np.where(np.arange(atoms) % 3 == 0, 8, 1).astype(np.int32),
+                            positions=rng.uniform(0.0, 3.5, (atoms, 3)), cells=np.zeros((1, 3, 3)),
+                            pbc=np.zeros((1, 3), np.int32), offsets=np.array([0, atoms]))
+    params = {"species": [1, 8], "n_max": 3, "l_max": 2, "r_cut": 3.0}
+    plan, basis = _plan(hip_context, params, "off", "float64")
+    try:
+        expected = _oracle_soap(oracle, dense, params, basis, "off")
+        for _ in range(2):
+            values, timing = plan.compute(dense)
+            assert timing["pairs"] > 512 * atoms // 2
+            assert scaled_error(values, expected) <= F64_GATE
+        work = workloads.config(1, "small")
+        values, _ = plan.compute(work.batch)
+        assert scaled_error(values, _oracle_soap(oracle, work.batch, params, basis, "off")) <= F64_GATE
+    finally:
+        plan.close()
+
+
 @pytest.mark.parametrize("n_max,l_max", [(1, 0), (2, 1), (3, 2), (4, 3), (4, 7), (5, 4), (6, 5), (7, 9),
                                          (8, 6), (8, 8), (8, 10)])
 def test_quad_kernel_shapes(hip_context, oracle, monkeypatch, n_max, l_max):
