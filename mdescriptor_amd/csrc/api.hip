@@ -596,7 +596,9 @@ int mdx_hip_soap_plan_create(mdx_hip_ctx* ctx, const mdx_soap_params* params, md
             const bool quad_range = -max_expo * plan->cutoff * plan->cutoff >= mdx::kQuadMinArgument;
             if (plan->use_mfma && defaults && quad_range && (choice == "auto" || choice == "quad")) {
                 const mdx::QuadPlanHost qp = mdx::plan_quad_tables(n, p.l_max, md.hpad, beta, pref, expo);
-                if (qp.waves > 0 && mdx::quad_lds_bytes(md) <= 64 * 1024) {
+                mdx::MfmaDims qd = md;
+                qd.crow = mdx::quad_coefficient_rows(plan->Sc, n);
+                if (qp.waves > 0 && mdx::quad_lds_bytes(qd) <= 64 * 1024) {
                     plan->quad_waves = qp.waves;
                     plan->quad_kg = qp.kg;
                     plan->quad_instr = qp.instr;

@@ -66,6 +66,20 @@ int device_compute_units() {
     return cached[dev];
 }
 
+StreamPoint::~StreamPoint() {
+    if (event_ != nullptr) (void)hipEventDestroy(event_);
+}
+
+void StreamPoint::wait(hipStream_t stream) {
+    if (event_ == nullptr) MDX_HIP(hipEventCreateWithFlags(&event_, hipEventDisableTiming));
+    MDX_HIP(hipEventRecord(event_, stream));
+    for (;;) {
+        const hipError_t e = hipEventQuery(event_);
+        if (e == hipSuccess) return;
+        if (e != hipErrorNotReady) MDX_HIP(e);
+    }
+}
+
 void DeviceBuffer::release() {
     if (ptr != nullptr) {
         (void)hipFree(ptr);
@@ -632,6 +646,33 @@ __global__ __launch_bounds__(kBlock) void k_scan_apply(const int32_t* in, int64_
     if (blockIdx.x == 0 && threadIdx.x == 0) out[n] = sums[nb];
 }
 
+// the whole scan in one workgroup, tile after tile (short arrays: one launch
+// instead of three)
+__global__ __launch_bounds__(kBlock) void k_scan_one(const int32_t* in, int64_t n, int64_t* out) {
+    __shared__ int64_t lds[kBlock];
+    int64_t carry = 0;
+    for (int64_t base = 0; base < n; base += kScanTile) {
+        int64_t vals[kScanItems];
+        int64_t local = 0;
+        for (int i = 0; i < kScanItems; ++i) {
+            const int64_t idx = base + static_cast<int64_t>(threadIdx.x) * kScanItems + i;
+            vals[i] = idx < n ? in[idx] : 0;
+            local += vals[i];
+        }
+        int64_t total;
+        int64_t run = carry + block_exclusive_scan(local, lds, total);
+        for (int i = 0; i < kScanItems; ++i) {
+            const int64_t idx = base + static_cast<int64_t>(threadIdx.x) * kScanItems + i;
+            if (idx < n) out[idx] = run;
+            run += vals[i];
+        }
+        carry += total;
+    }
+    if (threadIdx.x == 0) out[n] = carry;
+}
+
+constexpr int64_t kScanOneTiles = 8; // up to 8 tiles: one workgroup
+
 unsigned grid_for(int64_t work, int block = kBlock) {
     const int64_t blocks = (work + block - 1) / block;
     return static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(blocks, 1 << 20)));
@@ -641,6 +682,10 @@ unsigned grid_for(int64_t work, int block = kBlock) {
 
 void scan_counts(hipStream_t stream, const int32_t* in, int64_t* out, int64_t n, DeviceBuffer& tmp) {
     const int64_t nb = std::max<int64_t>(1, (n + kScanTile - 1) / kScanTile);
+    if (nb <= kScanOneTiles) {
+        hipLaunchKernelGGL(k_scan_one, dim3(1), dim3(kBlock), 0, stream, in, n, out);
+        return;
+    }
     tmp.reserve(static_cast<size_t>(nb + 1) * sizeof(int64_t));
     int64_t* sums = tmp.as<int64_t>();
     hipLaunchKernelGGL(k_scan_reduce, dim3(static_cast<unsigned>(nb)), dim3(kBlock), 0, stream, in, n, sums);
@@ -933,7 +978,9 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
         neighbors(Slotted{}, cap);
         unsigned long long st[kStatWords] = {};
         MDX_HIP(hipMemcpyAsync(st, stats, sizeof(st), hipMemcpyDeviceToHost, stream));
-        MDX_HIP(hipStreamSynchronize(stream));
+        // the expansion launch waits on these words: poll rather than sleep in
+        // a blocking synchronisation, whose wake-up costs tens of microseconds
+        gr.read_back.wait(stream);
         if (st[kStatError] != 0) throw Error(MDX_INTERNAL, "a centre fell outside its structure's cell grid");
         if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
         const int64_t pairs = static_cast<int64_t>(st[kStatRows]);

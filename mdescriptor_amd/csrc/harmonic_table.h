@@ -101,4 +101,34 @@ constexpr HarmonicRecurrence make_harmonic_recurrence() {
 
 constexpr HarmonicRecurrence kHarmonic = make_harmonic_recurrence();
 
+// Scaled form of the same recurrence, Q_l^m = S_lm Qs_l^m, with the scales
+// chosen so that the z coefficient of every step is one:
+//   Qs_m^m = (x + iy)^m Qs_0^0,  Qs_{m+1}^m = z Qs_m^m,
+//   Qs_l^m = z Qs_{l-1}^m - C_lm r^2 Qs_{l-2}^m,
+//   S_00 = N_00,  S_mm = D_m S_{m-1,m-1},  S_{m+1,m} = E_m S_mm,  S_lm = A_lm S_{l-1,m},
+//   C_lm = B_lm S_{l-2,m} / S_lm.
+// A step then costs one multiply-add and two multiplies; S_lm is applied once
+// per coefficient instead of once per neighbour.
+struct ScaledHarmonicRecurrence {
+    double s[kHarmonicLmax + 1][kHarmonicLmax + 1]; // S_lm, m <= l
+    double c[kHarmonicLmax + 1][kHarmonicLmax + 1]; // C_lm, m + 2 <= l
+};
+
+constexpr ScaledHarmonicRecurrence make_scaled_harmonic_recurrence() {
+    ScaledHarmonicRecurrence t{};
+    const HarmonicRecurrence h = make_harmonic_recurrence();
+    t.s[0][0] = h.n00;
+    for (int m = 1; m <= kHarmonicLmax; ++m) t.s[m][m] = h.d[m] * t.s[m - 1][m - 1];
+    for (int m = 0; m < kHarmonicLmax; ++m) t.s[m + 1][m] = h.e[m] * t.s[m][m];
+    for (int m = 0; m <= kHarmonicLmax; ++m) {
+        for (int l = m + 2; l <= kHarmonicLmax; ++l) {
+            t.s[l][m] = h.a[l][m] * t.s[l - 1][m];
+            t.c[l][m] = h.b[l][m] * t.s[l - 2][m] / t.s[l][m];
+        }
+    }
+    return t;
+}
+
+constexpr ScaledHarmonicRecurrence kScaledHarmonic = make_scaled_harmonic_recurrence();
+
 } // namespace mdx

@@ -97,6 +97,21 @@ struct PreparedBatch {
     DeviceBuffer d_offsets;   // i64[structures+1]
 };
 
+// An event recorded on a stream and polled until the stream reaches it (a
+// lower-latency wait than a blocking stream synchronisation).  Created on
+// first use on the current device; one per owner, not copyable.
+class StreamPoint {
+public:
+    StreamPoint() = default;
+    StreamPoint(const StreamPoint&) = delete;
+    StreamPoint& operator=(const StreamPoint&) = delete;
+    ~StreamPoint();
+    void wait(hipStream_t stream);
+
+private:
+    hipEvent_t event_ = nullptr;
+};
+
 // Device graph (kernel 1 output).  Pairs are indices into the cell-sorted
 // binned image arrays; rows are grouped by neighbour species when
 // n_species > 1 and keep the reference's candidate order inside a species.
@@ -125,6 +140,7 @@ struct DeviceGraph {
     DeviceBuffer pair_bin;   // u32 rows: [pairs] compact, [atoms * slots] slotted
     int64_t slots = 0;       // layout of the last build: 0 compact, else rows reserved per centre
     int64_t slot_cap = 512;  // rows per centre for the next slotted build (0: compact only)
+    StreamPoint read_back;   // completion of the statistics read-back
     DeviceBuffer scan_tmp;   // block sums of the scans
 };
 

@@ -426,7 +426,7 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
         md.clamp = p.clamp;
         md.Sc = p.Sc;
         md.compression = p.compression;
-        md.crow = mfma_coefficient_rows(p.Sc, p.n, p.compression);
+        md.crow = p.quad_waves > 0 ? quad_coefficient_rows(p.Sc, p.n) : mfma_coefficient_rows(p.Sc, p.n, p.compression);
         md.radial = p.radial_basis;
         md.grid = p.grid_size;
         md.weighted = p.weighted;

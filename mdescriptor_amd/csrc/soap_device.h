@@ -70,6 +70,53 @@ __device__ __forceinline__ void harmonics_fixed(double x, double y, double z, do
     }
 }
 
+// The same harmonics in the scaled form of harmonic_table.h: writes
+// Qs_l^m = Q_l^m / S_lm (the caller applies S_lm to whatever it accumulates
+// from them).  Same lanes, masks and layout as harmonics_fixed.
+template <int LM, int kStride>
+__device__ __forceinline__ void harmonics_scaled_fixed(double x, double y, double z, double scale, uint32_t mask,
+                                                      int comp, const ScaledHarmonicRecurrence* __restrict__ hr,
+                                                      double* out) {
+    const double r2 = x * x + y * y + z * z;
+    double sre = scale, sim = 0.0;
+#pragma unroll
+    for (int m = 0; m <= LM; ++m) {
+        if ((mask >> m) == 0) break;
+        if (m > 0) {
+            const double nr = fma(x, sre, -(y * sim));
+            const double ni = fma(x, sim, y * sre);
+            sre = nr;
+            sim = ni;
+        }
+        if (((mask >> m) & 1u) == 0) continue;
+        double* col = out + (comp == 0 ? -m : m) * kStride;
+        double q1 = comp == 0 ? sre : sim;
+        if (m > 0 || comp == 0) col[(m * m + m) * kStride] = q1;
+        if (m + 1 > LM) continue;
+        double q2 = q1;
+        q1 = z * q2;
+        if (m > 0 || comp == 0) col[((m + 1) * (m + 1) + (m + 1)) * kStride] = q1;
+#pragma unroll
+        for (int l = m + 2; l <= LM; ++l) {
+            const double q = fma(z, q1, -(hr->c[l][m] * r2) * q2);
+            if (m > 0 || comp == 0) col[(l * l + l) * kStride] = q;
+            q2 = q1;
+            q1 = q;
+        }
+    }
+}
+
+template <int LM = 0, int kTop = kHarmonicLmax, int kStride = 1>
+__device__ __forceinline__ void harmonics_scaled(double x, double y, double z, double scale, int l_max, uint32_t mask,
+                                                int comp, const ScaledHarmonicRecurrence* __restrict__ hr,
+                                                double* out) {
+    if (l_max == LM) {
+        harmonics_scaled_fixed<LM, kStride>(x, y, z, scale, mask, comp, hr, out);
+    } else if constexpr (LM < kTop) {
+        harmonics_scaled<LM + 1, kTop, kStride>(x, y, z, scale, l_max, mask, comp, hr, out);
+    }
+}
+
 // harmonics_fixed<l_max, kStride> for a run-time l_max <= kTop (a wave-uniform
 // branch chain)
 template <int LM = 0, int kTop = kHarmonicLmax, int kStride = 1>

@@ -99,6 +99,10 @@ struct QuadLane {
     int32_t cdst = -1, cnt = 0;
 };
 
+// LDS coefficient rows of the 4x4-block kernel: S*n channels, plus a zero row
+// for the Gram tiles' pad channels unless S*n is a multiple of 16
+inline int quad_coefficient_rows(int S, int n) { return S * n + ((S * n) % 16 != 0 ? 1 : 0); }
+
 struct QuadPlanHost {
     int waves = 0;               // 0: the shape is outside the kernel's limits
     int kg = 0;                  // radial groups of 4 channels (1 or 2)

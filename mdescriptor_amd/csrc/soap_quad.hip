@@ -88,6 +88,21 @@ typedef int i2 __attribute__((ext_vector_type(2)));
 // from the plan's fbase/fstride tables (layout of soap.cpp:997-1013); channel
 // pairs i > j and pad channels get an offset past the row, which the buffer's
 // range check drops, so the stores need no branches.
+template <int kSteps>
+__device__ __forceinline__ d4 gram_tile(const double* arow, const double* brow) {
+    double a[kSteps], b[kSteps];
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+        a[s] = arow[4 * s];
+        b[s] = brow[4 * s];
+    }
+    d4 acc = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) acc = mfma(a[s], b[s], acc);
+    return acc;
+}
+
+template <int kBytes>
 __device__ void power_spectrum_row(const double* s_c, const int* loff, const MfmaDims& d,
                                    const double* __restrict__ ps_pref, const int32_t* __restrict__ fbase,
                                    const int32_t* __restrict__ fstride, void* out_row, int wave, int waves) {
@@ -101,7 +116,7 @@ __device__ void power_spectrum_row(const double* s_c, const int* loff, const Mfm
     const int u_begin = wave * units / waves;
     const int u_end = (wave + 1) * units / waves;
     if (u_begin >= u_end) return;
-    const int esize = d.out_dtype;
+    constexpr int esize = kBytes;
     const __amdgpu_buffer_rsrc_t rsrc =
         __builtin_amdgcn_make_buffer_rsrc(out_row, 0, static_cast<int>(d.F * esize), 0x00020000);
     int p = u_begin / L;
@@ -133,11 +148,20 @@ __device__ void power_spectrum_row(const double* s_c, const int* loff, const Mfm
                 fs[r] = base >= 0 ? fstride[idx] * esize : 0;
             }
         }
-        const int steps = (2 * l + 4) / 4;
-        const int base = loff[l];
-        d4 acc4 = {0.0, 0.0, 0.0, 0.0};
-        for (int s = 0; s < steps; ++s) acc4 = mfma(arow[base + 4 * s], brow[base + 4 * s], acc4);
         const double pref = ps_pref[l];
+        // K steps of degree l: ceil((2l + 1) / 4), operands read before the MFMAs
+        const int base = loff[l];
+        d4 acc4;
+        switch ((2 * l + 4) / 4) {
+        case 1: acc4 = gram_tile<1>(arow + base, brow + base); break;
+        case 2: acc4 = gram_tile<2>(arow + base, brow + base); break;
+        case 3: acc4 = gram_tile<3>(arow + base, brow + base); break;
+        case 4: acc4 = gram_tile<4>(arow + base, brow + base); break;
+        default: {
+            acc4 = d4{0.0, 0.0, 0.0, 0.0};
+            for (int s = 0; s < (2 * l + 4) / 4; ++s) acc4 = mfma(arow[base + 4 * s], brow[base + 4 * s], acc4);
+        }
+        }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const double v = pref * acc4[r];
@@ -181,12 +205,13 @@ void k_soap_quad(
     const int T = kThreads / kWaveThreads;
     const int H = d.H, L = d.L, S = d.S, n = d.n;
     const int hp = d.hpad;          // padded c row
-    const int cw = d.crow * hp;     // c words, including the zero row
+    const int cw = d.crow * hp;     // c words (a zero row last unless S*n is a multiple of 16)
     double* s_y = lds;              // (H + 1) * kYStride, harmonic-major; row H stays zero
     double* s_d2 = s_y + (H + 1) * kYStride; // kNb
     double* s_tab = s_d2 + kNb;     // kQuadTab
     double* s_c = s_tab + kQuadTab; // cw
-    double* s_csum = s_c + cw;      // cw (inner average only)
+    double* s_scale = s_c + cw;     // hp: S_lm of each padded column (scaled harmonics)
+    double* s_csum = s_scale + hp;  // cw (inner average only)
     int* s_loff = reinterpret_cast<int*>(s_csum + (d.mode == 1 ? cw : 0)); // L + 1
     int* s_seg = s_loff + (L + 1);  // S + 1
     int* s_pseg = s_seg + (S + 1);  // S + 1
@@ -195,6 +220,16 @@ void k_soap_quad(
     for (int i = tid; i < kQuadTab; i += kThreads) s_tab[i] = exp2(static_cast<double>(i) / kQuadTab);
     for (int i = tid; i < (H + 1) * kYStride; i += kThreads) s_y[i] = 0.0;
     for (int i = tid; i < cw; i += kThreads) s_c[i] = 0.0;
+    for (int i = tid; i < hp; i += kThreads) {
+        // column i of the padded row: degree l block at loff[l], 4 ceil((2l+1)/4) wide
+        int l = 0, off = 0;
+        while (l + 1 < L && off + 4 * ((2 * l + 4) / 4) <= i) {
+            off += 4 * ((2 * l + 4) / 4);
+            ++l;
+        }
+        const int c = i - off;
+        s_scale[i] = c <= 2 * l ? kScaledHarmonic.s[l][c <= l ? l - c : c - l] : 0.0;
+    }
     if (tid == 0) {
         int off = 0;
         for (int l = 0; l <= L; ++l) {
@@ -310,11 +345,15 @@ void k_soap_quad(
             // count summed zeros and are not stored
             auto fold = [&](int q) {
                 double* cdst_q = s_c + q * n * hp + cdst;
+                // the harmonics were staged in the scaled form: each output
+                // column takes its S_lm (cdst is the column plus n' * hp)
+                const int nrow = (KG == 2 ? 4 * ((lane / 4) % 2) : 0) + lane / 16;
+                const double* scale_col = s_scale + (cdst - nrow * hp);
 #pragma unroll
                 for (int g = 0; g < G; ++g) {
                     double c = mfma4(beta_r, acc[g], 0.0);
                     if (KG == 2) c = mfma4(beta_s, half_mirror(acc[g]), c);
-                    if (cdst >= 0 && g < ccount) cdst_q[4 * g] = c;
+                    if (cdst >= 0 && g < ccount) cdst_q[4 * g] = c * scale_col[4 * g];
                 }
             };
             // operands of steps h and h + 1 of the chunk: exps and harmonic reads
@@ -393,7 +432,8 @@ void k_soap_quad(
                     asm volatile("" : "+s"(lm), "+s"(mk), "+s"(zero));
                     int part = comp;
                     asm volatile("" : "+v"(part));
-                    harmonics_q<0, kQuadLmax, kYStride>(dx, dy, dz, scale, lm, mk, part, &kHarmonic + zero, s_y + jj);
+                    harmonics_scaled<0, kQuadLmax, kYStride>(dx, dy, dz, scale, lm, mk, part, &kScaledHarmonic + zero,
+                                                             s_y + jj);
                 }
                 __syncthreads();
                 {
@@ -413,8 +453,12 @@ void k_soap_quad(
             prefetch_centre(centre + 1);
             __syncthreads();
             if (d.mode == 0) {
-                power_spectrum_row(s_c, s_loff, d, ps_pref, fbase, fstride, static_cast<char*>(out) + centre * pitch,
-                                   wave, T);
+                char* row = static_cast<char*>(out) + centre * pitch;
+                if (d.out_dtype == 4) {
+                    power_spectrum_row<4>(s_c, s_loff, d, ps_pref, fbase, fstride, row, wave, T);
+                } else {
+                    power_spectrum_row<8>(s_c, s_loff, d, ps_pref, fbase, fstride, row, wave, T);
+                }
             } else if (d.mode == 1) {
                 for (int i = tid; i < cw; i += kThreads) s_csum[i] += s_c[i];
             } else {
@@ -539,6 +583,7 @@ QuadPlanHost plan_quad_tables(int n, int l_max, int hpad, const std::vector<doub
             for (int g = 0; g < u.cnt; ++g) {
                 const int m = 4 * (u.g0 + g) + mcol;
                 q.ycol[g] = m <= 2 * u.l ? u.l * u.l + m : H;
+                // column l*l + m holds order |l - m| (cos parts first, then sin)
             }
             // fold: A operand = beta (row n' = lane % 4 of radial group grp,
             // k = lane / 16 of the block's own group, or of the partner's for
@@ -558,7 +603,7 @@ QuadPlanHost plan_quad_tables(int n, int l_max, int hpad, const std::vector<doub
 
 size_t quad_lds_bytes(const MfmaDims& d) {
     const size_t cw = static_cast<size_t>(d.crow) * static_cast<size_t>(d.hpad);
-    size_t words = static_cast<size_t>(d.H + 1) * kYStride + kNb + kQuadTab + cw;
+    size_t words = static_cast<size_t>(d.H + 1) * kYStride + kNb + kQuadTab + cw + d.hpad;
     if (d.mode == 1) words += cw;
     return words * sizeof(double) + static_cast<size_t>(d.L + 1 + 2 * (d.S + 1) + 1) * sizeof(int);
 }
