@@ -13,7 +13,7 @@ a ``cpu_baseline`` object (the reference's own C++ SOAP compiled in place,
 ``oracle/_ref``, timed on this host's cores on a bounded sample).
 
 ``roofline.traffic`` (HBM bytes per launch of that kernel) is read from the
-committed counter summary ``profiles/k_soap_mfma_<workload>_traffic.txt``
+committed counter summary ``profiles/<kernel>_<workload>_traffic.txt``
 when it exists for the benchmarked workload; it comes from two rocprofv3
 ``--pmc`` runs (FETCH_SIZE, WRITE_SIZE) of this script, each scaled by the
 same counter on a device copy of known size (``--calibrate-copy``).
