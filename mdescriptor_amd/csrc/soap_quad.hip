@@ -270,6 +270,13 @@ void k_soap_quad(
         }
     };
     if (item_first < item_last) prefetch_centre(item_begin ? item_begin[item_first] : item_first);
+    // lane pair jj = lane/2 holds the image position of slot jj of the next
+    // chunk (stale, finite values in pad slots), its row (-1: pad) and species;
+    // for a centre's first chunk these are loaded during the previous centre
+    // (first_ready) when there was one
+    double px = 0.0, py = 0.0, pz = 0.0;
+    int prow = -1, pq = 0;
+    bool first_ready = false;
     for (int64_t item = item_first; item < item_last; ++item) {
         const int64_t first = item_begin ? item_begin[item] : item;
         const int64_t last = item_begin ? item_begin[item + 1] : item + 1;
@@ -305,6 +312,8 @@ void k_soap_quad(
                     }
                 }
             }
+            // the following centre's metadata, in flight during this one
+            prefetch_centre(centre + 1);
             __syncthreads();
             // an empty species leaves its coefficients at zero
             for (int q = 0; q < S; ++q) {
@@ -320,11 +329,7 @@ void k_soap_quad(
                 const int off = p - s_pseg[q];
                 return off < s_seg[q + 1] - s_seg[q] ? s_seg[q] + off : -1;
             };
-            // lane pair jj = lane/2 holds the image position of slot jj of the
-            // next chunk (stale, finite values in pad slots)
-            double px = 0.0, py = 0.0, pz = 0.0;
-            int prow, pq;
-            {
+            if (!first_ready) {
                 prow = slot_row(lane / 2, pq);
                 if (prow >= 0) {
                     const uint32_t b = pair_bin[centre_pairs + prow];
@@ -450,7 +455,36 @@ void k_soap_quad(
                 __syncthreads();
             }
             if (slots > 0) fold(cur);
-            prefetch_centre(centre + 1);
+            // First chunk of the following centre: its slot rows from the
+            // prefetched species counts (the slot_row rule on register prefix
+            // sums), the row's bin now and the image position after the power
+            // spectrum, so that neither load waits at the next centre's start.
+            first_ready = centre + 1 < range_end;
+            uint32_t next_bin = 0;
+            if (first_ready) {
+                int rows = lane < S ? pre_count : 0;
+                int pad = (rows + 3) & ~3;
+                int rows_in = rows, pad_in = pad;
+#pragma unroll
+                for (int off = 1; off < kMaxSpecies; off *= 2) {
+                    const int r_up = __shfl_up(rows_in, off, kMaxSpecies);
+                    const int p_up = __shfl_up(pad_in, off, kMaxSpecies);
+                    if ((lane % kMaxSpecies) >= off) {
+                        rows_in += r_up;
+                        pad_in += p_up;
+                    }
+                }
+                const int p = lane / 2;
+                int q = 0;
+                for (int t = 1; t < S; ++t) q += p >= __builtin_amdgcn_readlane(pad_in, t - 1) ? 1 : 0;
+                const int seg_q = __shfl(rows_in - rows, q);
+                const int pseg_q = __shfl(pad_in - pad, q);
+                const int count_q = __shfl(rows, q);
+                const int off = p - pseg_q;
+                pq = q;
+                prow = off < count_q ? seg_q + off : -1;
+                if (prow >= 0) next_bin = pair_bin[lane_value(pre_bits, 3) + prow];
+            }
             __syncthreads();
             if (d.mode == 0) {
                 char* row = static_cast<char*>(out) + centre * pitch;
@@ -464,6 +498,11 @@ void k_soap_quad(
             } else {
                 power_spectrum_tiles(s_c, s_loff, d, ps_pref, centre == first ? 3 : 2, out, pitch, centre, part_row,
                                      wave, T);
+            }
+            if (first_ready && prow >= 0) {
+                px = bx[next_bin];
+                py = by[next_bin];
+                pz = bz[next_bin];
             }
             __syncthreads();
         }
