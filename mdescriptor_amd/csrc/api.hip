@@ -775,7 +775,7 @@ int mdx_hip_soap_run(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, mdx_device_bat
         DeviceScope scope(ctx->device);
         run_pipeline(ctx, *plan, batch->pb, batch->graph, batch->partials, out_device, out_pitch_bytes, cancel_flag,
                      timing);
-        MDX_HIP(hipStreamSynchronize(ctx->stream));
+        ctx->finished.wait(ctx->stream);
         fill_timing(ctx, timing, false);
     });
 }

@@ -66,6 +66,23 @@ int device_compute_units() {
     return cached[dev];
 }
 
+PinnedWords::~PinnedWords() {
+    if (words_ != nullptr) (void)hipHostFree(words_);
+}
+
+unsigned long long* PinnedWords::get(size_t count) {
+    if (count > count_) {
+        if (words_ != nullptr) MDX_HIP(hipHostFree(words_));
+        words_ = nullptr;
+        count_ = 0;
+        void* p = nullptr;
+        MDX_HIP(hipHostMalloc(&p, count * sizeof(unsigned long long), hipHostMallocDefault));
+        words_ = static_cast<unsigned long long*>(p);
+        count_ = count;
+    }
+    return words_;
+}
+
 StreamPoint::~StreamPoint() {
     if (event_ != nullptr) (void)hipEventDestroy(event_);
 }
@@ -976,8 +993,8 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
         // one pass: counts and rows at centre * cap
         gr.pair_bin.reserve(static_cast<size_t>(atoms * cap) * sizeof(uint32_t));
         neighbors(Slotted{}, cap);
-        unsigned long long st[kStatWords] = {};
-        MDX_HIP(hipMemcpyAsync(st, stats, sizeof(st), hipMemcpyDeviceToHost, stream));
+        unsigned long long* st = gr.stats_host.get(kStatWords);
+        MDX_HIP(hipMemcpyAsync(st, stats, kStatWords * sizeof(unsigned long long), hipMemcpyDeviceToHost, stream));
         // the expansion launch waits on these words: poll rather than sleep in
         // a blocking synchronisation, whose wake-up costs tens of microseconds
         gr.read_back.wait(stream);

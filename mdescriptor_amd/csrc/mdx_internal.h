@@ -100,6 +100,21 @@ struct PreparedBatch {
 // An event recorded on a stream and polled until the stream reaches it (a
 // lower-latency wait than a blocking stream synchronisation).  Created on
 // first use on the current device; one per owner, not copyable.
+// Page-locked host words for small device-to-host read-backs (a copy into
+// pageable memory goes through a staging buffer synchronously).
+class PinnedWords {
+public:
+    PinnedWords() = default;
+    PinnedWords(const PinnedWords&) = delete;
+    PinnedWords& operator=(const PinnedWords&) = delete;
+    ~PinnedWords();
+    unsigned long long* get(size_t count); // at least count words, allocated on first use
+
+private:
+    unsigned long long* words_ = nullptr;
+    size_t count_ = 0;
+};
+
 class StreamPoint {
 public:
     StreamPoint() = default;
@@ -141,6 +156,7 @@ struct DeviceGraph {
     int64_t slots = 0;       // layout of the last build: 0 compact, else rows reserved per centre
     int64_t slot_cap = 512;  // rows per centre for the next slotted build (0: compact only)
     StreamPoint read_back;   // completion of the statistics read-back
+    PinnedWords stats_host;  // its destination
     DeviceBuffer scan_tmp;   // block sums of the scans
 };
 
@@ -215,6 +231,7 @@ struct mdx_hip_ctx {
     hipEvent_t stage_events[2] = {};  // completion of the DMA into each staging half
     hipStream_t copy_stream = nullptr; // result downloads overlapped with the expansion launches
     std::vector<hipEvent_t> slice_events; // end of each expansion launch, waited on by copy_stream
+    mdx::StreamPoint finished;        // end of a device-batch run (polled)
 };
 
 struct mdx_soap_plan {
