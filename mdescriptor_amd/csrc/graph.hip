@@ -359,8 +359,8 @@ __global__ void k_centre_fill(const int64_t* centre_cell, const int32_t* centre_
 // bin index of every accepted image at pair_start[centre] onwards (wave
 // ballot + popcount compaction).  Slotted pass (kNbrSlotted, the SOAP
 // expansion's layout): both at once, each centre's rows at centre * cap
-// onwards (rows past cap are dropped and reported through stats: [0] the
-// total rows, [1] the largest row count of a centre).
+// onwards (rows past cap are dropped; stats[0] receives the total rows).
+// Both counting passes record the largest row count of a centre in stats[1].
 constexpr int kNbrThreads = 512;
 constexpr int kNbrWaves = kNbrThreads / kWave;
 constexpr int kStage = 1024;        // candidates staged in LDS per pass over a cell's centres
@@ -576,10 +576,10 @@ __global__ __launch_bounds__(kNbrThreads) void k_neighbors(
             if (kCount) {
                 for (int i = tid; i < nb; i += kNbrThreads) {
                     totals[s_centre[i]] = s_found[i];
+                    atomicMax(&stats[kStatMostRows], static_cast<unsigned long long>(s_found[i]));
                     if (kMode == kNbrSlotted) {
                         pair_start[s_centre[i]] = s_first[i];
                         atomicAdd(&stats[kStatRows], static_cast<unsigned long long>(s_found[i]));
-                        atomicMax(&stats[kStatMostRows], static_cast<unsigned long long>(s_found[i]));
                     }
                 }
                 for (int i = tid; i < nb * S; i += kNbrThreads) {
@@ -1003,6 +1003,7 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
         const int64_t pairs = static_cast<int64_t>(st[kStatRows]);
         const int64_t most = static_cast<int64_t>(st[kStatMostRows]);
         const int64_t binned = static_cast<int64_t>(st[kStatBinned]);
+        gr.most_rows = most;
         if (most <= cap) {
             gr.slots = cap;
             gr.pairs = pairs;
@@ -1031,6 +1032,7 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     MDX_HIP(hipMemcpyAsync(st, stats, sizeof(st), hipMemcpyDeviceToHost, stream));
     MDX_HIP(hipStreamSynchronize(stream));
     const int64_t binned = static_cast<int64_t>(st[kStatBinned]);
+    gr.most_rows = static_cast<int64_t>(st[kStatMostRows]);
     if (st[kStatError] != 0) throw Error(MDX_INTERNAL, "a centre fell outside its structure's cell grid");
     if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
     if (pairs >= (int64_t(1) << 40)) throw Error(MDX_INTERNAL, "implausible neighbour pair count");

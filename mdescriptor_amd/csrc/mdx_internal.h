@@ -133,6 +133,7 @@ private:
 struct DeviceGraph {
     int64_t binned = 0;
     int64_t pairs = 0;
+    int64_t most_rows = 0;   // largest row count of one centre
     int n_species = 1;
     DeviceBuffer counters;   // zero-filled per build: u64 statistics[kStatWords], then i32 cell
                              // counts of binning (count, fill) and of the centres, [cells + 1] each

@@ -412,6 +412,8 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
     const bool hook = on_slice != nullptr && *on_slice && p.average == 0;
     int64_t launches = 0;
     if (p.use_mfma) {
+        // the 4x4-block kernel where the plan chose it and every centre's rows fit its slot codes
+        const bool quad = p.quad_waves > 0 && g.most_rows < kQuadMaxRows;
         MfmaDims md{};
         md.S = p.S;
         md.n = p.n;
@@ -426,7 +428,7 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
         md.clamp = p.clamp;
         md.Sc = p.Sc;
         md.compression = p.compression;
-        md.crow = p.quad_waves > 0 ? quad_coefficient_rows(p.Sc, p.n) : mfma_coefficient_rows(p.Sc, p.n, p.compression);
+        md.crow = quad ? quad_coefficient_rows(p.Sc, p.n) : mfma_coefficient_rows(p.Sc, p.n, p.compression);
         md.radial = p.radial_basis;
         md.grid = p.grid_size;
         md.weighted = p.weighted;
@@ -459,7 +461,7 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
         for (int64_t base = 0; base < items; base += slice) {
             if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
             const int64_t count = std::min(slice, items - base);
-            if (p.quad_waves > 0) {
+            if (quad) {
                 launch_quad_expand(stream, p.quad_waves, p.quad_kg, p.quad_instr, pb, g, p.d_quad_lanes.as<QuadLane>(),
                                    tab.ps_pref, tab.fbase, tab.fstride, md, d_item_begin, base, count, out_device,
                                    pitch_bytes, d_partial);
@@ -477,7 +479,7 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
         if (events != nullptr) MDX_HIP(hipEventRecord(events[4], stream));
         if (timing != nullptr) {
             timing->expansion_launches = launches;
-            timing->expansion_tiles = p.quad_waves > 0 ? -p.quad_waves : tt;
+            timing->expansion_tiles = quad ? -p.quad_waves : tt;
         }
         return;
     }

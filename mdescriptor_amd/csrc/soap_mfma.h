@@ -80,6 +80,8 @@ constexpr int kQuadG = 4;
 constexpr double kQuadMinArgument = -5.0e6;
 constexpr int kQuadLmax = 10;
 constexpr int kQuadMaxWaves = 8;
+// rows of one centre the kernel's slot codes hold (row * 16 + species in 32 bits)
+constexpr int64_t kQuadMaxRows = int64_t(1) << 27;
 
 // Constants of one lane of one wavefront of the 4x4-block kernel.
 //   expo     radial exponent a_lk of the lane's A-operand row (k = 4 group +

@@ -213,9 +213,7 @@ void k_soap_quad(
     double* s_scale = s_c + cw;     // hp: S_lm of each padded column (scaled harmonics)
     double* s_csum = s_scale + hp;  // cw (inner average only)
     int* s_loff = reinterpret_cast<int*>(s_csum + (d.mode == 1 ? cw : 0)); // L + 1
-    int* s_seg = s_loff + (L + 1);  // S + 1
-    int* s_pseg = s_seg + (S + 1);  // S + 1
-    int* s_step = s_pseg + (S + 1); // 1
+    int* s_step = s_loff + (L + 1); // 1
 
     for (int i = tid; i < kQuadTab; i += kThreads) s_tab[i] = exp2(static_cast<double>(i) / kQuadTab);
     for (int i = tid; i < (H + 1) * kYStride; i += kThreads) s_y[i] = 0.0;
@@ -255,13 +253,13 @@ void k_soap_quad(
     const int64_t item_first = item_base + static_cast<int64_t>(blockIdx.x) * per_block;
     const int64_t item_last = min(item_first + per_block, item_base + items);
     const int64_t range_end = item_first >= item_last ? 0 : item_begin ? item_begin[item_last] : item_last;
-    // next centre's species counts (lanes < S), position bits (lanes 0-2) and
-    // first row (lane 3), loaded one centre ahead
+    // next centre's species row counts (lanes t, 16 + t and 32 + t for t < S),
+    // position bits (lanes 0-2) and first pair row (lane 3), loaded one centre ahead
     int pre_count = 0;
     int64_t pre_bits = 0;
     auto prefetch_centre = [&](int64_t c) {
         if (c < range_end) {
-            if (lane < S) pre_count = counts[c * S + lane];
+            if (lane % kMaxSpecies < S && lane < 3 * kMaxSpecies) pre_count = counts[c * S + lane % kMaxSpecies];
             if (lane < 3) {
                 pre_bits = __double_as_longlong(positions[c * 3 + lane]);
             } else if (lane == 3) {
@@ -270,12 +268,63 @@ void k_soap_quad(
         }
     };
     if (item_first < item_last) prefetch_centre(item_begin ? item_begin[item_first] : item_first);
-    // lane pair jj = lane/2 holds the image position of slot jj of the next
-    // chunk (stale, finite values in pad slots), its row (-1: pad) and species;
-    // for a centre's first chunk these are loaded during the previous centre
-    // (first_ready) when there was one
+    // Slot table of a centre, from pre_count.  Each species' rows fill a
+    // segment of slots padded to a multiple of 4 (a step never mixes
+    // species).  Lane t < S holds the first slot of species t, lane 16 + t the
+    // shift from its slots to its rows, lane 32 + t the end of its rows in
+    // slots; slots is the padded total and empty the bit mask of the species
+    // without rows.
+    int table = 0, slots = 0;
+    uint32_t empty = 0;
+    auto slot_table = [&]() {
+        const int seg = lane / kMaxSpecies;
+        int rows = seg < 3 && lane % kMaxSpecies < S ? pre_count : 0;
+        const int pad = (rows + 3) & ~3;
+        int rows_in = rows, pad_in = pad;
+#pragma unroll
+        for (int off = 1; off < kMaxSpecies; off *= 2) {
+            const int r_up = __shfl_up(rows_in, off, kMaxSpecies);
+            const int p_up = __shfl_up(pad_in, off, kMaxSpecies);
+            if ((lane % kMaxSpecies) >= off) {
+                rows_in += r_up;
+                pad_in += p_up;
+            }
+        }
+        const int start = pad_in - pad;
+        table = seg == 0 ? start : seg == 1 ? start - (rows_in - rows) : start + rows;
+        slots = __builtin_amdgcn_readlane(pad_in, S - 1);
+        empty = static_cast<uint32_t>(__ballot(lane < S && rows == 0));
+    };
+    // Row of slot base + lane / 2 times 16 plus its species, or -1 for a pad
+    // slot (base: the first slot of a chunk, the same in every lane).  The
+    // species of slot base comes from a scan of the segment starts; only
+    // segments that start inside the chunk are compared lane by lane.
+    auto slot_code = [&](int base) -> int {
+        int q0 = 0;
+        while (q0 + 1 < S && __builtin_amdgcn_readlane(table, q0 + 1) <= base) ++q0;
+        const int p = base + lane / 2;
+        int q = q0;
+        int shift = __builtin_amdgcn_readlane(table, kMaxSpecies + q0);
+        int end = __builtin_amdgcn_readlane(table, 2 * kMaxSpecies + q0);
+        for (int t = q0 + 1; t < S; ++t) {
+            const int first_slot = __builtin_amdgcn_readlane(table, t);
+            if (first_slot >= base + kNb) break;
+            if (p >= first_slot) {
+                q = t;
+                shift = __builtin_amdgcn_readlane(table, kMaxSpecies + t);
+                end = __builtin_amdgcn_readlane(table, 2 * kMaxSpecies + t);
+            }
+        }
+        return p < end ? ((p - shift) << 4) | q : -1;
+    };
+    // lane pair jj = lane/2 holds slot jj of the current chunk: its image
+    // position (stale, finite values in pad slots) and code (slot_code); of
+    // the next chunk, the code and the bin of the row.  For a centre's first
+    // two chunks these are loaded during the previous centre (first_ready)
+    // when there was one.
     double px = 0.0, py = 0.0, pz = 0.0;
-    int prow = -1, pq = 0;
+    int pcode = -1, ncode = -1;
+    uint32_t nbin = 0;
     bool first_ready = false;
     for (int64_t item = item_first; item < item_last; ++item) {
         const int64_t first = item_begin ? item_begin[item] : item;
@@ -289,58 +338,29 @@ void k_soap_quad(
             const double cy = __longlong_as_double(lane_value(pre_bits, 1));
             const double cz = __longlong_as_double(lane_value(pre_bits, 2));
             const int64_t centre_pairs = lane_value(pre_bits, 3);
-            // species segments of the centre's rows and their slots (each
-            // segment padded to a multiple of 4): exclusive sums over lanes < S
-            {
-                int rows = lane < S ? pre_count : 0;
-                int pad = (rows + 3) & ~3;
-#pragma unroll
-                for (int off = 1; off < kMaxSpecies; off *= 2) {
-                    const int r_up = __shfl_up(rows, off, kMaxSpecies);
-                    const int p_up = __shfl_up(pad, off, kMaxSpecies);
-                    if ((lane % kMaxSpecies) >= off) {
-                        rows += r_up;
-                        pad += p_up;
-                    }
-                }
-                if (wave == 0 && lane < S) {
-                    s_seg[lane + 1] = rows;
-                    s_pseg[lane + 1] = pad;
-                    if (lane == 0) {
-                        s_seg[0] = 0;
-                        s_pseg[0] = 0;
-                    }
-                }
-            }
-            // the following centre's metadata, in flight during this one
-            prefetch_centre(centre + 1);
-            __syncthreads();
-            // an empty species leaves its coefficients at zero
-            for (int q = 0; q < S; ++q) {
-                if (s_seg[q + 1] == s_seg[q]) {
-                    double* cdst_q = s_c + q * n * hp;
-                    for (int i = tid; i < n * hp; i += kThreads) cdst_q[i] = 0.0;
-                }
-            }
-            const int slots = s_pseg[S];
-            auto slot_row = [&](int p, int& q) -> int {
-                q = 0;
-                for (int t = 1; t < S; ++t) q += p >= s_pseg[t] ? 1 : 0;
-                const int off = p - s_pseg[q];
-                return off < s_seg[q + 1] - s_seg[q] ? s_seg[q] + off : -1;
-            };
             if (!first_ready) {
-                prow = slot_row(lane / 2, pq);
-                if (prow >= 0) {
-                    const uint32_t b = pair_bin[centre_pairs + prow];
+                slot_table();
+                pcode = slot_code(0);
+                if (pcode >= 0) {
+                    const uint32_t b = pair_bin[centre_pairs + (pcode >> 4)];
                     px = bx[b];
                     py = by[b];
                     pz = bz[b];
                 }
+                ncode = slot_code(kNb);
+                if (ncode >= 0) nbin = pair_bin[centre_pairs + (ncode >> 4)];
+            }
+            // the following centre's metadata, in flight during this one
+            prefetch_centre(centre + 1);
+            // an empty species leaves its coefficients at zero (the previous
+            // centre's readers of s_c finished at its last barrier)
+            for (uint32_t m = empty; m != 0; m &= m - 1) {
+                double* cdst_q = s_c + __builtin_ctz(m) * n * hp;
+                for (int i = tid; i < n * hp; i += kThreads) cdst_q[i] = 0.0;
             }
             // species of the first rows (the accumulators start there)
-            int cur = 0;
-            while (cur < S - 1 && s_seg[cur + 1] == 0) ++cur;
+            const uint32_t filled = ~empty & ((2u << (S - 1)) - 1u);
+            int cur = filled != 0 ? __builtin_ctz(filled) : 0;
             double acc[G];
 #pragma unroll
             for (int g = 0; g < G; ++g) acc[g] = 0.0;
@@ -422,11 +442,12 @@ void k_soap_quad(
                     const double dy = py - cy;
                     const double dz = pz - cz;
                     const double d2 = dx * dx + dy * dy + dz * dz;
-                    const double scale = prow >= 0 ? 1.0 : 0.0;
+                    const double scale = pcode >= 0 ? 1.0 : 0.0;
                     if (wave == 0) {
                         if (comp == 0) s_d2[jj] = d2;
                         // species of the 8 steps, 4 bits each, from lanes 0, 8, .., 56
-                        uint32_t bits = lane % 8 == 0 ? static_cast<uint32_t>(pq) << (4 * (lane / 8)) : 0u;
+                        // (the first slot of a step is never a pad slot)
+                        uint32_t bits = lane % 8 == 0 ? static_cast<uint32_t>(pcode & 15) << (4 * (lane / 8)) : 0u;
                         bits |= __shfl_xor(bits, 8);
                         bits |= __shfl_xor(bits, 16);
                         bits |= __shfl_xor(bits, 32);
@@ -442,48 +463,34 @@ void k_soap_quad(
                 }
                 __syncthreads();
                 {
-                    // loads of the next chunk
-                    prow = slot_row(j0 + kNb + lane / 2, pq);
-                    if (prow >= 0) {
-                        const uint32_t b = pair_bin[centre_pairs + prow];
-                        px = bx[b];
-                        py = by[b];
-                        pz = bz[b];
+                    // the next chunk's positions (its bin was loaded one chunk
+                    // ago), then the bin of the chunk after it
+                    pcode = ncode;
+                    if (pcode >= 0) {
+                        px = bx[nbin];
+                        py = by[nbin];
+                        pz = bz[nbin];
                     }
+                    ncode = slot_code(j0 + 2 * kNb);
+                    if (ncode >= 0) nbin = pair_bin[centre_pairs + (ncode >> 4)];
                 }
                 contract(j0);
                 __syncthreads();
             }
             if (slots > 0) fold(cur);
-            // First chunk of the following centre: its slot rows from the
-            // prefetched species counts (the slot_row rule on register prefix
-            // sums), the row's bin now and the image position after the power
-            // spectrum, so that neither load waits at the next centre's start.
+            // First two chunks of the following centre: its slot table from the
+            // prefetched species counts, the bins of both chunks now and the
+            // image positions of the first after the power spectrum, so that
+            // no load waits at the next centre's start.
             first_ready = centre + 1 < range_end;
             uint32_t next_bin = 0;
             if (first_ready) {
-                int rows = lane < S ? pre_count : 0;
-                int pad = (rows + 3) & ~3;
-                int rows_in = rows, pad_in = pad;
-#pragma unroll
-                for (int off = 1; off < kMaxSpecies; off *= 2) {
-                    const int r_up = __shfl_up(rows_in, off, kMaxSpecies);
-                    const int p_up = __shfl_up(pad_in, off, kMaxSpecies);
-                    if ((lane % kMaxSpecies) >= off) {
-                        rows_in += r_up;
-                        pad_in += p_up;
-                    }
-                }
-                const int p = lane / 2;
-                int q = 0;
-                for (int t = 1; t < S; ++t) q += p >= __builtin_amdgcn_readlane(pad_in, t - 1) ? 1 : 0;
-                const int seg_q = __shfl(rows_in - rows, q);
-                const int pseg_q = __shfl(pad_in - pad, q);
-                const int count_q = __shfl(rows, q);
-                const int off = p - pseg_q;
-                pq = q;
-                prow = off < count_q ? seg_q + off : -1;
-                if (prow >= 0) next_bin = pair_bin[lane_value(pre_bits, 3) + prow];
+                const int64_t next_pairs = lane_value(pre_bits, 3);
+                slot_table();
+                pcode = slot_code(0);
+                if (pcode >= 0) next_bin = pair_bin[next_pairs + (pcode >> 4)];
+                ncode = slot_code(kNb);
+                if (ncode >= 0) nbin = pair_bin[next_pairs + (ncode >> 4)];
             }
             __syncthreads();
             if (d.mode == 0) {
@@ -499,7 +506,7 @@ void k_soap_quad(
                 power_spectrum_tiles(s_c, s_loff, d, ps_pref, centre == first ? 3 : 2, out, pitch, centre, part_row,
                                      wave, T);
             }
-            if (first_ready && prow >= 0) {
+            if (first_ready && pcode >= 0) {
                 px = bx[next_bin];
                 py = by[next_bin];
                 pz = bz[next_bin];
@@ -644,7 +651,7 @@ size_t quad_lds_bytes(const MfmaDims& d) {
     const size_t cw = static_cast<size_t>(d.crow) * static_cast<size_t>(d.hpad);
     size_t words = static_cast<size_t>(d.H + 1) * kYStride + kNb + kQuadTab + cw + d.hpad;
     if (d.mode == 1) words += cw;
-    return words * sizeof(double) + static_cast<size_t>(d.L + 1 + 2 * (d.S + 1) + 1) * sizeof(int);
+    return words * sizeof(double) + static_cast<size_t>(d.L + 1 + 1) * sizeof(int);
 }
 
 void launch_quad_expand(hipStream_t stream, int waves, int kg, int instr, const PreparedBatch& pb, const DeviceGraph& g,
