@@ -177,7 +177,7 @@ __device__ inline int feature_index(int i, int j, int S, int n, float inv_n, int
 // summed density of soap.cpp:955-967).  All threads of the workgroup; the
 // caller synchronises before the power spectrum reads them.
 __device__ void species_sums(double* s_c, const MfmaDims& d, int tid, int threads) {
-    const int n = d.n, hp = d.hpad, W = d.Sc * n;
+    const int n = d.n, hp = d.cpitch, W = d.Sc * n;
     for (int i = tid; i < n * hp; i += threads) {
         const int n2 = i / hp, e = i - n2 * hp;
         double sum = 0.0;
@@ -187,8 +187,8 @@ __device__ void species_sums(double* s_c, const MfmaDims& d, int tid, int thread
 }
 
 // Power spectrum of the coefficients in LDS on 16x16 Gram tiles.  s_c holds
-// W + 1 rows of d.hpad values (row W and every pad entry are zero), entry
-// (row, l, m') at row*hpad + loff[l] + m'.  The units (tile pair, l), pair-
+// W + 1 rows of d.hpad values at a pitch of d.cpitch (row W and every pad
+// entry are zero), entry (row, l, m') at row*cpitch + loff[l] + m'.  The units (tile pair, l), pair-
 // major, are split into contiguous ranges over the `waves` wavefronts of the
 // workgroup (wavefront `wave` takes its range); units write disjoint
 // features, and a given feature always comes from the same wavefront.
@@ -212,7 +212,7 @@ __device__ void power_spectrum_walk(const double* s_c, const int* loff, const Mf
     const bool rect = kPaired && d.compression == 2; // A = channels, B = summed rows
     const int RB = rect ? (d.n + 15) / 16 : RT;
     const int L = d.L;
-    const int hp = d.hpad;
+    const int hp = d.cpitch;
     const int n = d.n;
     const float inv_n = 1.0f / static_cast<float>(n);
     const int units = (rect ? RT * RB : RT * (RT + 1) / 2) * L;

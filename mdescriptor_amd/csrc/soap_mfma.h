@@ -12,6 +12,7 @@ struct MfmaDims {
     int mode;      // 0 off, 1 inner, 2 outer
     int out_dtype; // 4 or 8
     int hpad;      // padded harmonic row: each l block rounded up to a multiple of 4
+    int cpitch;    // LDS row pitch of the coefficients (hpad, or quad_coefficient_pitch)
     int clamp;     // 1 when some radial exponent argument can fall below -700
     int64_t F;
     // harmonic m-columns computed by each wavefront of a workgroup (bit m of
@@ -91,7 +92,8 @@ constexpr int64_t kQuadMaxRows = int64_t(1) << 27;
 //            k = 4 group + lane / 16
 //   beta_s   the same for the partner block's accumulator (k of the other
 //            radial group; KG = 2 only)
-//   ycol[g]  harmonic read by the lane for instruction g (H: the zero entry)
+//   ycol[g]  harmonic read by the lane for instruction g (0 where the result
+//            is not stored or is scaled by 0)
 //   cdst     LDS offset (within a species block of c) of the lane's fold
 //            output for g = 0, + 4 g for instruction g; -1: not stored
 //   cnt      instructions in which the lane's block is active
@@ -104,6 +106,9 @@ struct QuadLane {
 // LDS coefficient rows of the 4x4-block kernel: S*n channels, plus a zero row
 // for the Gram tiles' pad channels unless S*n is a multiple of 16
 inline int quad_coefficient_rows(int S, int n) { return S * n + ((S * n) % 16 != 0 ? 1 : 0); }
+// LDS row pitch of the 4x4-block kernel's coefficients: odd, so that the 16
+// rows of a Gram-tile operand read fall in 16 different LDS banks
+inline int quad_coefficient_pitch(int hpad) { return hpad + 1; }
 
 struct QuadPlanHost {
     int waves = 0;               // 0: the shape is outside the kernel's limits

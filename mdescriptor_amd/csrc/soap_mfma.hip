@@ -648,6 +648,7 @@ void launch_mfma_expand(hipStream_t stream, int template_tiles, const PreparedBa
     // split the harmonic m-columns over the workgroup's wavefronts, longest
     // recurrence (l_max - m + 1 values) first onto the least-loaded one
     MfmaDims dm = d;
+    dm.cpitch = d.hpad;
     {
         int load[16] = {};
         for (int w = 0; w < 16; ++w) dm.harm_mask[w] = 0;
@@ -687,10 +688,13 @@ void launch_mfma_finalize(hipStream_t stream, const PreparedBatch& pb, const Mfm
                           const double* partial, const int64_t* struct_items, void* out, int64_t pitch) {
     const unsigned grid = static_cast<unsigned>(std::min<int64_t>(pb.structures, 1 << 20));
     if (d.mode == 1) {
+        // the partial rows are mean coefficients at a pitch of hpad
+        MfmaDims dm = d;
+        dm.cpitch = d.hpad;
         const size_t lds = static_cast<size_t>(d.crow) * d.hpad * sizeof(double)
             + static_cast<size_t>(d.L + 2) * sizeof(int);
         hipLaunchKernelGGL(k_mfma_finalize_inner, dim3(grid), dim3(kWaveThreads), lds, stream, partial, struct_items,
-                           pb.d_offsets.as<int64_t>(), pb.structures, tab, d, out, pitch);
+                           pb.d_offsets.as<int64_t>(), pb.structures, tab, dm, out, pitch);
     } else {
         hipLaunchKernelGGL(k_mfma_finalize_outer, dim3(grid), dim3(256), 0, stream, partial, struct_items,
                            pb.d_offsets.as<int64_t>(), pb.structures, d, out, pitch);

@@ -111,7 +111,7 @@ __device__ void power_spectrum_row(const double* s_c, const int* loff, const Mfm
     const int zero_row = d.crow - 1;
     const int RT = (W + 15) / 16;
     const int L = d.L;
-    const int hp = d.hpad;
+    const int hp = d.cpitch;
     const int units = RT * (RT + 1) / 2 * L;
     const int u_begin = wave * units / waves;
     const int u_end = (wave + 1) * units / waves;
@@ -205,9 +205,10 @@ void k_soap_quad(
     const int T = kThreads / kWaveThreads;
     const int H = d.H, L = d.L, S = d.S, n = d.n;
     const int hp = d.hpad;          // padded c row
-    const int cw = d.crow * hp;     // c words (a zero row last unless S*n is a multiple of 16)
-    double* s_y = lds;              // (H + 1) * kYStride, harmonic-major; row H stays zero
-    double* s_d2 = s_y + (H + 1) * kYStride; // kNb
+    const int cp = d.cpitch;        // its LDS pitch (odd)
+    const int cw = d.crow * cp;     // c words (a zero row last unless S*n is a multiple of 16)
+    double* s_y = lds;              // H * kYStride, harmonic-major
+    double* s_d2 = s_y + H * kYStride; // kNb
     double* s_tab = s_d2 + kNb;     // kQuadTab
     double* s_c = s_tab + kQuadTab; // cw
     double* s_scale = s_c + cw;     // hp: S_lm of each padded column (scaled harmonics)
@@ -216,7 +217,6 @@ void k_soap_quad(
     int* s_step = s_loff + (L + 1); // 1
 
     for (int i = tid; i < kQuadTab; i += kThreads) s_tab[i] = exp2(static_cast<double>(i) / kQuadTab);
-    for (int i = tid; i < (H + 1) * kYStride; i += kThreads) s_y[i] = 0.0;
     for (int i = tid; i < cw; i += kThreads) s_c[i] = 0.0;
     for (int i = tid; i < hp; i += kThreads) {
         // column i of the padded row: degree l block at loff[l], 4 ceil((2l+1)/4) wide
@@ -329,7 +329,8 @@ void k_soap_quad(
     for (int64_t item = item_first; item < item_last; ++item) {
         const int64_t first = item_begin ? item_begin[item] : item;
         const int64_t last = item_begin ? item_begin[item + 1] : item + 1;
-        double* part_row = partial != nullptr ? partial + item * (d.mode == 1 ? static_cast<int64_t>(cw) : d.F) : nullptr;
+        double* part_row =
+            partial != nullptr ? partial + item * (d.mode == 1 ? static_cast<int64_t>(d.crow) * hp : d.F) : nullptr;
         if (d.mode == 1) {
             for (int i = tid; i < cw; i += kThreads) s_csum[i] = 0.0;
         }
@@ -355,8 +356,8 @@ void k_soap_quad(
             // an empty species leaves its coefficients at zero (the previous
             // centre's readers of s_c finished at its last barrier)
             for (uint32_t m = empty; m != 0; m &= m - 1) {
-                double* cdst_q = s_c + __builtin_ctz(m) * n * hp;
-                for (int i = tid; i < n * hp; i += kThreads) cdst_q[i] = 0.0;
+                double* cdst_q = s_c + __builtin_ctz(m) * n * cp;
+                for (int i = tid; i < n * cp; i += kThreads) cdst_q[i] = 0.0;
             }
             // species of the first rows (the accumulators start there)
             const uint32_t filled = ~empty & ((2u << (S - 1)) - 1u);
@@ -369,11 +370,11 @@ void k_soap_quad(
             // half-mirror exchange (KG = 2); instructions past a block's own
             // count summed zeros and are not stored
             auto fold = [&](int q) {
-                double* cdst_q = s_c + q * n * hp + cdst;
+                double* cdst_q = s_c + q * n * cp + cdst;
                 // the harmonics were staged in the scaled form: each output
-                // column takes its S_lm (cdst is the column plus n' * hp)
+                // column takes its S_lm (cdst is the column plus n' * cp)
                 const int nrow = (KG == 2 ? 4 * ((lane / 4) % 2) : 0) + lane / 16;
-                const double* scale_col = s_scale + (cdst - nrow * hp);
+                const double* scale_col = s_scale + (cdst - nrow * cp);
 #pragma unroll
                 for (int g = 0; g < G; ++g) {
                     double c = mfma4(beta_r, acc[g], 0.0);
@@ -514,7 +515,8 @@ void k_soap_quad(
             __syncthreads();
         }
         if (d.mode == 1) {
-            for (int i = tid; i < cw; i += kThreads) part_row[i] = s_csum[i];
+            // partial rows at a pitch of hp (row r of s_csum starts at r * (hp + 1))
+            for (int i = tid; i < d.crow * hp; i += kThreads) part_row[i] = s_csum[i + i / hp];
         }
         __syncthreads();
     }
@@ -600,7 +602,6 @@ QuadPlanHost plan_quad_tables(int n, int l_max, int hpad, const std::vector<doub
     out.lanes.assign(static_cast<size_t>(T) * 64, QuadLane{});
     std::vector<int> loff(static_cast<size_t>(L) + 1, 0);
     for (int l = 0; l < L; ++l) loff[static_cast<size_t>(l) + 1] = loff[static_cast<size_t>(l)] + 4 * ((2 * l + 4) / 4);
-    const int H = L * L;
     auto beta = [&](int l, int np, int k) -> double {
         if (np >= n || k >= n) return 0.0;
         return beta_scaled[static_cast<size_t>((l * n + np) * n + k)] * pref[static_cast<size_t>(l * n + k)];
@@ -613,7 +614,10 @@ QuadPlanHost plan_quad_tables(int n, int l_max, int hpad, const std::vector<doub
             QuadLane& q = out.lanes[static_cast<size_t>(w) * 64 + static_cast<size_t>(lane)];
             const int b = (lane / 4) % 4;
             const int slot = b / KG; // unit slot of this block
-            for (int g = 0; g < kQuadG; ++g) q.ycol[g] = H;
+            // pad columns, idle blocks and instructions past a unit read
+            // harmonic 0 (finite): the fold stores nothing for the latter two
+            // and scales pad columns by an S_lm of 0
+            for (int g = 0; g < kQuadG; ++g) q.ycol[g] = 0;
             q.cdst = -1;
             q.cnt = 0;
             if (slot >= static_cast<int>(reg.size())) continue; // idle block
@@ -628,7 +632,7 @@ QuadPlanHost plan_quad_tables(int n, int l_max, int hpad, const std::vector<doub
             const int mcol = reversed ? 3 - col : col;
             for (int g = 0; g < u.cnt; ++g) {
                 const int m = 4 * (u.g0 + g) + mcol;
-                q.ycol[g] = m <= 2 * u.l ? u.l * u.l + m : H;
+                q.ycol[g] = m <= 2 * u.l ? u.l * u.l + m : 0;
                 // column l*l + m holds order |l - m| (cos parts first, then sin)
             }
             // fold: A operand = beta (row n' = lane % 4 of radial group grp,
@@ -639,7 +643,7 @@ QuadPlanHost plan_quad_tables(int n, int l_max, int hpad, const std::vector<doub
             q.beta_s = KG == 2 ? beta(u.l, np_a, 4 * (1 - grp) + lane / 16) : 0.0;
             const int np_out = 4 * grp + lane / 16;
             if (np_out < n) {
-                q.cdst = np_out * hpad + loff[static_cast<size_t>(u.l)] + 4 * u.g0 + mcol;
+                q.cdst = np_out * quad_coefficient_pitch(hpad) + loff[static_cast<size_t>(u.l)] + 4 * u.g0 + mcol;
                 q.cnt = u.cnt;
             }
         }
@@ -648,8 +652,8 @@ QuadPlanHost plan_quad_tables(int n, int l_max, int hpad, const std::vector<doub
 }
 
 size_t quad_lds_bytes(const MfmaDims& d) {
-    const size_t cw = static_cast<size_t>(d.crow) * static_cast<size_t>(d.hpad);
-    size_t words = static_cast<size_t>(d.H + 1) * kYStride + kNb + kQuadTab + cw + d.hpad;
+    const size_t cw = static_cast<size_t>(d.crow) * static_cast<size_t>(quad_coefficient_pitch(d.hpad));
+    size_t words = static_cast<size_t>(d.H) * kYStride + kNb + kQuadTab + cw + d.hpad;
     if (d.mode == 1) words += cw;
     return words * sizeof(double) + static_cast<size_t>(d.L + 1 + 1) * sizeof(int);
 }
@@ -661,6 +665,7 @@ void launch_quad_expand(hipStream_t stream, int waves, int kg, int instr, const 
     if (count <= 0) return;
     const size_t lds = quad_lds_bytes(d);
     MfmaDims dm = d;
+    dm.cpitch = quad_coefficient_pitch(d.hpad);
     {
         // harmonic m-columns over the wavefronts, longest recurrence first
         int load[16] = {};
