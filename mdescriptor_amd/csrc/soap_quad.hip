@@ -31,6 +31,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 namespace mdx {
 namespace {
@@ -214,7 +215,6 @@ void k_soap_quad(
     double* s_scale = s_c + cw;     // hp: S_lm of each padded column (scaled harmonics)
     double* s_csum = s_scale + hp;  // cw (inner average only)
     int* s_loff = reinterpret_cast<int*>(s_csum + (d.mode == 1 ? cw : 0)); // L + 1
-    int* s_step = s_loff + (L + 1); // 1
 
     for (int i = tid; i < kQuadTab; i += kThreads) s_tab[i] = exp2(static_cast<double>(i) / kQuadTab);
     for (int i = tid; i < cw; i += kThreads) s_c[i] = 0.0;
@@ -247,6 +247,12 @@ void k_soap_quad(
     for (int g = 0; g < G; ++g) yrow[g] = s_y + ql.ycol[g] * kYStride + lane / 16;
     const int cdst = ql.cdst;
     const int ccount = ql.cnt;
+    // MFMA instructions per step of this wavefront: its largest unit (the
+    // plan pads every wavefront to G; the common path runs only these)
+    int wave_instr = ccount;
+#pragma unroll
+    for (int off = 1; off < kWaveThreads; off *= 2) wave_instr = max(wave_instr, __shfl_xor(wave_instr, off));
+    wave_instr = __builtin_amdgcn_readfirstlane(wave_instr);
     const uint32_t hmask = d.harm_mask[wave];
     const int krow = lane / 16; // neighbour of the step this lane feeds (K index)
 
@@ -377,6 +383,7 @@ void k_soap_quad(
                 const double* scale_col = s_scale + (cdst - nrow * cp);
 #pragma unroll
                 for (int g = 0; g < G; ++g) {
+                    if (g >= wave_instr) break;
                     double c = mfma4(beta_r, acc[g], 0.0);
                     if (KG == 2) c = mfma4(beta_s, half_mirror(acc[g]), c);
                     if (cdst >= 0 && g < ccount) cdst_q[4 * g] = c * scale_col[4 * g];
@@ -392,23 +399,42 @@ void k_soap_quad(
                     for (int g = 0; g < G; ++g) yv[s][g] = yrow[g][4 * (h + s)];
                 }
             };
+            // the 8 steps of a chunk on the wavefront's own instruction count GW
+            auto steps_of_chunk = [&](auto gw) {
+                constexpr int GW = decltype(gw)::value;
+#pragma unroll
+                for (int h = 0; h < kNb / 4; h += 2) {
+                    double ev[2], yv[2][GW];
+#pragma unroll
+                    for (int s = 0; s < 2; ++s) {
+                        ev[s] = exp_neg64(-expo * s_d2[4 * (h + s) + krow], s_tab);
+#pragma unroll
+                        for (int g = 0; g < GW; ++g) yv[s][g] = yrow[g][4 * (h + s)];
+                    }
+#pragma unroll
+                    for (int s = 0; s < 2; ++s) {
+#pragma unroll
+                        for (int g = 0; g < GW; ++g) acc[g] = mfma4(ev[s], yv[s][g], acc[g]);
+                    }
+                }
+            };
+            uint32_t chunk_species = 0; // species of the current chunk's steps, 4 bits each
             // A chunk whose 8 steps all continue the current species (the common
             // case: one species' rows span several chunks) runs without per-step
             // checks; any other chunk checks each step for the end of the rows
             // and for a change of species.
             auto contract = [&](int j0) {
-                const uint32_t species = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(s_step[0]));
+                const uint32_t species = chunk_species;
                 const int nst = min(kNb / 4, (slots - j0) / 4);
                 if (nst == kNb / 4 && species == static_cast<uint32_t>(cur) * 0x11111111u) {
-#pragma unroll
-                    for (int h = 0; h < kNb / 4; h += 2) {
-                        double ev[2], yv[2][G];
-                        operands(h, ev, yv);
-#pragma unroll
-                        for (int s = 0; s < 2; ++s) {
-#pragma unroll
-                            for (int g = 0; g < G; ++g) acc[g] = mfma4(ev[s], yv[s][g], acc[g]);
-                        }
+                    if (G >= 4 && wave_instr >= 4) {
+                        steps_of_chunk(std::integral_constant<int, (G >= 4 ? 4 : G)>{});
+                    } else if (G >= 3 && wave_instr == 3) {
+                        steps_of_chunk(std::integral_constant<int, (G >= 3 ? 3 : G)>{});
+                    } else if (G >= 2 && wave_instr == 2) {
+                        steps_of_chunk(std::integral_constant<int, (G >= 2 ? 2 : G)>{});
+                    } else {
+                        steps_of_chunk(std::integral_constant<int, 1>{});
                     }
                     return;
                 }
@@ -436,7 +462,11 @@ void k_soap_quad(
             for (int j0 = 0; j0 < slots; j0 += kNb) {
                 {
                     // harmonics: two lanes per slot (cos / sin parts), this
-                    // wavefront's m-columns; pad slots get all-zero harmonics
+                    // wavefront's m-columns; pad slots get all-zero harmonics.
+                    // Every wavefront of the workgroup waits for the slowest
+                    // at the next barrier: this phase issues ahead of other
+                    // workgroups' contraction steps on the same SIMD.
+                    __builtin_amdgcn_s_setprio(2);
                     const int jj = lane / 2;
                     const int comp = lane % 2;
                     const double dx = px - cx;
@@ -444,15 +474,14 @@ void k_soap_quad(
                     const double dz = pz - cz;
                     const double d2 = dx * dx + dy * dy + dz * dz;
                     const double scale = pcode >= 0 ? 1.0 : 0.0;
-                    if (wave == 0) {
-                        if (comp == 0) s_d2[jj] = d2;
-                        // species of the 8 steps, 4 bits each, from lanes 0, 8, .., 56
-                        // (the first slot of a step is never a pad slot)
-                        uint32_t bits = lane % 8 == 0 ? static_cast<uint32_t>(pcode & 15) << (4 * (lane / 8)) : 0u;
-                        bits |= __shfl_xor(bits, 8);
-                        bits |= __shfl_xor(bits, 16);
-                        bits |= __shfl_xor(bits, 32);
-                        if (lane == 0) s_step[0] = static_cast<int>(bits);
+                    if (wave == 0 && comp == 0) s_d2[jj] = d2;
+                    // species of the 8 steps, 4 bits each, from the first slot
+                    // of each step (lane 8 h; never a pad slot within the rows)
+                    const int pq = pcode & 15;
+                    chunk_species = 0;
+#pragma unroll
+                    for (int h = 0; h < kNb / 4; ++h) {
+                        chunk_species |= static_cast<uint32_t>(__builtin_amdgcn_readlane(pq, 8 * h)) << (4 * h);
                     }
                     int lm = d.l_max, zero = 0;
                     uint32_t mk = hmask;
@@ -463,6 +492,7 @@ void k_soap_quad(
                                                              s_y + jj);
                 }
                 __syncthreads();
+                __builtin_amdgcn_s_setprio(0);
                 {
                     // the next chunk's positions (its bin was loaded one chunk
                     // ago), then the bin of the chunk after it
@@ -655,7 +685,7 @@ size_t quad_lds_bytes(const MfmaDims& d) {
     const size_t cw = static_cast<size_t>(d.crow) * static_cast<size_t>(quad_coefficient_pitch(d.hpad));
     size_t words = static_cast<size_t>(d.H) * kYStride + kNb + kQuadTab + cw + d.hpad;
     if (d.mode == 1) words += cw;
-    return words * sizeof(double) + static_cast<size_t>(d.L + 1 + 1) * sizeof(int);
+    return words * sizeof(double) + static_cast<size_t>(d.L + 1) * sizeof(int);
 }
 
 void launch_quad_expand(hipStream_t stream, int waves, int kg, int instr, const PreparedBatch& pb, const DeviceGraph& g,
