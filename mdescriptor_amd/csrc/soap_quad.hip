@@ -359,11 +359,19 @@ void k_soap_quad(
             }
             // the following centre's metadata, in flight during this one
             prefetch_centre(centre + 1);
-            // an empty species leaves its coefficients at zero (the previous
-            // centre's readers of s_c finished at its last barrier)
-            for (uint32_t m = empty; m != 0; m &= m - 1) {
-                double* cdst_q = s_c + __builtin_ctz(m) * n * cp;
-                for (int i = tid; i < n * cp; i += kThreads) cdst_q[i] = 0.0;
+            // An empty species leaves its coefficients at zero.  The previous
+            // centre's power spectrum may still read s_c: the zeros are
+            // written after the first barrier of this centre, which every
+            // wavefront reaches only after that power spectrum.
+            auto zero_empty_species = [&]() {
+                for (uint32_t m = empty; m != 0; m &= m - 1) {
+                    double* cdst_q = s_c + __builtin_ctz(m) * n * cp;
+                    for (int i = tid; i < n * cp; i += kThreads) cdst_q[i] = 0.0;
+                }
+            };
+            if (slots == 0) {
+                __syncthreads();
+                zero_empty_species();
             }
             // species of the first rows (the accumulators start there)
             const uint32_t filled = ~empty & ((2u << (S - 1)) - 1u);
@@ -493,6 +501,7 @@ void k_soap_quad(
                 }
                 __syncthreads();
                 __builtin_amdgcn_s_setprio(0);
+                if (j0 == 0) zero_empty_species();
                 {
                     // the next chunk's positions (its bin was loaded one chunk
                     // ago), then the bin of the chunk after it
@@ -542,9 +551,9 @@ void k_soap_quad(
                 py = by[next_bin];
                 pz = bz[next_bin];
             }
-            __syncthreads();
         }
         if (d.mode == 1) {
+            __syncthreads(); // every thread's last s_csum update
             // partial rows at a pitch of hp (row r of s_csum starts at r * (hp + 1))
             for (int i = tid; i < d.crow * hp; i += kThreads) part_row[i] = s_csum[i + i / hp];
         }
