@@ -706,16 +706,40 @@ void launch_quad_expand(hipStream_t stream, int waves, int kg, int instr, const 
     MfmaDims dm = d;
     dm.cpitch = quad_coefficient_pitch(d.hpad);
     {
-        // harmonic m-columns over the wavefronts, longest recurrence first
-        int load[16] = {};
-        for (int w = 0; w < 16; ++w) dm.harm_mask[w] = 0;
-        for (int m = 0; m <= d.l_max; ++m) {
-            int best = 0;
-            for (int w = 1; w < waves; ++w) {
-                if (load[w] < load[best]) best = w;
+        // Harmonic m-columns over the wavefronts in contiguous ranges that
+        // minimise the slowest wavefront's instruction count (the barrier
+        // after the harmonics waits for it).  A wavefront steps (x + iy)^m up
+        // to its last column (4 instructions per step); column m costs 2
+        // (its first entry), then 1 and 3 per further degree.
+        const int M = d.l_max + 1;
+        auto column = [&](int m) { return 2 + (m < d.l_max ? 1 + 3 * (d.l_max - m - 1) : 0); };
+        auto range_cost = [&](int a, int b) { // columns a .. b-1, a < b
+            int c = 4 * (b - 1);
+            for (int m = a; m < b; ++m) c += column(m);
+            return c;
+        };
+        constexpr int kInf = 1 << 30;
+        // best[w][i]: least slowest cost of columns 0 .. i-1 over w wavefronts
+        std::vector<std::vector<int>> best(static_cast<size_t>(waves) + 1, std::vector<int>(static_cast<size_t>(M) + 1, kInf));
+        std::vector<std::vector<int>> cut(static_cast<size_t>(waves) + 1, std::vector<int>(static_cast<size_t>(M) + 1, 0));
+        best[0][0] = 0;
+        for (int w = 1; w <= waves; ++w) {
+            for (int i = 0; i <= M; ++i) {
+                for (int j = 0; j <= i; ++j) {
+                    if (best[w - 1][j] == kInf) continue;
+                    const int c = std::max(best[w - 1][j], j < i ? range_cost(j, i) : 0);
+                    if (c < best[w][i]) {
+                        best[w][i] = c;
+                        cut[w][i] = j;
+                    }
+                }
             }
-            dm.harm_mask[best] |= 1u << m;
-            load[best] += d.l_max - m + 1;
+        }
+        for (int w = 0; w < 16; ++w) dm.harm_mask[w] = 0;
+        for (int w = waves, i = M; w >= 1; --w) {
+            const int j = cut[w][i];
+            for (int m = j; m < i; ++m) dm.harm_mask[w - 1] |= 1u << m;
+            i = j;
         }
     }
     const int64_t resident = std::max<int64_t>(1, std::min<int64_t>(32, (160 * 1024) / std::max<size_t>(lds, 1)));
