@@ -32,6 +32,7 @@
 #include <algorithm>
 #include <cmath>
 #include <type_traits>
+#include <utility>
 
 namespace mdx {
 namespace {
@@ -103,10 +104,24 @@ __device__ __forceinline__ d4 gram_tile(const double* arow, const double* brow) 
     return acc;
 }
 
+// first column of degree l in a padded coefficient row (each degree's block
+// rounded up to a multiple of 4 columns)
+constexpr int padded_offset(int l) {
+    int off = 0;
+    for (int i = 0; i < l; ++i) off += 4 * ((2 * i + 4) / 4);
+    return off;
+}
+
+// f(integral_constant<int, l>) for l = 0 .. kQuadLmax, in order
+template <typename F, int... Ls>
+__device__ __forceinline__ void for_each_degree(F&& f, std::integer_sequence<int, Ls...>) {
+    (f(std::integral_constant<int, Ls>{}), ...);
+}
+
 template <int kBytes>
-__device__ void power_spectrum_row(const double* s_c, const int* loff, const MfmaDims& d,
-                                   const double* __restrict__ ps_pref, const int32_t* __restrict__ fbase,
-                                   const int32_t* __restrict__ fstride, void* out_row, int wave, int waves) {
+__device__ void power_spectrum_row(const double* s_c, const MfmaDims& d, const double* __restrict__ ps_pref,
+                                   const int32_t* __restrict__ fbase, const int32_t* __restrict__ fstride,
+                                   void* out_row, int wave, int waves) {
     const int lane = threadIdx.x % kWaveThreads;
     const int W = d.S * d.n;
     const int zero_row = d.crow - 1;
@@ -116,29 +131,30 @@ __device__ void power_spectrum_row(const double* s_c, const int* loff, const Mfm
     const int units = RT * (RT + 1) / 2 * L;
     const int u_begin = wave * units / waves;
     const int u_end = (wave + 1) * units / waves;
-    if (u_begin >= u_end) return;
     constexpr int esize = kBytes;
     const __amdgpu_buffer_rsrc_t rsrc =
         __builtin_amdgcn_make_buffer_rsrc(out_row, 0, static_cast<int>(d.F * esize), 0x00020000);
-    int p = u_begin / L;
-    int l = u_begin - p * L;
-    int bi = 0;
-    while (p >= RT - bi) {
-        p -= RT - bi;
-        ++bi;
-    }
-    int bj = bi + p;
-    const double* arow = s_c;
-    const double* brow = s_c;
-    int fb[4] = {kDroppedOffset, kDroppedOffset, kDroppedOffset, kDroppedOffset}, fs[4] = {0, 0, 0, 0};
-    bool new_pair = true;
-    for (int u = u_begin; u < u_end; ++u) {
-        if (new_pair) {
-            new_pair = false;
-            const int ia = 16 * bi + lane % 16 < W ? 16 * bi + lane % 16 : zero_row;
-            const int jb = 16 * bj + lane % 16 < W ? 16 * bj + lane % 16 : zero_row;
-            arow = s_c + ia * hp + lane / 16;
-            brow = s_c + jb * hp + lane / 16;
+    // the range as runs of degrees of one tile pair; within a run the
+    // degrees are unrolled, so their K steps, column offsets and prefactor
+    // reads are fixed at compile time and consecutive degrees' reads and
+    // MFMAs overlap
+    int u = u_begin;
+    while (u < u_end) {
+        int p = u / L;
+        const int l0 = u - p * L;
+        const int l1 = min(L, l0 + (u_end - u));
+        int bi = 0;
+        while (p >= RT - bi) {
+            p -= RT - bi;
+            ++bi;
+        }
+        const int bj = bi + p;
+        const int ia = 16 * bi + lane % 16 < W ? 16 * bi + lane % 16 : zero_row;
+        const int jb = 16 * bj + lane % 16 < W ? 16 * bj + lane % 16 : zero_row;
+        const double* arow = s_c + ia * hp + lane / 16;
+        const double* brow = s_c + jb * hp + lane / 16;
+        int fb[4], fs[4];
+        {
             const int j = 16 * bj + lane % 16;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -149,39 +165,26 @@ __device__ void power_spectrum_row(const double* s_c, const int* loff, const Mfm
                 fs[r] = base >= 0 ? fstride[idx] * esize : 0;
             }
         }
-        const double pref = ps_pref[l];
-        // K steps of degree l: ceil((2l + 1) / 4), operands read before the MFMAs
-        const int base = loff[l];
-        d4 acc4;
-        switch ((2 * l + 4) / 4) {
-        case 1: acc4 = gram_tile<1>(arow + base, brow + base); break;
-        case 2: acc4 = gram_tile<2>(arow + base, brow + base); break;
-        case 3: acc4 = gram_tile<3>(arow + base, brow + base); break;
-        case 4: acc4 = gram_tile<4>(arow + base, brow + base); break;
-        default: {
-            acc4 = d4{0.0, 0.0, 0.0, 0.0};
-            for (int s = 0; s < (2 * l + 4) / 4; ++s) acc4 = mfma(arow[base + 4 * s], brow[base + 4 * s], acc4);
-        }
-        }
+        auto degree = [&](auto lc) {
+            constexpr int l = decltype(lc)::value;
+            if (l < l0 || l >= l1) return;
+            constexpr int kSteps = (2 * l + 4) / 4;
+            const d4 acc4 = gram_tile<kSteps>(arow + padded_offset(l), brow + padded_offset(l));
+            const double pref = ps_pref[l];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const double v = pref * acc4[r];
-            const int off = fb[r] + l * fs[r];
-            if (esize == 4) {
-                __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(static_cast<float>(v)), rsrc, off, 0, 0);
-            } else {
-                const i2 bits = {__double2loint(v), __double2hiint(v)};
-                __builtin_amdgcn_raw_buffer_store_b64(bits, rsrc, off, 0, 0);
+            for (int r = 0; r < 4; ++r) {
+                const double v = pref * acc4[r];
+                const int off = fb[r] + l * fs[r];
+                if (esize == 4) {
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(static_cast<float>(v)), rsrc, off, 0, 0);
+                } else {
+                    const i2 bits = {__double2loint(v), __double2hiint(v)};
+                    __builtin_amdgcn_raw_buffer_store_b64(bits, rsrc, off, 0, 0);
+                }
             }
-        }
-        if (++l == L) {
-            l = 0;
-            new_pair = true;
-            if (++bj == RT) {
-                ++bi;
-                bj = bi;
-            }
-        }
+        };
+        for_each_degree(degree, std::make_integer_sequence<int, kQuadLmax + 1>{});
+        u += l1 - l0;
     }
 }
 
@@ -536,9 +539,9 @@ void k_soap_quad(
             if (d.mode == 0) {
                 char* row = static_cast<char*>(out) + centre * pitch;
                 if (d.out_dtype == 4) {
-                    power_spectrum_row<4>(s_c, s_loff, d, ps_pref, fbase, fstride, row, wave, T);
+                    power_spectrum_row<4>(s_c, d, ps_pref, fbase, fstride, row, wave, T);
                 } else {
-                    power_spectrum_row<8>(s_c, s_loff, d, ps_pref, fbase, fstride, row, wave, T);
+                    power_spectrum_row<8>(s_c, d, ps_pref, fbase, fstride, row, wave, T);
                 }
             } else if (d.mode == 1) {
                 for (int i = tid; i < cw; i += kThreads) s_csum[i] += s_c[i];
