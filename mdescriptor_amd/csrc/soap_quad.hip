@@ -410,11 +410,14 @@ void k_soap_quad(
                     for (int g = 0; g < G; ++g) yv[s][g] = yrow[g][4 * (h + s)];
                 }
             };
-            // the 8 steps of a chunk on the wavefront's own instruction count GW
-            auto steps_of_chunk = [&](auto gw) {
+            // the steps of a chunk on the wavefront's own instruction count GW,
+            // in pairs up to the end of the centre's rows (a step past it, in
+            // the last pair, has slots with all-zero harmonics and adds zeros)
+            auto steps_of_chunk = [&](auto gw, int nst) {
                 constexpr int GW = decltype(gw)::value;
 #pragma unroll
                 for (int h = 0; h < kNb / 4; h += 2) {
+                    if (h >= nst) break;
                     double ev[2], yv[2][GW];
 #pragma unroll
                     for (int s = 0; s < 2; ++s) {
@@ -430,22 +433,23 @@ void k_soap_quad(
                 }
             };
             uint32_t chunk_species = 0; // species of the current chunk's steps, 4 bits each
-            // A chunk whose 8 steps all continue the current species (the common
-            // case: one species' rows span several chunks) runs without per-step
-            // checks; any other chunk checks each step for the end of the rows
-            // and for a change of species.
+            // A chunk whose steps within the rows all continue the current
+            // species (the common case: one species' rows span several chunks,
+            // and the centre's last chunk) runs without per-step checks; a
+            // chunk that changes species checks each step (a fold).
             auto contract = [&](int j0) {
                 const uint32_t species = chunk_species;
                 const int nst = min(kNb / 4, (slots - j0) / 4);
-                if (nst == kNb / 4 && species == static_cast<uint32_t>(cur) * 0x11111111u) {
+                const uint32_t live = nst >= kNb / 4 ? 0xffffffffu : (1u << (4 * nst)) - 1u;
+                if (((species ^ static_cast<uint32_t>(cur) * 0x11111111u) & live) == 0) {
                     if (G >= 4 && wave_instr >= 4) {
-                        steps_of_chunk(std::integral_constant<int, (G >= 4 ? 4 : G)>{});
+                        steps_of_chunk(std::integral_constant<int, (G >= 4 ? 4 : G)>{}, nst);
                     } else if (G >= 3 && wave_instr == 3) {
-                        steps_of_chunk(std::integral_constant<int, (G >= 3 ? 3 : G)>{});
+                        steps_of_chunk(std::integral_constant<int, (G >= 3 ? 3 : G)>{}, nst);
                     } else if (G >= 2 && wave_instr == 2) {
-                        steps_of_chunk(std::integral_constant<int, (G >= 2 ? 2 : G)>{});
+                        steps_of_chunk(std::integral_constant<int, (G >= 2 ? 2 : G)>{}, nst);
                     } else {
-                        steps_of_chunk(std::integral_constant<int, 1>{});
+                        steps_of_chunk(std::integral_constant<int, 1>{}, nst);
                     }
                     return;
                 }
