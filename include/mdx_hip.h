@@ -122,7 +122,9 @@ typedef struct mdx_timing {
     int64_t expansion_launches; /* launches of the expansion kernel in the run */
     int64_t expansion_tiles;    /* 16x16 tiles of the matrix-core kernel's template;
                                    minus the wavefronts of the 4x4-block kernel
-                                   when that ran; 0 when the generic kernel ran */
+                                   when that ran; -(1000 + wavefronts) when the
+                                   register-coefficient kernel ran; 0 when the
+                                   generic kernel ran */
 } mdx_timing;
 
 typedef struct mdx_hip_ctx mdx_hip_ctx;

@@ -20,7 +20,8 @@ CSRC = PACKAGE / "csrc"
 OBJ_DIR = PACKAGE / "_build"
 LIB_DIR = PACKAGE / "_lib"
 LIBRARY = LIB_DIR / "libmdx_hip.so"
-SOURCES = ("graph.hip", "soap.hip", "soap_mfma.hip", "soap_quad.hip", "neighbor_list.hip", "api.hip")
+SOURCES = ("graph.hip", "soap.hip", "soap_mfma.hip", "soap_quad.hip", "soap_block.hip", "neighbor_list.hip",
+           "api.hip")
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

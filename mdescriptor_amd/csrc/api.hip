@@ -7,6 +7,7 @@
 // cpp/cuda/src/backend.cu:339-345).
 #include "mdx_internal.h"
 #include "soap_mfma.h"
+#include "soap_block.h"
 
 #include <algorithm>
 #include <chrono>
@@ -557,8 +558,8 @@ int mdx_hip_soap_plan_create(mdx_hip_ctx* ctx, const mdx_soap_params* params, md
             // makes the 16x16-tile kernel mandatory, =quad the 4x4-block kernel
             const char* env = std::getenv("MDX_HIP_SOAP_KERNEL");
             const std::string choice = env != nullptr ? env : "auto";
-            if (choice != "auto" && choice != "generic" && choice != "mfma" && choice != "quad") {
-                throw mdx::Error(MDX_INVALID_ARGUMENT, "MDX_HIP_SOAP_KERNEL must be auto, generic, mfma or quad");
+            if (choice != "auto" && choice != "generic" && choice != "mfma" && choice != "quad" && choice != "block") {
+                throw mdx::Error(MDX_INVALID_ARGUMENT, "MDX_HIP_SOAP_KERNEL must be auto, generic, mfma, quad or block");
             }
             const mdx::MfmaPlanHost mp = mdx::plan_mfma_tables(plan->Sc, n, p.l_max, beta, pref);
             mdx::MfmaDims md{};
@@ -607,6 +608,22 @@ int mdx_hip_soap_plan_create(mdx_hip_ctx* ctx, const mdx_soap_params* params, md
             }
             if (choice == "quad" && plan->quad_waves == 0) {
                 throw mdx::Error(MDX_INVALID_ARGUMENT, "SOAP plan is outside the 4x4-block kernel's limits");
+            }
+            // register-coefficient kernel: default options, atom-level rows,
+            // a compiled (l_max, radial groups, species) shape
+            if (plan->use_mfma && defaults && quad_range && p.average == 0 && (choice == "auto" || choice == "block")) {
+                mdx::BlockPlanHost bp;
+                if (mdx::block_plan_tables(plan->S, n, p.l_max, beta, pref, expo, bp)) {
+                    plan->block_waves = bp.waves;
+                    plan->block_kg = bp.kg;
+                    plan->block_ncr = bp.ncr;
+                    upload(plan->d_block_e1, bp.lane_e1);
+                    upload(plan->d_block_beta, bp.lane_beta);
+                    upload(plan->d_block_ps, bp.ps_offsets);
+                }
+            }
+            if (choice == "block" && plan->block_waves == 0) {
+                throw mdx::Error(MDX_INVALID_ARGUMENT, "SOAP plan is outside the register-coefficient kernel's shapes");
             }
             if (plan->use_mfma) {
                 upload(plan->d_row_channel, mp.row_channel);

@@ -255,6 +255,11 @@ struct mdx_soap_plan {
     // not used), radial groups, MFMA instructions per step, lane constants
     int quad_waves = 0, quad_kg = 0, quad_instr = 0;
     mdx::DeviceBuffer d_quad_lanes;
+    // register-coefficient kernel (soap_block.hip), default options and
+    // average "off" only: wavefronts (0: not used), radial groups,
+    // coefficient registers, lane tables
+    int block_waves = 0, block_kg = 0, block_ncr = 0;
+    mdx::DeviceBuffer d_block_e1, d_block_beta, d_block_ps;
     // options beyond the GTO / uncompressed / unweighted default (mdx_soap_options)
     int Sc = 0;              // coefficient species: 1 for mu2, else S
     int compression = 0;     // 0 off, 1 mu2, 2 mu1nu1, 3 crossover

@@ -20,6 +20,7 @@
 // rows of each structure in a fixed order.
 #include "mdx_internal.h"
 #include "soap_mfma.h"
+#include "soap_block.h"
 
 #include <algorithm>
 #include <cmath>
@@ -412,8 +413,10 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
     const bool hook = on_slice != nullptr && *on_slice && p.average == 0;
     int64_t launches = 0;
     if (p.use_mfma) {
-        // the 4x4-block kernel where the plan chose it and every centre's rows fit its slot codes
-        const bool quad = p.quad_waves > 0 && g.most_rows < kQuadMaxRows;
+        // the register-coefficient kernel, else the 4x4-block kernel, where
+        // the plan chose them and every centre's rows fit their slot codes
+        const bool block = p.block_waves > 0 && p.average == 0 && g.most_rows < kQuadMaxRows;
+        const bool quad = !block && p.quad_waves > 0 && g.most_rows < kQuadMaxRows;
         MfmaDims md{};
         md.S = p.S;
         md.n = p.n;
@@ -461,7 +464,28 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
         for (int64_t base = 0; base < items; base += slice) {
             if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
             const int64_t count = std::min(slice, items - base);
-            if (quad) {
+            if (block) {
+                BlockArgs ba{};
+                ba.positions = pb.d_positions.as<double>();
+                ba.pair_start = g.pair_start.as<int64_t>();
+                ba.counts = g.counts.as<int32_t>();
+                ba.pair_bin = g.pair_bin.as<uint32_t>();
+                ba.bx = g.bin_x.as<double>();
+                ba.by = g.bin_y.as<double>();
+                ba.bz = g.bin_z.as<double>();
+                ba.lane_e1 = p.d_block_e1.as<double>();
+                ba.lane_beta = p.d_block_beta.as<double>();
+                ba.ps_offsets = p.d_block_ps.as<int2>();
+                ba.ps_pref = tab.ps_pref;
+                ba.S = p.S;
+                ba.out_dtype = p.out_dtype;
+                ba.F = p.features;
+                ba.item_base = base;
+                ba.items = count;
+                ba.out = out_device;
+                ba.pitch = pitch_bytes;
+                launch_block_expand(stream, p.l_max, p.block_kg, p.block_ncr, ba, count);
+            } else if (quad) {
                 launch_quad_expand(stream, p.quad_waves, p.quad_kg, p.quad_instr, pb, g, p.d_quad_lanes.as<QuadLane>(),
                                    tab.ps_pref, tab.fbase, tab.fstride, md, d_item_begin, base, count, out_device,
                                    pitch_bytes, d_partial);
@@ -479,7 +503,7 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
         if (events != nullptr) MDX_HIP(hipEventRecord(events[4], stream));
         if (timing != nullptr) {
             timing->expansion_launches = launches;
-            timing->expansion_tiles = quad ? -p.quad_waves : tt;
+            timing->expansion_tiles = block ? -(1000 + p.block_waves) : quad ? -p.quad_waves : tt;
         }
         return;
     }

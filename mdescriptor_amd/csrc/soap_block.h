@@ -1,0 +1,48 @@
+// Host/device interface of the register-coefficient SOAP kernel
+// (soap_block.hip): default options (GTO basis, no weighting, no
+// compression), atom-level rows (average "off").
+#pragma once
+
+#include "mdx_internal.h"
+
+namespace mdx {
+
+// Launch arguments (one struct, passed by value).
+struct BlockArgs {
+    const double* positions;    // f64[atoms * 3]
+    const int64_t* pair_start;  // first pair row of each centre
+    const int32_t* counts;      // rows per (centre, species)
+    const uint32_t* pair_bin;   // bin of each pair row
+    const double* bx;           // binned image positions
+    const double* by;
+    const double* bz;
+    const double* lane_e1;      // [l][register][64]: -a_lk 64/ln2 of the lane's exp row, 0 for pad rows
+    const double* lane_beta;    // [l][fold term][64]: beta^T operand of the lane
+    const int2* ps_offsets;     // [tile pair][value][64]: feature index at l = 0 and its stride per l
+    const double* ps_pref;      // [L]: pi sqrt(8/(2l+1))
+    int S;                      // species
+    int out_dtype;              // 4 or 8 bytes
+    int64_t F;                  // features per row
+    int64_t item_base, items, per_block;
+    void* out;
+    int64_t pitch;              // bytes between output rows
+};
+
+// Plan tables of the kernel for one SOAP shape.  beta_scaled is
+// pi^1.5 beta with index (l*n + n')*n + k, pref the radial prefactor of
+// channel l*n + k, expo the radial exponent a_lk.
+struct BlockPlanHost {
+    int kg = 0;      // radial groups of 4 channels
+    int ncr = 0;     // coefficient registers per (l, column group)
+    int waves = 0;   // wavefronts per workgroup
+    std::vector<double> lane_e1, lane_beta;
+    std::vector<int32_t> ps_offsets; // int2 pairs
+};
+
+// Fills out and returns true when (S, n, l_max) is one of the compiled shapes.
+bool block_plan_tables(int S, int n, int l_max, const std::vector<double>& beta_scaled, const std::vector<double>& pref,
+                       const std::vector<double>& expo, BlockPlanHost& out);
+size_t block_lds_bytes(int l_max, int kg);
+void launch_block_expand(hipStream_t stream, int l_max, int kg, int ncr, const BlockArgs& a, int64_t count);
+
+} // namespace mdx

@@ -1,0 +1,847 @@
+// Kernels 2-4 for the default SOAP options (GTO basis, no weighting, no
+// compression) with the coefficients held in registers: neighbour expansion
+// on 4x4x4 FP64 matrix-core blocks, beta fold, power spectrum on 16x16x4 FP64
+// Gram tiles and the row write (soap.cpp:864-930, 997-1013).
+//
+// One workgroup of T wavefronts handles one centre at a time.  Degree l is
+// owned by one wavefront, which keeps everything of that degree in its
+// registers: the contraction accumulators, the coefficients of every species
+// and the power spectrum.  The wavefronts share only the harmonic staging in
+// LDS, double-buffered, with one barrier per chunk of 32 neighbour slots.
+//
+// Matrix-core layouts (v_mfma_f64_4x4x4f64, four independent 4x4 blocks; the
+// block of lane L is b = (L/4) % 4):
+//   A operand lane L = A_b[row L % 4][k L / 16]
+//   B operand lane L = B_b[k L / 16][col L % 4]
+//   result    lane L = D_b[row L / 16][col L % 4]
+// and for v_mfma_f64_16x16x4f64: A lane L = A[row L % 16][k L / 16],
+// B lane L = B[k L / 16][col L % 16], result value r of lane L =
+// D[row 4 r + L / 16][col L % 16].
+//
+// Contraction, A[(l,k)][(l,m)] = sum_j e^{-a_lk d_j^2} Y_lm(j)
+// (soap.cpp:893-914).  An exp register of degree l holds, per block, radial
+// group rg (4 channels k) at step phase ph: R radial groups times P = 4/R
+// phases (R = 2 for two radial groups, else 1), so one register of exps feeds
+// P consecutive steps of 4 neighbours and no lane computes an exp that is not
+// used.  Its MFMA with the harmonic block of column group cg (4 columns of
+// degree l) accumulates blocks (rg, ph) x (k, m).  Each species' rows fill a
+// segment of slots padded to a whole step group (4 P slots), so a group never
+// mixes species.
+//
+// At a species change the phases of each accumulator are summed (row
+// rotations) and the species' radial groups are added into the block slots of
+// its "channel groups" (species q, radial group rg) of the coefficient
+// registers C[r], r = group / 4, slot group % 4 (for three radial groups, one
+// register per species, slot rg).  At the end of the centre every C[r] is
+// scaled by the harmonic scale S_lm of its columns (the staged harmonics are
+// the scaled recurrence of harmonic_table.h; pad columns have S_lm = 0) and
+// folded with beta (soap.cpp:915-926) in transposed form,
+//   c^T = A^T beta^T:  A operand = the accumulator (lane L = A[k L/16][m L%4]
+//   read as A^T[m][k]), B operand = beta^T (lane constant),
+// which leaves lane L of block (group) b holding c[n' = L % 4][m = L / 16]:
+// exactly a 16x16x4 Gram operand whose 16 rows are 4 channel groups x 4 radial
+// channels and whose K index is m.  The radial groups of a species mix through
+// the fold terms: two radial groups exchange blocks b and b^1 (lane swizzle),
+// three rotate the blocks of the species' register.
+//
+// Power spectrum (soap.cpp:997-1013): p_l[i][j] = sum_m c[i][m] c[j][m] for the
+// degrees a wavefront owns, one 16x16x4 MFMA per column group and register
+// pair, scaled by pi sqrt(8/(2l+1)) and stored with raw buffer stores whose
+// range check drops the pairs i > j and the pad channels.
+#include "soap_device.h"
+#include "soap_block.h"
+
+#include <algorithm>
+#include <cmath>
+#include <type_traits>
+#include <utility>
+
+namespace mdx {
+namespace {
+
+constexpr int kYS = kNb + 1;       // harmonic staging: entry h of slot j at h * kYS + j
+constexpr int kTab = 64;           // 2^(j/64) table entries
+constexpr int kDropped = 0x40000000; // byte offset no output row reaches (buffer range check drops it)
+
+// ---------------------------------------------------------------- plan ----
+
+constexpr int cgroups(int l) { return (2 * l + 4) / 4; } // ceil((2l+1)/4)
+
+template <int LM, int KG>
+struct BlockPlan {
+    static constexpr int L = LM + 1;
+    static constexpr int H = L * L;
+    static constexpr int R = KG == 2 ? 2 : 1;   // radial groups per exp register
+    static constexpr int P = 4 / R;             // step phases per exp register
+    static constexpr int RPL = KG / R;          // exp registers per degree
+    static constexpr int NT = KG == 1 ? 1 : KG == 2 ? 2 : 4; // fold terms
+    static constexpr int GS = 4 * P;            // slots per step group
+    static constexpr int GROUPS = kNb / GS;     // step groups per chunk
+    static constexpr int T = L < 4 ? L : 4;     // wavefronts
+    static constexpr int YROWS = H + 3;         // staged harmonic rows (pad columns of degree LM read up to H + 2)
+    static constexpr int YWORDS = YROWS * kYS;
+
+    // degrees of each wavefront: longest processing time first over the cost
+    // of a degree per step group (exps of 12 VALU instructions, 4 cycles each,
+    // and its MFMAs of 16 cycles)
+    struct Owners {
+        unsigned mask[4];
+    };
+    static constexpr Owners owners() {
+        Owners o{};
+        int load[4] = {0, 0, 0, 0};
+        bool done[L] = {};
+        for (int it = 0; it < L; ++it) {
+            int best = -1, best_cost = -1;
+            for (int l = L - 1; l >= 0; --l) {
+                const int c = RPL * (48 + 16 * cgroups(l));
+                if (!done[l] && c > best_cost) {
+                    best = l;
+                    best_cost = c;
+                }
+            }
+            done[best] = true;
+            int w = 0;
+            for (int v = 1; v < T; ++v)
+                if (load[v] < load[w]) w = v;
+            load[w] += best_cost;
+            o.mask[w] |= 1u << best;
+        }
+        return o;
+    }
+    static constexpr unsigned own(int w) { return owners().mask[w]; }
+
+    // harmonic m-columns of each wavefront: contiguous ranges minimising the
+    // slowest wavefront's VALU count.  Column m costs one instruction for
+    // degree m + 1 and three per further degree plus one store per degree;
+    // reaching T_m by the Chebyshev ladder costs two per step past m = 1.
+    struct Split {
+        int lo[4], hi[4];
+    };
+    static constexpr int column_cost(int m) {
+        return (m < LM ? 1 : 0) + 3 * (LM - m - 1 > 0 ? LM - m - 1 : 0) + (LM - m + 1);
+    }
+    static constexpr int range_cost(int a, int b) {
+        if (a >= b) return 0;
+        int c = 2 * (b - 1 > 1 ? b - 2 : 0);
+        for (int m = a; m < b; ++m) c += column_cost(m);
+        return c;
+    }
+    static constexpr Split split() {
+        constexpr int kInf = 1 << 29;
+        int best[5][L + 1] = {};
+        int cut[5][L + 1] = {};
+        for (int w = 0; w <= T; ++w)
+            for (int i = 0; i <= L; ++i) best[w][i] = kInf;
+        best[0][0] = 0;
+        for (int w = 1; w <= T; ++w) {
+            for (int i = 0; i <= L; ++i) {
+                for (int j = 0; j <= i; ++j) {
+                    if (best[w - 1][j] == kInf) continue;
+                    const int c = best[w - 1][j] > range_cost(j, i) ? best[w - 1][j] : range_cost(j, i);
+                    if (c < best[w][i]) {
+                        best[w][i] = c;
+                        cut[w][i] = j;
+                    }
+                }
+            }
+        }
+        Split s{};
+        int i = L;
+        for (int w = T; w >= 1; --w) {
+            const int j = cut[w][i];
+            s.lo[w - 1] = j;
+            s.hi[w - 1] = i;
+            i = j;
+        }
+        return s;
+    }
+    static constexpr int mlo(int w) { return split().lo[w]; }
+    static constexpr int mhi(int w) { return split().hi[w]; }
+};
+
+// owned (l, cg) pairs before degree l, and in total, for a wavefront's mask
+constexpr int units_before(unsigned mask, int l) {
+    int u = 0;
+    for (int i = 0; i < l; ++i)
+        if ((mask >> i) & 1u) u += cgroups(i);
+    return u;
+}
+constexpr int units_total(unsigned mask, int L) { return units_before(mask, L); }
+constexpr int degrees_before(unsigned mask, int l) {
+    int d = 0;
+    for (int i = 0; i < l; ++i)
+        if ((mask >> i) & 1u) ++d;
+    return d;
+}
+constexpr int popcount_c(unsigned m) { return m == 0 ? 0 : (int)(m & 1u) + popcount_c(m >> 1); }
+
+template <typename F, int... Is>
+__device__ __forceinline__ void static_for(F&& f, std::integer_sequence<int, Is...>) {
+    (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void unroll(F&& f) {
+    static_for(f, std::make_integer_sequence<int, N>{});
+}
+
+// --------------------------------------------------------------- device ---
+
+__device__ __forceinline__ double mfma4(double a, double b, double c) {
+    return __builtin_amdgcn_mfma_f64_4x4x4f64(a, b, c, 0, 0, 0);
+}
+
+// value of lane (L - k) mod 16 within each 16-lane row (DPP row rotate right
+// by k lanes): block b takes block (b - k / 4) mod 4
+template <int kLanes>
+__device__ __forceinline__ double row_rotate(double v) {
+    constexpr int ctrl = 0x120 + kLanes; // row_ror:kLanes
+    const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(v), ctrl, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(v), ctrl, 0xF, 0xF, false);
+    return __hiloint2double(hi, lo);
+}
+
+// value of lane L ^ 4 (block b takes block b ^ 1, columns unchanged)
+__device__ __forceinline__ double swap_blocks(double v) {
+    constexpr int pattern = 0x1F | (4 << 10); // swizzle bit mode: and 0x1f, or 0, xor 4
+    const int lo = __builtin_amdgcn_ds_swizzle(__double2loint(v), pattern);
+    const int hi = __builtin_amdgcn_ds_swizzle(__double2hiint(v), pattern);
+    return __hiloint2double(hi, lo);
+}
+
+// exp(-a d2) for d2 >= 0 and -a d2 >= -708, given e1 = -a 64/ln2: Tang's
+// table method (ACM TOMS 15(2), 1989) with the reduction on the product,
+// y = d2 e1 = 64k + j + rs (|rs| <= 1/2), exp = 2^k 2^(j/64) e^r, r = rs ln2/64,
+// e^r - 1 by its degree-5 Taylor polynomial in rs.  rs = fma(d2, e1, -(64k+j))
+// carries only e1's rounding: within 5e-15 relative of exp(-a d2) for
+// -a d2 >= -40, as close as libm's exp of the rounded product further out.
+// tab[j] = 2^(j/64) with j << 14 taken off its high word, so that adding
+// (64k + j) << 14 scales it by 2^k in one integer add.
+constexpr double kExpC1 = 0.693147180559945309417232121458176568 / 64.0;
+constexpr double kExpC2 = kExpC1 * kExpC1 / 2.0;
+constexpr double kExpC3 = kExpC2 * kExpC1 / 3.0;
+constexpr double kExpC4 = kExpC3 * kExpC1 / 4.0;
+constexpr double kExpC5 = kExpC4 * kExpC1 / 5.0;
+__device__ __forceinline__ double exp_neg(double d2, double e1, const int2* tab) {
+    constexpr double kShifter = 6755399441055744.0; // 1.5 * 2^52
+    const double s = fma(d2, e1, kShifter);
+    const double kf = s - kShifter;
+    const double rs = fma(d2, e1, -kf);
+    const int nj = __double2loint(s);
+    const int2 t = *reinterpret_cast<const int2*>(reinterpret_cast<const char*>(tab) + ((nj << 3) & 0x1f8));
+    double q = fma(kExpC5, rs, kExpC4);
+    q = fma(q, rs, kExpC3);
+    q = fma(q, rs, kExpC2);
+    q = fma(q, rs, kExpC1);
+    const double em1 = q * rs;
+    const double tk = __hiloint2double(t.y + (nj << 14), t.x);
+    return fma(tk, em1, tk);
+}
+
+// Column m of the scaled harmonics (harmonic_table.h) from T_m, one part per
+// lane: comp 0 the cos part (entry l*l + l - m), comp 1 the sin part
+// (l*l + l + m).  col0 is the lane's slot in the staging buffer.
+template <int LM, int M>
+__device__ __forceinline__ void harmonic_column(double tm, double z, double r2, int comp, double* col0) {
+    double* col = col0 + (comp != 0 ? M : -M) * kYS;
+    col[(M * M + M) * kYS] = tm;
+    if constexpr (M < LM) {
+        double q2 = tm;
+        double q1 = z * tm;
+        col[((M + 1) * (M + 1) + (M + 1)) * kYS] = q1;
+        unroll<LM - M - 1>([&](auto i) {
+            constexpr int l = M + 2 + decltype(i)::value;
+            constexpr double c = kScaledHarmonic.c[l][M];
+            const double q = fma(z, q1, -((c * r2) * q2));
+            col[(l * l + l) * kYS] = q;
+            q2 = q1;
+            q1 = q;
+        });
+    }
+}
+
+// Columns [MLO, MHI) of one slot's scaled harmonics.  Both lanes of a slot run
+// the Chebyshev ladder T_m = 2x T_{m-1} - (x^2+y^2) T_{m-2}, which gives the
+// cos part Re (x+iy)^m from (T_0, T_1) = (s, s x) and the sin part Im (x+iy)^m
+// from (0, s y); s is 1, or 0 for a pad slot.  The sin part of m = 0 is empty:
+// those lanes skip that column.
+template <int LM, int MLO, int MHI>
+__device__ __forceinline__ void harmonic_columns(double x, double y, double z, double s, int comp, double* col0) {
+    if constexpr (MLO < MHI) {
+        const double rho2 = fma(x, x, y * y);
+        const double r2 = fma(z, z, rho2);
+        const double tx = x + x;
+        double t0 = comp != 0 ? 0.0 : s;
+        double t1 = (comp != 0 ? y : x) * s;
+        unroll<MHI>([&](auto mc) {
+            constexpr int m = decltype(mc)::value;
+            double tm;
+            if constexpr (m == 0) {
+                tm = t0;
+            } else if constexpr (m == 1) {
+                tm = t1;
+            } else {
+                tm = fma(tx, t1, -(rho2 * t0));
+                t0 = t1;
+                t1 = tm;
+            }
+            if constexpr (m >= MLO) {
+                if constexpr (m == 0) {
+                    if (comp == 0) harmonic_column<LM, 0>(tm, z, r2, comp, col0);
+                } else {
+                    harmonic_column<LM, m>(tm, z, r2, comp, col0);
+                }
+            }
+        });
+    }
+}
+
+// a wave-uniform 64-bit value in scalar registers
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+    const int lo = __builtin_amdgcn_readfirstlane(static_cast<int>(v));
+    const int hi = __builtin_amdgcn_readfirstlane(static_cast<int>(v >> 32));
+    return static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | static_cast<uint32_t>(lo));
+}
+
+template <int LM, int KG, int NCR, int W>
+__device__ __forceinline__ void block_role(const BlockArgs& a, double* lds) {
+    using PL = BlockPlan<LM, KG>;
+    constexpr int L = PL::L, R = PL::R, P = PL::P, RPL = PL::RPL, NT = PL::NT, GS = PL::GS;
+    constexpr int GROUPS = PL::GROUPS;
+    constexpr unsigned kOwn = PL::own(W);
+    constexpr int NU = units_total(kOwn, L); // owned (l, cg) pairs
+    constexpr int ND = popcount_c(kOwn);     // owned degrees
+    constexpr int MLO = PL::mlo(W), MHI = PL::mhi(W);
+
+    const int lane = threadIdx.x % kWaveThreads;
+    const int S = a.S;
+    double* s_y = lds;                                        // 2 x YWORDS
+    double* s_d2 = s_y + 2 * PL::YWORDS;                      // 2 x kNb
+    const int2* s_tab = reinterpret_cast<const int2*>(s_d2 + 2 * kNb); // kTab
+    const double* s_scale = s_d2 + 2 * kNb + kTab;           // padded S_lm table
+
+    // lane constants of the owned degrees
+    double e1[ND][RPL];
+    double bt[ND][NT];
+    unroll<L>([&](auto lc) {
+        constexpr int l = decltype(lc)::value;
+        if constexpr ((kOwn >> l) & 1u) {
+            constexpr int d = degrees_before(kOwn, l);
+            unroll<RPL>([&](auto rc) {
+                constexpr int rr = decltype(rc)::value;
+                e1[d][rr] = a.lane_e1[(l * RPL + rr) * kWaveThreads + lane];
+            });
+            unroll<NT>([&](auto tc) {
+                constexpr int t = decltype(tc)::value;
+                bt[d][t] = a.lane_beta[(l * NT + t) * kWaveThreads + lane];
+            });
+        }
+    });
+    const int blk = (lane / 4) % 4;
+    const int ph = blk / R;
+    // staging reads: B operand of (l, cg) at ((l*l + 4 cg) kYS + GS g) + yread,
+    // the lane's slot of step group g at GS g + dread
+    const int yread = (lane % 4) * kYS + 4 * ph + lane / 16;
+    const int dread = 4 * ph + lane / 16;
+    // lanes of the block slots {0, 1} (KG = 2: the even species' groups)
+    const bool low_pair = (lane % 16) < 8;
+
+    // ---------------------------------------------------------- slot stream
+    // Work: centres [first, last) of this workgroup.  A centre's rows are
+    // grouped by species: cnt_t rows of species t after those of the species
+    // before it.  The stream cuts each species' rows into chunks of at most 32
+    // slots (a chunk never mixes species; its last step group may hold pad
+    // slots past the rows) and runs two chunks ahead of the contraction: each
+    // lane pair (two lanes per slot) loads the bin of its slot's row.  All of
+    // its state but the loaded bins is wave-uniform.
+    const int64_t item_first = a.item_base + static_cast<int64_t>(blockIdx.x) * a.per_block;
+    const int64_t item_last = min(item_first + a.per_block, a.item_base + a.items);
+    int pre_count = 0;     // next centre: rows of species t at lane t
+    int64_t pre_start = 0; // next centre: first pair row (lane 0)
+    auto prefetch_centre = [&](int64_t c) {
+        if (c < item_last) {
+            if (lane < S) pre_count = a.counts[c * S + lane];
+            if (lane == 0) pre_start = a.pair_start[c];
+        }
+    };
+    int cnt = 0;                       // stream centre: rows of species t at lane t
+    int64_t st_centre = item_first - 1;
+    int64_t st_row = 0;                // pair row of the next chunk's first slot
+    int st_q = 0;                      // species of the next chunk
+    int st_left = 0;                   // rows of species st_q not yet in a chunk
+    uint32_t st_more = 0;              // species after st_q with rows (bit mask)
+    auto next_species = [&]() {
+        st_q = __builtin_amdgcn_readfirstlane(__builtin_ctz(st_more));
+        st_more = __builtin_amdgcn_readfirstlane(st_more & (st_more - 1));
+        st_left = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(cnt, st_q));
+    };
+    auto enter_centre = [&]() {
+        st_centre = uniform64(st_centre + 1);
+        cnt = pre_count;
+        st_row = uniform64(lane_value(pre_start, 0));
+        st_more = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(__ballot(lane < S && cnt > 0)));
+        prefetch_centre(st_centre + 1);
+        st_left = 0;
+        if (st_more != 0) next_species();
+    };
+    // pipeline stage of one chunk; everything but the bin is wave-uniform
+    struct Stage {
+        int64_t centre; // -1: no chunk
+        int q;          // species
+        int rows;       // rows in the chunk (slots past them are pad slots)
+        int groups;     // step groups
+        bool last;      // last chunk of its centre
+        uint32_t bin;   // bin of the lane's slot row (slot < rows)
+    };
+    auto next_stage = [&]() -> Stage {
+        Stage s{-1, 0, 0, 0, false, 0u};
+        if (st_left == 0) {
+            if (st_more != 0) {
+                next_species();
+            } else {
+                if (st_centre + 1 >= item_last) return s;
+                enter_centre();
+            }
+        }
+        const int n = min(st_left, kNb);
+        s.centre = st_centre;
+        s.q = st_q;
+        s.rows = n;
+        s.groups = (n + GS - 1) / GS;
+        if (lane / 2 < n) s.bin = a.pair_bin[st_row + lane / 2];
+        st_row = uniform64(st_row + n);
+        st_left = __builtin_amdgcn_readfirstlane(st_left - n);
+        s.last = st_left == 0 && st_more == 0;
+        return s;
+    };
+
+    if (item_first < item_last) prefetch_centre(item_first);
+    Stage s0 = next_stage(); // chunk k (contraction)
+    Stage s1 = next_stage(); // chunk k + 1 (harmonics)
+    double px = 0.0, py = 0.0, pz = 0.0;
+    const int jj = lane / 2, comp = lane % 2;
+    auto load_positions = [&](const Stage& s) {
+        if (jj < s.rows) {
+            px = a.bx[s.bin];
+            py = a.by[s.bin];
+            pz = a.bz[s.bin];
+        }
+    };
+    // harmonics of a stage's slots from the centre position (cx, cy, cz)
+    auto harmonics = [&](const Stage& s, int buf, double cx, double cy, double cz) {
+        const double dx = px - cx, dy = py - cy, dz = pz - cz;
+        const bool real = jj < s.rows;
+        if constexpr (W == 0) {
+            // a pad slot's position is stale (a row of an earlier chunk,
+            // possibly of another structure): it enters the exp as d2 = 0
+            const double d2 = fma(dz, dz, fma(dx, dx, dy * dy));
+            if (comp == 0) s_d2[buf * kNb + jj] = real ? d2 : 0.0;
+        }
+        harmonic_columns<LM, MLO, MHI>(dx, dy, dz, real ? 1.0 : 0.0, comp, s_y + buf * PL::YWORDS + jj);
+    };
+
+    // prologue: harmonics of the first chunk
+    load_positions(s0);
+    if (uniform64(s0.centre) >= 0) {
+        const int64_t c = uniform64(s0.centre);
+        harmonics(s0, 0, a.positions[3 * c], a.positions[3 * c + 1], a.positions[3 * c + 2]);
+    }
+    load_positions(s1);
+    __syncthreads();
+
+    // accumulators and coefficient registers
+    double acc[NU][RPL];
+    double C[NU][NCR];
+    unroll<NU>([&](auto u) {
+        unroll<RPL>([&](auto r) { acc[decltype(u)::value][decltype(r)::value] = 0.0; });
+        unroll<NCR>([&](auto r) { C[decltype(u)::value][decltype(r)::value] = 0.0; });
+    });
+    int cur = -1; // species of the accumulators
+
+    // sum the phases of every accumulator and add species q's radial groups
+    // into its block slots of the coefficient registers
+    auto merge = [&](int q) {
+        unroll<NU>([&](auto uc) {
+            constexpr int u = decltype(uc)::value;
+            unroll<RPL>([&](auto rc) {
+                constexpr int rr = decltype(rc)::value;
+                double v = acc[u][rr];
+                v += row_rotate<8>(v);
+                if constexpr (P == 4) v += row_rotate<4>(v);
+                acc[u][rr] = 0.0;
+                if constexpr (KG == 2) {
+                    // groups 2q, 2q + 1: register q / 2, slots {0,1} or {2,3}
+                    const bool mine = low_pair == ((q & 1) == 0);
+                    unroll<NCR>([&](auto r) {
+                        if (decltype(r)::value == (q >> 1)) C[u][decltype(r)::value] += mine ? v : 0.0;
+                    });
+                } else if constexpr (KG == 1) {
+                    const bool mine = blk == (q & 3);
+                    unroll<NCR>([&](auto r) {
+                        if (decltype(r)::value == (q >> 2)) C[u][decltype(r)::value] += mine ? v : 0.0;
+                    });
+                } else {
+                    const bool mine = blk == rr;
+                    unroll<NCR>([&](auto r) {
+                        if (decltype(r)::value == q) C[u][decltype(r)::value] += mine ? v : 0.0;
+                    });
+                }
+            });
+        });
+    };
+
+    const int64_t F = a.F;
+    const int esize = a.out_dtype;
+    int k = 0;
+    while (uniform64(s0.centre) >= 0) {
+        const int buf = k & 1;
+        // wave-uniform facts of chunk k, in scalar registers
+        const int groups0 = __builtin_amdgcn_readfirstlane(s0.groups);
+        const bool last0 = __builtin_amdgcn_readfirstlane(s0.last ? 1 : 0) != 0;
+        const int64_t centre0 = uniform64(s0.centre);
+        const int q0 = __builtin_amdgcn_readfirstlane(s0.q);
+        // centre position of chunk k + 1 (scalar loads, used after the contraction)
+        const int64_t centre1 = uniform64(s1.centre);
+        const int64_t cpos1 = 3 * (centre1 >= 0 ? centre1 : 0);
+        const double cx1 = a.positions[cpos1], cy1 = a.positions[cpos1 + 1], cz1 = a.positions[cpos1 + 2];
+        // positions of chunk k + 1 in flight; bins of chunk k + 2
+        Stage s2 = next_stage();
+        // ------------------------------------------------ contraction of chunk k
+        {
+            const int prev = __builtin_amdgcn_readfirstlane(cur);
+            if (q0 != prev) {
+                if (prev >= 0) merge(prev);
+                cur = q0;
+            }
+            const double* ybuf = s_y + buf * PL::YWORDS + yread;
+            const double* dbuf = s_d2 + buf * kNb + dread;
+            unroll<GROUPS>([&](auto gc) {
+                constexpr int g = decltype(gc)::value;
+                if (g >= groups0) return;
+                const double d2 = dbuf[GS * g];
+                double ev[ND][RPL];
+                unroll<ND>([&](auto dc) {
+                    unroll<RPL>([&](auto rc) {
+                        ev[decltype(dc)::value][decltype(rc)::value] =
+                            exp_neg(d2, e1[decltype(dc)::value][decltype(rc)::value], s_tab);
+                    });
+                });
+                unroll<L>([&](auto lc) {
+                    constexpr int l = decltype(lc)::value;
+                    if constexpr ((kOwn >> l) & 1u) {
+                        constexpr int d = degrees_before(kOwn, l);
+                        constexpr int u0 = units_before(kOwn, l);
+                        unroll<cgroups(l)>([&](auto cc) {
+                            constexpr int cg = decltype(cc)::value;
+                            const double y = ybuf[(l * l + 4 * cg) * kYS + GS * g];
+                            unroll<RPL>([&](auto rc) {
+                                constexpr int rr = decltype(rc)::value;
+                                acc[u0 + cg][rr] = mfma4(ev[d][rr], y, acc[u0 + cg][rr]);
+                            });
+                        });
+                    }
+                });
+            });
+        }
+        // ------------------------------------ centre end: fold, power spectrum
+        if (last0) {
+            merge(__builtin_amdgcn_readfirstlane(cur));
+            cur = -1;
+            // fold: C <- (S_lm C)^T beta^T in place
+            unroll<L>([&](auto lc) {
+                constexpr int l = decltype(lc)::value;
+                if constexpr ((kOwn >> l) & 1u) {
+                    constexpr int d = degrees_before(kOwn, l);
+                    constexpr int u0 = units_before(kOwn, l);
+                    constexpr int loff = 4 * units_before(0xffffffffu, l);
+                    unroll<cgroups(l)>([&](auto cc) {
+                        constexpr int cg = decltype(cc)::value;
+                        const double sc = s_scale[loff + 4 * cg + lane % 4];
+                        unroll<NCR>([&](auto rc) {
+                            constexpr int r = decltype(rc)::value;
+                            const double v = C[u0 + cg][r] * sc;
+                            double c = mfma4(v, bt[d][0], 0.0);
+                            if constexpr (KG == 2) {
+                                c = mfma4(swap_blocks(v), bt[d][1], c);
+                            } else if constexpr (KG == 3) {
+                                c = mfma4(row_rotate<12>(v), bt[d][1], c); // block b takes b + 1
+                                c = mfma4(row_rotate<8>(v), bt[d][2], c);  // b + 2
+                                c = mfma4(row_rotate<4>(v), bt[d][3], c);  // b + 3
+                            }
+                            C[u0 + cg][r] = c;
+                        });
+                    });
+                }
+            });
+            // power spectrum of the owned degrees, written to the centre's row
+            char* row = static_cast<char*>(a.out) + centre0 * a.pitch;
+            const __amdgpu_buffer_rsrc_t rsrc =
+                __builtin_amdgcn_make_buffer_rsrc(row, 0, static_cast<int>(F * esize), 0x00020000);
+            int pair = 0;
+            unroll<NCR>([&](auto ic) {
+                constexpr int ri = decltype(ic)::value;
+                unroll<NCR>([&](auto jc) {
+                    constexpr int rj = decltype(jc)::value;
+                    if constexpr (ri <= rj) {
+                        int fb[4], fs[4];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int2 o = a.ps_offsets[((pair * 4 + r) * kWaveThreads) + lane];
+                            fb[r] = o.x * esize;
+                            fs[r] = o.y * esize;
+                        }
+                        unroll<L>([&](auto lc) {
+                            constexpr int l = decltype(lc)::value;
+                            if constexpr ((kOwn >> l) & 1u) {
+                                constexpr int u0 = units_before(kOwn, l);
+                                d4 D = {0.0, 0.0, 0.0, 0.0};
+                                unroll<cgroups(l)>([&](auto cc) {
+                                    constexpr int cg = decltype(cc)::value;
+                                    D = mfma(C[u0 + cg][ri], C[u0 + cg][rj], D);
+                                });
+                                const double pref = a.ps_pref[l];
+#pragma unroll
+                                for (int r = 0; r < 4; ++r) {
+                                    const double v = pref * D[r];
+                                    const int off = fb[r] + l * fs[r];
+                                    if (esize == 4) {
+                                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(static_cast<float>(v)), rsrc,
+                                                                              off, 0, 0);
+                                    } else {
+                                        typedef int i2v __attribute__((ext_vector_type(2)));
+                                        const i2v bits = {__double2loint(v), __double2hiint(v)};
+                                        __builtin_amdgcn_raw_buffer_store_b64(bits, rsrc, off, 0, 0);
+                                    }
+                                }
+                            }
+                        });
+                        ++pair;
+                    }
+                });
+            });
+            unroll<NU>([&](auto u) { unroll<NCR>([&](auto r) { C[decltype(u)::value][decltype(r)::value] = 0.0; }); });
+        }
+        // ---------------------------------------- harmonics of chunk k + 1
+        if (centre1 >= 0) harmonics(s1, buf ^ 1, cx1, cy1, cz1);
+        load_positions(s2);
+        s0 = s1;
+        s1 = s2;
+        ++k;
+        __syncthreads();
+    }
+}
+
+template <int LM, int KG, int NCR>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_soap_block(BlockArgs a) {
+    using PL = BlockPlan<LM, KG>;
+    extern __shared__ double lds[];
+    const int tid = threadIdx.x;
+    const int threads = static_cast<int>(blockDim.x);
+    double* s_y = lds;
+    double* s_d2 = s_y + 2 * PL::YWORDS;
+    int2* s_tab = reinterpret_cast<int2*>(s_d2 + 2 * kNb);
+    double* s_scale = s_d2 + 2 * kNb + kTab;
+    // pad rows of both staging buffers stay finite (zero); the scaled
+    // harmonics table and the exp table
+    for (int i = tid; i < 2 * 3 * kYS; i += threads) {
+        const int b = i / (3 * kYS), e = i - b * 3 * kYS;
+        s_y[b * PL::YWORDS + PL::H * kYS + e] = 0.0;
+    }
+    for (int i = tid; i < kTab; i += threads) {
+        const double t = exp2(static_cast<double>(i) / kTab);
+        s_tab[i] = int2{__double2loint(t), __double2hiint(t) - (i << 14)};
+    }
+    {
+        // S_lm of padded column i (degree l's block at 4 sum_{l' < l} cg(l'),
+        // 4 cg(l) wide; 0 past 2l)
+        constexpr int kPad = 4 * units_before(0xffffffffu, PL::L);
+        for (int i = tid; i < kPad; i += threads) {
+            int l = 0, off = 0;
+            while (l + 1 < PL::L && off + 4 * cgroups(l) <= i) {
+                off += 4 * cgroups(l);
+                ++l;
+            }
+            const int c = i - off;
+            s_scale[i] = c <= 2 * l ? kScaledHarmonic.s[l][c <= l ? l - c : c - l] : 0.0;
+        }
+    }
+    __syncthreads();
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWaveThreads);
+    if (wave == 0) {
+        block_role<LM, KG, NCR, 0>(a, lds);
+    } else if constexpr (PL::T > 1) {
+        if (wave == 1) {
+            block_role<LM, KG, NCR, (PL::T > 1 ? 1 : 0)>(a, lds);
+        } else if constexpr (PL::T > 2) {
+            if (wave == 2) {
+                block_role<LM, KG, NCR, (PL::T > 2 ? 2 : 0)>(a, lds);
+            } else if constexpr (PL::T > 3) {
+                block_role<LM, KG, NCR, (PL::T > 3 ? 3 : 0)>(a, lds);
+            }
+        }
+    }
+}
+
+template <int LM, int KG, int NCR>
+size_t lds_bytes() {
+    using PL = BlockPlan<LM, KG>;
+    return (2 * PL::YWORDS + 2 * kNb + kTab + 4 * units_before(0xffffffffu, PL::L)) * sizeof(double);
+}
+
+template <int LM, int KG, int NCR>
+void launch_shape(hipStream_t stream, const BlockArgs& a, int64_t count) {
+    using PL = BlockPlan<LM, KG>;
+    const size_t lds = lds_bytes<LM, KG, NCR>();
+    const int64_t resident = std::max<int64_t>(1, std::min<int64_t>(8, (160 * 1024) / std::max<size_t>(lds, 1)));
+    const int64_t target = std::max<int64_t>(1, 8 * resident * device_compute_units());
+    BlockArgs args = a;
+    args.per_block = std::max<int64_t>(1, (count + target - 1) / target);
+    const unsigned grid = static_cast<unsigned>((count + args.per_block - 1) / args.per_block);
+    hipLaunchKernelGGL((k_soap_block<LM, KG, NCR>), dim3(grid), dim3(PL::T * kWaveThreads), lds, stream, args);
+}
+
+using Launcher = void (*)(hipStream_t, const BlockArgs&, int64_t);
+
+// the shapes compiled: (l_max, radial groups, coefficient registers)
+struct ShapeEntry {
+    int l_max, kg, ncr;
+    Launcher launch;
+    int waves;
+};
+#define MDX_BLOCK_SHAPE(LM, KG, NCR) {LM, KG, NCR, &launch_shape<LM, KG, NCR>, BlockPlan<LM, KG>::T}
+const ShapeEntry kShapes[] = {
+    MDX_BLOCK_SHAPE(6, 2, 2),
+};
+#undef MDX_BLOCK_SHAPE
+
+const ShapeEntry* find_shape(int l_max, int kg, int ncr) {
+    for (const ShapeEntry& e : kShapes)
+        if (e.l_max == l_max && e.kg == kg && e.ncr == ncr) return &e;
+    return nullptr;
+}
+
+int coefficient_registers(int S, int kg) { return kg == 3 ? S : (S * kg + 3) / 4; }
+
+} // namespace
+
+bool block_plan_tables(int S, int n, int l_max, const std::vector<double>& beta_scaled, const std::vector<double>& pref,
+                       const std::vector<double>& expo, BlockPlanHost& out) {
+    out = BlockPlanHost{};
+    const int kg = (n + 3) / 4;
+    if (n < 1 || kg > 3 || (kg == 3 && S != 1)) return false;
+    const int ncr = coefficient_registers(S, kg);
+    const ShapeEntry* e = find_shape(l_max, kg, ncr);
+    if (e == nullptr) return false;
+    const int L = l_max + 1;
+    const int R = kg == 2 ? 2 : 1;
+    const int RPL = kg / R;
+    const int NT = kg == 1 ? 1 : kg == 2 ? 2 : 4;
+    const long double kScale = 64.0L / 0.693147180559945309417232121458176568L;
+    auto beta = [&](int l, int np, int k) -> double {
+        if (np >= n || k >= n || np < 0 || k < 0) return 0.0;
+        return beta_scaled[static_cast<size_t>((l * n + np) * n + k)] * pref[static_cast<size_t>(l * n + k)];
+    };
+    out.lane_e1.assign(static_cast<size_t>(L) * RPL * 64, 0.0);
+    out.lane_beta.assign(static_cast<size_t>(L) * NT * 64, 0.0);
+    for (int l = 0; l < L; ++l) {
+        for (int lane = 0; lane < 64; ++lane) {
+            const int b = (lane / 4) % 4;
+            for (int rr = 0; rr < RPL; ++rr) {
+                const int rg = rr * R + b % R;
+                const int k = 4 * rg + lane % 4;
+                out.lane_e1[static_cast<size_t>((l * RPL + rr) * 64 + lane)] =
+                    k < n ? static_cast<double>(-static_cast<long double>(expo[static_cast<size_t>(l * n + k)]) * kScale)
+                          : 0.0;
+            }
+            // beta^T operand: lane = beta^T[k = lane / 16][n' = lane % 4] of the
+            // fold term's (radial group in -> radial group out) block
+            for (int t = 0; t < NT; ++t) {
+                double v = 0.0;
+                if (kg == 1) {
+                    v = beta(l, lane % 4, lane / 16);
+                } else if (kg == 2) {
+                    const int rg = b % 2;
+                    const int rin = t == 0 ? rg : 1 - rg;
+                    v = beta(l, 4 * rg + lane % 4, 4 * rin + lane / 16);
+                } else {
+                    const int rin = (b + t) % 4;
+                    if (b < 3 && rin < 3) v = beta(l, 4 * b + lane % 4, 4 * rin + lane / 16);
+                }
+                out.lane_beta[static_cast<size_t>((l * NT + t) * 64 + lane)] = v;
+            }
+        }
+    }
+    // power-spectrum offsets: tile pair p = (ri <= rj), value r, lane: feature
+    // index at l = 0 and its stride per degree for channel i (group 4 ri + r,
+    // radial channel 4 rg + lane / 16) and channel j (group 4 rj + (lane % 16) / 4,
+    // 4 rg + lane % 4); pairs i > j and pad channels get kDropped
+    const int W = S * n;
+    auto channel = [&](int ri, int slot, int nl) -> int {
+        int t = 0, rg = 0;
+        if (kg == 3) {
+            t = ri;
+            rg = slot;
+            if (slot >= 3) return -1;
+        } else {
+            const int g = 4 * ri + slot;
+            t = g / kg;
+            rg = g % kg;
+        }
+        const int np = 4 * rg + nl;
+        if (t >= S || np >= n) return -1;
+        return t * n + np;
+    };
+    // feature index of channel pair (i, j), i <= j (soap.cpp:997-1013)
+    auto feature = [&](int i, int j, int& stride) -> int {
+        const int t1 = i / n, n1 = i % n, t2 = j / n, n2 = j % n;
+        int base = 0;
+        for (int a1 = 0; a1 < S; ++a1) {
+            for (int a2 = a1; a2 < S; ++a2) {
+                const int size = a1 == a2 ? n * (n + 1) / 2 : n * n;
+                if (a1 == t1 && a2 == t2) {
+                    stride = size;
+                    return base + (t1 == t2 ? n1 * n - n1 * (n1 - 1) / 2 + (n2 - n1) : n1 * n + n2);
+                }
+                base += L * size;
+            }
+        }
+        return -1;
+    };
+    for (int ri = 0; ri < ncr; ++ri) {
+        for (int rj = ri; rj < ncr; ++rj) {
+            for (int r = 0; r < 4; ++r) {
+                for (int lane = 0; lane < 64; ++lane) {
+                    const int i = channel(ri, r, lane / 16);
+                    const int j = channel(rj, (lane % 16) / 4, lane % 4);
+                    int fb = kDropped / 8, fs = 0;
+                    if (i >= 0 && j >= 0 && i <= j) fb = feature(i, j, fs);
+                    out.ps_offsets.push_back(fb);
+                    out.ps_offsets.push_back(fs);
+                }
+            }
+        }
+    }
+    (void)W;
+    out.kg = kg;
+    out.ncr = ncr;
+    out.waves = e->waves;
+    return true;
+}
+
+size_t block_lds_bytes(int l_max, int kg) {
+    const int L = l_max + 1, H = L * L;
+    int pad = 0;
+    for (int l = 0; l < L; ++l) pad += 4 * cgroups(l);
+    return static_cast<size_t>(2 * (H + 3) * kYS + 2 * kNb + kTab + pad) * sizeof(double);
+    (void)kg;
+}
+
+void launch_block_expand(hipStream_t stream, int l_max, int kg, int ncr, const BlockArgs& a, int64_t count) {
+    if (count <= 0) return;
+    const ShapeEntry* e = find_shape(l_max, kg, ncr);
+    if (e == nullptr) throw Error(MDX_INTERNAL, "SOAP shape is not compiled for the register-coefficient kernel");
+    e->launch(stream, a, count);
+    MDX_HIP(hipGetLastError());
+}
+
+} // namespace mdx

@@ -77,16 +77,18 @@ int mfma_template_tiles(int tiles);
 // (at most two radial groups of 4 channels), l_max <= kQuadLmax, at most
 // kQuadMaxWaves wavefronts and kQuadG MFMA instructions per wavefront and step.
 constexpr int kQuadG = 4;
-// smallest radial exponent argument -a d^2 the kernel's exp accepts
-constexpr double kQuadMinArgument = -5.0e6;
+// smallest radial exponent argument -a d^2 the kernel's exp accepts (its
+// result must be a normal number)
+constexpr double kQuadMinArgument = -700.0;
 constexpr int kQuadLmax = 10;
 constexpr int kQuadMaxWaves = 8;
 // rows of one centre the kernel's slot codes hold (row * 16 + species in 32 bits)
 constexpr int64_t kQuadMaxRows = int64_t(1) << 27;
 
 // Constants of one lane of one wavefront of the 4x4-block kernel.
-//   expo     radial exponent a_lk of the lane's A-operand row (k = 4 group +
-//            lane % 4 of its block's unit), 0 for pad rows and idle blocks
+//   exp_scale  -a_lk 64/ln2 for the radial exponent a_lk of the lane's
+//            A-operand row (k = 4 group + lane % 4 of its block's unit), 0 for
+//            pad rows and idle blocks
 //   beta_r   beta-fold A operand for the block's own accumulator:
 //            pi^1.5 beta[l][n'][k] pref[l][k], n' = 4 group + lane % 4,
 //            k = 4 group + lane / 16
@@ -98,7 +100,7 @@ constexpr int64_t kQuadMaxRows = int64_t(1) << 27;
 //            output for g = 0, + 4 g for instruction g; -1: not stored
 //   cnt      instructions in which the lane's block is active
 struct QuadLane {
-    double expo = 0.0, beta_r = 0.0, beta_s = 0.0;
+    double exp_scale = 0.0, beta_r = 0.0, beta_s = 0.0;
     int32_t ycol[kQuadG] = {};
     int32_t cdst = -1, cnt = 0;
 };

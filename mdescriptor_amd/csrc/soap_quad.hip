@@ -51,30 +51,40 @@ __device__ inline double half_mirror(double v) {
     return __hiloint2double(hi, lo);
 }
 
-// exp(x) for x <= 0 by the table-driven method of P. T. P. Tang (ACM TOMS
-// 15(2), 1989): x = (64k + j) ln2/64 + r, |r| <= ln2/128,
-// exp(x) = 2^k 2^(j/64) e^r, e^r - 1 by its degree-5 Taylor polynomial
-// (truncation below 4e-17 relative).  Within 2 ulp of libm over [-745, 0],
-// subnormal results included; exact 0 below.  The integer 64k must fit 32
-// bits: x >= -5.8e6, which the host checks for every plan that runs this
-// kernel (kQuadMinArgument).  tab[j] = 2^(j/64).
-__device__ inline double exp_neg64(double x, const double* tab) {
-    constexpr double kInvLn2x64 = 92.332482616893658071035179584121; // 64 / ln 2
-    constexpr double kHi = 0.010830417275428772;                      // ln2/64, 32 trailing zero bits
-    constexpr double kLo = 7.420820373486988e-09;                     // ln2/64 - kHi
-    constexpr double kShifter = 6755399441055744.0;                   // 1.5 * 2^52
-    const double s = fma(x, kInvLn2x64, kShifter);
+// exp(-a d2) for d2 >= 0, given e1 = -a 64/ln2, by the table-driven method
+// of P. T. P. Tang (ACM TOMS 15(2), 1989) with the argument reduction done
+// on the product: y = d2 e1 = 64k + j + rs, |rs| <= 1/2, and
+// exp(-a d2) = 2^k 2^(j/64) e^r with r = rs ln2/64; e^r - 1 by its degree-5
+// Taylor polynomial in rs (truncation below 4e-17 relative).  rs comes from
+// one fused multiply-add, d2 e1 - (64k + j), so its only rounding is that of
+// e1: the result is within 5e-15 relative of exp(-a d2) for -a d2 >= -40 and
+// as close as libm's exp of the rounded product -a * d2 further out.
+//
+// The table holds 2^(j/64) with (j << 14) taken off its high word, so that
+// adding n << 14 (n = 64k + j, the low word of the shifted y) to that word
+// multiplies by 2^k and restores the mantissa in one integer add.  The
+// result must be a normal number: -a d2 >= -708, which the host checks for
+// every plan that runs this kernel (kQuadMinArgument).
+constexpr double kExpC1 = 0.693147180559945309417232121458176568 / 64.0; // ln2/64
+constexpr double kExpC2 = kExpC1 * kExpC1 / 2.0;
+constexpr double kExpC3 = kExpC2 * kExpC1 / 3.0;
+constexpr double kExpC4 = kExpC3 * kExpC1 / 4.0;
+constexpr double kExpC5 = kExpC4 * kExpC1 / 5.0;
+constexpr double kExpScale = 64.0 / 0.693147180559945309417232121458176568; // e1 = -a * kExpScale
+__device__ __forceinline__ double exp_neg_scaled(double d2, double e1, const int2* tab) {
+    constexpr double kShifter = 6755399441055744.0; // 1.5 * 2^52
+    const double s = fma(d2, e1, kShifter);
     const double kf = s - kShifter;
-    double r = fma(kf, -kHi, x);
-    r = fma(kf, -kLo, r);
-    const int ki = __double2loint(s);
-    double q = fma(r, 1.0 / 120.0, 1.0 / 24.0);
-    q = fma(q, r, 1.0 / 6.0);
-    q = fma(q, r, 0.5);
-    q = fma(q, r, 1.0);
-    const double em1 = r * q; // e^r - 1
-    const double t = tab[ki & (kQuadTab - 1)];
-    return ldexp(fma(t, em1, t), ki >> 6);
+    const double rs = fma(d2, e1, -kf);
+    const int nj = __double2loint(s);
+    const int2 t = *reinterpret_cast<const int2*>(reinterpret_cast<const char*>(tab) + ((nj << 3) & 0x1f8));
+    double q = fma(kExpC5, rs, kExpC4);
+    q = fma(q, rs, kExpC3);
+    q = fma(q, rs, kExpC2);
+    q = fma(q, rs, kExpC1);
+    const double em1 = q * rs; // e^r - 1
+    const double tk = __hiloint2double(t.y + (nj << 14), t.x); // 2^k 2^(j/64)
+    return fma(tk, em1, tk);
 }
 
 // Byte offset that no output row reaches: a buffer store there is dropped by
@@ -204,22 +214,33 @@ void k_soap_quad(
     extern __shared__ double lds[];
     const int tid = threadIdx.x;
     const int lane = tid % kWaveThreads;
-    const int wave = __builtin_amdgcn_readfirstlane(tid / kWaveThreads);
     const int kThreads = static_cast<int>(blockDim.x);
     const int T = kThreads / kWaveThreads;
+    // The plan's wavefront roles carry unequal work (MFMA instructions per
+    // step differ).  Wavefront w of every workgroup tends to land on the same
+    // SIMD of a CU, so the roles rotate with the workgroup index: the
+    // workgroups sharing a CU spread each role over its SIMDs.
+#ifndef MDX_QUAD_ROTATE
+#define MDX_QUAD_ROTATE 1
+#endif
+    const int wave = __builtin_amdgcn_readfirstlane(MDX_QUAD_ROTATE ? (tid / kWaveThreads + static_cast<int>(blockIdx.x)) % T
+                                                                    : tid / kWaveThreads);
     const int H = d.H, L = d.L, S = d.S, n = d.n;
     const int hp = d.hpad;          // padded c row
     const int cp = d.cpitch;        // its LDS pitch (odd)
     const int cw = d.crow * cp;     // c words (a zero row last unless S*n is a multiple of 16)
     double* s_y = lds;              // H * kYStride, harmonic-major
     double* s_d2 = s_y + H * kYStride; // kNb
-    double* s_tab = s_d2 + kNb;     // kQuadTab
-    double* s_c = s_tab + kQuadTab; // cw
+    int2* s_tab = reinterpret_cast<int2*>(s_d2 + kNb); // kQuadTab biased 2^(j/64), see exp_neg_scaled
+    double* s_c = s_d2 + kNb + kQuadTab; // cw
     double* s_scale = s_c + cw;     // hp: S_lm of each padded column (scaled harmonics)
     double* s_csum = s_scale + hp;  // cw (inner average only)
     int* s_loff = reinterpret_cast<int*>(s_csum + (d.mode == 1 ? cw : 0)); // L + 1
 
-    for (int i = tid; i < kQuadTab; i += kThreads) s_tab[i] = exp2(static_cast<double>(i) / kQuadTab);
+    for (int i = tid; i < kQuadTab; i += kThreads) {
+        const double t = exp2(static_cast<double>(i) / kQuadTab);
+        s_tab[i] = int2{__double2loint(t), __double2hiint(t) - (i << 14)};
+    }
     for (int i = tid; i < cw; i += kThreads) s_c[i] = 0.0;
     for (int i = tid; i < hp; i += kThreads) {
         // column i of the padded row: degree l block at loff[l], 4 ceil((2l+1)/4) wide
@@ -241,7 +262,7 @@ void k_soap_quad(
     __syncthreads();
     // this lane's constants (see QuadLane)
     const QuadLane& ql = lanes[wave * kWaveThreads + lane];
-    const double expo = ql.expo;
+    const double e1 = ql.exp_scale;
     const double beta_r = ql.beta_r;
     const double beta_s = KG == 2 ? ql.beta_s : 0.0;
     // the lane's harmonic row of each instruction at its step's first slot
@@ -405,7 +426,7 @@ void k_soap_quad(
 #pragma unroll
                 for (int s = 0; s < 2; ++s) {
                     const int jj = 4 * (h + s) + krow;
-                    ev[s] = exp_neg64(-expo * s_d2[jj], s_tab);
+                    ev[s] = exp_neg_scaled(s_d2[jj], e1, s_tab);
 #pragma unroll
                     for (int g = 0; g < G; ++g) yv[s][g] = yrow[g][4 * (h + s)];
                 }
@@ -421,7 +442,7 @@ void k_soap_quad(
                     double ev[2], yv[2][GW];
 #pragma unroll
                     for (int s = 0; s < 2; ++s) {
-                        ev[s] = exp_neg64(-expo * s_d2[4 * (h + s) + krow], s_tab);
+                        ev[s] = exp_neg_scaled(s_d2[4 * (h + s) + krow], e1, s_tab);
 #pragma unroll
                         for (int g = 0; g < GW; ++g) yv[s][g] = yrow[g][4 * (h + s)];
                     }
@@ -489,7 +510,10 @@ void k_soap_quad(
                     const double dz = pz - cz;
                     const double d2 = dx * dx + dy * dy + dz * dz;
                     const double scale = pcode >= 0 ? 1.0 : 0.0;
-                    if (wave == 0 && comp == 0) s_d2[jj] = d2;
+                    // a pad slot's position is stale (an earlier row, possibly of
+                    // another structure): its d2 is unbounded, so it enters the
+                    // exp as 0 (its harmonics are zero)
+                    if (wave == 0 && comp == 0) s_d2[jj] = pcode >= 0 ? d2 : 0.0;
                     // species of the 8 steps, 4 bits each, from the first slot
                     // of each step (lane 8 h; never a pad slot within the rows)
                     const int pq = pcode & 15;
@@ -672,7 +696,10 @@ QuadPlanHost plan_quad_tables(int n, int l_max, int hpad, const std::vector<doub
             const bool reversed = KG == 2 && (b % 2) == 1;
             // A operand (exp): row lane % 4 of radial group grp
             const int k = 4 * grp + lane % 4;
-            q.expo = k < n ? expo[static_cast<size_t>(u.l * n + k)] : 0.0;
+            // exp_neg_scaled's e1 = -a 64/ln2, rounded once from a long double product
+            q.exp_scale = k < n ? static_cast<double>(-static_cast<long double>(expo[static_cast<size_t>(u.l * n + k)])
+                                                      * (64.0L / 0.693147180559945309417232121458176568L))
+                                : 0.0;
             // B operand (harmonics): column lane % 4 of column group g0 + g
             const int col = lane % 4;
             const int mcol = reversed ? 3 - col : col;

@@ -78,24 +78,28 @@ def test_soap_matches_oracle(hip_context, oracle, workload, average, dtype):
     _check(hip_context, oracle, workload.batch, workload.params, average, dtype)
 
 
-@pytest.mark.parametrize("kernel", ["generic", "mfma", "quad"])
+@pytest.mark.parametrize("kernel", ["generic", "mfma", "quad", "block"])
 def test_every_expansion_kernel_matches(hip_context, oracle, monkeypatch, kernel):
-    """The plan picks the 4x4-block kernel for the default options where it
-    fits (n_max <= 8), else the 16x16-tile kernel, with the generic kernel as
-    the last fallback.  Each stays parity-green when forced."""
+    """The plan picks the register-coefficient kernel for the default options
+    and atom-level rows where its shape is compiled, else the 4x4-block kernel
+    where it fits (n_max <= 8), else the 16x16-tile kernel, with the generic
+    kernel as the last fallback.  Each stays parity-green when forced."""
 
     monkeypatch.setenv("MDX_HIP_SOAP_KERNEL", kernel)
     work = workloads.config(2, "small")
-    for average in ("off", "inner", "outer"):
+    for average in ("off",) if kernel == "block" else ("off", "inner", "outer"):
         _, timing = _check(hip_context, oracle, work.batch, work.params, average, "float64")
         tiles = timing["expansion_tiles"]
-        assert (tiles < 0) if kernel == "quad" else (tiles > 0) if kernel == "mfma" else tiles == 0
+        expected = {"block": tiles <= -1000, "quad": -1000 < tiles < 0, "mfma": tiles > 0, "generic": tiles == 0}
+        assert expected[kernel], tiles
 
 
-def test_default_plan_runs_the_quad_kernel(hip_context, oracle):
+def test_default_plan_runs_the_block_kernel(hip_context, oracle):
     work = workloads.config(2, "small")
-    _, timing = _check(hip_context, oracle, work.batch, work.params, "off", "float32")
-    assert timing["expansion_tiles"] == -4  # four wavefronts of 4x4x4 blocks for n_max 8, l_max 6
+    for average, tiles in (("off", -1004), ("outer", -4)):
+        _, timing = _check(hip_context, oracle, work.batch, work.params, average, "float32")
+        # four wavefronts for n_max 8, l_max 6; averaged rows on the 4x4-block kernel
+        assert timing["expansion_tiles"] == tiles
 
 
 def _random_cluster(seed, atoms, species):
