@@ -613,7 +613,7 @@ int mdx_hip_soap_plan_create(mdx_hip_ctx* ctx, const mdx_soap_params* params, md
             // a compiled (l_max, radial groups, species) shape
             if (plan->use_mfma && defaults && quad_range && p.average == 0 && (choice == "auto" || choice == "block")) {
                 mdx::BlockPlanHost bp;
-                if (mdx::block_plan_tables(plan->S, n, p.l_max, beta, pref, expo, bp)) {
+                if (mdx::block_plan_tables(plan->S, n, p.l_max, p.out_dtype, beta, pref, expo, bp)) {
                     plan->block_waves = bp.waves;
                     plan->block_kg = bp.kg;
                     plan->block_ncr = bp.ncr;

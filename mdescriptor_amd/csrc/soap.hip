@@ -475,8 +475,7 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
                 ba.bz = g.bin_z.as<double>();
                 ba.lane_e1 = p.d_block_e1.as<double>();
                 ba.lane_beta = p.d_block_beta.as<double>();
-                ba.ps_offsets = p.d_block_ps.as<int2>();
-                ba.ps_pref = tab.ps_pref;
+                ba.ps_offsets = p.d_block_ps.as<int32_t>();
                 ba.S = p.S;
                 ba.out_dtype = p.out_dtype;
                 ba.F = p.features;

@@ -18,8 +18,7 @@ struct BlockArgs {
     const double* bz;
     const double* lane_e1;      // [l][register][64]: -a_lk 64/ln2 of the lane's exp row, 0 for pad rows
     const double* lane_beta;    // [l][fold term][64]: beta^T operand of the lane
-    const int2* ps_offsets;     // [tile pair][value][64]: feature index at l = 0 and its stride per l
-    const double* ps_pref;      // [L]: pi sqrt(8/(2l+1))
+    const int32_t* ps_offsets;  // [tile pair][value][64]: (byte offset at l = 0) << 9 | feature stride per l
     int S;                      // species
     int out_dtype;              // 4 or 8 bytes
     int64_t F;                  // features per row
@@ -36,12 +35,12 @@ struct BlockPlanHost {
     int ncr = 0;     // coefficient registers per (l, column group)
     int waves = 0;   // wavefronts per workgroup
     std::vector<double> lane_e1, lane_beta;
-    std::vector<int32_t> ps_offsets; // int2 pairs
+    std::vector<int32_t> ps_offsets; // packed feature offsets
 };
 
 // Fills out and returns true when (S, n, l_max) is one of the compiled shapes.
-bool block_plan_tables(int S, int n, int l_max, const std::vector<double>& beta_scaled, const std::vector<double>& pref,
-                       const std::vector<double>& expo, BlockPlanHost& out);
+bool block_plan_tables(int S, int n, int l_max, int out_dtype, const std::vector<double>& beta_scaled,
+                       const std::vector<double>& pref, const std::vector<double>& expo, BlockPlanHost& out);
 size_t block_lds_bytes(int l_max, int kg);
 void launch_block_expand(hipStream_t stream, int l_max, int kg, int ncr, const BlockArgs& a, int64_t count);
 

@@ -61,7 +61,27 @@ namespace {
 
 constexpr int kYS = kNb + 1;       // harmonic staging: entry h of slot j at h * kYS + j
 constexpr int kTab = 64;           // 2^(j/64) table entries
-constexpr int kDropped = 0x40000000; // byte offset no output row reaches (buffer range check drops it)
+// Power-spectrum feature offsets are packed as (byte offset << 9) | feature
+// stride per degree; a pair that is not stored gets kDroppedBytes, past the
+// end of every row this kernel writes (the buffer range check drops the
+// store).  Rows must be shorter than kDroppedBytes (checked on the host).
+constexpr int kStrideBits = 9;
+constexpr int kDroppedBytes = (1 << 22) - 1;
+
+// square root of pi sqrt(8 / (2l + 1)), the power-spectrum prefactor
+// (soap.cpp:513-516): each coefficient carries it, so the Gram product of two
+// coefficient rows carries the prefactor
+struct PsRoots {
+    double v[kHarmonicLmax + 1];
+};
+constexpr PsRoots make_ps_roots() {
+    PsRoots r{};
+    for (int l = 0; l <= kHarmonicLmax; ++l)
+        r.v[l] = detail::ct_sqrt(3.141592653589793238462643383279502884 * detail::ct_sqrt(8.0 / (2.0 * l + 1.0)));
+    return r;
+}
+__device__ constexpr PsRoots kPsRootTable = make_ps_roots();
+#define kPsRoot kPsRootTable.v
 
 // ---------------------------------------------------------------- plan ----
 
@@ -195,9 +215,9 @@ __device__ __forceinline__ double mfma4(double a, double b, double c) {
 // by k lanes): block b takes block (b - k / 4) mod 4
 template <int kLanes>
 __device__ __forceinline__ double row_rotate(double v) {
-    constexpr int ctrl = 0x120 + kLanes; // row_ror:kLanes
-    const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(v), ctrl, 0xF, 0xF, false);
-    const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(v), ctrl, 0xF, 0xF, false);
+    constexpr int ctrl = 0x120 + kLanes; // row_ror:kLanes (every lane reads a lane of its own row)
+    const int lo = __builtin_amdgcn_mov_dpp(__double2loint(v), ctrl, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_mov_dpp(__double2hiint(v), ctrl, 0xF, 0xF, false);
     return __hiloint2double(hi, lo);
 }
 
@@ -303,8 +323,8 @@ __device__ __forceinline__ int64_t uniform64(int64_t v) {
     return static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | static_cast<uint32_t>(lo));
 }
 
-template <int LM, int KG, int NCR, int W>
-__device__ __forceinline__ void block_role(const BlockArgs& a, double* lds) {
+template <int LM, int KG, int NCR, int ES, int W>
+__device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, const int* s_ps) {
     using PL = BlockPlan<LM, KG>;
     constexpr int L = PL::L, R = PL::R, P = PL::P, RPL = PL::RPL, NT = PL::NT, GS = PL::GS;
     constexpr int GROUPS = PL::GROUPS;
@@ -358,10 +378,16 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds) {
     const int64_t item_last = min(item_first + a.per_block, a.item_base + a.items);
     int pre_count = 0;     // next centre: rows of species t at lane t
     int64_t pre_start = 0; // next centre: first pair row (lane 0)
+    // Loads are unconditional in every lane (clamped to valid addresses) so
+    // that no merge of a loaded value forces an early wait for it.
     auto prefetch_centre = [&](int64_t c) {
         if (c < item_last) {
-            if (lane < S) pre_count = a.counts[c * S + lane];
-            if (lane == 0) pre_start = a.pair_start[c];
+            // the lane offset is recomputed here rather than kept live as a
+            // 64-bit address across the whole loop
+            int t = min(lane, S - 1);
+            asm volatile("" : "+v"(t));
+            pre_count = a.counts[c * S + t];
+            pre_start = a.pair_start[c];
         }
     };
     int cnt = 0;                       // stream centre: rows of species t at lane t
@@ -378,8 +404,9 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds) {
     auto enter_centre = [&]() {
         st_centre = uniform64(st_centre + 1);
         cnt = pre_count;
-        st_row = uniform64(lane_value(pre_start, 0));
+        st_row = uniform64(pre_start);
         st_more = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(__ballot(lane < S && cnt > 0)));
+        cnt = lane < S ? cnt : 0;
         prefetch_centre(st_centre + 1);
         st_left = 0;
         if (st_more != 0) next_species();
@@ -408,7 +435,9 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds) {
         s.q = st_q;
         s.rows = n;
         s.groups = (n + GS - 1) / GS;
-        if (lane / 2 < n) s.bin = a.pair_bin[st_row + lane / 2];
+        // pad slots load the chunk's last row (a centre always has its own
+        // row, so row 0 of the graph exists for an empty chunk)
+        s.bin = a.pair_bin[n > 0 ? st_row + min(lane / 2, n - 1) : 0];
         st_row = uniform64(st_row + n);
         st_left = __builtin_amdgcn_readfirstlane(st_left - n);
         s.last = st_left == 0 && st_more == 0;
@@ -421,11 +450,9 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds) {
     double px = 0.0, py = 0.0, pz = 0.0;
     const int jj = lane / 2, comp = lane % 2;
     auto load_positions = [&](const Stage& s) {
-        if (jj < s.rows) {
-            px = a.bx[s.bin];
-            py = a.by[s.bin];
-            pz = a.bz[s.bin];
-        }
+        px = a.bx[s.bin];
+        py = a.by[s.bin];
+        pz = a.bz[s.bin];
     };
     // harmonics of a stage's slots from the centre position (cx, cy, cz)
     auto harmonics = [&](const Stage& s, int buf, double cx, double cy, double cz) {
@@ -460,7 +487,11 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds) {
 
     // sum the phases of every accumulator and add species q's radial groups
     // into its block slots of the coefficient registers
-    auto merge = [&](int q) {
+    // Each species merges exactly once per centre, into block slots of its
+    // own (the coefficient registers start each centre at zero), so the merge
+    // overwrites those slots with a lane select.
+    auto merge_into = [&](auto rc_reg, int q) {
+        constexpr int rt = decltype(rc_reg)::value; // target coefficient register
         unroll<NU>([&](auto uc) {
             constexpr int u = decltype(uc)::value;
             unroll<RPL>([&](auto rc) {
@@ -469,29 +500,32 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds) {
                 v += row_rotate<8>(v);
                 if constexpr (P == 4) v += row_rotate<4>(v);
                 acc[u][rr] = 0.0;
+                bool mine;
                 if constexpr (KG == 2) {
-                    // groups 2q, 2q + 1: register q / 2, slots {0,1} or {2,3}
-                    const bool mine = low_pair == ((q & 1) == 0);
-                    unroll<NCR>([&](auto r) {
-                        if (decltype(r)::value == (q >> 1)) C[u][decltype(r)::value] += mine ? v : 0.0;
-                    });
+                    mine = low_pair == ((q & 1) == 0); // groups 2q, 2q + 1: slots {0,1} or {2,3}
                 } else if constexpr (KG == 1) {
-                    const bool mine = blk == (q & 3);
-                    unroll<NCR>([&](auto r) {
-                        if (decltype(r)::value == (q >> 2)) C[u][decltype(r)::value] += mine ? v : 0.0;
-                    });
+                    mine = blk == (q & 3);
                 } else {
-                    const bool mine = blk == rr;
-                    unroll<NCR>([&](auto r) {
-                        if (decltype(r)::value == q) C[u][decltype(r)::value] += mine ? v : 0.0;
-                    });
+                    mine = blk == rr;
                 }
+                C[u][rt] = mine ? v : C[u][rt];
+                // one unit at a time: bounds the registers live at once
+                __builtin_amdgcn_sched_barrier(0);
             });
+        });
+    };
+    // species q's coefficient register, chosen by a wave-uniform branch
+    auto merge = [&](int q) {
+        const int rt = KG == 2 ? q >> 1 : KG == 1 ? q >> 2 : q;
+        unroll<NCR>([&](auto r) {
+            if (rt == decltype(r)::value) {
+                asm volatile("" ::: "memory"); // keeps the branch (no selects over every register)
+                merge_into(r, q);
+            }
         });
     };
 
     const int64_t F = a.F;
-    const int esize = a.out_dtype;
     int k = 0;
     while (uniform64(s0.centre) >= 0) {
         const int buf = k & 1;
@@ -569,6 +603,7 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds) {
                                 c = mfma4(row_rotate<4>(v), bt[d][3], c);  // b + 3
                             }
                             C[u0 + cg][r] = c;
+                            __builtin_amdgcn_sched_barrier(0);
                         });
                     });
                 }
@@ -576,7 +611,7 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds) {
             // power spectrum of the owned degrees, written to the centre's row
             char* row = static_cast<char*>(a.out) + centre0 * a.pitch;
             const __amdgpu_buffer_rsrc_t rsrc =
-                __builtin_amdgcn_make_buffer_rsrc(row, 0, static_cast<int>(F * esize), 0x00020000);
+                __builtin_amdgcn_make_buffer_rsrc(row, 0, static_cast<int>(F * ES), 0x00020000);
             int pair = 0;
             unroll<NCR>([&](auto ic) {
                 constexpr int ri = decltype(ic)::value;
@@ -586,9 +621,9 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds) {
                         int fb[4], fs[4];
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
-                            const int2 o = a.ps_offsets[((pair * 4 + r) * kWaveThreads) + lane];
-                            fb[r] = o.x * esize;
-                            fs[r] = o.y * esize;
+                            const int o = s_ps[(pair * 4 + r) * kWaveThreads + lane];
+                            fb[r] = o >> kStrideBits; // bytes
+                            fs[r] = (o & ((1 << kStrideBits) - 1)) * ES;
                         }
                         unroll<L>([&](auto lc) {
                             constexpr int l = decltype(lc)::value;
@@ -599,12 +634,11 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds) {
                                     constexpr int cg = decltype(cc)::value;
                                     D = mfma(C[u0 + cg][ri], C[u0 + cg][rj], D);
                                 });
-                                const double pref = a.ps_pref[l];
 #pragma unroll
                                 for (int r = 0; r < 4; ++r) {
-                                    const double v = pref * D[r];
+                                    const double v = D[r]; // the coefficients carry sqrt(pi sqrt(8/(2l+1)))
                                     const int off = fb[r] + l * fs[r];
-                                    if (esize == 4) {
+                                    if constexpr (ES == 4) {
                                         __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(static_cast<float>(v)), rsrc,
                                                                               off, 0, 0);
                                     } else {
@@ -631,11 +665,16 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds) {
     }
 }
 
-template <int LM, int KG, int NCR>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_soap_block(BlockArgs a) {
+template <int LM, int KG, int NCR, int ES>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) void k_soap_block(BlockArgs a) {
     using PL = BlockPlan<LM, KG>;
-    extern __shared__ double lds[];
+    // staging buffers, d2, exp table, padded S_lm table, power-spectrum
+    // offsets; sized at compile time, so every LDS offset is an immediate
+    __shared__ double lds[2 * PL::YWORDS + 2 * kNb + kTab + 4 * units_before(0xffffffffu, PL::L)];
+    constexpr int kPsWords = NCR * (NCR + 1) / 2 * 4 * kWaveThreads;
+    __shared__ int s_ps[kPsWords];
     const int tid = threadIdx.x;
+    for (int i = tid; i < kPsWords; i += static_cast<int>(blockDim.x)) s_ps[i] = a.ps_offsets[i];
     const int threads = static_cast<int>(blockDim.x);
     double* s_y = lds;
     double* s_d2 = s_y + 2 * PL::YWORDS;
@@ -662,21 +701,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
                 ++l;
             }
             const int c = i - off;
-            s_scale[i] = c <= 2 * l ? kScaledHarmonic.s[l][c <= l ? l - c : c - l] : 0.0;
+            // S_lm times the square root of the degree's power-spectrum
+            // prefactor (the Gram product then carries the prefactor itself)
+            s_scale[i] = c <= 2 * l ? kScaledHarmonic.s[l][c <= l ? l - c : c - l] * kPsRoot[l] : 0.0;
         }
     }
     __syncthreads();
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWaveThreads);
     if (wave == 0) {
-        block_role<LM, KG, NCR, 0>(a, lds);
+        block_role<LM, KG, NCR, ES, 0>(a, lds, s_ps);
     } else if constexpr (PL::T > 1) {
         if (wave == 1) {
-            block_role<LM, KG, NCR, (PL::T > 1 ? 1 : 0)>(a, lds);
+            block_role<LM, KG, NCR, ES, (PL::T > 1 ? 1 : 0)>(a, lds, s_ps);
         } else if constexpr (PL::T > 2) {
             if (wave == 2) {
-                block_role<LM, KG, NCR, (PL::T > 2 ? 2 : 0)>(a, lds);
+                block_role<LM, KG, NCR, ES, (PL::T > 2 ? 2 : 0)>(a, lds, s_ps);
             } else if constexpr (PL::T > 3) {
-                block_role<LM, KG, NCR, (PL::T > 3 ? 3 : 0)>(a, lds);
+                block_role<LM, KG, NCR, ES, (PL::T > 3 ? 3 : 0)>(a, lds, s_ps);
             }
         }
     }
@@ -691,13 +732,17 @@ size_t lds_bytes() {
 template <int LM, int KG, int NCR>
 void launch_shape(hipStream_t stream, const BlockArgs& a, int64_t count) {
     using PL = BlockPlan<LM, KG>;
-    const size_t lds = lds_bytes<LM, KG, NCR>();
+    const size_t lds = lds_bytes<LM, KG, NCR>() + NCR * (NCR + 1) / 2 * 4 * kWaveThreads * sizeof(int);
     const int64_t resident = std::max<int64_t>(1, std::min<int64_t>(8, (160 * 1024) / std::max<size_t>(lds, 1)));
     const int64_t target = std::max<int64_t>(1, 8 * resident * device_compute_units());
     BlockArgs args = a;
     args.per_block = std::max<int64_t>(1, (count + target - 1) / target);
     const unsigned grid = static_cast<unsigned>((count + args.per_block - 1) / args.per_block);
-    hipLaunchKernelGGL((k_soap_block<LM, KG, NCR>), dim3(grid), dim3(PL::T * kWaveThreads), lds, stream, args);
+    if (a.out_dtype == 4) {
+        hipLaunchKernelGGL((k_soap_block<LM, KG, NCR, 4>), dim3(grid), dim3(PL::T * kWaveThreads), 0, stream, args);
+    } else {
+        hipLaunchKernelGGL((k_soap_block<LM, KG, NCR, 8>), dim3(grid), dim3(PL::T * kWaveThreads), 0, stream, args);
+    }
 }
 
 using Launcher = void (*)(hipStream_t, const BlockArgs&, int64_t);
@@ -724,8 +769,8 @@ int coefficient_registers(int S, int kg) { return kg == 3 ? S : (S * kg + 3) / 4
 
 } // namespace
 
-bool block_plan_tables(int S, int n, int l_max, const std::vector<double>& beta_scaled, const std::vector<double>& pref,
-                       const std::vector<double>& expo, BlockPlanHost& out) {
+bool block_plan_tables(int S, int n, int l_max, int out_dtype, const std::vector<double>& beta_scaled,
+                       const std::vector<double>& pref, const std::vector<double>& expo, BlockPlanHost& out) {
     out = BlockPlanHost{};
     const int kg = (n + 3) / 4;
     if (n < 1 || kg > 3 || (kg == 3 && S != 1)) return false;
@@ -733,6 +778,11 @@ bool block_plan_tables(int S, int n, int l_max, const std::vector<double>& beta_
     const ShapeEntry* e = find_shape(l_max, kg, ncr);
     if (e == nullptr) return false;
     const int L = l_max + 1;
+    {
+        const int64_t W = static_cast<int64_t>(S) * n;
+        const int64_t F = W * (W + 1) / 2 * L;
+        if (F * out_dtype >= kDroppedBytes || n * n >= (1 << kStrideBits)) return false;
+    }
     const int R = kg == 2 ? 2 : 1;
     const int RPL = kg / R;
     const int NT = kg == 1 ? 1 : kg == 2 ? 2 : 4;
@@ -774,7 +824,7 @@ bool block_plan_tables(int S, int n, int l_max, const std::vector<double>& beta_
     // power-spectrum offsets: tile pair p = (ri <= rj), value r, lane: feature
     // index at l = 0 and its stride per degree for channel i (group 4 ri + r,
     // radial channel 4 rg + lane / 16) and channel j (group 4 rj + (lane % 16) / 4,
-    // 4 rg + lane % 4); pairs i > j and pad channels get kDropped
+    // 4 rg + lane % 4); pairs i > j and pad channels get kDroppedBytes
     const int W = S * n;
     auto channel = [&](int ri, int slot, int nl) -> int {
         int t = 0, rg = 0;
@@ -813,15 +863,15 @@ bool block_plan_tables(int S, int n, int l_max, const std::vector<double>& beta_
                 for (int lane = 0; lane < 64; ++lane) {
                     const int i = channel(ri, r, lane / 16);
                     const int j = channel(rj, (lane % 16) / 4, lane % 4);
-                    int fb = kDropped / 8, fs = 0;
-                    if (i >= 0 && j >= 0 && i <= j) fb = feature(i, j, fs);
-                    out.ps_offsets.push_back(fb);
-                    out.ps_offsets.push_back(fs);
+                    int fb = kDroppedBytes, fs = 0;
+                    if (i >= 0 && j >= 0 && i <= j) {
+                        fb = feature(i, j, fs) * out_dtype;
+                    }
+                    out.ps_offsets.push_back((fb << kStrideBits) | fs);
                 }
             }
         }
     }
-    (void)W;
     out.kg = kg;
     out.ncr = ncr;
     out.waves = e->waves;
