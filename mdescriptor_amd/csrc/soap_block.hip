@@ -100,6 +100,12 @@ struct BlockPlan {
     static constexpr int T = L < 4 ? L : 4;     // wavefronts
     static constexpr int YROWS = H + 3;         // staged harmonic rows (pad columns of degree LM read up to H + 2)
     static constexpr int YWORDS = YROWS * kYS;
+#ifndef MDX_BLOCK_HARMONIC_WAVES
+#define MDX_BLOCK_HARMONIC_WAVES 1
+#endif
+    // wavefronts that stage the harmonics (the first HW roles): each pays a
+    // per-slot set-up, so fewer of them do less work in total
+    static constexpr int HW = MDX_BLOCK_HARMONIC_WAVES < T ? MDX_BLOCK_HARMONIC_WAVES : T;
 
     // degrees of each wavefront: longest processing time first over the cost
     // of a degree per step group (exps of 12 VALU instructions, 4 cycles each,
@@ -154,7 +160,7 @@ struct BlockPlan {
         for (int w = 0; w <= T; ++w)
             for (int i = 0; i <= L; ++i) best[w][i] = kInf;
         best[0][0] = 0;
-        for (int w = 1; w <= T; ++w) {
+        for (int w = 1; w <= HW; ++w) {
             for (int i = 0; i <= L; ++i) {
                 for (int j = 0; j <= i; ++j) {
                     if (best[w - 1][j] == kInf) continue;
@@ -168,7 +174,7 @@ struct BlockPlan {
         }
         Split s{};
         int i = L;
-        for (int w = T; w >= 1; --w) {
+        for (int w = HW; w >= 1; --w) {
             const int j = cut[w][i];
             s.lo[w - 1] = j;
             s.hi[w - 1] = i;
@@ -332,6 +338,7 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
     constexpr int NU = units_total(kOwn, L); // owned (l, cg) pairs
     constexpr int ND = popcount_c(kOwn);     // owned degrees
     constexpr int MLO = PL::mlo(W), MHI = PL::mhi(W);
+    constexpr bool kHarm = W < PL::HW; // this role stages harmonics (and loads the slots' positions)
 
     const int lane = threadIdx.x % kWaveThreads;
     const int S = a.S;
@@ -359,8 +366,11 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
     });
     const int blk = (lane / 4) % 4;
     const int ph = blk / R;
-    // staging reads: B operand of (l, cg) at ((l*l + 4 cg) kYS + GS g) + yread,
-    // the lane's slot of step group g at GS g + dread
+    // staging reads: B operand of (l, cg) at (l*l + 4 cg) kYS + GS g + yread,
+    // the lane's slot's d2 of step group g at GS g + dread.  A 64-bit LDS
+    // read is served 16 lanes at a time; those lanes (one neighbour k) read 4
+    // columns x P phases at a row pitch of 1 mod 16 doubles, all in
+    // different banks.
     const int yread = (lane % 4) * kYS + 4 * ph + lane / 16;
     const int dread = 4 * ph + lane / 16;
     // lanes of the block slots {0, 1} (KG = 2: the even species' groups)
@@ -437,7 +447,7 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
         s.groups = (n + GS - 1) / GS;
         // pad slots load the chunk's last row (a centre always has its own
         // row, so row 0 of the graph exists for an empty chunk)
-        s.bin = a.pair_bin[n > 0 ? st_row + min(lane / 2, n - 1) : 0];
+        if constexpr (kHarm) s.bin = a.pair_bin[n > 0 ? st_row + min(lane / 2, n - 1) : 0];
         st_row = uniform64(st_row + n);
         st_left = __builtin_amdgcn_readfirstlane(st_left - n);
         s.last = st_left == 0 && st_more == 0;
@@ -450,9 +460,11 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
     double px = 0.0, py = 0.0, pz = 0.0;
     const int jj = lane / 2, comp = lane % 2;
     auto load_positions = [&](const Stage& s) {
-        px = a.bx[s.bin];
-        py = a.by[s.bin];
-        pz = a.bz[s.bin];
+        if constexpr (kHarm) {
+            px = a.bx[s.bin];
+            py = a.by[s.bin];
+            pz = a.bz[s.bin];
+        }
     };
     // harmonics of a stage's slots from the centre position (cx, cy, cz)
     auto harmonics = [&](const Stage& s, int buf, double cx, double cy, double cz) {
@@ -469,7 +481,7 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
 
     // prologue: harmonics of the first chunk
     load_positions(s0);
-    if (uniform64(s0.centre) >= 0) {
+    if (kHarm && uniform64(s0.centre) >= 0) {
         const int64_t c = uniform64(s0.centre);
         harmonics(s0, 0, a.positions[3 * c], a.positions[3 * c + 1], a.positions[3 * c + 2]);
     }
@@ -537,7 +549,12 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
         // centre position of chunk k + 1 (scalar loads, used after the contraction)
         const int64_t centre1 = uniform64(s1.centre);
         const int64_t cpos1 = 3 * (centre1 >= 0 ? centre1 : 0);
-        const double cx1 = a.positions[cpos1], cy1 = a.positions[cpos1 + 1], cz1 = a.positions[cpos1 + 2];
+        double cx1 = 0.0, cy1 = 0.0, cz1 = 0.0;
+        if constexpr (kHarm) {
+            cx1 = a.positions[cpos1];
+            cy1 = a.positions[cpos1 + 1];
+            cz1 = a.positions[cpos1 + 2];
+        }
         // positions of chunk k + 1 in flight; bins of chunk k + 2
         Stage s2 = next_stage();
         // ------------------------------------------------ contraction of chunk k
@@ -656,7 +673,7 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
             unroll<NU>([&](auto u) { unroll<NCR>([&](auto r) { C[decltype(u)::value][decltype(r)::value] = 0.0; }); });
         }
         // ---------------------------------------- harmonics of chunk k + 1
-        if (centre1 >= 0) harmonics(s1, buf ^ 1, cx1, cy1, cz1);
+        if (kHarm && centre1 >= 0) harmonics(s1, buf ^ 1, cx1, cy1, cz1);
         load_positions(s2);
         s0 = s1;
         s1 = s2;
