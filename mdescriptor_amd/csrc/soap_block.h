@@ -16,7 +16,7 @@ struct BlockArgs {
     const double* bx;           // binned image positions
     const double* by;
     const double* bz;
-    const double* lane_e1;      // [l][register][64]: -a_lk 64/ln2 of the lane's exp row, 0 for pad rows
+    const double* lane_e1;      // [l][register][64]: -a_lk of the lane's exp row, 0 for pad rows
     const double* lane_beta;    // [l][fold term][64]: beta^T operand of the lane
     const int32_t* ps_offsets;  // [tile pair][value][64]: (byte offset at l = 0) << 9 | feature stride per l
     int S;                      // species

@@ -235,32 +235,32 @@ __device__ __forceinline__ double swap_blocks(double v) {
     return __hiloint2double(hi, lo);
 }
 
-// exp(-a d2) for d2 >= 0 and -a d2 >= -708, given e1 = -a 64/ln2: Tang's
-// table method (ACM TOMS 15(2), 1989) with the reduction on the product,
-// y = d2 e1 = 64k + j + rs (|rs| <= 1/2), exp = 2^k 2^(j/64) e^r, r = rs ln2/64,
-// e^r - 1 by its degree-5 Taylor polynomial in rs.  rs = fma(d2, e1, -(64k+j))
-// carries only e1's rounding: within 5e-15 relative of exp(-a d2) for
-// -a d2 >= -40, as close as libm's exp of the rounded product further out.
-// tab[j] = 2^(j/64) with j << 14 taken off its high word, so that adding
-// (64k + j) << 14 scales it by 2^k in one integer add.
-constexpr double kExpC1 = 0.693147180559945309417232121458176568 / 64.0;
-constexpr double kExpC2 = kExpC1 * kExpC1 / 2.0;
-constexpr double kExpC3 = kExpC2 * kExpC1 / 3.0;
-constexpr double kExpC4 = kExpC3 * kExpC1 / 4.0;
-constexpr double kExpC5 = kExpC4 * kExpC1 / 5.0;
-__device__ __forceinline__ double exp_neg(double d2, double e1, const int2* tab) {
-    constexpr double kShifter = 6755399441055744.0; // 1.5 * 2^52
-    const double s = fma(d2, e1, kShifter);
+// exp(x) for x = na * d2 (na = -a <= 0, d2 >= 0, x >= -708): x is rounded
+// exactly as the reference's exp(-a * d2) argument (soap.cpp:895-896), then
+// Tang's table method (ACM TOMS 15(2), 1989): x = (64k + j) ln2/64 + r with
+// the reduction against ln2/64 split in two (kf * hi exact), |r| <= ln2/128,
+// exp(x) = 2^k 2^(j/64) e^r, e^r - 1 by its degree-5 Taylor polynomial
+// (truncation below 4e-17 relative).  tab[j] = 2^(j/64) with j << 14 taken
+// off its high word, so that adding (64k + j) << 14 scales it by 2^k in one
+// integer add (the result is a normal number for x >= -708).
+__device__ __forceinline__ double exp_neg(double d2, double na, const int2* tab) {
+    constexpr double kInvLn2x64 = 92.332482616893658071035179584121; // 64 / ln 2
+    constexpr double kHi = 0.010830417275428772;                      // ln2/64, 32 trailing zero bits
+    constexpr double kLo = 7.420820373486988e-09;                     // ln2/64 - kHi
+    constexpr double kShifter = 6755399441055744.0;                   // 1.5 * 2^52
+    const double x = na * d2;
+    const double s = fma(x, kInvLn2x64, kShifter);
     const double kf = s - kShifter;
-    const double rs = fma(d2, e1, -kf);
+    double r = fma(kf, -kHi, x);
+    r = fma(kf, -kLo, r);
     const int nj = __double2loint(s);
     const int2 t = *reinterpret_cast<const int2*>(reinterpret_cast<const char*>(tab) + ((nj << 3) & 0x1f8));
-    double q = fma(kExpC5, rs, kExpC4);
-    q = fma(q, rs, kExpC3);
-    q = fma(q, rs, kExpC2);
-    q = fma(q, rs, kExpC1);
-    const double em1 = q * rs;
-    const double tk = __hiloint2double(t.y + (nj << 14), t.x);
+    double q = fma(r, 1.0 / 120.0, 1.0 / 24.0);
+    q = fma(q, r, 1.0 / 6.0);
+    q = fma(q, r, 0.5);
+    q = fma(q, r, 1.0);
+    const double em1 = r * q; // e^r - 1
+    const double tk = __hiloint2double(t.y + (nj << 14), t.x); // 2^k 2^(j/64)
     return fma(tk, em1, tk);
 }
 
@@ -772,7 +772,11 @@ struct ShapeEntry {
 };
 #define MDX_BLOCK_SHAPE(LM, KG, NCR) {LM, KG, NCR, &launch_shape<LM, KG, NCR>, BlockPlan<LM, KG>::T}
 const ShapeEntry kShapes[] = {
-    MDX_BLOCK_SHAPE(6, 2, 2),
+    MDX_BLOCK_SHAPE(3, 1, 1), // water (benchmark configuration 1)
+    MDX_BLOCK_SHAPE(6, 2, 2), // HCNO (configuration 2)
+    MDX_BLOCK_SHAPE(4, 2, 3), // molecules (configuration 3, atom-level rows)
+    MDX_BLOCK_SHAPE(8, 2, 3), // high-entropy alloy (configuration 4)
+    MDX_BLOCK_SHAPE(9, 3, 1), // liquid silicon (configuration 5)
 };
 #undef MDX_BLOCK_SHAPE
 
@@ -803,7 +807,6 @@ bool block_plan_tables(int S, int n, int l_max, int out_dtype, const std::vector
     const int R = kg == 2 ? 2 : 1;
     const int RPL = kg / R;
     const int NT = kg == 1 ? 1 : kg == 2 ? 2 : 4;
-    const long double kScale = 64.0L / 0.693147180559945309417232121458176568L;
     auto beta = [&](int l, int np, int k) -> double {
         if (np >= n || k >= n || np < 0 || k < 0) return 0.0;
         return beta_scaled[static_cast<size_t>((l * n + np) * n + k)] * pref[static_cast<size_t>(l * n + k)];
@@ -817,8 +820,7 @@ bool block_plan_tables(int S, int n, int l_max, int out_dtype, const std::vector
                 const int rg = rr * R + b % R;
                 const int k = 4 * rg + lane % 4;
                 out.lane_e1[static_cast<size_t>((l * RPL + rr) * 64 + lane)] =
-                    k < n ? static_cast<double>(-static_cast<long double>(expo[static_cast<size_t>(l * n + k)]) * kScale)
-                          : 0.0;
+                    k < n ? -expo[static_cast<size_t>(l * n + k)] : 0.0;
             }
             // beta^T operand: lane = beta^T[k = lane / 16][n' = lane % 4] of the
             // fold term's (radial group in -> radial group out) block

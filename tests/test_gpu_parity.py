@@ -159,6 +159,28 @@ def test_quad_kernel_shapes(hip_context, oracle, monkeypatch, n_max, l_max):
         assert timing["expansion_tiles"] < 0
 
 
+@pytest.mark.parametrize("species,n_max,l_max,r_cut", [
+    ([1, 8], 4, 3, 3.0), ([1, 8], 3, 3, 3.0),       # one radial group, four step phases per exp register
+    ([1, 6, 7, 8], 8, 6, 3.0), ([1, 6, 8], 7, 6, 3.0),  # two radial groups, two coefficient registers
+    ([1, 6, 7, 8, 9], 6, 4, 3.0), ([24, 26, 27, 28, 29], 8, 8, 3.0),  # five species: three registers
+    ([14], 12, 9, 6.0), ([14], 9, 9, 3.0),          # three radial groups: rotated beta fold
+])
+def test_block_kernel_shapes(hip_context, oracle, monkeypatch, species, n_max, l_max, r_cut):
+    """Every compiled shape of the register-coefficient kernel (one, two and
+    three radial groups; one to three coefficient registers; pad channels)
+    against the oracle, float64 and float32 rows.  Twelve GTO channels get a
+    6 A cutoff: packed into 3 A their overlap matrix is so ill-conditioned
+    (max |beta| 1.6e7) that any two summation orders, the oracle's and every
+    GPU kernel's alike, differ by 1e-9."""
+
+    monkeypatch.setenv("MDX_HIP_SOAP_KERNEL", "block")
+    batch = _random_cluster(10 * n_max + l_max, 30, species)
+    params = {"species": species, "n_max": n_max, "l_max": l_max, "r_cut": r_cut}
+    for dtype in ("float64", "float32"):
+        _, timing = _check(hip_context, oracle, batch, params, "off", dtype)
+        assert timing["expansion_tiles"] == -1004
+
+
 @pytest.mark.parametrize("cutoff", [3.5, 3.5 + SOAP_PAD])
 def test_golden_graphs(hip_context, oracle, cutoff):
     _, batch, _ = load_golden("reference_soap", "manifest.json")
