@@ -183,6 +183,24 @@ int mdx_hip_soap_run(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, mdx_device_bat
                      void* out_device, int64_t out_pitch_bytes, const volatile int32_t* cancel_flag,
                      mdx_timing* timing);
 
+/* Size of the static device scratch array of mdx_hip_soap_run_noalloc. */
+#define MDX_NOALLOC_SCRATCH_BYTES (64u << 20)
+
+/* mdx_hip_soap_run without device allocation.  No counterpart in the
+ * reference: for callers that cannot allocate device memory during the run
+ * (tight serving loops, code that must not call hipMalloc).  Same arguments,
+ * kernels and results as mdx_hip_soap_run; the run's scratch (neighbour graph,
+ * partial sums of the averaged modes) lives in one static device array of
+ * MDX_NOALLOC_SCRATCH_BYTES per device instead of buffers owned by the batch.
+ * The plan, the batch and out_device are the caller's, made beforehand.  A
+ * batch whose scratch does not fit returns MDX_INVALID_ARGUMENT with a message
+ * that names the maximum.  All contexts on one device share its array, which
+ * keeps the last call's contents: calls that overlap on one device (through
+ * different contexts; one context serialises its own calls) race. */
+int mdx_hip_soap_run_noalloc(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, mdx_device_batch* batch,
+                             void* out_device, int64_t out_pitch_bytes, const volatile int32_t* cancel_flag,
+                             mdx_timing* timing);
+
 /* Neighbour graph on the device, for parity and the pair-level API.
  * Replaces build_neighbor_graph (cpp/src/common/neighbor.cpp:703-768) as
  * exported by _native.build_neighbor_graph (cpp/src/bindings/module.cpp:887-935):

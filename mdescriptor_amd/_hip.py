@@ -208,6 +208,11 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, _i32p,
          ctypes.POINTER(Timing)],
     ),
+    "mdx_hip_soap_run_noalloc": (
+        ctypes.c_int,
+        [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, _i32p,
+         ctypes.POINTER(Timing)],
+    ),
     "mdx_hip_neighbors_build": (
         ctypes.c_int,
         [ctypes.c_void_p, ctypes.POINTER(BatchView), ctypes.c_double, ctypes.c_int32, _i64p],

@@ -22,6 +22,29 @@ namespace {
 
 thread_local std::string g_last_error;
 
+// Device scratch of mdx_hip_soap_run_noalloc: the neighbour graph and the
+// partial sums of one run.  Every device that loads the library holds one
+// copy until the process ends.  Host code never names the array itself (its
+// host-side symbol is not a device address): it uses the device address that
+// hipGetSymbolAddress returns, looked up once per device at context creation.
+constexpr size_t kStaticScratchBytes = size_t(MDX_NOALLOC_SCRATCH_BYTES);
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+// Device address of `scratch` on the current device (device index < 64).
+char* static_scratch(int device) {
+    static std::mutex lock;
+    static char* address[64] = {};
+    if (device < 0 || device >= 64) throw mdx::Error(MDX_INVALID_ARGUMENT, "HIP device index out of range");
+    std::lock_guard<std::mutex> guard(lock);
+    if (address[device] == nullptr) {
+        void* p = nullptr;
+        MDX_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (p == nullptr) throw mdx::Error(MDX_INTERNAL, "no device address for the static scratch array");
+        address[device] = static_cast<char*>(p);
+    }
+    return address[device];
+}
+
 template <typename Fn>
 int guarded(mdx_hip_ctx* ctx, Fn&& fn) {
     std::string message;
@@ -383,6 +406,15 @@ int mdx_hip_create(int device, mdx_hip_ctx** out) {
             for (auto& ev : ctx->events) MDX_HIP(hipEventCreate(&ev));
             for (auto& ev : ctx->stage_events) MDX_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
             for (auto& ev : ctx->list_events) MDX_HIP(hipEventCreate(&ev));
+            ctx->finished.prepare();
+            // what mdx_hip_soap_run_noalloc needs beyond the scratch array:
+            // the pinned statistics words and the read-back event
+            ctx->arena.base = static_scratch(device);
+            ctx->arena.capacity = kStaticScratchBytes;
+            ctx->static_graph.for_each_buffer([&](mdx::DeviceBuffer& b) { b.arena = &ctx->arena; });
+            ctx->static_partials.arena = &ctx->arena;
+            ctx->static_graph.stats_host.get(mdx::kStatWords);
+            ctx->static_graph.read_back.prepare();
         } catch (...) {
             mdx_hip_destroy(ctx);
             throw;
@@ -772,26 +804,57 @@ void mdx_hip_batch_destroy(mdx_device_batch* batch) {
     if (previous >= 0) (void)hipSetDevice(previous);
 }
 
+namespace {
+
+// Arguments of a device-batch run, checked as mdx_hip_soap_run documents.
+void check_device_run(const mdx_hip_ctx* ctx, const mdx_soap_plan* plan, const mdx_device_batch* batch,
+                      const void* out_device, int64_t out_pitch_bytes) {
+    if (plan == nullptr || batch == nullptr) throw mdx::Error(MDX_INVALID_ARGUMENT, "null plan or batch");
+    if (plan->device != ctx->device || batch->device != ctx->device) {
+        throw mdx::Error(MDX_INVALID_ARGUMENT, "plan or batch belongs to another device");
+    }
+    if (batch->pb.n_species != plan->S || batch->pb.cutoff != plan->cutoff) {
+        throw mdx::Error(MDX_INVALID_ARGUMENT, "device batch was prepared for another plan");
+    }
+    const int64_t rows = plan->average != 0 ? batch->pb.structures : batch->pb.atoms;
+    const int64_t row_bytes = plan->features * plan->out_dtype;
+    if (out_pitch_bytes < row_bytes) throw mdx::Error(MDX_INVALID_ARGUMENT, "output pitch is too small");
+    if (rows > 0 && row_bytes > 0 && out_device == nullptr) throw mdx::Error(MDX_INVALID_ARGUMENT, "null output");
+}
+
+} // namespace
+
 int mdx_hip_soap_run(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, mdx_device_batch* batch, void* out_device,
                      int64_t out_pitch_bytes, const volatile int32_t* cancel_flag, mdx_timing* timing) {
     if (ctx == nullptr) return MDX_INVALID_ARGUMENT;
     std::lock_guard<std::mutex> lock(ctx->mutex);
     return guarded(ctx, [&] {
-        if (plan == nullptr || batch == nullptr) throw mdx::Error(MDX_INVALID_ARGUMENT, "null plan or batch");
-        if (plan->device != ctx->device || batch->device != ctx->device) {
-            throw mdx::Error(MDX_INVALID_ARGUMENT, "plan or batch belongs to another device");
-        }
-        if (batch->pb.n_species != plan->S || batch->pb.cutoff != plan->cutoff) {
-            throw mdx::Error(MDX_INVALID_ARGUMENT, "device batch was prepared for another plan");
-        }
+        check_device_run(ctx, plan, batch, out_device, out_pitch_bytes);
         check_cancel(cancel_flag);
-        const int64_t rows = plan->average != 0 ? batch->pb.structures : batch->pb.atoms;
-        const int64_t row_bytes = plan->features * plan->out_dtype;
-        if (out_pitch_bytes < row_bytes) throw mdx::Error(MDX_INVALID_ARGUMENT, "output pitch is too small");
-        if (rows > 0 && row_bytes > 0 && out_device == nullptr) throw mdx::Error(MDX_INVALID_ARGUMENT, "null output");
         DeviceScope scope(ctx->device);
         run_pipeline(ctx, *plan, batch->pb, batch->graph, batch->partials, out_device, out_pitch_bytes, cancel_flag,
                      timing);
+        ctx->finished.wait(ctx->stream);
+        fill_timing(ctx, timing, false);
+    });
+}
+
+int mdx_hip_soap_run_noalloc(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, mdx_device_batch* batch,
+                             void* out_device, int64_t out_pitch_bytes, const volatile int32_t* cancel_flag,
+                             mdx_timing* timing) {
+    if (ctx == nullptr) return MDX_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    return guarded(ctx, [&] {
+        check_device_run(ctx, plan, batch, out_device, out_pitch_bytes);
+        check_cancel(cancel_flag);
+        DeviceScope scope(ctx->device);
+        // every piece is carved afresh from the start of the array; the
+        // graph's counters are cleared on the stream before each build
+        ctx->arena.reset();
+        ctx->static_graph.for_each_buffer([](mdx::DeviceBuffer& b) { b.release(); });
+        ctx->static_partials.release();
+        run_pipeline(ctx, *plan, batch->pb, ctx->static_graph, ctx->static_partials, out_device, out_pitch_bytes,
+                     cancel_flag, timing);
         ctx->finished.wait(ctx->stream);
         fill_timing(ctx, timing, false);
     });

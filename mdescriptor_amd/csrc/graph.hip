@@ -44,8 +44,30 @@ void check_hip(hipError_t code, const char* what) {
     throw Error(MDX_INTERNAL, std::string(what) + " failed: " + name);
 }
 
+void* ScratchArena::take(size_t size) {
+    const size_t rounded = std::max<size_t>(256, (size + 255) & ~size_t(255));
+    if (base == nullptr || rounded > capacity - used) {
+        throw Error(MDX_INVALID_ARGUMENT, "the batch needs more device scratch than the static maximum of " +
+                                              std::to_string(capacity) + " bytes");
+    }
+    void* p = base + used;
+    used += rounded;
+    return p;
+}
+
+void ScratchArena::rewind(void* piece) {
+    char* p = static_cast<char*>(piece);
+    if (p < base || p > base + used) throw Error(MDX_INTERNAL, "scratch piece outside its arena");
+    used = static_cast<size_t>(p - base);
+}
+
 void DeviceBuffer::reserve(size_t size) {
     if (size <= bytes && ptr != nullptr) return;
+    if (arena != nullptr) {
+        ptr = arena->take(size);
+        bytes = size;
+        return;
+    }
     release();
     const size_t rounded = std::max<size_t>(256, (size + 255) & ~size_t(255));
     MDX_HIP(hipMalloc(&ptr, rounded));
@@ -87,8 +109,12 @@ StreamPoint::~StreamPoint() {
     if (event_ != nullptr) (void)hipEventDestroy(event_);
 }
 
-void StreamPoint::wait(hipStream_t stream) {
+void StreamPoint::prepare() {
     if (event_ == nullptr) MDX_HIP(hipEventCreateWithFlags(&event_, hipEventDisableTiming));
+}
+
+void StreamPoint::wait(hipStream_t stream) {
+    prepare();
     MDX_HIP(hipEventRecord(event_, stream));
     for (;;) {
         const hipError_t e = hipEventQuery(event_);
@@ -98,7 +124,7 @@ void StreamPoint::wait(hipStream_t stream) {
 }
 
 void DeviceBuffer::release() {
-    if (ptr != nullptr) {
+    if (ptr != nullptr && arena == nullptr) {
         (void)hipFree(ptr);
     }
     ptr = nullptr;
@@ -987,7 +1013,11 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     using Fill = std::integral_constant<int, kNbrFill>;
     using Slotted = std::integral_constant<int, kNbrSlotted>;
     const int64_t cap = slotted ? gr.slot_cap : 0;
-    const bool use_slots = cap > 0 && atoms * cap * static_cast<int64_t>(sizeof(uint32_t)) <= kMaxSlottedBytes;
+    const int64_t slot_bytes = atoms * cap * static_cast<int64_t>(sizeof(uint32_t));
+    // from an arena, the slotted layout only when its rows fit in what is left
+    ScratchArena* arena = gr.pair_bin.arena;
+    const bool use_slots = cap > 0 && slot_bytes <= kMaxSlottedBytes &&
+                           (arena == nullptr || static_cast<size_t>(slot_bytes) <= arena->left());
     gr.slots = 0;
     if (use_slots) {
         // one pass: counts and rows at centre * cap
@@ -1015,6 +1045,13 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
         int64_t grown = kMinSlotCap;
         while (grown < most) grown *= 2;
         gr.slot_cap = grown <= kMaxSlotCap ? grown : 0;
+        if (arena != nullptr) {
+            // the slotted rows were the arena's last piece and are not read
+            // again: the compact rows reuse their space
+            arena->rewind(gr.pair_bin.ptr);
+            gr.pair_bin.ptr = nullptr;
+            gr.pair_bin.bytes = 0;
+        }
         scan_counts(stream, gr.totals.as<int32_t>(), gr.pair_start.as<int64_t>(), atoms, gr.scan_tmp);
         gr.pair_bin.reserve(std::max<size_t>(1, static_cast<size_t>(pairs) * sizeof(uint32_t)));
         neighbors(Fill{}, 0);

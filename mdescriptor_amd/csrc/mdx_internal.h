@@ -35,10 +35,27 @@ struct Error : std::runtime_error {
 void check_hip(hipError_t code, const char* what);
 #define MDX_HIP(call) ::mdx::check_hip((call), #call)
 
+// Bump allocator over a caller-owned block of device memory (the library's
+// static scratch array).  take() hands out 256-byte aligned pieces and throws
+// MDX_INVALID_ARGUMENT when the block is exhausted; rewind(p) gives back p
+// and every piece taken after it; reset() starts over.
+struct ScratchArena {
+    char* base = nullptr;
+    size_t capacity = 0;
+    size_t used = 0;
+    void* take(size_t size);
+    void rewind(void* piece);
+    size_t left() const { return capacity - used; }
+    void reset() { used = 0; }
+};
+
 // Grow-only device buffer.  Reallocated only when a larger size is asked for.
+// A buffer bound to an arena takes its memory from it instead and never
+// allocates or frees device memory.
 struct DeviceBuffer {
     void* ptr = nullptr;
     size_t bytes = 0;
+    ScratchArena* arena = nullptr;
     void reserve(size_t size);
     void release();
     template <typename T> T* as() const { return static_cast<T*>(ptr); }
@@ -121,6 +138,7 @@ public:
     StreamPoint(const StreamPoint&) = delete;
     StreamPoint& operator=(const StreamPoint&) = delete;
     ~StreamPoint();
+    void prepare(); // create the event on the current device now
     void wait(hipStream_t stream);
 
 private:
@@ -159,6 +177,15 @@ struct DeviceGraph {
     StreamPoint read_back;   // completion of the statistics read-back
     PinnedWords stats_host;  // its destination
     DeviceBuffer scan_tmp;   // block sums of the scans
+
+    template <typename F> void for_each_buffer(F f) {
+        for (DeviceBuffer* b : {&counters, &cell_start, &bin_key, &cell_species_start, &centre_struct, &bin_x,
+                                &bin_y, &bin_z, &bin_atom, &bin_image, &bin_type, &centre_cell, &centre_slot,
+                                &cell_centre_start, &cell_centres, &counts, &totals, &pair_start, &pair_bin,
+                                &scan_tmp}) {
+            f(*b);
+        }
+    }
 };
 
 // Build (or rebuild) the device graph of a prepared batch at pb.cutoff.
@@ -233,6 +260,12 @@ struct mdx_hip_ctx {
     hipStream_t copy_stream = nullptr; // result downloads overlapped with the expansion launches
     std::vector<hipEvent_t> slice_events; // end of each expansion launch, waited on by copy_stream
     mdx::StreamPoint finished;        // end of a device-batch run (polled)
+    // mdx_hip_soap_run_noalloc: the device's static scratch array as an arena,
+    // and the graph and partial sums that live in it (bound to the arena at
+    // context creation, emptied at the start of every call)
+    mdx::ScratchArena arena;
+    mdx::DeviceGraph static_graph;
+    mdx::DeviceBuffer static_partials;
 };
 
 struct mdx_soap_plan {
