@@ -1,8 +1,19 @@
-"""Lifecycle and the single ``compute`` boundary of a descriptor.
+"""Descriptor lifecycle: admission of a batch, cancellation, closing.
 
-Same contract as ``src/mdescriptor/core/descriptor.py:29-147``: input is
-coerced and validated before any device work, cancellation is checked before
-and after, ``close()`` is final, and an active descriptor cannot be pickled.
+Every public entry that computes (``compute`` and the device-output
+``SOAP.compute_into``) goes through the same two gates of the base class:
+
+* ``_admit`` runs before any device work: the descriptor must be open, the
+  control must not be cancelled, and the input is coerced to a
+  :class:`StructureBatch` and checked by the family (``_validate_batch``);
+  a ``TypeError``/``ValueError`` there surfaces as ``DescriptorInputError``
+  with the validator's path (or ``["input"]``).
+* ``_release`` runs after the device work: a cancellation requested in the
+  meantime still wins over the result.
+
+A closed descriptor stays closed and keeps its configuration and metadata;
+a live one cannot be pickled.  Contract of
+``src/mdescriptor/core/descriptor.py:29-147`` (messages and error classes).
 """
 
 from __future__ import annotations
@@ -18,9 +29,12 @@ from .errors import (
     MDescriptorError,
     _InputValidationError,
 )
-from .input import coerce_batch
+from .input import StructureBatch, coerce_batch
 from .options import CONFIGURATION_SCHEMA_VERSION
 from .result import DescriptorResult
+
+_CANCELLED = "descriptor computation was cancelled"
+_NOT_PICKLEABLE = "active descriptors are not pickleable; store a JSON configuration and rebuild"
 
 
 class DescriptorConfiguration:
@@ -38,7 +52,20 @@ class DescriptorConfiguration:
                 "parameters": deepcopy(self.parameters)}
 
 
+def cancel_requested(control: Any) -> bool:
+    """True when ``control`` (anything with a ``cancelled`` attribute or
+    method, or None) asks to stop."""
+
+    flag = getattr(control, "cancelled", False) if control is not None else False
+    if callable(flag):
+        flag = flag()
+    return bool(flag)
+
+
 class Descriptor(ABC):
+    """Base of the descriptor families; they implement ``_compute_batch``
+    and may narrow the accepted input with ``_validate_batch``."""
+
     name: ClassVar[str]
 
     def __init__(self) -> None:
@@ -46,6 +73,7 @@ class Descriptor(ABC):
         self._configuration = DescriptorConfiguration(CONFIGURATION_SCHEMA_VERSION, self.name, {})
         self._metadata_snapshot: dict[str, Any] = {}
 
+    # ------------------------------------------------------------- state
     @property
     def closed(self) -> bool:
         return self._closed
@@ -65,34 +93,51 @@ class Descriptor(ABC):
     def _set_configuration(self, schema_version: int, parameters: dict[str, Any]) -> None:
         self._configuration = DescriptorConfiguration(schema_version, self.name, parameters)
 
-    def compute(self, value: Any, *, control: Any = None) -> DescriptorResult:
-        """Compute one batch (descriptor.py:75-112)."""
+    # ------------------------------------------------------------- gates
+    def _ensure_open(self) -> None:
+        if self._closed:
+            raise ClosedDescriptorError(f"descriptor {self.name!r} is closed")
+
+    def _admit(self, value: Any, control: Any) -> StructureBatch:
+        """The checked batch of ``value``; nothing has touched a device yet."""
 
         self._ensure_open()
-        if _is_cancelled(control):
-            raise CancelledError("descriptor computation was cancelled")
+        if cancel_requested(control):
+            raise CancelledError(_CANCELLED)
         try:
             batch = coerce_batch(value)
             self._validate_batch(batch)
         except DescriptorInputError:
             raise
         except (TypeError, ValueError) as exc:
-            path = list(exc.path) if isinstance(exc, _InputValidationError) else ["input"]
-            raise DescriptorInputError(str(exc), path=path) from exc
+            where = list(exc.path) if isinstance(exc, _InputValidationError) else ["input"]
+            raise DescriptorInputError(str(exc), path=where) from exc
+        return batch
+
+    @staticmethod
+    def _release(control: Any) -> None:
+        """Raise if the computation was cancelled while it ran."""
+
+        if cancel_requested(control):
+            raise CancelledError(_CANCELLED)
+
+    # ------------------------------------------------------------- compute
+    def compute(self, value: Any, *, control: Any = None) -> DescriptorResult:
+        batch = self._admit(value, control)
         result = self._compute_batch(batch, control=control)
-        if _is_cancelled(control):
-            raise CancelledError("descriptor computation was cancelled")
-        if not isinstance(result, DescriptorResult):
-            raise MDescriptorError(f"{self.name} returned {type(result).__name__}, expected DescriptorResult")
-        return result
+        self._release(control)
+        if isinstance(result, DescriptorResult):
+            return result
+        raise MDescriptorError(f"{self.name} returned {type(result).__name__}, expected DescriptorResult")
 
     @abstractmethod
-    def _compute_batch(self, batch: Any, *, control: Any = None) -> DescriptorResult:
-        raise NotImplementedError
+    def _compute_batch(self, batch: StructureBatch, *, control: Any = None) -> DescriptorResult:
+        """One admitted batch through the family's backend."""
 
-    def _validate_batch(self, batch: Any) -> None:
-        del batch
+    def _validate_batch(self, batch: StructureBatch) -> None:
+        """Family-specific input checks (none by default)."""
 
+    # ------------------------------------------------------------- lifecycle
     def close(self) -> None:
         self._closed = True
 
@@ -100,24 +145,11 @@ class Descriptor(ABC):
         self._ensure_open()
         return self
 
-    def __exit__(self, exc_type: Any, exc_value: Any, traceback: Any) -> None:
+    def __exit__(self, *exc_info: Any) -> None:
         self.close()
 
     def __getstate__(self) -> Any:
-        raise TypeError("active descriptors are not pickleable; store a JSON configuration and rebuild")
-
-    def _ensure_open(self) -> None:
-        if self._closed:
-            raise ClosedDescriptorError(f"descriptor {self.name!r} is closed")
+        raise TypeError(_NOT_PICKLEABLE)
 
 
-def _is_cancelled(control: Any) -> bool:
-    if control is None:
-        return False
-    checker = getattr(control, "cancelled", None)
-    if checker is None:
-        return False
-    return bool(checker() if callable(checker) else checker)
-
-
-__all__ = ["Descriptor", "DescriptorConfiguration"]
+__all__ = ["Descriptor", "DescriptorConfiguration", "cancel_requested"]

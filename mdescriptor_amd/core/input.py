@@ -34,15 +34,15 @@ class StructureBatch:
     charge_spin: np.ndarray | None = None
 
     def __post_init__(self) -> None:
-        numbers = _integer_snapshot(self.numbers, np.int32, "numbers")
-        positions = _array_snapshot(self.positions, np.float64, "positions")
-        cells = _array_snapshot(self.cells, np.float64, "cells")
-        pbc = _integer_snapshot(self.pbc, np.int32, "pbc", allow_bool=True)
-        offsets = _integer_snapshot(self.offsets, np.int64, "offsets")
+        numbers = _owned_array(self.numbers, np.int32, "numbers")
+        positions = _owned_array(self.positions, np.float64, "positions")
+        cells = _owned_array(self.cells, np.float64, "cells")
+        pbc = _owned_array(self.pbc, np.int32, "pbc", allow_bool=True)
+        offsets = _owned_array(self.offsets, np.int64, "offsets")
         ids = tuple(str(value) for value in self.ids)
-        spins = None if self.spins is None else _array_snapshot(self.spins, np.float64, "spins")
-        charge_spin = None if self.charge_spin is None else _array_snapshot(self.charge_spin, np.float64,
-                                                                             "charge_spin")
+        spins = None if self.spins is None else _owned_array(self.spins, np.float64, "spins")
+        charge_spin = None if self.charge_spin is None else _owned_array(self.charge_spin, np.float64,
+                                                                          "charge_spin")
         if numbers.ndim != 1 or np.any(numbers <= 0):
             raise _input_error("numbers must be a one-dimensional array of positive atomic numbers", "numbers")
         if positions.shape != (len(numbers), 3):
@@ -72,13 +72,8 @@ class StructureBatch:
             raise _input_error("spins must have shape (total_atoms, 3)", "spins")
         if charge_spin is not None and charge_spin.shape != (len(ids), 2):
             raise _input_error("charge_spin must have shape (structures, 2)", "charge_spin")
-        for name, value in {
-            "numbers": numbers, "positions": positions, "cells": cells, "pbc": pbc, "offsets": offsets,
-            "ids": ids, "spins": spins, "charge_spin": charge_spin,
-        }.items():
-            if isinstance(value, np.ndarray):
-                value.setflags(write=False)
-            object.__setattr__(self, name, value)
+        _install(self, dict(numbers=numbers, positions=positions, cells=cells, pbc=pbc, offsets=offsets, ids=ids,
+                            spins=spins, charge_spin=charge_spin))
 
     @property
     def structures(self) -> int:
@@ -89,26 +84,19 @@ class StructureBatch:
         return len(self.numbers)
 
     def _slice_view(self, start: int, stop: int) -> StructureBatch:
-        """Read-only view of a complete structure range of a validated batch."""
+        """Structures [start, stop) of this validated batch as a read-only
+        batch sharing its arrays (no copy, no second validation)."""
 
-        if start < 0 or stop < start or stop > self.structures:
+        if not 0 <= start <= stop <= self.structures:
             raise ValueError("structure slice is outside the batch")
-        a0, a1 = int(self.offsets[start]), int(self.offsets[stop])
+        first_atom, end_atom = (int(self.offsets[i]) for i in (start, stop))
+        parts = {**{name: slice(first_atom, end_atom) for name in _PER_ATOM},
+                 **{name: slice(start, stop) for name in _PER_STRUCTURE}}
+        fields = {name: None if getattr(self, name) is None else getattr(self, name)[part]
+                  for name, part in parts.items()}
+        fields["offsets"] = (self.offsets[start:stop + 1] - first_atom).astype(np.int64)
         view = object.__new__(StructureBatch)
-        fields = {
-            "numbers": self.numbers[a0:a1],
-            "positions": self.positions[a0:a1],
-            "cells": self.cells[start:stop],
-            "pbc": self.pbc[start:stop],
-            "offsets": np.asarray(self.offsets[start:stop + 1] - a0, dtype=np.int64),
-            "ids": self.ids[start:stop],
-            "spins": None if self.spins is None else self.spins[a0:a1],
-            "charge_spin": None if self.charge_spin is None else self.charge_spin[start:stop],
-        }
-        for name, value in fields.items():
-            if isinstance(value, np.ndarray):
-                value.setflags(write=False)
-            object.__setattr__(view, name, value)
+        _install(view, fields)
         return view
 
     @classmethod
@@ -178,35 +166,51 @@ def _field(frame: Any, names: tuple[str, ...], index: int) -> Any:
                        {"cell": "cells", "id": "ids"}.get(names[0], names[0]))
 
 
-def _array_snapshot(value: Any, dtype: Any, name: str) -> np.ndarray:
-    try:
-        array = np.array(value, dtype=dtype, order="C", copy=True)
-    except (TypeError, ValueError, OverflowError) as exc:
-        raise _input_error(f"{name} must be a numeric array", name) from exc
-    if not np.isfinite(array).all():
-        raise _input_error(f"{name} must be finite", name)
-    return array
+# fields indexed by atom and by structure, for cutting a batch into
+# structure ranges (offsets are rebased separately)
+_PER_ATOM = ("numbers", "positions", "spins")
+_PER_STRUCTURE = ("cells", "pbc", "ids", "charge_spin")
 
 
-def _integer_snapshot(value: Any, dtype: Any, name: str, *, allow_bool: bool = False) -> np.ndarray:
+def _install(batch: StructureBatch, fields: dict[str, Any]) -> None:
+    """Set the fields of a frozen batch; its arrays become read-only."""
+
+    for name, value in fields.items():
+        if isinstance(value, np.ndarray):
+            value.setflags(write=False)
+        object.__setattr__(batch, name, value)
+
+
+def _owned_array(value: Any, dtype: Any, field: str, *, allow_bool: bool = False) -> np.ndarray:
+    """A private C-ordered copy of ``value`` as ``dtype``.
+
+    Floating fields must convert and be finite.  Integer fields accept
+    integer arrays, floats that are exact finite integers, and booleans
+    where ``allow_bool`` (pbc); the values must fit ``dtype``."""
+
+    if not np.issubdtype(dtype, np.integer):
+        try:
+            real = np.asarray(value, dtype=dtype)
+        except (TypeError, ValueError, OverflowError) as exc:
+            raise _input_error(f"{field} must be a numeric array", field) from exc
+        if not np.all(np.isfinite(real)):
+            raise _input_error(f"{field} must be finite", field)
+        return np.array(real, dtype=dtype, order="C", copy=True)
     try:
-        raw = np.asarray(value)
+        source = np.asarray(value)
     except (TypeError, ValueError, OverflowError) as exc:
-        raise _input_error(f"{name} must be an integer array", name) from exc
-    if raw.dtype.kind == "b":
-        if not allow_bool:
-            raise _input_error(f"{name} must contain integers, not booleans", name)
-    elif raw.dtype.kind in "iu":
-        pass
-    elif raw.dtype.kind == "f":
-        if not np.isfinite(raw).all() or not np.equal(raw, np.trunc(raw)).all():
-            raise _input_error(f"{name} must contain finite integers", name)
-    else:
-        raise _input_error(f"{name} must contain integers", name)
-    limits = np.iinfo(dtype)
-    if raw.size and (np.any(raw < limits.min) or np.any(raw > limits.max)):
-        raise _input_error(f"{name} contains values outside {dtype} range", name)
-    return np.array(raw, dtype=dtype, order="C", copy=True)
+        raise _input_error(f"{field} must be an integer array", field) from exc
+    kind = source.dtype.kind
+    if kind == "b" and not allow_bool:
+        raise _input_error(f"{field} must contain integers, not booleans", field)
+    if kind == "f" and not (np.all(np.isfinite(source)) and np.all(source == np.trunc(source))):
+        raise _input_error(f"{field} must contain finite integers", field)
+    if kind not in "biuf":
+        raise _input_error(f"{field} must contain integers", field)
+    bounds = np.iinfo(dtype)
+    if source.size and (source.min() < bounds.min or source.max() > bounds.max):
+        raise _input_error(f"{field} contains values outside {dtype} range", field)
+    return np.array(source, dtype=dtype, order="C", copy=True)
 
 
 def _input_error(message: str, field: str) -> _InputValidationError:

@@ -26,9 +26,8 @@ from typing import Any
 import numpy as np
 
 from ..core.backends import HipBackend
-from ..core.descriptor import Descriptor, _is_cancelled
-from ..core.errors import CancelledError, DescriptorConfigError, DescriptorInputError
-from ..core.input import coerce_batch
+from ..core.descriptor import Descriptor
+from ..core.errors import DescriptorConfigError, DescriptorInputError
 from ..core.options import CONFIGURATION_SCHEMA_VERSION, ExecutionOptions, OutputOptions, coerce_options
 from ..core.result import DescriptorResult, format_values, metadata_envelope, owned_values
 from ..core.species import require_species, validate_batch_species
@@ -357,16 +356,7 @@ class SOAP(Descriptor):
 
         from .. import _hip
 
-        self._ensure_open()
-        if _is_cancelled(control):
-            raise CancelledError("descriptor computation was cancelled")
-        try:
-            batch = coerce_batch(value)
-            self._validate_batch(batch)
-        except DescriptorInputError:
-            raise
-        except (TypeError, ValueError) as exc:
-            raise DescriptorInputError(str(exc), path=["input"]) from exc
+        batch = self._admit(value, control)
         try:
             target = _hip.DeviceArray(out)
             rows = batch.atoms if self._settings.average == "off" else batch.structures
@@ -380,8 +370,7 @@ class SOAP(Descriptor):
             raise
         except ValueError as exc:
             raise DescriptorInputError(str(exc), path=["input"]) from exc
-        if _is_cancelled(control):
-            raise CancelledError("descriptor computation was cancelled")
+        self._release(control)
         return out
 
     def close(self) -> None:

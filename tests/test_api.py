@@ -279,3 +279,56 @@ def test_batch_validation():
     assert batch.structures == 3 and batch.atoms == 9
     view = batch._slice_view(1, 3)
     assert view.offsets.tolist() == [0, 3, 6] and view.ids == ("w1", "w2")
+
+
+@pytest.mark.parametrize("species,message", [
+    (5, "species must be a sequence of atomic numbers"),
+    ([1, True], "species must contain integer atomic numbers"),
+    ([1, "x"], "species must contain integer atomic numbers"),
+    ([1, 2.5], "species must contain integer atomic numbers"),
+    ([1, float("nan")], "species must contain integer atomic numbers"),
+    ([], "species must be a non-empty sequence of unique atomic numbers"),
+    ([8, 8], "species must be a non-empty sequence of unique atomic numbers"),
+    ([0, 0], "species must be a non-empty sequence of unique atomic numbers"),
+    ([1, -8], "species must contain positive atomic numbers"),
+])
+def test_species_declaration_messages(species, message):
+    """Messages and path of the species contract (src/mdescriptor/core/species.py:16-58)."""
+
+    from mdescriptor_amd.core.species import normalize_species
+
+    with pytest.raises(mdx.DescriptorConfigError) as info:
+        normalize_species(species)
+    assert str(info.value) == message or info.value.message == message
+    assert list(info.value.path) == ["species"]
+
+
+def test_species_accepts_integral_values():
+    from mdescriptor_amd.core.species import normalize_species, validate_batch_species
+
+    assert normalize_species([np.int64(8), 1.0, "6"]) == (8, 1, 6)
+    assert normalize_species(None) is None
+    with pytest.raises(mdx.DescriptorInputError, match=r"outside its declaration: \[8\]"):
+        validate_batch_species(_water(), [1], descriptor="SOAP")
+
+
+def test_batch_field_conversion_messages():
+    base = dict(numbers=[1, 1], positions=np.zeros((2, 3)), cells=np.zeros((1, 3, 3)), pbc=[[0, 0, 0]],
+                offsets=[0, 2], ids=["a"])
+    for field, value, message in [
+        ("numbers", [True, True], "numbers must contain integers, not booleans"),
+        ("numbers", [1.5, 1.0], "numbers must contain finite integers"),
+        ("numbers", ["a", "b"], "numbers must contain integers"),
+        ("offsets", [0.0, 2.0], None),
+        ("pbc", [[False, False, False]], None),
+        ("positions", [["x", 0, 0], [0, 0, 0]], "positions must be a numeric array"),
+        ("positions", np.full((2, 3), np.inf), "positions must be finite"),
+        ("numbers", [2**40, 1], "numbers contains values outside"),
+    ]:
+        kwargs = dict(base, **{field: value})
+        if message is None:
+            mdx.StructureBatch(**kwargs)
+            continue
+        with pytest.raises(ValueError, match=message) as info:
+            mdx.StructureBatch(**kwargs)
+        assert list(info.value.path) == ["input", field]
