@@ -22,6 +22,10 @@ chemistry.
 
 from __future__ import annotations
 
+import multiprocessing
+import os
+import sys
+from concurrent.futures import ProcessPoolExecutor
 from dataclasses import dataclass
 from typing import Any
 
@@ -151,75 +155,161 @@ def hcno_cells(cells_count: int = 16, natoms: int = 4096) -> Workload:
                                                                average="off", dtype="float32"))
 
 
-def molecules(count: int = 20000) -> Workload:
-    """Configuration 3: isolated molecules grown by random self-avoiding steps."""
+_VALENCE = {6: 4, 7: 3, 8: 2, 9: 1}
+# tetrahedral bond directions: the bonds of a heavy atom point along the
+# first `valence` of them (the first facing the atom's parent)
+_TETRAHEDRON = np.array([[1.0, 1.0, 1.0], [1.0, -1.0, -1.0], [-1.0, 1.0, -1.0], [-1.0, -1.0, 1.0]]) / np.sqrt(3.0)
 
-    rng = _rng(3)
+
+def _rotation_to(u: np.ndarray, v: np.ndarray) -> np.ndarray:
+    """A rotation taking unit vector u onto unit vector v."""
+
+    axis = np.cross(u, v)
+    s, c = np.linalg.norm(axis), float(np.dot(u, v))
+    if s < 1e-12:
+        if c > 0:
+            return np.eye(3)
+        # half turn about any axis normal to u
+        normal = np.cross(u, [1.0, 0.0, 0.0] if abs(u[0]) < 0.9 else [0.0, 1.0, 0.0])
+        normal /= np.linalg.norm(normal)
+        return 2.0 * np.outer(normal, normal) - np.eye(3)
+    k = axis / s
+    kx = np.array([[0.0, -k[2], k[1]], [k[2], 0.0, -k[0]], [-k[1], k[0], 0.0]])
+    return np.eye(3) + s * kx + (1.0 - c) * kx @ kx
+
+
+def _random_rotations(rng: np.random.Generator, count: int) -> np.ndarray:
+    """`count` uniformly random rotation matrices (unit quaternions)."""
+
+    q = rng.normal(size=(count, 4))
+    q /= np.linalg.norm(q, axis=1, keepdims=True)
+    a, b, c, d = q.T
+    return np.stack([
+        np.stack([a * a + b * b - c * c - d * d, 2 * (b * c - a * d), 2 * (b * d + a * c)], -1),
+        np.stack([2 * (b * c + a * d), a * a - b * b + c * c - d * d, 2 * (c * d - a * b)], -1),
+        np.stack([2 * (b * d - a * c), 2 * (c * d + a * b), a * a - b * b - c * c + d * d], -1),
+    ], 1)
+
+
+def _twisted(directions: np.ndarray, axis: np.ndarray, angles: np.ndarray) -> np.ndarray:
+    """directions (k, 3) rotated about the unit axis by each angle: (R, k, 3)."""
+
+    cos, sin = np.cos(angles)[:, None, None], np.sin(angles)[:, None, None]
+    along = (directions @ axis)[None, :, None] * axis
+    return directions[None] * cos + np.cross(axis, directions)[None] * sin + along * (1.0 - cos)
+
+
+def _grow_molecule(rng: np.random.Generator, target: int) -> tuple[np.ndarray, np.ndarray] | None:
+    """One molecule of exactly `target` atoms, or None when this attempt
+    fails (the caller regrows).
+
+    Topology: a tree of heavy atoms (C/N/O/F drawn independently with
+    probabilities 0.70/0.15/0.12/0.03) grows from an atom with free valence,
+    the newest one with probability 0.7 so that chains grow away from the
+    rest; a heavy atom of valence v adds v - 1 atoms to the saturated size
+    sum(v) - h + 2, so heavy atoms are added until the saturated size
+    reaches the target (an overshoot fails the attempt), and every free
+    valence carries one H.
+
+    Geometry, heavy atoms in growth order: an atom's bonds point along a
+    tetrahedron whose first vertex faces its parent, twisted about that bond
+    at random, each bond 1.0-1.5 A long.  Of 128 random twists and lengths
+    whose new atoms keep 1.8 A from every atom but their bonded parent (and
+    from each other), the least crowded by the atoms already placed (sum of
+    d^-6) is taken; when none does, the attempt fails."""
+
     heavy_choice = np.array([6, 7, 8, 9])
     heavy_prob = np.array([0.70, 0.15, 0.12, 0.03])
-    valence = {6: 4, 7: 3, 8: 2, 9: 1}
-    numbers, positions = [], []
-    for _ in range(count):
-        target = int(rng.integers(9, 30))
-        n_heavy = max(1, int(round(target / 3.0)))
-        elements: list[int] = []
-        coords: list[np.ndarray] = []
-        bonds_left: list[int] = []
-
-        def place(parent: int | None) -> np.ndarray | None:
-            for _attempt in range(64):
-                if parent is None:
-                    return np.zeros(3)
-                direction = rng.normal(size=3)
-                direction /= np.linalg.norm(direction)
-                trial = coords[parent] + direction * rng.uniform(1.0, 1.5)
-                others = [c for i, c in enumerate(coords) if i != parent]
-                if not others or np.min(np.linalg.norm(np.asarray(others) - trial, axis=1)) >= 1.8:
-                    return trial
+    heavy = [int(rng.choice(heavy_choice, p=heavy_prob))]
+    parent_of = [-1]
+    free = [_VALENCE[heavy[0]]]
+    size = free[0] + 1
+    while size < target:
+        element = int(rng.choice(heavy_choice, p=heavy_prob))
+        open_atoms = [i for i, f in enumerate(free) if f > 0]
+        if not open_atoms or size + _VALENCE[element] - 1 > target:
             return None
+        parent = open_atoms[-1] if rng.random() < 0.7 else open_atoms[int(rng.integers(len(open_atoms)))]
+        heavy.append(element)
+        parent_of.append(parent)
+        free.append(_VALENCE[element] - 1)
+        free[parent] -= 1
+        size += _VALENCE[element] - 1
 
-        for h in range(n_heavy):
-            element = int(rng.choice(heavy_choice, p=heavy_prob))
-            if h == 0:
-                parents = [None]
-            else:
-                parents = [i for i, b in enumerate(bonds_left) if b > 0 and elements[i] != 1]
-                rng.shuffle(parents)
-                if not parents:
-                    break
-            placed = False
-            for parent in parents:
-                pos = place(parent)
-                if pos is not None:
-                    coords.append(pos)
-                    elements.append(element)
-                    bonds_left.append(valence[element] - (0 if parent is None else 1))
-                    if parent is not None:
-                        bonds_left[parent] -= 1
-                    placed = True
-                    break
-            if not placed:
-                break
-        while len(elements) < target:
-            parents = [i for i, b in enumerate(bonds_left) if b > 0 and elements[i] != 1]
-            if not parents:
-                parents = [i for i, e in enumerate(elements) if e != 1]
-            rng.shuffle(parents)
-            added = False
-            for parent in parents:
-                pos = place(parent)
-                if pos is not None:
-                    coords.append(pos)
-                    elements.append(1)
-                    bonds_left.append(0)
-                    bonds_left[parent] -= 1
-                    added = True
-                    break
-            if not added:
-                break
-        numbers.append(np.asarray(elements))
-        positions.append(np.asarray(coords) + rng.uniform(-20.0, 20.0, size=3))
-    batch = _pack(numbers, positions, [np.zeros((3, 3))] * count, [[0, 0, 0]] * count, "molecule")
+    elements = np.empty(target, dtype=np.int64)
+    coords = np.empty((target, 3))
+    slot = [0] * len(heavy)  # atom index of each heavy atom
+    elements[0], coords[0] = heavy[0], 0.0
+    placed = 1
+    trials = 128
+    for h in range(len(heavy)):
+        centre = coords[slot[h]]
+        children = [c for c in range(len(heavy)) if parent_of[c] == h]
+        bonds = [heavy[c] for c in children] + [1] * free[h]
+        k = len(bonds)
+        if k == 0:
+            continue
+        p = parent_of[h]
+        # `trials` candidate arrangements of the k bonds at once
+        if p >= 0:
+            back = coords[slot[p]] - centre
+            back /= np.linalg.norm(back)
+            base = (_rotation_to(_TETRAHEDRON[0], back) @ _TETRAHEDRON[1:1 + k].T).T
+            directions = _twisted(base, back, rng.uniform(0.0, 2.0 * np.pi, size=trials))
+        else:
+            directions = np.einsum("rij,kj->rki", _random_rotations(rng, trials), _TETRAHEDRON[:k])
+        positions = centre + directions * rng.uniform(1.0, 1.5, size=(trials, k, 1))
+        # 1.8 A from every placed atom but this centre, and between the new atoms
+        d2 = np.sum((positions[:, :, None, :] - coords[None, None, :placed, :]) ** 2, axis=3)
+        d2[:, :, slot[h]] = np.inf
+        clear = np.all(d2 >= 1.8 * 1.8, axis=(1, 2))
+        if k > 1:
+            mutual = np.sum((positions[:, :, None, :] - positions[:, None, :, :]) ** 2, axis=3)
+            mutual[:, np.arange(k), np.arange(k)] = np.inf
+            clear &= np.all(mutual >= 1.8 * 1.8, axis=(1, 2))
+        if not np.any(clear):
+            return None
+        crowding = np.where(clear, np.sum(1.0 / d2 ** 3, axis=(1, 2)), np.inf)
+        coords[placed:placed + k] = positions[int(np.argmin(crowding))]
+        elements[placed:placed + k] = bonds
+        for b, c in enumerate(children):
+            slot[c] = placed + b
+        placed += k
+    return elements, coords
+
+
+def _molecule(seed: np.random.SeedSequence) -> tuple[np.ndarray, np.ndarray]:
+    """One configuration-3 molecule from its own seed: a size drawn uniformly
+    in 9-29, grown (and regrown) until it has exactly that many atoms, then
+    placed at a random offset in a 40 A box."""
+
+    rng = np.random.Generator(np.random.PCG64(seed))
+    target = int(rng.integers(9, 30))
+    grown = None
+    while grown is None:
+        grown = _grow_molecule(rng, target)
+    elements, coords = grown
+    return elements, coords + rng.uniform(-20.0, 20.0, size=3)
+
+
+def molecules(count: int = 20000) -> Workload:
+    """Configuration 3: isolated molecules of 9-29 atoms (uniform), grown by
+    random self-avoiding steps.  Each molecule has its own seed, spawned
+    from the configuration's, so the batch is the same whether it is grown
+    in this process or, for large counts run from a script file, by a pool
+    of spawned (never forked) worker processes."""
+
+    seeds = np.random.SeedSequence(SEED_BASE + 3).spawn(count)
+    main = sys.modules.get("__main__")
+    main_file = getattr(main, "__file__", None)
+    workers = min(16, os.cpu_count() or 1)
+    if count >= 2000 and workers > 1 and main_file is not None and os.path.isfile(main_file):
+        with ProcessPoolExecutor(max_workers=workers, mp_context=multiprocessing.get_context("spawn")) as pool:
+            grown = list(pool.map(_molecule, seeds, chunksize=max(1, count // (4 * workers))))
+    else:
+        grown = [_molecule(seed) for seed in seeds]
+    batch = _pack([g[0] for g in grown], [g[1] for g in grown], [np.zeros((3, 3))] * count, [[0, 0, 0]] * count,
+                  "molecule")
     return Workload(f"molecules-{count}", batch, dict(species=[1, 6, 7, 8, 9], r_cut=5.0, n_max=6, l_max=4,
                                                       average="inner", dtype="float64"))
 

@@ -432,6 +432,28 @@ def test_full_config2_structure_against_oracle(hip_context, oracle):
         assert scaled_error(rows, expected) <= F32_GATE
 
 
+@pytest.mark.parametrize("index", [1, 3, 4])
+def test_full_size_configs_match_oracle(hip_context, oracle, index):
+    """Seeded full-size configurations 1 (12,288 water atoms), 3 (20,000
+    molecules, structure averages) and 4 (32,000-atom alloy) against the
+    oracle over the whole batch, at each configuration's own average mode
+    and output type."""
+
+    work = workloads.config(index)
+    p = work.params
+    print(f"config {index} ({work.name}): {work.batch.atoms} atoms", flush=True)
+    plan, basis = _plan(hip_context, p)
+    try:
+        values, timing = plan.compute(work.batch)
+    finally:
+        plan.close()
+    expected = _oracle_soap(oracle, work.batch, p, basis, p["average"])
+    assert values.shape == expected.shape and values.dtype == np.dtype(p["dtype"])
+    assert np.all(np.isfinite(values))
+    error = scaled_error(values, expected)
+    assert error <= (F64_GATE if p["dtype"] == "float64" else F32_GATE), f"scaled error {error:.3e}"
+
+
 def test_supercell_replication_at_full_size(hip_context):
     """A periodic cell tiled 2x2x2 gives every image the same features as its
     original atom (the 32000-atom HEA size, built from a 4000-atom cell)."""
