@@ -395,6 +395,13 @@ constexpr int kSegments = kMaxSpecies * 27;
 constexpr int kNoBoundary = 0x7fffffff;
 constexpr int kNbrCount = 0, kNbrFill = 1, kNbrSlotted = 2;
 
+// a wave-uniform 64-bit value in scalar registers
+__device__ inline int64_t uniform_i64(int64_t v) {
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v)));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v >> 32)));
+    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 __device__ inline uint64_t lane_range(int lo, int hi) {
     // bits lo .. hi-1 of a 64-lane mask, 0 <= lo <= hi <= 64
     const uint64_t upto_hi = hi >= 64 ? ~0ull : ((1ull << hi) - 1ull);
@@ -420,12 +427,12 @@ __global__ __launch_bounds__(kNbrThreads) void k_neighbors(
     __shared__ double s_cpos[kCentreBatch * 3]; // centre positions of the batch
     __shared__ int64_t s_first[kCentreBatch];   // first output row of each centre (fill pass)
     __shared__ int32_t s_found[kCentreBatch];
+    __shared__ int32_t s_limit[kCentreBatch];   // rows of each centre (fill pass)
     // rows of a centre before species boundary t (count pass)
     __shared__ int32_t s_bfound[kCentreBatch * kMaxSpecies];
     const int tid = threadIdx.x;
     const int lane = tid % kWave;
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
     const int nseg = S * 27;
     for (int64_t c = blockIdx.x; c < cells_total; c += gridDim.x) {
         const int64_t c0 = cell_centre_start[c], c1 = cell_centre_start[c + 1];
@@ -489,6 +496,7 @@ __global__ __launch_bounds__(kNbrThreads) void k_neighbors(
                 s_cpos[i * 3 + 1] = positions[static_cast<int64_t>(centre) * 3 + 1];
                 s_cpos[i * 3 + 2] = positions[static_cast<int64_t>(centre) * 3 + 2];
                 s_first[i] = kFill ? pair_start[centre] : kMode == kNbrSlotted ? centre * cap : 0;
+                if (kFill) s_limit[i] = totals[centre];
                 s_found[i] = 0;
             }
             for (int i = tid; i < nb * S; i += kNbrThreads) s_bfound[i] = 0;
@@ -537,7 +545,12 @@ __global__ __launch_bounds__(kNbrThreads) void k_neighbors(
                     const double py = s_cpos[ci * 3 + 1];
                     const double pz = s_cpos[ci * 3 + 2];
                     int32_t found = s_found[ci];
-                    const int64_t first_row = s_first[ci];
+                    // the centre's rows: from its first row, at most its counted
+                    // total (fill) or the slot capacity (slotted)
+                    const int64_t first_row = kWrite ? uniform_i64(s_first[ci]) : 0;
+                    const int64_t limit = kFill ? s_limit[ci] : kWrite ? cap : 0;
+                    const __amdgpu_buffer_rsrc_t rows = __builtin_amdgcn_make_buffer_rsrc(
+                        pair_bin + first_row, 0, static_cast<int>(limit * sizeof(uint32_t)), 0x00020000);
                     // next species boundary of the walk at or after v0 (count pass)
                     int t_next = 1;
                     int bnext = kNoBoundary;
@@ -548,8 +561,12 @@ __global__ __launch_bounds__(kNbrThreads) void k_neighbors(
                     // bookkeeping of one wavefront-wide group of candidates at i0
                     auto account = [&](int i0, bool accept, uint64_t mask, uint32_t b) {
                         if (kWrite && accept) {
-                            const int32_t k = found + static_cast<int32_t>(__popcll(mask & below));
-                            if (kFill || k < cap) pair_bin[first_row + k] = b;
+                            // row = rows so far + accepted lanes below this one; the
+                            // descriptor's range drops rows past the slot capacity
+                            const uint32_t row = __builtin_amdgcn_mbcnt_hi(
+                                static_cast<uint32_t>(mask >> 32),
+                                __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), static_cast<uint32_t>(found)));
+                            __builtin_amdgcn_raw_buffer_store_b32(b, rows, static_cast<int>(row * sizeof(uint32_t)), 0, 0);
                         }
                         if (kCount) {
                             while (bnext < v0 + i0 + kWave) {

@@ -60,7 +60,8 @@ namespace mdx {
 namespace {
 
 constexpr int kYS = kNb + 1;       // harmonic staging: entry h of slot j at h * kYS + j
-constexpr int kTab = 64;           // 2^(j/64) table entries
+constexpr int kTabBits = 8;
+constexpr int kTab = 1 << kTabBits; // 2^(j/256) table entries
 // Power-spectrum feature offsets are packed as (byte offset << 9) | feature
 // stride per degree; a pair that is not stored gets kDroppedBytes, past the
 // end of every row this kernel writes (the buffer range check drops the
@@ -98,7 +99,10 @@ struct BlockPlan {
     static constexpr int GS = 4 * P;            // slots per step group
     static constexpr int GROUPS = kNb / GS;     // step groups per chunk
     static constexpr int T = L < 4 ? L : 4;     // wavefronts
-    static constexpr int YROWS = H + 3;         // staged harmonic rows (pad columns of degree LM read up to H + 2)
+    // staged harmonic rows; the pad columns of degree LM (up to 3) read
+    // the rows that follow a buffer: the next buffer's first rows, or after
+    // the second buffer the d2 and exp tables, all finite
+    static constexpr int YROWS = H;
     static constexpr int YWORDS = YROWS * kYS;
 #ifndef MDX_BLOCK_HARMONIC_WAVES
 #define MDX_BLOCK_HARMONIC_WAVES 1
@@ -237,30 +241,31 @@ __device__ __forceinline__ double swap_blocks(double v) {
 
 // exp(x) for x = na * d2 (na = -a <= 0, d2 >= 0, x >= -708): x is rounded
 // exactly as the reference's exp(-a * d2) argument (soap.cpp:895-896), then
-// Tang's table method (ACM TOMS 15(2), 1989): x = (64k + j) ln2/64 + r with
-// the reduction against ln2/64 split in two (kf * hi exact), |r| <= ln2/128,
-// exp(x) = 2^k 2^(j/64) e^r, e^r - 1 by its degree-5 Taylor polynomial
-// (truncation below 4e-17 relative).  tab[j] = 2^(j/64) with j << 14 taken
-// off its high word, so that adding (64k + j) << 14 scales it by 2^k in one
-// integer add (the result is a normal number for x >= -708).
+// Tang's table method (ACM TOMS 15(2), 1989) with 256 entries:
+// x = (256k + j) ln2/256 + r, the reduction against ln2/256 split in two
+// (kf * hi exact for |kf| < 2^21), |r| <= ln2/512, exp(x) = 2^k 2^(j/256) e^r
+// with e^r - 1 by its degree-4 Taylor polynomial (truncation below 4e-17
+// relative).  tab[j] = 2^(j/256) with j << 12 taken off its high word, so
+// that adding (256k + j) << 12 scales it by 2^k in one integer add (the
+// result is a normal number for x >= -708).
 __device__ __forceinline__ double exp_neg(double d2, double na, const int2* tab) {
-    constexpr double kInvLn2x64 = 92.332482616893658071035179584121; // 64 / ln 2
-    constexpr double kHi = 0.010830417275428772;                      // ln2/64, 32 trailing zero bits
-    constexpr double kLo = 7.420820373486988e-09;                     // ln2/64 - kHi
-    constexpr double kShifter = 6755399441055744.0;                   // 1.5 * 2^52
+    constexpr double kInvLn2xT = 369.32993046757463228414071833648; // 256 / ln 2
+    constexpr double kHi = 0.010830417275428772 / 4.0;               // ln2/256, 32 trailing zero bits
+    constexpr double kLo = 7.420820373486988e-09 / 4.0;              // ln2/256 - kHi
+    constexpr double kShifter = 6755399441055744.0;                  // 1.5 * 2^52
     const double x = na * d2;
-    const double s = fma(x, kInvLn2x64, kShifter);
+    const double s = fma(x, kInvLn2xT, kShifter);
     const double kf = s - kShifter;
     double r = fma(kf, -kHi, x);
     r = fma(kf, -kLo, r);
     const int nj = __double2loint(s);
-    const int2 t = *reinterpret_cast<const int2*>(reinterpret_cast<const char*>(tab) + ((nj << 3) & 0x1f8));
-    double q = fma(r, 1.0 / 120.0, 1.0 / 24.0);
-    q = fma(q, r, 1.0 / 6.0);
+    const int2 t = *reinterpret_cast<const int2*>(reinterpret_cast<const char*>(tab) +
+                                                  ((nj << 3) & ((kTab - 1) << 3)));
+    double q = fma(r, 1.0 / 24.0, 1.0 / 6.0);
     q = fma(q, r, 0.5);
     q = fma(q, r, 1.0);
     const double em1 = r * q; // e^r - 1
-    const double tk = __hiloint2double(t.y + (nj << 14), t.x); // 2^k 2^(j/64)
+    const double tk = __hiloint2double(t.y + (nj << (20 - kTabBits)), t.x); // 2^k 2^(j/256)
     return fma(tk, em1, tk);
 }
 
@@ -392,10 +397,11 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
     // that no merge of a loaded value forces an early wait for it.
     auto prefetch_centre = [&](int64_t c) {
         if (c < item_last) {
-            // the lane offset is recomputed here rather than kept live as a
-            // 64-bit address across the whole loop
-            int t = min(lane, S - 1);
-            asm volatile("" : "+v"(t));
+            // the lane (species) index is recomputed here rather than kept
+            // live across the whole loop
+            int t;
+            asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(t));
+            t = min(t, S - 1);
             pre_count = a.counts[c * S + t];
             pre_start = a.pair_start[c];
         }
@@ -697,15 +703,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) void k
     double* s_d2 = s_y + 2 * PL::YWORDS;
     int2* s_tab = reinterpret_cast<int2*>(s_d2 + 2 * kNb);
     double* s_scale = s_d2 + 2 * kNb + kTab;
-    // pad rows of both staging buffers stay finite (zero); the scaled
-    // harmonics table and the exp table
-    for (int i = tid; i < 2 * 3 * kYS; i += threads) {
-        const int b = i / (3 * kYS), e = i - b * 3 * kYS;
-        s_y[b * PL::YWORDS + PL::H * kYS + e] = 0.0;
-    }
+    // the first rows of the second staging buffer, which the pad columns
+    // of the first chunk read, start finite (zero); the exp table
+    for (int i = tid; i < 3 * kYS; i += threads) s_y[PL::YWORDS + i] = 0.0;
     for (int i = tid; i < kTab; i += threads) {
         const double t = exp2(static_cast<double>(i) / kTab);
-        s_tab[i] = int2{__double2loint(t), __double2hiint(t) - (i << 14)};
+        s_tab[i] = int2{__double2loint(t), __double2hiint(t) - (i << (20 - kTabBits))};
     }
     {
         // S_lm of padded column i (degree l's block at 4 sum_{l' < l} cg(l'),
@@ -844,7 +847,6 @@ bool block_plan_tables(int S, int n, int l_max, int out_dtype, const std::vector
     // index at l = 0 and its stride per degree for channel i (group 4 ri + r,
     // radial channel 4 rg + lane / 16) and channel j (group 4 rj + (lane % 16) / 4,
     // 4 rg + lane % 4); pairs i > j and pad channels get kDroppedBytes
-    const int W = S * n;
     auto channel = [&](int ri, int slot, int nl) -> int {
         int t = 0, rg = 0;
         if (kg == 3) {
@@ -901,7 +903,7 @@ size_t block_lds_bytes(int l_max, int kg) {
     const int L = l_max + 1, H = L * L;
     int pad = 0;
     for (int l = 0; l < L; ++l) pad += 4 * cgroups(l);
-    return static_cast<size_t>(2 * (H + 3) * kYS + 2 * kNb + kTab + pad) * sizeof(double);
+    return static_cast<size_t>(2 * H * kYS + 2 * kNb + kTab + pad) * sizeof(double);
     (void)kg;
 }
 

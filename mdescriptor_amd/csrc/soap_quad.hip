@@ -70,7 +70,6 @@ constexpr double kExpC2 = kExpC1 * kExpC1 / 2.0;
 constexpr double kExpC3 = kExpC2 * kExpC1 / 3.0;
 constexpr double kExpC4 = kExpC3 * kExpC1 / 4.0;
 constexpr double kExpC5 = kExpC4 * kExpC1 / 5.0;
-constexpr double kExpScale = 64.0 / 0.693147180559945309417232121458176568; // e1 = -a * kExpScale
 __device__ __forceinline__ double exp_neg_scaled(double d2, double e1, const int2* tab) {
     constexpr double kShifter = 6755399441055744.0; // 1.5 * 2^52
     const double s = fma(d2, e1, kShifter);
@@ -220,11 +219,7 @@ void k_soap_quad(
     // step differ).  Wavefront w of every workgroup tends to land on the same
     // SIMD of a CU, so the roles rotate with the workgroup index: the
     // workgroups sharing a CU spread each role over its SIMDs.
-#ifndef MDX_QUAD_ROTATE
-#define MDX_QUAD_ROTATE 1
-#endif
-    const int wave = __builtin_amdgcn_readfirstlane(MDX_QUAD_ROTATE ? (tid / kWaveThreads + static_cast<int>(blockIdx.x)) % T
-                                                                    : tid / kWaveThreads);
+    const int wave = __builtin_amdgcn_readfirstlane((tid / kWaveThreads + static_cast<int>(blockIdx.x)) % T);
     const int H = d.H, L = d.L, S = d.S, n = d.n;
     const int hp = d.hpad;          // padded c row
     const int cp = d.cpitch;        // its LDS pitch (odd)
