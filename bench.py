@@ -8,9 +8,20 @@ uploaded once before timing; the output stays on the device.
 
 Prints one JSON line with the metric of BASELINE.json, a ``roofline`` object
 for the dominant kernel (the expansion kernel, FP64: its algorithmic flops
-per launch over its launch time from HIP events on the library's stream) and
-a ``cpu_baseline`` object (the reference's own C++ SOAP compiled in place,
-``oracle/_ref``, timed on this host's cores on a bounded sample).
+per launch over its launch time from HIP events on the library's stream;
+``profile_launch_ms`` is the same kernel's average in the committed rocprofv3
+kernel-trace summary ``profiles/<kernel>_<workload>_kernel_trace.md``, for a
+cross-check) and a ``cpu_baseline`` object: the reference's own C++ SOAP
+compiled in place (``oracle/_ref``) on this host, decomposed as the reference
+does (structures in parallel, threads capped at the structure count; one
+structure: centres in parallel), on OMP_NUM_THREADS threads (else every CPU
+the process may use), with the host's CPU count, model and OMP_NUM_THREADS.
+Its sample is the whole batch, except for configuration 5 a 46,656-atom cell
+of the same generator.
+
+``--config N`` selects benchmark configuration 1-5 (default 2, the headline);
+``--options NAME`` runs the line with SOAP options (mu1nu1 compression, pow
+weighting with w0, crossover with exp weighting) on that configuration.
 
 ``roofline.traffic`` (HBM bytes per launch of that kernel) is read from the
 committed counter summary ``profiles/<kernel>_<workload>_traffic.txt``
@@ -50,12 +61,63 @@ FP64_PEAK_TFLOPS = 78.6  # MI355X dense FP64 (vector and MFMA)
 HBM_PEAK_GBS = 8000.0
 
 
-def flops_per_env(kbar: float, S: int, n: int, l_max: int) -> float:
-    """Algorithmic FP64 flops per environment (FMA = 2): accumulation
-    2*K*n*H, beta contraction 2*S*n^2*H, power spectrum S*n*(S*n+1)*H."""
+# SOAP options of the option bench lines (--options): the parameters of the
+# option parity cases
+BENCH_OPTIONS = {
+    "off": None,
+    "mu1nu1": {"compression": "mu1nu1"},
+    "pow_w0": {"weighting": {"function": "pow", "r0": 2.0, "c": 2.0, "d": 1.0, "m": 3.0, "w0": 0.5}},
+    "crossover": {"compression": "crossover", "weighting": {"function": "exp", "r0": 2.0, "c": 1.0, "d": 0.2}},
+}
 
-    H = (l_max + 1) ** 2
-    return 2.0 * kbar * n * H + 2.0 * S * n * n * H + S * n * (S * n + 1) * H
+
+def flops_per_env(kbar: float, S: int, n: int, l_max: int, features: int | None = None,
+                  coefficient_species: int | None = None, spectra_per_env: float = 1.0) -> float:
+    """Algorithmic FP64 flops per environment (FMA = 2): accumulation
+    2*K*n*H, beta contraction 2*Sc*n^2*H (Sc coefficient species: 1 for mu2,
+    else S), power spectrum 2*(2l+1) per feature of degree l, i.e.
+    features/(l_max+1) * 2H (with compression off S*n*(S*n+1)*H), taken
+    `spectra_per_env` times per environment.""" 
+
+    L = l_max + 1
+    H = L * L
+    if features is None:
+        features = S * n * (S * n + 1) // 2 * L
+    sc = S if coefficient_species is None else coefficient_species
+    return 2.0 * kbar * n * H + 2.0 * sc * n * n * H + spectra_per_env * features / L * 2.0 * H
+
+
+def profile_average_us(workload_name: str, kernel: str) -> tuple[float | None, str | None]:
+    """Average duration of `kernel` in the committed rocprofv3 kernel-trace
+    summary of this workload (the ``| name | calls | average us |`` table)."""
+
+    path = ROOT / "profiles" / f"{kernel.split('<')[0]}_{workload_name}_kernel_trace.md"
+    if not path.is_file():
+        return None, None
+    for line in path.read_text().splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 3 and cells[0].startswith(kernel):
+            try:
+                return float(cells[2]), str(path.relative_to(ROOT))
+            except ValueError:
+                continue
+    return None, None
+
+
+def host_facts() -> dict:
+    """The host the CPU baseline ran on: logical CPUs, the ones this process
+    may use, OMP_NUM_THREADS and the CPU model."""
+
+    model = None
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)),
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS"), "cpu_model": model}
 
 
 def traffic_from_profile(workload_name: str, kernel: str = "k_soap_mfma") -> tuple[float | None, str | None]:
@@ -105,30 +167,53 @@ def end_to_end(plan, batch, repeats: int = 3) -> dict:
     return report
 
 
-def cpu_baseline(workload, alphas, betas, threads: int, budget_s: float = 30.0) -> dict:
+def cpu_sample(index: int, workload):
+    """The batch the CPU baseline times: the whole benchmark batch, except
+    for configuration 5 (216,000 atoms, minutes of CPU time) a 46,656-atom
+    cell of the same generator (same density, displacements and species)."""
+
+    from mdescriptor_amd import workloads
+
+    if index == 5:
+        return workloads.liquid_si(18)
+    return workload
+
+
+def cpu_baseline(index: int, workload, alphas, betas, threads: int, options: dict | None,
+                 budget_s: float = 30.0) -> dict:
+    """The reference's SOAP (compiled in place under oracle/_ref; else the
+    oracle port) on this host, as the reference runs it: structures in
+    parallel (threads capped at the structure count) or, for one structure,
+    centres in parallel."""
+
     from oracle import oracle
 
     kind = "reference" if oracle.reference_available() else "port"
+    sample = cpu_sample(index, workload)
     p = workload.params
-    batch = workload.batch
+    batch = sample.batch
     times = []
     while True:
         t0 = time.perf_counter()
         oracle.soap(batch, species=p["species"], n_max=p["n_max"], l_max=p["l_max"], r_cut=p["r_cut"],
                     sigma=1.0, alphas=alphas, betas=betas, average=p["average"], num_threads=threads,
-                    kind="ref" if kind == "reference" else "oracle")
+                    kind="ref" if kind == "reference" else "oracle", options=options)
         times.append(time.perf_counter() - t0)
         if len(times) >= 3 or sum(times) + times[-1] > budget_s:
             break
     seconds = statistics.median(times)
+    used = min(threads, batch.structures) if batch.structures > 1 else threads
+    decomposition = (f"structure-parallel over {batch.structures} structures" if batch.structures > 1
+                     else "centre-parallel over one structure")
     return {
         "value": batch.atoms / seconds,
         "unit": "atom-envs/s",
-        "cores": threads,
+        "cores": used,
         "kind": kind,
-        "sample": (f"full {workload.name} batch ({batch.atoms} envs, {batch.structures} structures), "
-                   f"reference decomposition (structure-parallel, threads capped at structures), "
-                   f"float64 compute, median of {len(times)} run(s) of {seconds:.2f}s"),
+        "sample": (f"{sample.name} ({batch.atoms} envs, {batch.structures} structures), {decomposition}, "
+                   f"{used} of {threads} threads, float64 compute, median of {len(times)} run(s) of "
+                   f"{seconds:.2f}s"),
+        "host": host_facts(),
     }
 
 
@@ -236,7 +321,7 @@ def neighbor_list_bench(args, workload) -> dict:
         from oracle import oracle
 
         kind = "reference" if oracle.reference_available() else "port"
-        threads = args.cpu_threads or min(len(os.sched_getaffinity(0)), 16)
+        threads = args.cpu_threads or int(os.environ.get("OMP_NUM_THREADS") or 0) or len(os.sched_getaffinity(0))
         times = []
         while True:
             t1 = time.perf_counter()
@@ -249,10 +334,11 @@ def neighbor_list_bench(args, workload) -> dict:
         result["cpu_baseline"] = {
             "value": len(table) / seconds,
             "unit": "pairs/s",
-            "cores": threads if kind == "reference" else 1,
+            "cores": threads,
             "kind": kind,
             "sample": f"full {workload.name} batch ({len(table)} pairs), median of {len(times)} run(s) of "
                       f"{seconds:.3f}s",
+            "host": host_facts(),
         }
     values.free()
     samples.free()
@@ -261,41 +347,21 @@ def neighbor_list_bench(args, workload) -> dict:
     return result
 
 
-def main() -> int:
-    parser = argparse.ArgumentParser(description=__doc__)
-    parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=20)
-    parser.add_argument("--warmup", type=int, default=3)
-    parser.add_argument("--config", type=int, default=2, help="benchmark configuration 1-5 (default 2)")
-    parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--cpu-threads", type=int, default=0)
-    parser.add_argument("--no-end-to-end", action="store_true")
-    parser.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB")
-    parser.add_argument("--path", choices=("soap", "neighbor-list"), default="soap")
-    parser.add_argument("--nl-cutoff", type=float, default=6.0)
-    parser.add_argument("--half", action="store_true", help="neighbor-list path: half list")
-    args = parser.parse_args()
-    if args.calibrate_copy:
-        return calibrate_copy(args.calibrate_copy)
-    if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only; the SOAP path shards by structure or "
-                                   "centre range across GPUs (see DESIGN.md) but no multi-GPU run is provided",
-                          "n_gpus": args.gpus}))
-        return 2
+def soap_bench(args, workload) -> dict:
+    """One configuration's SOAP line: `steps` device-resident runs of the hot
+    path (graph + expansion + write) after `warmup` untimed ones."""
 
-    from mdescriptor_amd import _hip, workloads
+    from mdescriptor_amd import _hip
     from mdescriptor_amd.descriptors.basis import basis_gto
 
-    workload = workloads.config(args.config)
-    if args.path == "neighbor-list":
-        print(json.dumps(neighbor_list_bench(args, workload)))
-        return 0
     p = workload.params
     batch = workload.batch
+    options = BENCH_OPTIONS[args.options]
     alphas, betas = basis_gto(p["r_cut"], p["n_max"], p["l_max"])
     ctx = _hip.Context(0)
     plan = _hip.SoapPlan(ctx, species=p["species"], n_max=p["n_max"], l_max=p["l_max"], r_cut=p["r_cut"],
-                         sigma=1.0, alphas=alphas, betas=betas, average=p["average"], dtype=p["dtype"])
+                         sigma=1.0, alphas=alphas, betas=betas, average=p["average"], dtype=p["dtype"],
+                         options=options)
     dbatch = _hip.DeviceBatch(plan, batch)
     itemsize = np.dtype(p["dtype"]).itemsize
     pitch = plan.features * itemsize
@@ -317,20 +383,32 @@ def main() -> int:
     pairs = timings[-1]["pairs"]
     kbar = pairs / envs
     S, n, l_max = len(p["species"]), p["n_max"], p["l_max"]
+    compression = (options or {}).get("compression", "off")
+    # with average "inner" the spectrum is formed once per structure by the
+    # finalize kernel, not by the expansion kernel timed here
+    spectra = 0.0 if p["average"] == "inner" else 1.0
+    per_env = flops_per_env(kbar, S, n, l_max, plan.features, 1 if compression == "mu2" else S, spectra)
     launches = max(1, int(timings[-1]["expansion_launches"]))
-    flops_launch = envs * flops_per_env(kbar, S, n, l_max) / launches
+    flops_launch = envs * per_env / launches
     launch_ms = statistics.mean(t["expansion_ms"] for t in timings) / launches
     achieved = flops_launch / (launch_ms * 1e-3) / 1e12
-    H = (l_max + 1) ** 2
     tiles = int(timings[-1]["expansion_tiles"])
-    family = "k_soap_quad" if tiles < 0 else "k_soap_mfma" if tiles > 0 else "k_soap_expand"
-    traffic, traffic_source = traffic_from_profile(workload.name, family)
-    if tiles < 0:
+    if tiles <= -1000:
+        family = "k_soap_block"
+        kernel = (f"k_soap_block ({-1000 - tiles} wavefronts per workgroup, one degree set each; register "
+                  f"coefficients on 4x4x4 and 16x16x4 FP64 MFMA; expansion + beta + power spectrum + write)")
+    elif tiles < 0:
+        family = "k_soap_quad"
         kernel = f"k_soap_quad ({-tiles} wavefronts of 4x4x4 FP64 MFMA; expansion + beta + power spectrum + write)"
     elif tiles > 0:
+        family = "k_soap_mfma"
         kernel = f"k_soap_mfma<{tiles}> (expansion + beta + power spectrum + write)"
     else:
+        family = "k_soap_expand"
         kernel = "k_soap_expand (expansion + beta + power spectrum + write)"
+    label = workload.name + ("" if args.options == "off" else f"_{args.options}")
+    traffic, traffic_source = traffic_from_profile(label, family)
+    profile_us, profile_source = profile_average_us(label, family)
     result = {
         "metric": METRIC,
         "value": value,
@@ -355,6 +433,7 @@ def main() -> int:
             "sigma": 1.0,
             "average": p["average"],
             "output_dtype": p["dtype"],
+            "options": options or "default (GTO, no weighting, compression off)",
             "parallelism": "single-gpu",
         },
         "roofline": {
@@ -368,6 +447,8 @@ def main() -> int:
             "flops_per_launch": flops_launch,
             "launch_ms": launch_ms,
             "traffic_source": traffic_source,
+            "profile_launch_ms": None if profile_us is None else profile_us * 1e-3,
+            "profile_source": profile_source,
         },
         "breakdown": {
             "graph_ms": statistics.mean(t["graph_ms"] for t in timings),
@@ -379,20 +460,54 @@ def main() -> int:
             "output_gbs": dbatch.rows * pitch / (launch_ms * launches * 1e-3) / 1e9,
             "features": plan.features,
             "exps_per_env": kbar * (l_max + 1) * n,
-            "flops_per_env": flops_per_env(kbar, S, n, l_max),
-            "H": H,
+            "flops_per_env": per_env,
+            "H": (l_max + 1) ** 2,
         },
     }
     if not args.no_end_to_end:
         result["end_to_end"] = end_to_end(plan, batch)
-    if not args.no_cpu_baseline:
-        threads = args.cpu_threads or min(batch.structures if batch.structures > 1 else 10**9,
-                                          len(os.sched_getaffinity(0)), 16)
-        result["cpu_baseline"] = cpu_baseline(workload, alphas, betas, threads)
     dbatch.close()
     plan.close()
     out.free()
-    print(json.dumps(result))
+    ctx.close()
+    if not args.no_cpu_baseline:
+        threads = args.cpu_threads or int(os.environ.get("OMP_NUM_THREADS") or 0) or len(os.sched_getaffinity(0))
+        result["cpu_baseline"] = cpu_baseline(args.config, workload, alphas, betas, threads, options)
+    return result
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--config", type=int, default=2, help="benchmark configuration 1-5 (default 2)")
+    parser.add_argument("--options", choices=sorted(BENCH_OPTIONS), default="off",
+                        help="SOAP options of the line (default: GTO, no weighting, compression off)")
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--cpu-threads", type=int, default=0,
+                        help="CPU baseline threads (default OMP_NUM_THREADS, else every CPU this process may use)")
+    parser.add_argument("--no-end-to-end", action="store_true")
+    parser.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB")
+    parser.add_argument("--path", choices=("soap", "neighbor-list"), default="soap")
+    parser.add_argument("--nl-cutoff", type=float, default=6.0)
+    parser.add_argument("--half", action="store_true", help="neighbor-list path: half list")
+    args = parser.parse_args()
+    if args.calibrate_copy:
+        return calibrate_copy(args.calibrate_copy)
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only; the SOAP path would shard by structure or "
+                                   "centre range across GPUs, but no multi-GPU run is provided",
+                          "n_gpus": args.gpus}))
+        return 2
+
+    from mdescriptor_amd import workloads
+
+    workload = workloads.config(args.config)
+    if args.path == "neighbor-list":
+        print(json.dumps(neighbor_list_bench(args, workload)))
+        return 0
+    print(json.dumps(soap_bench(args, workload)))
     return 0
 
 

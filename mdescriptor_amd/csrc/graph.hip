@@ -283,7 +283,7 @@ __global__ void k_bin_atoms(const StructGeom* geom, const ImageDesc* images, con
 // Order each cell by extended index (the reference fills cells in extended
 // order, neighbor.cpp:184-192) -- species first in Bins mode -- by ranking,
 // then materialise the binned images as SoA.  Keys are unique inside a cell.
-__global__ void k_bin_sort(const StructGeom* geom, int64_t nstruct, const ImageDesc* images,
+__global__ void k_bin_sort(const StructGeom* geom, const int32_t* cell_struct, const ImageDesc* images,
                            const double* positions, const int32_t* types, const int64_t* cell_start,
                            int64_t cells_total, const uint64_t* keys, double* bx, double* by, double* bz,
                            int32_t* batom, int32_t* bimage, int32_t* btype) {
@@ -291,9 +291,7 @@ __global__ void k_bin_sort(const StructGeom* geom, int64_t nstruct, const ImageD
         const int64_t start = cell_start[c];
         const int64_t n = cell_start[c + 1] - start;
         if (n == 0) continue;
-        int64_t s = find_by_begin(geom, nstruct, c, 1);
-        while (s + 1 < nstruct && geom[s + 1].cell_begin <= c) ++s;
-        const StructGeom& g = geom[s];
+        const StructGeom& g = geom[cell_struct[c]];
         for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
             const uint64_t full = keys[start + i];
             int64_t rank = 0;
@@ -314,13 +312,12 @@ __global__ void k_bin_sort(const StructGeom* geom, int64_t nstruct, const ImageD
 }
 
 // Home ROI cell and structure of every atom (the centres).
-__global__ void k_centre_cell(const StructGeom* geom, int64_t nstruct, const double* positions, int64_t atoms,
-                              int64_t* centre_cell, int32_t* centre_struct, int32_t* cell_ncentre,
+__global__ void k_centre_cell(const StructGeom* geom, const int32_t* atom_struct, const double* positions,
+                              int64_t atoms, int64_t* centre_cell, int32_t* centre_struct, int32_t* cell_ncentre,
                               int32_t* centre_slot, int32_t* error_flag) {
     for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < atoms;
          i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        int64_t s = find_by_begin(geom, nstruct, i, 2);
-        while (s + 1 < nstruct && geom[s + 1].atom_begin <= i) ++s;
+        const int32_t s = atom_struct[i];
         const StructGeom& g = geom[s];
         centre_struct[i] = static_cast<int32_t>(s);
         bool inside;
@@ -333,6 +330,18 @@ __global__ void k_centre_cell(const StructGeom* geom, int64_t nstruct, const dou
         }
         centre_cell[i] = c;
         centre_slot[i] = atomicAdd(&cell_ncentre[c], 1);
+    }
+}
+
+// Structure of every ROI cell: the last structure whose first cell is at or
+// before it (structures own consecutive cell ranges).  One thread per cell,
+// so the searches of all cells overlap their memory latency.
+__global__ void k_cell_struct(const StructGeom* geom, int64_t nstruct, int64_t cells_total, int32_t* cell_struct) {
+    for (int64_t c = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; c < cells_total;
+         c += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        int64_t s = find_by_begin(geom, nstruct, c, 1);
+        while (s + 1 < nstruct && geom[s + 1].cell_begin <= c) ++s;
+        cell_struct[c] = static_cast<int32_t>(s);
     }
 }
 
@@ -411,7 +420,7 @@ __device__ inline uint64_t lane_range(int lo, int hi) {
 
 template <int kMode>
 __global__ __launch_bounds__(kNbrThreads) void k_neighbors(
-    const StructGeom* geom, int64_t nstruct, const double* positions, int64_t cells_total,
+    const StructGeom* geom, const int32_t* cell_struct, const double* positions, int64_t cells_total,
     const int64_t* cell_centre_start, const int32_t* cell_centres, const int64_t* cell_start,
     const int64_t* cell_species_start, const double* bx, const double* by, const double* bz, int S,
     double accept_max, int32_t* counts, int32_t* totals, int64_t* pair_start, uint32_t* pair_bin, int64_t cap,
@@ -437,17 +446,7 @@ __global__ __launch_bounds__(kNbrThreads) void k_neighbors(
     for (int64_t c = blockIdx.x; c < cells_total; c += gridDim.x) {
         const int64_t c0 = cell_centre_start[c], c1 = cell_centre_start[c + 1];
         if (c0 == c1) continue;
-        int64_t sidx = 0;
-        {
-            int64_t lo = 0, hi = nstruct;
-            while (hi - lo > 1) {
-                const int64_t mid = (lo + hi) / 2;
-                if (geom[mid].cell_begin <= c) lo = mid; else hi = mid;
-            }
-            sidx = lo;
-            while (sidx + 1 < nstruct && geom[sidx + 1].cell_begin <= c) ++sidx;
-        }
-        const StructGeom& g = geom[sidx];
+        const StructGeom& g = geom[cell_struct[c]];
         // segments in walk order: index sp * 27 + k, k = the z/y/x cell offset
         for (int t = tid; t < nseg; t += kNbrThreads) {
             const int sp = t / 27, k = t - sp * 27;
@@ -782,6 +781,11 @@ void prepare_batch(const mdx_batch_view& batch, const int32_t* species, int n_sp
         }
     }
     out.geom.assign(static_cast<size_t>(batch.structures), StructGeom{});
+    out.atom_struct.resize(static_cast<size_t>(batch.atoms));
+    for (int64_t s = 0; s < batch.structures; ++s) {
+        std::fill(out.atom_struct.begin() + batch.offsets[s], out.atom_struct.begin() + batch.offsets[s + 1],
+                  static_cast<int32_t>(s));
+    }
     out.images.clear();
     int64_t ext = 0, cells = 0;
     for (int64_t s = 0; s < batch.structures; ++s) {
@@ -901,6 +905,7 @@ void upload_batch(hipStream_t stream, const mdx_batch_view& batch, PreparedBatch
     const size_t atoms = static_cast<size_t>(pb.atoms);
     pb.d_positions.reserve(std::max<size_t>(1, atoms * 3 * sizeof(double)));
     pb.d_types.reserve(std::max<size_t>(1, atoms * sizeof(int32_t)));
+    pb.d_atom_struct.reserve(std::max<size_t>(1, atoms * sizeof(int32_t)));
     pb.d_geom.reserve(std::max<size_t>(1, pb.geom.size() * sizeof(StructGeom)));
     pb.d_images.reserve(std::max<size_t>(1, pb.images.size() * sizeof(ImageDesc)));
     pb.d_offsets.reserve(pb.offsets.size() * sizeof(int64_t));
@@ -909,6 +914,8 @@ void upload_batch(hipStream_t stream, const mdx_batch_view& batch, PreparedBatch
                                hipMemcpyHostToDevice, stream));
         MDX_HIP(hipMemcpyAsync(pb.d_types.ptr, pb.types.data(), atoms * sizeof(int32_t), hipMemcpyHostToDevice,
                                stream));
+        MDX_HIP(hipMemcpyAsync(pb.d_atom_struct.ptr, pb.atom_struct.data(), atoms * sizeof(int32_t),
+                               hipMemcpyHostToDevice, stream));
     }
     if (!pb.geom.empty()) {
         MDX_HIP(hipMemcpyAsync(pb.d_geom.ptr, pb.geom.data(), pb.geom.size() * sizeof(StructGeom),
@@ -968,6 +975,7 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     gr.centre_slot.reserve(static_cast<size_t>(atoms) * sizeof(int32_t));
     gr.cell_centres.reserve(static_cast<size_t>(atoms) * sizeof(int32_t));
     gr.cell_centre_start.reserve(cells1 * sizeof(int64_t));
+    gr.cell_struct.reserve(static_cast<size_t>(cells) * sizeof(int32_t));
     gr.bin_key.reserve(static_cast<size_t>(ext) * sizeof(uint64_t));
     gr.bin_x.reserve(static_cast<size_t>(ext) * sizeof(double));
     gr.bin_y.reserve(static_cast<size_t>(ext) * sizeof(double));
@@ -980,9 +988,11 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     MDX_HIP(hipMemsetAsync(gr.counters.ptr, 0, counter_bytes, stream));
 
     // home cell and structure of every atom (the centres)
-    hipLaunchKernelGGL(k_centre_cell, dim3(grid_for(atoms)), dim3(kBlock), 0, stream, geom, nstruct, pos, atoms,
-                       gr.centre_cell.as<int64_t>(), gr.centre_struct.as<int32_t>(), cell_ncentre,
-                       gr.centre_slot.as<int32_t>(), error_flag);
+    hipLaunchKernelGGL(k_centre_cell, dim3(grid_for(atoms)), dim3(kBlock), 0, stream, geom,
+                       pb.d_atom_struct.as<int32_t>(), pos, atoms, gr.centre_cell.as<int64_t>(),
+                       gr.centre_struct.as<int32_t>(), cell_ncentre, gr.centre_slot.as<int32_t>(), error_flag);
+    hipLaunchKernelGGL(k_cell_struct, dim3(grid_for(cells)), dim3(kBlock), 0, stream, geom, nstruct, cells,
+                       gr.cell_struct.as<int32_t>());
     // bin every periodic image into its ROI cell, sorted by (species, extended index)
     int max_images = 1;
     for (const StructGeom& sg : pb.geom) max_images = std::max(max_images, static_cast<int>(sg.n_images));
@@ -996,7 +1006,8 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
                        gr.centre_struct.as<int32_t>(), pb.d_types.as<int32_t>(), S > 1 ? 1 : 0, atoms, max_images,
                        cell_fill, gr.cell_start.as<int64_t>(), gr.bin_key.as<uint64_t>());
     const unsigned cell_grid = static_cast<unsigned>(std::min<int64_t>(cells, 1 << 20));
-    hipLaunchKernelGGL(k_bin_sort, dim3(cell_grid), dim3(kBlock), 0, stream, geom, nstruct, images, pos,
+    hipLaunchKernelGGL(k_bin_sort, dim3(cell_grid), dim3(kBlock), 0, stream, geom, gr.cell_struct.as<int32_t>(),
+                       images, pos,
                        pb.d_types.as<int32_t>(), gr.cell_start.as<int64_t>(), cells, gr.bin_key.as<uint64_t>(),
                        gr.bin_x.as<double>(), gr.bin_y.as<double>(), gr.bin_z.as<double>(), gr.bin_atom.as<int32_t>(),
                        gr.bin_image.as<int32_t>(), gr.bin_type.as<int32_t>());
@@ -1019,7 +1030,8 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     const unsigned cell_blocks = static_cast<unsigned>(std::min<int64_t>(cells, 1 << 20));
     auto neighbors = [&](auto mode, int64_t cap) {
         hipLaunchKernelGGL(k_neighbors<decltype(mode)::value>, dim3(cell_blocks), dim3(kNbrThreads), 0, stream, geom,
-                           nstruct, pos, cells, gr.cell_centre_start.as<int64_t>(), gr.cell_centres.as<int32_t>(),
+                           gr.cell_struct.as<int32_t>(), pos, cells, gr.cell_centre_start.as<int64_t>(),
+                           gr.cell_centres.as<int32_t>(),
                            gr.cell_start.as<int64_t>(), gr.cell_species_start.as<int64_t>(), gr.bin_x.as<double>(),
                            gr.bin_y.as<double>(), gr.bin_z.as<double>(), S, accept_max, gr.counts.as<int32_t>(),
                            gr.totals.as<int32_t>(), gr.pair_start.as<int64_t>(), gr.pair_bin.as<uint32_t>(), cap,

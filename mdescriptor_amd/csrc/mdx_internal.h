@@ -103,12 +103,14 @@ struct PreparedBatch {
     std::vector<StructGeom> geom;
     std::vector<ImageDesc> images;
     std::vector<int32_t> types; // species index per atom (0 when species are ignored)
+    std::vector<int32_t> atom_struct; // structure of each atom
     std::vector<int64_t> offsets;
     // work items of the averaged SOAP modes (host copies outlive the async upload)
     std::vector<int64_t> item_begin, struct_items;
     int n_species = 1;
     DeviceBuffer d_positions; // f64[atoms*3]
     DeviceBuffer d_types;     // i32[atoms]
+    DeviceBuffer d_atom_struct; // i32[atoms]
     DeviceBuffer d_geom;      // StructGeom[structures]
     DeviceBuffer d_images;    // ImageDesc[...]
     DeviceBuffer d_offsets;   // i64[structures+1]
@@ -167,6 +169,7 @@ struct DeviceGraph {
     DeviceBuffer centre_slot;                       // i32 place of the atom among its cell's centres
     DeviceBuffer cell_centre_start;                 // i64[cells + 1] first entry of a cell in cell_centres
     DeviceBuffer cell_centres;                      // i32[atoms] centres grouped by home cell
+    DeviceBuffer cell_struct;                       // i32[cells] structure of each ROI cell
     DeviceBuffer counts;     // i32[atoms * n_species]
     DeviceBuffer totals;     // i32[atoms]
     DeviceBuffer pair_start; // i64[atoms + 1]: first row of each centre (compact: the
@@ -181,7 +184,8 @@ struct DeviceGraph {
     template <typename F> void for_each_buffer(F f) {
         for (DeviceBuffer* b : {&counters, &cell_start, &bin_key, &cell_species_start, &centre_struct, &bin_x,
                                 &bin_y, &bin_z, &bin_atom, &bin_image, &bin_type, &centre_cell, &centre_slot,
-                                &cell_centre_start, &cell_centres, &counts, &totals, &pair_start, &pair_bin,
+                                &cell_centre_start, &cell_centres, &cell_struct, &counts, &totals, &pair_start,
+                                &pair_bin,
                                 &scan_tmp}) {
             f(*b);
         }
