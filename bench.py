@@ -19,6 +19,9 @@ the process may use), with the host's CPU count, model and OMP_NUM_THREADS.
 Its sample is the whole batch, except for configuration 5 a 46,656-atom cell
 of the same generator.
 
+``--peaks`` only measures this device's FP64 (vector FMA, 16x16x4 MFMA) and
+HBM copy rates with the probes of ``mdescriptor_amd/csrc/peaks.hip``.
+
 ``--config N`` selects benchmark configuration 1-5 (default 2, the headline);
 ``--options NAME`` runs the line with SOAP options (mu1nu1 compression, pow
 weighting with w0, crossover with exp weighting) on that configuration.
@@ -143,6 +146,32 @@ def calibrate_copy(mib: int) -> int:
     torch.cuda.synchronize()
     print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4, "launches": 5}))
     return 0
+
+
+def peaks() -> dict:
+    """Measured peak rates of this device, for reading the roofline against
+    them: FP64 FMA on the vector ALU, FP64 16x16x4 MFMA, and a 1 GiB HBM copy
+    (mdescriptor_amd/csrc/peaks.hip)."""
+
+    import ctypes
+
+    lib = ctypes.CDLL(str(ROOT / "mdescriptor_amd" / "_lib" / "libmdx_peaks.so"))
+    lib.mdx_peak_run.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int, ctypes.POINTER(ctypes.c_double),
+                                 ctypes.POINTER(ctypes.c_double)]
+    lib.mdx_peak_run.restype = ctypes.c_int
+    report = {}
+    for which, name, size, repeats, unit, scale, published in (
+            (0, "fp64_valu_fma", 0, 10, "TFLOP/s", 1e12, FP64_PEAK_TFLOPS),
+            (1, "fp64_mfma_16x16x4", 0, 10, "TFLOP/s", 1e12, FP64_PEAK_TFLOPS),
+            (2, "hbm_copy", 1 << 30, 20, "GB/s", 1e9, HBM_PEAK_GBS)):
+        seconds, work = ctypes.c_double(), ctypes.c_double()
+        rc = lib.mdx_peak_run(which, size, repeats, ctypes.byref(seconds), ctypes.byref(work))
+        if rc != 0:
+            raise RuntimeError(f"peak probe {name} failed with HIP error {rc}")
+        rate = work.value / seconds.value / scale
+        report[name] = {"value": rate, "unit": unit, "published_peak": published, "frac": rate / published,
+                        "launch_ms": seconds.value * 1e3, "work_per_launch": work.value}
+    return report
 
 
 def end_to_end(plan, batch, repeats: int = 3) -> dict:
@@ -489,12 +518,16 @@ def main() -> int:
                         help="CPU baseline threads (default OMP_NUM_THREADS, else every CPU this process may use)")
     parser.add_argument("--no-end-to-end", action="store_true")
     parser.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB")
+    parser.add_argument("--peaks", action="store_true", help="only measure this device's FP64 and HBM peak rates")
     parser.add_argument("--path", choices=("soap", "neighbor-list"), default="soap")
     parser.add_argument("--nl-cutoff", type=float, default=6.0)
     parser.add_argument("--half", action="store_true", help="neighbor-list path: half list")
     args = parser.parse_args()
     if args.calibrate_copy:
         return calibrate_copy(args.calibrate_copy)
+    if args.peaks:
+        print(json.dumps(peaks()))
+        return 0
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; the SOAP path would shard by structure or "
                                    "centre range across GPUs, but no multi-GPU run is provided",

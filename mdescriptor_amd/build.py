@@ -1,4 +1,5 @@
-"""Build the gfx950 SOAP library in-tree: ``mdescriptor_amd/_lib/libmdx_hip.so``.
+"""Build the gfx950 SOAP library in-tree: ``mdescriptor_amd/_lib/libmdx_hip.so``
+(and the peak-rate probes of the roofline, ``libmdx_peaks.so``).
 
 Run ``python -m mdescriptor_amd.build``.  Every source under ``csrc/`` is
 compiled with hipcc for gfx950 only, with FP contraction off (the device code
@@ -22,6 +23,9 @@ LIB_DIR = PACKAGE / "_lib"
 LIBRARY = LIB_DIR / "libmdx_hip.so"
 SOURCES = ("graph.hip", "soap.hip", "soap_mfma.hip", "soap_quad.hip", "soap_block.hip", "neighbor_list.hip",
            "api.hip")
+# peak-rate probes for the roofline (bench.py --peaks), a library of their own
+PEAKS_SOURCE = "peaks.hip"
+PEAKS_LIBRARY = LIB_DIR / "libmdx_peaks.so"
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -68,15 +72,16 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
             print(messages, file=sys.stderr)
         return obj
 
-    workers = jobs or min(len(SOURCES), int(os.environ.get("MAX_JOBS", "8")))
+    workers = jobs or min(len(SOURCES) + 1, int(os.environ.get("MAX_JOBS", "8")))
     with ThreadPoolExecutor(max_workers=max(1, workers)) as pool:
-        objects = list(pool.map(compile_one, SOURCES))
-    tmp = LIBRARY.with_suffix(".so.tmp")
-    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-o", str(tmp), *map(str, objects)]
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    if proc.returncode != 0:
-        raise RuntimeError(f"linking {LIBRARY.name} failed:\n{proc.stdout}{proc.stderr}")
-    os.replace(tmp, LIBRARY)
+        objects = list(pool.map(compile_one, (*SOURCES, PEAKS_SOURCE)))
+    for library, parts in ((LIBRARY, objects[:-1]), (PEAKS_LIBRARY, objects[-1:])):
+        tmp = library.with_suffix(".so.tmp")
+        cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-o", str(tmp), *map(str, parts)]
+        proc = subprocess.run(cmd, capture_output=True, text=True)
+        if proc.returncode != 0:
+            raise RuntimeError(f"linking {library.name} failed:\n{proc.stdout}{proc.stderr}")
+        os.replace(tmp, library)
     return LIBRARY
 
 
