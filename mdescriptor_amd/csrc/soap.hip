@@ -369,13 +369,20 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
     const int64_t rows = p.average != 0 ? pb.structures : pb.atoms;
     if (rows == 0 || d.F == 0) return;
 
+    // the register-coefficient kernel where the plan chose it (atom-level
+    // rows, or structure averages of the inner kind, which it forms from the
+    // structure's centres directly) and every centre's rows fit their slot codes
+    const bool block = p.block_waves > 0 && (p.average == 0 || p.average == 1) &&
+                       g.most_rows < kQuadMaxRows;
+    const bool block_inner = block && p.average == 1;
+
     // work items
     std::vector<int64_t>& item_begin_h = pb.item_begin;
     std::vector<int64_t>& struct_items_h = pb.struct_items;
     item_begin_h.clear();
     struct_items_h.clear();
-    int64_t items = pb.atoms;
-    if (p.average != 0) {
+    int64_t items = block_inner ? pb.structures : pb.atoms;
+    if (p.average != 0 && !block_inner) {
         struct_items_h.resize(static_cast<size_t>(pb.structures) + 1);
         for (int64_t s = 0; s < pb.structures; ++s) {
             struct_items_h[static_cast<size_t>(s)] = static_cast<int64_t>(item_begin_h.size());
@@ -392,7 +399,7 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
     int64_t* d_item_begin = nullptr;
     int64_t* d_struct_items = nullptr;
     double* d_partial = nullptr;
-    if (p.average != 0) {
+    if (p.average != 0 && !block_inner) {
         const size_t inner_width = p.use_mfma ? static_cast<size_t>(mfma_coefficient_rows(p.Sc, p.n, p.compression)) * static_cast<size_t>(p.hpad)
                                               : static_cast<size_t>(d.C);
         const size_t width = p.average == 1 ? inner_width : static_cast<size_t>(d.F);
@@ -412,10 +419,8 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
     const int64_t slice = slice_items > 0 ? slice_items : int64_t(1) << 17;
     const bool hook = on_slice != nullptr && *on_slice && p.average == 0;
     int64_t launches = 0;
-    if (p.use_mfma) {
-        // the register-coefficient kernel, else the 4x4-block kernel, where
-        // the plan chose them and every centre's rows fit their slot codes
-        const bool block = p.block_waves > 0 && p.average == 0 && g.most_rows < kQuadMaxRows;
+    if (block || p.use_mfma) {
+        // else the 4x4-block kernel where the plan chose it
         const bool quad = !block && p.quad_waves > 0 && g.most_rows < kQuadMaxRows;
         MfmaDims md{};
         md.S = p.S;
@@ -481,6 +486,7 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
                 ba.F = p.features;
                 ba.item_base = base;
                 ba.items = count;
+                ba.struct_offsets = block_inner ? pb.d_offsets.as<int64_t>() : nullptr;
                 ba.out = out_device;
                 ba.pitch = pitch_bytes;
                 launch_block_expand(stream, p.l_max, p.block_kg, p.block_ncr, ba, count);
@@ -496,7 +502,17 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
             if (hook) (*on_slice)(base, count);
         }
         if (events != nullptr) MDX_HIP(hipEventRecord(events[3], stream));
-        if (p.average != 0) {
+        if (block_inner) {
+            // rows of structures without atoms (the expansion visits none of them)
+            bool empty = false;
+            for (int64_t st = 0; st < pb.structures && !empty; ++st) {
+                empty = pb.offsets[static_cast<size_t>(st) + 1] == pb.offsets[static_cast<size_t>(st)];
+            }
+            if (empty) {
+                launch_block_zero_rows(stream, pb.d_offsets.as<int64_t>(), pb.structures, out_device, pitch_bytes,
+                                       p.features * p.out_dtype);
+            }
+        } else if (p.average != 0) {
             launch_mfma_finalize(stream, pb, tab, md, d_partial, d_struct_items, out_device, pitch_bytes);
         }
         if (events != nullptr) MDX_HIP(hipEventRecord(events[4], stream));

@@ -1,6 +1,7 @@
 // Host/device interface of the register-coefficient SOAP kernel
 // (soap_block.hip): default options (GTO basis, no weighting, no
-// compression), atom-level rows (average "off").
+// compression), atom-level rows (average "off") or a row per structure of
+// its centres' averaged coefficients (average "inner").
 #pragma once
 
 #include "mdx_internal.h"
@@ -22,7 +23,9 @@ struct BlockArgs {
     int S;                      // species
     int out_dtype;              // 4 or 8 bytes
     int64_t F;                  // features per row
-    int64_t item_base, items, per_block;
+    int64_t item_base, items, per_block; // centres, or structures when struct_offsets is set
+    const int64_t* struct_offsets;       // null: a row per centre; else first centre of each structure
+                                         // (+ end): a row per structure, its centres' average
     void* out;
     int64_t pitch;              // bytes between output rows
 };
@@ -43,5 +46,9 @@ bool block_plan_tables(int S, int n, int l_max, int out_dtype, const std::vector
                        const std::vector<double>& pref, const std::vector<double>& expo, BlockPlanHost& out);
 size_t block_lds_bytes(int l_max, int kg);
 void launch_block_expand(hipStream_t stream, int l_max, int kg, int ncr, const BlockArgs& a, int64_t count);
+// Zero the rows of the structures without atoms (structure averages; the
+// expansion writes only the rows of structures it visits).
+void launch_block_zero_rows(hipStream_t stream, const int64_t* struct_offsets, int64_t structures, void* out,
+                            int64_t pitch, int64_t row_bytes);
 
 } // namespace mdx

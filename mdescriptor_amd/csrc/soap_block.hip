@@ -334,7 +334,7 @@ __device__ __forceinline__ int64_t uniform64(int64_t v) {
     return static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | static_cast<uint32_t>(lo));
 }
 
-template <int LM, int KG, int NCR, int ES, int W>
+template <int LM, int KG, int NCR, int ES, bool AVG, int W>
 __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, const int* s_ps) {
     using PL = BlockPlan<LM, KG>;
     constexpr int L = PL::L, R = PL::R, P = PL::P, RPL = PL::RPL, NT = PL::NT, GS = PL::GS;
@@ -382,15 +382,21 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
     const bool low_pair = (lane % 16) < 8;
 
     // ---------------------------------------------------------- slot stream
-    // Work: centres [first, last) of this workgroup.  A centre's rows are
-    // grouped by species: cnt_t rows of species t after those of the species
+    // A centre's rows are grouped by species: cnt_t rows of species t after those of the species
     // before it.  The stream cuts each species' rows into chunks of at most 32
     // slots (a chunk never mixes species; its last step group may hold pad
     // slots past the rows) and runs two chunks ahead of the contraction: each
     // lane pair (two lanes per slot) loads the bin of its slot's row.  All of
     // its state but the loaded bins is wave-uniform.
-    const int64_t item_first = a.item_base + static_cast<int64_t>(blockIdx.x) * a.per_block;
-    const int64_t item_last = min(item_first + a.per_block, a.item_base + a.items);
+    // Work: items [first, last) of this workgroup -- centres, or with
+    // structure averages whole structures, whose centres are consecutive
+    const int64_t work_first = a.item_base + static_cast<int64_t>(blockIdx.x) * a.per_block;
+    const int64_t work_last = min(work_first + a.per_block, a.item_base + a.items);
+    constexpr bool inner = AVG; // rows of structure averages (a.struct_offsets set)
+    const int64_t item_first = inner ? uniform64(a.struct_offsets[work_first]) : work_first;
+    const int64_t item_last = inner ? uniform64(a.struct_offsets[work_last]) : work_last;
+    // structure of the stream's centre and its centre range (inner)
+    int64_t st_struct = work_first - 1, st_struct_end = item_first;
     int pre_count = 0;     // next centre: rows of species t at lane t
     int64_t pre_start = 0; // next centre: first pair row (lane 0)
     // Loads are unconditional in every lane (clamped to valid addresses) so
@@ -419,6 +425,13 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
     };
     auto enter_centre = [&]() {
         st_centre = uniform64(st_centre + 1);
+        if constexpr (inner) {
+            // skip to the centre's structure (empty structures have no centres)
+            while (st_centre >= st_struct_end) {
+                st_struct = uniform64(st_struct + 1);
+                st_struct_end = uniform64(a.struct_offsets[st_struct + 1]);
+            }
+        }
         cnt = pre_count;
         st_row = uniform64(pre_start);
         st_more = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(__ballot(lane < S && cnt > 0)));
@@ -433,11 +446,13 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
         int q;          // species
         int rows;       // rows in the chunk (slots past them are pad slots)
         int groups;     // step groups
-        bool last;      // last chunk of its centre
+        bool ends;      // last chunk of its centre
+        bool last;      // last chunk of its output row: of its centre, or of its structure (inner)
         uint32_t bin;   // bin of the lane's slot row (slot < rows)
+        int64_t row;    // output row (centre, or structure)
     };
     auto next_stage = [&]() -> Stage {
-        Stage s{-1, 0, 0, 0, false, 0u};
+        Stage s{-1, 0, 0, 0, false, false, 0u, 0};
         if (st_left == 0) {
             if (st_more != 0) {
                 next_species();
@@ -456,7 +471,14 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
         if constexpr (kHarm) s.bin = a.pair_bin[n > 0 ? st_row + min(lane / 2, n - 1) : 0];
         st_row = uniform64(st_row + n);
         st_left = __builtin_amdgcn_readfirstlane(st_left - n);
-        s.last = st_left == 0 && st_more == 0;
+        s.ends = st_left == 0 && st_more == 0;
+        s.last = s.ends;
+        s.row = st_centre;
+        if constexpr (inner) {
+            // the structure's average: one row when its last centre ends
+            s.last = s.ends && st_centre + 1 == st_struct_end;
+            s.row = st_struct;
+        }
         return s;
     };
 
@@ -504,10 +526,10 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
     int cur = -1; // species of the accumulators
 
     // sum the phases of every accumulator and add species q's radial groups
-    // into its block slots of the coefficient registers
-    // Each species merges exactly once per centre, into block slots of its
-    // own (the coefficient registers start each centre at zero), so the merge
-    // overwrites those slots with a lane select.
+    // into its block slots of the coefficient registers (which start every
+    // output row at zero).  A species merges once per centre: for a centre's
+    // own row the merge overwrites its slots with a lane select, for a
+    // structure average it adds to them.
     auto merge_into = [&](auto rc_reg, int q) {
         constexpr int rt = decltype(rc_reg)::value; // target coefficient register
         unroll<NU>([&](auto uc) {
@@ -526,7 +548,11 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
                 } else {
                     mine = blk == rr;
                 }
-                C[u][rt] = mine ? v : C[u][rt];
+                if constexpr (inner) {
+                    C[u][rt] = mine ? C[u][rt] + v : C[u][rt];
+                } else {
+                    C[u][rt] = mine ? v : C[u][rt];
+                }
                 // one unit at a time: bounds the registers live at once
                 __builtin_amdgcn_sched_barrier(0);
             });
@@ -550,7 +576,9 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
         // wave-uniform facts of chunk k, in scalar registers
         const int groups0 = __builtin_amdgcn_readfirstlane(s0.groups);
         const bool last0 = __builtin_amdgcn_readfirstlane(s0.last ? 1 : 0) != 0;
+        const bool ends0 = inner ? __builtin_amdgcn_readfirstlane(s0.ends ? 1 : 0) != 0 : last0;
         const int64_t centre0 = uniform64(s0.centre);
+        const int64_t row0 = uniform64(s0.row);
         const int q0 = __builtin_amdgcn_readfirstlane(s0.q);
         // centre position of chunk k + 1 (scalar loads, used after the contraction)
         const int64_t centre1 = uniform64(s1.centre);
@@ -600,10 +628,20 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
                 });
             });
         }
-        // ------------------------------------ centre end: fold, power spectrum
-        if (last0) {
+        // a centre's sums end in the coefficient registers (an average
+        // thereby sums per-centre coefficients, as a centre's row does)
+        if (ends0) {
             merge(__builtin_amdgcn_readfirstlane(cur));
             cur = -1;
+        }
+        // ------------------------------------ row end: fold, power spectrum
+        if (last0) {
+            // an average's coefficients carry 1 / (atoms of the structure)
+            double scale0 = 1.0;
+            if constexpr (inner) {
+                scale0 = 1.0 / static_cast<double>(uniform64(a.struct_offsets[row0 + 1]) -
+                                                   uniform64(a.struct_offsets[row0]));
+            }
             // fold: C <- (S_lm C)^T beta^T in place
             unroll<L>([&](auto lc) {
                 constexpr int l = decltype(lc)::value;
@@ -613,7 +651,7 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
                     constexpr int loff = 4 * units_before(0xffffffffu, l);
                     unroll<cgroups(l)>([&](auto cc) {
                         constexpr int cg = decltype(cc)::value;
-                        const double sc = s_scale[loff + 4 * cg + lane % 4];
+                        const double sc = s_scale[loff + 4 * cg + lane % 4] * scale0;
                         unroll<NCR>([&](auto rc) {
                             constexpr int r = decltype(rc)::value;
                             const double v = C[u0 + cg][r] * sc;
@@ -632,7 +670,7 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
                 }
             });
             // power spectrum of the owned degrees, written to the centre's row
-            char* row = static_cast<char*>(a.out) + centre0 * a.pitch;
+            char* row = static_cast<char*>(a.out) + row0 * a.pitch;
             const __amdgpu_buffer_rsrc_t rsrc =
                 __builtin_amdgcn_make_buffer_rsrc(row, 0, static_cast<int>(F * ES), 0x00020000);
             int pair = 0;
@@ -688,7 +726,7 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
     }
 }
 
-template <int LM, int KG, int NCR, int ES>
+template <int LM, int KG, int NCR, int ES, bool AVG>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) void k_soap_block(BlockArgs a) {
     using PL = BlockPlan<LM, KG>;
     // staging buffers, d2, exp table, padded S_lm table, power-spectrum
@@ -729,15 +767,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) void k
     __syncthreads();
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWaveThreads);
     if (wave == 0) {
-        block_role<LM, KG, NCR, ES, 0>(a, lds, s_ps);
+        block_role<LM, KG, NCR, ES, AVG, 0>(a, lds, s_ps);
     } else if constexpr (PL::T > 1) {
         if (wave == 1) {
-            block_role<LM, KG, NCR, ES, (PL::T > 1 ? 1 : 0)>(a, lds, s_ps);
+            block_role<LM, KG, NCR, ES, AVG, (PL::T > 1 ? 1 : 0)>(a, lds, s_ps);
         } else if constexpr (PL::T > 2) {
             if (wave == 2) {
-                block_role<LM, KG, NCR, ES, (PL::T > 2 ? 2 : 0)>(a, lds, s_ps);
+                block_role<LM, KG, NCR, ES, AVG, (PL::T > 2 ? 2 : 0)>(a, lds, s_ps);
             } else if constexpr (PL::T > 3) {
-                block_role<LM, KG, NCR, ES, (PL::T > 3 ? 3 : 0)>(a, lds, s_ps);
+                block_role<LM, KG, NCR, ES, AVG, (PL::T > 3 ? 3 : 0)>(a, lds, s_ps);
             }
         }
     }
@@ -758,10 +796,17 @@ void launch_shape(hipStream_t stream, const BlockArgs& a, int64_t count) {
     BlockArgs args = a;
     args.per_block = std::max<int64_t>(1, (count + target - 1) / target);
     const unsigned grid = static_cast<unsigned>((count + args.per_block - 1) / args.per_block);
-    if (a.out_dtype == 4) {
-        hipLaunchKernelGGL((k_soap_block<LM, KG, NCR, 4>), dim3(grid), dim3(PL::T * kWaveThreads), 0, stream, args);
+    const dim3 threads(PL::T * kWaveThreads);
+    if (a.struct_offsets == nullptr) {
+        if (a.out_dtype == 4) {
+            hipLaunchKernelGGL((k_soap_block<LM, KG, NCR, 4, false>), dim3(grid), threads, 0, stream, args);
+        } else {
+            hipLaunchKernelGGL((k_soap_block<LM, KG, NCR, 8, false>), dim3(grid), threads, 0, stream, args);
+        }
+    } else if (a.out_dtype == 4) {
+        hipLaunchKernelGGL((k_soap_block<LM, KG, NCR, 4, true>), dim3(grid), threads, 0, stream, args);
     } else {
-        hipLaunchKernelGGL((k_soap_block<LM, KG, NCR, 8>), dim3(grid), dim3(PL::T * kWaveThreads), 0, stream, args);
+        hipLaunchKernelGGL((k_soap_block<LM, KG, NCR, 8, true>), dim3(grid), threads, 0, stream, args);
     }
 }
 
@@ -777,7 +822,7 @@ struct ShapeEntry {
 const ShapeEntry kShapes[] = {
     MDX_BLOCK_SHAPE(3, 1, 1), // water (benchmark configuration 1)
     MDX_BLOCK_SHAPE(6, 2, 2), // HCNO (configuration 2)
-    MDX_BLOCK_SHAPE(4, 2, 3), // molecules (configuration 3, atom-level rows)
+    MDX_BLOCK_SHAPE(4, 2, 3), // molecules (configuration 3)
     MDX_BLOCK_SHAPE(8, 2, 3), // high-entropy alloy (configuration 4)
     MDX_BLOCK_SHAPE(9, 3, 1), // liquid silicon (configuration 5)
 };
@@ -912,6 +957,29 @@ void launch_block_expand(hipStream_t stream, int l_max, int kg, int ncr, const B
     const ShapeEntry* e = find_shape(l_max, kg, ncr);
     if (e == nullptr) throw Error(MDX_INTERNAL, "SOAP shape is not compiled for the register-coefficient kernel");
     e->launch(stream, a, count);
+    MDX_HIP(hipGetLastError());
+}
+
+namespace {
+
+// one workgroup per structure without atoms; its row's bytes zeroed
+__global__ void k_block_zero_rows(const int64_t* struct_offsets, int64_t structures, char* out, int64_t pitch,
+                                  int64_t row_bytes) {
+    for (int64_t s = blockIdx.x; s < structures; s += gridDim.x) {
+        if (struct_offsets[s + 1] != struct_offsets[s]) continue;
+        char* row = out + s * pitch;
+        for (int64_t i = threadIdx.x; i < row_bytes; i += blockDim.x) row[i] = 0;
+    }
+}
+
+} // namespace
+
+void launch_block_zero_rows(hipStream_t stream, const int64_t* struct_offsets, int64_t structures, void* out,
+                            int64_t pitch, int64_t row_bytes) {
+    if (structures <= 0 || row_bytes <= 0) return;
+    const unsigned grid = static_cast<unsigned>(std::min<int64_t>(structures, 1 << 16));
+    hipLaunchKernelGGL(k_block_zero_rows, dim3(grid), dim3(256), 0, stream, struct_offsets, structures,
+                       static_cast<char*>(out), pitch, row_bytes);
     MDX_HIP(hipGetLastError());
 }
 

@@ -81,13 +81,14 @@ def test_soap_matches_oracle(hip_context, oracle, workload, average, dtype):
 @pytest.mark.parametrize("kernel", ["generic", "mfma", "quad", "block"])
 def test_every_expansion_kernel_matches(hip_context, oracle, monkeypatch, kernel):
     """The plan picks the register-coefficient kernel for the default options
-    and atom-level rows where its shape is compiled, else the 4x4-block kernel
+    with atom-level rows or inner averages where its shape is compiled, else
+    the 4x4-block kernel
     where it fits (n_max <= 8), else the 16x16-tile kernel, with the generic
     kernel as the last fallback.  Each stays parity-green when forced."""
 
     monkeypatch.setenv("MDX_HIP_SOAP_KERNEL", kernel)
     work = workloads.config(2, "small")
-    for average in ("off",) if kernel == "block" else ("off", "inner", "outer"):
+    for average in ("off", "inner") if kernel == "block" else ("off", "inner", "outer"):
         _, timing = _check(hip_context, oracle, work.batch, work.params, average, "float64")
         tiles = timing["expansion_tiles"]
         expected = {"block": tiles <= -1000, "quad": -1000 < tiles < 0, "mfma": tiles > 0, "generic": tiles == 0}
@@ -96,9 +97,9 @@ def test_every_expansion_kernel_matches(hip_context, oracle, monkeypatch, kernel
 
 def test_default_plan_runs_the_block_kernel(hip_context, oracle):
     work = workloads.config(2, "small")
-    for average, tiles in (("off", -1004), ("outer", -4)):
+    for average, tiles in (("off", -1004), ("inner", -1004), ("outer", -4)):
         _, timing = _check(hip_context, oracle, work.batch, work.params, average, "float32")
-        # four wavefronts for n_max 8, l_max 6; averaged rows on the 4x4-block kernel
+        # four wavefronts for n_max 8, l_max 6; outer averages on the 4x4-block kernel
         assert timing["expansion_tiles"] == tiles
 
 
@@ -176,9 +177,33 @@ def test_block_kernel_shapes(hip_context, oracle, monkeypatch, species, n_max, l
     monkeypatch.setenv("MDX_HIP_SOAP_KERNEL", "block")
     batch = _random_cluster(10 * n_max + l_max, 30, species)
     params = {"species": species, "n_max": n_max, "l_max": l_max, "r_cut": r_cut}
-    for dtype in ("float64", "float32"):
-        _, timing = _check(hip_context, oracle, batch, params, "off", dtype)
+    for dtype, average in (("float64", "off"), ("float32", "off"), ("float64", "inner"), ("float32", "inner")):
+        _, timing = _check(hip_context, oracle, batch, params, average, dtype)
         assert timing["expansion_tiles"] == -1004
+
+
+def test_block_kernel_inner_average_with_empty_structures(hip_context, oracle, monkeypatch):
+    """Inner averages on the register-coefficient kernel: a workgroup streams
+    the centres of several whole structures and writes one row per structure;
+    structures without atoms (first, inside, last) get zero rows."""
+
+    monkeypatch.setenv("MDX_HIP_SOAP_KERNEL", "block")
+    work = workloads.config(3, "small")
+    b = work.batch
+    keep = [b._slice_view(0, 40), b._slice_view(40, b.structures)]
+    numbers = np.concatenate([keep[0].numbers, keep[1].numbers])
+    positions = np.concatenate([keep[0].positions, keep[1].positions])
+    sizes = [0] + list(np.diff(keep[0].offsets)) + [0, 0] + list(np.diff(keep[1].offsets)) + [0]
+    offsets = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
+    structures = len(sizes)
+    batch = mdx.StructureBatch(numbers, positions, np.zeros((structures, 3, 3)), np.zeros((structures, 3)),
+                               offsets, [str(i) for i in range(structures)])
+    for dtype in ("float64", "float32"):
+        values, timing = _check(hip_context, oracle, batch, work.params, "inner", dtype)
+        assert timing["expansion_tiles"] == -1004
+        assert values.shape[0] == structures
+        for row in np.flatnonzero(np.diff(offsets) == 0):
+            assert np.all(values[row] == 0.0)
 
 
 @pytest.mark.parametrize("cutoff", [3.5, 3.5 + SOAP_PAD])
