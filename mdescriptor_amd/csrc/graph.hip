@@ -394,8 +394,8 @@ __global__ void k_centre_fill(const int64_t* centre_cell, const int32_t* centre_
 // bin index of every accepted image at pair_start[centre] onwards (wave
 // ballot + popcount compaction).  Slotted pass (kNbrSlotted, the SOAP
 // expansion's layout): both at once, each centre's rows at centre * cap
-// onwards (rows past cap are dropped; stats[0] receives the total rows).
-// Both counting passes record the largest row count of a centre in stats[1].
+// onwards (rows past cap are dropped; the statistics lines receive the total
+// rows).  Both counting passes record the largest row count of a centre there.
 constexpr int kNbrThreads = 512;
 constexpr int kNbrWaves = kNbrThreads / kWave;
 constexpr int kStage = 1024;        // candidates staged in LDS per pass over a cell's centres
@@ -403,6 +403,7 @@ constexpr int kCentreBatch = 128;   // centres whose running counts live in LDS 
 constexpr int kSegments = kMaxSpecies * 27;
 constexpr int kNoBoundary = 0x7fffffff;
 constexpr int kNbrCount = 0, kNbrFill = 1, kNbrSlotted = 2;
+constexpr int kWaveCellImages = kWave; // binned images of a cell searched by one wavefront
 
 // a wave-uniform 64-bit value in scalar registers
 __device__ inline int64_t uniform_i64(int64_t v) {
@@ -420,8 +421,8 @@ __device__ inline uint64_t lane_range(int lo, int hi) {
 
 template <int kMode>
 __global__ __launch_bounds__(kNbrThreads) void k_neighbors(
-    const StructGeom* geom, const int32_t* cell_struct, const double* positions, int64_t cells_total,
-    const int64_t* cell_centre_start, const int32_t* cell_centres, const int64_t* cell_start,
+    const StructGeom* geom, const int32_t* cell_struct, const double* positions, const int32_t* cell_list,
+    int64_t cells_total, const int64_t* cell_centre_start, const int32_t* cell_centres, const int64_t* cell_start,
     const int64_t* cell_species_start, const double* bx, const double* by, const double* bz, int S,
     double accept_max, int32_t* counts, int32_t* totals, int64_t* pair_start, uint32_t* pair_bin, int64_t cap,
     unsigned long long* stats) {
@@ -443,7 +444,9 @@ __global__ __launch_bounds__(kNbrThreads) void k_neighbors(
     const int lane = tid % kWave;
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int nseg = S * 27;
-    for (int64_t c = blockIdx.x; c < cells_total; c += gridDim.x) {
+    // the cells of the list, or (no list) every cell
+    for (int64_t w = blockIdx.x; w < cells_total; w += gridDim.x) {
+        const int64_t c = cell_list != nullptr ? static_cast<int64_t>(cell_list[w]) : w;
         const int64_t c0 = cell_centre_start[c], c1 = cell_centre_start[c + 1];
         if (c0 == c1) continue;
         const StructGeom& g = geom[cell_struct[c]];
@@ -618,10 +621,11 @@ __global__ __launch_bounds__(kNbrThreads) void k_neighbors(
             if (kCount) {
                 for (int i = tid; i < nb; i += kNbrThreads) {
                     totals[s_centre[i]] = s_found[i];
-                    atomicMax(&stats[kStatMostRows], static_cast<unsigned long long>(s_found[i]));
+                    const int sl = static_cast<int>((blockIdx.x + static_cast<unsigned>(i)) % kStatLanes);
+                    atomicMax(&stats[stat_most(sl)], static_cast<unsigned long long>(s_found[i]));
                     if (kMode == kNbrSlotted) {
                         pair_start[s_centre[i]] = s_first[i];
-                        atomicAdd(&stats[kStatRows], static_cast<unsigned long long>(s_found[i]));
+                        atomicAdd(&stats[stat_rows(sl)], static_cast<unsigned long long>(s_found[i]));
                     }
                 }
                 for (int i = tid; i < nb * S; i += kNbrThreads) {
@@ -634,6 +638,88 @@ __global__ __launch_bounds__(kNbrThreads) void k_neighbors(
                 }
             }
             __syncthreads();
+        }
+    }
+}
+
+// Kernel 1 for the cells of structures whose region of interest is a single
+// cell holding at most one wavefront of binned images (small molecules):
+// every image of the structure is a candidate of each of its centres, and
+// the 27-cell walk of k_neighbors visits only the home cell, so its candidate
+// sequence is the cell's bins in order.  One wavefront per cell, candidate =
+// lane: per centre one distance test, a ballot, and the rows written at
+// their place in the sequence (mbcnt); the counts per species are the
+// ballot's popcounts over the species' lane ranges.  Same passes, rows and
+// counts as k_neighbors.
+template <int kMode>
+__global__ __launch_bounds__(kBlock) void k_neighbors_wave(
+    const int32_t* wave_cells, int64_t n_cells, const double* positions, const int64_t* cell_centre_start,
+    const int32_t* cell_centres, const int64_t* cell_start, const int64_t* cell_species_start, const double* bx,
+    const double* by, const double* bz, int S, double accept_max, int32_t* counts, int32_t* totals,
+    int64_t* pair_start, uint32_t* pair_bin, int64_t cap, unsigned long long* stats) {
+    constexpr bool kFill = kMode == kNbrFill;
+    constexpr bool kCount = kMode != kNbrFill;
+    constexpr bool kWrite = kMode != kNbrCount;
+    constexpr int kWavesPerBlock = kBlock / kWave;
+    const int lane = threadIdx.x % kWave;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+    int32_t most = 0;
+    int64_t rows_total = 0;
+    for (int64_t w = uniform_i64(static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave);
+         w < n_cells; w += stride) {
+        const int64_t c = uniform_i64(wave_cells[w]);
+        const int64_t start = uniform_i64(cell_start[c]);
+        // at most a wavefront of images (the host's choice of these cells)
+        const int n = __builtin_amdgcn_readfirstlane(static_cast<int>(min<int64_t>(cell_start[c + 1] - start, kWave)));
+        if (n <= 0) continue;
+        const bool real = lane < n;
+        const uint32_t bin = static_cast<uint32_t>(start + (real ? lane : 0));
+        const double x = bx[bin], y = by[bin], z = bz[bin];
+        // species t of the cell at lanes [lo, hi) (lane t holds its own range)
+        int lo = 0, hi = n;
+        if (kCount && S > 1 && lane < S) {
+            lo = static_cast<int>(cell_species_start[c * S + lane] - start);
+            hi = lane + 1 == S ? n : static_cast<int>(cell_species_start[c * S + lane + 1] - start);
+        }
+        const uint64_t species_lanes = lane_range(lo, hi);
+        const int64_t k0 = uniform_i64(cell_centre_start[c]), k1 = uniform_i64(cell_centre_start[c + 1]);
+        for (int64_t k = k0; k < k1; ++k) {
+            const int64_t centre = __builtin_amdgcn_readfirstlane(cell_centres[k]);
+            const double px = positions[centre * 3 + 0];
+            const double py = positions[centre * 3 + 1];
+            const double pz = positions[centre * 3 + 2];
+            // displacement = image - centre; d^2 = (dx*dx + dy*dy) + dz*dz, no
+            // contraction (as k_neighbors)
+            const double dx = x - px;
+            const double dy = y - py;
+            const double dz = z - pz;
+            const double d2 = dx * dx + dy * dy + dz * dz;
+            const bool accept = real && d2 <= accept_max;
+            const uint64_t mask = __ballot(accept);
+            const int32_t found = static_cast<int32_t>(__popcll(mask));
+            if (kWrite) {
+                const int64_t first = kFill ? uniform_i64(pair_start[centre]) : centre * cap;
+                const int64_t limit = kFill ? static_cast<int64_t>(totals[centre]) : cap;
+                const uint32_t row = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                                               __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
+                if (accept && row < limit) pair_bin[first + row] = bin;
+            }
+            if (kCount) {
+                if (lane < S) counts[centre * S + lane] = static_cast<int32_t>(__popcll(mask & species_lanes));
+                if (lane == 0) {
+                    totals[centre] = found;
+                    if (kMode == kNbrSlotted) pair_start[centre] = centre * cap;
+                }
+                most = max(most, found);
+                rows_total += found;
+            }
+        }
+    }
+    if (kCount && lane == 0) {
+        const int sl = static_cast<int>((blockIdx.x * kWavesPerBlock + threadIdx.x / kWave) % kStatLanes);
+        if (most > 0) atomicMax(&stats[stat_most(sl)], static_cast<unsigned long long>(most));
+        if (kMode == kNbrSlotted && rows_total > 0) {
+            atomicAdd(&stats[stat_rows(sl)], static_cast<unsigned long long>(rows_total));
         }
     }
 }
@@ -899,6 +985,29 @@ void prepare_batch(const mdx_batch_view& batch, const int32_t* species, int n_sp
     }
     out.ext_total = ext;
     out.cells_total = cells;
+    // wavefront cells: a one-cell ROI (every image binned into it) holding at
+    // most a wavefront of images; then every other cell, if there are any
+    out.cell_lists.clear();
+    out.most_images = 0;
+    for (const StructGeom& g : out.geom) {
+        out.most_images = std::max(out.most_images, static_cast<int64_t>(g.natoms) * g.n_images);
+    }
+    auto one_cell = [](const StructGeom& g) {
+        return g.natoms > 0 && g.roi_dim[0] == 1 && g.roi_dim[1] == 1 && g.roi_dim[2] == 1 &&
+               static_cast<int64_t>(g.natoms) * g.n_images <= kWaveCellImages;
+    };
+    for (const StructGeom& g : out.geom) {
+        if (one_cell(g)) out.cell_lists.push_back(static_cast<int32_t>(g.cell_begin));
+    }
+    out.wave_cells = static_cast<int64_t>(out.cell_lists.size());
+    if (out.wave_cells > 0) {
+        for (int64_t s = 0; s < batch.structures; ++s) {
+            const StructGeom& g = out.geom[static_cast<size_t>(s)];
+            if (g.natoms == 0 || one_cell(g)) continue;
+            const int64_t end = s + 1 < batch.structures ? out.geom[static_cast<size_t>(s) + 1].cell_begin : cells;
+            for (int64_t c = g.cell_begin; c < end; ++c) out.cell_lists.push_back(static_cast<int32_t>(c));
+        }
+    }
 }
 
 void upload_batch(hipStream_t stream, const mdx_batch_view& batch, PreparedBatch& pb) {
@@ -909,6 +1018,11 @@ void upload_batch(hipStream_t stream, const mdx_batch_view& batch, PreparedBatch
     pb.d_geom.reserve(std::max<size_t>(1, pb.geom.size() * sizeof(StructGeom)));
     pb.d_images.reserve(std::max<size_t>(1, pb.images.size() * sizeof(ImageDesc)));
     pb.d_offsets.reserve(pb.offsets.size() * sizeof(int64_t));
+    pb.d_cell_lists.reserve(std::max<size_t>(1, pb.cell_lists.size() * sizeof(int32_t)));
+    if (!pb.cell_lists.empty()) {
+        MDX_HIP(hipMemcpyAsync(pb.d_cell_lists.ptr, pb.cell_lists.data(), pb.cell_lists.size() * sizeof(int32_t),
+                               hipMemcpyHostToDevice, stream));
+    }
     if (atoms > 0) {
         MDX_HIP(hipMemcpyAsync(pb.d_positions.ptr, batch.positions, atoms * 3 * sizeof(double),
                                hipMemcpyHostToDevice, stream));
@@ -931,6 +1045,20 @@ void upload_batch(hipStream_t stream, const mdx_batch_view& batch, PreparedBatch
     // but wait so the host vectors may change after return
     MDX_HIP(hipStreamSynchronize(stream));
 }
+
+namespace {
+
+// rows and largest row count over the statistics lines
+void reduce_stats(const unsigned long long* st, int64_t& rows, int64_t& most) {
+    rows = 0;
+    most = 0;
+    for (int l = 0; l < kStatLanes; ++l) {
+        rows += static_cast<int64_t>(st[stat_rows(l)]);
+        most = std::max(most, static_cast<int64_t>(st[stat_most(l)]));
+    }
+}
+
+} // namespace
 
 int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr, const volatile int32_t* cancel,
                     bool slotted) {
@@ -1027,21 +1155,43 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     // d^2 < c^2 is d^2 <= the largest double below c^2
     const double cutoff2 = pb.cutoff * pb.cutoff;
     const double accept_max = pb.include_boundary ? cutoff2 : std::nextafter(cutoff2, 0.0);
-    const unsigned cell_blocks = static_cast<unsigned>(std::min<int64_t>(cells, 1 << 20));
+    // cells searched by whole workgroups: the list after the wavefront cells,
+    // or every cell when there are none
+    const int64_t wave_cells = pb.wave_cells;
+    const int32_t* lists = pb.d_cell_lists.as<int32_t>();
+    const int64_t big_cells = wave_cells > 0 ? static_cast<int64_t>(pb.cell_lists.size()) - wave_cells : cells;
+    const int32_t* big_list = wave_cells > 0 ? lists + wave_cells : nullptr;
     auto neighbors = [&](auto mode, int64_t cap) {
-        hipLaunchKernelGGL(k_neighbors<decltype(mode)::value>, dim3(cell_blocks), dim3(kNbrThreads), 0, stream, geom,
-                           gr.cell_struct.as<int32_t>(), pos, cells, gr.cell_centre_start.as<int64_t>(),
-                           gr.cell_centres.as<int32_t>(),
-                           gr.cell_start.as<int64_t>(), gr.cell_species_start.as<int64_t>(), gr.bin_x.as<double>(),
-                           gr.bin_y.as<double>(), gr.bin_z.as<double>(), S, accept_max, gr.counts.as<int32_t>(),
-                           gr.totals.as<int32_t>(), gr.pair_start.as<int64_t>(), gr.pair_bin.as<uint32_t>(), cap,
-                           stats);
+        if (big_cells > 0) {
+            const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(big_cells, 1 << 20));
+            hipLaunchKernelGGL(k_neighbors<decltype(mode)::value>, dim3(blocks), dim3(kNbrThreads), 0, stream, geom,
+                               gr.cell_struct.as<int32_t>(), pos, big_list, big_cells,
+                               gr.cell_centre_start.as<int64_t>(), gr.cell_centres.as<int32_t>(),
+                               gr.cell_start.as<int64_t>(), gr.cell_species_start.as<int64_t>(),
+                               gr.bin_x.as<double>(), gr.bin_y.as<double>(), gr.bin_z.as<double>(), S, accept_max,
+                               gr.counts.as<int32_t>(), gr.totals.as<int32_t>(), gr.pair_start.as<int64_t>(),
+                               gr.pair_bin.as<uint32_t>(), cap, stats);
+        }
+        if (wave_cells > 0) {
+            constexpr int64_t per_block = kBlock / kWave;
+            const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((wave_cells + per_block - 1) / per_block,
+                                                                            1 << 20));
+            hipLaunchKernelGGL(k_neighbors_wave<decltype(mode)::value>, dim3(blocks), dim3(kBlock), 0, stream, lists,
+                               wave_cells, pos, gr.cell_centre_start.as<int64_t>(), gr.cell_centres.as<int32_t>(),
+                               gr.cell_start.as<int64_t>(), gr.cell_species_start.as<int64_t>(),
+                               gr.bin_x.as<double>(), gr.bin_y.as<double>(), gr.bin_z.as<double>(), S, accept_max,
+                               gr.counts.as<int32_t>(), gr.totals.as<int32_t>(), gr.pair_start.as<int64_t>(),
+                               gr.pair_bin.as<uint32_t>(), cap, stats);
+        }
         MDX_HIP(hipGetLastError());
     };
     using Count = std::integral_constant<int, kNbrCount>;
     using Fill = std::integral_constant<int, kNbrFill>;
     using Slotted = std::integral_constant<int, kNbrSlotted>;
-    const int64_t cap = slotted ? gr.slot_cap : 0;
+    // slots no wider than the most rows a centre can have (a structure's
+    // binned images), in whole 64-byte lines: small structures keep their
+    // rows close together
+    const int64_t cap = slotted ? std::min(gr.slot_cap, std::max<int64_t>(16, (pb.most_images + 15) / 16 * 16)) : 0;
     const int64_t slot_bytes = atoms * cap * static_cast<int64_t>(sizeof(uint32_t));
     // from an arena, the slotted layout only when its rows fit in what is left
     ScratchArena* arena = gr.pair_bin.arena;
@@ -1059,8 +1209,8 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
         gr.read_back.wait(stream);
         if (st[kStatError] != 0) throw Error(MDX_INTERNAL, "a centre fell outside its structure's cell grid");
         if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
-        const int64_t pairs = static_cast<int64_t>(st[kStatRows]);
-        const int64_t most = static_cast<int64_t>(st[kStatMostRows]);
+        int64_t pairs = 0, most = 0;
+        reduce_stats(st, pairs, most);
         const int64_t binned = static_cast<int64_t>(st[kStatBinned]);
         gr.most_rows = most;
         if (most <= cap) {
@@ -1098,7 +1248,8 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     MDX_HIP(hipMemcpyAsync(st, stats, sizeof(st), hipMemcpyDeviceToHost, stream));
     MDX_HIP(hipStreamSynchronize(stream));
     const int64_t binned = static_cast<int64_t>(st[kStatBinned]);
-    gr.most_rows = static_cast<int64_t>(st[kStatMostRows]);
+    int64_t counted = 0;
+    reduce_stats(st, counted, gr.most_rows);
     if (st[kStatError] != 0) throw Error(MDX_INTERNAL, "a centre fell outside its structure's cell grid");
     if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
     if (pairs >= (int64_t(1) << 40)) throw Error(MDX_INTERNAL, "implausible neighbour pair count");

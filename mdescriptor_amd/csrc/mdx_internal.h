@@ -108,6 +108,14 @@ struct PreparedBatch {
     // work items of the averaged SOAP modes (host copies outlive the async upload)
     std::vector<int64_t> item_begin, struct_items;
     int n_species = 1;
+    // ROI cells searched one wavefront per cell (structures whose ROI is one
+    // cell with at most a wavefront of binned images), then, when there are
+    // any, the other cells: cell_lists[0, wave_cells) and [wave_cells, end)
+    std::vector<int32_t> cell_lists;
+    int64_t wave_cells = 0;
+    // most binned images of one structure: no centre has more rows
+    int64_t most_images = 0;
+    DeviceBuffer d_cell_lists; // i32[cell_lists.size()]
     DeviceBuffer d_positions; // f64[atoms*3]
     DeviceBuffer d_types;     // i32[atoms]
     DeviceBuffer d_atom_struct; // i32[atoms]
@@ -198,10 +206,17 @@ struct DeviceGraph {
 // count and a fill pass) when every centre fits; graph.slots records the
 // layout built.  Only consumers that read rows through pair_start[centre] and
 // the per-species counts may ask for it (the SOAP expansion).
-// graph statistics words, read back once per build: rows of the search pass,
-// the largest row count of a centre, binned images, and an error flag (set by a
-// kernel on an internal inconsistency)
-constexpr int kStatRows = 0, kStatMostRows = 1, kStatBinned = 2, kStatError = 3, kStatWords = 4;
+// graph statistics words, read back once per build: binned images and an
+// error flag (set by a kernel on an internal inconsistency) in the first
+// 128-byte line, then kStatLanes lines of (rows of the search pass, largest
+// row count of a centre).  The search kernels spread their atomics over those
+// lines: atomics on one address serialise across the whole device.
+constexpr int kStatBinned = 0, kStatError = 1;
+constexpr int kStatLineWords = 16;
+constexpr int kStatLanes = 32;
+constexpr int kStatWords = kStatLineWords * (1 + kStatLanes);
+__host__ __device__ constexpr int stat_rows(int lane) { return kStatLineWords * (1 + lane); }
+__host__ __device__ constexpr int stat_most(int lane) { return kStatLineWords * (1 + lane) + 1; }
 constexpr int64_t kMinSlotCap = 512;
 constexpr int64_t kMaxSlotCap = 8192;
 constexpr int64_t kMaxSlottedBytes = int64_t(4) << 30;
