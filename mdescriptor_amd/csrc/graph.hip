@@ -263,6 +263,20 @@ __global__ void k_bin_atoms(const StructGeom* geom, const ImageDesc* images, con
              a += static_cast<int64_t>(gridDim.x) * blockDim.x) {
             const StructGeom& g = geom[centre_struct[a]];
             if (q >= g.n_images) continue;
+            const uint32_t j = static_cast<uint32_t>(a - g.atom_begin);
+            const uint32_t ext = static_cast<uint32_t>(q) * static_cast<uint32_t>(g.natoms) + j;
+            if (g.one_cell != 0) {
+                // every image in the one cell: its count is known and the
+                // extended index is a free slot (no atomics)
+                const int64_t c = g.cell_begin;
+                if (kFill) {
+                    const uint64_t major = species_major ? static_cast<uint64_t>(types[a]) << 32 : 0;
+                    keys[cell_start[c] + ext] = major | ext;
+                } else if (ext == 0) {
+                    cell_count[c] = g.natoms * g.n_images;
+                }
+                continue;
+            }
             const ImageDesc& im = images[g.image_begin + q];
             bool inside;
             const int64_t c = roi_cell(g, positions[a * 3 + 0] + im.shift[0], positions[a * 3 + 1] + im.shift[1],
@@ -271,8 +285,7 @@ __global__ void k_bin_atoms(const StructGeom* geom, const ImageDesc* images, con
             if (kFill) {
                 const int32_t slot = atomicAdd(&cell_count[c], 1);
                 const uint64_t major = species_major ? static_cast<uint64_t>(types[a]) << 32 : 0;
-                const uint32_t j = static_cast<uint32_t>(a - g.atom_begin);
-                keys[cell_start[c] + slot] = major | (static_cast<uint32_t>(q) * static_cast<uint32_t>(g.natoms) + j);
+                keys[cell_start[c] + slot] = major | ext;
             } else {
                 atomicAdd(&cell_count[c], 1);
             }
@@ -320,6 +333,14 @@ __global__ void k_centre_cell(const StructGeom* geom, const int32_t* atom_struct
         const int32_t s = atom_struct[i];
         const StructGeom& g = geom[s];
         centre_struct[i] = static_cast<int32_t>(s);
+        if (g.one_cell != 0) {
+            // every atom of the structure is a centre of its one cell
+            const int32_t j = static_cast<int32_t>(i - g.atom_begin);
+            centre_cell[i] = g.cell_begin;
+            centre_slot[i] = j;
+            if (j == 0) cell_ncentre[g.cell_begin] = g.natoms;
+            continue;
+        }
         bool inside;
         const int64_t c = roi_cell(g, positions[i * 3 + 0], positions[i * 3 + 1], positions[i * 3 + 2], inside);
         if (!inside) {
@@ -996,14 +1017,15 @@ void prepare_batch(const mdx_batch_view& batch, const int32_t* species, int n_sp
         return g.natoms > 0 && g.roi_dim[0] == 1 && g.roi_dim[1] == 1 && g.roi_dim[2] == 1 &&
                static_cast<int64_t>(g.natoms) * g.n_images <= kWaveCellImages;
     };
-    for (const StructGeom& g : out.geom) {
-        if (one_cell(g)) out.cell_lists.push_back(static_cast<int32_t>(g.cell_begin));
+    for (StructGeom& g : out.geom) {
+        g.one_cell = one_cell(g) ? 1 : 0;
+        if (g.one_cell != 0) out.cell_lists.push_back(static_cast<int32_t>(g.cell_begin));
     }
     out.wave_cells = static_cast<int64_t>(out.cell_lists.size());
     if (out.wave_cells > 0) {
         for (int64_t s = 0; s < batch.structures; ++s) {
             const StructGeom& g = out.geom[static_cast<size_t>(s)];
-            if (g.natoms == 0 || one_cell(g)) continue;
+            if (g.natoms == 0 || g.one_cell != 0) continue;
             const int64_t end = s + 1 < batch.structures ? out.geom[static_cast<size_t>(s) + 1].cell_begin : cells;
             for (int64_t c = g.cell_begin; c < end; ++c) out.cell_lists.push_back(static_cast<int32_t>(c));
         }

@@ -79,7 +79,7 @@ struct StructGeom {
     int32_t dims[3];     // full grid dimensions
     int32_t roi_lo[3];   // ROI box origin (grid coordinates)
     int32_t roi_dim[3];  // ROI box extent
-    int32_t pad;
+    int32_t one_cell;    // 1: the ROI is one cell holding every image, at most a wavefront of them
     double minimum[3];   // grid origin (bounding box minus padding)
     double spacing[3];   // cell widths
 };
