@@ -375,6 +375,10 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
     const bool block = p.block_waves > 0 && (p.average == 0 || p.average == 1) &&
                        g.most_rows < kQuadMaxRows;
     const bool block_inner = block && p.average == 1;
+    int64_t largest_structure = 0;
+    for (size_t st = 0; st + 1 < pb.offsets.size(); ++st) {
+        largest_structure = std::max(largest_structure, pb.offsets[st + 1] - pb.offsets[st]);
+    }
 
     // work items
     std::vector<int64_t>& item_begin_h = pb.item_begin;
@@ -487,6 +491,7 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
                 ba.item_base = base;
                 ba.items = count;
                 ba.struct_offsets = block_inner ? pb.d_offsets.as<int64_t>() : nullptr;
+                ba.small_structures = block_inner && largest_structure <= kBlockSmallAtoms ? 1 : 0;
                 ba.out = out_device;
                 ba.pitch = pitch_bytes;
                 launch_block_expand(stream, p.l_max, p.block_kg, p.block_ncr, ba, count);

@@ -8,6 +8,12 @@
 
 namespace mdx {
 
+// Stream kinds of the kernel: a row per centre; a row per structure (inner
+// average) from a centre-by-centre stream; the same from a species-major
+// stream over the structure's pairs (structures of at most 64 atoms).
+constexpr int kBlockRows = 0, kBlockInner = 1, kBlockInnerSmall = 2;
+constexpr int kBlockSmallAtoms = 64;
+
 // Launch arguments (one struct, passed by value).
 struct BlockArgs {
     const double* positions;    // f64[atoms * 3]
@@ -26,6 +32,7 @@ struct BlockArgs {
     int64_t item_base, items, per_block; // centres, or structures when struct_offsets is set
     const int64_t* struct_offsets;       // null: a row per centre; else first centre of each structure
                                          // (+ end): a row per structure, its centres' average
+    int small_structures;                // averages: every structure has at most 64 atoms
     void* out;
     int64_t pitch;              // bytes between output rows
 };

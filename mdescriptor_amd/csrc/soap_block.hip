@@ -334,7 +334,7 @@ __device__ __forceinline__ int64_t uniform64(int64_t v) {
     return static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | static_cast<uint32_t>(lo));
 }
 
-template <int LM, int KG, int NCR, int ES, bool AVG, int W>
+template <int LM, int KG, int NCR, int ES, int MODE, int W>
 __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, const int* s_ps) {
     using PL = BlockPlan<LM, KG>;
     constexpr int L = PL::L, R = PL::R, P = PL::P, RPL = PL::RPL, NT = PL::NT, GS = PL::GS;
@@ -392,7 +392,10 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
     // structure averages whole structures, whose centres are consecutive
     const int64_t work_first = a.item_base + static_cast<int64_t>(blockIdx.x) * a.per_block;
     const int64_t work_last = min(work_first + a.per_block, a.item_base + a.items);
-    constexpr bool inner = AVG; // rows of structure averages (a.struct_offsets set)
+    constexpr bool inner = MODE != kBlockRows; // rows of structure averages (a.struct_offsets set)
+    // structures of at most a wavefront of atoms: pairs streamed species-major
+    // across the structure's centres (an average sums them in any order)
+    constexpr bool kSpeciesMajor = MODE == kBlockInnerSmall;
     const int64_t item_first = inner ? uniform64(a.struct_offsets[work_first]) : work_first;
     const int64_t item_last = inner ? uniform64(a.struct_offsets[work_last]) : work_last;
     // structure of the stream's centre and its centre range (inner)
@@ -440,9 +443,59 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
         st_left = 0;
         if (st_more != 0) next_species();
     };
-    // pipeline stage of one chunk; everything but the bin is wave-uniform
+    // Species-major stream (structures of at most 64 atoms): lane i stands
+    // for centre i of the structure.  For species q the structure's rows of
+    // that species, centre after centre, form one sequence cut into chunks;
+    // a slot finds its centre by a binary search over the centres' running
+    // row totals (end_i) and its row at rowbase_i + (slot - first slot of
+    // centre i), rowbase_i being the centre's first row of species q.
+    int64_t sm_a0 = 0;      // first atom (centre) of the structure
+    int sm_n = 0;           // its atoms
+    int sm_total = 0;       // rows of species st_q over the structure
+    int sm_base = 0;        // first slot of the next chunk
+    int64_t l_rowbase = 0;  // lane i: first row of species st_q of centre i
+    int l_cnt = 0;          // lane i: rows of species st_q of centre i
+    int l_end = 0;          // lane i: rows of species st_q of centres 0..i
+    auto sm_species = [&]() {
+        st_q = __builtin_amdgcn_readfirstlane(__builtin_ctz(st_more));
+        st_more = __builtin_amdgcn_readfirstlane(st_more & (st_more - 1));
+        // the rows of the species before (none between: they have no rows)
+        l_rowbase += l_cnt;
+        l_cnt = lane < sm_n ? a.counts[(sm_a0 + lane) * S + st_q] : 0;
+        int v = l_cnt;
+#pragma unroll
+        for (int off = 1; off < kWaveThreads; off *= 2) {
+            const int u = __shfl_up(v, off);
+            if (lane >= off) v += u;
+        }
+        l_end = v;
+        sm_total = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(v, kWaveThreads - 1));
+        sm_base = 0;
+    };
+    auto sm_structure = [&]() -> bool {
+        // the next structure with atoms, if any
+        do {
+            st_struct = uniform64(st_struct + 1);
+        } while (st_struct < work_last &&
+                 uniform64(a.struct_offsets[st_struct + 1]) == uniform64(a.struct_offsets[st_struct]));
+        if (st_struct >= work_last) return false;
+        sm_a0 = uniform64(a.struct_offsets[st_struct]);
+        sm_n = __builtin_amdgcn_readfirstlane(static_cast<int>(uniform64(a.struct_offsets[st_struct + 1]) - sm_a0));
+        l_rowbase = lane < sm_n ? a.pair_start[sm_a0 + lane] : 0;
+        l_cnt = 0;
+        // species with rows in the structure
+        uint32_t present = 0;
+        for (int t = 0; t < S; ++t) {
+            const int c = lane < sm_n ? a.counts[(sm_a0 + lane) * S + t] : 0;
+            if (__ballot(c > 0) != 0) present |= 1u << t;
+        }
+        st_more = __builtin_amdgcn_readfirstlane(present);
+        return true;
+    };
+    // pipeline stage of one chunk; everything but the bin and the centre is
+    // wave-uniform
     struct Stage {
-        int64_t centre; // -1: no chunk
+        int64_t centre; // -1: no chunk (species-major: the structure)
         int q;          // species
         int rows;       // rows in the chunk (slots past them are pad slots)
         int groups;     // step groups
@@ -450,9 +503,55 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
         bool last;      // last chunk of its output row: of its centre, or of its structure (inner)
         uint32_t bin;   // bin of the lane's slot row (slot < rows)
         int64_t row;    // output row (centre, or structure)
+        int catom;      // species-major: centre (atom) of the lane's slot
     };
     auto next_stage = [&]() -> Stage {
-        Stage s{-1, 0, 0, 0, false, false, 0u, 0};
+        Stage s{-1, 0, 0, 0, false, false, 0u, 0, 0};
+        if constexpr (kSpeciesMajor) {
+            if (sm_base >= sm_total) {
+                if (st_more == 0) {
+                    if (!sm_structure()) return s;
+                    if (st_more == 0) {
+                        // no rows at all: an empty chunk ends the structure (a zero row)
+                        s.centre = st_struct;
+                        s.q = st_q;
+                        s.ends = s.last = true;
+                        s.row = st_struct;
+                        return s;
+                    }
+                }
+                sm_species();
+            }
+            const int n = min(sm_total - sm_base, kNb);
+            s.centre = st_struct;
+            s.q = st_q;
+            s.rows = n;
+            s.groups = (n + GS - 1) / GS;
+            if constexpr (kHarm) {
+                // pad slots repeat the chunk's last slot
+                const int slot = sm_base + min(lane / 2, n - 1);
+                // centre of the slot: the first whose running total exceeds it
+                int lo = 0, hi = sm_n - 1;
+#pragma unroll
+                for (int it = 0; it < 6; ++it) {
+                    const int mid = (lo + hi) / 2;
+                    const bool right = __shfl(l_end, mid) <= slot;
+                    lo = right ? mid + 1 : lo;
+                    hi = right ? hi : mid;
+                }
+                const int before = __shfl(l_end, lo) - __shfl(l_cnt, lo);
+                const int64_t base = static_cast<int64_t>(
+                    (static_cast<uint64_t>(static_cast<uint32_t>(__shfl(static_cast<int>(l_rowbase >> 32), lo))) << 32) |
+                    static_cast<uint32_t>(__shfl(static_cast<int>(l_rowbase), lo)));
+                s.bin = a.pair_bin[base + (slot - before)];
+                s.catom = static_cast<int>(sm_a0) + lo;
+            }
+            sm_base = __builtin_amdgcn_readfirstlane(sm_base + n);
+            s.last = sm_base >= sm_total && st_more == 0;
+            s.ends = s.last;
+            s.row = st_struct;
+            return s;
+        }
         if (st_left == 0) {
             if (st_more != 0) {
                 next_species();
@@ -482,16 +581,22 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
         return s;
     };
 
-    if (item_first < item_last) prefetch_centre(item_first);
+    if (!kSpeciesMajor && item_first < item_last) prefetch_centre(item_first);
     Stage s0 = next_stage(); // chunk k (contraction)
     Stage s1 = next_stage(); // chunk k + 1 (harmonics)
     double px = 0.0, py = 0.0, pz = 0.0;
+    double qx = 0.0, qy = 0.0, qz = 0.0; // species-major: the slot's centre
     const int jj = lane / 2, comp = lane % 2;
     auto load_positions = [&](const Stage& s) {
         if constexpr (kHarm) {
             px = a.bx[s.bin];
             py = a.by[s.bin];
             pz = a.bz[s.bin];
+            if constexpr (kSpeciesMajor) {
+                qx = a.positions[3 * static_cast<int64_t>(s.catom)];
+                qy = a.positions[3 * static_cast<int64_t>(s.catom) + 1];
+                qz = a.positions[3 * static_cast<int64_t>(s.catom) + 2];
+            }
         }
     };
     // harmonics of a stage's slots from the centre position (cx, cy, cz)
@@ -510,8 +615,12 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
     // prologue: harmonics of the first chunk
     load_positions(s0);
     if (kHarm && uniform64(s0.centre) >= 0) {
-        const int64_t c = uniform64(s0.centre);
-        harmonics(s0, 0, a.positions[3 * c], a.positions[3 * c + 1], a.positions[3 * c + 2]);
+        if constexpr (kSpeciesMajor) {
+            harmonics(s0, 0, qx, qy, qz);
+        } else {
+            const int64_t c = uniform64(s0.centre);
+            harmonics(s0, 0, a.positions[3 * c], a.positions[3 * c + 1], a.positions[3 * c + 2]);
+        }
     }
     load_positions(s1);
     __syncthreads();
@@ -584,7 +693,7 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
         const int64_t centre1 = uniform64(s1.centre);
         const int64_t cpos1 = 3 * (centre1 >= 0 ? centre1 : 0);
         double cx1 = 0.0, cy1 = 0.0, cz1 = 0.0;
-        if constexpr (kHarm) {
+        if constexpr (kHarm && !kSpeciesMajor) {
             cx1 = a.positions[cpos1];
             cy1 = a.positions[cpos1 + 1];
             cz1 = a.positions[cpos1 + 2];
@@ -717,7 +826,13 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
             unroll<NU>([&](auto u) { unroll<NCR>([&](auto r) { C[decltype(u)::value][decltype(r)::value] = 0.0; }); });
         }
         // ---------------------------------------- harmonics of chunk k + 1
-        if (kHarm && centre1 >= 0) harmonics(s1, buf ^ 1, cx1, cy1, cz1);
+        if (kHarm && centre1 >= 0) {
+            if constexpr (kSpeciesMajor) {
+                harmonics(s1, buf ^ 1, qx, qy, qz);
+            } else {
+                harmonics(s1, buf ^ 1, cx1, cy1, cz1);
+            }
+        }
         load_positions(s2);
         s0 = s1;
         s1 = s2;
@@ -726,7 +841,7 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
     }
 }
 
-template <int LM, int KG, int NCR, int ES, bool AVG>
+template <int LM, int KG, int NCR, int ES, int MODE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) void k_soap_block(BlockArgs a) {
     using PL = BlockPlan<LM, KG>;
     // staging buffers, d2, exp table, padded S_lm table, power-spectrum
@@ -767,15 +882,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) void k
     __syncthreads();
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWaveThreads);
     if (wave == 0) {
-        block_role<LM, KG, NCR, ES, AVG, 0>(a, lds, s_ps);
+        block_role<LM, KG, NCR, ES, MODE, 0>(a, lds, s_ps);
     } else if constexpr (PL::T > 1) {
         if (wave == 1) {
-            block_role<LM, KG, NCR, ES, AVG, (PL::T > 1 ? 1 : 0)>(a, lds, s_ps);
+            block_role<LM, KG, NCR, ES, MODE, (PL::T > 1 ? 1 : 0)>(a, lds, s_ps);
         } else if constexpr (PL::T > 2) {
             if (wave == 2) {
-                block_role<LM, KG, NCR, ES, AVG, (PL::T > 2 ? 2 : 0)>(a, lds, s_ps);
+                block_role<LM, KG, NCR, ES, MODE, (PL::T > 2 ? 2 : 0)>(a, lds, s_ps);
             } else if constexpr (PL::T > 3) {
-                block_role<LM, KG, NCR, ES, AVG, (PL::T > 3 ? 3 : 0)>(a, lds, s_ps);
+                block_role<LM, KG, NCR, ES, MODE, (PL::T > 3 ? 3 : 0)>(a, lds, s_ps);
             }
         }
     }
@@ -797,16 +912,21 @@ void launch_shape(hipStream_t stream, const BlockArgs& a, int64_t count) {
     args.per_block = std::max<int64_t>(1, (count + target - 1) / target);
     const unsigned grid = static_cast<unsigned>((count + args.per_block - 1) / args.per_block);
     const dim3 threads(PL::T * kWaveThreads);
-    if (a.struct_offsets == nullptr) {
+    const int mode = a.struct_offsets == nullptr ? kBlockRows : a.small_structures ? kBlockInnerSmall : kBlockInner;
+    auto launch = [&](auto m) {
+        constexpr int M = decltype(m)::value;
         if (a.out_dtype == 4) {
-            hipLaunchKernelGGL((k_soap_block<LM, KG, NCR, 4, false>), dim3(grid), threads, 0, stream, args);
+            hipLaunchKernelGGL((k_soap_block<LM, KG, NCR, 4, M>), dim3(grid), threads, 0, stream, args);
         } else {
-            hipLaunchKernelGGL((k_soap_block<LM, KG, NCR, 8, false>), dim3(grid), threads, 0, stream, args);
+            hipLaunchKernelGGL((k_soap_block<LM, KG, NCR, 8, M>), dim3(grid), threads, 0, stream, args);
         }
-    } else if (a.out_dtype == 4) {
-        hipLaunchKernelGGL((k_soap_block<LM, KG, NCR, 4, true>), dim3(grid), threads, 0, stream, args);
+    };
+    if (mode == kBlockRows) {
+        launch(std::integral_constant<int, kBlockRows>{});
+    } else if (mode == kBlockInner) {
+        launch(std::integral_constant<int, kBlockInner>{});
     } else {
-        hipLaunchKernelGGL((k_soap_block<LM, KG, NCR, 8, true>), dim3(grid), threads, 0, stream, args);
+        launch(std::integral_constant<int, kBlockInnerSmall>{});
     }
 }
 
