@@ -252,6 +252,9 @@ __device__ inline void image_position(const StructGeom& g, const ImageDesc* imag
 
 // Binning walks (image, atom) pairs on a 2-D grid (y: image, x: atom), so no
 // index division is needed.  The extended index of (image q, local atom j) is
+constexpr int kLdsBinCells = 2048; // ROI cells of a structure binned in LDS, at most
+constexpr int kBinChunk = 4096;    // images per LDS binning workgroup
+
 // q * natoms + j (neighbor.cpp:519-528).  Count pass: cell_count[c] += 1;
 // fill pass: keys at cell_start[c] + a slot taken from cell_count.
 template <bool kFill>
@@ -262,7 +265,7 @@ __global__ void k_bin_atoms(const StructGeom* geom, const ImageDesc* images, con
         for (int64_t a = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; a < atoms;
              a += static_cast<int64_t>(gridDim.x) * blockDim.x) {
             const StructGeom& g = geom[centre_struct[a]];
-            if (q >= g.n_images) continue;
+            if (q >= g.n_images || g.lds_bins != 0) continue;
             const uint32_t j = static_cast<uint32_t>(a - g.atom_begin);
             const uint32_t ext = static_cast<uint32_t>(q) * static_cast<uint32_t>(g.natoms) + j;
             if (g.one_cell != 0) {
@@ -290,6 +293,68 @@ __global__ void k_bin_atoms(const StructGeom* geom, const ImageDesc* images, con
                 atomicAdd(&cell_count[c], 1);
             }
         }
+    }
+}
+
+// Binning of the structures with few ROI cells, a run of kBinChunk images
+// per workgroup: each image takes a slot among the workgroup's images of its
+// cell from an LDS counter; then one global atomic per (workgroup, cell)
+// adds the workgroup's count (count pass) or reserves the workgroup's range
+// of the cell (fill pass).  Same cells, keys and cell counts as
+// k_bin_atoms; the order inside a cell is restored by k_bin_sort.
+constexpr int kBinThreads = 512;
+constexpr int kBinPer = kBinChunk / kBinThreads;
+
+template <bool kFill>
+__global__ __launch_bounds__(kBinThreads) void k_bin_lds(const BinChunk* chunks, const StructGeom* geom,
+                                                         const ImageDesc* images, const double* positions,
+                                                         const int32_t* types, int species_major, int32_t* cell_count,
+                                                         const int64_t* cell_start, uint64_t* keys) {
+    __shared__ int32_t s_count[kLdsBinCells];
+    __shared__ int32_t s_base[kFill ? kLdsBinCells : 1];
+    const BinChunk ch = chunks[blockIdx.x];
+    const StructGeom& g = geom[ch.structure];
+    const int ncells = g.roi_dim[0] * g.roi_dim[1] * g.roi_dim[2];
+    const int tid = threadIdx.x;
+    for (int i = tid; i < ncells; i += kBinThreads) s_count[i] = 0;
+    __syncthreads();
+    int lc[kBinPer], slot[kBinPer];
+#pragma unroll
+    for (int r = 0; r < kBinPer; ++r) {
+        const int e = tid + r * kBinThreads;
+        lc[r] = -1;
+        slot[r] = 0;
+        if (e < ch.count) {
+            const int64_t ext = ch.first + e;
+            const int64_t q = ext / g.natoms;
+            const int64_t a = g.atom_begin + (ext - q * g.natoms);
+            const ImageDesc& im = images[g.image_begin + q];
+            bool inside;
+            const int64_t c = roi_cell(g, positions[a * 3 + 0] + im.shift[0], positions[a * 3 + 1] + im.shift[1],
+                                       positions[a * 3 + 2] + im.shift[2], inside);
+            if (inside) {
+                lc[r] = static_cast<int>(c - g.cell_begin);
+                slot[r] = atomicAdd(&s_count[lc[r]], 1);
+            }
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < ncells; i += kBinThreads) {
+        const int n = s_count[i];
+        if (n == 0) continue;
+        const int base = atomicAdd(&cell_count[g.cell_begin + i], n);
+        if (kFill) s_base[i] = base;
+    }
+    if (!kFill) return;
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kBinPer; ++r) {
+        if (lc[r] < 0) continue;
+        const int64_t ext = ch.first + tid + r * kBinThreads;
+        const int64_t a = g.atom_begin + ext % g.natoms;
+        const uint64_t major = species_major ? static_cast<uint64_t>(types[a]) << 32 : 0;
+        const int64_t c = g.cell_begin + lc[r];
+        keys[cell_start[c] + s_base[lc[r]] + slot[r]] = major | static_cast<uint64_t>(ext);
     }
 }
 
@@ -703,12 +768,24 @@ __global__ __launch_bounds__(kBlock) void k_neighbors_wave(
             hi = lane + 1 == S ? n : static_cast<int>(cell_species_start[c * S + lane + 1] - start);
         }
         const uint64_t species_lanes = lane_range(lo, hi);
-        const int64_t k0 = uniform_i64(cell_centre_start[c]), k1 = uniform_i64(cell_centre_start[c + 1]);
-        for (int64_t k = k0; k < k1; ++k) {
-            const int64_t centre = __builtin_amdgcn_readfirstlane(cell_centres[k]);
-            const double px = positions[centre * 3 + 0];
-            const double py = positions[centre * 3 + 1];
-            const double pz = positions[centre * 3 + 2];
+        // the cell's centres (the structure's atoms, at most a wavefront) one
+        // per lane, read into scalars centre by centre
+        const int64_t k0 = uniform_i64(cell_centre_start[c]);
+        const int nk = __builtin_amdgcn_readfirstlane(
+            static_cast<int>(min<int64_t>(uniform_i64(cell_centre_start[c + 1]) - k0, kWave)));
+        if (nk <= 0) continue;
+        const int my_centre = cell_centres[k0 + min(lane, nk - 1)];
+        const double cx = positions[static_cast<int64_t>(my_centre) * 3 + 0];
+        const double cy = positions[static_cast<int64_t>(my_centre) * 3 + 1];
+        const double cz = positions[static_cast<int64_t>(my_centre) * 3 + 2];
+        for (int k = 0; k < nk; ++k) {
+            const int64_t centre = __builtin_amdgcn_readlane(my_centre, k);
+            const double px = __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(cx), k),
+                                               __builtin_amdgcn_readlane(__double2loint(cx), k));
+            const double py = __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(cy), k),
+                                               __builtin_amdgcn_readlane(__double2loint(cy), k));
+            const double pz = __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(cz), k),
+                                               __builtin_amdgcn_readlane(__double2loint(cz), k));
             // displacement = image - centre; d^2 = (dx*dx + dy*dy) + dz*dz, no
             // contraction (as k_neighbors)
             const double dx = x - px;
@@ -1017,9 +1094,23 @@ void prepare_batch(const mdx_batch_view& batch, const int32_t* species, int n_sp
         return g.natoms > 0 && g.roi_dim[0] == 1 && g.roi_dim[1] == 1 && g.roi_dim[2] == 1 &&
                static_cast<int64_t>(g.natoms) * g.n_images <= kWaveCellImages;
     };
-    for (StructGeom& g : out.geom) {
+    out.bin_chunks.clear();
+    out.direct_bins = false;
+    for (int64_t s = 0; s < batch.structures; ++s) {
+        StructGeom& g = out.geom[static_cast<size_t>(s)];
         g.one_cell = one_cell(g) ? 1 : 0;
         if (g.one_cell != 0) out.cell_lists.push_back(static_cast<int32_t>(g.cell_begin));
+        const int64_t roi = static_cast<int64_t>(g.roi_dim[0]) * g.roi_dim[1] * g.roi_dim[2];
+        g.lds_bins = g.natoms > 0 && g.one_cell == 0 && roi <= kLdsBinCells ? 1 : 0;
+        if (g.lds_bins != 0) {
+            const int64_t images = static_cast<int64_t>(g.natoms) * g.n_images;
+            for (int64_t first = 0; first < images; first += kBinChunk) {
+                out.bin_chunks.push_back(BinChunk{first, static_cast<int32_t>(s),
+                                                  static_cast<int32_t>(std::min<int64_t>(kBinChunk, images - first))});
+            }
+        } else if (g.natoms > 0) {
+            out.direct_bins = true;
+        }
     }
     out.wave_cells = static_cast<int64_t>(out.cell_lists.size());
     if (out.wave_cells > 0) {
@@ -1041,6 +1132,11 @@ void upload_batch(hipStream_t stream, const mdx_batch_view& batch, PreparedBatch
     pb.d_images.reserve(std::max<size_t>(1, pb.images.size() * sizeof(ImageDesc)));
     pb.d_offsets.reserve(pb.offsets.size() * sizeof(int64_t));
     pb.d_cell_lists.reserve(std::max<size_t>(1, pb.cell_lists.size() * sizeof(int32_t)));
+    pb.d_bin_chunks.reserve(std::max<size_t>(1, pb.bin_chunks.size() * sizeof(BinChunk)));
+    if (!pb.bin_chunks.empty()) {
+        MDX_HIP(hipMemcpyAsync(pb.d_bin_chunks.ptr, pb.bin_chunks.data(), pb.bin_chunks.size() * sizeof(BinChunk),
+                               hipMemcpyHostToDevice, stream));
+    }
     if (!pb.cell_lists.empty()) {
         MDX_HIP(hipMemcpyAsync(pb.d_cell_lists.ptr, pb.cell_lists.data(), pb.cell_lists.size() * sizeof(int32_t),
                                hipMemcpyHostToDevice, stream));
@@ -1148,15 +1244,34 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     for (const StructGeom& sg : pb.geom) max_images = std::max(max_images, static_cast<int>(sg.n_images));
     const dim3 bin_grid(static_cast<unsigned>(std::min<int64_t>((atoms + kBlock - 1) / kBlock, 1 << 16)),
                         static_cast<unsigned>(std::min(max_images, 65535)));
-    hipLaunchKernelGGL(k_bin_atoms<false>, bin_grid, dim3(kBlock), 0, stream, geom, images, pos,
-                       gr.centre_struct.as<int32_t>(), pb.d_types.as<int32_t>(), 0, atoms, max_images, cell_count,
-                       static_cast<const int64_t*>(nullptr), static_cast<uint64_t*>(nullptr));
+    const unsigned chunk_grid = static_cast<unsigned>(pb.bin_chunks.size());
+    const BinChunk* chunks = pb.d_bin_chunks.as<BinChunk>();
+    const int species_major = S > 1 ? 1 : 0;
+    if (pb.direct_bins) {
+        hipLaunchKernelGGL(k_bin_atoms<false>, bin_grid, dim3(kBlock), 0, stream, geom, images, pos,
+                           gr.centre_struct.as<int32_t>(), pb.d_types.as<int32_t>(), 0, atoms, max_images, cell_count,
+                           static_cast<const int64_t*>(nullptr), static_cast<uint64_t*>(nullptr));
+    }
+    if (chunk_grid > 0) {
+        hipLaunchKernelGGL(k_bin_lds<false>, dim3(chunk_grid), dim3(kBinThreads), 0, stream, chunks, geom, images, pos,
+                           pb.d_types.as<int32_t>(), 0, cell_count, static_cast<const int64_t*>(nullptr),
+                           static_cast<uint64_t*>(nullptr));
+    }
     scan_counts(stream, cell_count, gr.cell_start.as<int64_t>(), cells, gr.scan_tmp);
-    hipLaunchKernelGGL(k_bin_atoms<true>, bin_grid, dim3(kBlock), 0, stream, geom, images, pos,
-                       gr.centre_struct.as<int32_t>(), pb.d_types.as<int32_t>(), S > 1 ? 1 : 0, atoms, max_images,
-                       cell_fill, gr.cell_start.as<int64_t>(), gr.bin_key.as<uint64_t>());
+    if (pb.direct_bins) {
+        hipLaunchKernelGGL(k_bin_atoms<true>, bin_grid, dim3(kBlock), 0, stream, geom, images, pos,
+                           gr.centre_struct.as<int32_t>(), pb.d_types.as<int32_t>(), species_major, atoms, max_images,
+                           cell_fill, gr.cell_start.as<int64_t>(), gr.bin_key.as<uint64_t>());
+    }
+    if (chunk_grid > 0) {
+        hipLaunchKernelGGL(k_bin_lds<true>, dim3(chunk_grid), dim3(kBinThreads), 0, stream, chunks, geom, images, pos,
+                           pb.d_types.as<int32_t>(), species_major, cell_fill, gr.cell_start.as<int64_t>(),
+                           gr.bin_key.as<uint64_t>());
+    }
     const unsigned cell_grid = static_cast<unsigned>(std::min<int64_t>(cells, 1 << 20));
-    hipLaunchKernelGGL(k_bin_sort, dim3(cell_grid), dim3(kBlock), 0, stream, geom, gr.cell_struct.as<int32_t>(),
+    // a wavefront per cell when cells hold a wavefront of images on average
+    const int sort_threads = ext <= static_cast<int64_t>(kWave) * cells ? kWave : kBlock;
+    hipLaunchKernelGGL(k_bin_sort, dim3(cell_grid), dim3(sort_threads), 0, stream, geom, gr.cell_struct.as<int32_t>(),
                        images, pos,
                        pb.d_types.as<int32_t>(), gr.cell_start.as<int64_t>(), cells, gr.bin_key.as<uint64_t>(),
                        gr.bin_x.as<double>(), gr.bin_y.as<double>(), gr.bin_z.as<double>(), gr.bin_atom.as<int32_t>(),

@@ -80,8 +80,18 @@ struct StructGeom {
     int32_t roi_lo[3];   // ROI box origin (grid coordinates)
     int32_t roi_dim[3];  // ROI box extent
     int32_t one_cell;    // 1: the ROI is one cell holding every image, at most a wavefront of them
+    int32_t lds_bins;    // 1: binned by workgroups counting in LDS over the ROI cells (kLdsBinCells or fewer)
+    int32_t reserved;
     double minimum[3];   // grid origin (bounding box minus padding)
     double spacing[3];   // cell widths
+};
+
+// A run of one structure's binned images [first, first + count) in extended
+// (image-major) order: the work of one binning workgroup.
+struct BinChunk {
+    int64_t first;
+    int32_t structure;
+    int32_t count;
 };
 
 // Periodic image: integer shift and its Cartesian vector, computed on the
@@ -115,6 +125,11 @@ struct PreparedBatch {
     int64_t wave_cells = 0;
     // most binned images of one structure: no centre has more rows
     int64_t most_images = 0;
+    // binning work of the structures binned in LDS; whether any other
+    // structure has images (those are binned with global atomics)
+    std::vector<BinChunk> bin_chunks;
+    bool direct_bins = false;
+    DeviceBuffer d_bin_chunks; // BinChunk[bin_chunks.size()]
     DeviceBuffer d_cell_lists; // i32[cell_lists.size()]
     DeviceBuffer d_positions; // f64[atoms*3]
     DeviceBuffer d_types;     // i32[atoms]
