@@ -74,20 +74,21 @@ BENCH_OPTIONS = {
 }
 
 
-def flops_per_env(kbar: float, S: int, n: int, l_max: int, features: int | None = None,
-                  coefficient_species: int | None = None, spectra_per_env: float = 1.0) -> float:
-    """Algorithmic FP64 flops per environment (FMA = 2): accumulation
-    2*K*n*H, beta contraction 2*Sc*n^2*H (Sc coefficient species: 1 for mu2,
-    else S), power spectrum 2*(2l+1) per feature of degree l, i.e.
-    features/(l_max+1) * 2H (with compression off S*n*(S*n+1)*H), taken
-    `spectra_per_env` times per environment.""" 
+def algorithmic_flops(envs: int, rows: int, kbar: float, S: int, n: int, l_max: int, features: int | None = None,
+                      coefficient_species: int | None = None) -> float:
+    """Algorithmic FP64 flops of one pass (FMA = 2): accumulation 2*K*n*H
+    per environment; per output row (a centre, or with inner averages a
+    structure, whose coefficients are averaged before the fold) the beta
+    contraction 2*Sc*n^2*H (Sc coefficient species: 1 for mu2, else S) and
+    the power spectrum, 2*(2l+1) per feature of degree l, i.e.
+    features/(l_max+1) * 2H (with compression off S*n*(S*n+1)*H).""" 
 
     L = l_max + 1
     H = L * L
     if features is None:
         features = S * n * (S * n + 1) // 2 * L
     sc = S if coefficient_species is None else coefficient_species
-    return 2.0 * kbar * n * H + 2.0 * sc * n * n * H + spectra_per_env * features / L * 2.0 * H
+    return envs * 2.0 * kbar * n * H + rows * (2.0 * sc * n * n * H + features / L * 2.0 * H)
 
 
 def profile_average_us(workload_name: str, kernel: str) -> tuple[float | None, str | None]:
@@ -413,12 +414,11 @@ def soap_bench(args, workload) -> dict:
     kbar = pairs / envs
     S, n, l_max = len(p["species"]), p["n_max"], p["l_max"]
     compression = (options or {}).get("compression", "off")
-    # with average "inner" the spectrum is formed once per structure by the
-    # finalize kernel, not by the expansion kernel timed here
-    spectra = 0.0 if p["average"] == "inner" else 1.0
-    per_env = flops_per_env(kbar, S, n, l_max, plan.features, 1 if compression == "mu2" else S, spectra)
+    rows = batch.structures if p["average"] == "inner" else envs
+    total_flops = algorithmic_flops(envs, rows, kbar, S, n, l_max, plan.features, 1 if compression == "mu2" else S)
+    per_env = total_flops / envs
     launches = max(1, int(timings[-1]["expansion_launches"]))
-    flops_launch = envs * per_env / launches
+    flops_launch = total_flops / launches
     launch_ms = statistics.mean(t["expansion_ms"] for t in timings) / launches
     achieved = flops_launch / (launch_ms * 1e-3) / 1e12
     tiles = int(timings[-1]["expansion_tiles"])
