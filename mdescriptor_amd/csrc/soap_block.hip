@@ -104,22 +104,24 @@ struct BlockPlan {
     // the second buffer the d2 and exp tables, all finite
     static constexpr int YROWS = H;
     static constexpr int YWORDS = YROWS * kYS;
-#ifndef MDX_BLOCK_HARMONIC_WAVES
-#define MDX_BLOCK_HARMONIC_WAVES 1
-#endif
     // wavefronts that stage the harmonics (the first HW roles): each pays a
-    // per-slot set-up, so fewer of them do less work in total
-    static constexpr int HW = MDX_BLOCK_HARMONIC_WAVES < T ? MDX_BLOCK_HARMONIC_WAVES : T;
+    // per-slot set-up, so fewer of them do less work in total; from l_max 8
+    // one wavefront's share of the columns outweighs it (measured: two
+    // wavefronts 6 % faster at l_max 8 and 9, 7-11 % slower at 3, 4 and 6)
+    static constexpr int HW = (LM >= 8 ? 2 : 1) < T ? (LM >= 8 ? 2 : 1) : T;
 
     // degrees of each wavefront: longest processing time first over the cost
     // of a degree per step group (exps of 12 VALU instructions, 4 cycles each,
-    // and its MFMAs of 16 cycles)
+    // and its MFMAs of 16 cycles), the harmonic wavefronts starting with
+    // their share of the staging (their columns' VALU instructions per chunk,
+    // 4 cycles each, spread over the chunk's step groups)
     struct Owners {
         unsigned mask[4];
     };
     static constexpr Owners owners() {
         Owners o{};
         int load[4] = {0, 0, 0, 0};
+        for (int w = 0; w < HW; ++w) load[w] = 4 * range_cost(mlo(w), mhi(w)) / GROUPS;
         bool done[L] = {};
         for (int it = 0; it < L; ++it) {
             int best = -1, best_cost = -1;
