@@ -25,6 +25,8 @@
 #include <type_traits>
 
 #include <algorithm>
+#include <chrono>
+#include <thread>
 #include <cmath>
 #include <cstring>
 #include <limits>
@@ -116,10 +118,20 @@ void StreamPoint::prepare() {
 void StreamPoint::wait(hipStream_t stream) {
     prepare();
     MDX_HIP(hipEventRecord(event_, stream));
+    // Poll first: the short waits (the graph statistics) would otherwise pay
+    // a blocking synchronisation's wake-up of tens of microseconds.  Past
+    // 200 us of polling yield the core between polls, past 2 ms block.
+    const auto start = std::chrono::steady_clock::now();
     for (;;) {
         const hipError_t e = hipEventQuery(event_);
         if (e == hipSuccess) return;
         if (e != hipErrorNotReady) MDX_HIP(e);
+        const auto waited = std::chrono::steady_clock::now() - start;
+        if (waited > std::chrono::milliseconds(2)) {
+            MDX_HIP(hipEventSynchronize(event_));
+            return;
+        }
+        if (waited > std::chrono::microseconds(200)) std::this_thread::yield();
     }
 }
 
@@ -1336,8 +1348,13 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
                            (arena == nullptr || static_cast<size_t>(slot_bytes) <= arena->left());
     gr.slots = 0;
     if (use_slots) {
-        // one pass: counts and rows at centre * cap
-        gr.pair_bin.reserve(static_cast<size_t>(atoms * cap) * sizeof(uint32_t));
+        // one pass: counts and rows at centre * cap; a reservation four times
+        // what is needed and over 256 MiB (left by a denser batch) goes back
+        const size_t need = static_cast<size_t>(atoms * cap) * sizeof(uint32_t);
+        if (arena == nullptr && gr.pair_bin.bytes > 4 * need && gr.pair_bin.bytes > (size_t(256) << 20)) {
+            gr.pair_bin.release();
+        }
+        gr.pair_bin.reserve(need);
         neighbors(Slotted{}, cap);
         unsigned long long* st = gr.stats_host.get(kStatWords);
         MDX_HIP(hipMemcpyAsync(st, stats, kStatWords * sizeof(unsigned long long), hipMemcpyDeviceToHost, stream));
@@ -1351,6 +1368,10 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
         const int64_t binned = static_cast<int64_t>(st[kStatBinned]);
         gr.most_rows = most;
         if (most <= cap) {
+            // slots grown for a denser batch shrink back to what fits this one
+            int64_t fit = kMinSlotCap;
+            while (fit < most) fit *= 2;
+            if (fit < gr.slot_cap) gr.slot_cap = fit;
             gr.slots = cap;
             gr.pairs = pairs;
             gr.binned = binned;
@@ -1387,6 +1408,12 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     const int64_t binned = static_cast<int64_t>(st[kStatBinned]);
     int64_t counted = 0;
     reduce_stats(st, counted, gr.most_rows);
+    if (slotted && gr.slot_cap == 0 && gr.most_rows <= kMaxSlotCap) {
+        // the slotted layout again once a batch's centres fit a slot
+        int64_t fit = kMinSlotCap;
+        while (fit < gr.most_rows) fit *= 2;
+        gr.slot_cap = fit;
+    }
     if (st[kStatError] != 0) throw Error(MDX_INTERNAL, "a centre fell outside its structure's cell grid");
     if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
     if (pairs >= (int64_t(1) << 40)) throw Error(MDX_INTERNAL, "implausible neighbour pair count");

@@ -182,6 +182,24 @@ def test_block_kernel_shapes(hip_context, oracle, monkeypatch, species, n_max, l
         assert timing["expansion_tiles"] == -1004
 
 
+@pytest.mark.parametrize("kernel", ["block", "quad", "mfma"])
+def test_far_translated_structures(hip_context, oracle, monkeypatch, kernel):
+    """Molecules placed 1e4-3e4 A from the origin and from each other: a pad
+    slot of a chunk may hold the position of another structure's atom, which
+    must not reach an exp (a far-out argument overflows the table exp's
+    exponent); every matrix-core kernel against the oracle."""
+
+    monkeypatch.setenv("MDX_HIP_SOAP_KERNEL", kernel)
+    work = workloads.config(3, "small")
+    part = work.batch._slice_view(0, 12)
+    shifts = np.repeat(np.array([[1e4 * (s + 1), -2e4 * (s % 2), 3e4 * (s % 3)] for s in range(part.structures)]),
+                       np.diff(part.offsets), axis=0)
+    batch = mdx.StructureBatch(part.numbers, part.positions + shifts, part.cells, part.pbc, part.offsets,
+                               list(part.ids))
+    for average in ("off", "inner") if kernel == "block" else ("off", "inner", "outer"):
+        _check(hip_context, oracle, batch, work.params, average, "float64")
+
+
 def test_block_kernel_inner_average_with_empty_structures(hip_context, oracle, monkeypatch):
     """Inner averages on the register-coefficient kernel: a workgroup streams
     the centres of several whole structures and writes one row per structure;
