@@ -717,6 +717,10 @@ __global__ __launch_bounds__(kNbrThreads) void k_neighbors(
                 __syncthreads();
             }
             if (kCount) {
+                if (tid == 0) {
+                    atomicAdd(&stats[stat_centres(static_cast<int>(blockIdx.x % kStatLanes))],
+                              static_cast<unsigned long long>(nb));
+                }
                 for (int i = tid; i < nb; i += kNbrThreads) {
                     totals[s_centre[i]] = s_found[i];
                     const int sl = static_cast<int>((blockIdx.x + static_cast<unsigned>(i)) % kStatLanes);
@@ -763,6 +767,7 @@ __global__ __launch_bounds__(kBlock) void k_neighbors_wave(
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
     int32_t most = 0;
     int64_t rows_total = 0;
+    int64_t searched = 0; // centres
     for (int64_t w = uniform_i64(static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave);
          w < n_cells; w += stride) {
         const int64_t c = uniform_i64(wave_cells[w]);
@@ -824,9 +829,11 @@ __global__ __launch_bounds__(kBlock) void k_neighbors_wave(
                 rows_total += found;
             }
         }
+        searched += nk;
     }
     if (kCount && lane == 0) {
         const int sl = static_cast<int>((blockIdx.x * kWavesPerBlock + threadIdx.x / kWave) % kStatLanes);
+        if (searched > 0) atomicAdd(&stats[stat_centres(sl)], static_cast<unsigned long long>(searched));
         if (most > 0) atomicMax(&stats[stat_most(sl)], static_cast<unsigned long long>(most));
         if (kMode == kNbrSlotted && rows_total > 0) {
             atomicAdd(&stats[stat_rows(sl)], static_cast<unsigned long long>(rows_total));
@@ -984,8 +991,14 @@ void prepare_batch(const mdx_batch_view& batch, const int32_t* species, int n_sp
     }
     out.images.clear();
     int64_t ext = 0, cells = 0;
+    // home cells holding centres (global ROI cell indices, ascending per
+    // structure): the cells the search visits
+    std::vector<int32_t> occupied;
+    std::vector<int64_t> homes;
+    std::vector<int64_t> occupied_begin(static_cast<size_t>(batch.structures) + 1, 0);
     for (int64_t s = 0; s < batch.structures; ++s) {
         StructGeom& g = out.geom[static_cast<size_t>(s)];
+        occupied_begin[static_cast<size_t>(s)] = static_cast<int64_t>(occupied.size());
         std::memset(&g, 0, sizeof(g));
         const int64_t begin = batch.offsets[s];
         const int64_t natoms = batch.offsets[s + 1] - begin;
@@ -1085,18 +1098,36 @@ void prepare_batch(const mdx_batch_view& batch, const int32_t* species, int n_sp
             g.roi_dim[a] = hi - g.roi_lo[a] + 1;
             volume *= g.roi_dim[a];
         }
+        // the same cell arithmetic as the device's roi_cell
+        homes.clear();
+        for (int64_t i = begin; i < begin + natoms; ++i) {
+            int64_t local = 0;
+            for (int a = 2; a >= 0; --a) {
+                const int c = grid_coordinate(batch.positions[i * 3 + a], g.minimum[a], g.spacing[a], g.dims[a]);
+                local = local * g.roi_dim[a] + (c - g.roi_lo[a]);
+            }
+            homes.push_back(cells + local);
+        }
+        std::sort(homes.begin(), homes.end());
+        homes.erase(std::unique(homes.begin(), homes.end()), homes.end());
+        for (int64_t c : homes) occupied.push_back(static_cast<int32_t>(c));
         cells += volume;
         if (cells > (int64_t(1) << 30)) {
             throw Error(MDX_INVALID_ARGUMENT, "neighbor cell-grid exceeds the device graph capacity");
         }
     }
+    occupied_begin[static_cast<size_t>(batch.structures)] = static_cast<int64_t>(occupied.size());
     if (ext >= (int64_t(1) << 32) - 1) {
         throw Error(MDX_INVALID_ARGUMENT, "periodic images exceed the device graph capacity");
     }
     out.ext_total = ext;
     out.cells_total = cells;
     // wavefront cells: a one-cell ROI (every image binned into it) holding at
-    // most a wavefront of images; then every other cell, if there are any
+    // most a wavefront of images; then the other structures' home cells that
+    // hold centres, which whole workgroups search: consecutive workgroups
+    // go to consecutive XCDs, so listing only those cells spreads the search
+    // over the chip (a periodic box's occupied cells can otherwise fall on a
+    // few XCDs: 8 of a water box's 64 ROI cells, on 4 XCDs)
     out.cell_lists.clear();
     out.most_images = 0;
     for (const StructGeom& g : out.geom) {
@@ -1125,13 +1156,11 @@ void prepare_batch(const mdx_batch_view& batch, const int32_t* species, int n_sp
         }
     }
     out.wave_cells = static_cast<int64_t>(out.cell_lists.size());
-    if (out.wave_cells > 0) {
-        for (int64_t s = 0; s < batch.structures; ++s) {
-            const StructGeom& g = out.geom[static_cast<size_t>(s)];
-            if (g.natoms == 0 || g.one_cell != 0) continue;
-            const int64_t end = s + 1 < batch.structures ? out.geom[static_cast<size_t>(s) + 1].cell_begin : cells;
-            for (int64_t c = g.cell_begin; c < end; ++c) out.cell_lists.push_back(static_cast<int32_t>(c));
-        }
+    for (int64_t s = 0; s < batch.structures; ++s) {
+        const StructGeom& g = out.geom[static_cast<size_t>(s)];
+        if (g.natoms == 0 || g.one_cell != 0) continue;
+        out.cell_lists.insert(out.cell_lists.end(), occupied.begin() + occupied_begin[static_cast<size_t>(s)],
+                              occupied.begin() + occupied_begin[static_cast<size_t>(s) + 1]);
     }
 }
 
@@ -1178,14 +1207,19 @@ void upload_batch(hipStream_t stream, const mdx_batch_view& batch, PreparedBatch
 
 namespace {
 
-// rows and largest row count over the statistics lines
-void reduce_stats(const unsigned long long* st, int64_t& rows, int64_t& most) {
+// rows and largest row count over the statistics lines; every centre must
+// have been searched (the host's list of home cells holding centres and the
+// device's placement of the centres agree)
+void reduce_stats(const unsigned long long* st, int64_t atoms, int64_t& rows, int64_t& most) {
     rows = 0;
     most = 0;
+    int64_t centres = 0;
     for (int l = 0; l < kStatLanes; ++l) {
         rows += static_cast<int64_t>(st[stat_rows(l)]);
         most = std::max(most, static_cast<int64_t>(st[stat_most(l)]));
+        centres += static_cast<int64_t>(st[stat_centres(l)]);
     }
+    if (centres != atoms) throw Error(MDX_INTERNAL, "the neighbour search missed a centre's home cell");
 }
 
 } // namespace
@@ -1308,8 +1342,8 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     // or every cell when there are none
     const int64_t wave_cells = pb.wave_cells;
     const int32_t* lists = pb.d_cell_lists.as<int32_t>();
-    const int64_t big_cells = wave_cells > 0 ? static_cast<int64_t>(pb.cell_lists.size()) - wave_cells : cells;
-    const int32_t* big_list = wave_cells > 0 ? lists + wave_cells : nullptr;
+    const int64_t big_cells = static_cast<int64_t>(pb.cell_lists.size()) - wave_cells;
+    const int32_t* big_list = lists + wave_cells;
     auto neighbors = [&](auto mode, int64_t cap) {
         if (big_cells > 0) {
             const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(big_cells, 1 << 20));
@@ -1364,7 +1398,7 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
         if (st[kStatError] != 0) throw Error(MDX_INTERNAL, "a centre fell outside its structure's cell grid");
         if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
         int64_t pairs = 0, most = 0;
-        reduce_stats(st, pairs, most);
+        reduce_stats(st, atoms, pairs, most);
         const int64_t binned = static_cast<int64_t>(st[kStatBinned]);
         gr.most_rows = most;
         if (most <= cap) {
@@ -1407,14 +1441,14 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     MDX_HIP(hipStreamSynchronize(stream));
     const int64_t binned = static_cast<int64_t>(st[kStatBinned]);
     int64_t counted = 0;
-    reduce_stats(st, counted, gr.most_rows);
+    if (st[kStatError] != 0) throw Error(MDX_INTERNAL, "a centre fell outside its structure's cell grid");
+    reduce_stats(st, atoms, counted, gr.most_rows);
     if (slotted && gr.slot_cap == 0 && gr.most_rows <= kMaxSlotCap) {
         // the slotted layout again once a batch's centres fit a slot
         int64_t fit = kMinSlotCap;
         while (fit < gr.most_rows) fit *= 2;
         gr.slot_cap = fit;
     }
-    if (st[kStatError] != 0) throw Error(MDX_INTERNAL, "a centre fell outside its structure's cell grid");
     if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
     if (pairs >= (int64_t(1) << 40)) throw Error(MDX_INTERNAL, "implausible neighbour pair count");
     gr.pair_bin.reserve(std::max<size_t>(1, static_cast<size_t>(pairs) * sizeof(uint32_t)));

@@ -119,8 +119,9 @@ struct PreparedBatch {
     std::vector<int64_t> item_begin, struct_items;
     int n_species = 1;
     // ROI cells searched one wavefront per cell (structures whose ROI is one
-    // cell with at most a wavefront of binned images), then, when there are
-    // any, the other cells: cell_lists[0, wave_cells) and [wave_cells, end)
+    // cell with at most a wavefront of binned images), then the other
+    // structures' home cells holding centres: cell_lists[0, wave_cells) and
+    // [wave_cells, end)
     std::vector<int32_t> cell_lists;
     int64_t wave_cells = 0;
     // most binned images of one structure: no centre has more rows
@@ -224,14 +225,16 @@ struct DeviceGraph {
 // graph statistics words, read back once per build: binned images and an
 // error flag (set by a kernel on an internal inconsistency) in the first
 // 128-byte line, then kStatLanes lines of (rows of the search pass, largest
-// row count of a centre).  The search kernels spread their atomics over those
-// lines: atomics on one address serialise across the whole device.
+// row count of a centre, centres searched).  The search kernels spread their
+// atomics over those lines: atomics on one address serialise across the
+// whole device.
 constexpr int kStatBinned = 0, kStatError = 1;
 constexpr int kStatLineWords = 16;
 constexpr int kStatLanes = 32;
 constexpr int kStatWords = kStatLineWords * (1 + kStatLanes);
 __host__ __device__ constexpr int stat_rows(int lane) { return kStatLineWords * (1 + lane); }
 __host__ __device__ constexpr int stat_most(int lane) { return kStatLineWords * (1 + lane) + 1; }
+__host__ __device__ constexpr int stat_centres(int lane) { return kStatLineWords * (1 + lane) + 2; }
 constexpr int64_t kMinSlotCap = 512;
 constexpr int64_t kMaxSlotCap = 8192;
 constexpr int64_t kMaxSlottedBytes = int64_t(4) << 30;
