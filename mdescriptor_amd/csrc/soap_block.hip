@@ -244,22 +244,23 @@ __device__ __forceinline__ double swap_blocks(double v) {
 // exp(x) for x = na * d2 (na = -a <= 0, d2 >= 0, x >= -708): x is rounded
 // exactly as the reference's exp(-a * d2) argument (soap.cpp:895-896), then
 // Tang's table method (ACM TOMS 15(2), 1989) with 256 entries:
-// x = (256k + j) ln2/256 + r, the reduction against ln2/256 split in two
-// (kf * hi exact for |kf| < 2^21), |r| <= ln2/512, exp(x) = 2^k 2^(j/256) e^r
+// x = (256k + j) ln2/256 + r, |r| <= ln2/512, exp(x) = 2^k 2^(j/256) e^r
 // with e^r - 1 by its degree-4 Taylor polynomial (truncation below 4e-17
-// relative).  tab[j] = 2^(j/256) with j << 12 taken off its high word, so
-// that adding (256k + j) << 12 scales it by 2^k in one integer add (the
-// result is a normal number for x >= -708).
+// relative).  The reduction is one fma against ln2/256 rounded to a double
+// (relative error 3.4e-17), which puts |x| * 3.4e-17 of relative error on the
+// result: 3.4e-16 at x = -10, less than the rounding of x itself (|x| *
+// 1.1e-16) that the reference's own argument carries, so a second, low-part
+// fma would buy nothing at the features' accuracy.  tab[j] = 2^(j/256) with
+// j << 12 taken off its high word, so that adding (256k + j) << 12 scales it
+// by 2^k in one integer add (the result is a normal number for x >= -708).
 __device__ __forceinline__ double exp_neg(double d2, double na, const int2* tab) {
     constexpr double kInvLn2xT = 369.32993046757463228414071833648; // 256 / ln 2
-    constexpr double kHi = 0.010830417275428772 / 4.0;               // ln2/256, 32 trailing zero bits
-    constexpr double kLo = 7.420820373486988e-09 / 4.0;              // ln2/256 - kHi
+    constexpr double kLn2OverT = 0.0027076061740622863;              // ln 2 / 256
     constexpr double kShifter = 6755399441055744.0;                  // 1.5 * 2^52
     const double x = na * d2;
     const double s = fma(x, kInvLn2xT, kShifter);
     const double kf = s - kShifter;
-    double r = fma(kf, -kHi, x);
-    r = fma(kf, -kLo, r);
+    const double r = fma(kf, -kLn2OverT, x);
     const int nj = __double2loint(s);
     const int2 t = *reinterpret_cast<const int2*>(reinterpret_cast<const char*>(tab) +
                                                   ((nj << 3) & ((kTab - 1) << 3)));
