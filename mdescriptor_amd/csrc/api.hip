@@ -641,12 +641,14 @@ int mdx_hip_soap_plan_create(mdx_hip_ctx* ctx, const mdx_soap_params* params, md
             if (choice == "quad" && plan->quad_waves == 0) {
                 throw mdx::Error(MDX_INVALID_ARGUMENT, "SOAP plan is outside the 4x4-block kernel's limits");
             }
-            // register-coefficient kernel: default options, atom-level rows or
-            // inner structure averages, a compiled (l_max, radial groups,
-            // species) shape; it keeps its coefficients in registers, so the
-            // tile kernel's LDS limit does not apply to it
-            if (defaults && quad_range && (p.average == 0 || p.average == 1) &&
-                (choice == "auto" || choice == "block")) {
+            // register-coefficient kernel: GTO basis, no compression, atom-level
+            // rows (weighted or not) or unweighted inner structure averages, a
+            // compiled (l_max, radial groups, species) shape; it keeps its
+            // coefficients in registers, so the tile kernel's LDS limit does
+            // not apply to it
+            const bool block_options = plan->compression == 0 && plan->radial_basis == 0 &&
+                                       (p.average == 0 || (p.average == 1 && plan->weighted == 0));
+            if (block_options && quad_range && (choice == "auto" || choice == "block")) {
                 mdx::BlockPlanHost bp;
                 if (mdx::block_plan_tables(plan->S, n, p.l_max, p.out_dtype, beta, pref, expo, bp)) {
                     plan->block_waves = bp.waves;

@@ -370,9 +370,10 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
     if (rows == 0 || d.F == 0) return;
 
     // the register-coefficient kernel where the plan chose it (atom-level
-    // rows, or structure averages of the inner kind, which it forms from the
-    // structure's centres directly) and every centre's rows fit their slot codes
-    const bool block = p.block_waves > 0 && (p.average == 0 || p.average == 1) &&
+    // rows, with or without weights, or unweighted structure averages of the
+    // inner kind, which it forms from the structure's centres directly) and
+    // every centre's rows fit their slot codes
+    const bool block = p.block_waves > 0 && (p.average == 0 || (p.average == 1 && p.weighted == 0)) &&
                        g.most_rows < kQuadMaxRows;
     const bool block_inner = block && p.average == 1;
     int64_t largest_structure = 0;
@@ -492,6 +493,17 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
                 ba.items = count;
                 ba.struct_offsets = block_inner ? pb.d_offsets.as<int64_t>() : nullptr;
                 ba.small_structures = block_inner && largest_structure <= kBlockSmallAtoms ? 1 : 0;
+                if (p.weighted != 0) {
+                    ba.weighting = p.weighting;
+                    ba.has_w0 = p.has_w0;
+                    ba.w_r0 = p.w_r0;
+                    ba.w_c = p.w_c;
+                    ba.w_d = p.w_d;
+                    ba.w_m = p.w_m;
+                    ba.w_w0 = p.w_w0;
+                    ba.species_w = p.d_species_w.as<double>();
+                    ba.bin_atom = g.bin_atom.as<int32_t>();
+                }
                 ba.out = out_device;
                 ba.pitch = pitch_bytes;
                 launch_block_expand(stream, p.l_max, p.block_kg, p.block_ncr, ba, count);

@@ -1,7 +1,7 @@
 // Host/device interface of the register-coefficient SOAP kernel
-// (soap_block.hip): default options (GTO basis, no weighting, no
-// compression), atom-level rows (average "off") or a row per structure of
-// its centres' averaged coefficients (average "inner").
+// (soap_block.hip): GTO basis, no compression; atom-level rows (average
+// "off"), with or without neighbour weights, or a row per structure of its
+// centres' averaged coefficients (average "inner").
 #pragma once
 
 #include "mdx_internal.h"
@@ -10,8 +10,9 @@ namespace mdx {
 
 // Stream kinds of the kernel: a row per centre; a row per structure (inner
 // average) from a centre-by-centre stream; the same from a species-major
-// stream over the structure's pairs (structures of at most 64 atoms).
-constexpr int kBlockRows = 0, kBlockInner = 1, kBlockInnerSmall = 2;
+// stream over the structure's pairs (structures of at most 64 atoms); a row
+// per centre with weighted neighbours.
+constexpr int kBlockRows = 0, kBlockInner = 1, kBlockInnerSmall = 2, kBlockRowsWeighted = 3;
 constexpr int kBlockSmallAtoms = 64;
 
 // Launch arguments (one struct, passed by value).
@@ -33,6 +34,13 @@ struct BlockArgs {
     const int64_t* struct_offsets;       // null: a row per centre; else first centre of each structure
                                          // (+ end): a row per structure, its centres' average
     int small_structures;                // averages: every structure has at most 64 atoms
+    // neighbour weights (soap_weight): distance function kind (0 none),
+    // its parameters, w0 for the centre's own image, species weights
+    int weighting;
+    int has_w0;
+    double w_r0, w_c, w_d, w_m, w_w0;
+    const double* species_w;             // null: no weights
+    const int32_t* bin_atom;             // atom of each binned image
     void* out;
     int64_t pitch;              // bytes between output rows
 };

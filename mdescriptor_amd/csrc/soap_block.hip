@@ -395,7 +395,8 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
     // structure averages whole structures, whose centres are consecutive
     const int64_t work_first = a.item_base + static_cast<int64_t>(blockIdx.x) * a.per_block;
     const int64_t work_last = min(work_first + a.per_block, a.item_base + a.items);
-    constexpr bool inner = MODE != kBlockRows; // rows of structure averages (a.struct_offsets set)
+    constexpr bool inner = MODE == kBlockInner || MODE == kBlockInnerSmall; // rows of structure averages
+    constexpr bool kWeighted = MODE == kBlockRowsWeighted; // neighbour weights scale the harmonic seeds
     // structures of at most a wavefront of atoms: pairs streamed species-major
     // across the structure's centres (an average sums them in any order)
     constexpr bool kSpeciesMajor = MODE == kBlockInnerSmall;
@@ -589,12 +590,16 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
     Stage s1 = next_stage(); // chunk k + 1 (harmonics)
     double px = 0.0, py = 0.0, pz = 0.0;
     double qx = 0.0, qy = 0.0, qz = 0.0; // species-major: the slot's centre
+    int patom = -1;                      // weights with w0: the slot's image's atom
     const int jj = lane / 2, comp = lane % 2;
     auto load_positions = [&](const Stage& s) {
         if constexpr (kHarm) {
             px = a.bx[s.bin];
             py = a.by[s.bin];
             pz = a.bz[s.bin];
+            if constexpr (kWeighted) {
+                if (a.has_w0 != 0) patom = a.bin_atom[s.bin];
+            }
             if constexpr (kSpeciesMajor) {
                 qx = a.positions[3 * static_cast<int64_t>(s.catom)];
                 qy = a.positions[3 * static_cast<int64_t>(s.catom) + 1];
@@ -612,7 +617,17 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
             const double d2 = fma(dz, dz, fma(dx, dx, dy * dy));
             if (comp == 0) s_d2[buf * kNb + jj] = real ? d2 : 0.0;
         }
-        harmonic_columns<LM, MLO, MHI>(dx, dy, dz, real ? 1.0 : 0.0, comp, s_y + buf * PL::YWORDS + jj);
+        double seed = real ? 1.0 : 0.0;
+        if constexpr (kWeighted) {
+            // the neighbour's weight (soap_weight, soap.cpp:389-420); the
+            // centre's own image is the image of the centre atom at distance 0
+            // (a non-zero shift of a nonsingular cell never is)
+            const double r2 = fma(dz, dz, fma(dx, dx, dy * dy));
+            double w = weight_function(a.weighting, a.w_r0, a.w_c, a.w_d, a.w_m, sqrt(r2));
+            if (a.has_w0 != 0 && r2 == 0.0 && static_cast<int64_t>(patom) == uniform64(s.centre)) w = a.w_w0;
+            seed = real ? w * a.species_w[__builtin_amdgcn_readfirstlane(s.q)] : 0.0;
+        }
+        harmonic_columns<LM, MLO, MHI>(dx, dy, dz, seed, comp, s_y + buf * PL::YWORDS + jj);
     };
 
     // prologue: harmonics of the first chunk
@@ -844,8 +859,11 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
     }
 }
 
+// Five wavefronts per SIMD (96 VGPRs); four for the weighted rows, whose
+// distance function (pow) needs the registers of a fifth
 template <int LM, int KG, int NCR, int ES, int MODE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) void k_soap_block(BlockArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == kBlockRowsWeighted ? 4 : 5))) void
+k_soap_block(BlockArgs a) {
     using PL = BlockPlan<LM, KG>;
     // staging buffers, d2, exp table, padded S_lm table, power-spectrum
     // offsets; sized at compile time, so every LDS offset is an immediate
@@ -915,7 +933,8 @@ void launch_shape(hipStream_t stream, const BlockArgs& a, int64_t count) {
     args.per_block = std::max<int64_t>(1, (count + target - 1) / target);
     const unsigned grid = static_cast<unsigned>((count + args.per_block - 1) / args.per_block);
     const dim3 threads(PL::T * kWaveThreads);
-    const int mode = a.struct_offsets == nullptr ? kBlockRows : a.small_structures ? kBlockInnerSmall : kBlockInner;
+    const int mode = a.struct_offsets != nullptr ? (a.small_structures ? kBlockInnerSmall : kBlockInner)
+                     : a.species_w != nullptr ? kBlockRowsWeighted : kBlockRows;
     auto launch = [&](auto m) {
         constexpr int M = decltype(m)::value;
         if (a.out_dtype == 4) {
@@ -928,8 +947,10 @@ void launch_shape(hipStream_t stream, const BlockArgs& a, int64_t count) {
         launch(std::integral_constant<int, kBlockRows>{});
     } else if (mode == kBlockInner) {
         launch(std::integral_constant<int, kBlockInner>{});
-    } else {
+    } else if (mode == kBlockInnerSmall) {
         launch(std::integral_constant<int, kBlockInnerSmall>{});
+    } else {
+        launch(std::integral_constant<int, kBlockRowsWeighted>{});
     }
 }
 

@@ -326,5 +326,16 @@ __device__ inline void power_spectrum_tiles(const double* s_c, const int* loff, 
 
 constexpr double kPi = 3.141592653589793238462643383279502884;
 
+// Distance function of a neighbour's weight (soap_weight, soap.cpp:389-420):
+// 1 poly, c (1 + 2x^3 - 3x^2)^m for x = r / r0 <= 1, else 0; 2 pow,
+// c / (d + x^m); 3 exp, c / (d + e^-x); 0 none (1).
+__device__ inline double weight_function(int kind, double r0, double c, double d, double m, double distance) {
+    if (kind == 0) return 1.0;
+    const double ratio = distance / r0;
+    if (kind == 1) return distance > r0 ? 0.0 : c * pow(1.0 + 2.0 * ratio * ratio * ratio - 3.0 * ratio * ratio, m);
+    if (kind == 2) return c / (d + pow(ratio, m));
+    return c / (d + exp(-ratio));
+}
+
 } // namespace
 } // namespace mdx

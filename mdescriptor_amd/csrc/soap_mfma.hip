@@ -67,17 +67,7 @@ __device__ inline double exp_neg(double x, const double* tab64) {
 // Weight of one neighbour (soap_weight, soap.cpp:389-420): the distance
 // function, w0 for the centre's own image, times the species weight.
 __device__ inline double neighbour_weight(const MfmaDims& d, double distance, bool exact_self, double species_w) {
-    double value = 1.0;
-    if (d.weighting != 0) {
-        const double ratio = distance / d.w_r0;
-        if (d.weighting == 1) {
-            value = distance > d.w_r0 ? 0.0 : d.w_c * pow(1.0 + 2.0 * ratio * ratio * ratio - 3.0 * ratio * ratio, d.w_m);
-        } else if (d.weighting == 2) {
-            value = d.w_c / (d.w_d + pow(ratio, d.w_m));
-        } else {
-            value = d.w_c / (d.w_d + exp(-ratio));
-        }
-    }
+    double value = weight_function(d.weighting, d.w_r0, d.w_c, d.w_d, d.w_m, distance);
     if (exact_self && d.has_w0) value = d.w_w0;
     return value * species_w;
 }

@@ -62,6 +62,41 @@ def test_option_at_hcno_shape(hip_context, oracle, name):
     _run(hip_context, oracle, 2, name, "off", limit=8)
 
 
+WEIGHTS = ["poly", "pow_w0", "exp", "w0_only", "species_weights"]
+
+
+@pytest.mark.parametrize("shape", [(1, 4, 3), (2, 8, 6), (3, 6, 4), (4, 8, 8), (5, 9, 9)])
+@pytest.mark.parametrize("name", WEIGHTS)
+def test_weights_on_register_coefficient_kernel(hip_context, oracle, monkeypatch, shape, name):
+    """Neighbour weights on the register-coefficient kernel (atom-level rows)
+    for each compiled shape: the configuration's species and structures at
+    its (n_max, l_max), config 5 with nine channels (three radial groups).
+    Twelve channels with pow or poly weights are too ill-conditioned for the
+    gate (max |beta| 1e5 at 5.5 A): there any two summation orders differ by
+    1-2e-10 scaled, this kernel's and the 16x16 kernel's alike."""
+
+    config, n_max, l_max = shape
+    cut_scale = 1.0
+    monkeypatch.setenv("MDX_HIP_SOAP_KERNEL", "block")
+    w = workloads.config(config, "small")
+    p = w.params
+    r_cut = p["r_cut"] * cut_scale
+    options = option_arguments(name, p["species"], r_cut, n_max)
+    alphas, betas = basis_gto(r_cut, n_max, l_max)
+    plan = _hip.SoapPlan(hip_context, species=p["species"], n_max=n_max, l_max=l_max, r_cut=r_cut, sigma=1.0,
+                         alphas=alphas, betas=betas, average="off", dtype="float64", options=options)
+    try:
+        values, timing = plan.compute(w.batch)
+    finally:
+        plan.close()
+    assert timing["expansion_tiles"] <= -1000
+    expected = oracle.soap(w.batch, species=p["species"], n_max=n_max, l_max=l_max, r_cut=r_cut, sigma=1.0,
+                           alphas=alphas, betas=betas, average="off", options=options)
+    assert np.all(np.isfinite(values))
+    error = scaled_error(values, expected)
+    assert error <= F64_GATE, f"{name} {shape}: scaled error {error:.3e}"
+
+
 @pytest.mark.parametrize("name", ["polynomial", "mu1nu1", "exp"])
 def test_option_float32(hip_context, oracle, name):
     _run(hip_context, oracle, 1, name, "off", dtype="float32")
