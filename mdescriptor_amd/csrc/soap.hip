@@ -370,10 +370,11 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
     if (rows == 0 || d.F == 0) return;
 
     // the register-coefficient kernel where the plan chose it (atom-level
-    // rows, with or without weights, or unweighted structure averages of the
-    // inner kind, which it forms from the structure's centres directly) and
-    // every centre's rows fit their slot codes
-    const bool block = p.block_waves > 0 && (p.average == 0 || (p.average == 1 && p.weighted == 0)) &&
+    // rows, with or without weights and with the compressions it takes, or
+    // unweighted, uncompressed structure averages of the inner kind, which it
+    // forms from the structure's centres directly) and every centre's rows
+    // fit their slot codes
+    const bool block = p.block_waves > 0 && (p.average == 0 || (p.average == 1 && p.weighted == 0 && p.compression == 0)) &&
                        g.most_rows < kQuadMaxRows;
     const bool block_inner = block && p.average == 1;
     int64_t largest_structure = 0;
@@ -493,6 +494,7 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
                 ba.items = count;
                 ba.struct_offsets = block_inner ? pb.d_offsets.as<int64_t>() : nullptr;
                 ba.small_structures = block_inner && largest_structure <= kBlockSmallAtoms ? 1 : 0;
+                ba.summed = p.compression == 2 ? 1 : 0;
                 if (p.weighted != 0) {
                     ba.weighting = p.weighting;
                     ba.has_w0 = p.has_w0;

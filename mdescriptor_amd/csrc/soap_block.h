@@ -11,8 +11,9 @@ namespace mdx {
 // Stream kinds of the kernel: a row per centre; a row per structure (inner
 // average) from a centre-by-centre stream; the same from a species-major
 // stream over the structure's pairs (structures of at most 64 atoms); a row
-// per centre with weighted neighbours.
-constexpr int kBlockRows = 0, kBlockInner = 1, kBlockInnerSmall = 2, kBlockRowsWeighted = 3;
+// per centre with weighted neighbours; a row per centre of mu1nu1 features
+// (each channel against the species-summed channels).
+constexpr int kBlockRows = 0, kBlockInner = 1, kBlockInnerSmall = 2, kBlockRowsWeighted = 3, kBlockRowsSummed = 4;
 constexpr int kBlockSmallAtoms = 64;
 
 // Launch arguments (one struct, passed by value).
@@ -41,6 +42,7 @@ struct BlockArgs {
     double w_r0, w_c, w_d, w_m, w_w0;
     const double* species_w;             // null: no weights
     const int32_t* bin_atom;             // atom of each binned image
+    int summed;                          // mu1nu1: spectrum against the species-summed coefficients
     void* out;
     int64_t pitch;              // bytes between output rows
 };
@@ -57,7 +59,9 @@ struct BlockPlanHost {
 };
 
 // Fills out and returns true when (S, n, l_max) is one of the compiled shapes.
-bool block_plan_tables(int S, int n, int l_max, int out_dtype, const std::vector<double>& beta_scaled,
+// compression: 0 off, 2 mu1nu1, 3 crossover (the feature layouts of
+// soap.cpp:948-1013); mu2 is not taken.
+bool block_plan_tables(int S, int n, int l_max, int out_dtype, int compression, const std::vector<double>& beta_scaled,
                        const std::vector<double>& pref, const std::vector<double>& expo, BlockPlanHost& out);
 size_t block_lds_bytes(int l_max, int kg);
 void launch_block_expand(hipStream_t stream, int l_max, int kg, int ncr, const BlockArgs& a, int64_t count);

@@ -397,6 +397,7 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
     const int64_t work_last = min(work_first + a.per_block, a.item_base + a.items);
     constexpr bool inner = MODE == kBlockInner || MODE == kBlockInnerSmall; // rows of structure averages
     constexpr bool kWeighted = MODE == kBlockRowsWeighted; // neighbour weights scale the harmonic seeds
+    constexpr bool kSummed = MODE == kBlockRowsSummed;     // mu1nu1: against the species-summed coefficients
     // structures of at most a wavefront of atoms: pairs streamed species-major
     // across the structure's centres (an average sums them in any order)
     constexpr bool kSpeciesMajor = MODE == kBlockInnerSmall;
@@ -800,12 +801,67 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
             char* row = static_cast<char*>(a.out) + row0 * a.pitch;
             const __amdgpu_buffer_rsrc_t rsrc =
                 __builtin_amdgcn_make_buffer_rsrc(row, 0, static_cast<int>(F * ES), 0x00020000);
+            // one 4-value store per lane and value of a Gram tile
+            auto store_tile = [&](const d4& D, const int* fb, const int* fs, int l) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const double v = D[r]; // the coefficients carry sqrt(pi sqrt(8/(2l+1)))
+                    const int off = fb[r] + l * fs[r];
+                    if constexpr (ES == 4) {
+                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(static_cast<float>(v)), rsrc, off, 0, 0);
+                    } else {
+                        typedef int i2v __attribute__((ext_vector_type(2)));
+                        const i2v bits = {__double2loint(v), __double2hiint(v)};
+                        __builtin_amdgcn_raw_buffer_store_b64(bits, rsrc, off, 0, 0);
+                    }
+                }
+            };
+            if constexpr (kSummed) {
+                // species-summed coefficients: the registers added, then the
+                // species' blocks of a register (KG 2: b and b ^ 2; KG 1: all
+                // four; KG 3 holds one species)
+                double cs[NU];
+                unroll<NU>([&](auto uc) {
+                    constexpr int u = decltype(uc)::value;
+                    double v = C[u][0];
+                    unroll<NCR - 1>([&](auto rc) { v += C[u][decltype(rc)::value + 1]; });
+                    if constexpr (KG == 2) {
+                        v += row_rotate<8>(v);
+                    } else if constexpr (KG == 1) {
+                        v += row_rotate<8>(v);
+                        v += row_rotate<4>(v);
+                    }
+                    cs[u] = v;
+                });
+                unroll<NCR>([&](auto ic) {
+                    constexpr int ri = decltype(ic)::value;
+                    int fb[4], fs[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int o = s_ps[(ri * 4 + r) * kWaveThreads + lane];
+                        fb[r] = o >> kStrideBits; // bytes
+                        fs[r] = (o & ((1 << kStrideBits) - 1)) * ES;
+                    }
+                    unroll<L>([&](auto lc) {
+                        constexpr int l = decltype(lc)::value;
+                        if constexpr ((kOwn >> l) & 1u) {
+                            constexpr int u0 = units_before(kOwn, l);
+                            d4 D = {0.0, 0.0, 0.0, 0.0};
+                            unroll<cgroups(l)>([&](auto cc) {
+                                constexpr int cg = decltype(cc)::value;
+                                D = mfma(C[u0 + cg][ri], cs[u0 + cg], D);
+                            });
+                            store_tile(D, fb, fs, l);
+                        }
+                    });
+                });
+            }
             int pair = 0;
             unroll<NCR>([&](auto ic) {
                 constexpr int ri = decltype(ic)::value;
                 unroll<NCR>([&](auto jc) {
                     constexpr int rj = decltype(jc)::value;
-                    if constexpr (ri <= rj) {
+                    if constexpr (!kSummed && ri <= rj) {
                         int fb[4], fs[4];
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
@@ -822,19 +878,7 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
                                     constexpr int cg = decltype(cc)::value;
                                     D = mfma(C[u0 + cg][ri], C[u0 + cg][rj], D);
                                 });
-#pragma unroll
-                                for (int r = 0; r < 4; ++r) {
-                                    const double v = D[r]; // the coefficients carry sqrt(pi sqrt(8/(2l+1)))
-                                    const int off = fb[r] + l * fs[r];
-                                    if constexpr (ES == 4) {
-                                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(static_cast<float>(v)), rsrc,
-                                                                              off, 0, 0);
-                                    } else {
-                                        typedef int i2v __attribute__((ext_vector_type(2)));
-                                        const i2v bits = {__double2loint(v), __double2hiint(v)};
-                                        __builtin_amdgcn_raw_buffer_store_b64(bits, rsrc, off, 0, 0);
-                                    }
-                                }
+                                store_tile(D, fb, fs, l);
                             }
                         });
                         ++pair;
@@ -860,9 +904,10 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
 }
 
 // Five wavefronts per SIMD (96 VGPRs); four for the weighted rows, whose
-// distance function (pow) needs the registers of a fifth
+// distance function (pow) needs the registers of a fifth, and for mu1nu1,
+// whose summed coefficients stay live beside the registers
 template <int LM, int KG, int NCR, int ES, int MODE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == kBlockRowsWeighted ? 4 : 5))) void
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE >= kBlockRowsWeighted ? 4 : 5))) void
 k_soap_block(BlockArgs a) {
     using PL = BlockPlan<LM, KG>;
     // staging buffers, d2, exp table, padded S_lm table, power-spectrum
@@ -934,7 +979,9 @@ void launch_shape(hipStream_t stream, const BlockArgs& a, int64_t count) {
     const unsigned grid = static_cast<unsigned>((count + args.per_block - 1) / args.per_block);
     const dim3 threads(PL::T * kWaveThreads);
     const int mode = a.struct_offsets != nullptr ? (a.small_structures ? kBlockInnerSmall : kBlockInner)
-                     : a.species_w != nullptr ? kBlockRowsWeighted : kBlockRows;
+                     : a.species_w != nullptr ? kBlockRowsWeighted
+                     : a.summed != 0          ? kBlockRowsSummed
+                                              : kBlockRows;
     auto launch = [&](auto m) {
         constexpr int M = decltype(m)::value;
         if (a.out_dtype == 4) {
@@ -949,8 +996,10 @@ void launch_shape(hipStream_t stream, const BlockArgs& a, int64_t count) {
         launch(std::integral_constant<int, kBlockInner>{});
     } else if (mode == kBlockInnerSmall) {
         launch(std::integral_constant<int, kBlockInnerSmall>{});
-    } else {
+    } else if (mode == kBlockRowsWeighted) {
         launch(std::integral_constant<int, kBlockRowsWeighted>{});
+    } else {
+        launch(std::integral_constant<int, kBlockRowsSummed>{});
     }
 }
 
@@ -982,9 +1031,10 @@ int coefficient_registers(int S, int kg) { return kg == 3 ? S : (S * kg + 3) / 4
 
 } // namespace
 
-bool block_plan_tables(int S, int n, int l_max, int out_dtype, const std::vector<double>& beta_scaled,
+bool block_plan_tables(int S, int n, int l_max, int out_dtype, int compression, const std::vector<double>& beta_scaled,
                        const std::vector<double>& pref, const std::vector<double>& expo, BlockPlanHost& out) {
     out = BlockPlanHost{};
+    if (compression != 0 && compression != 2 && compression != 3) return false;
     const int kg = (n + 3) / 4;
     if (n < 1 || kg > 3 || (kg == 3 && S != 1)) return false;
     const int ncr = coefficient_registers(S, kg);
@@ -993,7 +1043,7 @@ bool block_plan_tables(int S, int n, int l_max, int out_dtype, const std::vector
     const int L = l_max + 1;
     {
         const int64_t W = static_cast<int64_t>(S) * n;
-        const int64_t F = W * (W + 1) / 2 * L;
+        const int64_t F = compression == 2 ? W * n * L : compression == 3 ? W * (n + 1) / 2 * L : W * (W + 1) / 2 * L;
         if (F * out_dtype >= kDroppedBytes || n * n >= (1 << kStrideBits)) return false;
     }
     const int R = kg == 2 ? 2 : 1;
@@ -1067,17 +1117,49 @@ bool block_plan_tables(int S, int n, int l_max, int out_dtype, const std::vector
         }
         return -1;
     };
-    for (int ri = 0; ri < ncr; ++ri) {
-        for (int rj = ri; rj < ncr; ++rj) {
+    if (compression == 2) {
+        // mu1nu1 (soap.cpp:969-981): channel i = (t, n1) of register ri
+        // against the species-summed channel n2, feature t L n^2 + l n^2 +
+        // n1 n + n2.  The summed register repeats its channels in every
+        // species' blocks; its first kg blocks are taken.
+        for (int ri = 0; ri < ncr; ++ri) {
             for (int r = 0; r < 4; ++r) {
                 for (int lane = 0; lane < 64; ++lane) {
                     const int i = channel(ri, r, lane / 16);
-                    const int j = channel(rj, (lane % 16) / 4, lane % 4);
+                    const int slot = (lane % 16) / 4;
+                    const int j = slot < kg ? 4 * slot + lane % 4 : n;
                     int fb = kDroppedBytes, fs = 0;
-                    if (i >= 0 && j >= 0 && i <= j) {
-                        fb = feature(i, j, fs) * out_dtype;
+                    if (i >= 0 && j < n) {
+                        const int t = i / n;
+                        fb = (t * L * n * n + (i - t * n) * n + j) * out_dtype;
+                        fs = n * n;
                     }
                     out.ps_offsets.push_back((fb << kStrideBits) | fs);
+                }
+            }
+        }
+    } else {
+        for (int ri = 0; ri < ncr; ++ri) {
+            for (int rj = ri; rj < ncr; ++rj) {
+                for (int r = 0; r < 4; ++r) {
+                    for (int lane = 0; lane < 64; ++lane) {
+                        const int i = channel(ri, r, lane / 16);
+                        const int j = channel(rj, (lane % 16) / 4, lane % 4);
+                        int fb = kDroppedBytes, fs = 0;
+                        if (i >= 0 && j >= 0 && i <= j) {
+                            if (compression == 3) {
+                                // crossover (soap.cpp:983-995): same species only
+                                const int t1 = i / n, t2 = j / n, n1 = i % n, n2 = j % n;
+                                if (t1 == t2) {
+                                    fs = n * (n + 1) / 2;
+                                    fb = (t1 * L * fs + n1 * n - n1 * (n1 - 1) / 2 + (n2 - n1)) * out_dtype;
+                                }
+                            } else {
+                                fb = feature(i, j, fs) * out_dtype;
+                            }
+                        }
+                        out.ps_offsets.push_back((fb << kStrideBits) | fs);
+                    }
                 }
             }
         }

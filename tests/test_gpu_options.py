@@ -62,14 +62,15 @@ def test_option_at_hcno_shape(hip_context, oracle, name):
     _run(hip_context, oracle, 2, name, "off", limit=8)
 
 
-WEIGHTS = ["poly", "pow_w0", "exp", "w0_only", "species_weights"]
+# the options the register-coefficient kernel takes with atom-level rows
+BLOCK_OPTIONS = ["poly", "pow_w0", "exp", "w0_only", "species_weights", "mu1nu1", "crossover"]
 
 
 @pytest.mark.parametrize("shape", [(1, 4, 3), (2, 8, 6), (3, 6, 4), (4, 8, 8), (5, 9, 9)])
-@pytest.mark.parametrize("name", WEIGHTS)
-def test_weights_on_register_coefficient_kernel(hip_context, oracle, monkeypatch, shape, name):
-    """Neighbour weights on the register-coefficient kernel (atom-level rows)
-    for each compiled shape: the configuration's species and structures at
+@pytest.mark.parametrize("name", BLOCK_OPTIONS)
+def test_options_on_register_coefficient_kernel(hip_context, oracle, monkeypatch, shape, name):
+    """Neighbour weights and the mu1nu1 and crossover compressions on the
+    register-coefficient kernel (atom-level rows) for each compiled shape: the configuration's species and structures at
     its (n_max, l_max), config 5 with nine channels (three radial groups).
     Twelve channels with pow or poly weights are too ill-conditioned for the
     gate (max |beta| 1e5 at 5.5 A): there any two summation orders differ by
