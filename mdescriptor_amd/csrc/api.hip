@@ -615,7 +615,9 @@ int mdx_hip_soap_plan_create(mdx_hip_ctx* ctx, const mdx_soap_params* params, md
             md.clamp = max_expo * plan->cutoff * plan->cutoff > 700.0 ? 1 : 0;
             plan->hpad = md.hpad;
             plan->clamp = md.clamp;
-            const bool fits = mdx::mfma_template_tiles(mp.tiles) > 0 && mdx::mfma_lds_bytes(md) <= 64 * 1024;
+            // the workgroup's LDS: 160 KiB on gfx950 (dynamic, no opt-in needed)
+            const size_t lds_limit = mdx::device_workgroup_lds();
+            const bool fits = mdx::mfma_template_tiles(mp.tiles) > 0 && mdx::mfma_lds_bytes(md) <= lds_limit;
             // only the matrix-core kernel implements weighting, compression and the polynomial basis
             const bool defaults = plan->compression == 0 && plan->radial_basis == 0 && plan->weighted == 0;
             plan->use_mfma = fits && (choice != "generic" || !defaults);
@@ -631,7 +633,7 @@ int mdx_hip_soap_plan_create(mdx_hip_ctx* ctx, const mdx_soap_params* params, md
                 const mdx::QuadPlanHost qp = mdx::plan_quad_tables(n, p.l_max, md.hpad, beta, pref, expo);
                 mdx::MfmaDims qd = md;
                 qd.crow = mdx::quad_coefficient_rows(plan->Sc, n);
-                if (qp.waves > 0 && mdx::quad_lds_bytes(qd) <= 64 * 1024) {
+                if (qp.waves > 0 && mdx::quad_lds_bytes(qd) <= lds_limit) {
                     plan->quad_waves = qp.waves;
                     plan->quad_kg = qp.kg;
                     plan->quad_instr = qp.instr;

@@ -90,6 +90,19 @@ int device_compute_units() {
     return cached[dev];
 }
 
+size_t device_workgroup_lds() {
+    static int cached[64] = {};
+    int dev = 0;
+    MDX_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) return 64 * 1024;
+    if (cached[dev] == 0) {
+        int bytes = 0;
+        MDX_HIP(hipDeviceGetAttribute(&bytes, hipDeviceAttributeMaxSharedMemoryPerBlock, dev));
+        cached[dev] = bytes > 0 ? bytes : 64 * 1024;
+    }
+    return static_cast<size_t>(cached[dev]);
+}
+
 PinnedWords::~PinnedWords() {
     if (words_ != nullptr) (void)hipHostFree(words_);
 }

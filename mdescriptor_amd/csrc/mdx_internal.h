@@ -243,6 +243,9 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
 
 // Compute units of the current device (queried once per process and device).
 int device_compute_units();
+// LDS bytes one workgroup may use on the current device (queried once per
+// process and device; 160 KiB on gfx950)
+size_t device_workgroup_lds();
 
 // Exclusive scan of n int32 counts into n+1 int64 offsets (out[n] = total).
 void scan_counts(hipStream_t stream, const int32_t* in, int64_t* out, int64_t n, DeviceBuffer& tmp);
