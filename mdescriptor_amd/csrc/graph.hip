@@ -241,18 +241,6 @@ __host__ __device__ inline int grid_coordinate(double value, double origin, doub
 
 // ---------------------------------------------------------------- device side
 
-__device__ inline int64_t find_by_begin(const StructGeom* geom, int64_t n, int64_t value, int which) {
-    // last structure whose begin (ext/cell/atom by `which`) is <= value
-    int64_t lo = 0, hi = n;
-    while (hi - lo > 1) {
-        const int64_t mid = (lo + hi) / 2;
-        const int64_t b = which == 0 ? geom[mid].ext_begin : which == 1 ? geom[mid].cell_begin : geom[mid].atom_begin;
-        if (b <= value) lo = mid; else hi = mid;
-    }
-    // skip empty structures that share the same begin
-    return lo;
-}
-
 __device__ inline int64_t roi_cell(const StructGeom& g, double x, double y, double z, bool& inside) {
     const int cx = grid_coordinate(x, g.minimum[0], g.spacing[0], g.dims[0]);
     const int cy = grid_coordinate(y, g.minimum[1], g.spacing[1], g.dims[1]);
@@ -284,12 +272,12 @@ constexpr int kBinChunk = 4096;    // images per LDS binning workgroup
 // fill pass: keys at cell_start[c] + a slot taken from cell_count.
 template <bool kFill>
 __global__ void k_bin_atoms(const StructGeom* geom, const ImageDesc* images, const double* positions,
-                            const int32_t* centre_struct, const int32_t* types, int species_major, int64_t atoms,
+                            const int32_t* atom_struct, const int32_t* types, int species_major, int64_t atoms,
                             int max_images, int32_t* cell_count, const int64_t* cell_start, uint64_t* keys) {
     for (int q = blockIdx.y; q < max_images; q += gridDim.y) {
         for (int64_t a = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; a < atoms;
              a += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-            const StructGeom& g = geom[centre_struct[a]];
+            const StructGeom& g = geom[atom_struct[a]];
             if (q >= g.n_images || g.lds_bins != 0) continue;
             const uint32_t j = static_cast<uint32_t>(a - g.atom_begin);
             const uint32_t ext = static_cast<uint32_t>(q) * static_cast<uint32_t>(g.natoms) + j;
@@ -389,7 +377,9 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_lds(const BinChunk* chunks,
 __global__ void k_bin_sort(const StructGeom* geom, const int32_t* cell_struct, const ImageDesc* images,
                            const double* positions, const int32_t* types, const int64_t* cell_start,
                            int64_t cells_total, const uint64_t* keys, double* bx, double* by, double* bz,
-                           int32_t* batom, int32_t* bimage, int32_t* btype) {
+                           int32_t* batom, int32_t* bimage, int32_t* btype, unsigned long long* stats) {
+    // the binned image total, read back with the search statistics
+    if (blockIdx.x == 0 && threadIdx.x == 0) stats[kStatBinned] = static_cast<unsigned long long>(cell_start[cells_total]);
     for (int64_t c = blockIdx.x; c < cells_total; c += gridDim.x) {
         const int64_t start = cell_start[c];
         const int64_t n = cell_start[c + 1] - start;
@@ -414,48 +404,6 @@ __global__ void k_bin_sort(const StructGeom* geom, const int32_t* cell_struct, c
     }
 }
 
-// Home ROI cell and structure of every atom (the centres).
-__global__ void k_centre_cell(const StructGeom* geom, const int32_t* atom_struct, const double* positions,
-                              int64_t atoms, int64_t* centre_cell, int32_t* centre_struct, int32_t* cell_ncentre,
-                              int32_t* centre_slot, int32_t* error_flag) {
-    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < atoms;
-         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        const int32_t s = atom_struct[i];
-        const StructGeom& g = geom[s];
-        centre_struct[i] = static_cast<int32_t>(s);
-        if (g.one_cell != 0) {
-            // every atom of the structure is a centre of its one cell
-            const int32_t j = static_cast<int32_t>(i - g.atom_begin);
-            centre_cell[i] = g.cell_begin;
-            centre_slot[i] = j;
-            if (j == 0) cell_ncentre[g.cell_begin] = g.natoms;
-            continue;
-        }
-        bool inside;
-        const int64_t c = roi_cell(g, positions[i * 3 + 0], positions[i * 3 + 1], positions[i * 3 + 2], inside);
-        if (!inside) {
-            // the host placed every centre inside the ROI with the same arithmetic
-            atomicOr(error_flag, 1);
-            centre_cell[i] = -1;
-            continue;
-        }
-        centre_cell[i] = c;
-        centre_slot[i] = atomicAdd(&cell_ncentre[c], 1);
-    }
-}
-
-// Structure of every ROI cell: the last structure whose first cell is at or
-// before it (structures own consecutive cell ranges).  One thread per cell,
-// so the searches of all cells overlap their memory latency.
-__global__ void k_cell_struct(const StructGeom* geom, int64_t nstruct, int64_t cells_total, int32_t* cell_struct) {
-    for (int64_t c = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; c < cells_total;
-         c += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        int64_t s = find_by_begin(geom, nstruct, c, 1);
-        while (s + 1 < nstruct && geom[s + 1].cell_begin <= c) ++s;
-        cell_struct[c] = static_cast<int32_t>(s);
-    }
-}
-
 // First bin of each species in each cell (Bins mode: cells are sorted by
 // species); species t of cell c spans [start[c*S + t], start[c*S + t + 1])
 // with the cell's end after the last species.  One thread per (cell, t):
@@ -473,20 +421,6 @@ __global__ void k_cell_species(const int64_t* cell_start, int64_t cells_total, c
             if (btype[mid] < t) lo = mid + 1; else hi = mid;
         }
         cell_species_start[w] = lo;
-    }
-}
-
-// Centres of each ROI cell in one list: centre_slot (from k_centre_cell) is
-// the centre's place among its cell's centres.
-__global__ void k_centre_fill(const int64_t* centre_cell, const int32_t* centre_slot, int64_t atoms,
-                              const int64_t* cell_centre_start, int32_t* cell_centres, const int64_t* cell_start,
-                              int64_t cells, unsigned long long* stats) {
-    // the binned image total, read back with the search statistics
-    if (blockIdx.x == 0 && threadIdx.x == 0) stats[kStatBinned] = static_cast<unsigned long long>(cell_start[cells]);
-    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < atoms;
-         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        const int64_t c = centre_cell[i];
-        if (c >= 0) cell_centres[cell_centre_start[c] + centre_slot[i]] = static_cast<int32_t>(i);
     }
 }
 
@@ -1009,6 +943,7 @@ void prepare_batch(const mdx_batch_view& batch, const int32_t* species, int n_sp
     std::vector<int32_t> occupied;
     std::vector<int64_t> homes;
     std::vector<int64_t> occupied_begin(static_cast<size_t>(batch.structures) + 1, 0);
+    std::vector<int64_t> atom_home(static_cast<size_t>(batch.atoms), 0);
     for (int64_t s = 0; s < batch.structures; ++s) {
         StructGeom& g = out.geom[static_cast<size_t>(s)];
         occupied_begin[static_cast<size_t>(s)] = static_cast<int64_t>(occupied.size());
@@ -1120,6 +1055,7 @@ void prepare_batch(const mdx_batch_view& batch, const int32_t* species, int n_sp
                 local = local * g.roi_dim[a] + (c - g.roi_lo[a]);
             }
             homes.push_back(cells + local);
+            atom_home[static_cast<size_t>(i)] = cells + local;
         }
         std::sort(homes.begin(), homes.end());
         homes.erase(std::unique(homes.begin(), homes.end()), homes.end());
@@ -1130,6 +1066,27 @@ void prepare_batch(const mdx_batch_view& batch, const int32_t* species, int n_sp
         }
     }
     occupied_begin[static_cast<size_t>(batch.structures)] = static_cast<int64_t>(occupied.size());
+    // centres by home cell (a counting sort, atom order inside a cell) and the
+    // structure of every cell
+    out.cell_centre_start.assign(static_cast<size_t>(cells) + 1, 0);
+    for (int64_t i = 0; i < batch.atoms; ++i) ++out.cell_centre_start[static_cast<size_t>(atom_home[static_cast<size_t>(i)]) + 1];
+    for (int64_t c = 0; c < cells; ++c) {
+        out.cell_centre_start[static_cast<size_t>(c) + 1] += out.cell_centre_start[static_cast<size_t>(c)];
+    }
+    out.cell_centres.assign(static_cast<size_t>(batch.atoms), 0);
+    {
+        std::vector<int64_t> next(out.cell_centre_start.begin(), out.cell_centre_start.end() - 1);
+        for (int64_t i = 0; i < batch.atoms; ++i) {
+            out.cell_centres[static_cast<size_t>(next[static_cast<size_t>(atom_home[static_cast<size_t>(i)])]++)] =
+                static_cast<int32_t>(i);
+        }
+    }
+    out.cell_struct.assign(static_cast<size_t>(cells), 0);
+    for (int64_t s = 0; s < batch.structures; ++s) {
+        const int64_t first = out.geom[static_cast<size_t>(s)].cell_begin;
+        const int64_t end = s + 1 < batch.structures ? out.geom[static_cast<size_t>(s) + 1].cell_begin : cells;
+        std::fill(out.cell_struct.begin() + first, out.cell_struct.begin() + end, static_cast<int32_t>(s));
+    }
     if (ext >= (int64_t(1) << 32) - 1) {
         throw Error(MDX_INVALID_ARGUMENT, "periodic images exceed the device graph capacity");
     }
@@ -1187,6 +1144,21 @@ void upload_batch(hipStream_t stream, const mdx_batch_view& batch, PreparedBatch
     pb.d_offsets.reserve(pb.offsets.size() * sizeof(int64_t));
     pb.d_cell_lists.reserve(std::max<size_t>(1, pb.cell_lists.size() * sizeof(int32_t)));
     pb.d_bin_chunks.reserve(std::max<size_t>(1, pb.bin_chunks.size() * sizeof(BinChunk)));
+    pb.d_cell_centre_start.reserve(std::max<size_t>(1, pb.cell_centre_start.size() * sizeof(int64_t)));
+    pb.d_cell_centres.reserve(std::max<size_t>(1, pb.cell_centres.size() * sizeof(int32_t)));
+    pb.d_cell_struct.reserve(std::max<size_t>(1, pb.cell_struct.size() * sizeof(int32_t)));
+    if (!pb.cell_centre_start.empty()) {
+        MDX_HIP(hipMemcpyAsync(pb.d_cell_centre_start.ptr, pb.cell_centre_start.data(),
+                               pb.cell_centre_start.size() * sizeof(int64_t), hipMemcpyHostToDevice, stream));
+    }
+    if (!pb.cell_centres.empty()) {
+        MDX_HIP(hipMemcpyAsync(pb.d_cell_centres.ptr, pb.cell_centres.data(), pb.cell_centres.size() * sizeof(int32_t),
+                               hipMemcpyHostToDevice, stream));
+    }
+    if (!pb.cell_struct.empty()) {
+        MDX_HIP(hipMemcpyAsync(pb.d_cell_struct.ptr, pb.cell_struct.data(), pb.cell_struct.size() * sizeof(int32_t),
+                               hipMemcpyHostToDevice, stream));
+    }
     if (!pb.bin_chunks.empty()) {
         MDX_HIP(hipMemcpyAsync(pb.d_bin_chunks.ptr, pb.bin_chunks.data(), pb.bin_chunks.size() * sizeof(BinChunk),
                                hipMemcpyHostToDevice, stream));
@@ -1243,7 +1215,6 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     gr.n_species = S;
     const int64_t atoms = pb.atoms;
     const int64_t cells = pb.cells_total;
-    const int64_t nstruct = pb.structures;
     const size_t cells1 = static_cast<size_t>(cells + 1);
     gr.pair_start.reserve(static_cast<size_t>(atoms + 1) * sizeof(int64_t));
     gr.slots = 0;
@@ -1263,24 +1234,16 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
         throw Error(MDX_INVALID_ARGUMENT, "periodic images exceed the device graph capacity");
     }
 
-    // one zero-filled block: search statistics (error flag among them), then
-    // the cell counters of binning (count, fill) and of the centres
-    const size_t counter_bytes = kStatWords * sizeof(unsigned long long) + 3 * cells1 * sizeof(int32_t);
+    // one zero-filled block: search statistics, then the cell counters of
+    // binning (count, fill)
+    const size_t counter_bytes = kStatWords * sizeof(unsigned long long) + 2 * cells1 * sizeof(int32_t);
     gr.counters.reserve(counter_bytes);
     unsigned long long* stats = gr.counters.as<unsigned long long>();
-    int32_t* error_flag = reinterpret_cast<int32_t*>(stats + kStatError);
     int32_t* cell_count = reinterpret_cast<int32_t*>(stats + kStatWords);
     int32_t* cell_fill = cell_count + cells1;
-    int32_t* cell_ncentre = cell_fill + cells1;
     gr.cell_start.reserve(cells1 * sizeof(int64_t));
     gr.cell_species_start.reserve(std::max<size_t>(1, static_cast<size_t>(cells) * static_cast<size_t>(S)) *
                                   sizeof(int64_t));
-    gr.centre_cell.reserve(static_cast<size_t>(atoms) * sizeof(int64_t));
-    gr.centre_struct.reserve(static_cast<size_t>(atoms) * sizeof(int32_t));
-    gr.centre_slot.reserve(static_cast<size_t>(atoms) * sizeof(int32_t));
-    gr.cell_centres.reserve(static_cast<size_t>(atoms) * sizeof(int32_t));
-    gr.cell_centre_start.reserve(cells1 * sizeof(int64_t));
-    gr.cell_struct.reserve(static_cast<size_t>(cells) * sizeof(int32_t));
     gr.bin_key.reserve(static_cast<size_t>(ext) * sizeof(uint64_t));
     gr.bin_x.reserve(static_cast<size_t>(ext) * sizeof(double));
     gr.bin_y.reserve(static_cast<size_t>(ext) * sizeof(double));
@@ -1292,13 +1255,8 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     gr.totals.reserve(static_cast<size_t>(atoms) * sizeof(int32_t));
     MDX_HIP(hipMemsetAsync(gr.counters.ptr, 0, counter_bytes, stream));
 
-    // home cell and structure of every atom (the centres)
-    hipLaunchKernelGGL(k_centre_cell, dim3(grid_for(atoms)), dim3(kBlock), 0, stream, geom,
-                       pb.d_atom_struct.as<int32_t>(), pos, atoms, gr.centre_cell.as<int64_t>(),
-                       gr.centre_struct.as<int32_t>(), cell_ncentre, gr.centre_slot.as<int32_t>(), error_flag);
-    hipLaunchKernelGGL(k_cell_struct, dim3(grid_for(cells)), dim3(kBlock), 0, stream, geom, nstruct, cells,
-                       gr.cell_struct.as<int32_t>());
-    // bin every periodic image into its ROI cell, sorted by (species, extended index)
+    // the centres' home cells and the cells' structures come with the batch
+    // (prepare_batch); bin every periodic image into its ROI cell, sorted by (species, extended index)
     int max_images = 1;
     for (const StructGeom& sg : pb.geom) max_images = std::max(max_images, static_cast<int>(sg.n_images));
     const dim3 bin_grid(static_cast<unsigned>(std::min<int64_t>((atoms + kBlock - 1) / kBlock, 1 << 16)),
@@ -1308,7 +1266,7 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     const int species_major = S > 1 ? 1 : 0;
     if (pb.direct_bins) {
         hipLaunchKernelGGL(k_bin_atoms<false>, bin_grid, dim3(kBlock), 0, stream, geom, images, pos,
-                           gr.centre_struct.as<int32_t>(), pb.d_types.as<int32_t>(), 0, atoms, max_images, cell_count,
+                           pb.d_atom_struct.as<int32_t>(), pb.d_types.as<int32_t>(), 0, atoms, max_images, cell_count,
                            static_cast<const int64_t*>(nullptr), static_cast<uint64_t*>(nullptr));
     }
     if (chunk_grid > 0) {
@@ -1319,7 +1277,7 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     scan_counts(stream, cell_count, gr.cell_start.as<int64_t>(), cells, gr.scan_tmp);
     if (pb.direct_bins) {
         hipLaunchKernelGGL(k_bin_atoms<true>, bin_grid, dim3(kBlock), 0, stream, geom, images, pos,
-                           gr.centre_struct.as<int32_t>(), pb.d_types.as<int32_t>(), species_major, atoms, max_images,
+                           pb.d_atom_struct.as<int32_t>(), pb.d_types.as<int32_t>(), species_major, atoms, max_images,
                            cell_fill, gr.cell_start.as<int64_t>(), gr.bin_key.as<uint64_t>());
     }
     if (chunk_grid > 0) {
@@ -1330,21 +1288,16 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     const unsigned cell_grid = static_cast<unsigned>(std::min<int64_t>(cells, 1 << 20));
     // a wavefront per cell when cells hold a wavefront of images on average
     const int sort_threads = ext <= static_cast<int64_t>(kWave) * cells ? kWave : kBlock;
-    hipLaunchKernelGGL(k_bin_sort, dim3(cell_grid), dim3(sort_threads), 0, stream, geom, gr.cell_struct.as<int32_t>(),
-                       images, pos,
-                       pb.d_types.as<int32_t>(), gr.cell_start.as<int64_t>(), cells, gr.bin_key.as<uint64_t>(),
-                       gr.bin_x.as<double>(), gr.bin_y.as<double>(), gr.bin_z.as<double>(), gr.bin_atom.as<int32_t>(),
-                       gr.bin_image.as<int32_t>(), gr.bin_type.as<int32_t>());
+    hipLaunchKernelGGL(k_bin_sort, dim3(cell_grid), dim3(sort_threads), 0, stream, geom,
+                       pb.d_cell_struct.as<int32_t>(), images, pos, pb.d_types.as<int32_t>(), gr.cell_start.as<int64_t>(),
+                       cells, gr.bin_key.as<uint64_t>(), gr.bin_x.as<double>(), gr.bin_y.as<double>(),
+                       gr.bin_z.as<double>(), gr.bin_atom.as<int32_t>(), gr.bin_image.as<int32_t>(),
+                       gr.bin_type.as<int32_t>(), stats);
     if (S > 1) {
         hipLaunchKernelGGL(k_cell_species, dim3(grid_for(cells * S)), dim3(kBlock), 0, stream,
                            gr.cell_start.as<int64_t>(), cells, gr.bin_type.as<int32_t>(), S,
                            gr.cell_species_start.as<int64_t>());
     }
-    // centres grouped by home cell
-    scan_counts(stream, cell_ncentre, gr.cell_centre_start.as<int64_t>(), cells, gr.scan_tmp);
-    hipLaunchKernelGGL(k_centre_fill, dim3(grid_for(atoms)), dim3(kBlock), 0, stream, gr.centre_cell.as<int64_t>(),
-                       gr.centre_slot.as<int32_t>(), atoms, gr.cell_centre_start.as<int64_t>(),
-                       gr.cell_centres.as<int32_t>(), gr.cell_start.as<int64_t>(), cells, stats);
     MDX_HIP(hipGetLastError());
     if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
 
@@ -1361,8 +1314,8 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
         if (big_cells > 0) {
             const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(big_cells, 1 << 20));
             hipLaunchKernelGGL(k_neighbors<decltype(mode)::value>, dim3(blocks), dim3(kNbrThreads), 0, stream, geom,
-                               gr.cell_struct.as<int32_t>(), pos, big_list, big_cells,
-                               gr.cell_centre_start.as<int64_t>(), gr.cell_centres.as<int32_t>(),
+                               pb.d_cell_struct.as<int32_t>(), pos, big_list, big_cells,
+                               pb.d_cell_centre_start.as<int64_t>(), pb.d_cell_centres.as<int32_t>(),
                                gr.cell_start.as<int64_t>(), gr.cell_species_start.as<int64_t>(),
                                gr.bin_x.as<double>(), gr.bin_y.as<double>(), gr.bin_z.as<double>(), S, accept_max,
                                gr.counts.as<int32_t>(), gr.totals.as<int32_t>(), gr.pair_start.as<int64_t>(),
@@ -1373,7 +1326,7 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
             const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((wave_cells + per_block - 1) / per_block,
                                                                             1 << 20));
             hipLaunchKernelGGL(k_neighbors_wave<decltype(mode)::value>, dim3(blocks), dim3(kBlock), 0, stream, lists,
-                               wave_cells, pos, gr.cell_centre_start.as<int64_t>(), gr.cell_centres.as<int32_t>(),
+                               wave_cells, pos, pb.d_cell_centre_start.as<int64_t>(), pb.d_cell_centres.as<int32_t>(),
                                gr.cell_start.as<int64_t>(), gr.cell_species_start.as<int64_t>(),
                                gr.bin_x.as<double>(), gr.bin_y.as<double>(), gr.bin_z.as<double>(), S, accept_max,
                                gr.counts.as<int32_t>(), gr.totals.as<int32_t>(), gr.pair_start.as<int64_t>(),
@@ -1408,7 +1361,6 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
         // the expansion launch waits on these words: poll rather than sleep in
         // a blocking synchronisation, whose wake-up costs tens of microseconds
         gr.read_back.wait(stream);
-        if (st[kStatError] != 0) throw Error(MDX_INTERNAL, "a centre fell outside its structure's cell grid");
         if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
         int64_t pairs = 0, most = 0;
         reduce_stats(st, atoms, pairs, most);
@@ -1454,7 +1406,6 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     MDX_HIP(hipStreamSynchronize(stream));
     const int64_t binned = static_cast<int64_t>(st[kStatBinned]);
     int64_t counted = 0;
-    if (st[kStatError] != 0) throw Error(MDX_INTERNAL, "a centre fell outside its structure's cell grid");
     reduce_stats(st, atoms, counted, gr.most_rows);
     if (slotted && gr.slot_cap == 0 && gr.most_rows <= kMaxSlotCap) {
         // the slotted layout again once a batch's centres fit a slot

@@ -129,6 +129,13 @@ struct PreparedBatch {
     // binning work of the structures binned in LDS; whether any other
     // structure has images (those are binned with global atomics)
     std::vector<BinChunk> bin_chunks;
+    // centres grouped by home ROI cell (atom order inside a cell): cell c's
+    // centres are cell_centres[cell_centre_start[c], cell_centre_start[c+1]);
+    // the structure of every ROI cell.  Built on the host with the device's
+    // cell arithmetic.
+    std::vector<int64_t> cell_centre_start;
+    std::vector<int32_t> cell_centres, cell_struct;
+    DeviceBuffer d_cell_centre_start, d_cell_centres, d_cell_struct;
     bool direct_bins = false;
     DeviceBuffer d_bin_chunks; // BinChunk[bin_chunks.size()]
     DeviceBuffer d_cell_lists; // i32[cell_lists.size()]
@@ -180,20 +187,14 @@ struct DeviceGraph {
     int64_t most_rows = 0;   // largest row count of one centre
     int n_species = 1;
     DeviceBuffer counters;   // zero-filled per build: u64 statistics[kStatWords], then i32 cell
-                             // counts of binning (count, fill) and of the centres, [cells + 1] each
+                             // counts of binning (count, fill), [cells + 1] each
     DeviceBuffer cell_start; // i64[cells + 1] first bin of each ROI cell
     DeviceBuffer bin_key;                           // unsorted u64 keys, (species << 32) | extended index
     DeviceBuffer cell_species_start;                // i64[cells * n_species]: first bin of each species in a cell
-    DeviceBuffer centre_struct;                     // i32 structure of each atom
     DeviceBuffer bin_x, bin_y, bin_z;               // f64 positions of binned images (sorted)
     DeviceBuffer bin_atom;                          // i32 global atom index
     DeviceBuffer bin_image;                         // i32 global image index
     DeviceBuffer bin_type;                          // i32 species index
-    DeviceBuffer centre_cell;                       // i64 home ROI cell per atom
-    DeviceBuffer centre_slot;                       // i32 place of the atom among its cell's centres
-    DeviceBuffer cell_centre_start;                 // i64[cells + 1] first entry of a cell in cell_centres
-    DeviceBuffer cell_centres;                      // i32[atoms] centres grouped by home cell
-    DeviceBuffer cell_struct;                       // i32[cells] structure of each ROI cell
     DeviceBuffer counts;     // i32[atoms * n_species]
     DeviceBuffer totals;     // i32[atoms]
     DeviceBuffer pair_start; // i64[atoms + 1]: first row of each centre (compact: the
@@ -206,10 +207,8 @@ struct DeviceGraph {
     DeviceBuffer scan_tmp;   // block sums of the scans
 
     template <typename F> void for_each_buffer(F f) {
-        for (DeviceBuffer* b : {&counters, &cell_start, &bin_key, &cell_species_start, &centre_struct, &bin_x,
-                                &bin_y, &bin_z, &bin_atom, &bin_image, &bin_type, &centre_cell, &centre_slot,
-                                &cell_centre_start, &cell_centres, &cell_struct, &counts, &totals, &pair_start,
-                                &pair_bin,
+        for (DeviceBuffer* b : {&counters, &cell_start, &bin_key, &cell_species_start, &bin_x, &bin_y, &bin_z,
+                                &bin_atom, &bin_image, &bin_type, &counts, &totals, &pair_start, &pair_bin,
                                 &scan_tmp}) {
             f(*b);
         }
@@ -222,13 +221,12 @@ struct DeviceGraph {
 // count and a fill pass) when every centre fits; graph.slots records the
 // layout built.  Only consumers that read rows through pair_start[centre] and
 // the per-species counts may ask for it (the SOAP expansion).
-// graph statistics words, read back once per build: binned images and an
-// error flag (set by a kernel on an internal inconsistency) in the first
-// 128-byte line, then kStatLanes lines of (rows of the search pass, largest
+// graph statistics words, read back once per build: binned images in the
+// first 128-byte line, then kStatLanes lines of (rows of the search pass, largest
 // row count of a centre, centres searched).  The search kernels spread their
 // atomics over those lines: atomics on one address serialise across the
 // whole device.
-constexpr int kStatBinned = 0, kStatError = 1;
+constexpr int kStatBinned = 0;
 constexpr int kStatLineWords = 16;
 constexpr int kStatLanes = 32;
 constexpr int kStatWords = kStatLineWords * (1 + kStatLanes);

@@ -270,7 +270,7 @@ void fill_neighbor_list(hipStream_t stream, const PreparedBatch& pb, const Devic
     hipLaunchKernelGGL(k_list_fill, dim3(list_grid(pb.atoms)), dim3(kListThreads), 0, stream,
                        list_graph(pb, graph, list.full, list.self_pairs), list.kept_start.as<int64_t>(),
                        pb.d_positions.as<double>(), graph.bin_x.as<double>(), graph.bin_y.as<double>(),
-                       graph.bin_z.as<double>(), graph.centre_struct.as<int32_t>(), pb.d_offsets.as<int64_t>(), out);
+                       graph.bin_z.as<double>(), pb.d_atom_struct.as<int32_t>(), pb.d_offsets.as<int64_t>(), out);
     MDX_HIP(hipGetLastError());
 }
 
