@@ -946,7 +946,10 @@ int mdx_hip_neighbor_list(mdx_hip_ctx* ctx, const mdx_batch_view* batch, double 
         mdx::upload_batch(ctx->stream, *batch, pb);
         ctx->list_filled = false;
         MDX_HIP(hipEventRecord(ctx->list_events[0], ctx->stream));
-        mdx::build_graph(ctx->stream, pb, ctx->graph, cancel_flag);
+        // one search pass into per-centre slots (the compact two-pass layout
+        // when a centre overflows its slot); the list kernels read each
+        // centre's rows in the reference's order either way
+        mdx::build_graph(ctx->stream, pb, ctx->graph, cancel_flag, true);
         MDX_HIP(hipEventRecord(ctx->list_events[1], ctx->stream));
         check_cancel(cancel_flag);
         const int64_t rows = mdx::count_neighbor_list(ctx->stream, pb, ctx->graph, full_neighbor_list != 0 ? 1 : 0,

@@ -219,8 +219,9 @@ struct DeviceGraph {
 // Returns the pair count.  Polls cancel between launches.  slotted: the rows
 // may be laid out at centre * graph.slot_cap (one search pass instead of a
 // count and a fill pass) when every centre fits; graph.slots records the
-// layout built.  Only consumers that read rows through pair_start[centre] and
-// the per-species counts may ask for it (the SOAP expansion).
+// layout built.  Only consumers that read a centre's rows as pair_start[centre]
+// onwards, totals[centre] of them (or the per-species counts), may ask for it:
+// the SOAP expansion and the NeighborList kernels.
 // graph statistics words, read back once per build: binned images in the
 // first 128-byte line, then kStatLanes lines of (rows of the search pass, largest
 // row count of a centre, centres searched).  The search kernels spread their

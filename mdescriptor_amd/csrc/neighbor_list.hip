@@ -58,7 +58,8 @@ __device__ inline bool keep_record(int64_t centre, int64_t atom, int32_t sa, int
 }
 
 struct ListGraph {
-    const int64_t* pair_start; // i64[atoms + 1]
+    const int64_t* pair_start; // i64[atoms]: first row of each centre (compact or slotted layout)
+    const int32_t* totals;     // i32[atoms]: rows of each centre
     const uint32_t* pair_bin;  // u32[pairs]
     const int32_t* bin_atom;
     const int32_t* bin_image;
@@ -92,7 +93,7 @@ __global__ __launch_bounds__(kListThreads) void k_list_count(ListGraph g, int32_
     const int lane = threadIdx.x;
     for (int64_t c0 = blockIdx.x; c0 < g.atoms; c0 += gridDim.x) {
         const int64_t c = wave_centre(c0);
-        const int64_t begin = g.pair_start[c], end = g.pair_start[c + 1];
+        const int64_t begin = g.pair_start[c], end = begin + g.totals[c];
         int count = 0;
         for (int64_t base = begin; base < end; base += kListThreads) {
             uint32_t bin;
@@ -130,7 +131,7 @@ __global__ __launch_bounds__(kListThreads) void k_list_fill(ListGraph g, const i
     const uint64_t below = (uint64_t(1) << lane) - 1;
     for (int64_t c0 = blockIdx.x; c0 < g.atoms; c0 += gridDim.x) {
         const int64_t c = wave_centre(c0);
-        const int64_t begin = g.pair_start[c], end = g.pair_start[c + 1];
+        const int64_t begin = g.pair_start[c], end = begin + g.totals[c];
         if (begin == end) continue;
         int64_t row0 = kept_start[c];
         const double cx = positions[c * 3 + 0], cy = positions[c * 3 + 1], cz = positions[c * 3 + 2];
@@ -214,6 +215,7 @@ __global__ void k_list_offsets(const int64_t* kept_start, const int64_t* atom_of
 ListGraph list_graph(const PreparedBatch& pb, const DeviceGraph& g, int full, int self_pairs) {
     ListGraph lg;
     lg.pair_start = g.pair_start.as<int64_t>();
+    lg.totals = g.totals.as<int32_t>();
     lg.pair_bin = g.pair_bin.as<uint32_t>();
     lg.bin_atom = g.bin_atom.as<int32_t>();
     lg.bin_image = g.bin_image.as<int32_t>();
