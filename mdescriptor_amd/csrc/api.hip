@@ -238,10 +238,22 @@ void run_pipeline(mdx_hip_ctx* ctx, const mdx_soap_plan& plan, mdx::PreparedBatc
                   mdx_timing* timing, int64_t slice = 0, const mdx::SliceHook* on_slice = nullptr) {
     hipStream_t s = ctx->stream;
     MDX_HIP(hipEventRecord(ctx->events[0], s));
-    const int64_t pairs = mdx::build_graph(s, pb, graph, cancel, true);
+    // the expansion is queued behind the slotted search without waiting for
+    // its statistics (no host round trip between them); they are checked
+    // after, and a batch whose centre overflowed its slot runs again on the
+    // compact layout
+    mdx::build_graph(s, pb, graph, cancel, true, true);
     MDX_HIP(hipEventRecord(ctx->events[1], s));
     check_cancel(cancel);
     mdx::run_soap(s, plan, pb, graph, out_device, pitch, partials, cancel, ctx->events, timing, slice, on_slice);
+    if (!mdx::complete_graph(pb, graph, cancel)) {
+        MDX_HIP(hipStreamSynchronize(s)); // the first expansion's buffers are replaced
+        mdx::build_graph(s, pb, graph, cancel, true);
+        MDX_HIP(hipEventRecord(ctx->events[1], s));
+        check_cancel(cancel);
+        mdx::run_soap(s, plan, pb, graph, out_device, pitch, partials, cancel, ctx->events, timing, slice, on_slice);
+    }
+    const int64_t pairs = graph.pairs;
     const int64_t rows = plan.average != 0 ? pb.structures : pb.atoms;
     if (rows == 0 || plan.features == 0) {
         MDX_HIP(hipEventRecord(ctx->events[2], s));

@@ -129,8 +129,16 @@ void StreamPoint::prepare() {
 }
 
 void StreamPoint::wait(hipStream_t stream) {
+    record(stream);
+    sync();
+}
+
+void StreamPoint::record(hipStream_t stream) {
     prepare();
     MDX_HIP(hipEventRecord(event_, stream));
+}
+
+void StreamPoint::sync() {
     // Poll first: the short waits (the graph statistics) would otherwise pay
     // a blocking synchronisation's wake-up of tens of microseconds.  Past
     // 200 us of polling yield the core between polls, past 2 ms block.
@@ -681,8 +689,16 @@ __global__ __launch_bounds__(kNbrThreads) void k_neighbors(
                     const int ci = i / S, t = i - ci * S;
                     // rows before boundaries t and t + 1 (boundary 0 is the start; a
                     // boundary at or past the end of the walk is the centre's total)
-                    const int32_t lo = t == 0 ? 0 : s_segpre[t * 27] >= total ? s_found[ci] : s_bfound[i];
-                    const int32_t hi = t + 1 == S || s_segpre[(t + 1) * 27] >= total ? s_found[ci] : s_bfound[i + 1];
+                    int32_t lo = t == 0 ? 0 : s_segpre[t * 27] >= total ? s_found[ci] : s_bfound[i];
+                    int32_t hi = t + 1 == S || s_segpre[(t + 1) * 27] >= total ? s_found[ci] : s_bfound[i + 1];
+                    if (kMode == kNbrSlotted) {
+                        // an overflowing centre's counts cover only the rows its
+                        // slot holds, so a consumer launched before the host sees
+                        // the overflow reads no row past the slot (the totals and
+                        // the statistics keep the true counts)
+                        lo = static_cast<int32_t>(min<int64_t>(lo, cap));
+                        hi = static_cast<int32_t>(min<int64_t>(hi, cap));
+                    }
                     counts[static_cast<int64_t>(s_centre[ci]) * S + t] = hi - lo;
                 }
             }
@@ -1210,7 +1226,8 @@ void reduce_stats(const unsigned long long* st, int64_t atoms, int64_t& rows, in
 } // namespace
 
 int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr, const volatile int32_t* cancel,
-                    bool slotted) {
+                    bool slotted, bool defer_stats) {
+    gr.stats_pending = false;
     const int S = pb.n_species;
     gr.n_species = S;
     const int64_t atoms = pb.atoms;
@@ -1358,6 +1375,19 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
         neighbors(Slotted{}, cap);
         unsigned long long* st = gr.stats_host.get(kStatWords);
         MDX_HIP(hipMemcpyAsync(st, stats, kStatWords * sizeof(unsigned long long), hipMemcpyDeviceToHost, stream));
+        if (defer_stats && arena == nullptr) {
+            // the consumer is launched before the statistics are read
+            // (complete_graph); until then every centre counts as fitting.
+            // Not from an arena: a rebuild after an overflow would need the
+            // space of the pieces taken after the slotted rows.
+            gr.read_back.record(stream);
+            gr.stats_pending = true;
+            gr.slots = cap;
+            gr.most_rows = cap;
+            gr.pairs = -1;
+            gr.binned = -1;
+            return -1;
+        }
         // the expansion launch waits on these words: poll rather than sleep in
         // a blocking synchronisation, whose wake-up costs tens of microseconds
         gr.read_back.wait(stream);
@@ -1420,6 +1450,34 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     gr.pairs = pairs;
     gr.binned = binned;
     return pairs;
+}
+
+bool complete_graph(const PreparedBatch& pb, DeviceGraph& gr, const volatile int32_t* cancel) {
+    if (!gr.stats_pending) return true;
+    gr.stats_pending = false;
+    gr.read_back.sync();
+    const unsigned long long* st = gr.stats_host.get(kStatWords);
+    int64_t pairs = 0, most = 0;
+    reduce_stats(st, pb.atoms, pairs, most);
+    if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
+    gr.binned = static_cast<int64_t>(st[kStatBinned]);
+    gr.most_rows = most;
+    gr.pairs = pairs;
+    const int64_t cap = gr.slots;
+    if (most <= cap) {
+        // slots grown for a denser batch shrink back to what fits this one
+        int64_t fit = kMinSlotCap;
+        while (fit < most) fit *= 2;
+        if (fit < gr.slot_cap) gr.slot_cap = fit;
+        return true;
+    }
+    // a centre overflowed its slot: later builds use a larger one (or the
+    // compact layout); this batch is built again by the caller
+    int64_t grown = kMinSlotCap;
+    while (grown < most) grown *= 2;
+    gr.slot_cap = grown <= kMaxSlotCap ? grown : 0;
+    gr.slots = 0;
+    return false;
 }
 
 } // namespace mdx

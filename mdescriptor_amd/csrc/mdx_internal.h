@@ -172,7 +172,9 @@ public:
     StreamPoint& operator=(const StreamPoint&) = delete;
     ~StreamPoint();
     void prepare(); // create the event on the current device now
-    void wait(hipStream_t stream);
+    void wait(hipStream_t stream); // record, then sync
+    void record(hipStream_t stream);
+    void sync(); // until the stream reaches the last recorded point
 
 private:
     hipEvent_t event_ = nullptr;
@@ -185,6 +187,7 @@ struct DeviceGraph {
     int64_t binned = 0;
     int64_t pairs = 0;
     int64_t most_rows = 0;   // largest row count of one centre
+    bool stats_pending = false; // a deferred slotted build whose statistics are not read yet
     int n_species = 1;
     DeviceBuffer counters;   // zero-filled per build: u64 statistics[kStatWords], then i32 cell
                              // counts of binning (count, fill), [cells + 1] each
@@ -238,7 +241,14 @@ constexpr int64_t kMinSlotCap = 512;
 constexpr int64_t kMaxSlotCap = 8192;
 constexpr int64_t kMaxSlottedBytes = int64_t(4) << 30;
 int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& graph,
-                    const volatile int32_t* cancel, bool slotted = false);
+                    const volatile int32_t* cancel, bool slotted = false, bool defer_stats = false);
+// With defer_stats a slotted build returns (-1) before its statistics are
+// read: the caller may queue the graph's consumer at once, then calls
+// complete_graph, which reads them.  false: a centre overflowed its slot (the
+// slotted search clamped its counts to the slot, so the queued consumer read
+// only valid rows, with wrong results for it); build the batch again and
+// rerun the consumer.
+bool complete_graph(const PreparedBatch& pb, DeviceGraph& graph, const volatile int32_t* cancel);
 
 // Compute units of the current device (queried once per process and device).
 int device_compute_units();
