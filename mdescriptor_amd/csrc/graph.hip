@@ -412,24 +412,172 @@ __global__ void k_bin_sort(const StructGeom* geom, const int32_t* cell_struct, c
     }
 }
 
-// First bin of each species in each cell (Bins mode: cells are sorted by
-// species); species t of cell c spans [start[c*S + t], start[c*S + t + 1])
-// with the cell's end after the last species.  One thread per (cell, t):
-// a lower-bound search for t in the cell's sorted species column.
+// The runs of each cell: species t of cell c spans [runs[c*(S+1) + t],
+// runs[c*(S+1) + t + 1]) (Bins mode: cells are sorted by species) and
+// runs[c*(S+1) + S] is the cell's end.  One thread per (cell, t): a
+// lower-bound search for t in the cell's sorted species column.
 __global__ void k_cell_species(const int64_t* cell_start, int64_t cells_total, const int32_t* btype, int S,
-                               int64_t* cell_species_start) {
-    const int64_t work = cells_total * S;
+                               int64_t* cell_runs) {
+    const int64_t work = cells_total * (S + 1);
     for (int64_t w = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; w < work;
          w += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        const int64_t c = w / S;
-        const int t = static_cast<int>(w - c * S);
+        const int64_t c = w / (S + 1);
+        const int t = static_cast<int>(w - c * (S + 1));
         int64_t lo = cell_start[c], hi = cell_start[c + 1];
-        while (lo < hi) {
-            const int64_t mid = lo + (hi - lo) / 2;
-            if (btype[mid] < t) lo = mid + 1; else hi = mid;
+        if (t == S) {
+            lo = hi;
+        } else if (S > 1) {
+            while (lo < hi) {
+                const int64_t mid = lo + (hi - lo) / 2;
+                if (btype[mid] < t) lo = mid + 1; else hi = mid;
+            }
         }
-        cell_species_start[w] = lo;
+        cell_runs[w] = lo;
     }
+}
+
+// Binning of a whole structure by one workgroup, for batches whose every
+// structure has at most kLdsBinCells ROI cells and kStructImages images:
+// the image count of each cell in LDS, their scan, 32-bit keys (species
+// << 16 | extended index) at the cells' places in LDS, the rank of each key
+// inside its cell, then the binned images as SoA and each cell's runs.
+// The structure's bins start at its first extended index (ext_begin), so no
+// scan across structures is needed (the bins between its last binned image
+// and the next structure's first stay unused).  Same cells, order and runs
+// as k_bin_lds / k_bin_atoms + k_bin_sort + k_cell_species.
+constexpr int kStructThreads = 1024;
+constexpr int kStructImages = 8192;
+constexpr int kStructMinImages = 1024; // images per structure, on average, for this path
+constexpr int kStructPer = kStructImages / kStructThreads;
+constexpr int kStructCellsPer = kLdsBinCells / kStructThreads;
+
+__global__ __launch_bounds__(kStructThreads) void k_bin_struct(const StructGeom* geom, const ImageDesc* images,
+                                                               const double* positions, const int32_t* types, int S,
+                                                               double* bx, double* by, double* bz, int32_t* batom,
+                                                               int32_t* bimage, int32_t* btype, int64_t* cell_runs,
+                                                               unsigned long long* stats) {
+    __shared__ int32_t s_count[kLdsBinCells];
+    __shared__ int32_t s_start[kLdsBinCells];
+    __shared__ uint32_t s_key[kStructImages];
+    __shared__ int32_t s_wave[kStructThreads / kWave];
+    const StructGeom& g = geom[blockIdx.x];
+    const int natoms = g.natoms;
+    if (natoms == 0) return; // no cells
+    const int ncells = g.roi_dim[0] * g.roi_dim[1] * g.roi_dim[2];
+    const int n_ext = natoms * g.n_images;
+    const int tid = threadIdx.x;
+    const int lane = tid % kWave;
+    const int wave = tid / kWave;
+    for (int i = tid; i < ncells; i += kStructThreads) s_count[i] = 0;
+    __syncthreads();
+    // each image's ROI cell (every image of a one-cell structure is in its
+    // one cell; -1: outside the region), all gathers first, then its slot
+    // among the cell's images
+    int lc[kStructPer], slot[kStructPer];
+#pragma unroll
+    for (int r = 0; r < kStructPer; ++r) {
+        const int e = tid + r * kStructThreads;
+        lc[r] = -1;
+        if (e < n_ext) {
+            int c = 0;
+            bool inside = true;
+            if (g.one_cell == 0) {
+                const int q = e / natoms;
+                const int64_t a = g.atom_begin + (e - q * natoms);
+                const ImageDesc& im = images[g.image_begin + q];
+                c = static_cast<int>(roi_cell(g, positions[a * 3 + 0] + im.shift[0],
+                                              positions[a * 3 + 1] + im.shift[1],
+                                              positions[a * 3 + 2] + im.shift[2], inside) - g.cell_begin);
+            }
+            if (inside) lc[r] = c;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < kStructPer; ++r) slot[r] = lc[r] >= 0 ? atomicAdd(&s_count[lc[r]], 1) : 0;
+    __syncthreads();
+    // exclusive scan of the cell counts, kStructCellsPer consecutive cells a thread
+    int v[kStructCellsPer];
+    int sum = 0;
+#pragma unroll
+    for (int k = 0; k < kStructCellsPer; ++k) {
+        const int i = tid * kStructCellsPer + k;
+        v[k] = i < ncells ? s_count[i] : 0;
+        sum += v[k];
+    }
+    int incl = sum;
+#pragma unroll
+    for (int off = 1; off < kWave; off *= 2) {
+        const int u = __shfl_up(incl, off);
+        if (lane >= off) incl += u;
+    }
+    if (lane == kWave - 1) s_wave[wave] = incl;
+    __syncthreads();
+    int before = 0, binned = 0;
+    for (int w = 0; w < kStructThreads / kWave; ++w) {
+        if (w < wave) before += s_wave[w];
+        binned += s_wave[w];
+    }
+    int run = before + incl - sum;
+#pragma unroll
+    for (int k = 0; k < kStructCellsPer; ++k) {
+        const int i = tid * kStructCellsPer + k;
+        if (i < ncells) s_start[i] = run;
+        run += v[k];
+    }
+    __syncthreads();
+    // keys at their cells' places, in slot order
+    uint32_t key[kStructPer];
+#pragma unroll
+    for (int r = 0; r < kStructPer; ++r) {
+        key[r] = 0;
+        if (lc[r] < 0) continue;
+        const int e = tid + r * kStructThreads;
+        const int64_t a = g.atom_begin + e % natoms;
+        key[r] = (S > 1 ? static_cast<uint32_t>(types[a]) << 16 : 0u) | static_cast<uint32_t>(e);
+        s_key[s_start[lc[r]] + slot[r]] = key[r];
+    }
+    __syncthreads();
+    // each image at its rank inside its cell: (species, extended index)
+    // order; all ranks first, then the gathers and stores
+    const int64_t base = g.ext_begin;
+    int rank[kStructPer];
+#pragma unroll
+    for (int r = 0; r < kStructPer; ++r) {
+        rank[r] = 0;
+        if (lc[r] < 0) continue;
+        const int st = s_start[lc[r]], n = s_count[lc[r]];
+        int below = 0;
+        for (int j = 0; j < n; ++j) below += s_key[st + j] < key[r] ? 1 : 0;
+        rank[r] = st + below;
+    }
+#pragma unroll
+    for (int r = 0; r < kStructPer; ++r) {
+        if (lc[r] < 0) continue;
+        const int64_t dest = base + rank[r];
+        const int e = tid + r * kStructThreads;
+        double x, y, z;
+        int64_t atom, image;
+        image_position(g, images, positions, e, x, y, z, atom, image);
+        bx[dest] = x;
+        by[dest] = y;
+        bz[dest] = z;
+        batom[dest] = static_cast<int32_t>(atom);
+        bimage[dest] = static_cast<int32_t>(image);
+        btype[dest] = types[atom];
+    }
+    // runs: the cell's keys below species t, and its end
+    for (int w = tid; w < ncells * (S + 1); w += kStructThreads) {
+        const int c = w / (S + 1), t = w - c * (S + 1);
+        const int st = s_start[c], n = s_count[c];
+        int below = n;
+        if (t < S) {
+            below = 0;
+            for (int j = 0; j < n; ++j) below += static_cast<int>(s_key[st + j] >> 16) < t ? 1 : 0;
+        }
+        cell_runs[(g.cell_begin + c) * (S + 1) + t] = base + st + below;
+    }
+    // the binned image total, read back with the search statistics
+    if (tid == 0 && binned > 0) atomicAdd(&stats[kStatBinned], static_cast<unsigned long long>(binned));
 }
 
 // Kernel 1: the neighbour rows of the centres of one home cell per
@@ -475,8 +623,8 @@ __device__ inline uint64_t lane_range(int lo, int hi) {
 template <int kMode>
 __global__ __launch_bounds__(kNbrThreads) void k_neighbors(
     const StructGeom* geom, const int32_t* cell_struct, const double* positions, const int32_t* cell_list,
-    int64_t cells_total, const int64_t* cell_centre_start, const int32_t* cell_centres, const int64_t* cell_start,
-    const int64_t* cell_species_start, const double* bx, const double* by, const double* bz, int S,
+    int64_t cells_total, const int64_t* cell_centre_start, const int32_t* cell_centres, const int64_t* cell_runs,
+    const double* bx, const double* by, const double* bz, int S,
     double accept_max, int32_t* counts, int32_t* totals, int64_t* pair_start, uint32_t* pair_bin, int64_t cap,
     unsigned long long* stats) {
     constexpr bool kFill = kMode == kNbrFill;
@@ -516,8 +664,8 @@ __global__ __launch_bounds__(kNbrThreads) void k_neighbors(
                 const int64_t nc = g.cell_begin + (ix - g.roi_lo[0])
                     + static_cast<int64_t>(g.roi_dim[0])
                         * ((iy - g.roi_lo[1]) + static_cast<int64_t>(g.roi_dim[1]) * (iz - g.roi_lo[2]));
-                start = S == 1 ? cell_start[nc] : cell_species_start[nc * S + sp];
-                const int64_t end = S == 1 || sp + 1 == S ? cell_start[nc + 1] : cell_species_start[nc * S + sp + 1];
+                start = cell_runs[nc * (S + 1) + sp];
+                const int64_t end = cell_runs[nc * (S + 1) + sp + 1];
                 len = end - start;
             }
             s_segstart[t] = start;
@@ -719,7 +867,7 @@ __global__ __launch_bounds__(kNbrThreads) void k_neighbors(
 template <int kMode>
 __global__ __launch_bounds__(kBlock) void k_neighbors_wave(
     const int32_t* wave_cells, int64_t n_cells, const double* positions, const int64_t* cell_centre_start,
-    const int32_t* cell_centres, const int64_t* cell_start, const int64_t* cell_species_start, const double* bx,
+    const int32_t* cell_centres, const int64_t* cell_runs, const double* bx,
     const double* by, const double* bz, int S, double accept_max, int32_t* counts, int32_t* totals,
     int64_t* pair_start, uint32_t* pair_bin, int64_t cap, unsigned long long* stats) {
     constexpr bool kFill = kMode == kNbrFill;
@@ -734,9 +882,10 @@ __global__ __launch_bounds__(kBlock) void k_neighbors_wave(
     for (int64_t w = uniform_i64(static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave);
          w < n_cells; w += stride) {
         const int64_t c = uniform_i64(wave_cells[w]);
-        const int64_t start = uniform_i64(cell_start[c]);
+        const int64_t start = uniform_i64(cell_runs[c * (S + 1)]);
         // at most a wavefront of images (the host's choice of these cells)
-        const int n = __builtin_amdgcn_readfirstlane(static_cast<int>(min<int64_t>(cell_start[c + 1] - start, kWave)));
+        const int n = __builtin_amdgcn_readfirstlane(
+            static_cast<int>(min<int64_t>(cell_runs[c * (S + 1) + S] - start, kWave)));
         if (n <= 0) continue;
         const bool real = lane < n;
         const uint32_t bin = static_cast<uint32_t>(start + (real ? lane : 0));
@@ -744,8 +893,8 @@ __global__ __launch_bounds__(kBlock) void k_neighbors_wave(
         // species t of the cell at lanes [lo, hi) (lane t holds its own range)
         int lo = 0, hi = n;
         if (kCount && S > 1 && lane < S) {
-            lo = static_cast<int>(cell_species_start[c * S + lane] - start);
-            hi = lane + 1 == S ? n : static_cast<int>(cell_species_start[c * S + lane + 1] - start);
+            lo = static_cast<int>(cell_runs[c * (S + 1) + lane] - start);
+            hi = min(n, static_cast<int>(cell_runs[c * (S + 1) + lane + 1] - start));
         }
         const uint64_t species_lanes = lane_range(lo, hi);
         // the cell's centres (the structure's atoms, at most a wavefront) one
@@ -1141,6 +1290,21 @@ void prepare_batch(const mdx_batch_view& batch, const int32_t* species, int n_sp
             out.direct_bins = true;
         }
     }
+    // one binning workgroup per structure when every structure fits one and
+    // they average enough images to keep a workgroup busy
+    {
+        int64_t images_total = 0, filled = 0;
+        bool fits = true;
+        for (const StructGeom& g : out.geom) {
+            if (g.natoms == 0) continue;
+            const int64_t roi = static_cast<int64_t>(g.roi_dim[0]) * g.roi_dim[1] * g.roi_dim[2];
+            const int64_t images = static_cast<int64_t>(g.natoms) * g.n_images;
+            fits = fits && roi <= kLdsBinCells && images <= kStructImages;
+            images_total += images;
+            ++filled;
+        }
+        out.struct_bins = fits && filled > 0 && images_total >= kStructMinImages * filled;
+    }
     out.wave_cells = static_cast<int64_t>(out.cell_lists.size());
     for (int64_t s = 0; s < batch.structures; ++s) {
         const StructGeom& g = out.geom[static_cast<size_t>(s)];
@@ -1259,8 +1423,8 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     int32_t* cell_count = reinterpret_cast<int32_t*>(stats + kStatWords);
     int32_t* cell_fill = cell_count + cells1;
     gr.cell_start.reserve(cells1 * sizeof(int64_t));
-    gr.cell_species_start.reserve(std::max<size_t>(1, static_cast<size_t>(cells) * static_cast<size_t>(S)) *
-                                  sizeof(int64_t));
+    gr.cell_runs.reserve(std::max<size_t>(1, static_cast<size_t>(cells) * static_cast<size_t>(S + 1)) *
+                         sizeof(int64_t));
     gr.bin_key.reserve(static_cast<size_t>(ext) * sizeof(uint64_t));
     gr.bin_x.reserve(static_cast<size_t>(ext) * sizeof(double));
     gr.bin_y.reserve(static_cast<size_t>(ext) * sizeof(double));
@@ -1274,46 +1438,51 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
 
     // the centres' home cells and the cells' structures come with the batch
     // (prepare_batch); bin every periodic image into its ROI cell, sorted by (species, extended index)
-    int max_images = 1;
-    for (const StructGeom& sg : pb.geom) max_images = std::max(max_images, static_cast<int>(sg.n_images));
-    const dim3 bin_grid(static_cast<unsigned>(std::min<int64_t>((atoms + kBlock - 1) / kBlock, 1 << 16)),
-                        static_cast<unsigned>(std::min(max_images, 65535)));
-    const unsigned chunk_grid = static_cast<unsigned>(pb.bin_chunks.size());
-    const BinChunk* chunks = pb.d_bin_chunks.as<BinChunk>();
-    const int species_major = S > 1 ? 1 : 0;
-    if (pb.direct_bins) {
-        hipLaunchKernelGGL(k_bin_atoms<false>, bin_grid, dim3(kBlock), 0, stream, geom, images, pos,
-                           pb.d_atom_struct.as<int32_t>(), pb.d_types.as<int32_t>(), 0, atoms, max_images, cell_count,
-                           static_cast<const int64_t*>(nullptr), static_cast<uint64_t*>(nullptr));
-    }
-    if (chunk_grid > 0) {
-        hipLaunchKernelGGL(k_bin_lds<false>, dim3(chunk_grid), dim3(kBinThreads), 0, stream, chunks, geom, images, pos,
-                           pb.d_types.as<int32_t>(), 0, cell_count, static_cast<const int64_t*>(nullptr),
-                           static_cast<uint64_t*>(nullptr));
-    }
-    scan_counts(stream, cell_count, gr.cell_start.as<int64_t>(), cells, gr.scan_tmp);
-    if (pb.direct_bins) {
-        hipLaunchKernelGGL(k_bin_atoms<true>, bin_grid, dim3(kBlock), 0, stream, geom, images, pos,
-                           pb.d_atom_struct.as<int32_t>(), pb.d_types.as<int32_t>(), species_major, atoms, max_images,
-                           cell_fill, gr.cell_start.as<int64_t>(), gr.bin_key.as<uint64_t>());
-    }
-    if (chunk_grid > 0) {
-        hipLaunchKernelGGL(k_bin_lds<true>, dim3(chunk_grid), dim3(kBinThreads), 0, stream, chunks, geom, images, pos,
-                           pb.d_types.as<int32_t>(), species_major, cell_fill, gr.cell_start.as<int64_t>(),
-                           gr.bin_key.as<uint64_t>());
-    }
-    const unsigned cell_grid = static_cast<unsigned>(std::min<int64_t>(cells, 1 << 20));
-    // a wavefront per cell when cells hold a wavefront of images on average
-    const int sort_threads = ext <= static_cast<int64_t>(kWave) * cells ? kWave : kBlock;
-    hipLaunchKernelGGL(k_bin_sort, dim3(cell_grid), dim3(sort_threads), 0, stream, geom,
-                       pb.d_cell_struct.as<int32_t>(), images, pos, pb.d_types.as<int32_t>(), gr.cell_start.as<int64_t>(),
-                       cells, gr.bin_key.as<uint64_t>(), gr.bin_x.as<double>(), gr.bin_y.as<double>(),
-                       gr.bin_z.as<double>(), gr.bin_atom.as<int32_t>(), gr.bin_image.as<int32_t>(),
-                       gr.bin_type.as<int32_t>(), stats);
-    if (S > 1) {
-        hipLaunchKernelGGL(k_cell_species, dim3(grid_for(cells * S)), dim3(kBlock), 0, stream,
-                           gr.cell_start.as<int64_t>(), cells, gr.bin_type.as<int32_t>(), S,
-                           gr.cell_species_start.as<int64_t>());
+    if (pb.struct_bins) {
+        // one workgroup per structure: no scan, sort or run search between kernels
+        hipLaunchKernelGGL(k_bin_struct, dim3(static_cast<unsigned>(pb.geom.size())), dim3(kStructThreads), 0, stream,
+                           geom, images, pos, pb.d_types.as<int32_t>(), S, gr.bin_x.as<double>(),
+                           gr.bin_y.as<double>(), gr.bin_z.as<double>(), gr.bin_atom.as<int32_t>(),
+                           gr.bin_image.as<int32_t>(), gr.bin_type.as<int32_t>(), gr.cell_runs.as<int64_t>(), stats);
+    } else {
+        int max_images = 1;
+        for (const StructGeom& sg : pb.geom) max_images = std::max(max_images, static_cast<int>(sg.n_images));
+        const dim3 bin_grid(static_cast<unsigned>(std::min<int64_t>((atoms + kBlock - 1) / kBlock, 1 << 16)),
+                            static_cast<unsigned>(std::min(max_images, 65535)));
+        const unsigned chunk_grid = static_cast<unsigned>(pb.bin_chunks.size());
+        const BinChunk* chunks = pb.d_bin_chunks.as<BinChunk>();
+        const int species_major = S > 1 ? 1 : 0;
+        if (pb.direct_bins) {
+            hipLaunchKernelGGL(k_bin_atoms<false>, bin_grid, dim3(kBlock), 0, stream, geom, images, pos,
+                               pb.d_atom_struct.as<int32_t>(), pb.d_types.as<int32_t>(), 0, atoms, max_images, cell_count,
+                               static_cast<const int64_t*>(nullptr), static_cast<uint64_t*>(nullptr));
+        }
+        if (chunk_grid > 0) {
+            hipLaunchKernelGGL(k_bin_lds<false>, dim3(chunk_grid), dim3(kBinThreads), 0, stream, chunks, geom, images, pos,
+                               pb.d_types.as<int32_t>(), 0, cell_count, static_cast<const int64_t*>(nullptr),
+                               static_cast<uint64_t*>(nullptr));
+        }
+        scan_counts(stream, cell_count, gr.cell_start.as<int64_t>(), cells, gr.scan_tmp);
+        if (pb.direct_bins) {
+            hipLaunchKernelGGL(k_bin_atoms<true>, bin_grid, dim3(kBlock), 0, stream, geom, images, pos,
+                               pb.d_atom_struct.as<int32_t>(), pb.d_types.as<int32_t>(), species_major, atoms, max_images,
+                               cell_fill, gr.cell_start.as<int64_t>(), gr.bin_key.as<uint64_t>());
+        }
+        if (chunk_grid > 0) {
+            hipLaunchKernelGGL(k_bin_lds<true>, dim3(chunk_grid), dim3(kBinThreads), 0, stream, chunks, geom, images, pos,
+                               pb.d_types.as<int32_t>(), species_major, cell_fill, gr.cell_start.as<int64_t>(),
+                               gr.bin_key.as<uint64_t>());
+        }
+        const unsigned cell_grid = static_cast<unsigned>(std::min<int64_t>(cells, 1 << 20));
+        // a wavefront per cell when cells hold a wavefront of images on average
+        const int sort_threads = ext <= static_cast<int64_t>(kWave) * cells ? kWave : kBlock;
+        hipLaunchKernelGGL(k_bin_sort, dim3(cell_grid), dim3(sort_threads), 0, stream, geom,
+                           pb.d_cell_struct.as<int32_t>(), images, pos, pb.d_types.as<int32_t>(), gr.cell_start.as<int64_t>(),
+                           cells, gr.bin_key.as<uint64_t>(), gr.bin_x.as<double>(), gr.bin_y.as<double>(),
+                           gr.bin_z.as<double>(), gr.bin_atom.as<int32_t>(), gr.bin_image.as<int32_t>(),
+                           gr.bin_type.as<int32_t>(), stats);
+        hipLaunchKernelGGL(k_cell_species, dim3(grid_for(cells * (S + 1))), dim3(kBlock), 0, stream,
+                           gr.cell_start.as<int64_t>(), cells, gr.bin_type.as<int32_t>(), S, gr.cell_runs.as<int64_t>());
     }
     MDX_HIP(hipGetLastError());
     if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
@@ -1333,7 +1502,7 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
             hipLaunchKernelGGL(k_neighbors<decltype(mode)::value>, dim3(blocks), dim3(kNbrThreads), 0, stream, geom,
                                pb.d_cell_struct.as<int32_t>(), pos, big_list, big_cells,
                                pb.d_cell_centre_start.as<int64_t>(), pb.d_cell_centres.as<int32_t>(),
-                               gr.cell_start.as<int64_t>(), gr.cell_species_start.as<int64_t>(),
+                               gr.cell_runs.as<int64_t>(),
                                gr.bin_x.as<double>(), gr.bin_y.as<double>(), gr.bin_z.as<double>(), S, accept_max,
                                gr.counts.as<int32_t>(), gr.totals.as<int32_t>(), gr.pair_start.as<int64_t>(),
                                gr.pair_bin.as<uint32_t>(), cap, stats);
@@ -1344,7 +1513,7 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
                                                                             1 << 20));
             hipLaunchKernelGGL(k_neighbors_wave<decltype(mode)::value>, dim3(blocks), dim3(kBlock), 0, stream, lists,
                                wave_cells, pos, pb.d_cell_centre_start.as<int64_t>(), pb.d_cell_centres.as<int32_t>(),
-                               gr.cell_start.as<int64_t>(), gr.cell_species_start.as<int64_t>(),
+                               gr.cell_runs.as<int64_t>(),
                                gr.bin_x.as<double>(), gr.bin_y.as<double>(), gr.bin_z.as<double>(), S, accept_max,
                                gr.counts.as<int32_t>(), gr.totals.as<int32_t>(), gr.pair_start.as<int64_t>(),
                                gr.pair_bin.as<uint32_t>(), cap, stats);

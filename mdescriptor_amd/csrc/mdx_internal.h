@@ -137,6 +137,9 @@ struct PreparedBatch {
     std::vector<int32_t> cell_centres, cell_struct;
     DeviceBuffer d_cell_centre_start, d_cell_centres, d_cell_struct;
     bool direct_bins = false;
+    // every structure is binned by one workgroup of k_bin_struct (each has at
+    // most 2,048 ROI cells and 8,192 images, and they average 1,024 images or more)
+    bool struct_bins = false;
     DeviceBuffer d_bin_chunks; // BinChunk[bin_chunks.size()]
     DeviceBuffer d_cell_lists; // i32[cell_lists.size()]
     DeviceBuffer d_positions; // f64[atoms*3]
@@ -193,7 +196,7 @@ struct DeviceGraph {
                              // counts of binning (count, fill), [cells + 1] each
     DeviceBuffer cell_start; // i64[cells + 1] first bin of each ROI cell
     DeviceBuffer bin_key;                           // unsorted u64 keys, (species << 32) | extended index
-    DeviceBuffer cell_species_start;                // i64[cells * n_species]: first bin of each species in a cell
+    DeviceBuffer cell_runs;  // i64[cells * (n_species + 1)]: first bin of each species in a cell, then its end
     DeviceBuffer bin_x, bin_y, bin_z;               // f64 positions of binned images (sorted)
     DeviceBuffer bin_atom;                          // i32 global atom index
     DeviceBuffer bin_image;                         // i32 global image index
@@ -210,7 +213,7 @@ struct DeviceGraph {
     DeviceBuffer scan_tmp;   // block sums of the scans
 
     template <typename F> void for_each_buffer(F f) {
-        for (DeviceBuffer* b : {&counters, &cell_start, &bin_key, &cell_species_start, &bin_x, &bin_y, &bin_z,
+        for (DeviceBuffer* b : {&counters, &cell_start, &bin_key, &cell_runs, &bin_x, &bin_y, &bin_z,
                                 &bin_atom, &bin_image, &bin_type, &counts, &totals, &pair_start, &pair_bin,
                                 &scan_tmp}) {
             f(*b);

@@ -142,6 +142,56 @@ def test_slot_overflow_falls_back_to_the_compact_layout(hip_context, oracle):
         plan.close()
 
 
+def _small_periodic_batch(seed, species, boxes=3, atoms=150, box=8.0):
+    """Periodic boxes of 27 images each (cutoff below the box length), a
+    five-atom molecule whose region is one cell, and an empty structure: a
+    batch whose structures each fit one binning workgroup."""
+
+    rng = np.random.default_rng(seed)
+    parts, cells, pbc, offsets = [], [], [], [0]
+    for _ in range(boxes):
+        parts.append(rng.uniform(0.0, box, (atoms, 3)))
+        cells.append(np.eye(3) * box)
+        pbc.append([1, 1, 1])
+        offsets.append(offsets[-1] + atoms)
+    parts.append(rng.uniform(0.0, 1.5, (5, 3)))
+    cells.append(np.zeros((3, 3)))
+    pbc.append([0, 0, 0])
+    offsets.append(offsets[-1] + 5)
+    cells.append(np.zeros((3, 3)))
+    pbc.append([0, 0, 0])
+    offsets.append(offsets[-1])
+    n = offsets[-1]
+    numbers = np.array([species[i % len(species)] for i in range(n)], np.int32)
+    return SimpleNamespace(numbers=numbers, positions=np.concatenate(parts), cells=np.stack(cells),
+                           pbc=np.array(pbc, np.int32), offsets=np.array(offsets))
+
+
+@pytest.mark.parametrize("species", [[14], [1, 8], [1, 6, 8]])
+def test_one_workgroup_per_structure_binning(hip_context, oracle, species):
+    """Batches whose structures each have at most 2,048 region cells and
+    8,192 images (1,024 or more on average) are binned one structure per
+    workgroup, each structure's bins from its first extended index.  The
+    graph, the SOAP rows and the NeighborList must match the oracle as on
+    the multi-kernel path, with one species and several, a one-cell
+    molecule (searched by wavefronts) and an empty structure in the batch."""
+
+    batch = _small_periodic_batch(11 + len(species), species)
+    params = {"species": species, "n_max": 4, "l_max": 3, "r_cut": 3.0}
+    cutoff = params["r_cut"] + SOAP_PAD
+    ours = _hip.neighbor_graph(hip_context, batch, cutoff)
+    theirs = oracle.graph(batch, cutoff)
+    for key in theirs:
+        np.testing.assert_array_equal(ours[key], theirs[key], err_msg=key)
+    for average in ("off", "inner"):
+        _check(hip_context, oracle, batch, params, average, "float64")
+    for full in (True, False):
+        listed = _hip.neighbor_list(hip_context, batch, params["r_cut"], full_neighbor_list=full, table=True)
+        table, offsets = oracle.neighbor_list(batch, params["r_cut"], full_neighbor_list=full, self_pairs=False)
+        np.testing.assert_array_equal(listed["offsets"], offsets)
+        np.testing.assert_array_equal(listed["table"], table)
+
+
 @pytest.mark.parametrize("n_max,l_max", [(1, 0), (2, 1), (3, 2), (4, 3), (4, 7), (5, 4), (6, 5), (7, 9),
                                          (8, 6), (8, 8), (8, 10)])
 def test_quad_kernel_shapes(hip_context, oracle, monkeypatch, n_max, l_max):
