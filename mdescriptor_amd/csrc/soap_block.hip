@@ -903,6 +903,10 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
     }
 }
 
+// Gram tiles of the power-spectrum offset table: the register pairs ri <= rj,
+// or (summed coefficients) the registers
+constexpr int ps_tiles(int ncr, bool summed) { return summed ? ncr : ncr * (ncr + 1) / 2; }
+
 // Five wavefronts per SIMD (96 VGPRs); four for the weighted rows, whose
 // distance function (pow) needs the registers of a fifth, and for mu1nu1,
 // whose summed coefficients stay live beside the registers
@@ -913,7 +917,9 @@ k_soap_block(BlockArgs a) {
     // staging buffers, d2, exp table, padded S_lm table, power-spectrum
     // offsets; sized at compile time, so every LDS offset is an immediate
     __shared__ double lds[2 * PL::YWORDS + 2 * kNb + kTab + 4 * units_before(0xffffffffu, PL::L)];
-    constexpr int kPsWords = NCR * (NCR + 1) / 2 * 4 * kWaveThreads;
+    // the plan's offset table: a tile per register pair, or (mu1nu1) one per
+    // register against the species-summed one; no more is read
+    constexpr int kPsWords = ps_tiles(NCR, MODE == kBlockRowsSummed) * 4 * kWaveThreads;
     __shared__ int s_ps[kPsWords];
     const int tid = threadIdx.x;
     for (int i = tid; i < kPsWords; i += static_cast<int>(blockDim.x)) s_ps[i] = a.ps_offsets[i];
@@ -1163,6 +1169,10 @@ bool block_plan_tables(int S, int n, int l_max, int out_dtype, int compression, 
                 }
             }
         }
+    }
+    // the kernel stages exactly this many entries
+    if (out.ps_offsets.size() != static_cast<size_t>(ps_tiles(ncr, compression == 2)) * 4 * 64) {
+        throw Error(MDX_INTERNAL, "power-spectrum offset table does not match the expansion kernel");
     }
     out.kg = kg;
     out.ncr = ncr;
