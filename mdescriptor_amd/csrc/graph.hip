@@ -451,16 +451,17 @@ constexpr int kStructMinImages = 1024; // images per structure, on average, for 
 constexpr int kStructPer = kStructImages / kStructThreads;
 constexpr int kStructCellsPer = kLdsBinCells / kStructThreads;
 
-__global__ __launch_bounds__(kStructThreads) void k_bin_struct(const StructGeom* geom, const ImageDesc* images,
-                                                               const double* positions, const int32_t* types, int S,
-                                                               double* bx, double* by, double* bz, int32_t* batom,
-                                                               int32_t* bimage, int32_t* btype, int64_t* cell_runs,
+__global__ __launch_bounds__(kStructThreads) void k_bin_struct(const int32_t* list, const StructGeom* geom,
+                                                               const ImageDesc* images, const double* positions,
+                                                               const int32_t* types, int S, double* bx, double* by,
+                                                               double* bz, int32_t* batom, int32_t* bimage,
+                                                               int32_t* btype, int64_t* cell_runs,
                                                                unsigned long long* stats) {
     __shared__ int32_t s_count[kLdsBinCells];
     __shared__ int32_t s_start[kLdsBinCells];
     __shared__ uint32_t s_key[kStructImages];
     __shared__ int32_t s_wave[kStructThreads / kWave];
-    const StructGeom& g = geom[blockIdx.x];
+    const StructGeom& g = geom[list[blockIdx.x]];
     const int natoms = g.natoms;
     if (natoms == 0) return; // no cells
     const int ncells = g.roi_dim[0] * g.roi_dim[1] * g.roi_dim[2];
@@ -577,7 +578,76 @@ __global__ __launch_bounds__(kStructThreads) void k_bin_struct(const StructGeom*
         cell_runs[(g.cell_begin + c) * (S + 1) + t] = base + st + below;
     }
     // the binned image total, read back with the search statistics
-    if (tid == 0 && binned > 0) atomicAdd(&stats[kStatBinned], static_cast<unsigned long long>(binned));
+    if (tid == 0 && binned > 0) {
+        atomicAdd(&stats[stat_binned(static_cast<int>(blockIdx.x % kStatLanes))], static_cast<unsigned long long>(binned));
+    }
+}
+
+// Binning of structures of at most a wavefront of images and kSmallCells ROI
+// cells (small molecules), a wavefront each: lane e holds image e and its
+// key (ROI cell << 11 | species << 6 | e; images outside the region sort
+// last); its rank among the structure's keys is its bin, from the
+// structure's first extended index as in k_bin_struct, and the runs of a
+// cell count the keys below (cell, species t) for t = 0 .. S (t = S: the
+// cell's end).  Same cells, order and runs as the other binning paths.
+constexpr int kSmallImages = kWave;
+constexpr int kSmallCells = 64;
+
+__global__ __launch_bounds__(kBlock) void k_bin_small(const int32_t* list, int64_t count, const StructGeom* geom,
+                                                      const ImageDesc* images, const double* positions,
+                                                      const int32_t* types, int S, double* bx, double* by, double* bz,
+                                                      int32_t* batom, int32_t* bimage, int32_t* btype,
+                                                      int64_t* cell_runs, unsigned long long* stats) {
+    constexpr int kWaves = kBlock / kWave;
+    const int lane = threadIdx.x % kWave;
+    const int64_t w = static_cast<int64_t>(blockIdx.x) * kWaves + threadIdx.x / kWave;
+    if (w >= count) return;
+    const StructGeom& g = geom[list[w]];
+    const int n_ext = g.natoms * g.n_images; // at most kSmallImages (the host's choice)
+    const int ncells = g.roi_dim[0] * g.roi_dim[1] * g.roi_dim[2];
+    constexpr uint32_t kOutside = 0xffffffffu;
+    uint32_t key = kOutside;
+    double x = 0.0, y = 0.0, z = 0.0;
+    int64_t atom = 0, image = 0;
+    if (lane < n_ext) {
+        image_position(g, images, positions, lane, x, y, z, atom, image);
+        int c = 0;
+        bool inside = true;
+        if (g.one_cell == 0) c = static_cast<int>(roi_cell(g, x, y, z, inside) - g.cell_begin);
+        if (inside) {
+            key = (static_cast<uint32_t>(c) << 11) | (static_cast<uint32_t>(types[atom]) << 6) |
+                  static_cast<uint32_t>(lane);
+        }
+    }
+    int rank = 0;
+    for (int j = 0; j < n_ext; ++j) {
+        rank += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(key), j)) < key ? 1 : 0;
+    }
+    const int64_t base = g.ext_begin;
+    if (key != kOutside) {
+        const int64_t dest = base + rank;
+        bx[dest] = x;
+        by[dest] = y;
+        bz[dest] = z;
+        batom[dest] = static_cast<int32_t>(atom);
+        bimage[dest] = static_cast<int32_t>(image);
+        btype[dest] = types[atom];
+    }
+    const int pairs = ncells * (S + 1);
+    for (int p0 = 0; p0 < pairs; p0 += kWave) {
+        const int p = p0 + lane;
+        const int c = p / (S + 1), t = p - c * (S + 1);
+        const uint32_t bound = (static_cast<uint32_t>(c) << 11) | (static_cast<uint32_t>(t) << 6);
+        int below = 0;
+        for (int j = 0; j < n_ext; ++j) {
+            below += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(key), j)) < bound ? 1 : 0;
+        }
+        if (p < pairs) cell_runs[(g.cell_begin + c) * (S + 1) + t] = base + below;
+    }
+    const int binned = static_cast<int>(__popcll(__ballot(key != kOutside)));
+    if (lane == 0 && binned > 0) {
+        atomicAdd(&stats[stat_binned(static_cast<int>(w % kStatLanes))], static_cast<unsigned long long>(binned));
+    }
 }
 
 // Kernel 1: the neighbour rows of the centres of one home cell per
@@ -1298,20 +1368,35 @@ void prepare_batch(const mdx_batch_view& batch, const int32_t* species, int n_sp
             out.direct_bins = true;
         }
     }
-    // one binning workgroup per structure when every structure fits one and
-    // they average enough images to keep a workgroup busy
+    // structures binned on their own when each fits a wavefront (small) or a
+    // workgroup, the workgroup ones averaging enough images to keep it busy
     {
-        int64_t images_total = 0, filled = 0;
+        int64_t images_total = 0, large = 0;
         bool fits = true;
-        for (const StructGeom& g : out.geom) {
+        out.struct_list.clear();
+        for (size_t s = 0; s < out.geom.size(); ++s) {
+            const StructGeom& g = out.geom[s];
             if (g.natoms == 0) continue;
             const int64_t roi = static_cast<int64_t>(g.roi_dim[0]) * g.roi_dim[1] * g.roi_dim[2];
             const int64_t images = static_cast<int64_t>(g.natoms) * g.n_images;
-            fits = fits && roi <= kLdsBinCells && images <= kStructImages;
-            images_total += images;
-            ++filled;
+            if (images <= kSmallImages && roi <= kSmallCells) {
+                out.struct_list.push_back(static_cast<int32_t>(s));
+            } else {
+                fits = fits && roi <= kLdsBinCells && images <= kStructImages;
+                images_total += images;
+                ++large;
+            }
         }
-        out.struct_bins = fits && filled > 0 && images_total >= kStructMinImages * filled;
+        out.small_structs = static_cast<int64_t>(out.struct_list.size());
+        for (size_t s = 0; s < out.geom.size() && fits; ++s) {
+            const StructGeom& g = out.geom[s];
+            const int64_t roi = static_cast<int64_t>(g.roi_dim[0]) * g.roi_dim[1] * g.roi_dim[2];
+            const int64_t images = static_cast<int64_t>(g.natoms) * g.n_images;
+            if (g.natoms > 0 && !(images <= kSmallImages && roi <= kSmallCells)) {
+                out.struct_list.push_back(static_cast<int32_t>(s));
+            }
+        }
+        out.struct_bins = fits && !out.struct_list.empty() && images_total >= kStructMinImages * large;
     }
     out.wave_cells = static_cast<int64_t>(out.cell_lists.size());
     for (int64_t s = 0; s < batch.structures; ++s) {
@@ -1331,6 +1416,11 @@ void upload_batch(hipStream_t stream, const mdx_batch_view& batch, PreparedBatch
     pb.d_images.reserve(std::max<size_t>(1, pb.images.size() * sizeof(ImageDesc)));
     pb.d_offsets.reserve(pb.offsets.size() * sizeof(int64_t));
     pb.d_cell_lists.reserve(std::max<size_t>(1, pb.cell_lists.size() * sizeof(int32_t)));
+    pb.d_struct_list.reserve(std::max<size_t>(1, pb.struct_list.size() * sizeof(int32_t)));
+    if (pb.struct_bins) {
+        MDX_HIP(hipMemcpyAsync(pb.d_struct_list.ptr, pb.struct_list.data(), pb.struct_list.size() * sizeof(int32_t),
+                               hipMemcpyHostToDevice, stream));
+    }
     pb.d_bin_chunks.reserve(std::max<size_t>(1, pb.bin_chunks.size() * sizeof(BinChunk)));
     pb.d_cell_centre_start.reserve(std::max<size_t>(1, pb.cell_centre_start.size() * sizeof(int64_t)));
     pb.d_cell_centres.reserve(std::max<size_t>(1, pb.cell_centres.size() * sizeof(int32_t)));
@@ -1383,6 +1473,14 @@ namespace {
 // rows and largest row count over the statistics lines; every centre must
 // have been searched (the host's list of home cells holding centres and the
 // device's placement of the centres agree)
+// binned images: the multi-kernel binning's total, or the per-structure
+// binnings' counts spread over the statistics lines
+int64_t binned_total(const unsigned long long* st) {
+    int64_t binned = static_cast<int64_t>(st[kStatBinned]);
+    for (int l = 0; l < kStatLanes; ++l) binned += static_cast<int64_t>(st[stat_binned(l)]);
+    return binned;
+}
+
 void reduce_stats(const unsigned long long* st, int64_t atoms, int64_t& rows, int64_t& most) {
     rows = 0;
     most = 0;
@@ -1447,11 +1545,25 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     // the centres' home cells and the cells' structures come with the batch
     // (prepare_batch); bin every periodic image into its ROI cell, sorted by (species, extended index)
     if (pb.struct_bins) {
-        // one workgroup per structure: no scan, sort or run search between kernels
-        hipLaunchKernelGGL(k_bin_struct, dim3(static_cast<unsigned>(pb.geom.size())), dim3(kStructThreads), 0, stream,
-                           geom, images, pos, pb.d_types.as<int32_t>(), S, gr.bin_x.as<double>(),
-                           gr.bin_y.as<double>(), gr.bin_z.as<double>(), gr.bin_atom.as<int32_t>(),
-                           gr.bin_image.as<int32_t>(), gr.bin_type.as<int32_t>(), gr.cell_runs.as<int64_t>(), stats);
+        // each structure on its own: no scan, sort or run search between kernels
+        const int32_t* list = pb.d_struct_list.as<int32_t>();
+        const int64_t small = pb.small_structs;
+        const int64_t large = static_cast<int64_t>(pb.struct_list.size()) - small;
+        if (small > 0) {
+            constexpr int64_t per_block = kBlock / kWave;
+            hipLaunchKernelGGL(k_bin_small, dim3(static_cast<unsigned>((small + per_block - 1) / per_block)),
+                               dim3(kBlock), 0, stream, list, small, geom, images, pos, pb.d_types.as<int32_t>(), S,
+                               gr.bin_x.as<double>(), gr.bin_y.as<double>(), gr.bin_z.as<double>(),
+                               gr.bin_atom.as<int32_t>(), gr.bin_image.as<int32_t>(), gr.bin_type.as<int32_t>(),
+                               gr.cell_runs.as<int64_t>(), stats);
+        }
+        if (large > 0) {
+            hipLaunchKernelGGL(k_bin_struct, dim3(static_cast<unsigned>(large)), dim3(kStructThreads), 0, stream,
+                               list + small, geom, images, pos, pb.d_types.as<int32_t>(), S, gr.bin_x.as<double>(),
+                               gr.bin_y.as<double>(), gr.bin_z.as<double>(), gr.bin_atom.as<int32_t>(),
+                               gr.bin_image.as<int32_t>(), gr.bin_type.as<int32_t>(), gr.cell_runs.as<int64_t>(),
+                               stats);
+        }
     } else {
         int max_images = 1;
         for (const StructGeom& sg : pb.geom) max_images = std::max(max_images, static_cast<int>(sg.n_images));
@@ -1571,7 +1683,7 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
         if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
         int64_t pairs = 0, most = 0;
         reduce_stats(st, atoms, pairs, most);
-        const int64_t binned = static_cast<int64_t>(st[kStatBinned]);
+        const int64_t binned = binned_total(st);
         gr.most_rows = most;
         if (most <= cap) {
             // slots grown for a denser batch shrink back to what fits this one
@@ -1611,7 +1723,7 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     unsigned long long st[kStatWords] = {};
     MDX_HIP(hipMemcpyAsync(st, stats, sizeof(st), hipMemcpyDeviceToHost, stream));
     MDX_HIP(hipStreamSynchronize(stream));
-    const int64_t binned = static_cast<int64_t>(st[kStatBinned]);
+    const int64_t binned = binned_total(st);
     int64_t counted = 0;
     reduce_stats(st, atoms, counted, gr.most_rows);
     if (slotted && gr.slot_cap == 0 && gr.most_rows <= kMaxSlotCap) {
@@ -1637,7 +1749,7 @@ bool complete_graph(const PreparedBatch& pb, DeviceGraph& gr, const volatile int
     int64_t pairs = 0, most = 0;
     reduce_stats(st, pb.atoms, pairs, most);
     if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
-    gr.binned = static_cast<int64_t>(st[kStatBinned]);
+    gr.binned = binned_total(st);
     gr.most_rows = most;
     gr.pairs = pairs;
     const int64_t cap = gr.slots;

@@ -137,9 +137,14 @@ struct PreparedBatch {
     std::vector<int32_t> cell_centres, cell_struct;
     DeviceBuffer d_cell_centre_start, d_cell_centres, d_cell_struct;
     bool direct_bins = false;
-    // every structure is binned by one workgroup of k_bin_struct (each has at
-    // most 2,048 ROI cells and 8,192 images, and they average 1,024 images or more)
+    // every structure is binned on its own, its bins from its first extended
+    // index: by a wavefront of k_bin_small (at most 64 images and 64 ROI
+    // cells) or a workgroup of k_bin_struct (at most 2,048 ROI cells and 8,192
+    // images; those average 1,024 images or more)
     bool struct_bins = false;
+    std::vector<int32_t> struct_list; // the k_bin_small structures, then the k_bin_struct ones
+    int64_t small_structs = 0;
+    DeviceBuffer d_struct_list;
     DeviceBuffer d_bin_chunks; // BinChunk[bin_chunks.size()]
     DeviceBuffer d_cell_lists; // i32[cell_lists.size()]
     DeviceBuffer d_positions; // f64[atoms*3]
@@ -240,6 +245,7 @@ constexpr int kStatWords = kStatLineWords * (1 + kStatLanes);
 __host__ __device__ constexpr int stat_rows(int lane) { return kStatLineWords * (1 + lane); }
 __host__ __device__ constexpr int stat_most(int lane) { return kStatLineWords * (1 + lane) + 1; }
 __host__ __device__ constexpr int stat_centres(int lane) { return kStatLineWords * (1 + lane) + 2; }
+__host__ __device__ constexpr int stat_binned(int lane) { return kStatLineWords * (1 + lane) + 3; }
 constexpr int64_t kMinSlotCap = 512;
 constexpr int64_t kMaxSlotCap = 8192;
 constexpr int64_t kMaxSlottedBytes = int64_t(4) << 30;

@@ -171,10 +171,11 @@ def _small_periodic_batch(seed, species, boxes=3, atoms=150, box=8.0):
 def test_one_workgroup_per_structure_binning(hip_context, oracle, species):
     """Batches whose structures each have at most 2,048 region cells and
     8,192 images (1,024 or more on average) are binned one structure per
-    workgroup, each structure's bins from its first extended index.  The
-    graph, the SOAP rows and the NeighborList must match the oracle as on
-    the multi-kernel path, with one species and several, a one-cell
-    molecule (searched by wavefronts) and an empty structure in the batch."""
+    workgroup, and structures of at most 64 images one per wavefront, each
+    structure's bins from its first extended index.  The graph, the SOAP
+    rows and the NeighborList must match the oracle as on the multi-kernel
+    path, with one species and several, a one-cell molecule (binned and
+    searched by wavefronts) and an empty structure in the batch."""
 
     batch = _small_periodic_batch(11 + len(species), species)
     params = {"species": species, "n_max": 4, "l_max": 3, "r_cut": 3.0}
