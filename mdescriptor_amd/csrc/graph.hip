@@ -449,6 +449,7 @@ constexpr int kStructThreads = 1024;
 constexpr int kStructImages = 8192;
 constexpr int kStructMinImages = 1024; // images per structure, on average, for this path
 constexpr int kStructPer = kStructImages / kStructThreads;
+static_assert(kStructImages <= (1 << 16), "extended index below the species bits of a key");
 constexpr int kStructCellsPer = kLdsBinCells / kStructThreads;
 
 __global__ __launch_bounds__(kStructThreads) void k_bin_struct(const int32_t* list, const StructGeom* geom,
@@ -592,6 +593,7 @@ __global__ __launch_bounds__(kStructThreads) void k_bin_struct(const int32_t* li
 // cell's end).  Same cells, order and runs as the other binning paths.
 constexpr int kSmallImages = kWave;
 constexpr int kSmallCells = 64;
+static_assert(kMaxSpecies < 32 && kSmallImages <= 64, "species and image fields of a small structure's key");
 
 __global__ __launch_bounds__(kBlock) void k_bin_small(const int32_t* list, int64_t count, const StructGeom* geom,
                                                       const ImageDesc* images, const double* positions,
