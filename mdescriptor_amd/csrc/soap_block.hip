@@ -981,7 +981,11 @@ void launch_shape(hipStream_t stream, const BlockArgs& a, int64_t count) {
     const int64_t resident = std::max<int64_t>(1, std::min<int64_t>(8, (160 * 1024) / std::max<size_t>(lds, 1)));
     const int64_t target = std::max<int64_t>(1, 8 * resident * device_compute_units());
     BlockArgs args = a;
-    args.per_block = std::max<int64_t>(1, (count + target - 1) / target);
+    // atom-level rows: at least two centres a workgroup, so the exp table and
+    // the stage pipeline are set up for more than one (config 1's expansion
+    // 0.090 -> 0.085 ms); structure averages keep one structure a workgroup
+    const int64_t least = a.struct_offsets != nullptr ? 1 : 2;
+    args.per_block = std::max<int64_t>(least, (count + target - 1) / target);
     const unsigned grid = static_cast<unsigned>((count + args.per_block - 1) / args.per_block);
     const dim3 threads(PL::T * kWaveThreads);
     const int mode = a.struct_offsets != nullptr ? (a.small_structures ? kBlockInnerSmall : kBlockInner)
