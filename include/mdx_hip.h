@@ -175,6 +175,23 @@ int mdx_hip_batch_upload(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, const mdx_
                          mdx_device_batch** out);
 void mdx_hip_batch_destroy(mdx_device_batch* batch);
 
+/* New positions for a device-resident batch (a new frame of the same system:
+ * numbers, cells, pbc and offsets are kept): positions f64[atoms*3], C order,
+ * in host or device memory.  Replaces the position part of the per-call
+ * upload of Backend::compute (cpp/cuda/src/backend.cu:353-356) for a caller
+ * that keeps its batch on the device; the reference itself takes each frame
+ * as a new StructureBatch (src/mdescriptor/core/input.py:39-122).  Everything
+ * that depends on positions (cell grid, regions of interest, home cells,
+ * graph) is rebuilt on the device by the next run, as compute_soap rebuilds
+ * its grid on every call (cpp/src/standalone/soap.cpp:1218-1245,
+ * cpp/src/common/neighbor.cpp:135-194, 551).  Host positions are checked
+ * ("positions must be finite") and copied before the call returns.  Device
+ * positions are copied on the context's stream, after the work already
+ * queued there and before the next run on this context reads them; the caller
+ * keeps them unchanged until that run returns.  A non-finite device position
+ * makes that run return MDX_INVALID_ARGUMENT with the same message. */
+int mdx_hip_batch_set_positions(mdx_hip_ctx* ctx, mdx_device_batch* batch, const double* positions);
+
 /* ... then run the SOAP pipeline on it, writing into device memory out_device
  * (rows x features, row stride out_pitch_bytes).  No host copy of the result;
  * the call returns after the stream has finished.  Same computation as

@@ -203,6 +203,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(BatchView), ctypes.POINTER(ctypes.c_void_p)],
     ),
     "mdx_hip_batch_destroy": (None, [ctypes.c_void_p]),
+    "mdx_hip_batch_set_positions": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
     "mdx_hip_soap_run": (
         ctypes.c_int,
         [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, _i32p,
@@ -488,6 +489,24 @@ class DeviceBatch:
         ctx.check(ctx.lib.mdx_hip_batch_upload(ctx.handle, plan.handle, ctypes.byref(self.arrays.view),
                                                ctypes.byref(handle)))
         self.handle = handle
+
+    def set_positions(self, positions: Any) -> None:
+        """New positions for the resident batch (a new frame of the same
+        system): a host array of shape (atoms, 3), or the device address (an
+        int) of atoms * 3 float64 values.  Everything that depends on
+        positions is rebuilt on the device by the next :meth:`run`."""
+
+        ctx = self.plan.context
+        if isinstance(positions, int):
+            address = ctypes.c_void_p(positions)
+            keep = None
+        else:
+            keep = np.ascontiguousarray(positions, dtype=np.float64)
+            if keep.size != 3 * len(self.arrays.numbers):
+                raise ValueError("positions must hold atoms * 3 values")
+            address = keep.ctypes.data_as(ctypes.c_void_p)
+        ctx.check(ctx.lib.mdx_hip_batch_set_positions(ctx.handle, self.handle, address))
+        del keep
 
     def run(self, out_device_ptr: int, pitch_bytes: int, cancel: ctypes.c_int32 | None = None) -> dict[str, float]:
         ctx = self.plan.context
@@ -915,6 +934,14 @@ class DeviceMemory:
         if self.runtime().hipMemcpy(out.ctypes.data_as(ctypes.c_void_p), self.ptr, out.nbytes, 2) != 0:
             raise HipError("hipMemcpy device-to-host failed")
         return out
+
+    def from_host(self, array: np.ndarray) -> "DeviceMemory":
+        data = np.ascontiguousarray(array)
+        if data.nbytes > self.nbytes:
+            raise ValueError("host array larger than the device allocation")
+        if self.runtime().hipMemcpy(self.ptr, data.ctypes.data_as(ctypes.c_void_p), data.nbytes, 1) != 0:
+            raise HipError("hipMemcpy host-to-device failed")
+        return self
 
     @classmethod
     def synchronize(cls) -> None:

@@ -21,7 +21,7 @@ CSRC = PACKAGE / "csrc"
 OBJ_DIR = PACKAGE / "_build"
 LIB_DIR = PACKAGE / "_lib"
 LIBRARY = LIB_DIR / "libmdx_hip.so"
-SOURCES = ("graph.hip", "soap.hip", "soap_mfma.hip", "soap_quad.hip", "soap_block.hip", "neighbor_list.hip",
+SOURCES = ("graph.hip", "frame.hip", "soap.hip", "soap_mfma.hip", "soap_quad.hip", "soap_block.hip", "neighbor_list.hip",
            "api.hip")
 # peak-rate probes for the roofline (bench.py --peaks), a library of their own
 PEAKS_SOURCE = "peaks.hip"

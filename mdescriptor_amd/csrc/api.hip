@@ -248,7 +248,7 @@ void run_pipeline(mdx_hip_ctx* ctx, const mdx_soap_plan& plan, mdx::PreparedBatc
     mdx::run_soap(s, plan, pb, graph, out_device, pitch, partials, cancel, ctx->events, timing, slice, on_slice);
     if (!mdx::complete_graph(pb, graph, cancel)) {
         MDX_HIP(hipStreamSynchronize(s)); // the first expansion's buffers are replaced
-        mdx::build_graph(s, pb, graph, cancel, true);
+        mdx::build_graph(s, pb, graph, cancel, true, false, true);
         MDX_HIP(hipEventRecord(ctx->events[1], s));
         check_cancel(cancel);
         mdx::run_soap(s, plan, pb, graph, out_device, pitch, partials, cancel, ctx->events, timing, slice, on_slice);
@@ -814,6 +814,31 @@ int mdx_hip_batch_upload(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, const mdx_
             throw;
         }
         *out = db;
+    });
+}
+
+int mdx_hip_batch_set_positions(mdx_hip_ctx* ctx, mdx_device_batch* batch, const double* positions) {
+    if (ctx == nullptr) return MDX_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    return guarded(ctx, [&] {
+        if (batch == nullptr) throw mdx::Error(MDX_INVALID_ARGUMENT, "null batch");
+        if (batch->device != ctx->device) throw mdx::Error(MDX_INVALID_ARGUMENT, "batch belongs to another device");
+        const size_t values = static_cast<size_t>(batch->pb.atoms) * 3;
+        if (values == 0) return;
+        if (positions == nullptr) throw mdx::Error(MDX_INVALID_ARGUMENT, "null positions");
+        DeviceScope scope(ctx->device);
+        if (is_device_memory(positions)) {
+            // checked for finiteness by the next run's frame kernels
+            MDX_HIP(hipMemcpyAsync(batch->pb.d_positions.ptr, positions, values * sizeof(double),
+                                   hipMemcpyDeviceToDevice, ctx->stream));
+            return;
+        }
+        for (size_t i = 0; i < values; ++i) {
+            if (!std::isfinite(positions[i])) throw mdx::Error(MDX_INVALID_ARGUMENT, "positions must be finite");
+        }
+        MDX_HIP(hipMemcpyAsync(batch->pb.d_positions.ptr, positions, values * sizeof(double), hipMemcpyHostToDevice,
+                               ctx->stream));
+        MDX_HIP(hipStreamSynchronize(ctx->stream));
     });
 }
 

@@ -239,14 +239,6 @@ void validate_batch(const mdx_batch_view& b) {
     }
 }
 
-// CellGrid::coordinate (neighbor.cpp:122-132); shared by host and device.
-__host__ __device__ inline int grid_coordinate(double value, double origin, double width, int dim) {
-    const double scaled = (value - origin) / width;
-    if (!(scaled > 0.0)) return 0;
-    if (!__builtin_isfinite(scaled) || scaled >= static_cast<double>(dim)) return dim - 1;
-    return static_cast<int>(scaled);
-}
-
 // ---------------------------------------------------------------- device side
 
 __device__ inline int64_t roi_cell(const StructGeom& g, double x, double y, double z, bool& inside) {
@@ -273,8 +265,6 @@ __device__ inline void image_position(const StructGeom& g, const ImageDesc* imag
 
 // Binning walks (image, atom) pairs on a 2-D grid (y: image, x: atom), so no
 // index division is needed.  The extended index of (image q, local atom j) is
-constexpr int kLdsBinCells = 2048; // ROI cells of a structure binned in LDS, at most
-constexpr int kBinChunk = 4096;    // images per LDS binning workgroup
 
 // q * natoms + j (neighbor.cpp:519-528).  Count pass: cell_count[c] += 1;
 // fill pass: keys at cell_start[c] + a slot taken from cell_count.
@@ -446,8 +436,6 @@ __global__ void k_cell_species(const int64_t* cell_start, int64_t cells_total, c
 // and the next structure's first stay unused).  Same cells, order and runs
 // as k_bin_lds / k_bin_atoms + k_bin_sort + k_cell_species.
 constexpr int kStructThreads = 1024;
-constexpr int kStructImages = 8192;
-constexpr int kStructMinImages = 1024; // images per structure, on average, for this path
 constexpr int kStructPer = kStructImages / kStructThreads;
 static_assert(kStructImages <= (1 << 16), "extended index below the species bits of a key");
 constexpr int kStructCellsPer = kLdsBinCells / kStructThreads;
@@ -591,8 +579,6 @@ __global__ __launch_bounds__(kStructThreads) void k_bin_struct(const int32_t* li
 // structure's first extended index as in k_bin_struct, and the runs of a
 // cell count the keys below (cell, species t) for t = 0 .. S (t = S: the
 // cell's end).  Same cells, order and runs as the other binning paths.
-constexpr int kSmallImages = kWave;
-constexpr int kSmallCells = 64;
 static_assert(kMaxSpecies < 32 && kSmallImages <= 64, "species and image fields of a small structure's key");
 
 __global__ __launch_bounds__(kBlock) void k_bin_small(const int32_t* list, int64_t count, const StructGeom* geom,
@@ -676,7 +662,6 @@ constexpr int kCentreBatch = 128;   // centres whose running counts live in LDS 
 constexpr int kSegments = kMaxSpecies * 27;
 constexpr int kNoBoundary = 0x7fffffff;
 constexpr int kNbrCount = 0, kNbrFill = 1, kNbrSlotted = 2;
-constexpr int kWaveCellImages = kWave; // binned images of a cell searched by one wavefront
 
 // a wave-uniform 64-bit value in scalar registers
 __device__ inline int64_t uniform_i64(int64_t v) {
@@ -695,7 +680,7 @@ __device__ inline uint64_t lane_range(int lo, int hi) {
 template <int kMode>
 __global__ __launch_bounds__(kNbrThreads) void k_neighbors(
     const StructGeom* geom, const int32_t* cell_struct, const double* positions, const int32_t* cell_list,
-    int64_t cells_total, const int64_t* cell_centre_start, const int32_t* cell_centres, const int64_t* cell_runs,
+    const unsigned long long* list_count, const int64_t* cell_centre_start, const int32_t* cell_centres, const int64_t* cell_runs,
     const double* bx, const double* by, const double* bz, int S,
     double accept_max, int32_t* counts, int32_t* totals, int64_t* pair_start, uint32_t* pair_bin, int64_t cap,
     unsigned long long* stats) {
@@ -717,9 +702,10 @@ __global__ __launch_bounds__(kNbrThreads) void k_neighbors(
     const int lane = tid % kWave;
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int nseg = S * 27;
-    // the cells of the list, or (no list) every cell
-    for (int64_t w = blockIdx.x; w < cells_total; w += gridDim.x) {
-        const int64_t c = cell_list != nullptr ? static_cast<int64_t>(cell_list[w]) : w;
+    // the cells of the list
+    const int64_t listed = static_cast<int64_t>(*list_count);
+    for (int64_t w = blockIdx.x; w < listed; w += gridDim.x) {
+        const int64_t c = static_cast<int64_t>(cell_list[w]);
         const int64_t c0 = cell_centre_start[c], c1 = cell_centre_start[c + 1];
         if (c0 == c1) continue;
         const StructGeom& g = geom[cell_struct[c]];
@@ -1182,23 +1168,18 @@ void prepare_batch(const mdx_batch_view& batch, const int32_t* species, int n_sp
                   static_cast<int32_t>(s));
     }
     out.images.clear();
-    int64_t ext = 0, cells = 0;
-    // home cells holding centres (global ROI cell indices, ascending per
-    // structure): the cells the search visits
-    std::vector<int32_t> occupied;
-    std::vector<int64_t> homes;
-    std::vector<int64_t> occupied_begin(static_cast<size_t>(batch.structures) + 1, 0);
-    std::vector<int64_t> atom_home(static_cast<size_t>(batch.atoms), 0);
+    out.most_images = 0;
+    out.max_images = 1;
+    out.chunk_bound = 0;
+    int64_t ext = 0;
     for (int64_t s = 0; s < batch.structures; ++s) {
         StructGeom& g = out.geom[static_cast<size_t>(s)];
-        occupied_begin[static_cast<size_t>(s)] = static_cast<int64_t>(occupied.size());
         std::memset(&g, 0, sizeof(g));
         const int64_t begin = batch.offsets[s];
         const int64_t natoms = batch.offsets[s + 1] - begin;
         g.atom_begin = begin;
         g.natoms = static_cast<int32_t>(natoms);
         g.ext_begin = ext;
-        g.cell_begin = cells;
         g.image_begin = static_cast<int64_t>(out.images.size());
         const double* cell = batch.cells + s * 9;
         const bool periodic = batch.pbc[s * 3] == 1;
@@ -1241,172 +1222,31 @@ void prepare_batch(const mdx_batch_view& batch, const int32_t* species, int n_sp
                 }
             }
         }
-        if (natoms == 0) {
-            g.dims[0] = g.dims[1] = g.dims[2] = 1;
-            g.spacing[0] = g.spacing[1] = g.spacing[2] = cutoff;
-            continue;
-        }
-        ext += natoms * n_images;
-        // bounding box of every image (build_grid, neighbor.cpp:143-158); rounding
-        // is monotonic, so min over images of fl(min_j r_j + s) equals the
-        // minimum over all image positions.
+        // the extreme shifts per axis: the frame's bounding box of every image
+        // (build_grid, neighbor.cpp:143-158) is the atoms' box moved by them
         for (int a = 0; a < 3; ++a) {
-            double lo = batch.positions[begin * 3 + a], hi = lo;
-            for (int64_t i = begin; i < begin + natoms; ++i) {
-                lo = std::min(lo, batch.positions[i * 3 + a]);
-                hi = std::max(hi, batch.positions[i * 3 + a]);
-            }
-            double mn = 0.0, mx = 0.0;
+            double lo = 0.0, hi = 0.0;
             for (int64_t q = 0; q < n_images; ++q) {
                 const double sh = out.images[static_cast<size_t>(g.image_begin + q)].shift[a];
-                const double l2 = lo + sh, h2 = hi + sh;
-                if (q == 0 || l2 < mn) mn = l2;
-                if (q == 0 || h2 > mx) mx = h2;
+                if (q == 0 || sh < lo) lo = sh;
+                if (q == 0 || sh > hi) hi = sh;
             }
-            mn -= 1e-10;
-            mx += 1e-10;
-            g.minimum[a] = mn;
-            const double range = mx - mn;
-            const double ncell = range / cutoff;
-            if (!std::isfinite(range) || range < 0.0 || !std::isfinite(ncell) || ncell > 1.0e6) {
-                throw Error(MDX_INVALID_ARGUMENT, "neighbor cell-grid dimension exceeds the device graph capacity");
-            }
-            g.dims[a] = std::max(1, static_cast<int>(ncell));
-            g.spacing[a] = std::max(cutoff, range / g.dims[a]);
+            g.shift_lo[a] = lo;
+            g.shift_hi[a] = hi;
         }
-        // region of interest: cells within one cell of a centre
-        int lo_c[3] = {std::numeric_limits<int>::max(), std::numeric_limits<int>::max(), std::numeric_limits<int>::max()};
-        int hi_c[3] = {-1, -1, -1};
-        for (int64_t i = begin; i < begin + natoms; ++i) {
-            for (int a = 0; a < 3; ++a) {
-                const int c = grid_coordinate(batch.positions[i * 3 + a], g.minimum[a], g.spacing[a], g.dims[a]);
-                lo_c[a] = std::min(lo_c[a], c);
-                hi_c[a] = std::max(hi_c[a], c);
-            }
-        }
-        int64_t volume = 1;
-        for (int a = 0; a < 3; ++a) {
-            g.roi_lo[a] = std::max(0, lo_c[a] - 1);
-            const int hi = std::min(g.dims[a] - 1, hi_c[a] + 1);
-            g.roi_dim[a] = hi - g.roi_lo[a] + 1;
-            volume *= g.roi_dim[a];
-        }
-        // the same cell arithmetic as the device's roi_cell
-        homes.clear();
-        for (int64_t i = begin; i < begin + natoms; ++i) {
-            int64_t local = 0;
-            for (int a = 2; a >= 0; --a) {
-                const int c = grid_coordinate(batch.positions[i * 3 + a], g.minimum[a], g.spacing[a], g.dims[a]);
-                local = local * g.roi_dim[a] + (c - g.roi_lo[a]);
-            }
-            homes.push_back(cells + local);
-            atom_home[static_cast<size_t>(i)] = cells + local;
-        }
-        std::sort(homes.begin(), homes.end());
-        homes.erase(std::unique(homes.begin(), homes.end()), homes.end());
-        for (int64_t c : homes) occupied.push_back(static_cast<int32_t>(c));
-        cells += volume;
-        if (cells > (int64_t(1) << 30)) {
-            throw Error(MDX_INVALID_ARGUMENT, "neighbor cell-grid exceeds the device graph capacity");
-        }
-    }
-    occupied_begin[static_cast<size_t>(batch.structures)] = static_cast<int64_t>(occupied.size());
-    // centres by home cell (a counting sort, atom order inside a cell) and the
-    // structure of every cell
-    out.cell_centre_start.assign(static_cast<size_t>(cells) + 1, 0);
-    for (int64_t i = 0; i < batch.atoms; ++i) ++out.cell_centre_start[static_cast<size_t>(atom_home[static_cast<size_t>(i)]) + 1];
-    for (int64_t c = 0; c < cells; ++c) {
-        out.cell_centre_start[static_cast<size_t>(c) + 1] += out.cell_centre_start[static_cast<size_t>(c)];
-    }
-    out.cell_centres.assign(static_cast<size_t>(batch.atoms), 0);
-    {
-        std::vector<int64_t> next(out.cell_centre_start.begin(), out.cell_centre_start.end() - 1);
-        for (int64_t i = 0; i < batch.atoms; ++i) {
-            out.cell_centres[static_cast<size_t>(next[static_cast<size_t>(atom_home[static_cast<size_t>(i)])]++)] =
-                static_cast<int32_t>(i);
-        }
-    }
-    out.cell_struct.assign(static_cast<size_t>(cells), 0);
-    for (int64_t s = 0; s < batch.structures; ++s) {
-        const int64_t first = out.geom[static_cast<size_t>(s)].cell_begin;
-        const int64_t end = s + 1 < batch.structures ? out.geom[static_cast<size_t>(s) + 1].cell_begin : cells;
-        std::fill(out.cell_struct.begin() + first, out.cell_struct.begin() + end, static_cast<int32_t>(s));
+        out.max_images = std::max(out.max_images, static_cast<int>(n_images));
+        if (natoms == 0) continue;
+        const int64_t images = natoms * n_images;
+        ext += images;
+        out.most_images = std::max(out.most_images, images);
+        out.chunk_bound += (images + kBinChunk - 1) / kBinChunk;
     }
     if (ext >= (int64_t(1) << 32) - 1) {
         throw Error(MDX_INVALID_ARGUMENT, "periodic images exceed the device graph capacity");
     }
     out.ext_total = ext;
-    out.cells_total = cells;
-    // wavefront cells: a one-cell ROI (every image binned into it) holding at
-    // most a wavefront of images; then the other structures' home cells that
-    // hold centres, which whole workgroups search: consecutive workgroups
-    // go to consecutive XCDs, so listing only those cells spreads the search
-    // over the chip (a periodic box's occupied cells can otherwise fall on a
-    // few XCDs: 8 of a water box's 64 ROI cells, on 4 XCDs)
-    out.cell_lists.clear();
-    out.most_images = 0;
-    for (const StructGeom& g : out.geom) {
-        out.most_images = std::max(out.most_images, static_cast<int64_t>(g.natoms) * g.n_images);
-    }
-    auto one_cell = [](const StructGeom& g) {
-        return g.natoms > 0 && g.roi_dim[0] == 1 && g.roi_dim[1] == 1 && g.roi_dim[2] == 1 &&
-               static_cast<int64_t>(g.natoms) * g.n_images <= kWaveCellImages;
-    };
-    out.bin_chunks.clear();
-    out.direct_bins = false;
-    for (int64_t s = 0; s < batch.structures; ++s) {
-        StructGeom& g = out.geom[static_cast<size_t>(s)];
-        g.one_cell = one_cell(g) ? 1 : 0;
-        if (g.one_cell != 0) out.cell_lists.push_back(static_cast<int32_t>(g.cell_begin));
-        const int64_t roi = static_cast<int64_t>(g.roi_dim[0]) * g.roi_dim[1] * g.roi_dim[2];
-        g.lds_bins = g.natoms > 0 && g.one_cell == 0 && roi <= kLdsBinCells ? 1 : 0;
-        if (g.lds_bins != 0) {
-            const int64_t images = static_cast<int64_t>(g.natoms) * g.n_images;
-            for (int64_t first = 0; first < images; first += kBinChunk) {
-                out.bin_chunks.push_back(BinChunk{first, static_cast<int32_t>(s),
-                                                  static_cast<int32_t>(std::min<int64_t>(kBinChunk, images - first))});
-            }
-        } else if (g.natoms > 0) {
-            out.direct_bins = true;
-        }
-    }
-    // structures binned on their own when each fits a wavefront (small) or a
-    // workgroup, the workgroup ones averaging enough images to keep it busy
-    {
-        int64_t images_total = 0, large = 0;
-        bool fits = true;
-        out.struct_list.clear();
-        for (size_t s = 0; s < out.geom.size(); ++s) {
-            const StructGeom& g = out.geom[s];
-            if (g.natoms == 0) continue;
-            const int64_t roi = static_cast<int64_t>(g.roi_dim[0]) * g.roi_dim[1] * g.roi_dim[2];
-            const int64_t images = static_cast<int64_t>(g.natoms) * g.n_images;
-            if (images <= kSmallImages && roi <= kSmallCells) {
-                out.struct_list.push_back(static_cast<int32_t>(s));
-            } else {
-                fits = fits && roi <= kLdsBinCells && images <= kStructImages;
-                images_total += images;
-                ++large;
-            }
-        }
-        out.small_structs = static_cast<int64_t>(out.struct_list.size());
-        for (size_t s = 0; s < out.geom.size() && fits; ++s) {
-            const StructGeom& g = out.geom[s];
-            const int64_t roi = static_cast<int64_t>(g.roi_dim[0]) * g.roi_dim[1] * g.roi_dim[2];
-            const int64_t images = static_cast<int64_t>(g.natoms) * g.n_images;
-            if (g.natoms > 0 && !(images <= kSmallImages && roi <= kSmallCells)) {
-                out.struct_list.push_back(static_cast<int32_t>(s));
-            }
-        }
-        out.struct_bins = fits && !out.struct_list.empty() && images_total >= kStructMinImages * large;
-    }
-    out.wave_cells = static_cast<int64_t>(out.cell_lists.size());
-    for (int64_t s = 0; s < batch.structures; ++s) {
-        const StructGeom& g = out.geom[static_cast<size_t>(s)];
-        if (g.natoms == 0 || g.one_cell != 0) continue;
-        out.cell_lists.insert(out.cell_lists.end(), occupied.begin() + occupied_begin[static_cast<size_t>(s)],
-                              occupied.begin() + occupied_begin[static_cast<size_t>(s) + 1]);
-    }
+    out.cells_total = out.wave_cells = out.big_bound = out.chunks = out.small_structs = out.large_structs = 0;
+    out.direct_bins = out.struct_bins = false;
 }
 
 void upload_batch(hipStream_t stream, const mdx_batch_view& batch, PreparedBatch& pb) {
@@ -1417,36 +1257,7 @@ void upload_batch(hipStream_t stream, const mdx_batch_view& batch, PreparedBatch
     pb.d_geom.reserve(std::max<size_t>(1, pb.geom.size() * sizeof(StructGeom)));
     pb.d_images.reserve(std::max<size_t>(1, pb.images.size() * sizeof(ImageDesc)));
     pb.d_offsets.reserve(pb.offsets.size() * sizeof(int64_t));
-    pb.d_cell_lists.reserve(std::max<size_t>(1, pb.cell_lists.size() * sizeof(int32_t)));
-    pb.d_struct_list.reserve(std::max<size_t>(1, pb.struct_list.size() * sizeof(int32_t)));
-    if (pb.struct_bins) {
-        MDX_HIP(hipMemcpyAsync(pb.d_struct_list.ptr, pb.struct_list.data(), pb.struct_list.size() * sizeof(int32_t),
-                               hipMemcpyHostToDevice, stream));
-    }
-    pb.d_bin_chunks.reserve(std::max<size_t>(1, pb.bin_chunks.size() * sizeof(BinChunk)));
-    pb.d_cell_centre_start.reserve(std::max<size_t>(1, pb.cell_centre_start.size() * sizeof(int64_t)));
-    pb.d_cell_centres.reserve(std::max<size_t>(1, pb.cell_centres.size() * sizeof(int32_t)));
-    pb.d_cell_struct.reserve(std::max<size_t>(1, pb.cell_struct.size() * sizeof(int32_t)));
-    if (!pb.cell_centre_start.empty()) {
-        MDX_HIP(hipMemcpyAsync(pb.d_cell_centre_start.ptr, pb.cell_centre_start.data(),
-                               pb.cell_centre_start.size() * sizeof(int64_t), hipMemcpyHostToDevice, stream));
-    }
-    if (!pb.cell_centres.empty()) {
-        MDX_HIP(hipMemcpyAsync(pb.d_cell_centres.ptr, pb.cell_centres.data(), pb.cell_centres.size() * sizeof(int32_t),
-                               hipMemcpyHostToDevice, stream));
-    }
-    if (!pb.cell_struct.empty()) {
-        MDX_HIP(hipMemcpyAsync(pb.d_cell_struct.ptr, pb.cell_struct.data(), pb.cell_struct.size() * sizeof(int32_t),
-                               hipMemcpyHostToDevice, stream));
-    }
-    if (!pb.bin_chunks.empty()) {
-        MDX_HIP(hipMemcpyAsync(pb.d_bin_chunks.ptr, pb.bin_chunks.data(), pb.bin_chunks.size() * sizeof(BinChunk),
-                               hipMemcpyHostToDevice, stream));
-    }
-    if (!pb.cell_lists.empty()) {
-        MDX_HIP(hipMemcpyAsync(pb.d_cell_lists.ptr, pb.cell_lists.data(), pb.cell_lists.size() * sizeof(int32_t),
-                               hipMemcpyHostToDevice, stream));
-    }
+    size_frame(pb);
     if (atoms > 0) {
         MDX_HIP(hipMemcpyAsync(pb.d_positions.ptr, batch.positions, atoms * 3 * sizeof(double),
                                hipMemcpyHostToDevice, stream));
@@ -1497,23 +1308,27 @@ void reduce_stats(const unsigned long long* st, int64_t atoms, int64_t& rows, in
 
 } // namespace
 
-int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr, const volatile int32_t* cancel,
-                    bool slotted, bool defer_stats) {
+int64_t build_graph(hipStream_t stream, PreparedBatch& pb, DeviceGraph& gr, const volatile int32_t* cancel,
+                    bool slotted, bool defer_stats, bool reuse_frame) {
     gr.stats_pending = false;
     const int S = pb.n_species;
     gr.n_species = S;
     const int64_t atoms = pb.atoms;
-    const int64_t cells = pb.cells_total;
-    const size_t cells1 = static_cast<size_t>(cells + 1);
     gr.pair_start.reserve(static_cast<size_t>(atoms + 1) * sizeof(int64_t));
     gr.slots = 0;
+    // the position-dependent inputs: grid, regions of interest, binning
+    // paths and search lists, on the device (one host round trip)
+    if (!reuse_frame) prepare_frame(stream, pb);
+    const int64_t cells = pb.cells_total;
     if (atoms == 0 || cells == 0) {
         MDX_HIP(hipMemsetAsync(gr.pair_start.ptr, 0, static_cast<size_t>(atoms + 1) * sizeof(int64_t), stream));
         gr.counts.reserve(std::max<size_t>(1, static_cast<size_t>(atoms * S) * sizeof(int32_t)));
         gr.pairs = 0;
         gr.binned = 0;
+        gr.most_rows = gr.row_bound = 0;
         return 0;
     }
+    const size_t cells1 = static_cast<size_t>(cells + 1);
     const StructGeom* geom = pb.d_geom.as<StructGeom>();
     const ImageDesc* images = pb.d_images.as<ImageDesc>();
     const double* pos = pb.d_positions.as<double>();
@@ -1524,12 +1339,13 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     }
 
     // one zero-filled block: search statistics, then the cell counters of
-    // binning (count, fill)
-    const size_t counter_bytes = kStatWords * sizeof(unsigned long long) + 2 * cells1 * sizeof(int32_t);
+    // binning (count, fill) and the centres of each home cell
+    const size_t counter_bytes = kStatWords * sizeof(unsigned long long) + 3 * cells1 * sizeof(int32_t);
     gr.counters.reserve(counter_bytes);
     unsigned long long* stats = gr.counters.as<unsigned long long>();
     int32_t* cell_count = reinterpret_cast<int32_t*>(stats + kStatWords);
     int32_t* cell_fill = cell_count + cells1;
+    int32_t* centre_count = cell_fill + cells1;
     gr.cell_start.reserve(cells1 * sizeof(int64_t));
     gr.cell_runs.reserve(std::max<size_t>(1, static_cast<size_t>(cells) * static_cast<size_t>(S + 1)) *
                          sizeof(int64_t));
@@ -1543,14 +1359,16 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     gr.counts.reserve(static_cast<size_t>(atoms * S) * sizeof(int32_t));
     gr.totals.reserve(static_cast<size_t>(atoms) * sizeof(int32_t));
     MDX_HIP(hipMemsetAsync(gr.counters.ptr, 0, counter_bytes, stream));
+    // the centres grouped by home cell, the structure of every ROI cell (a
+    // rebuild of the same frame keeps the graph's from the first build)
+    if (!reuse_frame) place_centres(stream, pb, gr, centre_count);
 
-    // the centres' home cells and the cells' structures come with the batch
-    // (prepare_batch); bin every periodic image into its ROI cell, sorted by (species, extended index)
+    // bin every periodic image into its ROI cell, sorted by (species, extended index)
     if (pb.struct_bins) {
         // each structure on its own: no scan, sort or run search between kernels
         const int32_t* list = pb.d_struct_list.as<int32_t>();
         const int64_t small = pb.small_structs;
-        const int64_t large = static_cast<int64_t>(pb.struct_list.size()) - small;
+        const int64_t large = pb.large_structs;
         if (small > 0) {
             constexpr int64_t per_block = kBlock / kWave;
             hipLaunchKernelGGL(k_bin_small, dim3(static_cast<unsigned>((small + per_block - 1) / per_block)),
@@ -1567,11 +1385,10 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
                                stats);
         }
     } else {
-        int max_images = 1;
-        for (const StructGeom& sg : pb.geom) max_images = std::max(max_images, static_cast<int>(sg.n_images));
+        const int max_images = pb.max_images;
         const dim3 bin_grid(static_cast<unsigned>(std::min<int64_t>((atoms + kBlock - 1) / kBlock, 1 << 16)),
                             static_cast<unsigned>(std::min(max_images, 65535)));
-        const unsigned chunk_grid = static_cast<unsigned>(pb.bin_chunks.size());
+        const unsigned chunk_grid = static_cast<unsigned>(pb.chunks);
         const BinChunk* chunks = pb.d_bin_chunks.as<BinChunk>();
         const int species_major = S > 1 ? 1 : 0;
         if (pb.direct_bins) {
@@ -1599,7 +1416,7 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
         // a wavefront per cell when cells hold a wavefront of images on average
         const int sort_threads = ext <= static_cast<int64_t>(kWave) * cells ? kWave : kBlock;
         hipLaunchKernelGGL(k_bin_sort, dim3(cell_grid), dim3(sort_threads), 0, stream, geom,
-                           pb.d_cell_struct.as<int32_t>(), images, pos, pb.d_types.as<int32_t>(), gr.cell_start.as<int64_t>(),
+                           gr.cell_struct.as<int32_t>(), images, pos, pb.d_types.as<int32_t>(), gr.cell_start.as<int64_t>(),
                            cells, gr.bin_key.as<uint64_t>(), gr.bin_x.as<double>(), gr.bin_y.as<double>(),
                            gr.bin_z.as<double>(), gr.bin_atom.as<int32_t>(), gr.bin_image.as<int32_t>(),
                            gr.bin_type.as<int32_t>(), stats);
@@ -1612,18 +1429,21 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     // d^2 < c^2 is d^2 <= the largest double below c^2
     const double cutoff2 = pb.cutoff * pb.cutoff;
     const double accept_max = pb.include_boundary ? cutoff2 : std::nextafter(cutoff2, 0.0);
-    // cells searched by whole workgroups: the list after the wavefront cells,
-    // or every cell when there are none
+    // cells searched by whole workgroups: the list after the wavefront
+    // cells, whose length the frame counted on the device (at most
+    // big_bound: workgroups past it return at once)
     const int64_t wave_cells = pb.wave_cells;
     const int32_t* lists = pb.d_cell_lists.as<int32_t>();
-    const int64_t big_cells = static_cast<int64_t>(pb.cell_lists.size()) - wave_cells;
+    const int64_t big_bound = pb.big_bound;
     const int32_t* big_list = lists + wave_cells;
+    const unsigned long long* big_count = reinterpret_cast<const unsigned long long*>(
+        static_cast<const char*>(pb.d_frame.ptr) + pb.frame_summary) + kFrameBigCells;
     auto neighbors = [&](auto mode, int64_t cap) {
-        if (big_cells > 0) {
-            const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(big_cells, 1 << 20));
+        if (big_bound > 0) {
+            const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(big_bound, 1 << 20));
             hipLaunchKernelGGL(k_neighbors<decltype(mode)::value>, dim3(blocks), dim3(kNbrThreads), 0, stream, geom,
-                               pb.d_cell_struct.as<int32_t>(), pos, big_list, big_cells,
-                               pb.d_cell_centre_start.as<int64_t>(), pb.d_cell_centres.as<int32_t>(),
+                               gr.cell_struct.as<int32_t>(), pos, big_list, big_count,
+                               gr.cell_centre_start.as<int64_t>(), pb.d_cell_centres.as<int32_t>(),
                                gr.cell_runs.as<int64_t>(),
                                gr.bin_x.as<double>(), gr.bin_y.as<double>(), gr.bin_z.as<double>(), S, accept_max,
                                gr.counts.as<int32_t>(), gr.totals.as<int32_t>(), gr.pair_start.as<int64_t>(),
@@ -1634,7 +1454,7 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
             const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((wave_cells + per_block - 1) / per_block,
                                                                             1 << 20));
             hipLaunchKernelGGL(k_neighbors_wave<decltype(mode)::value>, dim3(blocks), dim3(kBlock), 0, stream, lists,
-                               wave_cells, pos, pb.d_cell_centre_start.as<int64_t>(), pb.d_cell_centres.as<int32_t>(),
+                               wave_cells, pos, gr.cell_centre_start.as<int64_t>(), pb.d_cell_centres.as<int32_t>(),
                                gr.cell_runs.as<int64_t>(),
                                gr.bin_x.as<double>(), gr.bin_y.as<double>(), gr.bin_z.as<double>(), S, accept_max,
                                gr.counts.as<int32_t>(), gr.totals.as<int32_t>(), gr.pair_start.as<int64_t>(),
@@ -1674,7 +1494,8 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
             gr.read_back.record(stream);
             gr.stats_pending = true;
             gr.slots = cap;
-            gr.most_rows = cap;
+            gr.most_rows = 0;
+            gr.row_bound = cap;
             gr.pairs = -1;
             gr.binned = -1;
             return -1;
@@ -1687,6 +1508,7 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
         reduce_stats(st, atoms, pairs, most);
         const int64_t binned = binned_total(st);
         gr.most_rows = most;
+        gr.row_bound = most;
         if (most <= cap) {
             // slots grown for a denser batch shrink back to what fits this one
             int64_t fit = kMinSlotCap;
@@ -1709,6 +1531,10 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
             gr.pair_bin.ptr = nullptr;
             gr.pair_bin.bytes = 0;
         }
+        // the slotted pass cut the overflowing centres' per-species counts to
+        // their slots: a count pass writes the true ones (the fill pass writes
+        // rows only)
+        neighbors(Count{}, 0);
         scan_counts(stream, gr.totals.as<int32_t>(), gr.pair_start.as<int64_t>(), atoms, gr.scan_tmp);
         gr.pair_bin.reserve(std::max<size_t>(1, static_cast<size_t>(pairs) * sizeof(uint32_t)));
         neighbors(Fill{}, 0);
@@ -1728,6 +1554,7 @@ int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& gr
     const int64_t binned = binned_total(st);
     int64_t counted = 0;
     reduce_stats(st, atoms, counted, gr.most_rows);
+    gr.row_bound = gr.most_rows;
     if (slotted && gr.slot_cap == 0 && gr.most_rows <= kMaxSlotCap) {
         // the slotted layout again once a batch's centres fit a slot
         int64_t fit = kMinSlotCap;
@@ -1753,6 +1580,7 @@ bool complete_graph(const PreparedBatch& pb, DeviceGraph& gr, const volatile int
     if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
     gr.binned = binned_total(st);
     gr.most_rows = most;
+    gr.row_bound = most;
     gr.pairs = pairs;
     const int64_t cap = gr.slots;
     if (most <= cap) {

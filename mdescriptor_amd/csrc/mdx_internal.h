@@ -84,7 +84,30 @@ struct StructGeom {
     int32_t reserved;
     double minimum[3];   // grid origin (bounding box minus padding)
     double spacing[3];   // cell widths
+    // smallest and largest image shift per axis (topology: fixed with the
+    // cell); the bounding box of every image is the atoms' box moved by them
+    double shift_lo[3];
+    double shift_hi[3];
 };
+
+// Binning paths and their limits (kernel 1).  Which path a structure takes
+// depends on its region of interest, so on the positions: the frame kernels
+// classify every structure on the device each time a graph is built.
+constexpr int kLdsBinCells = 2048;     // ROI cells of a structure binned in LDS, at most
+constexpr int kBinChunk = 4096;        // images per LDS binning workgroup
+constexpr int kStructImages = 8192;    // images of a structure binned by one workgroup, at most
+constexpr int kStructMinImages = 1024; // images per such structure, on average, for that path
+constexpr int kSmallImages = kWave;    // images of a structure binned by one wavefront, at most
+constexpr int kSmallCells = 64;        // ... and its ROI cells
+constexpr int kWaveCellImages = kWave; // binned images of a one-cell structure searched by one wavefront
+
+// CellGrid::coordinate (neighbor.cpp:122-132); shared by host and device.
+__host__ __device__ inline int grid_coordinate(double value, double origin, double width, int dim) {
+    const double scaled = (value - origin) / width;
+    if (!(scaled > 0.0)) return 0;
+    if (!__builtin_isfinite(scaled) || scaled >= static_cast<double>(dim)) return dim - 1;
+    return static_cast<int>(scaled);
+}
 
 // A run of one structure's binned images [first, first + count) in extended
 // (image-major) order: the work of one binning workgroup.
@@ -102,62 +125,6 @@ struct ImageDesc {
     int32_t pad;
 };
 
-// Host-side prepared batch: geometry plus device copies of the inputs.
-struct PreparedBatch {
-    int64_t structures = 0;
-    int64_t atoms = 0;
-    int64_t ext_total = 0;   // sum over structures of natoms * n_images
-    int64_t cells_total = 0; // ROI cells over all structures
-    double cutoff = 0.0;
-    int include_boundary = 1;  // d^2 <= cutoff^2 (1) or d^2 < cutoff^2 (0), neighbor.cpp:553-555
-    std::vector<StructGeom> geom;
-    std::vector<ImageDesc> images;
-    std::vector<int32_t> types; // species index per atom (0 when species are ignored)
-    std::vector<int32_t> atom_struct; // structure of each atom
-    std::vector<int64_t> offsets;
-    // work items of the averaged SOAP modes (host copies outlive the async upload)
-    std::vector<int64_t> item_begin, struct_items;
-    int n_species = 1;
-    // ROI cells searched one wavefront per cell (structures whose ROI is one
-    // cell with at most a wavefront of binned images), then the other
-    // structures' home cells holding centres: cell_lists[0, wave_cells) and
-    // [wave_cells, end)
-    std::vector<int32_t> cell_lists;
-    int64_t wave_cells = 0;
-    // most binned images of one structure: no centre has more rows
-    int64_t most_images = 0;
-    // binning work of the structures binned in LDS; whether any other
-    // structure has images (those are binned with global atomics)
-    std::vector<BinChunk> bin_chunks;
-    // centres grouped by home ROI cell (atom order inside a cell): cell c's
-    // centres are cell_centres[cell_centre_start[c], cell_centre_start[c+1]);
-    // the structure of every ROI cell.  Built on the host with the device's
-    // cell arithmetic.
-    std::vector<int64_t> cell_centre_start;
-    std::vector<int32_t> cell_centres, cell_struct;
-    DeviceBuffer d_cell_centre_start, d_cell_centres, d_cell_struct;
-    bool direct_bins = false;
-    // every structure is binned on its own, its bins from its first extended
-    // index: by a wavefront of k_bin_small (at most 64 images and 64 ROI
-    // cells) or a workgroup of k_bin_struct (at most 2,048 ROI cells and 8,192
-    // images; those average 1,024 images or more)
-    bool struct_bins = false;
-    std::vector<int32_t> struct_list; // the k_bin_small structures, then the k_bin_struct ones
-    int64_t small_structs = 0;
-    DeviceBuffer d_struct_list;
-    DeviceBuffer d_bin_chunks; // BinChunk[bin_chunks.size()]
-    DeviceBuffer d_cell_lists; // i32[cell_lists.size()]
-    DeviceBuffer d_positions; // f64[atoms*3]
-    DeviceBuffer d_types;     // i32[atoms]
-    DeviceBuffer d_atom_struct; // i32[atoms]
-    DeviceBuffer d_geom;      // StructGeom[structures]
-    DeviceBuffer d_images;    // ImageDesc[...]
-    DeviceBuffer d_offsets;   // i64[structures+1]
-};
-
-// An event recorded on a stream and polled until the stream reaches it (a
-// lower-latency wait than a blocking stream synchronisation).  Created on
-// first use on the current device; one per owner, not copyable.
 // Page-locked host words for small device-to-host read-backs (a copy into
 // pageable memory goes through a staging buffer synchronously).
 class PinnedWords {
@@ -173,6 +140,9 @@ private:
     size_t count_ = 0;
 };
 
+// An event recorded on a stream and polled until the stream reaches it (a
+// lower-latency wait than a blocking stream synchronisation).  Created on
+// first use on the current device; one per owner, not copyable.
 class StreamPoint {
 public:
     StreamPoint() = default;
@@ -188,18 +158,109 @@ private:
     hipEvent_t event_ = nullptr;
 };
 
+// Words of a frame's summary, read back once per graph build after the frame
+// kernels have classified the structures (frame.hip).
+enum FrameWord {
+    kFrameCells = 0,      // ROI cells of the batch
+    kFrameWaveCells,      // one-cell structures (searched one wavefront each)
+    kFrameChunks,         // LDS binning chunks
+    kFrameSmall,          // structures of at most kSmallImages images and kSmallCells ROI cells
+    kFrameLarge,          // other structures with atoms
+    kFrameLargeFit,       // ... of which fit one binning workgroup
+    kFrameLargeImages,    // images of the large structures
+    kFrameDirect,         // structures with atoms binned with global atomics
+    kFrameBigBound,       // sum over workgroup-searched structures of min(ROI cells, atoms)
+    kFrameStatus,         // error bits (kFrameNonFinite, kFrameGridTooLarge)
+    kFrameBigCells,       // home cells of workgroup-searched structures that hold centres (counted after the read-back)
+    kFrameWords = 16
+};
+constexpr unsigned long long kFrameNonFinite = 1;   // a position is not finite
+constexpr unsigned long long kFrameGridTooLarge = 2; // a grid dimension is not finite or above 1e6 cells
+
+// A structure batch on the device.  Topology (everything fixed by numbers,
+// cells, pbc and offsets) is prepared on the host once per batch; everything
+// that depends on positions (the cell grid, each structure's region of
+// interest and binning path, the centres' home cells and the lists the
+// search walks) is rebuilt on the device by the frame kernels at the start of
+// every graph build (prepare_frame), so a batch whose positions change keeps
+// its topology and only re-runs those kernels.
+struct PreparedBatch {
+    int64_t structures = 0;
+    int64_t atoms = 0;
+    int64_t ext_total = 0;   // sum over structures of natoms * n_images
+    double cutoff = 0.0;
+    int include_boundary = 1;  // d^2 <= cutoff^2 (1) or d^2 < cutoff^2 (0), neighbor.cpp:553-555
+    int n_species = 1;
+    // topology, host copies (uploaded by upload_batch)
+    std::vector<StructGeom> geom; // position-dependent fields zero until a frame fills them on the device
+    std::vector<ImageDesc> images;
+    std::vector<int32_t> types; // species index per atom (0 when species are ignored)
+    std::vector<int32_t> atom_struct; // structure of each atom
+    std::vector<int64_t> offsets;
+    // work items of the averaged SOAP modes (host copies outlive the async upload)
+    std::vector<int64_t> item_begin, struct_items;
+    int64_t most_images = 0;  // most binned images of one structure: no centre has more rows
+    int max_images = 1;       // most periodic images of one structure
+    int64_t chunk_bound = 0;  // LDS binning chunks if every structure took that path
+    // the last frame's summary (prepare_frame)
+    int64_t cells_total = 0;  // ROI cells over all structures
+    int64_t wave_cells = 0;   // one-cell structures: cell_lists[0, wave_cells)
+    int64_t big_bound = 0;    // workgroup-searched home cells, at most: cell_lists[wave_cells, ...)
+    int64_t chunks = 0;       // LDS binning chunks (bin_chunks)
+    int64_t small_structs = 0, large_structs = 0;
+    bool direct_bins = false; // some structure is binned with global atomics (k_bin_atoms)
+    // every structure is binned on its own, its bins from its first extended
+    // index: by a wavefront of k_bin_small (at most 64 images and 64 ROI
+    // cells) or a workgroup of k_bin_struct (at most 2,048 ROI cells and 8,192
+    // images; those average 1,024 images or more)
+    bool struct_bins = false;
+    // device copies of the inputs and topology
+    DeviceBuffer d_positions; // f64[atoms*3]
+    DeviceBuffer d_types;     // i32[atoms]
+    DeviceBuffer d_atom_struct; // i32[atoms]
+    DeviceBuffer d_geom;      // StructGeom[structures]
+    DeviceBuffer d_images;    // ImageDesc[...]
+    DeviceBuffer d_offsets;   // i64[structures+1]
+    // frame arrays, written on the device by the frame kernels (sized by the
+    // topology at upload, so a run allocates none of them):
+    //   frame: u64 box words [structures * 6] (per axis: the largest order
+    //     key of -x, then of x), u32 span words [structures * 6] (per axis: ~
+    //     smallest and largest grid coordinate of a centre), then per
+    //     structure i64 ROI cells, i32 class bits, i32 chunks, then the
+    //     summary words [kFrameWords]; zero-filled at the start of a frame
+    DeviceBuffer d_frame;
+    size_t frame_bytes = 0, frame_span = 0, frame_vol = 0, frame_cls = 0, frame_nch = 0, frame_summary = 0;
+    DeviceBuffer d_struct_cells; // i64[structures + 1]: first ROI cell of each structure, then the total
+    DeviceBuffer d_cell_lists;   // i32[structures + atoms]: one-cell structures' cells, then searched home cells
+    DeviceBuffer d_struct_list;  // i32[structures]: the k_bin_small structures, then the k_bin_struct ones
+    DeviceBuffer d_bin_chunks;   // BinChunk[chunk_bound]
+    DeviceBuffer d_cell_centres; // i32[atoms]: centres grouped by home cell
+    DeviceBuffer d_atom_cell;    // u64[atoms]: grid coordinates of each centre (x | y << 21 | z << 42)
+    DeviceBuffer d_atom_home;    // i32[atoms]: home ROI cell
+    DeviceBuffer d_atom_rank;    // i32[atoms]: place among its home cell's centres
+    PinnedWords frame_host;      // the summary, read back
+    StreamPoint frame_read;
+};
+
 // Device graph (kernel 1 output).  Pairs are indices into the cell-sorted
 // binned image arrays; rows are grouped by neighbour species when
 // n_species > 1 and keep the reference's candidate order inside a species.
 struct DeviceGraph {
     int64_t binned = 0;
     int64_t pairs = 0;
-    int64_t most_rows = 0;   // largest row count of one centre
+    int64_t most_rows = 0;   // largest row count of one centre (valid once the statistics are read)
+    int64_t row_bound = 0;   // no centre has more rows in the current layout: the slot width while
+                             // the statistics are pending, else most_rows (what consumers may read
+                             // before complete_graph)
     bool stats_pending = false; // a deferred slotted build whose statistics are not read yet
     int n_species = 1;
     DeviceBuffer counters;   // zero-filled per build: u64 statistics[kStatWords], then i32 cell
-                             // counts of binning (count, fill), [cells + 1] each
+                             // counts of binning (count, fill) and the centres of each home
+                             // cell, [cells + 1] each
     DeviceBuffer cell_start; // i64[cells + 1] first bin of each ROI cell
+    DeviceBuffer cell_centre_start; // i64[cells + 1]: cell c's centres are the batch's
+                                    // cell_centres[cell_centre_start[c], cell_centre_start[c + 1])
+    DeviceBuffer cell_struct;       // i32[cells]: structure of each ROI cell
     DeviceBuffer bin_key;                           // unsorted u64 keys, (species << 32) | extended index
     DeviceBuffer cell_runs;  // i64[cells * (n_species + 1)]: first bin of each species in a cell, then its end
     DeviceBuffer bin_x, bin_y, bin_z;               // f64 positions of binned images (sorted)
@@ -218,7 +279,8 @@ struct DeviceGraph {
     DeviceBuffer scan_tmp;   // block sums of the scans
 
     template <typename F> void for_each_buffer(F f) {
-        for (DeviceBuffer* b : {&counters, &cell_start, &bin_key, &cell_runs, &bin_x, &bin_y, &bin_z,
+        for (DeviceBuffer* b : {&counters, &cell_start, &cell_centre_start, &cell_struct, &bin_key, &cell_runs,
+                                &bin_x, &bin_y, &bin_z,
                                 &bin_atom, &bin_image, &bin_type, &counts, &totals, &pair_start, &pair_bin,
                                 &scan_tmp}) {
             f(*b);
@@ -249,8 +311,11 @@ __host__ __device__ constexpr int stat_binned(int lane) { return kStatLineWords 
 constexpr int64_t kMinSlotCap = 512;
 constexpr int64_t kMaxSlotCap = 8192;
 constexpr int64_t kMaxSlottedBytes = int64_t(4) << 30;
-int64_t build_graph(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& graph,
-                    const volatile int32_t* cancel, bool slotted = false, bool defer_stats = false);
+// The frame runs first (prepare_frame) unless reuse_frame: a rebuild of the
+// same positions after a slot overflow.
+int64_t build_graph(hipStream_t stream, PreparedBatch& pb, DeviceGraph& graph,
+                    const volatile int32_t* cancel, bool slotted = false, bool defer_stats = false,
+                    bool reuse_frame = false);
 // With defer_stats a slotted build returns (-1) before its statistics are
 // read: the caller may queue the graph's consumer at once, then calls
 // complete_graph, which reads them.  false: a centre overflowed its slot (the
@@ -268,11 +333,27 @@ size_t device_workgroup_lds();
 // Exclusive scan of n int32 counts into n+1 int64 offsets (out[n] = total).
 void scan_counts(hipStream_t stream, const int32_t* in, int64_t* out, int64_t n, DeviceBuffer& tmp);
 
-// Prepare a batch on the host (validation, species map, image tables, grid
-// geometry) for cutoff; species may be null (all atoms one species).
+// Prepare a batch's topology on the host (validation, species map, image
+// tables, per-structure extents) for cutoff; species may be null (all atoms
+// one species).  Nothing here depends on positions beyond their validation.
 void prepare_batch(const mdx_batch_view& batch, const int32_t* species, int n_species, double cutoff,
                    PreparedBatch& out);
+// Upload the topology and the positions, and size the frame arrays.
 void upload_batch(hipStream_t stream, const mdx_batch_view& batch, PreparedBatch& pb);
+
+// The frame (frame.hip): from the positions on the device, each structure's
+// cell grid (bounding box of its images, dimensions, spacing), region of
+// interest and binning path, written into d_geom; the lists of the binning
+// and search kernels; the summary, read back into pb (one host round trip);
+// then, into the graph, the centres grouped by home cell and the structure of
+// every ROI cell.  The first half (prepare_frame) runs before the graph's
+// counters are sized and cleared, the second (place_centres) after.
+// Throws MDX_INVALID_ARGUMENT for non-finite positions or a grid beyond the
+// device graph's capacity, with the messages of prepare_batch's checks.
+void prepare_frame(hipStream_t stream, PreparedBatch& pb);
+// Size the frame arrays of a batch from its topology (upload_batch).
+void size_frame(PreparedBatch& pb);
+void place_centres(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& graph, int32_t* centre_count);
 
 // NeighborList descriptor over a one-species device graph (neighbor_list.hip).
 struct NeighborListState {

@@ -375,7 +375,7 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
     // forms from the structure's centres directly) and every centre's rows
     // fit their slot codes
     const bool block = p.block_waves > 0 && (p.average == 0 || (p.average == 1 && p.weighted == 0 && p.compression == 0)) &&
-                       g.most_rows < kQuadMaxRows;
+                       g.row_bound < kQuadMaxRows;
     const bool block_inner = block && p.average == 1;
     int64_t largest_structure = 0;
     for (size_t st = 0; st + 1 < pb.offsets.size(); ++st) {
@@ -427,7 +427,7 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
     int64_t launches = 0;
     if (block || p.use_mfma) {
         // else the 4x4-block kernel where the plan chose it
-        const bool quad = !block && p.quad_waves > 0 && g.most_rows < kQuadMaxRows;
+        const bool quad = !block && p.quad_waves > 0 && g.row_bound < kQuadMaxRows;
         MfmaDims md{};
         md.S = p.S;
         md.n = p.n;

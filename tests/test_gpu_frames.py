@@ -1,0 +1,318 @@
+"""New frames of a device-resident batch, the large-structure binning path and
+slot overflows, against the CPU oracle through the C-ABI.
+
+Everything of the neighbour search that depends on positions (cell grid,
+regions of interest, binning path of each structure, home cells, search
+lists) is rebuilt on the device at the start of every graph build.  These
+tests move the atoms of a resident batch (``mdx_hip_batch_set_positions``,
+from host and from device memory), including moves that change a structure's
+binning path, and require the rows of the next run to match the oracle on the
+new positions, the pair count to equal the oracle graph's, and the rows to
+equal a fresh ``mdx_hip_soap_compute`` on the same positions bit for bit.
+
+Structures with more than 2,048 ROI cells are binned by image-level atomics
+(``k_bin_atoms``) and sorted per cell; a sparse box and a 64,000-atom liquid
+silicon cell take that path, and their graph, SOAP rows and NeighborList
+table must equal the oracle's.
+
+A centre with more rows than its slot makes the run build the graph again
+(mdx_hip_soap_run, plan compute) or lay it out compactly in place
+(mdx_hip_soap_run_noalloc): every averaging mode, a weighted and an mu1nu1
+plan are checked on the call that overflows.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+
+from conftest import SOAP_PAD, edge_batch, scaled_error
+from mdescriptor_amd import _hip, workloads
+from mdescriptor_amd.descriptors.basis import basis_gto
+
+pytestmark = pytest.mark.gpu
+
+F64_GATE = 1e-10
+F32_GATE = 2e-5
+
+
+def _plan(ctx, params, average, dtype, options=None):
+    alphas, betas = basis_gto(params["r_cut"], params["n_max"], params["l_max"])
+    plan = _hip.SoapPlan(ctx, species=params["species"], n_max=params["n_max"], l_max=params["l_max"],
+                         r_cut=params["r_cut"], sigma=1.0, alphas=alphas, betas=betas, average=average, dtype=dtype,
+                         options=options)
+    return plan, (alphas, betas)
+
+
+def _oracle_soap(oracle, batch, params, basis, average, options=None):
+    return oracle.soap(batch, species=params["species"], n_max=params["n_max"], l_max=params["l_max"],
+                       r_cut=params["r_cut"], sigma=1.0, alphas=basis[0], betas=basis[1], average=average,
+                       options=options, num_threads=0)
+
+
+def _moved(batch, positions):
+    return SimpleNamespace(numbers=batch.numbers, positions=np.asarray(positions, np.float64), cells=batch.cells,
+                           pbc=batch.pbc, offsets=batch.offsets)
+
+
+def _gate(dtype):
+    return F64_GATE if dtype == "float64" else F32_GATE
+
+
+def _frames(batch, seed):
+    """Three new frames: a small jitter, a larger one, and every structure
+    stretched about its first atom by 1.6 (molecules outgrow one cell, boxes
+    reach more cells: binning paths change)."""
+
+    rng = np.random.default_rng(seed)
+    base = np.asarray(batch.positions, np.float64)
+    stretched = base.copy()
+    offsets = np.asarray(batch.offsets)
+    for s in range(len(offsets) - 1):
+        a, b = int(offsets[s]), int(offsets[s + 1])
+        if b > a:
+            stretched[a:b] = base[a] + 1.6 * (base[a:b] - base[a])
+    return [base + rng.normal(0.0, 0.05, base.shape), base + rng.normal(0.0, 0.4, base.shape), stretched]
+
+
+class _Resident:
+    """A device batch and its output buffer."""
+
+    def __init__(self, plan, batch):
+        self.plan = plan
+        self.batch = _hip.DeviceBatch(plan, batch)
+        self.pitch = plan.features * plan.dtype.itemsize
+        self.out = _hip.DeviceMemory(max(1, self.batch.rows * self.pitch))
+
+    def run(self, entry="mdx_hip_soap_run"):
+        ctx = self.plan.context
+        timing = _hip.Timing()
+        ctx.check(getattr(ctx.lib, entry)(ctx.handle, self.plan.handle, self.batch.handle,
+                                          ctypes.c_void_p(self.out.address), self.pitch, None, ctypes.byref(timing)))
+        rows = self.out.to_host(np.empty((self.batch.rows, self.plan.features), self.plan.dtype))
+        return rows, timing.as_dict()
+
+    def close(self):
+        self.out.free()
+        self.batch.close()
+
+
+def _frame_batches():
+    cases = []
+    for index in (1, 2, 3):
+        work = workloads.config(index, "small")
+        cases.append((f"config{index}", work.batch, work.params))
+    edge = edge_batch()
+    cases.append(("edge", edge, {"species": [1, 6, 8], "n_max": 4, "l_max": 4, "r_cut": 3.5}))
+    return cases
+
+
+FRAME_CASES = _frame_batches()
+
+
+@pytest.mark.parametrize("case", range(len(FRAME_CASES)), ids=[c[0] for c in FRAME_CASES])
+@pytest.mark.parametrize("average,dtype", [("off", "float64"), ("inner", "float64"), ("off", "float32")])
+def test_new_frames_match_oracle(hip_context, oracle, case, average, dtype):
+    name, batch, params = FRAME_CASES[case]
+    plan, basis = _plan(hip_context, params, average, dtype)
+    resident = _Resident(plan, batch)
+    device_positions = None
+    try:
+        first, _ = resident.run()
+        expected = _oracle_soap(oracle, batch, params, basis, average)
+        assert scaled_error(first, expected) <= _gate(dtype)
+        for k, positions in enumerate(_frames(batch, 31 + case)):
+            print(f"{name} {average} {dtype}: frame {k}", flush=True)
+            moved = _moved(batch, positions)
+            if k == 1:
+                # device-memory positions: copied on the context's stream
+                device_positions = _hip.DeviceMemory(positions.nbytes).from_host(positions)
+                resident.batch.set_positions(device_positions.address)
+            else:
+                resident.batch.set_positions(positions)
+            rows, timing = resident.run()
+            expected = _oracle_soap(oracle, moved, params, basis, average)
+            assert rows.shape == expected.shape
+            error = scaled_error(rows, expected)
+            assert error <= _gate(dtype), f"{name} frame {k}: scaled error {error:.3e}"
+            graph = oracle.graph(moved, params["r_cut"] + SOAP_PAD)
+            assert timing["pairs"] == len(graph["atoms"])
+            fresh, _ = plan.compute(moved)
+            np.testing.assert_array_equal(rows, fresh)
+            if device_positions is not None:
+                device_positions.free()
+                device_positions = None
+    finally:
+        resident.close()
+        plan.close()
+
+
+def test_frames_alternate_between_binning_paths(hip_context, oracle):
+    """Molecules that fit one cell, then spread over many (the per-molecule
+    wavefront binning and one-cell search give way to the multi-kernel
+    binning and workgroup search), then back."""
+
+    work = workloads.config(3, "small")
+    params = work.params
+    plan, basis = _plan(hip_context, params, "inner", "float64")
+    resident = _Resident(plan, work.batch)
+    base = np.asarray(work.batch.positions, np.float64)
+    try:
+        for k, scale in enumerate((1.0, 6.0, 1.0, 3.0)):
+            positions = base * scale
+            resident.batch.set_positions(positions)
+            rows, timing = resident.run()
+            moved = _moved(work.batch, positions)
+            expected = _oracle_soap(oracle, moved, params, basis, "inner")
+            assert scaled_error(rows, expected) <= F64_GATE, f"frame {k} (scale {scale})"
+            assert timing["pairs"] == len(oracle.graph(moved, params["r_cut"] + SOAP_PAD)["atoms"])
+    finally:
+        resident.close()
+        plan.close()
+
+
+def test_non_finite_positions_are_rejected(hip_context):
+    work = workloads.config(2, "small")
+    plan, _ = _plan(hip_context, work.params, "off", "float64")
+    resident = _Resident(plan, work.batch)
+    try:
+        good, _ = resident.run()
+        bad = np.array(work.batch.positions, np.float64)
+        bad[17, 1] = np.nan
+        with pytest.raises(ValueError, match="positions must be finite"):
+            resident.batch.set_positions(bad)
+        memory = _hip.DeviceMemory(bad.nbytes).from_host(bad)
+        resident.batch.set_positions(memory.address)
+        with pytest.raises(ValueError, match="positions must be finite"):
+            resident.run()
+        memory.free()
+        resident.batch.set_positions(np.asarray(work.batch.positions, np.float64))
+        again, _ = resident.run()
+        np.testing.assert_array_equal(again, good)
+    finally:
+        resident.close()
+        plan.close()
+
+
+def _roi_cells(batch, cutoff):
+    """ROI cells of each structure by the reference's grid (build_grid,
+    neighbor.cpp:135-194): to confirm which binning path a test reaches."""
+
+    out = []
+    offsets = np.asarray(batch.offsets)
+    for s in range(len(offsets) - 1):
+        pos = np.asarray(batch.positions[offsets[s]:offsets[s + 1]], np.float64)
+        cell = np.asarray(batch.cells[s], np.float64)
+        if np.all(np.asarray(batch.pbc[s]) == 1):
+            inv = np.linalg.inv(cell)
+            b = np.floor(cutoff * np.linalg.norm(inv, axis=0) + 1.0).astype(int)
+            shifts = np.array([[i, j, k] for i in range(-b[0], b[0] + 1) for j in range(-b[1], b[1] + 1)
+                               for k in range(-b[2], b[2] + 1)], np.float64) @ cell
+        else:
+            shifts = np.zeros((1, 3))
+        lo = pos.min(axis=0) + shifts.min(axis=0) - 1e-10
+        hi = pos.max(axis=0) + shifts.max(axis=0) + 1e-10
+        dims = np.maximum(1, ((hi - lo) / cutoff).astype(int))
+        spacing = np.maximum(cutoff, (hi - lo) / dims)
+        c = np.clip(((pos - lo) / spacing).astype(int), 0, dims - 1)
+        roi = np.minimum(dims - 1, c.max(axis=0) + 1) - np.maximum(0, c.min(axis=0) - 1) + 1
+        out.append(int(np.prod(roi)))
+    return out
+
+
+def _sparse_box():
+    rng = np.random.default_rng(2024)
+    atoms, length = 2000, 120.0
+    return SimpleNamespace(numbers=rng.choice([1, 6, 8], size=atoms).astype(np.int32),
+                           positions=rng.uniform(0.0, length, (atoms, 3)), cells=np.eye(3)[None] * length,
+                           pbc=np.ones((1, 3), np.int32), offsets=np.array([0, atoms], np.int64))
+
+
+LARGE_CASES = {
+    "sparse-box": (_sparse_box, {"species": [1, 6, 8], "n_max": 4, "l_max": 4, "r_cut": 3.0}),
+    "liquid-si-64000": (lambda: workloads.liquid_si(20).batch,
+                        {"species": [14], "n_max": 12, "l_max": 9, "r_cut": 5.5}),
+}
+
+
+@pytest.mark.parametrize("name", sorted(LARGE_CASES))
+def test_large_structure_binning_matches_oracle(hip_context, oracle, name):
+    make, params = LARGE_CASES[name]
+    batch = make()
+    cutoff = params["r_cut"] + SOAP_PAD
+    assert max(_roi_cells(batch, cutoff)) > 2048  # the image-atomics binning path
+    print(f"{name}: {batch.offsets[-1]} atoms, ROI cells {_roi_cells(batch, cutoff)}", flush=True)
+    ours = _hip.neighbor_graph(hip_context, batch, cutoff)
+    theirs = oracle.graph(batch, cutoff)
+    for key in theirs:
+        np.testing.assert_array_equal(ours[key], theirs[key], err_msg=f"{name}: {key}")
+    del ours, theirs
+    for dtype in ("float64", "float32"):
+        plan, basis = _plan(hip_context, params, "off", dtype)
+        try:
+            values, _ = plan.compute(batch)
+        finally:
+            plan.close()
+        expected = _oracle_soap(oracle, batch, params, basis, "off")
+        error = scaled_error(values, expected)
+        assert error <= _gate(dtype), f"{name} {dtype}: scaled error {error:.3e}"
+    list_cutoff = params["r_cut"]
+    listed = _hip.neighbor_list(hip_context, batch, list_cutoff, full_neighbor_list=True, table=True)
+    table, offsets = oracle.neighbor_list(batch, list_cutoff, full_neighbor_list=True, self_pairs=False)
+    np.testing.assert_array_equal(listed["offsets"], offsets)
+    np.testing.assert_array_equal(listed["table"], table)
+
+
+def _dense_cluster():
+    rng = np.random.default_rng(7)
+    atoms = 640
+    return SimpleNamespace(numbers=np.where(np.arange(atoms) % 3 == 0, 8, 1).astype(np.int32),
+                           positions=rng.uniform(0.0, 3.5, (atoms, 3)), cells=np.zeros((1, 3, 3)),
+                           pbc=np.zeros((1, 3), np.int32), offsets=np.array([0, atoms]))
+
+
+def _two_dense_clusters():
+    one = _dense_cluster()
+    return SimpleNamespace(numbers=np.concatenate([one.numbers, one.numbers]),
+                           positions=np.concatenate([one.positions, one.positions[::-1] + 40.0]),
+                           cells=np.zeros((2, 3, 3)), pbc=np.zeros((2, 3), np.int32),
+                           offsets=np.array([0, 640, 1280]))
+
+
+OVERFLOW_PLANS = {
+    "default": None,
+    "weighted": {"weighting": {"function": "pow", "r0": 2.0, "c": 2.0, "d": 1.0, "m": 3.0, "w0": 0.5}},
+    "mu1nu1": {"compression": "mu1nu1"},
+}
+OVERFLOW_PARAMS = {"species": [1, 8], "n_max": 3, "l_max": 2, "r_cut": 3.0}
+
+
+@pytest.mark.parametrize("options", sorted(OVERFLOW_PLANS))
+@pytest.mark.parametrize("average", ["off", "inner", "outer"])
+@pytest.mark.parametrize("entry", ["compute", "mdx_hip_soap_run"])
+def test_slot_overflow_on_the_first_call(hip_context, oracle, options, average, entry):
+    """Every centre of these clusters has more than 512 rows, so the first
+    call on a fresh plan and batch overflows its slots and runs the graph and
+    the expansion again; its rows must match the oracle."""
+
+    batch = _two_dense_clusters()
+    opts = OVERFLOW_PLANS[options]
+    plan, basis = _plan(hip_context, OVERFLOW_PARAMS, average, "float64", opts)
+    try:
+        if entry == "compute":
+            rows, timing = plan.compute(batch)
+        else:
+            resident = _Resident(plan, batch)
+            try:
+                rows, timing = resident.run()
+            finally:
+                resident.close()
+        assert timing["pairs"] > 512 * 1280
+        expected = _oracle_soap(oracle, batch, OVERFLOW_PARAMS, basis, average, opts)
+        error = scaled_error(rows, expected)
+        assert error <= F64_GATE, f"{options} {average} {entry}: scaled error {error:.3e}"
+    finally:
+        plan.close()

@@ -182,3 +182,29 @@ def test_noalloc_refuses_batches_beyond_the_array(context):
         np.testing.assert_array_equal(rows, expected)
     finally:
         plan.close()
+
+
+def test_noalloc_slot_overflow_matches_device_run(context):
+    """A dense cluster whose every centre has more rows than the static
+    graph's first slot width: the no-allocation run lays the overflowing
+    batch out compactly in place (counting the true per-species rows again),
+    and its rows equal mdx_hip_soap_run's on both calls (the second with the
+    wider slot the first left behind) and on a smaller batch after them."""
+
+    rng = np.random.default_rng(7)
+    atoms = 640
+    dense = SimpleNamespace(numbers=np.where(np.arange(atoms) % 3 == 0, 8, 1).astype(np.int32),
+                            positions=rng.uniform(0.0, 3.5, (atoms, 3)), cells=np.zeros((1, 3, 3)),
+                            pbc=np.zeros((1, 3), np.int32), offsets=np.array([0, atoms], np.int64))
+    params = {"species": [1, 8], "n_max": 3, "l_max": 2, "r_cut": 3.0}
+    for average in ("off", "inner"):
+        plan = _plan(context, params, average, "float64")
+        try:
+            for batch in (dense, dense, _smaller(dense)):
+                print(f"dense cluster {average}: {len(batch.numbers)} atoms", flush=True)
+                expected, reference = _run(context, plan, batch, "mdx_hip_soap_run")
+                rows, timing = _run(context, plan, batch, "mdx_hip_soap_run_noalloc")
+                assert timing.pairs == reference.pairs
+                np.testing.assert_array_equal(rows, expected)
+        finally:
+            plan.close()
