@@ -1,14 +1,21 @@
 #!/usr/bin/env python
 """SOAP atom-environments per second on one MI355X (benchmark configuration 2).
 
-One step is one pass of the hot path over the batch resident in HBM:
-neighbour graph (kernel 1) + per-centre expansion, power spectrum and float32
-write (kernels 2-4), exactly what ``mdx_hip_soap_run`` does.  Inputs are
-uploaded once before timing; the output stays on the device.
+One step is one pass of the hot path over a new frame of the batch resident
+in HBM: the frame's positions (``mdx_hip_batch_set_positions`` from one of
+four frames uploaded before timing, a device-to-device copy), then
+``mdx_hip_soap_run``: everything of the neighbour search that depends on
+positions (cell grid, regions of interest, binning paths, home cells, search
+lists, built on the device), the neighbour graph (kernel 1) and the
+per-centre expansion, power spectrum and float32 write (kernels 2-4).  The
+frames are the seeded configuration jittered by 0.02 A (Gaussian, per
+coordinate), a different frame every step; the output stays on the device.
 
 Prints one JSON line with the metric of BASELINE.json, a ``roofline`` object
-for the dominant kernel (the expansion kernel, FP64: its algorithmic flops
-per launch over its launch time from HIP events on the library's stream;
+for the dominant kernel (the expansion kernel; bound by FP64 or HBM,
+whichever roofline time of the configuration is longer: algorithmic FP64
+flops, or algorithmic bytes (output plus 28 B of numbers and positions per
+atom), per launch over its launch time from HIP events on the library's stream;
 ``profile_launch_ms`` is the same kernel's average in the committed rocprofv3
 kernel-trace summary ``profiles/<kernel>_<workload>_kernel_trace.md``, for a
 cross-check) and a ``cpu_baseline`` object: the reference's own C++ SOAP
@@ -91,6 +98,33 @@ def algorithmic_flops(envs: int, rows: int, kbar: float, S: int, n: int, l_max: 
     return envs * 2.0 * kbar * n * H + rows * (2.0 * sc * n * n * H + features / L * 2.0 * H)
 
 
+def algorithmic_bytes(envs: int, rows: int, features: int, itemsize: int) -> float:
+    """Algorithmic HBM bytes of one pass: every output value written once,
+    numbers and positions (28 B) of every atom read once."""
+
+    return rows * features * itemsize + 28.0 * envs
+
+
+def roofline_bound(flops: float, nbytes: float) -> str:
+    """The configuration's bound: FP64 ("mfma") or HBM ("hbm"), whichever
+    roofline time is longer (T_roof = max(flops / FP64 peak, bytes / HBM peak))."""
+
+    return "mfma" if flops / (FP64_PEAK_TFLOPS * 1e12) >= nbytes / (HBM_PEAK_GBS * 1e9) else "hbm"
+
+
+FRAMES = 4
+FRAME_JITTER = 0.02
+
+
+def frame_positions(batch, count: int) -> list[np.ndarray]:
+    """`count` frames of the batch: its positions plus seeded Gaussian noise of
+    FRAME_JITTER angstrom per coordinate (frame 0 included)."""
+
+    rng = np.random.Generator(np.random.PCG64(20261202))
+    base = np.ascontiguousarray(batch.positions, dtype=np.float64).reshape(-1, 3)
+    return [np.ascontiguousarray(base + rng.normal(0.0, FRAME_JITTER, base.shape)) for _ in range(count)]
+
+
 def profile_average_us(workload_name: str, kernel: str) -> tuple[float | None, str | None]:
     """Average duration of `kernel` in the committed rocprofv3 kernel-trace
     summary of this workload (the ``| name | calls | average us |`` table)."""
@@ -164,7 +198,10 @@ def peaks() -> dict:
     for which, name, size, repeats, unit, scale, published in (
             (0, "fp64_valu_fma", 0, 10, "TFLOP/s", 1e12, FP64_PEAK_TFLOPS),
             (1, "fp64_mfma_16x16x4", 0, 10, "TFLOP/s", 1e12, FP64_PEAK_TFLOPS),
-            (2, "hbm_copy", 1 << 30, 20, "GB/s", 1e9, HBM_PEAK_GBS)):
+            (2, "hbm_copy", 1 << 30, 20, "GB/s", 1e9, HBM_PEAK_GBS),
+            (3, "hbm_copy_stream", 4 << 30, 20, "GB/s", 1e9, HBM_PEAK_GBS),
+            (4, "hbm_read_stream", 4 << 30, 20, "GB/s", 1e9, HBM_PEAK_GBS),
+            (5, "hbm_write_stream", 4 << 30, 20, "GB/s", 1e9, HBM_PEAK_GBS)):
         seconds, work = ctypes.c_double(), ctypes.c_double()
         rc = lib.mdx_peak_run(which, size, repeats, ctypes.byref(seconds), ctypes.byref(work))
         if rc != 0:
@@ -396,16 +433,24 @@ def soap_bench(args, workload) -> dict:
     itemsize = np.dtype(p["dtype"]).itemsize
     pitch = plan.features * itemsize
     out = _hip.DeviceMemory(dbatch.rows * pitch)
+    frames = frame_positions(batch, FRAMES)
+    on_device = [_hip.DeviceMemory(f.nbytes).from_host(f) for f in frames]
 
-    for _ in range(args.warmup):
-        dbatch.run(out.address, pitch)
+    def step(k: int) -> dict:
+        dbatch.set_positions(on_device[k % FRAMES].address)
+        return dbatch.run(out.address, pitch)
+
+    for k in range(args.warmup):
+        step(k)
     _hip.DeviceMemory.synchronize()
     timings = []
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        timings.append(dbatch.run(out.address, pitch))
+    for k in range(args.steps):
+        timings.append(step(args.warmup + k))
     _hip.DeviceMemory.synchronize()
     elapsed = time.perf_counter() - t0
+    for memory in on_device:
+        memory.free()
 
     envs = batch.atoms
     ms_per_step = 1e3 * elapsed / args.steps
@@ -420,7 +465,15 @@ def soap_bench(args, workload) -> dict:
     launches = max(1, int(timings[-1]["expansion_launches"]))
     flops_launch = total_flops / launches
     launch_ms = statistics.mean(t["expansion_ms"] for t in timings) / launches
-    achieved = flops_launch / (launch_ms * 1e-3) / 1e12
+    total_bytes = algorithmic_bytes(envs, rows, plan.features, itemsize)
+    bytes_launch = total_bytes / launches
+    bound = roofline_bound(total_flops, total_bytes)
+    if bound == "mfma":
+        achieved = flops_launch / (launch_ms * 1e-3) / 1e12
+        peak, unit = FP64_PEAK_TFLOPS, "TFLOP/s"
+    else:
+        achieved = bytes_launch / (launch_ms * 1e-3) / 1e9
+        peak, unit = HBM_PEAK_GBS, "GB/s"
     tiles = int(timings[-1]["expansion_tiles"])
     if tiles <= -1000:
         family = "k_soap_block"
@@ -466,19 +519,24 @@ def soap_bench(args, workload) -> dict:
             "parallelism": "single-gpu",
         },
         "roofline": {
-            "bound": "mfma",
+            "bound": bound,
             "achieved": achieved,
-            "peak": FP64_PEAK_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": achieved / FP64_PEAK_TFLOPS,
+            "peak": peak,
+            "unit": unit,
+            "frac": achieved / peak,
             "traffic": traffic,
             "kernel": kernel,
             "flops_per_launch": flops_launch,
+            "bytes_per_launch": bytes_launch,
+            "fp64_frac": flops_launch / (launch_ms * 1e-3) / 1e12 / FP64_PEAK_TFLOPS,
+            "hbm_frac": bytes_launch / (launch_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "roofline_ms": 1e3 * max(total_flops / (FP64_PEAK_TFLOPS * 1e12), total_bytes / (HBM_PEAK_GBS * 1e9)),
             "launch_ms": launch_ms,
             "traffic_source": traffic_source,
             "profile_launch_ms": None if profile_us is None else profile_us * 1e-3,
             "profile_source": profile_source,
         },
+        "frames": f"{FRAMES} frames (seeded positions + N(0, {FRAME_JITTER} A) per coordinate), a new one each step",
         "breakdown": {
             "graph_ms": statistics.mean(t["graph_ms"] for t in timings),
             "expansion_ms": statistics.mean(t["expansion_ms"] for t in timings),

@@ -316,14 +316,30 @@ __global__ void k_bin_atoms(const StructGeom* geom, const ImageDesc* images, con
 constexpr int kBinThreads = 512;
 constexpr int kBinPer = kBinChunk / kBinThreads;
 
+// The chunk of workgroup b: structure s is the last whose first chunk
+// (struct_chunks, a scan of every structure's chunk count) is at or before
+// b (structures without chunks share their successor's first chunk).
+__device__ inline BinChunk bin_chunk(const int64_t* struct_chunks, int64_t structures, const StructGeom* geom,
+                                     int64_t b) {
+    int64_t lo = 0, hi = structures;
+    while (hi - lo > 1) {
+        const int64_t mid = (lo + hi) / 2;
+        if (struct_chunks[mid] <= b) lo = mid; else hi = mid;
+    }
+    const int64_t first = (b - struct_chunks[lo]) * kBinChunk;
+    const int64_t images = static_cast<int64_t>(geom[lo].natoms) * geom[lo].n_images;
+    return BinChunk{first, static_cast<int32_t>(lo), static_cast<int32_t>(min<int64_t>(kBinChunk, images - first))};
+}
+
 template <bool kFill>
-__global__ __launch_bounds__(kBinThreads) void k_bin_lds(const BinChunk* chunks, const StructGeom* geom,
+__global__ __launch_bounds__(kBinThreads) void k_bin_lds(const int64_t* struct_chunks, int64_t structures,
+                                                         const StructGeom* geom,
                                                          const ImageDesc* images, const double* positions,
                                                          const int32_t* types, int species_major, int32_t* cell_count,
                                                          const int64_t* cell_start, uint64_t* keys) {
     __shared__ int32_t s_count[kLdsBinCells];
     __shared__ int32_t s_base[kFill ? kLdsBinCells : 1];
-    const BinChunk ch = chunks[blockIdx.x];
+    const BinChunk ch = bin_chunk(struct_chunks, structures, geom, blockIdx.x);
     const StructGeom& g = geom[ch.structure];
     const int ncells = g.roi_dim[0] * g.roi_dim[1] * g.roi_dim[2];
     const int tid = threadIdx.x;
@@ -1023,19 +1039,31 @@ __global__ __launch_bounds__(kBlock) void k_neighbors_wave(
 constexpr int kScanItems = 8;
 constexpr int kScanTile = kBlock * kScanItems;
 
+// Exclusive scan over the workgroup (kBlock threads): wavefront scans by
+// shuffles, then the wavefront totals through LDS (lds holds at least
+// kBlock / kWave values).
 __device__ int64_t block_exclusive_scan(int64_t value, int64_t* lds, int64_t& total) {
-    lds[threadIdx.x] = value;
-    __syncthreads();
-    for (int offset = 1; offset < kBlock; offset *= 2) {
-        const int64_t add = threadIdx.x >= offset ? lds[threadIdx.x - offset] : 0;
-        __syncthreads();
-        lds[threadIdx.x] += add;
-        __syncthreads();
+    constexpr int kWaves = kBlock / kWave;
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    int64_t inclusive = value;
+#pragma unroll
+    for (int offset = 1; offset < kWave; offset *= 2) {
+        const int64_t add = __shfl_up(inclusive, offset);
+        if (lane >= offset) inclusive += add;
     }
-    const int64_t inclusive = lds[threadIdx.x];
-    total = lds[kBlock - 1];
+    if (lane == kWave - 1) lds[wave] = inclusive;
     __syncthreads();
-    return inclusive - value;
+    int64_t before = 0;
+    total = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+        const int64_t x = lds[w];
+        before += w < wave ? x : 0;
+        total += x;
+    }
+    __syncthreads();
+    return before + inclusive - value;
 }
 
 __global__ __launch_bounds__(kBlock) void k_scan_reduce(const int32_t* in, int64_t n, int64_t* sums) {
@@ -1245,6 +1273,7 @@ void prepare_batch(const mdx_batch_view& batch, const int32_t* species, int n_sp
         throw Error(MDX_INVALID_ARGUMENT, "periodic images exceed the device graph capacity");
     }
     out.ext_total = ext;
+    frame_items(out);
     out.cells_total = out.wave_cells = out.big_bound = out.chunks = out.small_structs = out.large_structs = 0;
     out.direct_bins = out.struct_bins = false;
 }
@@ -1258,6 +1287,20 @@ void upload_batch(hipStream_t stream, const mdx_batch_view& batch, PreparedBatch
     pb.d_images.reserve(std::max<size_t>(1, pb.images.size() * sizeof(ImageDesc)));
     pb.d_offsets.reserve(pb.offsets.size() * sizeof(int64_t));
     size_frame(pb);
+    if (!pb.frame_items.empty()) {
+        MDX_HIP(hipMemcpyAsync(pb.d_frame_items.ptr, pb.frame_items.data(), pb.frame_items.size() * sizeof(FrameItem),
+                               hipMemcpyHostToDevice, stream));
+    }
+    MDX_HIP(hipMemcpyAsync(pb.d_frame_item_start.ptr, pb.frame_item_start.data(),
+                           pb.frame_item_start.size() * sizeof(int64_t), hipMemcpyHostToDevice, stream));
+    if (!pb.frame_fused.empty()) {
+        MDX_HIP(hipMemcpyAsync(pb.d_frame_lists.ptr, pb.frame_fused.data(), pb.frame_fused.size() * sizeof(int32_t),
+                               hipMemcpyHostToDevice, stream));
+    }
+    if (!pb.frame_large.empty()) {
+        MDX_HIP(hipMemcpyAsync(pb.d_frame_lists.as<int32_t>() + pb.frame_fused.size(), pb.frame_large.data(),
+                               pb.frame_large.size() * sizeof(int32_t), hipMemcpyHostToDevice, stream));
+    }
     if (atoms > 0) {
         MDX_HIP(hipMemcpyAsync(pb.d_positions.ptr, batch.positions, atoms * 3 * sizeof(double),
                                hipMemcpyHostToDevice, stream));
@@ -1317,8 +1360,9 @@ int64_t build_graph(hipStream_t stream, PreparedBatch& pb, DeviceGraph& gr, cons
     gr.pair_start.reserve(static_cast<size_t>(atoms + 1) * sizeof(int64_t));
     gr.slots = 0;
     // the position-dependent inputs: grid, regions of interest, binning
-    // paths and search lists, on the device (one host round trip)
-    if (!reuse_frame) prepare_frame(stream, pb);
+    // paths, centres by home cell and search lists, on the device (one host
+    // round trip); it leaves the counter block cleared
+    if (!reuse_frame) prepare_frame(stream, pb, gr);
     const int64_t cells = pb.cells_total;
     if (atoms == 0 || cells == 0) {
         MDX_HIP(hipMemsetAsync(gr.pair_start.ptr, 0, static_cast<size_t>(atoms + 1) * sizeof(int64_t), stream));
@@ -1338,14 +1382,13 @@ int64_t build_graph(hipStream_t stream, PreparedBatch& pb, DeviceGraph& gr, cons
         throw Error(MDX_INVALID_ARGUMENT, "periodic images exceed the device graph capacity");
     }
 
-    // one zero-filled block: search statistics, then the cell counters of
-    // binning (count, fill) and the centres of each home cell
-    const size_t counter_bytes = kStatWords * sizeof(unsigned long long) + 3 * cells1 * sizeof(int32_t);
-    gr.counters.reserve(counter_bytes);
+    // the zero-filled counter block: search statistics, then the cell
+    // counters of binning (count, fill) and the centres of each home cell
+    const int64_t capacity = gr.cell_capacity;
+    if (reuse_frame) MDX_HIP(hipMemsetAsync(gr.counters.ptr, 0, graph_counter_bytes(capacity), stream));
     unsigned long long* stats = gr.counters.as<unsigned long long>();
-    int32_t* cell_count = reinterpret_cast<int32_t*>(stats + kStatWords);
-    int32_t* cell_fill = cell_count + cells1;
-    int32_t* centre_count = cell_fill + cells1;
+    int32_t* cell_count = graph_cell_counters(gr, capacity, 0);
+    int32_t* cell_fill = graph_cell_counters(gr, capacity, 1);
     gr.cell_start.reserve(cells1 * sizeof(int64_t));
     gr.cell_runs.reserve(std::max<size_t>(1, static_cast<size_t>(cells) * static_cast<size_t>(S + 1)) *
                          sizeof(int64_t));
@@ -1358,10 +1401,6 @@ int64_t build_graph(hipStream_t stream, PreparedBatch& pb, DeviceGraph& gr, cons
     gr.bin_type.reserve(static_cast<size_t>(ext) * sizeof(int32_t));
     gr.counts.reserve(static_cast<size_t>(atoms * S) * sizeof(int32_t));
     gr.totals.reserve(static_cast<size_t>(atoms) * sizeof(int32_t));
-    MDX_HIP(hipMemsetAsync(gr.counters.ptr, 0, counter_bytes, stream));
-    // the centres grouped by home cell, the structure of every ROI cell (a
-    // rebuild of the same frame keeps the graph's from the first build)
-    if (!reuse_frame) place_centres(stream, pb, gr, centre_count);
 
     // bin every periodic image into its ROI cell, sorted by (species, extended index)
     if (pb.struct_bins) {
@@ -1389,7 +1428,7 @@ int64_t build_graph(hipStream_t stream, PreparedBatch& pb, DeviceGraph& gr, cons
         const dim3 bin_grid(static_cast<unsigned>(std::min<int64_t>((atoms + kBlock - 1) / kBlock, 1 << 16)),
                             static_cast<unsigned>(std::min(max_images, 65535)));
         const unsigned chunk_grid = static_cast<unsigned>(pb.chunks);
-        const BinChunk* chunks = pb.d_bin_chunks.as<BinChunk>();
+        const int64_t* chunks = pb.d_struct_chunks.as<int64_t>();
         const int species_major = S > 1 ? 1 : 0;
         if (pb.direct_bins) {
             hipLaunchKernelGGL(k_bin_atoms<false>, bin_grid, dim3(kBlock), 0, stream, geom, images, pos,
@@ -1397,7 +1436,8 @@ int64_t build_graph(hipStream_t stream, PreparedBatch& pb, DeviceGraph& gr, cons
                                static_cast<const int64_t*>(nullptr), static_cast<uint64_t*>(nullptr));
         }
         if (chunk_grid > 0) {
-            hipLaunchKernelGGL(k_bin_lds<false>, dim3(chunk_grid), dim3(kBinThreads), 0, stream, chunks, geom, images, pos,
+            hipLaunchKernelGGL(k_bin_lds<false>, dim3(chunk_grid), dim3(kBinThreads), 0, stream, chunks,
+                               pb.structures, geom, images, pos,
                                pb.d_types.as<int32_t>(), 0, cell_count, static_cast<const int64_t*>(nullptr),
                                static_cast<uint64_t*>(nullptr));
         }
@@ -1408,7 +1448,8 @@ int64_t build_graph(hipStream_t stream, PreparedBatch& pb, DeviceGraph& gr, cons
                                cell_fill, gr.cell_start.as<int64_t>(), gr.bin_key.as<uint64_t>());
         }
         if (chunk_grid > 0) {
-            hipLaunchKernelGGL(k_bin_lds<true>, dim3(chunk_grid), dim3(kBinThreads), 0, stream, chunks, geom, images, pos,
+            hipLaunchKernelGGL(k_bin_lds<true>, dim3(chunk_grid), dim3(kBinThreads), 0, stream, chunks,
+                               pb.structures, geom, images, pos,
                                pb.d_types.as<int32_t>(), species_major, cell_fill, gr.cell_start.as<int64_t>(),
                                gr.bin_key.as<uint64_t>());
         }

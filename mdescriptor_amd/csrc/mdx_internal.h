@@ -117,6 +117,18 @@ struct BinChunk {
     int32_t count;
 };
 
+// A run of at most kItemAtoms atoms of one structure: the unit of work of the
+// frame's per-atom kernels (one wavefront each).
+struct FrameItem {
+    int64_t first;
+    int32_t large;   // index of the structure in PreparedBatch::frame_large
+    int32_t count;
+};
+constexpr int kItemAtoms = 256;
+// structures of at most this many atoms take their whole frame in one
+// wavefront (k_frame_fused); larger ones are split into items
+constexpr int kFuseAtoms = 1024;
+
 // Periodic image: integer shift and its Cartesian vector, computed on the
 // host as ((n0*a + n1*b) + n2*c) per component (neighbor.cpp:472-474).
 struct ImageDesc {
@@ -201,7 +213,11 @@ struct PreparedBatch {
     std::vector<int64_t> item_begin, struct_items;
     int64_t most_images = 0;  // most binned images of one structure: no centre has more rows
     int max_images = 1;       // most periodic images of one structure
-    int64_t chunk_bound = 0;  // LDS binning chunks if every structure took that path
+    int64_t chunk_bound = 0;  // LDS binning chunks if every structure took that path (a check of the summary)
+    std::vector<int32_t> frame_fused;       // structures of at most kFuseAtoms atoms (frame_items())
+    std::vector<int32_t> frame_large;       // the others ...
+    std::vector<FrameItem> frame_items;     // ... split into atom runs
+    std::vector<int64_t> frame_item_start;  // first item of each large structure, [frame_large.size() + 1]
     // the last frame's summary (prepare_frame)
     int64_t cells_total = 0;  // ROI cells over all structures
     int64_t wave_cells = 0;   // one-cell structures: cell_lists[0, wave_cells)
@@ -223,17 +239,23 @@ struct PreparedBatch {
     DeviceBuffer d_offsets;   // i64[structures+1]
     // frame arrays, written on the device by the frame kernels (sized by the
     // topology at upload, so a run allocates none of them):
-    //   frame: u64 box words [structures * 6] (per axis: the largest order
-    //     key of -x, then of x), u32 span words [structures * 6] (per axis: ~
-    //     smallest and largest grid coordinate of a centre), then per
-    //     structure i64 ROI cells, i32 class bits, i32 chunks, then the
-    //     summary words [kFrameWords]; zero-filled at the start of a frame
+    //   frame: per item u64 box words [6] (per axis: the largest order key
+    //     of -x, then of x) and u32 span words [6] (per axis: ~ smallest and
+    //     largest grid coordinate of a centre), then per structure i64 ROI
+    //     cells, i32 class bits, i32 chunks, then the list workgroups' sums,
+    //     then the summary words [kFrameWords] (cleared at the start of a
+    //     frame)
     DeviceBuffer d_frame;
-    size_t frame_bytes = 0, frame_span = 0, frame_vol = 0, frame_cls = 0, frame_nch = 0, frame_summary = 0;
+    size_t frame_bytes = 0, frame_span = 0, frame_vol = 0, frame_cls = 0, frame_nch = 0, frame_blocks = 0,
+           frame_done = 0, frame_summary = 0;
+    bool frame_done_clear = false; // the item counters (frame_done) were cleared since the arrays were sized
+    DeviceBuffer d_frame_items;      // FrameItem[frame_items.size()]
+    DeviceBuffer d_frame_item_start; // i64[frame_large.size() + 1]
+    DeviceBuffer d_frame_lists;      // i32: frame_fused, then frame_large
     DeviceBuffer d_struct_cells; // i64[structures + 1]: first ROI cell of each structure, then the total
+    DeviceBuffer d_struct_chunks; // i64[structures + 1]: first LDS binning chunk of each structure, then the total
     DeviceBuffer d_cell_lists;   // i32[structures + atoms]: one-cell structures' cells, then searched home cells
     DeviceBuffer d_struct_list;  // i32[structures]: the k_bin_small structures, then the k_bin_struct ones
-    DeviceBuffer d_bin_chunks;   // BinChunk[chunk_bound]
     DeviceBuffer d_cell_centres; // i32[atoms]: centres grouped by home cell
     DeviceBuffer d_atom_cell;    // u64[atoms]: grid coordinates of each centre (x | y << 21 | z << 42)
     DeviceBuffer d_atom_home;    // i32[atoms]: home ROI cell
@@ -272,6 +294,7 @@ struct DeviceGraph {
     DeviceBuffer pair_start; // i64[atoms + 1]: first row of each centre (compact: the
                              // prefix sum of totals, pair_start[atoms] = pairs; slotted: centre * slots)
     DeviceBuffer pair_bin;   // u32 rows: [pairs] compact, [atoms * slots] slotted
+    int64_t cell_capacity = 0; // ROI cells the cell arrays (counters, cell_centre_start, cell_struct) hold
     int64_t slots = 0;       // layout of the last build: 0 compact, else rows reserved per centre
     int64_t slot_cap = 512;  // rows per centre for the next slotted build (0: compact only)
     StreamPoint read_back;   // completion of the statistics read-back
@@ -304,6 +327,12 @@ constexpr int kStatBinned = 0;
 constexpr int kStatLineWords = 16;
 constexpr int kStatLanes = 32;
 constexpr int kStatWords = kStatLineWords * (1 + kStatLanes);
+// The i32 cell counters in a graph's counter block sized for `capacity`
+// cells: 0 binning counts, 1 binning fill cursors, 2 centres per home cell.
+inline int32_t* graph_cell_counters(DeviceGraph& g, int64_t capacity, int which) {
+    return reinterpret_cast<int32_t*>(g.counters.as<unsigned long long>() + kStatWords) + which * (capacity + 1);
+}
+inline int32_t* graph_centre_counts(DeviceGraph& g, int64_t capacity) { return graph_cell_counters(g, capacity, 2); }
 __host__ __device__ constexpr int stat_rows(int lane) { return kStatLineWords * (1 + lane); }
 __host__ __device__ constexpr int stat_most(int lane) { return kStatLineWords * (1 + lane) + 1; }
 __host__ __device__ constexpr int stat_centres(int lane) { return kStatLineWords * (1 + lane) + 2; }
@@ -346,14 +375,22 @@ void upload_batch(hipStream_t stream, const mdx_batch_view& batch, PreparedBatch
 // interest and binning path, written into d_geom; the lists of the binning
 // and search kernels; the summary, read back into pb (one host round trip);
 // then, into the graph, the centres grouped by home cell and the structure of
-// every ROI cell.  The first half (prepare_frame) runs before the graph's
-// counters are sized and cleared, the second (place_centres) after.
+// every ROI cell (before the read-back when the graph's cell arrays have
+// room for this frame's cells, else after it).
 // Throws MDX_INVALID_ARGUMENT for non-finite positions or a grid beyond the
 // device graph's capacity, with the messages of prepare_batch's checks.
-void prepare_frame(hipStream_t stream, PreparedBatch& pb);
-// Size the frame arrays of a batch from its topology (upload_batch).
+void prepare_frame(hipStream_t stream, PreparedBatch& pb, DeviceGraph& graph);
+// The graph's zero-filled counter block for `capacity` cells: statistics,
+// then i32 cell counts of binning (count, fill) and the centres of each
+// home cell, [capacity + 1] each; its size, and room for it and the other
+// cell arrays of the frame.
+size_t graph_counter_bytes(int64_t capacity);
+void reserve_cells(DeviceGraph& graph, int64_t capacity);
+// The frame kernels' atom runs of a batch (prepare_batch), and the sizes of
+// its frame arrays (upload_batch), from its topology.
+void frame_items(PreparedBatch& pb);
 void size_frame(PreparedBatch& pb);
-void place_centres(hipStream_t stream, const PreparedBatch& pb, DeviceGraph& graph, int32_t* centre_count);
+
 
 // NeighborList descriptor over a one-species device graph (neighbor_list.hip).
 struct NeighborListState {

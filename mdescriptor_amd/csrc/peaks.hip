@@ -55,6 +55,51 @@ __global__ __launch_bounds__(kBlock) void k_copy(const double4* src, double4* ds
     }
 }
 
+// Streaming forms: each thread moves kUnroll 16-byte vectors per iteration,
+// all loads issued before the stores, with non-temporal hints (the data is
+// touched once: no reason to keep it in the caches).  n16 counts 16-byte
+// vectors and is a multiple of kUnroll * kBlock * gridDim.x (the host sizes
+// the buffer so), so no iteration needs a bounds check per vector.
+constexpr int kUnroll = 4;
+typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(kBlock) void k_copy_stream(const u4* src, u4* dst, int64_t n16) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock * kUnroll;
+    for (int64_t base = (blockIdx.x * static_cast<int64_t>(kBlock)) * kUnroll + threadIdx.x; base < n16;
+         base += stride) {
+        u4 v[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) v[u] = __builtin_nontemporal_load(&src[base + u * kBlock]);
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) __builtin_nontemporal_store(v[u], &dst[base + u * kBlock]);
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void k_read_stream(const u4* src, int64_t n16, unsigned* out) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock * kUnroll;
+    unsigned acc = 0;
+    for (int64_t base = (blockIdx.x * static_cast<int64_t>(kBlock)) * kUnroll + threadIdx.x; base < n16;
+         base += stride) {
+        u4 v[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) v[u] = __builtin_nontemporal_load(&src[base + u * kBlock]);
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    // keep the loads live (the buffer is zero-filled: never taken)
+    if (acc == 0x9e3779b9u) out[blockIdx.x * kBlock + threadIdx.x] = acc;
+}
+
+__global__ __launch_bounds__(kBlock) void k_write_stream(u4* dst, int64_t n16) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock * kUnroll;
+    const u4 v = {threadIdx.x, blockIdx.x, 0u, 1u};
+    for (int64_t base = (blockIdx.x * static_cast<int64_t>(kBlock)) * kUnroll + threadIdx.x; base < n16;
+         base += stride) {
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) __builtin_nontemporal_store(v, &dst[base + u * kBlock]);
+    }
+}
+
 int device_cus() {
     int dev = 0, cus = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 0;
@@ -67,9 +112,11 @@ int device_cus() {
 extern "C" {
 
 // which: 0 FP64 FMA (vector ALU), 1 FP64 MFMA 16x16x4, 2 HBM copy of `size`
-// bytes.  Returns 0 on success, else the HIP error code.  *seconds receives
-// the time per launch, *work the flops (0, 1) or bytes read + written (2)
-// per launch.
+// bytes (32-byte elements, grid-stride), 3 the same copy streamed (16-byte
+// vectors, four per thread in flight, non-temporal), 4 a streamed read of
+// `size` bytes, 5 a streamed write of `size` bytes.  Returns 0 on success,
+// else the HIP error code.  *seconds receives the time per launch, *work the
+// flops (0, 1) or bytes read + written (2-5) per launch.
 int mdx_peak_run(int which, int64_t size, int repeats, double* seconds, double* work) {
     const int cus = device_cus();
     if (cus <= 0 || repeats <= 0 || seconds == nullptr || work == nullptr) return 1;
@@ -83,10 +130,17 @@ int mdx_peak_run(int which, int64_t size, int repeats, double* seconds, double* 
     // enough workgroups for 8 wavefronts per SIMD on every CU
     const unsigned grid = static_cast<unsigned>(cus) * 8;
     const int iterations = 4096;
-    const size_t bytes = which == 2 ? static_cast<size_t>(size) : grid * kBlock * sizeof(double);
+    const bool memory = which >= 2;
+    // the streamed probes move whole rounds of the grid: size rounded down to
+    // a multiple of grid * 4 (workgroups) * kBlock * kUnroll * 16 bytes
+    const size_t round = static_cast<size_t>(grid) * 4 * kBlock * kUnroll * 16;
+    const size_t bytes = !memory ? grid * kBlock * sizeof(double)
+                         : which == 2 ? static_cast<size_t>(size)
+                                      : static_cast<size_t>(size) / round * round;
+    if (memory && bytes == 0) return 1;
     if (rc == hipSuccess) rc = hipMalloc(&a, bytes);
-    if (rc == hipSuccess && which == 2) rc = hipMalloc(&b, bytes);
-    if (rc == hipSuccess && which == 2) rc = hipMemsetAsync(a, 0, bytes, stream);
+    if (rc == hipSuccess && (which == 2 || which == 3 || which == 4)) rc = hipMalloc(&b, which == 4 ? round : bytes);
+    if (rc == hipSuccess && memory) rc = hipMemsetAsync(a, 0, bytes, stream);
     auto launch = [&]() {
         if (which == 0) {
             hipLaunchKernelGGL(k_fma_f64, dim3(grid), dim3(kBlock), 0, stream, static_cast<double*>(a), iterations,
@@ -94,10 +148,21 @@ int mdx_peak_run(int which, int64_t size, int repeats, double* seconds, double* 
         } else if (which == 1) {
             hipLaunchKernelGGL(k_mfma_f64, dim3(grid), dim3(kBlock), 0, stream, static_cast<double*>(a), iterations,
                                1e-6);
-        } else {
+        } else if (which == 2) {
             const int64_t n = static_cast<int64_t>(bytes / sizeof(double4));
             hipLaunchKernelGGL(k_copy, dim3(grid * 4), dim3(kBlock), 0, stream, static_cast<const double4*>(a),
                                static_cast<double4*>(b), n);
+        } else {
+            const int64_t n16 = static_cast<int64_t>(bytes / 16);
+            if (which == 3) {
+                hipLaunchKernelGGL(k_copy_stream, dim3(grid * 4), dim3(kBlock), 0, stream,
+                                   static_cast<const u4*>(a), static_cast<u4*>(b), n16);
+            } else if (which == 4) {
+                hipLaunchKernelGGL(k_read_stream, dim3(grid * 4), dim3(kBlock), 0, stream,
+                                   static_cast<const u4*>(a), n16, static_cast<unsigned*>(b));
+            } else {
+                hipLaunchKernelGGL(k_write_stream, dim3(grid * 4), dim3(kBlock), 0, stream, static_cast<u4*>(a), n16);
+            }
         }
     };
     if (rc == hipSuccess) {
@@ -119,8 +184,10 @@ int mdx_peak_run(int which, int64_t size, int repeats, double* seconds, double* 
             *work = 2.0 * kChains * iterations * threads;
         } else if (which == 1) {
             *work = 2.0 * 16 * 16 * 4 * kAcc * iterations * (threads / 64.0);
-        } else {
+        } else if (which == 2) {
             *work = 2.0 * static_cast<double>(bytes / sizeof(double4) * sizeof(double4));
+        } else {
+            *work = (which == 3 ? 2.0 : 1.0) * static_cast<double>(bytes);
         }
     }
     if (a != nullptr) (void)hipFree(a);
