@@ -676,6 +676,7 @@ int mdx_hip_soap_plan_create(mdx_hip_ctx* ctx, const mdx_soap_params* params, md
                     upload(plan->d_block_ps, bp.ps_offsets);
                 }
             }
+            plan->block_forced = choice == "block";
             if (choice == "block" && plan->block_waves == 0) {
                 throw mdx::Error(MDX_INVALID_ARGUMENT, "SOAP plan is outside the register-coefficient kernel's shapes");
             }

@@ -468,6 +468,7 @@ struct mdx_soap_plan {
     // average "off" only: wavefronts (0: not used), radial groups,
     // coefficient registers, lane tables
     int block_waves = 0, block_kg = 0, block_ncr = 0;
+    bool block_forced = false; // MDX_HIP_SOAP_KERNEL=block: also for inner averages of few large structures
     mdx::DeviceBuffer d_block_e1, d_block_beta, d_block_ps;
     // options beyond the GTO / uncompressed / unweighted default (mdx_soap_options)
     int Sc = 0;              // coefficient species: 1 for mu2, else S

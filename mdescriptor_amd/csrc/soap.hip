@@ -374,13 +374,22 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
     // unweighted, uncompressed structure averages of the inner kind, which it
     // forms from the structure's centres directly) and every centre's rows
     // fit their slot codes
-    const bool block = p.block_waves > 0 && (p.average == 0 || (p.average == 1 && p.weighted == 0 && p.compression == 0)) &&
-                       g.row_bound < kQuadMaxRows;
-    const bool block_inner = block && p.average == 1;
+    // It forms a structure's average in one workgroup, so it takes inner
+    // averages only when the structures are small (a wavefront of atoms) or
+    // many enough to fill the device (four per compute unit); a batch of a
+    // few large structures (16 cells of 4,096 atoms: 16 workgroups, 50 ms)
+    // takes the 4x4-block kernel, whose workgroups sum runs of centres into
+    // partial sums reduced per structure (2.5 ms).
     int64_t largest_structure = 0;
     for (size_t st = 0; st + 1 < pb.offsets.size(); ++st) {
         largest_structure = std::max(largest_structure, pb.offsets[st + 1] - pb.offsets[st]);
     }
+    const bool inner_fits = largest_structure <= kBlockSmallAtoms || p.block_forced ||
+                            pb.structures >= 4 * static_cast<int64_t>(device_compute_units());
+    const bool block = p.block_waves > 0 &&
+                       (p.average == 0 || (p.average == 1 && p.weighted == 0 && p.compression == 0 && inner_fits)) &&
+                       g.row_bound < kQuadMaxRows;
+    const bool block_inner = block && p.average == 1;
 
     // work items
     std::vector<int64_t>& item_begin_h = pb.item_begin;
@@ -505,6 +514,8 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
                     ba.w_w0 = p.w_w0;
                     ba.species_w = p.d_species_w.as<double>();
                     ba.bin_atom = g.bin_atom.as<int32_t>();
+                    ba.bin_image = g.bin_image.as<int32_t>();
+                    ba.images = pb.d_images.as<ImageDesc>();
                 }
                 ba.out = out_device;
                 ba.pitch = pitch_bytes;

@@ -25,7 +25,7 @@ struct BlockArgs {
     const double* bx;           // binned image positions
     const double* by;
     const double* bz;
-    const double* lane_e1;      // [l][register][64]: -a_lk of the lane's exp row, 0 for pad rows
+    const double* lane_e1;      // [l][register][64]: -a_lk of the lane's exp row (float32 rows: -a_lk 256/ln2), 0 for pad rows
     const double* lane_beta;    // [l][fold term][64]: beta^T operand of the lane
     const int32_t* ps_offsets;  // [tile pair][value][64]: (byte offset at l = 0) << 9 | feature stride per l
     int S;                      // species
@@ -42,6 +42,8 @@ struct BlockArgs {
     double w_r0, w_c, w_d, w_m, w_w0;
     const double* species_w;             // null: no weights
     const int32_t* bin_atom;             // atom of each binned image
+    const int32_t* bin_image;            // image of each binned image (w0: the exact self pair)
+    const ImageDesc* images;             // image table (integer shifts)
     int summed;                          // mu1nu1: spectrum against the species-summed coefficients
     void* out;
     int64_t pitch;              // bytes between output rows
@@ -63,7 +65,6 @@ struct BlockPlanHost {
 // soap.cpp:948-1013); mu2 is not taken.
 bool block_plan_tables(int S, int n, int l_max, int out_dtype, int compression, const std::vector<double>& beta_scaled,
                        const std::vector<double>& pref, const std::vector<double>& expo, BlockPlanHost& out);
-size_t block_lds_bytes(int l_max, int kg);
 void launch_block_expand(hipStream_t stream, int l_max, int kg, int ncr, const BlockArgs& a, int64_t count);
 // Zero the rows of the structures without atoms (structure averages; the
 // expansion writes only the rows of structures it visits).

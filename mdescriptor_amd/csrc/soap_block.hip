@@ -241,35 +241,60 @@ __device__ __forceinline__ double swap_blocks(double v) {
     return __hiloint2double(hi, lo);
 }
 
-// exp(x) for x = na * d2 (na = -a <= 0, d2 >= 0, x >= -708): x is rounded
-// exactly as the reference's exp(-a * d2) argument (soap.cpp:895-896), then
-// Tang's table method (ACM TOMS 15(2), 1989) with 256 entries:
-// x = (256k + j) ln2/256 + r, |r| <= ln2/512, exp(x) = 2^k 2^(j/256) e^r
-// with e^r - 1 by its degree-4 Taylor polynomial (truncation below 4e-17
-// relative).  The reduction is one fma against ln2/256 rounded to a double
-// (relative error 3.4e-17), which puts |x| * 3.4e-17 of relative error on the
-// result: 3.4e-16 at x = -10, less than the rounding of x itself (|x| *
-// 1.1e-16) that the reference's own argument carries, so a second, low-part
-// fma would buy nothing at the features' accuracy.  tab[j] = 2^(j/256) with
-// j << 12 taken off its high word, so that adding (256k + j) << 12 scales it
-// by 2^k in one integer add (the result is a normal number for x >= -708).
+// exp(x) for x = -a d2 (a >= 0, d2 >= 0, x >= -708) by Tang's table method
+// (ACM TOMS 15(2), 1989) with 256 entries: x = (256k + j) ln2/256 + r,
+// |r| <= ln2/512, exp(x) = 2^k 2^(j/256) e^r with e^r - 1 by its degree-4
+// Taylor polynomial (truncation below 4e-17 relative).  tab[j] = 2^(j/256)
+// with j << 12 taken off its high word, so that adding (256k + j) << 12
+// scales it by 2^k in one integer add (the result is a normal number for
+// x >= -708).
+//   kScaled false (float64 rows): na = -a.  x is rounded exactly as the
+// reference's exp(-a * d2) argument (soap.cpp:895-896); the reduction is one
+// fma against ln2/256 rounded to a double (relative error 3.4e-17), which
+// puts |x| * 3.4e-17 of relative error on the result: less than the rounding
+// of x itself (|x| * 1.1e-16) that the reference's own argument carries.
+//   kScaled true (float32 rows): na = -a 256/ln2, rounded once on the host,
+// so y = x 256/ln2 comes from one fma with the shifter and the reduced
+// argument r = y - (256k + j) from a second (no product of its own): one
+// multiply fewer per exp, for |x| * 2.2e-16 of relative error against the
+// reference's exp -- below 1e-14 for the arguments of these plans, far under
+// the float32 rows' 2e-5 gate even after the beta fold's cancellation
+// (1e5-fold for 8 channels).
+template <bool kScaled>
 __device__ __forceinline__ double exp_neg(double d2, double na, const int2* tab) {
     constexpr double kInvLn2xT = 369.32993046757463228414071833648; // 256 / ln 2
     constexpr double kLn2OverT = 0.0027076061740622863;              // ln 2 / 256
     constexpr double kShifter = 6755399441055744.0;                  // 1.5 * 2^52
-    const double x = na * d2;
-    const double s = fma(x, kInvLn2xT, kShifter);
-    const double kf = s - kShifter;
-    const double r = fma(kf, -kLn2OverT, x);
+    double s, r, q;
+    if constexpr (kScaled) {
+        s = fma(na, d2, kShifter);
+        const double kf = s - kShifter;
+        r = fma(na, d2, -kf); // in units of ln2/256, |r| <= 1/2
+        // e^(c r) - 1 = r (c + r (c^2/2 + r (c^3/6 + r c^4/24))), c = ln2/256
+        constexpr double c = kLn2OverT;
+        q = fma(r, c * c * c * c / 24.0, c * c * c / 6.0);
+        q = fma(q, r, c * c / 2.0);
+        q = fma(q, r, c);
+    } else {
+        const double x = na * d2;
+        s = fma(x, kInvLn2xT, kShifter);
+        const double kf = s - kShifter;
+        r = fma(kf, -kLn2OverT, x);
+        q = fma(r, 1.0 / 24.0, 1.0 / 6.0);
+        q = fma(q, r, 0.5);
+        q = fma(q, r, 1.0);
+    }
     const int nj = __double2loint(s);
     const int2 t = *reinterpret_cast<const int2*>(reinterpret_cast<const char*>(tab) +
                                                   ((nj << 3) & ((kTab - 1) << 3)));
-    double q = fma(r, 1.0 / 24.0, 1.0 / 6.0);
-    q = fma(q, r, 0.5);
-    q = fma(q, r, 1.0);
     const double em1 = r * q; // e^r - 1
     const double tk = __hiloint2double(t.y + (nj << (20 - kTabBits)), t.x); // 2^k 2^(j/256)
     return fma(tk, em1, tk);
+}
+
+// the lane constant of exp_neg<kScaled> for the exponent a
+inline double exp_lane_constant(double a, bool scaled) {
+    return scaled ? -a * 369.32993046757463228414071833648 : -a;
 }
 
 // Column m of the scaled harmonics (harmonic_table.h) from T_m, one part per
@@ -591,7 +616,8 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
     Stage s1 = next_stage(); // chunk k + 1 (harmonics)
     double px = 0.0, py = 0.0, pz = 0.0;
     double qx = 0.0, qy = 0.0, qz = 0.0; // species-major: the slot's centre
-    int patom = -1;                      // weights with w0: the slot's image's atom
+    int patom = -1;                      // weights with w0: the slot's image's atom, -1 unless the
+                                         // image has the zero shift
     const int jj = lane / 2, comp = lane % 2;
     auto load_positions = [&](const Stage& s) {
         if constexpr (kHarm) {
@@ -599,7 +625,11 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
             py = a.by[s.bin];
             pz = a.bz[s.bin];
             if constexpr (kWeighted) {
-                if (a.has_w0 != 0) patom = a.bin_atom[s.bin];
+                if (a.has_w0 != 0) {
+                    const ImageDesc& image = a.images[a.bin_image[s.bin]];
+                    const bool zero = image.n[0] == 0 && image.n[1] == 0 && image.n[2] == 0;
+                    patom = zero ? a.bin_atom[s.bin] : -1;
+                }
             }
             if constexpr (kSpeciesMajor) {
                 qx = a.positions[3 * static_cast<int64_t>(s.catom)];
@@ -620,12 +650,12 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
         }
         double seed = real ? 1.0 : 0.0;
         if constexpr (kWeighted) {
-            // the neighbour's weight (soap_weight, soap.cpp:389-420); the
-            // centre's own image is the image of the centre atom at distance 0
-            // (a non-zero shift of a nonsingular cell never is)
+            // the neighbour's weight (soap_weight, soap.cpp:389-420); w0 for
+            // the exact self pair, the centre's own atom under the zero shift
+            // (NeighborView::exact_self, neighbor.cpp:683-689)
             const double r2 = fma(dz, dz, fma(dx, dx, dy * dy));
             double w = weight_function(a.weighting, a.w_r0, a.w_c, a.w_d, a.w_m, sqrt(r2));
-            if (a.has_w0 != 0 && r2 == 0.0 && static_cast<int64_t>(patom) == uniform64(s.centre)) w = a.w_w0;
+            if (a.has_w0 != 0 && static_cast<int64_t>(patom) == uniform64(s.centre)) w = a.w_w0;
             seed = real ? w * a.species_w[__builtin_amdgcn_readfirstlane(s.q)] : 0.0;
         }
         harmonic_columns<LM, MLO, MHI>(dx, dy, dz, seed, comp, s_y + buf * PL::YWORDS + jj);
@@ -705,7 +735,6 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
         const int groups0 = __builtin_amdgcn_readfirstlane(s0.groups);
         const bool last0 = __builtin_amdgcn_readfirstlane(s0.last ? 1 : 0) != 0;
         const bool ends0 = inner ? __builtin_amdgcn_readfirstlane(s0.ends ? 1 : 0) != 0 : last0;
-        const int64_t centre0 = uniform64(s0.centre);
         const int64_t row0 = uniform64(s0.row);
         const int q0 = __builtin_amdgcn_readfirstlane(s0.q);
         // centre position of chunk k + 1 (scalar loads, used after the contraction)
@@ -736,7 +765,7 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
                 unroll<ND>([&](auto dc) {
                     unroll<RPL>([&](auto rc) {
                         ev[decltype(dc)::value][decltype(rc)::value] =
-                            exp_neg(d2, e1[decltype(dc)::value][decltype(rc)::value], s_tab);
+                            exp_neg<ES == 4>(d2, e1[decltype(dc)::value][decltype(rc)::value], s_tab);
                     });
                 });
                 unroll<L>([&](auto lc) {
@@ -977,7 +1006,7 @@ size_t lds_bytes() {
 template <int LM, int KG, int NCR>
 void launch_shape(hipStream_t stream, const BlockArgs& a, int64_t count) {
     using PL = BlockPlan<LM, KG>;
-    const size_t lds = lds_bytes<LM, KG, NCR>() + NCR * (NCR + 1) / 2 * 4 * kWaveThreads * sizeof(int);
+    const size_t lds = lds_bytes<LM, KG, NCR>() + ps_tiles(NCR, a.summed != 0) * 4 * kWaveThreads * sizeof(int);
     const int64_t resident = std::max<int64_t>(1, std::min<int64_t>(8, (160 * 1024) / std::max<size_t>(lds, 1)));
     const int64_t target = std::max<int64_t>(1, 8 * resident * device_compute_units());
     BlockArgs args = a;
@@ -1072,7 +1101,7 @@ bool block_plan_tables(int S, int n, int l_max, int out_dtype, int compression, 
                 const int rg = rr * R + b % R;
                 const int k = 4 * rg + lane % 4;
                 out.lane_e1[static_cast<size_t>((l * RPL + rr) * 64 + lane)] =
-                    k < n ? -expo[static_cast<size_t>(l * n + k)] : 0.0;
+                    k < n ? exp_lane_constant(expo[static_cast<size_t>(l * n + k)], out_dtype == 4) : 0.0;
             }
             // beta^T operand: lane = beta^T[k = lane / 16][n' = lane % 4] of the
             // fold term's (radial group in -> radial group out) block
@@ -1184,13 +1213,6 @@ bool block_plan_tables(int S, int n, int l_max, int out_dtype, int compression, 
     return true;
 }
 
-size_t block_lds_bytes(int l_max, int kg) {
-    const int L = l_max + 1, H = L * L;
-    int pad = 0;
-    for (int l = 0; l < L; ++l) pad += 4 * cgroups(l);
-    return static_cast<size_t>(2 * H * kYS + 2 * kNb + kTab + pad) * sizeof(double);
-    (void)kg;
-}
 
 void launch_block_expand(hipStream_t stream, int l_max, int kg, int ncr, const BlockArgs& a, int64_t count) {
     if (count <= 0) return;
