@@ -72,13 +72,42 @@ HBM_PEAK_GBS = 8000.0
 
 
 # SOAP options of the option bench lines (--options): the parameters of the
-# option parity cases
+# option parity cases, and the average mode where a line sets its own
+POW_W0 = {"function": "pow", "r0": 2.0, "c": 2.0, "d": 1.0, "m": 3.0, "w0": 0.5}
 BENCH_OPTIONS = {
-    "off": None,
-    "mu1nu1": {"compression": "mu1nu1"},
-    "pow_w0": {"weighting": {"function": "pow", "r0": 2.0, "c": 2.0, "d": 1.0, "m": 3.0, "w0": 0.5}},
-    "crossover": {"compression": "crossover", "weighting": {"function": "exp", "r0": 2.0, "c": 1.0, "d": 0.2}},
+    "off": (None, None),
+    "mu1nu1": ({"compression": "mu1nu1"}, None),
+    "mu2": ({"compression": "mu2"}, None),
+    "pow_w0": ({"weighting": POW_W0}, None),
+    "crossover": ({"compression": "crossover", "weighting": {"function": "exp", "r0": 2.0, "c": 1.0, "d": 0.2}}, None),
+    "polynomial": ({"polynomial": "basis"}, None),
+    "outer": (None, "outer"),
+    "inner": (None, "inner"),
+    "inner_pow_w0": ({"weighting": POW_W0}, "inner"),
 }
+
+
+def describe_options(options: dict | None):
+    """JSON-safe description of a line's SOAP options."""
+
+    if not options:
+        return "default (GTO, no weighting, compression off)"
+    out = {k: v for k, v in options.items() if k != "polynomial"}
+    if options.get("polynomial") is not None:
+        out["radial_basis"] = f"polynomial ({len(options['polynomial'][0])}-point radial grid)"
+    return out
+
+
+def bench_options(name: str, params: dict) -> tuple[dict | None, str]:
+    """The SOAP options and average mode of option line `name` on a
+    configuration (the polynomial basis built for its r_cut and n_max)."""
+
+    from mdescriptor_amd.descriptors.basis import basis_polynomial
+
+    options, average = BENCH_OPTIONS[name]
+    if options is not None and options.get("polynomial") == "basis":
+        options = dict(options, polynomial=basis_polynomial(params["r_cut"], params["n_max"]))
+    return options, average or params["average"]
 
 
 def algorithmic_flops(envs: int, rows: int, kbar: float, S: int, n: int, l_max: int, features: int | None = None,
@@ -246,7 +275,7 @@ def cpu_sample(index: int, workload):
     return workload
 
 
-def cpu_baseline(index: int, workload, alphas, betas, threads: int, options: dict | None,
+def cpu_baseline(index: int, workload, alphas, betas, threads: int, options: dict | None, average: str,
                  budget_s: float = 30.0) -> dict:
     """The reference's SOAP (compiled in place under oracle/_ref; else the
     oracle port) on this host, as the reference runs it: structures in
@@ -263,7 +292,7 @@ def cpu_baseline(index: int, workload, alphas, betas, threads: int, options: dic
     while True:
         t0 = time.perf_counter()
         oracle.soap(batch, species=p["species"], n_max=p["n_max"], l_max=p["l_max"], r_cut=p["r_cut"],
-                    sigma=1.0, alphas=alphas, betas=betas, average=p["average"], num_threads=threads,
+                    sigma=1.0, alphas=alphas, betas=betas, average=average, num_threads=threads,
                     kind="ref" if kind == "reference" else "oracle", options=options)
         times.append(time.perf_counter() - t0)
         if len(times) >= 3 or sum(times) + times[-1] > budget_s:
@@ -423,11 +452,11 @@ def soap_bench(args, workload) -> dict:
 
     p = workload.params
     batch = workload.batch
-    options = BENCH_OPTIONS[args.options]
+    options, average = bench_options(args.options, p)
     alphas, betas = basis_gto(p["r_cut"], p["n_max"], p["l_max"])
     ctx = _hip.Context(0)
     plan = _hip.SoapPlan(ctx, species=p["species"], n_max=p["n_max"], l_max=p["l_max"], r_cut=p["r_cut"],
-                         sigma=1.0, alphas=alphas, betas=betas, average=p["average"], dtype=p["dtype"],
+                         sigma=1.0, alphas=alphas, betas=betas, average=average, dtype=p["dtype"],
                          options=options)
     dbatch = _hip.DeviceBatch(plan, batch)
     itemsize = np.dtype(p["dtype"]).itemsize
@@ -459,8 +488,12 @@ def soap_bench(args, workload) -> dict:
     kbar = pairs / envs
     S, n, l_max = len(p["species"]), p["n_max"], p["l_max"]
     compression = (options or {}).get("compression", "off")
-    rows = batch.structures if p["average"] == "inner" else envs
-    total_flops = algorithmic_flops(envs, rows, kbar, S, n, l_max, plan.features, 1 if compression == "mu2" else S)
+    # the fold and the spectrum run once per output row, except for outer
+    # averages (once per centre, the spectra then averaged)
+    rows = batch.structures if average != "off" else envs
+    fold_rows = batch.structures if average == "inner" else envs
+    total_flops = algorithmic_flops(envs, fold_rows, kbar, S, n, l_max, plan.features,
+                                    1 if compression == "mu2" else S)
     per_env = total_flops / envs
     launches = max(1, int(timings[-1]["expansion_launches"]))
     flops_launch = total_flops / launches
@@ -513,9 +546,9 @@ def soap_bench(args, workload) -> dict:
             "l_max": l_max,
             "r_cut": p["r_cut"],
             "sigma": 1.0,
-            "average": p["average"],
+            "average": average,
             "output_dtype": p["dtype"],
-            "options": options or "default (GTO, no weighting, compression off)",
+            "options": describe_options(options),
             "parallelism": "single-gpu",
         },
         "roofline": {
@@ -559,7 +592,7 @@ def soap_bench(args, workload) -> dict:
     ctx.close()
     if not args.no_cpu_baseline:
         threads = args.cpu_threads or int(os.environ.get("OMP_NUM_THREADS") or 0) or len(os.sched_getaffinity(0))
-        result["cpu_baseline"] = cpu_baseline(args.config, workload, alphas, betas, threads, options)
+        result["cpu_baseline"] = cpu_baseline(args.config, workload, alphas, betas, threads, options, average)
     return result
 
 
