@@ -14,7 +14,11 @@ from typing import Any
 
 
 class MDescriptorError(Exception):
-    """Base class for errors raised by the public descriptor API."""
+    """Root of every error the descriptor API raises.
+
+    Carries a machine-readable ``code``, the location in the inputs that
+    failed (``path``, optional) and JSON-safe ``details``; ``to_dict`` gives
+    the serialised form."""
 
     default_code = "mdescriptor_error"
 
@@ -36,7 +40,8 @@ class MDescriptorError(Exception):
 
 
 class _InputValidationError(ValueError):
-    """Input error that carries the field validated at the source."""
+    """ValueError raised while a field of the input is checked; ``path`` names
+    that field so the public error can point at it."""
 
     def __init__(self, message: str, path: tuple[str | int, ...]) -> None:
         self.path = path
@@ -44,31 +49,33 @@ class _InputValidationError(ValueError):
 
 
 class DescriptorConfigError(MDescriptorError, ValueError):
-    """A descriptor option or capability declaration is invalid."""
+    """Raised when the options of a descriptor (or what a backend declares it
+    supports) are rejected."""
 
     default_code = "invalid_configuration"
 
 
 class DescriptorInputError(MDescriptorError, ValueError):
-    """An input batch does not satisfy the descriptor input contract."""
+    """Raised when a structure batch breaks the input rules of a descriptor."""
 
     default_code = "invalid_input"
 
 
 class UnsupportedPeriodicityError(DescriptorInputError):
-    """The input periodicity is not supported by the selected descriptor."""
+    """Raised for a batch whose periodicity the chosen descriptor cannot take."""
 
     default_code = "unsupported_periodicity"
 
 
 class ClosedDescriptorError(MDescriptorError, RuntimeError):
-    """An operation was attempted after a descriptor was closed."""
+    """Raised when a descriptor is used after ``close()``."""
 
     default_code = "closed_descriptor"
 
 
 class CancelledError(MDescriptorError, RuntimeError):
-    """A cooperative descriptor computation was cancelled."""
+    """Raised when a computation stops because its ``ComputeControl`` asked
+    it to."""
 
     default_code = "cancelled"
 

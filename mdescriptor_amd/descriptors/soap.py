@@ -48,58 +48,74 @@ class _KernelValueError(ValueError):
         self.path = path
 
 
+# Per weighting function: the shape parameters it takes besides r0 and c, in
+# the order they are checked; each defaults to -1 (absent, hence rejected).
+# pow and exp also take a positive threshold (default 1e-2), used only to
+# infer a missing cutoff.  (Contract of core.py:97-153: the same messages,
+# defaults and cutoff formulas.)
+_WEIGHTING_SHAPES = {"poly": ("m",), "pow": ("d", "m"), "exp": ("d",)}
+_SHAPE_ERRORS = {"d": "SOAP pow/exp weighting requires d >= 0", "m": "SOAP {} weighting requires m >= 0"}
+
+
+def _poly_cutoff(options: dict[str, Any]) -> float:
+    return options["r0"]
+
+
+def _pow_cutoff(options: dict[str, Any]) -> float:
+    base = options["c"] / options["threshold"] - options["d"]
+    if options["m"] <= 0.0 or base <= 0.0:
+        raise ValueError("cannot infer SOAP pow weighting cutoff")
+    return options["r0"] * base ** (1.0 / options["m"])
+
+
+def _exp_cutoff(options: dict[str, Any]) -> float:
+    base = options["c"] / options["threshold"] - options["d"]
+    if base <= 1.0:
+        raise ValueError("cannot infer SOAP exp weighting cutoff")
+    return float(options["r0"] * np.log(base))
+
+
+# the radius where each weighting function falls to the threshold
+_CUTOFF_RULES = {"poly": _poly_cutoff, "pow": _pow_cutoff, "exp": _exp_cutoff}
+
+
 def _weighting_config(weighting: Mapping[str, Any] | None, r_cut: float | None) -> tuple[dict[str, Any], float]:
     """Canonical weighting options and the resolved cutoff (core.py:97-153).
 
-    Without a weighting function the cutoff must be given.  With one, a
-    missing cutoff is inferred from the function: ``r0`` for ``poly``,
+    Without a weighting function the cutoff must be given (else 6 A).  With
+    one, a missing cutoff is inferred from the function: ``r0`` for ``poly``,
     ``r0 (c/threshold - d)^(1/m)`` for ``pow`` and ``r0 ln(c/threshold - d)``
     for ``exp``.
     """
 
-    weighting = dict(weighting or {})
-    function = weighting.get("function")
-    if function is not None:
-        function = str(function)
-        if function not in {"poly", "pow", "exp"}:
+    options = dict(weighting or {})
+    kind = options.get("function")
+    if kind is not None:
+        kind = str(kind)
+        shapes = _WEIGHTING_SHAPES.get(kind)
+        if shapes is None:
             raise ValueError("SOAP weighting function must be 'poly', 'pow', or 'exp'")
-        r0 = float(weighting.get("r0", 0.0))
-        c = float(weighting.get("c", -1.0))
+        r0, c = float(options.get("r0", 0.0)), float(options.get("c", -1.0))
         if r0 <= 0.0 or c < 0.0:
             raise ValueError("SOAP weighting requires r0 > 0 and c >= 0")
-        weighting["r0"], weighting["c"] = r0, c
-        if function in {"poly", "pow"}:
-            m = float(weighting.get("m", -1.0))
-            if m < 0.0:
-                raise ValueError(f"SOAP {function} weighting requires m >= 0")
-            weighting["m"] = m
-        if function in {"pow", "exp"}:
-            d = float(weighting.get("d", -1.0))
-            if d < 0.0:
-                raise ValueError("SOAP pow/exp weighting requires d >= 0")
-            weighting["d"] = d
-            weighting["threshold"] = float(weighting.get("threshold", 1e-2))
-            if weighting["threshold"] <= 0.0:
+        options["r0"], options["c"] = r0, c
+        for name in shapes:
+            value = float(options.get(name, -1.0))
+            if value < 0.0:
+                raise ValueError(_SHAPE_ERRORS[name].format(kind))
+            options[name] = value
+        if "d" in shapes:
+            options["threshold"] = float(options.get("threshold", 1e-2))
+            if options["threshold"] <= 0.0:
                 raise ValueError("SOAP weighting threshold must be positive")
-    if "w0" in weighting:
-        weighting["w0"] = float(weighting["w0"])
-        if weighting["w0"] < 0.0:
+    if "w0" in options:
+        options["w0"] = float(options["w0"])
+        if options["w0"] < 0.0:
             raise ValueError("SOAP weighting w0 must be non-negative")
     if r_cut is not None:
-        return weighting, float(r_cut)
-    if function == "poly":
-        return weighting, weighting["r0"]
-    if function in {"pow", "exp"}:
-        argument = weighting["c"] / weighting["threshold"] - weighting["d"]
-        if function == "pow":
-            if weighting["m"] <= 0.0 or argument <= 0.0:
-                raise ValueError("cannot infer SOAP pow weighting cutoff")
-            return weighting, weighting["r0"] * argument ** (1.0 / weighting["m"])
-        if argument <= 1.0:
-            raise ValueError("cannot infer SOAP exp weighting cutoff")
-        return weighting, float(weighting["r0"] * np.log(argument))
-    # The reference falls back to 6 Angstrom when neither is given.
-    return weighting, 6.0
+        return options, float(r_cut)
+    rule = _CUTOFF_RULES.get(kind) if kind is not None else None
+    return options, 6.0 if rule is None else rule(options)
 
 
 class SoapSettings:

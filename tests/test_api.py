@@ -136,6 +136,47 @@ def test_weighting_cutoff_inference():
     assert SoapSettings(species=[1]).r_cut == 6.0
 
 
+# (weighting, r_cut, expected cutoff or the first error message): the checks of
+# _soap_weighting_config (core.py:97-153) in their order -- function, then r0
+# and c, then d before m for pow, then the threshold, then w0 -- and the
+# inferred cutoffs r0, r0 (c/t - d)^(1/m), r0 ln(c/t - d)
+WEIGHTING_CASES = [
+    ({"function": "gauss", "r0": 1.0, "c": 1.0}, None, "must be 'poly', 'pow', or 'exp'"),
+    ({"function": "poly", "c": 1.0, "m": 1.0}, None, "requires r0 > 0 and c >= 0"),
+    ({"function": "pow", "r0": 1.0, "m": 1.0, "d": 0.0}, None, "requires r0 > 0 and c >= 0"),
+    ({"function": "poly", "r0": 1.0, "c": 1.0}, None, "SOAP poly weighting requires m >= 0"),
+    ({"function": "pow", "r0": 1.0, "c": 1.0}, None, "SOAP pow/exp weighting requires d >= 0"),
+    ({"function": "pow", "r0": 1.0, "c": 1.0, "d": 0.5}, None, "SOAP pow weighting requires m >= 0"),
+    ({"function": "exp", "r0": 1.0, "c": 1.0}, None, "SOAP pow/exp weighting requires d >= 0"),
+    ({"function": "exp", "r0": 1.0, "c": 1.0, "d": 0.0, "threshold": 0.0}, None, "threshold must be positive"),
+    ({"function": "poly", "r0": 2.5, "c": 1.0, "m": 2.0, "w0": -1.0}, None, "w0 must be non-negative"),
+    ({"w0": 0.25}, None, 6.0),
+    ({"function": "poly", "r0": 2.5, "c": 0.0, "m": 0.0}, None, 2.5),
+    ({"function": "poly", "r0": 2.5, "c": 1.0, "m": 2.0}, 4.0, 4.0),
+    ({"function": "pow", "r0": 2.0, "c": 1.0, "d": 1.0, "m": 2.0, "threshold": 0.5}, None, 2.0),
+    ({"function": "pow", "r0": 2.0, "c": 1.0, "d": 0.0, "m": 0.0}, None, "cannot infer SOAP pow"),
+    ({"function": "pow", "r0": 2.0, "c": 1.0, "d": 200.0, "m": 1.0}, None, "cannot infer SOAP pow"),
+    ({"function": "exp", "r0": 3.0, "c": 2.0, "d": 1.0, "threshold": 0.1}, None, 3.0 * np.log(19.0)),
+    ({"function": "exp", "r0": 3.0, "c": 0.01, "d": 0.0}, None, "cannot infer SOAP exp"),
+]
+
+
+@pytest.mark.parametrize("case", range(len(WEIGHTING_CASES)))
+def test_weighting_checks_and_cutoffs(case):
+    from mdescriptor_amd.descriptors.soap import _weighting_config
+
+    weighting, r_cut, expected = WEIGHTING_CASES[case]
+    if isinstance(expected, str):
+        with pytest.raises(ValueError, match=expected):
+            _weighting_config(weighting, r_cut)
+        return
+    options, cutoff = _weighting_config(weighting, r_cut)
+    assert cutoff == pytest.approx(expected, rel=1e-15)
+    if weighting.get("function") in ("pow", "exp"):
+        assert options["threshold"] == weighting.get("threshold", 1e-2)
+        assert list(options)[-1] == "threshold" or "threshold" in weighting
+
+
 @pytest.mark.parametrize("manifest", ["manifest.json", "external_manifest.json"])
 def test_metadata_envelope_matches_golden(manifest):
     meta, _, _ = load_golden("reference_soap", manifest)
