@@ -109,6 +109,12 @@ struct BlockPlan {
     // one wavefront's share of the columns outweighs it (measured: two
     // wavefronts 6 % faster at l_max 8 and 9, 7-11 % slower at 3, 4 and 6)
     static constexpr int HW = (LM >= 8 ? 2 : 1) < T ? (LM >= 8 ? 2 : 1) : T;
+    // with one harmonic wavefront it owns no degree: its staging alone is
+    // about as long as two degrees' exps, and the wavefronts of a workgroup
+    // meet at a barrier every chunk (measured: 9-10 % faster at l_max 3 and
+    // 4, 4 % at 6; with two harmonic wavefronts, l_max 8 and 9, the
+    // remaining two would hold every degree: 40 % slower)
+    static constexpr bool HO = HW == 1 && T > 1;
 
     // degrees of each wavefront: longest processing time first over the cost
     // of a degree per step group (exps of 12 VALU instructions, 4 cycles each,
@@ -121,7 +127,7 @@ struct BlockPlan {
     static constexpr Owners owners() {
         Owners o{};
         int load[4] = {0, 0, 0, 0};
-        for (int w = 0; w < HW; ++w) load[w] = 4 * range_cost(mlo(w), mhi(w)) / GROUPS;
+        for (int w = 0; w < HW; ++w) load[w] = HO ? (1 << 20) : 4 * range_cost(mlo(w), mhi(w)) / GROUPS;
         bool done[L] = {};
         for (int it = 0; it < L; ++it) {
             int best = -1, best_cost = -1;
@@ -243,23 +249,25 @@ __device__ __forceinline__ double swap_blocks(double v) {
 
 // exp(x) for x = -a d2 (a >= 0, d2 >= 0, x >= -708) by Tang's table method
 // (ACM TOMS 15(2), 1989) with 256 entries: x = (256k + j) ln2/256 + r,
-// |r| <= ln2/512, exp(x) = 2^k 2^(j/256) e^r with e^r - 1 by its degree-4
-// Taylor polynomial (truncation below 4e-17 relative).  tab[j] = 2^(j/256)
+// |r| <= ln2/512, exp(x) = 2^k 2^(j/256) e^r with e^r - 1 by a short
+// Taylor polynomial (below).  tab[j] = 2^(j/256)
 // with j << 12 taken off its high word, so that adding (256k + j) << 12
 // scales it by 2^k in one integer add (the result is a normal number for
 // x >= -708).
-//   kScaled false (float64 rows): na = -a.  x is rounded exactly as the
+//   kScaled false (float64 rows): na = -a, degree 4 (truncation below 4e-17
+// relative).  x is rounded exactly as the
 // reference's exp(-a * d2) argument (soap.cpp:895-896); the reduction is one
 // fma against ln2/256 rounded to a double (relative error 3.4e-17), which
 // puts |x| * 3.4e-17 of relative error on the result: less than the rounding
 // of x itself (|x| * 1.1e-16) that the reference's own argument carries.
 //   kScaled true (float32 rows): na = -a 256/ln2, rounded once on the host,
 // so y = x 256/ln2 comes from one fma with the shifter and the reduced
-// argument r = y - (256k + j) from a second (no product of its own): one
-// multiply fewer per exp, for |x| * 2.2e-16 of relative error against the
-// reference's exp -- below 1e-14 for the arguments of these plans, far under
-// the float32 rows' 2e-5 gate even after the beta fold's cancellation
-// (1e5-fold for 8 channels).
+// argument r = y - (256k + j) from a second (no product of its own), and
+// e^r by its degree-3 Taylor polynomial (truncation below 1.4e-13 relative)
+// evaluated as 1 + (e^r - 1) and scaled by the table entry in one multiply:
+// two instructions fewer per exp, for |x| * 2.2e-16 + 1.4e-13 of relative
+// error against the reference's exp -- far under the float32 rows' 2e-5 gate
+// even after the beta fold's cancellation (2.3e5-fold for 8 channels: 3e-8).
 template <bool kScaled>
 __device__ __forceinline__ double exp_neg(double d2, double na, const int2* tab) {
     constexpr double kInvLn2xT = 369.32993046757463228414071833648; // 256 / ln 2
@@ -271,10 +279,11 @@ __device__ __forceinline__ double exp_neg(double d2, double na, const int2* tab)
         const double kf = s - kShifter;
         r = fma(na, d2, -kf); // in units of ln2/256, |r| <= 1/2
         // e^(c r) - 1 = r (c + r (c^2/2 + r (c^3/6 + r c^4/24))), c = ln2/256
+        // e^(c r) = 1 + r (c + r (c^2/2 + r c^3/6)), c = ln2/256
         constexpr double c = kLn2OverT;
-        q = fma(r, c * c * c * c / 24.0, c * c * c / 6.0);
-        q = fma(q, r, c * c / 2.0);
+        q = fma(r, c * c * c / 6.0, c * c / 2.0);
         q = fma(q, r, c);
+        q = fma(q, r, 1.0);
     } else {
         const double x = na * d2;
         s = fma(x, kInvLn2xT, kShifter);
@@ -287,8 +296,9 @@ __device__ __forceinline__ double exp_neg(double d2, double na, const int2* tab)
     const int nj = __double2loint(s);
     const int2 t = *reinterpret_cast<const int2*>(reinterpret_cast<const char*>(tab) +
                                                   ((nj << 3) & ((kTab - 1) << 3)));
-    const double em1 = r * q; // e^r - 1
     const double tk = __hiloint2double(t.y + (nj << (20 - kTabBits)), t.x); // 2^k 2^(j/256)
+    if constexpr (kScaled) return tk * q;
+    const double em1 = r * q; // e^r - 1
     return fma(tk, em1, tk);
 }
 
@@ -381,8 +391,8 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
     const double* s_scale = s_d2 + 2 * kNb + kTab;           // padded S_lm table
 
     // lane constants of the owned degrees
-    double e1[ND][RPL];
-    double bt[ND][NT];
+    double e1[ND > 0 ? ND : 1][RPL];
+    double bt[ND > 0 ? ND : 1][NT];
     unroll<L>([&](auto lc) {
         constexpr int l = decltype(lc)::value;
         if constexpr ((kOwn >> l) & 1u) {
@@ -675,8 +685,8 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
     __syncthreads();
 
     // accumulators and coefficient registers
-    double acc[NU][RPL];
-    double C[NU][NCR];
+    double acc[NU > 0 ? NU : 1][RPL];
+    double C[NU > 0 ? NU : 1][NCR];
     unroll<NU>([&](auto u) {
         unroll<RPL>([&](auto r) { acc[decltype(u)::value][decltype(r)::value] = 0.0; });
         unroll<NCR>([&](auto r) { C[decltype(u)::value][decltype(r)::value] = 0.0; });
@@ -684,12 +694,26 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
     int cur = -1; // species of the accumulators
 
     // sum the phases of every accumulator and add species q's radial groups
-    // into its block slots of the coefficient registers (which start every
-    // output row at zero).  A species merges once per centre: for a centre's
-    // own row the merge overwrites its slots with a lane select, for a
-    // structure average it adds to them.
-    auto merge_into = [&](auto rc_reg, int q) {
-        constexpr int rt = decltype(rc_reg)::value; // target coefficient register
+    // into its block slots of the coefficient registers, which start every
+    // output row at zero (a species merges once per centre; a structure
+    // average adds its centres' sums): per lane and register a factor of 1
+    // (the lane's block slot and the register belong to q) or 0, and one fma
+    // per register
+    auto merge = [&](int q) {
+        const int rt = KG == 2 ? q >> 1 : KG == 1 ? q >> 2 : q;
+        double sel[RPL][NCR];
+        unroll<RPL>([&](auto rc) {
+            constexpr int rr = decltype(rc)::value;
+            bool mine;
+            if constexpr (KG == 2) {
+                mine = low_pair == ((q & 1) == 0);
+            } else if constexpr (KG == 1) {
+                mine = blk == (q & 3);
+            } else {
+                mine = blk == rr;
+            }
+            unroll<NCR>([&](auto r) { sel[rr][decltype(r)::value] = mine && rt == decltype(r)::value ? 1.0 : 0.0; });
+        });
         unroll<NU>([&](auto uc) {
             constexpr int u = decltype(uc)::value;
             unroll<RPL>([&](auto rc) {
@@ -698,32 +722,12 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
                 v += row_rotate<8>(v);
                 if constexpr (P == 4) v += row_rotate<4>(v);
                 acc[u][rr] = 0.0;
-                bool mine;
-                if constexpr (KG == 2) {
-                    mine = low_pair == ((q & 1) == 0); // groups 2q, 2q + 1: slots {0,1} or {2,3}
-                } else if constexpr (KG == 1) {
-                    mine = blk == (q & 3);
-                } else {
-                    mine = blk == rr;
-                }
-                if constexpr (inner) {
-                    C[u][rt] = mine ? C[u][rt] + v : C[u][rt];
-                } else {
-                    C[u][rt] = mine ? v : C[u][rt];
-                }
-                // one unit at a time: bounds the registers live at once
+                unroll<NCR>([&](auto r) {
+                    constexpr int ri = decltype(r)::value;
+                    C[u][ri] = fma(v, sel[rr][ri], C[u][ri]);
+                });
                 __builtin_amdgcn_sched_barrier(0);
             });
-        });
-    };
-    // species q's coefficient register, chosen by a wave-uniform branch
-    auto merge = [&](int q) {
-        const int rt = KG == 2 ? q >> 1 : KG == 1 ? q >> 2 : q;
-        unroll<NCR>([&](auto r) {
-            if (rt == decltype(r)::value) {
-                asm volatile("" ::: "memory"); // keeps the branch (no selects over every register)
-                merge_into(r, q);
-            }
         });
     };
 
@@ -761,7 +765,7 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
                 constexpr int g = decltype(gc)::value;
                 if (g >= groups0) return;
                 const double d2 = dbuf[GS * g];
-                double ev[ND][RPL];
+                double ev[ND > 0 ? ND : 1][RPL];
                 unroll<ND>([&](auto dc) {
                     unroll<RPL>([&](auto rc) {
                         ev[decltype(dc)::value][decltype(rc)::value] =
@@ -849,7 +853,7 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
                 // species-summed coefficients: the registers added, then the
                 // species' blocks of a register (KG 2: b and b ^ 2; KG 1: all
                 // four; KG 3 holds one species)
-                double cs[NU];
+                double cs[NU > 0 ? NU : 1];
                 unroll<NU>([&](auto uc) {
                     constexpr int u = decltype(uc)::value;
                     double v = C[u][0];
