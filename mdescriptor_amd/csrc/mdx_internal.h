@@ -209,8 +209,9 @@ struct PreparedBatch {
     std::vector<int32_t> types; // species index per atom (0 when species are ignored)
     std::vector<int32_t> atom_struct; // structure of each atom
     std::vector<int64_t> offsets;
-    // work items of the averaged SOAP modes (host copies outlive the async upload)
-    std::vector<int64_t> item_begin, struct_items;
+    // work items of the averaged SOAP modes and the folded rows' structure
+    // ranges (host copies outlive the async upload)
+    std::vector<int64_t> item_begin, struct_items, fold_items;
     int64_t most_images = 0;  // most binned images of one structure: no centre has more rows
     int max_images = 1;       // most periodic images of one structure
     int64_t chunk_bound = 0;  // LDS binning chunks if every structure took that path (a check of the summary)

@@ -320,6 +320,30 @@ __global__ __launch_bounds__(kBlock) void k_finalize_outer(const double* partial
     }
 }
 
+// Structure averages: the expansion leaves one partial row (width doubles)
+// per item of kItemCentres centres.  A structure of thousands of atoms has
+// hundreds of items, too many for the finalize kernels' one workgroup per
+// structure to walk (16 structures of 4,096 atoms: 1.1 ms), so they are
+// first folded in parallel: split z of structure s sums the structure's
+// items [z * per_split, (z + 1) * per_split) in order into folded row
+// s * splits + z (a split past the structure's items is zero), and the
+// finalize then walks the structure's splits.  The order of the sums is fixed,
+// so the result does not depend on the launch.
+constexpr int kFoldItems = 16; // items per split
+__global__ __launch_bounds__(kBlock) void k_fold_partials(const double* partial, int64_t width,
+                                                          const int64_t* struct_items, int64_t col_tiles,
+                                                          int splits, double* folded) {
+    const int64_t s = blockIdx.x / col_tiles;
+    const int64_t col = (blockIdx.x - s * col_tiles) * kBlock + threadIdx.x;
+    if (col >= width) return;
+    const int64_t ib = struct_items[s], ie = struct_items[s + 1];
+    const int64_t a = ib + static_cast<int64_t>(blockIdx.y) * kFoldItems;
+    const int64_t b = min(a + kFoldItems, ie);
+    double sum = 0.0;
+    for (int64_t it = a; it < b; ++it) sum += partial[it * width + col];
+    folded[(s * splits + blockIdx.y) * width + col] = sum;
+}
+
 size_t expand_lds_bytes(const mdx_soap_plan& p, int CH, int acc_words) {
     const size_t words = static_cast<size_t>(CH) * 4 + static_cast<size_t>(CH) * p.H + static_cast<size_t>(CH) * p.LN
         + static_cast<size_t>(p.coeff_size) + static_cast<size_t>(p.L) * p.n * p.n + 2 * static_cast<size_t>(p.LN)
@@ -414,20 +438,58 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
     int64_t* d_item_begin = nullptr;
     int64_t* d_struct_items = nullptr;
     double* d_partial = nullptr;
+    // folded partial rows (see k_fold_partials): splits per structure, the
+    // folded rows and their structure ranges
+    int fold_splits = 0;
+    size_t partial_width = 0;
+    double* d_folded = nullptr;
+    int64_t* d_fold_items = nullptr;
+    std::vector<int64_t>& fold_items_h = pb.fold_items;
     if (p.average != 0 && !block_inner) {
         const size_t inner_width = p.use_mfma ? static_cast<size_t>(mfma_coefficient_rows(p.Sc, p.n, p.compression)) * static_cast<size_t>(p.hpad)
                                               : static_cast<size_t>(d.C);
         const size_t width = p.average == 1 ? inner_width : static_cast<size_t>(d.F);
-        const size_t head = ((item_begin_h.size() + struct_items_h.size()) * sizeof(int64_t) + 255) & ~size_t(255);
-        scratch.reserve(head + static_cast<size_t>(items) * width * sizeof(double));
+        partial_width = width;
+        int64_t most_items = 0;
+        for (int64_t s = 0; s < pb.structures; ++s) {
+            most_items = std::max(most_items, struct_items_h[static_cast<size_t>(s) + 1] - struct_items_h[static_cast<size_t>(s)]);
+        }
+        if (most_items > 2 * kFoldItems) fold_splits = static_cast<int>((most_items + kFoldItems - 1) / kFoldItems);
+        fold_items_h.clear();
+        if (fold_splits > 0) {
+            for (int64_t s = 0; s <= pb.structures; ++s) fold_items_h.push_back(s * fold_splits);
+        }
+        const size_t head = ((item_begin_h.size() + struct_items_h.size() + fold_items_h.size()) * sizeof(int64_t) + 255) &
+                            ~size_t(255);
+        const size_t partial_bytes = (static_cast<size_t>(items) * width * sizeof(double) + 255) & ~size_t(255);
+        const size_t folded_bytes = static_cast<size_t>(pb.structures) * static_cast<size_t>(fold_splits) * width * sizeof(double);
+        scratch.reserve(head + partial_bytes + folded_bytes);
         d_item_begin = scratch.as<int64_t>();
         d_struct_items = d_item_begin + item_begin_h.size();
+        d_fold_items = d_struct_items + struct_items_h.size();
         d_partial = reinterpret_cast<double*>(static_cast<char*>(scratch.ptr) + head);
+        if (fold_splits > 0) d_folded = reinterpret_cast<double*>(static_cast<char*>(scratch.ptr) + head + partial_bytes);
         MDX_HIP(hipMemcpyAsync(d_item_begin, item_begin_h.data(), item_begin_h.size() * sizeof(int64_t),
                                hipMemcpyHostToDevice, stream));
         MDX_HIP(hipMemcpyAsync(d_struct_items, struct_items_h.data(), struct_items_h.size() * sizeof(int64_t),
                                hipMemcpyHostToDevice, stream));
+        if (fold_splits > 0) {
+            MDX_HIP(hipMemcpyAsync(d_fold_items, fold_items_h.data(), fold_items_h.size() * sizeof(int64_t),
+                                   hipMemcpyHostToDevice, stream));
+        }
     }
+    // the partial rows the finalize kernels walk, folded first where
+    // structures have many items
+    auto fold = [&]() -> std::pair<const double*, const int64_t*> {
+        if (fold_splits == 0) return {d_partial, d_struct_items};
+        const int64_t col_tiles = (static_cast<int64_t>(partial_width) + kBlock - 1) / kBlock;
+        hipLaunchKernelGGL(k_fold_partials, dim3(static_cast<unsigned>(col_tiles * pb.structures),
+                                                 static_cast<unsigned>(fold_splits)),
+                           dim3(kBlock), 0, stream, d_partial, static_cast<int64_t>(partial_width), d_struct_items,
+                           col_tiles, fold_splits, d_folded);
+        MDX_HIP(hipGetLastError());
+        return {d_folded, d_fold_items};
+    };
 
     // launch in slices so cancellation is polled between launches (and, for
     // an atom-level run, so the caller can copy finished rows out meanwhile)
@@ -543,7 +605,8 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
                                        p.features * p.out_dtype);
             }
         } else if (p.average != 0) {
-            launch_mfma_finalize(stream, pb, tab, md, d_partial, d_struct_items, out_device, pitch_bytes);
+            const auto rows_in = fold();
+            launch_mfma_finalize(stream, pb, tab, md, rows_in.first, rows_in.second, out_device, pitch_bytes);
         }
         if (events != nullptr) MDX_HIP(hipEventRecord(events[4], stream));
         if (timing != nullptr) {
@@ -582,13 +645,14 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
     if (events != nullptr) MDX_HIP(hipEventRecord(events[3], stream));
     if (p.average != 0) {
         const unsigned grid = static_cast<unsigned>(std::min<int64_t>(pb.structures, 1 << 20));
+        const auto rows_in = fold();
         if (p.average == 1) {
             hipLaunchKernelGGL(k_finalize_inner, dim3(grid), dim3(kBlock), static_cast<size_t>(d.C) * sizeof(double),
-                               stream, d_partial, d_struct_items, pb.d_offsets.as<int64_t>(), pb.structures, d,
+                               stream, rows_in.first, rows_in.second, pb.d_offsets.as<int64_t>(), pb.structures, d,
                                p.d_ps_pref.as<double>(), p.d_feat_a.as<int32_t>(), p.d_feat_b.as<int32_t>(), out_device,
                                pitch_bytes);
         } else {
-            hipLaunchKernelGGL(k_finalize_outer, dim3(grid), dim3(kBlock), 0, stream, d_partial, d_struct_items,
+            hipLaunchKernelGGL(k_finalize_outer, dim3(grid), dim3(kBlock), 0, stream, rows_in.first, rows_in.second,
                                pb.d_offsets.as<int64_t>(), pb.structures, d, out_device, pitch_bytes);
         }
         MDX_HIP(hipGetLastError());
