@@ -411,9 +411,12 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
     const bool inner_fits = largest_structure <= kBlockSmallAtoms || p.block_forced ||
                             pb.structures >= 4 * static_cast<int64_t>(device_compute_units());
     const bool block = p.block_waves > 0 &&
-                       (p.average == 0 || (p.average == 1 && p.weighted == 0 && p.compression == 0 && inner_fits)) &&
+                       (p.average == 0 || (p.average == 1 && p.weighted == 0 && p.compression == 0)) &&
                        g.row_bound < kQuadMaxRows;
-    const bool block_inner = block && p.average == 1;
+    const bool block_inner = block && p.average == 1 && inner_fits;
+    // other inner averages on that kernel: runs of a structure's centres
+    // into partial rows, folded, then a launch of one workgroup per structure
+    const bool block_runs = block && p.average == 1 && !inner_fits;
 
     // work items
     std::vector<int64_t>& item_begin_h = pb.item_begin;
@@ -448,7 +451,9 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
     if (p.average != 0 && !block_inner) {
         const size_t inner_width = p.use_mfma ? static_cast<size_t>(mfma_coefficient_rows(p.Sc, p.n, p.compression)) * static_cast<size_t>(p.hpad)
                                               : static_cast<size_t>(d.C);
-        const size_t width = p.average == 1 ? inner_width : static_cast<size_t>(d.F);
+        const size_t width = block_runs ? static_cast<size_t>(block_partial_width(p.l_max, p.block_ncr))
+                             : p.average == 1 ? inner_width
+                                              : static_cast<size_t>(d.F);
         partial_width = width;
         int64_t most_items = 0;
         for (int64_t s = 0; s < pb.structures; ++s) {
@@ -542,6 +547,7 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
         tab.bin_image = g.bin_image.as<int32_t>();
         tab.images = pb.d_images.as<ImageDesc>();
         const int tt = mfma_template_tiles(p.tiles);
+        BlockArgs block_args{};
         if (events != nullptr) MDX_HIP(hipEventRecord(events[2], stream));
         for (int64_t base = 0; base < items; base += slice) {
             if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
@@ -563,7 +569,8 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
                 ba.F = p.features;
                 ba.item_base = base;
                 ba.items = count;
-                ba.struct_offsets = block_inner ? pb.d_offsets.as<int64_t>() : nullptr;
+                ba.struct_offsets = block_inner ? pb.d_offsets.as<int64_t>() : block_runs ? d_item_begin : nullptr;
+                ba.partial_out = block_runs ? d_partial : nullptr;
                 ba.small_structures = block_inner && largest_structure <= kBlockSmallAtoms ? 1 : 0;
                 ba.summed = p.compression == 2 ? 1 : 0;
                 if (p.weighted != 0) {
@@ -581,6 +588,7 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
                 }
                 ba.out = out_device;
                 ba.pitch = pitch_bytes;
+                block_args = ba;
                 launch_block_expand(stream, p.l_max, p.block_kg, p.block_ncr, ba, count);
             } else if (quad) {
                 launch_quad_expand(stream, p.quad_waves, p.quad_kg, p.quad_instr, pb, g, p.d_quad_lanes.as<QuadLane>(),
@@ -594,7 +602,18 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
             if (hook) (*on_slice)(base, count);
         }
         if (events != nullptr) MDX_HIP(hipEventRecord(events[3], stream));
-        if (block_inner) {
+        if (block_runs) {
+            // the structures' rows from their folded partial rows
+            const auto rows_in = fold();
+            BlockArgs fa = block_args;
+            fa.partial_out = nullptr;
+            fa.partial_in = rows_in.first;
+            fa.part_items = rows_in.second;
+            fa.struct_offsets = pb.d_offsets.as<int64_t>();
+            fa.item_base = 0;
+            fa.items = pb.structures;
+            launch_block_expand(stream, p.l_max, p.block_kg, p.block_ncr, fa, pb.structures);
+        } else if (block_inner) {
             // rows of structures without atoms (the expansion visits none of them)
             bool empty = false;
             for (int64_t st = 0; st < pb.structures && !empty; ++st) {

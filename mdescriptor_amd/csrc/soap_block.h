@@ -12,8 +12,12 @@ namespace mdx {
 // average) from a centre-by-centre stream; the same from a species-major
 // stream over the structure's pairs (structures of at most 64 atoms); a row
 // per centre with weighted neighbours; a row per centre of mu1nu1 features
-// (each channel against the species-summed channels).
-constexpr int kBlockRows = 0, kBlockInner = 1, kBlockInnerSmall = 2, kBlockRowsWeighted = 3, kBlockRowsSummed = 4;
+// (each channel against the species-summed channels); inner averages of
+// large structures in two launches: runs of a structure's centres leave
+// their summed coefficient registers in partial rows, then a row per
+// structure from the sum of its partial rows.
+constexpr int kBlockRows = 0, kBlockInner = 1, kBlockInnerSmall = 2, kBlockRowsWeighted = 3, kBlockRowsSummed = 4,
+              kBlockInnerRuns = 5, kBlockInnerFinal = 6;
 constexpr int kBlockSmallAtoms = 64;
 
 // Launch arguments (one struct, passed by value).
@@ -45,6 +49,15 @@ struct BlockArgs {
     const int32_t* bin_image;            // image of each binned image (w0: the exact self pair)
     const ImageDesc* images;             // image table (integer shifts)
     int summed;                          // mu1nu1: spectrum against the species-summed coefficients
+    // inner averages in two launches: the runs' launch writes partial_out
+    // (struct_offsets = first centre of each run, + end), the final launch
+    // reads partial_in (items = structures, struct_offsets = the batch's
+    // atom offsets, part_items = each structure's partial rows, + end).  A
+    // partial row holds every wavefront's coefficient registers, lane-major
+    // (block_partial_width doubles).
+    double* partial_out;
+    const double* partial_in;
+    const int64_t* part_items;
     void* out;
     int64_t pitch;              // bytes between output rows
 };
@@ -66,6 +79,8 @@ struct BlockPlanHost {
 bool block_plan_tables(int S, int n, int l_max, int out_dtype, int compression, const std::vector<double>& beta_scaled,
                        const std::vector<double>& pref, const std::vector<double>& expo, BlockPlanHost& out);
 void launch_block_expand(hipStream_t stream, int l_max, int kg, int ncr, const BlockArgs& a, int64_t count);
+// doubles in one partial row of the runs' launch
+int64_t block_partial_width(int l_max, int ncr);
 // Zero the rows of the structures without atoms (structure averages; the
 // expansion writes only the rows of structures it visits).
 void launch_block_zero_rows(hipStream_t stream, const int64_t* struct_offsets, int64_t structures, void* out,

@@ -430,7 +430,18 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
     // structure averages whole structures, whose centres are consecutive
     const int64_t work_first = a.item_base + static_cast<int64_t>(blockIdx.x) * a.per_block;
     const int64_t work_last = min(work_first + a.per_block, a.item_base + a.items);
-    constexpr bool inner = MODE == kBlockInner || MODE == kBlockInnerSmall; // rows of structure averages
+    // rows of structure averages (the runs' launch sums a run of a structure's
+    // centres the same way, into a partial row)
+    constexpr bool inner = MODE == kBlockInner || MODE == kBlockInnerSmall || MODE == kBlockInnerRuns;
+    constexpr bool kRuns = MODE == kBlockInnerRuns;
+    constexpr bool kFinal = MODE == kBlockInnerFinal;
+    // this wavefront's registers in a partial row, and the row's width
+    constexpr int kPartBase = [] {
+        int u = 0;
+        for (int w = 0; w < W; ++w) u += units_total(PL::own(w), L);
+        return u;
+    }() * NCR * kWaveThreads;
+    constexpr int64_t kPartWidth = static_cast<int64_t>(units_total(0xffffffffu, L)) * NCR * kWaveThreads;
     constexpr bool kWeighted = MODE == kBlockRowsWeighted; // neighbour weights scale the harmonic seeds
     constexpr bool kSummed = MODE == kBlockRowsSummed;     // mu1nu1: against the species-summed coefficients
     // structures of at most a wavefront of atoms: pairs streamed species-major
@@ -621,6 +632,194 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
         return s;
     };
 
+    // accumulators and coefficient registers
+    double acc[NU > 0 ? NU : 1][RPL];
+    double C[NU > 0 ? NU : 1][NCR];
+    unroll<NU>([&](auto u) {
+        unroll<RPL>([&](auto r) { acc[decltype(u)::value][decltype(r)::value] = 0.0; });
+        unroll<NCR>([&](auto r) { C[decltype(u)::value][decltype(r)::value] = 0.0; });
+    });
+    int cur = -1; // species of the accumulators
+
+    // sum the phases of every accumulator and add species q's radial groups
+    // into its block slots of the coefficient registers, which start every
+    // output row at zero (a species merges once per centre; a structure
+    // average adds its centres' sums): per lane and register a factor of 1
+    // (the lane's block slot and the register belong to q) or 0, and one fma
+    // per register
+    auto merge = [&](int q) {
+        const int rt = KG == 2 ? q >> 1 : KG == 1 ? q >> 2 : q;
+        double sel[RPL][NCR];
+        unroll<RPL>([&](auto rc) {
+            constexpr int rr = decltype(rc)::value;
+            bool mine;
+            if constexpr (KG == 2) {
+                mine = low_pair == ((q & 1) == 0);
+            } else if constexpr (KG == 1) {
+                mine = blk == (q & 3);
+            } else {
+                mine = blk == rr;
+            }
+            unroll<NCR>([&](auto r) { sel[rr][decltype(r)::value] = mine && rt == decltype(r)::value ? 1.0 : 0.0; });
+        });
+        unroll<NU>([&](auto uc) {
+            constexpr int u = decltype(uc)::value;
+            unroll<RPL>([&](auto rc) {
+                constexpr int rr = decltype(rc)::value;
+                double v = acc[u][rr];
+                v += row_rotate<8>(v);
+                if constexpr (P == 4) v += row_rotate<4>(v);
+                acc[u][rr] = 0.0;
+                unroll<NCR>([&](auto r) {
+                    constexpr int ri = decltype(r)::value;
+                    C[u][ri] = fma(v, sel[rr][ri], C[u][ri]);
+                });
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        });
+    };
+
+    const int64_t F = a.F;
+    // row end: C <- (S_lm C)^T beta^T scaled by scale0, the power spectrum of
+    // the owned degrees to output row row0, and C back to zero
+    auto row_end = [&](int64_t row0, double scale0) {
+        // fold: C <- (S_lm C)^T beta^T in place
+        unroll<L>([&](auto lc) {
+            constexpr int l = decltype(lc)::value;
+            if constexpr ((kOwn >> l) & 1u) {
+                constexpr int d = degrees_before(kOwn, l);
+                constexpr int u0 = units_before(kOwn, l);
+                constexpr int loff = 4 * units_before(0xffffffffu, l);
+                unroll<cgroups(l)>([&](auto cc) {
+                    constexpr int cg = decltype(cc)::value;
+                    const double sc = s_scale[loff + 4 * cg + lane % 4] * scale0;
+                    unroll<NCR>([&](auto rc) {
+                        constexpr int r = decltype(rc)::value;
+                        const double v = C[u0 + cg][r] * sc;
+                        double c = mfma4(v, bt[d][0], 0.0);
+                        if constexpr (KG == 2) {
+                            c = mfma4(swap_blocks(v), bt[d][1], c);
+                        } else if constexpr (KG == 3) {
+                            c = mfma4(row_rotate<12>(v), bt[d][1], c); // block b takes b + 1
+                            c = mfma4(row_rotate<8>(v), bt[d][2], c);  // b + 2
+                            c = mfma4(row_rotate<4>(v), bt[d][3], c);  // b + 3
+                        }
+                        C[u0 + cg][r] = c;
+                        __builtin_amdgcn_sched_barrier(0);
+                    });
+                });
+            }
+        });
+        // power spectrum of the owned degrees, written to the centre's row
+        char* row = static_cast<char*>(a.out) + row0 * a.pitch;
+        const __amdgpu_buffer_rsrc_t rsrc =
+            __builtin_amdgcn_make_buffer_rsrc(row, 0, static_cast<int>(F * ES), 0x00020000);
+        // one 4-value store per lane and value of a Gram tile
+        auto store_tile = [&](const d4& D, const int* fb, const int* fs, int l) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const double v = D[r]; // the coefficients carry sqrt(pi sqrt(8/(2l+1)))
+                const int off = fb[r] + l * fs[r];
+                if constexpr (ES == 4) {
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(static_cast<float>(v)), rsrc, off, 0, 0);
+                } else {
+                    typedef int i2v __attribute__((ext_vector_type(2)));
+                    const i2v bits = {__double2loint(v), __double2hiint(v)};
+                    __builtin_amdgcn_raw_buffer_store_b64(bits, rsrc, off, 0, 0);
+                }
+            }
+        };
+        if constexpr (kSummed) {
+            // species-summed coefficients: the registers added, then the
+            // species' blocks of a register (KG 2: b and b ^ 2; KG 1: all
+            // four; KG 3 holds one species)
+            double cs[NU > 0 ? NU : 1];
+            unroll<NU>([&](auto uc) {
+                constexpr int u = decltype(uc)::value;
+                double v = C[u][0];
+                unroll<NCR - 1>([&](auto rc) { v += C[u][decltype(rc)::value + 1]; });
+                if constexpr (KG == 2) {
+                    v += row_rotate<8>(v);
+                } else if constexpr (KG == 1) {
+                    v += row_rotate<8>(v);
+                    v += row_rotate<4>(v);
+                }
+                cs[u] = v;
+            });
+            unroll<NCR>([&](auto ic) {
+                constexpr int ri = decltype(ic)::value;
+                int fb[4], fs[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int o = s_ps[(ri * 4 + r) * kWaveThreads + lane];
+                    fb[r] = o >> kStrideBits; // bytes
+                    fs[r] = (o & ((1 << kStrideBits) - 1)) * ES;
+                }
+                unroll<L>([&](auto lc) {
+                    constexpr int l = decltype(lc)::value;
+                    if constexpr ((kOwn >> l) & 1u) {
+                        constexpr int u0 = units_before(kOwn, l);
+                        d4 D = {0.0, 0.0, 0.0, 0.0};
+                        unroll<cgroups(l)>([&](auto cc) {
+                            constexpr int cg = decltype(cc)::value;
+                            D = mfma(C[u0 + cg][ri], cs[u0 + cg], D);
+                        });
+                        store_tile(D, fb, fs, l);
+                    }
+                });
+            });
+        }
+        int pair = 0;
+        unroll<NCR>([&](auto ic) {
+            constexpr int ri = decltype(ic)::value;
+            unroll<NCR>([&](auto jc) {
+                constexpr int rj = decltype(jc)::value;
+                if constexpr (!kSummed && ri <= rj) {
+                    int fb[4], fs[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int o = s_ps[(pair * 4 + r) * kWaveThreads + lane];
+                        fb[r] = o >> kStrideBits; // bytes
+                        fs[r] = (o & ((1 << kStrideBits) - 1)) * ES;
+                    }
+                    unroll<L>([&](auto lc) {
+                        constexpr int l = decltype(lc)::value;
+                        if constexpr ((kOwn >> l) & 1u) {
+                            constexpr int u0 = units_before(kOwn, l);
+                            d4 D = {0.0, 0.0, 0.0, 0.0};
+                            unroll<cgroups(l)>([&](auto cc) {
+                                constexpr int cg = decltype(cc)::value;
+                                D = mfma(C[u0 + cg][ri], C[u0 + cg][rj], D);
+                            });
+                            store_tile(D, fb, fs, l);
+                        }
+                    });
+                    ++pair;
+                }
+            });
+        });
+        unroll<NU>([&](auto u) { unroll<NCR>([&](auto r) { C[decltype(u)::value][decltype(r)::value] = 0.0; }); });
+    };
+
+    if constexpr (kFinal) {
+        // structure rows from the sums of their partial rows (in order)
+        for (int64_t s = work_first; s < work_last; ++s) {
+            const int64_t r0 = uniform64(a.part_items[s]), r1 = uniform64(a.part_items[s + 1]);
+            const double* part = a.partial_in + kPartBase + lane;
+            unroll<NU>([&](auto uc) {
+                unroll<NCR>([&](auto rc) {
+                    constexpr int u = decltype(uc)::value, r = decltype(rc)::value;
+                    double v = 0.0;
+                    for (int64_t it = r0; it < r1; ++it) v += part[it * kPartWidth + (u * NCR + r) * kWaveThreads];
+                    C[u][r] = v;
+                });
+            });
+            const int64_t atoms = uniform64(a.struct_offsets[s + 1]) - uniform64(a.struct_offsets[s]);
+            row_end(s, atoms > 0 ? 1.0 / static_cast<double>(atoms) : 0.0);
+        }
+        return;
+    }
+
     if (!kSpeciesMajor && item_first < item_last) prefetch_centre(item_first);
     Stage s0 = next_stage(); // chunk k (contraction)
     Stage s1 = next_stage(); // chunk k + 1 (harmonics)
@@ -684,54 +883,6 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
     load_positions(s1);
     __syncthreads();
 
-    // accumulators and coefficient registers
-    double acc[NU > 0 ? NU : 1][RPL];
-    double C[NU > 0 ? NU : 1][NCR];
-    unroll<NU>([&](auto u) {
-        unroll<RPL>([&](auto r) { acc[decltype(u)::value][decltype(r)::value] = 0.0; });
-        unroll<NCR>([&](auto r) { C[decltype(u)::value][decltype(r)::value] = 0.0; });
-    });
-    int cur = -1; // species of the accumulators
-
-    // sum the phases of every accumulator and add species q's radial groups
-    // into its block slots of the coefficient registers, which start every
-    // output row at zero (a species merges once per centre; a structure
-    // average adds its centres' sums): per lane and register a factor of 1
-    // (the lane's block slot and the register belong to q) or 0, and one fma
-    // per register
-    auto merge = [&](int q) {
-        const int rt = KG == 2 ? q >> 1 : KG == 1 ? q >> 2 : q;
-        double sel[RPL][NCR];
-        unroll<RPL>([&](auto rc) {
-            constexpr int rr = decltype(rc)::value;
-            bool mine;
-            if constexpr (KG == 2) {
-                mine = low_pair == ((q & 1) == 0);
-            } else if constexpr (KG == 1) {
-                mine = blk == (q & 3);
-            } else {
-                mine = blk == rr;
-            }
-            unroll<NCR>([&](auto r) { sel[rr][decltype(r)::value] = mine && rt == decltype(r)::value ? 1.0 : 0.0; });
-        });
-        unroll<NU>([&](auto uc) {
-            constexpr int u = decltype(uc)::value;
-            unroll<RPL>([&](auto rc) {
-                constexpr int rr = decltype(rc)::value;
-                double v = acc[u][rr];
-                v += row_rotate<8>(v);
-                if constexpr (P == 4) v += row_rotate<4>(v);
-                acc[u][rr] = 0.0;
-                unroll<NCR>([&](auto r) {
-                    constexpr int ri = decltype(r)::value;
-                    C[u][ri] = fma(v, sel[rr][ri], C[u][ri]);
-                });
-                __builtin_amdgcn_sched_barrier(0);
-            });
-        });
-    };
-
-    const int64_t F = a.F;
     int k = 0;
     while (uniform64(s0.centre) >= 0) {
         const int buf = k & 1;
@@ -797,128 +948,25 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
         }
         // ------------------------------------ row end: fold, power spectrum
         if (last0) {
-            // an average's coefficients carry 1 / (atoms of the structure)
-            double scale0 = 1.0;
-            if constexpr (inner) {
-                scale0 = 1.0 / static_cast<double>(uniform64(a.struct_offsets[row0 + 1]) -
-                                                   uniform64(a.struct_offsets[row0]));
-            }
-            // fold: C <- (S_lm C)^T beta^T in place
-            unroll<L>([&](auto lc) {
-                constexpr int l = decltype(lc)::value;
-                if constexpr ((kOwn >> l) & 1u) {
-                    constexpr int d = degrees_before(kOwn, l);
-                    constexpr int u0 = units_before(kOwn, l);
-                    constexpr int loff = 4 * units_before(0xffffffffu, l);
-                    unroll<cgroups(l)>([&](auto cc) {
-                        constexpr int cg = decltype(cc)::value;
-                        const double sc = s_scale[loff + 4 * cg + lane % 4] * scale0;
-                        unroll<NCR>([&](auto rc) {
-                            constexpr int r = decltype(rc)::value;
-                            const double v = C[u0 + cg][r] * sc;
-                            double c = mfma4(v, bt[d][0], 0.0);
-                            if constexpr (KG == 2) {
-                                c = mfma4(swap_blocks(v), bt[d][1], c);
-                            } else if constexpr (KG == 3) {
-                                c = mfma4(row_rotate<12>(v), bt[d][1], c); // block b takes b + 1
-                                c = mfma4(row_rotate<8>(v), bt[d][2], c);  // b + 2
-                                c = mfma4(row_rotate<4>(v), bt[d][3], c);  // b + 3
-                            }
-                            C[u0 + cg][r] = c;
-                            __builtin_amdgcn_sched_barrier(0);
-                        });
-                    });
-                }
-            });
-            // power spectrum of the owned degrees, written to the centre's row
-            char* row = static_cast<char*>(a.out) + row0 * a.pitch;
-            const __amdgpu_buffer_rsrc_t rsrc =
-                __builtin_amdgcn_make_buffer_rsrc(row, 0, static_cast<int>(F * ES), 0x00020000);
-            // one 4-value store per lane and value of a Gram tile
-            auto store_tile = [&](const d4& D, const int* fb, const int* fs, int l) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const double v = D[r]; // the coefficients carry sqrt(pi sqrt(8/(2l+1)))
-                    const int off = fb[r] + l * fs[r];
-                    if constexpr (ES == 4) {
-                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(static_cast<float>(v)), rsrc, off, 0, 0);
-                    } else {
-                        typedef int i2v __attribute__((ext_vector_type(2)));
-                        const i2v bits = {__double2loint(v), __double2hiint(v)};
-                        __builtin_amdgcn_raw_buffer_store_b64(bits, rsrc, off, 0, 0);
-                    }
-                }
-            };
-            if constexpr (kSummed) {
-                // species-summed coefficients: the registers added, then the
-                // species' blocks of a register (KG 2: b and b ^ 2; KG 1: all
-                // four; KG 3 holds one species)
-                double cs[NU > 0 ? NU : 1];
+            if constexpr (kRuns) {
+                // the run's summed coefficient registers to its partial row
+                double* part = a.partial_out + row0 * kPartWidth + kPartBase + lane;
                 unroll<NU>([&](auto uc) {
-                    constexpr int u = decltype(uc)::value;
-                    double v = C[u][0];
-                    unroll<NCR - 1>([&](auto rc) { v += C[u][decltype(rc)::value + 1]; });
-                    if constexpr (KG == 2) {
-                        v += row_rotate<8>(v);
-                    } else if constexpr (KG == 1) {
-                        v += row_rotate<8>(v);
-                        v += row_rotate<4>(v);
-                    }
-                    cs[u] = v;
-                });
-                unroll<NCR>([&](auto ic) {
-                    constexpr int ri = decltype(ic)::value;
-                    int fb[4], fs[4];
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int o = s_ps[(ri * 4 + r) * kWaveThreads + lane];
-                        fb[r] = o >> kStrideBits; // bytes
-                        fs[r] = (o & ((1 << kStrideBits) - 1)) * ES;
-                    }
-                    unroll<L>([&](auto lc) {
-                        constexpr int l = decltype(lc)::value;
-                        if constexpr ((kOwn >> l) & 1u) {
-                            constexpr int u0 = units_before(kOwn, l);
-                            d4 D = {0.0, 0.0, 0.0, 0.0};
-                            unroll<cgroups(l)>([&](auto cc) {
-                                constexpr int cg = decltype(cc)::value;
-                                D = mfma(C[u0 + cg][ri], cs[u0 + cg], D);
-                            });
-                            store_tile(D, fb, fs, l);
-                        }
+                    unroll<NCR>([&](auto rc) {
+                        constexpr int u = decltype(uc)::value, r = decltype(rc)::value;
+                        part[(u * NCR + r) * kWaveThreads] = C[u][r];
+                        C[u][r] = 0.0;
                     });
                 });
+            } else {
+                // an average's coefficients carry 1 / (atoms of the structure)
+                double scale0 = 1.0;
+                if constexpr (inner) {
+                    scale0 = 1.0 / static_cast<double>(uniform64(a.struct_offsets[row0 + 1]) -
+                                                       uniform64(a.struct_offsets[row0]));
+                }
+                row_end(row0, scale0);
             }
-            int pair = 0;
-            unroll<NCR>([&](auto ic) {
-                constexpr int ri = decltype(ic)::value;
-                unroll<NCR>([&](auto jc) {
-                    constexpr int rj = decltype(jc)::value;
-                    if constexpr (!kSummed && ri <= rj) {
-                        int fb[4], fs[4];
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            const int o = s_ps[(pair * 4 + r) * kWaveThreads + lane];
-                            fb[r] = o >> kStrideBits; // bytes
-                            fs[r] = (o & ((1 << kStrideBits) - 1)) * ES;
-                        }
-                        unroll<L>([&](auto lc) {
-                            constexpr int l = decltype(lc)::value;
-                            if constexpr ((kOwn >> l) & 1u) {
-                                constexpr int u0 = units_before(kOwn, l);
-                                d4 D = {0.0, 0.0, 0.0, 0.0};
-                                unroll<cgroups(l)>([&](auto cc) {
-                                    constexpr int cg = decltype(cc)::value;
-                                    D = mfma(C[u0 + cg][ri], C[u0 + cg][rj], D);
-                                });
-                                store_tile(D, fb, fs, l);
-                            }
-                        });
-                        ++pair;
-                    }
-                });
-            });
-            unroll<NU>([&](auto u) { unroll<NCR>([&](auto r) { C[decltype(u)::value][decltype(r)::value] = 0.0; }); });
         }
         // ---------------------------------------- harmonics of chunk k + 1
         if (kHarm && centre1 >= 0) {
@@ -944,7 +992,8 @@ constexpr int ps_tiles(int ncr, bool summed) { return summed ? ncr : ncr * (ncr 
 // distance function (pow) needs the registers of a fifth, and for mu1nu1,
 // whose summed coefficients stay live beside the registers
 template <int LM, int KG, int NCR, int ES, int MODE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE >= kBlockRowsWeighted ? 4 : 5))) void
+__global__ __launch_bounds__(256) __attribute__((
+    amdgpu_waves_per_eu(MODE == kBlockRowsWeighted || MODE == kBlockRowsSummed ? 4 : 5))) void
 k_soap_block(BlockArgs a) {
     using PL = BlockPlan<LM, KG>;
     // staging buffers, d2, exp table, padded S_lm table, power-spectrum
@@ -1021,7 +1070,9 @@ void launch_shape(hipStream_t stream, const BlockArgs& a, int64_t count) {
     args.per_block = std::max<int64_t>(least, (count + target - 1) / target);
     const unsigned grid = static_cast<unsigned>((count + args.per_block - 1) / args.per_block);
     const dim3 threads(PL::T * kWaveThreads);
-    const int mode = a.struct_offsets != nullptr ? (a.small_structures ? kBlockInnerSmall : kBlockInner)
+    const int mode = a.partial_in != nullptr    ? kBlockInnerFinal
+                     : a.partial_out != nullptr ? kBlockInnerRuns
+                     : a.struct_offsets != nullptr ? (a.small_structures ? kBlockInnerSmall : kBlockInner)
                      : a.species_w != nullptr ? kBlockRowsWeighted
                      : a.summed != 0          ? kBlockRowsSummed
                                               : kBlockRows;
@@ -1041,6 +1092,10 @@ void launch_shape(hipStream_t stream, const BlockArgs& a, int64_t count) {
         launch(std::integral_constant<int, kBlockInnerSmall>{});
     } else if (mode == kBlockRowsWeighted) {
         launch(std::integral_constant<int, kBlockRowsWeighted>{});
+    } else if (mode == kBlockInnerRuns) {
+        launch(std::integral_constant<int, kBlockInnerRuns>{});
+    } else if (mode == kBlockInnerFinal) {
+        launch(std::integral_constant<int, kBlockInnerFinal>{});
     } else {
         launch(std::integral_constant<int, kBlockRowsSummed>{});
     }
@@ -1073,6 +1128,10 @@ const ShapeEntry* find_shape(int l_max, int kg, int ncr) {
 int coefficient_registers(int S, int kg) { return kg == 3 ? S : (S * kg + 3) / 4; }
 
 } // namespace
+
+int64_t block_partial_width(int l_max, int ncr) {
+    return static_cast<int64_t>(units_total(0xffffffffu, l_max + 1)) * ncr * kWaveThreads;
+}
 
 bool block_plan_tables(int S, int n, int l_max, int out_dtype, int compression, const std::vector<double>& beta_scaled,
                        const std::vector<double>& pref, const std::vector<double>& expo, BlockPlanHost& out) {

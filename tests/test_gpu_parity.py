@@ -97,10 +97,11 @@ def test_every_expansion_kernel_matches(hip_context, oracle, monkeypatch, kernel
 
 def test_default_plan_runs_the_block_kernel(hip_context, oracle):
     work = workloads.config(2, "small")
-    for average, tiles in (("off", -1004), ("inner", -4), ("outer", -4)):
+    for average, tiles in (("off", -1004), ("inner", -1004), ("outer", -4)):
         _, timing = _check(hip_context, oracle, work.batch, work.params, average, "float32")
-        # four wavefronts for n_max 8, l_max 6; outer averages, and inner
-        # averages of two 512-atom structures (too few workgroups), on the
+        # four wavefronts for n_max 8, l_max 6; inner averages of two 512-atom
+        # structures (too few for a workgroup each) as runs of centres into
+        # partial rows and a launch per structure; outer averages on the
         # 4x4-block kernel
         assert timing["expansion_tiles"] == tiles
     molecules = workloads.config(3, "small")
