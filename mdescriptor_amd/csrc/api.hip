@@ -657,17 +657,21 @@ int mdx_hip_soap_plan_create(mdx_hip_ctx* ctx, const mdx_soap_params* params, md
             }
             // register-coefficient kernel: GTO basis; atom-level rows with
             // compression off, crossover (weighted or not) or mu1nu1
-            // (unweighted), or unweighted inner structure averages without
+            // (unweighted), the same rows as float64 partial rows of an outer
+            // average, or unweighted inner structure averages without
             // compression; a compiled (l_max, radial groups, species) shape.
             // It keeps its coefficients in registers, so the tile kernel's LDS
             // limit does not apply to it
             const int cm = plan->compression;
-            const bool block_rows = p.average == 0 && (cm == 0 || cm == 3 || (cm == 2 && plan->weighted == 0));
+            const bool block_rows = (p.average == 0 || p.average == 2) &&
+                                    (cm == 0 || cm == 3 || (cm == 2 && plan->weighted == 0));
             const bool block_inner = p.average == 1 && cm == 0 && plan->weighted == 0;
             const bool block_options = plan->radial_basis == 0 && (block_rows || block_inner);
             if (block_options && quad_range && (choice == "auto" || choice == "block")) {
                 mdx::BlockPlanHost bp;
-                if (mdx::block_plan_tables(plan->S, n, p.l_max, p.out_dtype, cm, beta, pref, expo, bp)) {
+                // an outer average's rows are float64 partial rows
+                const int row_dtype = p.average == 2 ? 8 : p.out_dtype;
+                if (mdx::block_plan_tables(plan->S, n, p.l_max, row_dtype, cm, beta, pref, expo, bp)) {
                     plan->block_waves = bp.waves;
                     plan->block_kg = bp.kg;
                     plan->block_ncr = bp.ncr;

@@ -320,25 +320,27 @@ __global__ __launch_bounds__(kBlock) void k_finalize_outer(const double* partial
     }
 }
 
-// Structure averages: the expansion leaves one partial row (width doubles)
-// per item of kItemCentres centres.  A structure of thousands of atoms has
-// hundreds of items, too many for the finalize kernels' one workgroup per
-// structure to walk (16 structures of 4,096 atoms: 1.1 ms), so they are
-// first folded in parallel: split z of structure s sums the structure's
-// items [z * per_split, (z + 1) * per_split) in order into folded row
-// s * splits + z (a split past the structure's items is zero), and the
-// finalize then walks the structure's splits.  The order of the sums is fixed,
-// so the result does not depend on the launch.
-constexpr int kFoldItems = 16; // items per split
+// Structure averages: the expansion leaves partial rows (width doubles),
+// one per item of kItemCentres centres or one per centre.  A structure of
+// thousands of atoms has hundreds of them or more, too many for the finalize
+// kernels' one workgroup per structure to walk (16 structures of 4,096
+// atoms: 1.1 ms), so they are first folded in parallel: split z of
+// structure s sums the structure's rows [z * per_split, (z + 1) * per_split)
+// in order into folded row s * splits + z (a split past the structure's rows
+// is zero), and the finalize then walks the structure's splits (at most
+// kFoldSplits).  The order of the sums is fixed, so the result does not
+// depend on the launch.
+constexpr int kFoldItems = 16;  // rows per split, at least
+constexpr int kFoldSplits = 32; // splits per structure, at most
 __global__ __launch_bounds__(kBlock) void k_fold_partials(const double* partial, int64_t width,
                                                           const int64_t* struct_items, int64_t col_tiles,
-                                                          int splits, double* folded) {
+                                                          int splits, int64_t per_split, double* folded) {
     const int64_t s = blockIdx.x / col_tiles;
     const int64_t col = (blockIdx.x - s * col_tiles) * kBlock + threadIdx.x;
     if (col >= width) return;
     const int64_t ib = struct_items[s], ie = struct_items[s + 1];
-    const int64_t a = ib + static_cast<int64_t>(blockIdx.y) * kFoldItems;
-    const int64_t b = min(a + kFoldItems, ie);
+    const int64_t a = ib + static_cast<int64_t>(blockIdx.y) * per_split;
+    const int64_t b = min(a + per_split, ie);
     double sum = 0.0;
     for (int64_t it = a; it < b; ++it) sum += partial[it * width + col];
     folded[(s * splits + blockIdx.y) * width + col] = sum;
@@ -398,25 +400,33 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
     // unweighted, uncompressed structure averages of the inner kind, which it
     // forms from the structure's centres directly) and every centre's rows
     // fit their slot codes
-    // It forms a structure's average in one workgroup, so it takes inner
-    // averages only when the structures are small (a wavefront of atoms) or
-    // many enough to fill the device (four per compute unit); a batch of a
-    // few large structures (16 cells of 4,096 atoms: 16 workgroups, 50 ms)
-    // takes the 4x4-block kernel, whose workgroups sum runs of centres into
-    // partial sums reduced per structure (2.5 ms).
+    // It forms a structure's inner average in one workgroup when the
+    // structures are small (a wavefront of atoms) or many enough to fill the
+    // device (four per compute unit); a batch of a few large structures (16
+    // cells of 4,096 atoms: 16 workgroups, 50 ms) sums runs of centres into
+    // partial coefficient rows instead, reduced per structure (1.1 ms).
     int64_t largest_structure = 0;
     for (size_t st = 0; st + 1 < pb.offsets.size(); ++st) {
         largest_structure = std::max(largest_structure, pb.offsets[st + 1] - pb.offsets[st]);
     }
     const bool inner_fits = largest_structure <= kBlockSmallAtoms || p.block_forced ||
                             pb.structures >= 4 * static_cast<int64_t>(device_compute_units());
+    // Outer averages of the same large structures take it too: every
+    // centre's row as a float64 partial row (at most 4 GiB of them), folded
+    // per structure, then the mean (k_finalize_outer).  Many small
+    // structures keep the 4x4-block kernel, whose partial rows sum runs of
+    // centres in LDS (a row per centre would multiply the traffic by the
+    // run length).
+    const bool outer_fits = (!inner_fits || p.block_forced) && static_cast<double>(pb.atoms) * static_cast<double>(d.F) * 8.0 <= 4294967296.0;
     const bool block = p.block_waves > 0 &&
-                       (p.average == 0 || (p.average == 1 && p.weighted == 0 && p.compression == 0)) &&
+                       (p.average == 0 || (p.average == 2 && outer_fits) ||
+                        (p.average == 1 && p.weighted == 0 && p.compression == 0)) &&
                        g.row_bound < kQuadMaxRows;
     const bool block_inner = block && p.average == 1 && inner_fits;
     // other inner averages on that kernel: runs of a structure's centres
     // into partial rows, folded, then a launch of one workgroup per structure
     const bool block_runs = block && p.average == 1 && !inner_fits;
+    const bool block_outer = block && p.average == 2;
 
     // work items
     std::vector<int64_t>& item_begin_h = pb.item_begin;
@@ -424,7 +434,10 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
     item_begin_h.clear();
     struct_items_h.clear();
     int64_t items = block_inner ? pb.structures : pb.atoms;
-    if (p.average != 0 && !block_inner) {
+    if (block_outer) {
+        // items are the centres, a structure's partial rows its atoms
+        struct_items_h = pb.offsets;
+    } else if (p.average != 0 && !block_inner) {
         struct_items_h.resize(static_cast<size_t>(pb.structures) + 1);
         for (int64_t s = 0; s < pb.structures; ++s) {
             struct_items_h[static_cast<size_t>(s)] = static_cast<int64_t>(item_begin_h.size());
@@ -444,6 +457,7 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
     // folded partial rows (see k_fold_partials): splits per structure, the
     // folded rows and their structure ranges
     int fold_splits = 0;
+    int64_t fold_per_split = 0;
     size_t partial_width = 0;
     double* d_folded = nullptr;
     int64_t* d_fold_items = nullptr;
@@ -459,7 +473,10 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
         for (int64_t s = 0; s < pb.structures; ++s) {
             most_items = std::max(most_items, struct_items_h[static_cast<size_t>(s) + 1] - struct_items_h[static_cast<size_t>(s)]);
         }
-        if (most_items > 2 * kFoldItems) fold_splits = static_cast<int>((most_items + kFoldItems - 1) / kFoldItems);
+        if (most_items > 2 * kFoldItems) {
+            fold_splits = static_cast<int>(std::min<int64_t>((most_items + kFoldItems - 1) / kFoldItems, kFoldSplits));
+            fold_per_split = (most_items + fold_splits - 1) / fold_splits;
+        }
         fold_items_h.clear();
         if (fold_splits > 0) {
             for (int64_t s = 0; s <= pb.structures; ++s) fold_items_h.push_back(s * fold_splits);
@@ -474,8 +491,10 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
         d_fold_items = d_struct_items + struct_items_h.size();
         d_partial = reinterpret_cast<double*>(static_cast<char*>(scratch.ptr) + head);
         if (fold_splits > 0) d_folded = reinterpret_cast<double*>(static_cast<char*>(scratch.ptr) + head + partial_bytes);
-        MDX_HIP(hipMemcpyAsync(d_item_begin, item_begin_h.data(), item_begin_h.size() * sizeof(int64_t),
-                               hipMemcpyHostToDevice, stream));
+        if (!item_begin_h.empty()) {
+            MDX_HIP(hipMemcpyAsync(d_item_begin, item_begin_h.data(), item_begin_h.size() * sizeof(int64_t),
+                                   hipMemcpyHostToDevice, stream));
+        }
         MDX_HIP(hipMemcpyAsync(d_struct_items, struct_items_h.data(), struct_items_h.size() * sizeof(int64_t),
                                hipMemcpyHostToDevice, stream));
         if (fold_splits > 0) {
@@ -491,7 +510,7 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
         hipLaunchKernelGGL(k_fold_partials, dim3(static_cast<unsigned>(col_tiles * pb.structures),
                                                  static_cast<unsigned>(fold_splits)),
                            dim3(kBlock), 0, stream, d_partial, static_cast<int64_t>(partial_width), d_struct_items,
-                           col_tiles, fold_splits, d_folded);
+                           col_tiles, fold_splits, fold_per_split, d_folded);
         MDX_HIP(hipGetLastError());
         return {d_folded, d_fold_items};
     };
@@ -565,7 +584,7 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
                 ba.lane_beta = p.d_block_beta.as<double>();
                 ba.ps_offsets = p.d_block_ps.as<int32_t>();
                 ba.S = p.S;
-                ba.out_dtype = p.out_dtype;
+                ba.out_dtype = block_outer ? 8 : p.out_dtype;
                 ba.F = p.features;
                 ba.item_base = base;
                 ba.items = count;
@@ -586,8 +605,8 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
                     ba.bin_image = g.bin_image.as<int32_t>();
                     ba.images = pb.d_images.as<ImageDesc>();
                 }
-                ba.out = out_device;
-                ba.pitch = pitch_bytes;
+                ba.out = block_outer ? static_cast<void*>(d_partial) : out_device;
+                ba.pitch = block_outer ? static_cast<int64_t>(partial_width * sizeof(double)) : pitch_bytes;
                 block_args = ba;
                 launch_block_expand(stream, p.l_max, p.block_kg, p.block_ncr, ba, count);
             } else if (quad) {
@@ -602,7 +621,13 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
             if (hook) (*on_slice)(base, count);
         }
         if (events != nullptr) MDX_HIP(hipEventRecord(events[3], stream));
-        if (block_runs) {
+        if (block_outer) {
+            const auto rows_in = fold();
+            hipLaunchKernelGGL(k_finalize_outer, dim3(static_cast<unsigned>(std::min<int64_t>(pb.structures, 1 << 20))),
+                               dim3(kBlock), 0, stream, rows_in.first, rows_in.second, pb.d_offsets.as<int64_t>(),
+                               pb.structures, d, out_device, pitch_bytes);
+            MDX_HIP(hipGetLastError());
+        } else if (block_runs) {
             // the structures' rows from their folded partial rows
             const auto rows_in = fold();
             BlockArgs fa = block_args;

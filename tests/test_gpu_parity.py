@@ -81,14 +81,15 @@ def test_soap_matches_oracle(hip_context, oracle, workload, average, dtype):
 @pytest.mark.parametrize("kernel", ["generic", "mfma", "quad", "block"])
 def test_every_expansion_kernel_matches(hip_context, oracle, monkeypatch, kernel):
     """The plan picks the register-coefficient kernel for the default options
-    with atom-level rows or inner averages where its shape is compiled, else
+    with atom-level rows, inner averages, or outer averages of large
+    structures where its shape is compiled, else
     the 4x4-block kernel
     where it fits (n_max <= 8), else the 16x16-tile kernel, with the generic
     kernel as the last fallback.  Each stays parity-green when forced."""
 
     monkeypatch.setenv("MDX_HIP_SOAP_KERNEL", kernel)
     work = workloads.config(2, "small")
-    for average in ("off", "inner") if kernel == "block" else ("off", "inner", "outer"):
+    for average in ("off", "inner", "outer"):
         _, timing = _check(hip_context, oracle, work.batch, work.params, average, "float64")
         tiles = timing["expansion_tiles"]
         expected = {"block": tiles <= -1000, "quad": -1000 < tiles < 0, "mfma": tiles > 0, "generic": tiles == 0}
@@ -97,17 +98,21 @@ def test_every_expansion_kernel_matches(hip_context, oracle, monkeypatch, kernel
 
 def test_default_plan_runs_the_block_kernel(hip_context, oracle):
     work = workloads.config(2, "small")
-    for average, tiles in (("off", -1004), ("inner", -1004), ("outer", -4)):
+    for average, tiles in (("off", -1004), ("inner", -1004), ("outer", -1004)):
         _, timing = _check(hip_context, oracle, work.batch, work.params, average, "float32")
         # four wavefronts for n_max 8, l_max 6; inner averages of two 512-atom
         # structures (too few for a workgroup each) as runs of centres into
-        # partial rows and a launch per structure; outer averages on the
-        # 4x4-block kernel
+        # partial rows and a launch per structure; outer averages as float64
+        # rows per centre, reduced per structure
         assert timing["expansion_tiles"] == tiles
     molecules = workloads.config(3, "small")
     _, timing = _check(hip_context, oracle, molecules.batch, molecules.params, "inner", "float64")
     # inner averages of molecules (at most 64 atoms): a workgroup per structure
     assert timing["expansion_tiles"] <= -1000
+    # their outer averages stay on the 4x4-block kernel (partial rows per run
+    # of centres rather than per centre)
+    _, timing = _check(hip_context, oracle, molecules.batch, molecules.params, "outer", "float64")
+    assert -1000 < timing["expansion_tiles"] < 0
 
 
 def _random_cluster(seed, atoms, species):
@@ -254,7 +259,7 @@ def test_far_translated_structures(hip_context, oracle, monkeypatch, kernel):
                        np.diff(part.offsets), axis=0)
     batch = mdx.StructureBatch(part.numbers, part.positions + shifts, part.cells, part.pbc, part.offsets,
                                list(part.ids))
-    for average in ("off", "inner") if kernel == "block" else ("off", "inner", "outer"):
+    for average in ("off", "inner", "outer"):
         _check(hip_context, oracle, batch, work.params, average, "float64")
 
 
