@@ -7,28 +7,33 @@
 // cpp/src/standalone/soap.cpp:1218-1245).  Here the same grid, and what the
 // device search needs beyond it, comes from the kernels below and one
 // read-back of sixteen words.  A structure of at most kFuseAtoms atoms takes
-// its whole frame in one wavefront (k_frame_fused).  Larger ones are split
-// into items of kItemAtoms atoms (a topology table built with the batch), one
-// wavefront per item, and the per-structure steps take one wavefront per
-// structure, which reduces its items' partial results (no atomics: device
-// atomics on one address serialise across the chip).
+// its whole frame in one wavefront (frame_small).  Larger ones are split into
+// items of kItemAtoms atoms (a topology table built with the batch), one
+// wavefront per item; the last item wavefront of a structure to finish
+// reduces its items' partial results and does the per-structure step (no
+// atomics on shared words: device atomics on one address serialise across
+// the chip).
 //
-//   k_frame_fused     per small structure: all of the four steps below
-//   k_frame_bounds    per item: largest and smallest coordinate per axis
-//   k_frame_grid      per structure: bounding box of its images, grid
-//                     origin, dimensions and spacing
-//   k_frame_span      per item: each centre's grid coordinates, their
-//                     smallest and largest
-//   k_frame_classify  per structure: region of interest, binning path, LDS
-//                     chunks
+//   k_frame_first     one wavefront per unit: a small structure's whole
+//                     frame (bounding box, grid, centres' grid coordinates,
+//                     region of interest, binning path), or an item's
+//                     largest and smallest coordinate per axis, the last
+//                     item of a structure writing its grid (origin,
+//                     dimensions, spacing from the box of its images)
+//   k_frame_span      per item of a large structure: each centre's grid
+//                     coordinates and their extremes, the last item
+//                     classifying the structure (region of interest, binning
+//                     path, LDS chunks)
 //   k_lists_*         scan over the structures (one workgroup per 2,048
 //                     structures and a scan of the workgroups' sums when
 //                     there are more): first ROI cell of each structure, the
 //                     one-cell structures' cells, the binning lists; the
 //                     summary words
-//   (read-back)       the host sizes the graph and picks the launches
 //   k_frame_homes     each centre's home cell and place in it; the home
 //                     cells of workgroup-searched structures, listed
+//                     (queued before the read-back, for the capacity the
+//                     graph already holds)
+//   (read-back)       the host sizes the graph and picks the launches
 //   scan              first centre of each cell
 //   k_frame_place     the centres grouped by home cell; each cell's structure
 //
@@ -162,7 +167,7 @@ __device__ inline void reduce_items(const T* part, int64_t i0, int64_t i1, int l
     flag = wave_max(flag);
 }
 
-// Class bits of a structure (k_frame_classify -> the list scan).
+// Class bits of a structure (classify_structure -> the list scan).
 constexpr int kClassOneCell = 1;  // the ROI is one cell holding at most a wavefront of images
 constexpr int kClassLds = 2;      // binned by k_bin_lds chunks (ROI of at most kLdsBinCells cells)
 constexpr int kClassSmall = 4;    // binned by one wavefront of k_bin_small

@@ -126,7 +126,7 @@ struct FrameItem {
 };
 constexpr int kItemAtoms = 256;
 // structures of at most this many atoms take their whole frame in one
-// wavefront (k_frame_fused); larger ones are split into items
+// wavefront (frame_small in k_frame_first); larger ones are split into items
 constexpr int kFuseAtoms = 1024;
 
 // Periodic image: integer shift and its Cartesian vector, computed on the
