@@ -304,7 +304,8 @@ __global__ __launch_bounds__(kBlock) void k_finalize_inner(const double* partial
 }
 
 // outer: mean of the atoms' power spectra (soap.cpp:1068-1120); empty
-// structures give zeros.
+// structures give zeros.  blockIdx.y splits a row's features over
+// gridDim.y workgroups.
 __global__ __launch_bounds__(kBlock) void k_finalize_outer(const double* partial, const int64_t* struct_items,
                                                           const int64_t* offsets, int64_t structures, SoapDims d,
                                                           void* out, int64_t pitch) {
@@ -312,7 +313,8 @@ __global__ __launch_bounds__(kBlock) void k_finalize_outer(const double* partial
         const int64_t natoms = offsets[s + 1] - offsets[s];
         const double inv = natoms > 0 ? 1.0 / static_cast<double>(natoms) : 0.0;
         const int64_t ib = struct_items[s], ie = struct_items[s + 1];
-        for (int64_t f = threadIdx.x; f < d.F; f += kBlock) {
+        for (int64_t f = static_cast<int64_t>(blockIdx.y) * kBlock + threadIdx.x; f < d.F;
+             f += static_cast<int64_t>(gridDim.y) * kBlock) {
             double sum = 0.0;
             for (int64_t it = ib; it < ie; ++it) sum += partial[it * d.F + f];
             store_value(out, pitch, s, f, natoms > 0 ? sum * inv : 0.0, d.out_dtype);
@@ -623,7 +625,10 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
         if (events != nullptr) MDX_HIP(hipEventRecord(events[3], stream));
         if (block_outer) {
             const auto rows_in = fold();
-            hipLaunchKernelGGL(k_finalize_outer, dim3(static_cast<unsigned>(std::min<int64_t>(pb.structures, 1 << 20))),
+            // a workgroup per structure and 256 features
+            const unsigned col_tiles = static_cast<unsigned>((d.F + kBlock - 1) / kBlock);
+            hipLaunchKernelGGL(k_finalize_outer,
+                               dim3(static_cast<unsigned>(std::min<int64_t>(pb.structures, 1 << 20)), std::min(col_tiles, 65535u)),
                                dim3(kBlock), 0, stream, rows_in.first, rows_in.second, pb.d_offsets.as<int64_t>(),
                                pb.structures, d, out_device, pitch_bytes);
             MDX_HIP(hipGetLastError());

@@ -138,10 +138,147 @@ __device__ void polynomial_radial(const double* s_r, double* s_f, double* s_g, c
     }
 }
 
-// kGeneral adds neighbour weights and the polynomial basis; without them the
+// The same radial functions with the sums over the grid in registers: up
+// to kPolyDegrees degrees (L) and kPolyGroups radial groups, the common
+// case.  A wavefront takes one half
+// of the chunk's slots and one of P parts of the grid, four points at a
+// time.  Lane L evaluates K_0..K_{L-1} for slot L % 16 of its half at grid
+// point L / 16 of the four, which is the A operand of v_mfma_f64_4x4x4f64
+// (block b = (L / 4) % 4 holds slots 4b..4b+3: A_b lane L = A_b[slot
+// L % 4][point L / 16]); the B operand is the quadrature-weighted basis of
+// radial group g (B lane L = w_q r_q^2 g_{4g + L % 4}(r_q) at point L / 16,
+// the same for every block), so one MFMA per degree and radial group
+// accumulates 4 slots x 4 channels per block with no padded channels, and
+// no barrier sits inside the grid loop.  Result lane L holds slot
+// 4b + L / 16, channel 4g + L % 4.  The parts' results go to s_g in part
+// order (part 0 writes, the others add, a barrier between), so the sums do
+// not depend on the schedule.
+constexpr int kPolyDegrees = 8;
+constexpr int kPolyGroups = 2; // radial groups of 4 channels (n <= 8)
+__device__ __forceinline__ double mfma4(double a, double b, double c) {
+    return __builtin_amdgcn_mfma_f64_4x4x4f64(a, b, c, 0, 0, 0);
+}
+__device__ void polynomial_radial_regs(const double* s_r, double* s_g, const double* s_tab, const MfmaTables& tab,
+                                       const MfmaDims& d, int tid, int wave, int threads, int waves) {
+    const int lane = tid % kWaveThreads;
+    const int L = d.L, n = d.n, Q = d.grid;
+    const int KG = (n + 3) / 4;
+    const int GP = L * n + 1;
+    const int parts = waves >= 2 ? waves / 2 : 1;
+    const int blocks = (Q + 3) / 4;                       // grid blocks of 4 points
+    const int per_part = (blocks + parts - 1) / parts;
+    const int units = waves >= 2 ? 2 * parts : 1;
+    const double eta = d.eta;
+    // the pad entry of every slot's row stays zero
+    for (int i = tid; i < kNb; i += threads) s_g[i * GP + GP - 1] = 0.0;
+    for (int u0 = 0; u0 < (waves >= 2 ? 1 : 2); ++u0) {
+        // one wavefront: both halves in turn; else unit = wavefront
+        const int unit = waves >= 2 ? wave : u0;
+        const bool active = unit < units || waves < 2;
+        const int half = waves >= 2 ? unit % 2 : u0;
+        const int part = waves >= 2 ? unit / 2 : 0;
+        double acc[kPolyDegrees][kPolyGroups];
+#pragma unroll
+        for (int l = 0; l < kPolyDegrees; ++l) {
+#pragma unroll
+            for (int g = 0; g < kPolyGroups; ++g) acc[l][g] = 0.0;
+        }
+        if (active) {
+            const double radius = s_r[16 * half + lane % 16];
+            const int b0 = part * per_part, b1 = min(blocks, b0 + per_part);
+            // two grid blocks per iteration: their table loads, exps and
+            // degree recurrences are independent, so their latencies overlap
+            for (int blk0 = b0; blk0 < b1; blk0 += 2) {
+                double a_before[2], a_last[2], a_pref[2], bb[2][kPolyGroups];
+                bool a_centre[2];
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const int blk = blk0 + u;
+                    const int q = 4 * blk + lane / 16;
+                    const bool on_grid = blk < b1 && q < Q;
+                    const double radial = on_grid ? tab.poly_grid[q] : 1.0;
+#pragma unroll
+                    for (int g = 0; g < kPolyGroups; ++g) {
+                        const int k = 4 * g + lane % 4;
+                        bb[u][g] = g < KG && on_grid && k < n ? tab.poly_bw[q * n + k] : 0.0;
+                    }
+                    // K_l (soap.cpp:450-492): the l = 0 special case at r <= 1e-14
+                    double before, last;
+                    const bool at_centre = radius <= 1e-14;
+                    double prefactor = 0.0;
+                    if (at_centre) {
+                        before = exp_neg(-eta * (radial * radial), s_tab);
+                        last = 0.0;
+                    } else {
+                        prefactor = 0.25 / (eta * radius * radial);
+                        const double minus = exp_neg(-eta * (radial - radius) * (radial - radius), s_tab);
+                        const double plus = exp_neg(-eta * (radial + radius) * (radial + radius), s_tab);
+                        before = prefactor * (minus - plus);
+                        last = prefactor * (minus + plus - 2.0 * before);
+                    }
+                    if (!on_grid) {
+                        before = 0.0;
+                        last = 0.0;
+                    }
+                    a_before[u] = before;
+                    a_last[u] = last;
+                    a_pref[u] = prefactor;
+                    a_centre[u] = at_centre;
+                }
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+#pragma unroll
+                    for (int g = 0; g < kPolyGroups; ++g) {
+                        if (g < KG) acc[0][g] = mfma4(a_before[u], bb[u][g], acc[0][g]);
+                    }
+                }
+#pragma unroll
+                for (int l = 1; l < kPolyDegrees; ++l) {
+                    if (l < L) {
+#pragma unroll
+                        for (int u = 0; u < 2; ++u) {
+                            double value = a_last[u];
+                            if (l >= 2) {
+                                const double next = a_before[u] - a_pref[u] * (4.0 * l - 2.0) * a_last[u];
+                                value = a_centre[u] ? 0.0 : (next > 0.0 ? next : 0.0);
+                                a_before[u] = a_last[u];
+                                a_last[u] = value;
+                            }
+#pragma unroll
+                            for (int g = 0; g < kPolyGroups; ++g) {
+                                if (g < KG) acc[l][g] = mfma4(value, bb[u][g], acc[l][g]);
+                            }
+                        }
+                    }
+                }
+            }
+        }
+        // the parts' sums, in part order
+        const int slot = 16 * half + 4 * ((lane / 4) % 4) + lane / 16;
+        for (int p = 0; p < parts; ++p) {
+            if (active && part == p) {
+#pragma unroll
+                for (int l = 0; l < kPolyDegrees; ++l) {
+#pragma unroll
+                    for (int g = 0; g < kPolyGroups; ++g) {
+                        const int k = 4 * g + lane % 4;
+                        if (l < L && g < KG && k < n) {
+                            double& v = s_g[slot * GP + l * n + k];
+                            v = p == 0 ? acc[l][g] : v + acc[l][g];
+                        }
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// kGeneral adds neighbour weights (kPoly: and the polynomial basis, whose
+// sums over the grid hold registers of their own); without them the
 // kernel keeps at least 4 wavefronts per SIMD (a 128-VGPR budget the
 // compiler must fit), with them 2.
-template <int T, bool kGeneral>
+template <int T, bool kGeneral, bool kPoly>
 __global__ __launch_bounds__(T * kWaveThreads, kGeneral ? 2 : 4) void k_soap_mfma(
     const double* __restrict__ positions, const int64_t* __restrict__ pair_start, const int32_t* __restrict__ counts,
     const uint32_t* __restrict__ pair_bin, const double* __restrict__ bx, const double* __restrict__ by,
@@ -348,7 +485,7 @@ __global__ __launch_bounds__(T * kWaveThreads, kGeneral ? 2 : 4) void k_soap_mfm
                         scale = neighbour_weight(d, sqrt(d2), pself, tab.species_w[pq]);
                     }
                     double hx = dx, hy = dy, hz = dz, slot_value = d2;
-                    if (kGeneral && d.radial == 1) {
+                    if (kPoly) {
                         // polynomial: harmonics of the direction, times 4 pi w (soap.cpp:833-836);
                         // the radial functions need the distance
                         const double radius = sqrt(d2);
@@ -386,8 +523,12 @@ __global__ __launch_bounds__(T * kWaveThreads, kGeneral ? 2 : 4) void k_soap_mfm
                     harmonics_q(hx, hy, hz, scale, lm, mk, part, &kHarmonic + zero, s_y + jj * HP);
                 }
                 __syncthreads();
-                if (kGeneral && d.radial == 1) {
-                    polynomial_radial(s_d2, s_f, s_g, tab, d, tid, wave, kThreads, T);
+                if constexpr (kPoly) {
+                    if (L <= kPolyDegrees && n <= 4 * kPolyGroups) {
+                        polynomial_radial_regs(s_d2, s_g, s_tab, tab, d, tid, wave, kThreads, T);
+                    } else {
+                        polynomial_radial(s_d2, s_f, s_g, tab, d, tid, wave, kThreads, T);
+                    }
                 }
                 {
                     // issue the loads of the next chunk now
@@ -411,7 +552,7 @@ __global__ __launch_bounds__(T * kWaveThreads, kGeneral ? 2 : 4) void k_soap_mfm
 #pragma unroll
                         for (int s = 0; s < 4; ++s) {
                             const int jj = 4 * (h + s) + lane / 16;
-                            av[s] = !kGeneral || d.radial == 0 ? exp_neg(-expo * s_d2[jj], s_tab) : s_g[jj * GP + gcol];
+                            av[s] = !kPoly ? exp_neg(-expo * s_d2[jj], s_tab) : s_g[jj * GP + gcol];
                             yv[s] = s_y[jj * HP + ycol];
                         }
 #pragma unroll
@@ -509,7 +650,8 @@ void launch(hipStream_t stream, unsigned grid, int64_t per_block, size_t lds, co
             const DeviceGraph& g, const MfmaTables& tab, const MfmaDims& d, const int64_t* item_begin, int64_t base,
             int64_t count, void* out, int64_t pitch, double* partial) {
     const bool general = d.weighted != 0 || d.radial != 0;
-    auto kernel = general ? k_soap_mfma<T, true> : k_soap_mfma<T, false>;
+    auto kernel = d.radial != 0 ? k_soap_mfma<T, true, true> : general ? k_soap_mfma<T, true, false>
+                                                                       : k_soap_mfma<T, false, false>;
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(T * kWaveThreads), lds, stream, pb.d_positions.as<double>(),
                        g.pair_start.as<int64_t>(), g.counts.as<int32_t>(), g.pair_bin.as<uint32_t>(), g.bin_x.as<double>(),
                        g.bin_y.as<double>(), g.bin_z.as<double>(), tab, tab.ps_pref, d, item_begin, base,
