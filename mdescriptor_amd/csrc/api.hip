@@ -656,16 +656,17 @@ int mdx_hip_soap_plan_create(mdx_hip_ctx* ctx, const mdx_soap_params* params, md
                 throw mdx::Error(MDX_INVALID_ARGUMENT, "SOAP plan is outside the 4x4-block kernel's limits");
             }
             // register-coefficient kernel: GTO basis; atom-level rows with
-            // compression off, crossover (weighted or not) or mu1nu1
+            // compression off, mu2 or crossover (weighted or not) or mu1nu1
             // (unweighted), the same rows as float64 partial rows of an outer
-            // average, or unweighted inner structure averages without
-            // compression; a compiled (l_max, radial groups, species) shape.
+            // average, or inner structure averages without compression
+            // (weighted: large structures only); a compiled (l_max, radial
+            // groups, species) shape.
             // It keeps its coefficients in registers, so the tile kernel's LDS
             // limit does not apply to it
             const int cm = plan->compression;
             const bool block_rows = (p.average == 0 || p.average == 2) &&
-                                    (cm == 0 || cm == 3 || (cm == 2 && plan->weighted == 0));
-            const bool block_inner = p.average == 1 && cm == 0 && plan->weighted == 0;
+                                    (cm == 0 || cm == 1 || cm == 3 || (cm == 2 && plan->weighted == 0));
+            const bool block_inner = p.average == 1 && cm == 0;
             const bool block_options = plan->radial_basis == 0 && (block_rows || block_inner);
             if (block_options && quad_range && (choice == "auto" || choice == "block")) {
                 mdx::BlockPlanHost bp;

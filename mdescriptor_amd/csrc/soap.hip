@@ -420,9 +420,11 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
     // centres in LDS (a row per centre would multiply the traffic by the
     // run length).
     const bool outer_fits = (!inner_fits || p.block_forced) && static_cast<double>(pb.atoms) * static_cast<double>(d.F) * 8.0 <= 4294967296.0;
+    // (inner averages with neighbour weights only as runs of centres: the
+    // per-structure modes do not weight)
     const bool block = p.block_waves > 0 &&
                        (p.average == 0 || (p.average == 2 && outer_fits) ||
-                        (p.average == 1 && p.weighted == 0 && p.compression == 0)) &&
+                        (p.average == 1 && p.compression == 0 && (p.weighted == 0 || !inner_fits))) &&
                        g.row_bound < kQuadMaxRows;
     const bool block_inner = block && p.average == 1 && inner_fits;
     // other inner averages on that kernel: runs of a structure's centres
@@ -594,6 +596,7 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
                 ba.partial_out = block_runs ? d_partial : nullptr;
                 ba.small_structures = block_inner && largest_structure <= kBlockSmallAtoms ? 1 : 0;
                 ba.summed = p.compression == 2 ? 1 : 0;
+                ba.mu2 = p.compression == 1 ? 1 : 0;
                 if (p.weighted != 0) {
                     ba.weighting = p.weighting;
                     ba.has_w0 = p.has_w0;

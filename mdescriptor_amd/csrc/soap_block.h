@@ -14,10 +14,11 @@ namespace mdx {
 // per centre with weighted neighbours; a row per centre of mu1nu1 features
 // (each channel against the species-summed channels); inner averages of
 // large structures in two launches: runs of a structure's centres leave
-// their summed coefficient registers in partial rows, then a row per
-// structure from the sum of its partial rows.
+// their summed coefficient registers in partial rows (with or without
+// neighbour weights), then a row per structure from the sum of its partial
+// rows.
 constexpr int kBlockRows = 0, kBlockInner = 1, kBlockInnerSmall = 2, kBlockRowsWeighted = 3, kBlockRowsSummed = 4,
-              kBlockInnerRuns = 5, kBlockInnerFinal = 6;
+              kBlockInnerRuns = 5, kBlockInnerFinal = 6, kBlockInnerRunsWeighted = 7;
 constexpr int kBlockSmallAtoms = 64;
 
 // Launch arguments (one struct, passed by value).
@@ -49,6 +50,7 @@ struct BlockArgs {
     const int32_t* bin_image;            // image of each binned image (w0: the exact self pair)
     const ImageDesc* images;             // image table (integer shifts)
     int summed;                          // mu1nu1: spectrum against the species-summed coefficients
+    int mu2;                             // mu2: every species' sums into the first species' slots
     // inner averages in two launches: the runs' launch writes partial_out
     // (struct_offsets = first centre of each run, + end), the final launch
     // reads partial_in (items = structures, struct_offsets = the batch's
@@ -74,8 +76,9 @@ struct BlockPlanHost {
 };
 
 // Fills out and returns true when (S, n, l_max) is one of the compiled shapes.
-// compression: 0 off, 2 mu1nu1, 3 crossover (the feature layouts of
-// soap.cpp:948-1013); mu2 is not taken.
+// compression: 0 off, 1 mu2 (one coefficient species: the shape of S
+// species, the feature layout of one), 2 mu1nu1, 3 crossover (the feature
+// layouts of soap.cpp:948-1013).
 bool block_plan_tables(int S, int n, int l_max, int out_dtype, int compression, const std::vector<double>& beta_scaled,
                        const std::vector<double>& pref, const std::vector<double>& expo, BlockPlanHost& out);
 void launch_block_expand(hipStream_t stream, int l_max, int kg, int ncr, const BlockArgs& a, int64_t count);

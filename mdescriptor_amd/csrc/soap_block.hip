@@ -432,8 +432,9 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
     const int64_t work_last = min(work_first + a.per_block, a.item_base + a.items);
     // rows of structure averages (the runs' launch sums a run of a structure's
     // centres the same way, into a partial row)
-    constexpr bool inner = MODE == kBlockInner || MODE == kBlockInnerSmall || MODE == kBlockInnerRuns;
-    constexpr bool kRuns = MODE == kBlockInnerRuns;
+    constexpr bool inner = MODE == kBlockInner || MODE == kBlockInnerSmall || MODE == kBlockInnerRuns ||
+                           MODE == kBlockInnerRunsWeighted;
+    constexpr bool kRuns = MODE == kBlockInnerRuns || MODE == kBlockInnerRunsWeighted;
     constexpr bool kFinal = MODE == kBlockInnerFinal;
     // this wavefront's registers in a partial row, and the row's width
     constexpr int kPartBase = [] {
@@ -442,7 +443,8 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
         return u;
     }() * NCR * kWaveThreads;
     constexpr int64_t kPartWidth = static_cast<int64_t>(units_total(0xffffffffu, L)) * NCR * kWaveThreads;
-    constexpr bool kWeighted = MODE == kBlockRowsWeighted; // neighbour weights scale the harmonic seeds
+    // neighbour weights scale the harmonic seeds
+    constexpr bool kWeighted = MODE == kBlockRowsWeighted || MODE == kBlockInnerRunsWeighted;
     constexpr bool kSummed = MODE == kBlockRowsSummed;     // mu1nu1: against the species-summed coefficients
     // structures of at most a wavefront of atoms: pairs streamed species-major
     // across the structure's centres (an average sums them in any order)
@@ -647,7 +649,9 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
     // average adds its centres' sums): per lane and register a factor of 1
     // (the lane's block slot and the register belong to q) or 0, and one fma
     // per register
-    auto merge = [&](int q) {
+    auto merge = [&](int q_in) {
+        // mu2: one coefficient species, the first species' slots
+        const int q = a.mu2 != 0 ? 0 : q_in;
         const int rt = KG == 2 ? q >> 1 : KG == 1 ? q >> 2 : q;
         double sel[RPL][NCR];
         unroll<RPL>([&](auto rc) {
@@ -993,7 +997,8 @@ constexpr int ps_tiles(int ncr, bool summed) { return summed ? ncr : ncr * (ncr 
 // whose summed coefficients stay live beside the registers
 template <int LM, int KG, int NCR, int ES, int MODE>
 __global__ __launch_bounds__(256) __attribute__((
-    amdgpu_waves_per_eu(MODE == kBlockRowsWeighted || MODE == kBlockRowsSummed ? 4 : 5))) void
+    amdgpu_waves_per_eu(MODE == kBlockRowsWeighted || MODE == kBlockInnerRunsWeighted || MODE == kBlockRowsSummed ? 4
+                                                                                                           : 5))) void
 k_soap_block(BlockArgs a) {
     using PL = BlockPlan<LM, KG>;
     // staging buffers, d2, exp table, padded S_lm table, power-spectrum
@@ -1071,7 +1076,7 @@ void launch_shape(hipStream_t stream, const BlockArgs& a, int64_t count) {
     const unsigned grid = static_cast<unsigned>((count + args.per_block - 1) / args.per_block);
     const dim3 threads(PL::T * kWaveThreads);
     const int mode = a.partial_in != nullptr    ? kBlockInnerFinal
-                     : a.partial_out != nullptr ? kBlockInnerRuns
+                     : a.partial_out != nullptr ? (a.species_w != nullptr ? kBlockInnerRunsWeighted : kBlockInnerRuns)
                      : a.struct_offsets != nullptr ? (a.small_structures ? kBlockInnerSmall : kBlockInner)
                      : a.species_w != nullptr ? kBlockRowsWeighted
                      : a.summed != 0          ? kBlockRowsSummed
@@ -1094,6 +1099,8 @@ void launch_shape(hipStream_t stream, const BlockArgs& a, int64_t count) {
         launch(std::integral_constant<int, kBlockRowsWeighted>{});
     } else if (mode == kBlockInnerRuns) {
         launch(std::integral_constant<int, kBlockInnerRuns>{});
+    } else if (mode == kBlockInnerRunsWeighted) {
+        launch(std::integral_constant<int, kBlockInnerRunsWeighted>{});
     } else if (mode == kBlockInnerFinal) {
         launch(std::integral_constant<int, kBlockInnerFinal>{});
     } else {
@@ -1136,7 +1143,9 @@ int64_t block_partial_width(int l_max, int ncr) {
 bool block_plan_tables(int S, int n, int l_max, int out_dtype, int compression, const std::vector<double>& beta_scaled,
                        const std::vector<double>& pref, const std::vector<double>& expo, BlockPlanHost& out) {
     out = BlockPlanHost{};
-    if (compression != 0 && compression != 2 && compression != 3) return false;
+    if (compression < 0 || compression > 3) return false;
+    // species of the coefficients and the feature layout (mu2: one)
+    const int St = compression == 1 ? 1 : S;
     const int kg = (n + 3) / 4;
     if (n < 1 || kg > 3 || (kg == 3 && S != 1)) return false;
     const int ncr = coefficient_registers(S, kg);
@@ -1144,7 +1153,7 @@ bool block_plan_tables(int S, int n, int l_max, int out_dtype, int compression, 
     if (e == nullptr) return false;
     const int L = l_max + 1;
     {
-        const int64_t W = static_cast<int64_t>(S) * n;
+        const int64_t W = static_cast<int64_t>(St) * n;
         const int64_t F = compression == 2 ? W * n * L : compression == 3 ? W * (n + 1) / 2 * L : W * (W + 1) / 2 * L;
         if (F * out_dtype >= kDroppedBytes || n * n >= (1 << kStrideBits)) return false;
     }
@@ -1200,15 +1209,15 @@ bool block_plan_tables(int S, int n, int l_max, int out_dtype, int compression, 
             rg = g % kg;
         }
         const int np = 4 * rg + nl;
-        if (t >= S || np >= n) return -1;
+        if (t >= St || np >= n) return -1;
         return t * n + np;
     };
     // feature index of channel pair (i, j), i <= j (soap.cpp:997-1013)
     auto feature = [&](int i, int j, int& stride) -> int {
         const int t1 = i / n, n1 = i % n, t2 = j / n, n2 = j % n;
         int base = 0;
-        for (int a1 = 0; a1 < S; ++a1) {
-            for (int a2 = a1; a2 < S; ++a2) {
+        for (int a1 = 0; a1 < St; ++a1) {
+            for (int a2 = a1; a2 < St; ++a2) {
                 const int size = a1 == a2 ? n * (n + 1) / 2 : n * n;
                 if (a1 == t1 && a2 == t2) {
                     stride = size;

@@ -63,7 +63,7 @@ def test_option_at_hcno_shape(hip_context, oracle, name):
 
 
 # the options the register-coefficient kernel takes with atom-level rows
-BLOCK_OPTIONS = ["poly", "pow_w0", "exp", "w0_only", "species_weights", "mu1nu1", "crossover"]
+BLOCK_OPTIONS = ["poly", "pow_w0", "exp", "w0_only", "species_weights", "mu1nu1", "crossover", "mu2"]
 
 
 @pytest.mark.parametrize("shape", [(1, 4, 3), (2, 8, 6), (3, 6, 4), (4, 8, 8), (5, 9, 9)])
@@ -96,6 +96,31 @@ def test_options_on_register_coefficient_kernel(hip_context, oracle, monkeypatch
     assert np.all(np.isfinite(values))
     error = scaled_error(values, expected)
     assert error <= F64_GATE, f"{name} {shape}: scaled error {error:.3e}"
+
+
+@pytest.mark.parametrize("name", ["pow_w0", "species_weights", "poly"])
+@pytest.mark.parametrize("dtype", ["float64", "float32"])
+def test_weighted_inner_average_on_register_coefficient_kernel(hip_context, oracle, name, dtype):
+    """Inner averages of two 512-atom HCNO cells with neighbour weights: runs
+    of centres into partial coefficient rows (weights on the harmonic seeds,
+    w0 on each centre's own image), then a launch per structure."""
+
+    w = workloads.config(2, "small")
+    p = w.params
+    options = option_arguments(name, p["species"], p["r_cut"], p["n_max"])
+    alphas, betas = basis_gto(p["r_cut"], p["n_max"], p["l_max"])
+    plan = _hip.SoapPlan(hip_context, species=p["species"], n_max=p["n_max"], l_max=p["l_max"], r_cut=p["r_cut"],
+                         sigma=1.0, alphas=alphas, betas=betas, average="inner", dtype=dtype, options=options)
+    try:
+        values, timing = plan.compute(w.batch)
+    finally:
+        plan.close()
+    assert timing["expansion_tiles"] <= -1000
+    expected = oracle.soap(w.batch, species=p["species"], n_max=p["n_max"], l_max=p["l_max"], r_cut=p["r_cut"],
+                           sigma=1.0, alphas=alphas, betas=betas, average="inner", options=options)
+    assert values.shape == expected.shape
+    error = scaled_error(values, expected)
+    assert error <= (F64_GATE if dtype == "float64" else F32_GATE), f"{name} {dtype}: scaled error {error:.3e}"
 
 
 @pytest.mark.parametrize("name", ["polynomial", "mu1nu1", "exp"])
