@@ -1039,11 +1039,12 @@ __global__ __launch_bounds__(kBlock) void k_neighbors_wave(
 constexpr int kScanItems = 8;
 constexpr int kScanTile = kBlock * kScanItems;
 
-// Exclusive scan over the workgroup (kBlock threads): wavefront scans by
+// Exclusive scan over the workgroup (kThreads threads): wavefront scans by
 // shuffles, then the wavefront totals through LDS (lds holds at least
-// kBlock / kWave values).
+// kThreads / kWave values).
+template <int kThreads = kBlock>
 __device__ int64_t block_exclusive_scan(int64_t value, int64_t* lds, int64_t& total) {
-    constexpr int kWaves = kBlock / kWave;
+    constexpr int kWaves = kThreads / kWave;
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
     int64_t inclusive = value;
@@ -1114,12 +1115,15 @@ __global__ __launch_bounds__(kBlock) void k_scan_apply(const int32_t* in, int64_
     if (blockIdx.x == 0 && threadIdx.x == 0) out[n] = sums[nb];
 }
 
-// the whole scan in one workgroup, tile after tile (short arrays: one launch
-// instead of three)
-__global__ __launch_bounds__(kBlock) void k_scan_one(const int32_t* in, int64_t n, int64_t* out) {
-    __shared__ int64_t lds[kBlock];
+// the whole scan in one workgroup of 1,024 threads, tile after tile (short
+// arrays, up to 8,192 entries a tile: one launch instead of three, and for
+// the graph's cell counts one tile instead of three of 2,048)
+constexpr int kScanOneThreads = 1024;
+constexpr int kScanOneTile = kScanOneThreads * kScanItems;
+__global__ __launch_bounds__(kScanOneThreads) void k_scan_one(const int32_t* in, int64_t n, int64_t* out) {
+    __shared__ int64_t lds[kScanOneThreads / kWave];
     int64_t carry = 0;
-    for (int64_t base = 0; base < n; base += kScanTile) {
+    for (int64_t base = 0; base < n; base += kScanOneTile) {
         int64_t vals[kScanItems];
         int64_t local = 0;
         for (int i = 0; i < kScanItems; ++i) {
@@ -1128,7 +1132,7 @@ __global__ __launch_bounds__(kBlock) void k_scan_one(const int32_t* in, int64_t 
             local += vals[i];
         }
         int64_t total;
-        int64_t run = carry + block_exclusive_scan(local, lds, total);
+        int64_t run = carry + block_exclusive_scan<kScanOneThreads>(local, lds, total);
         for (int i = 0; i < kScanItems; ++i) {
             const int64_t idx = base + static_cast<int64_t>(threadIdx.x) * kScanItems + i;
             if (idx < n) out[idx] = run;
@@ -1139,7 +1143,7 @@ __global__ __launch_bounds__(kBlock) void k_scan_one(const int32_t* in, int64_t 
     if (threadIdx.x == 0) out[n] = carry;
 }
 
-constexpr int64_t kScanOneTiles = 8; // up to 8 tiles: one workgroup
+constexpr int64_t kScanOneTiles = 8; // up to 8 tiles of kScanTile (2 of kScanOneTile): one workgroup
 
 unsigned grid_for(int64_t work, int block = kBlock) {
     const int64_t blocks = (work + block - 1) / block;
@@ -1151,7 +1155,7 @@ unsigned grid_for(int64_t work, int block = kBlock) {
 void scan_counts(hipStream_t stream, const int32_t* in, int64_t* out, int64_t n, DeviceBuffer& tmp) {
     const int64_t nb = std::max<int64_t>(1, (n + kScanTile - 1) / kScanTile);
     if (nb <= kScanOneTiles) {
-        hipLaunchKernelGGL(k_scan_one, dim3(1), dim3(kBlock), 0, stream, in, n, out);
+        hipLaunchKernelGGL(k_scan_one, dim3(1), dim3(kScanOneThreads), 0, stream, in, n, out);
         return;
     }
     tmp.reserve(static_cast<size_t>(nb + 1) * sizeof(int64_t));
