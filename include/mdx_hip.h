@@ -218,6 +218,28 @@ int mdx_hip_soap_run_noalloc(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, mdx_de
                              void* out_device, int64_t out_pitch_bytes, const volatile int32_t* cancel_flag,
                              mdx_timing* timing);
 
+/* A trajectory frame on a device-resident batch without waiting for it:
+ * positions (f64[atoms*3], C order, host or device memory) replace the
+ * batch's, and the SOAP pipeline runs on them into out_device, as
+ * mdx_hip_batch_set_positions followed by mdx_hip_soap_run.  No counterpart
+ * in the reference, which rebuilds its grid and graph in each compute_soap
+ * call and returns after the call (cpp/src/standalone/soap.cpp:1218-1245):
+ * for callers that step through frames (molecular dynamics, trajectory
+ * analysis).  The call returns once the frame's graph is built and its
+ * expansion queued; the positions have been read by then.  The batch
+ * alternates two sets of device buffers, so the graph of one frame is built
+ * on a second stream while the previous frame's expansion runs.  Results are
+ * bit-identical to the synchronous run.  out_device of a frame is complete
+ * after mdx_hip_wait (or after a later synchronous call on the same batch);
+ * the caller keeps it alive and unread until then.  A non-finite position
+ * returns MDX_INVALID_ARGUMENT ("positions must be finite"). */
+int mdx_hip_soap_run_frame(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, mdx_device_batch* batch,
+                           const double* positions, void* out_device, int64_t out_pitch_bytes,
+                           const volatile int32_t* cancel_flag);
+
+/* Wait for every frame queued on the context by mdx_hip_soap_run_frame. */
+int mdx_hip_wait(mdx_hip_ctx* ctx);
+
 /* Neighbour graph on the device, for parity and the pair-level API.
  * Replaces build_neighbor_graph (cpp/src/common/neighbor.cpp:703-768) as
  * exported by _native.build_neighbor_graph (cpp/src/bindings/module.cpp:887-935):

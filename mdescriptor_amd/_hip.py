@@ -214,6 +214,12 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, _i32p,
          ctypes.POINTER(Timing)],
     ),
+    "mdx_hip_soap_run_frame": (
+        ctypes.c_int,
+        [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+         _i32p],
+    ),
+    "mdx_hip_wait": (ctypes.c_int, [ctypes.c_void_p]),
     "mdx_hip_neighbors_build": (
         ctypes.c_int,
         [ctypes.c_void_p, ctypes.POINTER(BatchView), ctypes.c_double, ctypes.c_int32, _i64p],
@@ -311,6 +317,11 @@ class Context:
     def check(self, status: int) -> None:
         if status != MDX_OK:
             _raise_for(status, (self.lib.mdx_hip_last_error(self.handle) or b"").decode())
+
+    def wait(self) -> None:
+        """Wait for the frames queued by :meth:`DeviceBatch.run_frame`."""
+
+        self.check(self.lib.mdx_hip_wait(self.handle))
 
     def close(self) -> None:
         if getattr(self, "handle", None) is not None and self.handle.value:
@@ -515,6 +526,28 @@ class DeviceBatch:
         ctx.check(ctx.lib.mdx_hip_soap_run(ctx.handle, self.plan.handle, self.handle, ctypes.c_void_p(out_device_ptr),
                                            int(pitch_bytes), flag, ctypes.byref(timing)))
         return timing.as_dict()
+
+    def run_frame(self, positions: Any, out_device_ptr: int, pitch_bytes: int,
+                  cancel: ctypes.c_int32 | None = None) -> None:
+        """One trajectory frame without waiting for it: new positions (a host
+        array of shape (atoms, 3), or the device address of atoms * 3 float64
+        values) and the descriptors of them into out_device_ptr.  The output
+        is complete after :meth:`Context.wait`; the next frame's graph is
+        built while this frame's expansion runs."""
+
+        ctx = self.plan.context
+        if isinstance(positions, int):
+            address = ctypes.c_void_p(positions)
+            keep = None
+        else:
+            keep = np.ascontiguousarray(positions, dtype=np.float64)
+            if keep.size != 3 * len(self.arrays.numbers):
+                raise ValueError("positions must hold atoms * 3 values")
+            address = keep.ctypes.data_as(ctypes.c_void_p)
+        flag = ctypes.pointer(cancel) if cancel is not None else None
+        ctx.check(ctx.lib.mdx_hip_soap_run_frame(ctx.handle, self.plan.handle, self.handle, address,
+                                                 ctypes.c_void_p(out_device_ptr), int(pitch_bytes), flag))
+        del keep
 
     def close(self) -> None:
         if getattr(self, "handle", None) is not None and self.handle.value:

@@ -415,6 +415,7 @@ int mdx_hip_create(int device, mdx_hip_ctx** out) {
             ctx->device = device;
             MDX_HIP(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
             MDX_HIP(hipStreamCreateWithFlags(&ctx->copy_stream, hipStreamNonBlocking));
+            MDX_HIP(hipStreamCreateWithFlags(&ctx->graph_stream, hipStreamNonBlocking));
             for (auto& ev : ctx->events) MDX_HIP(hipEventCreate(&ev));
             for (auto& ev : ctx->stage_events) MDX_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
             for (auto& ev : ctx->list_events) MDX_HIP(hipEventCreate(&ev));
@@ -444,6 +445,7 @@ void mdx_hip_destroy(mdx_hip_ctx* ctx) {
         std::lock_guard<std::mutex> lock(ctx->mutex);
         if (ctx->stream != nullptr) (void)hipStreamSynchronize(ctx->stream);
         if (ctx->copy_stream != nullptr) (void)hipStreamSynchronize(ctx->copy_stream);
+        if (ctx->graph_stream != nullptr) (void)hipStreamSynchronize(ctx->graph_stream);
         for (auto& ev : ctx->slice_events) {
             if (ev != nullptr) (void)hipEventDestroy(ev);
         }
@@ -465,9 +467,11 @@ void mdx_hip_destroy(mdx_hip_ctx* ctx) {
     }
     hipStream_t stream = ctx->stream;
     hipStream_t copy_stream = ctx->copy_stream;
+    hipStream_t graph_stream = ctx->graph_stream;
     delete ctx; // device buffers are freed by their destructors
     if (stream != nullptr) (void)hipStreamDestroy(stream);
     if (copy_stream != nullptr) (void)hipStreamDestroy(copy_stream);
+    if (graph_stream != nullptr) (void)hipStreamDestroy(graph_stream);
     if (previous >= 0) (void)hipSetDevice(previous);
 }
 
@@ -815,6 +819,13 @@ int mdx_hip_batch_upload(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, const mdx_
             db->pb.include_boundary = 1;
             mdx::prepare_batch(*batch, plan->species.data(), plan->S, plan->cutoff, db->pb);
             mdx::upload_batch(ctx->stream, *batch, db->pb);
+            // the host copy from which pipelined frames prepare their second set
+            const size_t atoms = static_cast<size_t>(batch->atoms), structures = static_cast<size_t>(batch->structures);
+            db->host_numbers.assign(batch->numbers, batch->numbers + atoms);
+            db->host_positions.assign(batch->positions, batch->positions + 3 * atoms);
+            db->host_cells.assign(batch->cells, batch->cells + 9 * structures);
+            db->host_pbc.assign(batch->pbc, batch->pbc + 3 * structures);
+            db->host_offsets.assign(batch->offsets, batch->offsets + structures + 1);
         } catch (...) {
             delete db;
             throw;
@@ -822,6 +833,21 @@ int mdx_hip_batch_upload(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, const mdx_
         *out = db;
     });
 }
+
+namespace {
+
+// Wait for the pipelined frames still running on a batch (their expansions
+// read its sets), so that a synchronous call may reuse set 0.
+void quiesce(mdx_device_batch* batch) {
+    for (int k = 0; k < 2; ++k) {
+        if (batch->queued[k]) {
+            MDX_HIP(hipEventSynchronize(batch->done[k]));
+            batch->queued[k] = false;
+        }
+    }
+}
+
+} // namespace
 
 int mdx_hip_batch_set_positions(mdx_hip_ctx* ctx, mdx_device_batch* batch, const double* positions) {
     if (ctx == nullptr) return MDX_INVALID_ARGUMENT;
@@ -833,6 +859,7 @@ int mdx_hip_batch_set_positions(mdx_hip_ctx* ctx, mdx_device_batch* batch, const
         if (values == 0) return;
         if (positions == nullptr) throw mdx::Error(MDX_INVALID_ARGUMENT, "null positions");
         DeviceScope scope(ctx->device);
+        quiesce(batch);
         if (is_device_memory(positions)) {
             // checked for finiteness by the next run's frame kernels
             MDX_HIP(hipMemcpyAsync(batch->pb.d_positions.ptr, positions, values * sizeof(double),
@@ -885,6 +912,7 @@ int mdx_hip_soap_run(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, mdx_device_bat
         check_device_run(ctx, plan, batch, out_device, out_pitch_bytes);
         check_cancel(cancel_flag);
         DeviceScope scope(ctx->device);
+        quiesce(batch);
         run_pipeline(ctx, *plan, batch->pb, batch->graph, batch->partials, out_device, out_pitch_bytes, cancel_flag,
                      timing);
         ctx->finished.wait(ctx->stream);
@@ -901,6 +929,7 @@ int mdx_hip_soap_run_noalloc(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, mdx_de
         check_device_run(ctx, plan, batch, out_device, out_pitch_bytes);
         check_cancel(cancel_flag);
         DeviceScope scope(ctx->device);
+        quiesce(batch);
         // every piece is carved afresh from the start of the array; the
         // graph's counters are cleared on the stream before each build
         ctx->arena.reset();
@@ -910,6 +939,91 @@ int mdx_hip_soap_run_noalloc(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, mdx_de
                      cancel_flag, timing);
         ctx->finished.wait(ctx->stream);
         fill_timing(ctx, timing, false);
+    });
+}
+
+int mdx_hip_soap_run_frame(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, mdx_device_batch* batch,
+                           const double* positions, void* out_device, int64_t out_pitch_bytes,
+                           const volatile int32_t* cancel_flag) {
+    if (ctx == nullptr) return MDX_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    return guarded(ctx, [&] {
+        check_device_run(ctx, plan, batch, out_device, out_pitch_bytes);
+        check_cancel(cancel_flag);
+        const size_t values = static_cast<size_t>(batch->pb.atoms) * 3;
+        if (values > 0 && positions == nullptr) throw mdx::Error(MDX_INVALID_ARGUMENT, "null positions");
+        DeviceScope scope(ctx->device);
+        const int k = batch->next_set;
+        if (k == 1 && batch->pb2 == nullptr) {
+            // the second set: the batch prepared again from its host copy
+            auto pb2 = std::make_unique<mdx::PreparedBatch>();
+            const mdx_batch_view view{batch->host_numbers.data(), batch->host_positions.data(),
+                                      batch->host_cells.data(), batch->host_pbc.data(), batch->host_offsets.data(),
+                                      static_cast<int64_t>(batch->host_offsets.size()) - 1,
+                                      static_cast<int64_t>(batch->host_numbers.size())};
+            pb2->include_boundary = 1;
+            mdx::prepare_batch(view, plan->species.data(), plan->S, plan->cutoff, *pb2);
+            mdx::upload_batch(ctx->graph_stream, view, *pb2);
+            batch->pb2 = std::move(pb2);
+        }
+        for (int e = 0; e < 2; ++e) {
+            if (batch->ready[e] == nullptr) MDX_HIP(hipEventCreateWithFlags(&batch->ready[e], hipEventDisableTiming));
+            if (batch->done[e] == nullptr) MDX_HIP(hipEventCreateWithFlags(&batch->done[e], hipEventDisableTiming));
+        }
+        mdx::PreparedBatch& pb = k == 0 ? batch->pb : *batch->pb2;
+        mdx::DeviceGraph& graph = k == 0 ? batch->graph : batch->graph2;
+        mdx::DeviceBuffer& partials = k == 0 ? batch->partials : batch->partials2;
+        // the set's buffers are rebuilt (and may be reallocated) only after
+        // the expansion that last read them has finished
+        if (batch->queued[k]) {
+            MDX_HIP(hipEventSynchronize(batch->done[k]));
+            batch->queued[k] = false;
+        }
+        hipStream_t gs = ctx->graph_stream, s = ctx->stream;
+        if (values > 0) {
+            if (is_device_memory(positions)) {
+                // checked for finiteness by the frame kernels below
+                MDX_HIP(hipMemcpyAsync(pb.d_positions.ptr, positions, values * sizeof(double),
+                                       hipMemcpyDeviceToDevice, gs));
+            } else {
+                for (size_t i = 0; i < values; ++i) {
+                    if (!std::isfinite(positions[i])) {
+                        throw mdx::Error(MDX_INVALID_ARGUMENT, "positions must be finite");
+                    }
+                }
+                MDX_HIP(hipMemcpyAsync(pb.d_positions.ptr, positions, values * sizeof(double),
+                                       hipMemcpyHostToDevice, gs));
+            }
+        }
+        // this frame's graph on the second stream, beside the previous
+        // frame's expansion; its expansion on the main stream behind both
+        mdx::build_graph(gs, pb, graph, cancel_flag, true, true);
+        MDX_HIP(hipEventRecord(batch->ready[k], gs));
+        MDX_HIP(hipStreamWaitEvent(s, batch->ready[k], 0));
+        check_cancel(cancel_flag);
+        mdx::run_soap(s, *plan, pb, graph, out_device, out_pitch_bytes, partials, cancel_flag, nullptr, nullptr);
+        if (!mdx::complete_graph(pb, graph, cancel_flag)) {
+            // a centre overflowed its slot: the frame again, in order, on the
+            // main stream (its buffers are replaced)
+            MDX_HIP(hipStreamSynchronize(s));
+            MDX_HIP(hipStreamSynchronize(gs));
+            mdx::build_graph(s, pb, graph, cancel_flag, true, false, true);
+            check_cancel(cancel_flag);
+            mdx::run_soap(s, *plan, pb, graph, out_device, out_pitch_bytes, partials, cancel_flag, nullptr, nullptr);
+        }
+        MDX_HIP(hipEventRecord(batch->done[k], s));
+        batch->queued[k] = true;
+        batch->next_set = k ^ 1;
+    });
+}
+
+int mdx_hip_wait(mdx_hip_ctx* ctx) {
+    if (ctx == nullptr) return MDX_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    return guarded(ctx, [&] {
+        DeviceScope scope(ctx->device);
+        MDX_HIP(hipStreamSynchronize(ctx->graph_stream));
+        MDX_HIP(hipStreamSynchronize(ctx->stream));
     });
 }
 

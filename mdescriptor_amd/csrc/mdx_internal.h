@@ -13,6 +13,7 @@
 #include <mutex>
 #include <stdexcept>
 #include <string>
+#include <memory>
 #include <vector>
 
 #include "../../include/mdx_hip.h"
@@ -437,6 +438,7 @@ struct mdx_hip_ctx {
     hipEvent_t events[8] = {};
     hipEvent_t stage_events[2] = {};  // completion of the DMA into each staging half
     hipStream_t copy_stream = nullptr; // result downloads overlapped with the expansion launches
+    hipStream_t graph_stream = nullptr; // pipelined frames: the next frame's graph beside this one's expansion
     std::vector<hipEvent_t> slice_events; // end of each expansion launch, waited on by copy_stream
     mdx::StreamPoint finished;        // end of a device-batch run (polled)
     // mdx_hip_soap_run_noalloc: the device's static scratch array as an arena,
@@ -491,6 +493,27 @@ struct mdx_device_batch {
     mdx::PreparedBatch pb;
     mdx::DeviceGraph graph;
     mdx::DeviceBuffer partials;
+    // Pipelined frames (mdx_hip_soap_run_frame) alternate two sets: set 0 is
+    // the one above, set 1 is prepared on the first such run from the host
+    // copy of the batch kept here.  A set is rebuilt only after the expansion
+    // that last read it has finished (done[set]).
+    std::unique_ptr<mdx::PreparedBatch> pb2;
+    mdx::DeviceGraph graph2;
+    mdx::DeviceBuffer partials2;
+    std::vector<int32_t> host_numbers, host_pbc;
+    std::vector<double> host_positions, host_cells;
+    std::vector<int64_t> host_offsets;
+    int next_set = 0;
+    hipEvent_t ready[2] = {}; // graph of the set built (second stream)
+    hipEvent_t done[2] = {};  // expansion of the set finished (main stream)
+    bool queued[2] = {};      // done[set] recorded and not yet waited for
+    ~mdx_device_batch() {
+        for (int k = 0; k < 2; ++k) {
+            if (queued[k]) (void)hipEventSynchronize(done[k]);
+            if (ready[k] != nullptr) (void)hipEventDestroy(ready[k]);
+            if (done[k] != nullptr) (void)hipEventDestroy(done[k]);
+        }
+    }
 };
 
 namespace mdx {

@@ -316,3 +316,118 @@ def test_slot_overflow_on_the_first_call(hip_context, oracle, options, average, 
         assert error <= F64_GATE, f"{options} {average} {entry}: scaled error {error:.3e}"
     finally:
         plan.close()
+
+
+def _pipelined(plan, batch, frames, device_frames=()):
+    """Rows of each frame through mdx_hip_soap_run_frame (all queued, one
+    wait at the end), each frame into its own output buffer; frames whose
+    index is in device_frames hand their positions over in device memory."""
+
+    resident = _Resident(plan, batch)
+    outs = [_hip.DeviceMemory(max(1, resident.batch.rows * resident.pitch)) for _ in frames]
+    staged = []
+    try:
+        for k, positions in enumerate(frames):
+            print(f"pipelined frame {k}", flush=True)
+            if k in device_frames:
+                staged.append(_hip.DeviceMemory(positions.nbytes).from_host(positions))
+                resident.batch.run_frame(staged[-1].address, outs[k].address, resident.pitch)
+            else:
+                resident.batch.run_frame(positions, outs[k].address, resident.pitch)
+        plan.context.wait()
+        shape = (resident.batch.rows, plan.features)
+        return [out.to_host(np.empty(shape, plan.dtype)) for out in outs]
+    finally:
+        for memory in (*outs, *staged):
+            memory.free()
+        resident.close()
+
+
+def _sequential(plan, batch, frames):
+    resident = _Resident(plan, batch)
+    try:
+        rows = []
+        for positions in frames:
+            resident.batch.set_positions(positions)
+            rows.append(resident.run()[0])
+        return rows
+    finally:
+        resident.close()
+
+
+@pytest.mark.parametrize("case", range(len(FRAME_CASES)), ids=[c[0] for c in FRAME_CASES])
+@pytest.mark.parametrize("average,dtype", [("off", "float64"), ("inner", "float64"), ("outer", "float64"),
+                                           ("off", "float32")])
+def test_pipelined_frames_equal_synchronous_runs(hip_context, oracle, case, average, dtype):
+    """Frames queued back to back (graph of frame k+1 built beside the
+    expansion of frame k, the two buffer sets of the batch alternating) give
+    the rows of one synchronous run per frame, bit for bit; the last frame is
+    also checked against the oracle."""
+
+    name, batch, params = FRAME_CASES[case]
+    plan, basis = _plan(hip_context, params, average, dtype)
+    base = np.asarray(batch.positions, np.float64)
+    frames = [base, *_frames(batch, 57 + case), base + 0.01]
+    try:
+        expected = _sequential(plan, batch, frames)
+        got = _pipelined(plan, batch, frames, device_frames=(2,))
+        for k, (rows, want) in enumerate(zip(got, expected)):
+            np.testing.assert_array_equal(rows, want, err_msg=f"{name} {average} {dtype} frame {k}")
+        last = _oracle_soap(oracle, _moved(batch, frames[-1]), params, basis, average)
+        assert scaled_error(got[-1], last) <= _gate(dtype)
+    finally:
+        plan.close()
+
+
+@pytest.mark.parametrize("average", ["off", "outer"])
+def test_pipelined_frames_with_slot_overflow(hip_context, oracle, average):
+    """Both buffer sets start with slots smaller than a centre's rows: the
+    first frame on each overflows and is built again inside the call."""
+
+    batch = _two_dense_clusters()
+    plan, basis = _plan(hip_context, OVERFLOW_PARAMS, average, "float64")
+    base = np.asarray(batch.positions, np.float64)
+    rng = np.random.default_rng(5)
+    frames = [base + rng.normal(0.0, 0.02, base.shape) for _ in range(4)]
+    try:
+        got = _pipelined(plan, batch, frames)
+        for k, positions in enumerate(frames):
+            expected = _oracle_soap(oracle, _moved(batch, positions), OVERFLOW_PARAMS, basis, average)
+            error = scaled_error(got[k], expected)
+            assert error <= F64_GATE, f"{average} frame {k}: scaled error {error:.3e}"
+    finally:
+        plan.close()
+
+
+def test_pipelined_frame_rejects_non_finite_positions(hip_context):
+    """A non-finite frame (host or device memory) fails its call; the frames
+    before it and after it are unaffected."""
+
+    work = workloads.config(2, "small")
+    plan, _ = _plan(hip_context, work.params, "off", "float64")
+    base = np.asarray(work.batch.positions, np.float64)
+    bad = base.copy()
+    bad[17, 1] = np.inf
+    resident = _Resident(plan, work.batch)
+    outs = [_hip.DeviceMemory(max(1, resident.batch.rows * resident.pitch)) for _ in range(2)]
+    memory = _hip.DeviceMemory(bad.nbytes).from_host(bad)
+    try:
+        resident.batch.run_frame(base, outs[0].address, resident.pitch)
+        with pytest.raises(ValueError, match="positions must be finite"):
+            resident.batch.run_frame(bad, outs[1].address, resident.pitch)
+        with pytest.raises(ValueError, match="positions must be finite"):
+            resident.batch.run_frame(memory.address, outs[1].address, resident.pitch)
+        resident.batch.run_frame(base, outs[1].address, resident.pitch)
+        plan.context.wait()
+        shape = (resident.batch.rows, plan.features)
+        first = outs[0].to_host(np.empty(shape, plan.dtype))
+        second = outs[1].to_host(np.empty(shape, plan.dtype))
+        fresh, _ = plan.compute(work.batch)
+        np.testing.assert_array_equal(first, fresh)
+        np.testing.assert_array_equal(second, fresh)
+    finally:
+        memory.free()
+        for out in outs:
+            out.free()
+        resident.close()
+        plan.close()
