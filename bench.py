@@ -12,7 +12,7 @@ jittered by 0.02 A (Gaussian, per coordinate), a different frame every step,
 each written to one of two output buffers on the device.  Steps are
 pipelined: the graph of frame k+1 is built on the context's second stream
 while the expansion of frame k runs; the timed region ends after every step
-has finished (``mdx_hip_wait``).  The same steps as one synchronous
+has finished (``mdx_hip_batch_wait``).  The same steps as one synchronous
 ``mdx_hip_batch_set_positions`` + ``mdx_hip_soap_run`` each are timed before
 it (``sequential``), and give the per-stage breakdown and the expansion
 kernel's launch time.
@@ -496,12 +496,12 @@ def soap_bench(args, workload) -> dict:
     # on the context's second stream while the previous frame's expansion runs
     for k in range(args.warmup):
         frame(k)
-    ctx.wait()
+    dbatch.wait()
     _hip.DeviceMemory.synchronize()
     t0 = time.perf_counter()
     for k in range(args.steps):
         frame(args.warmup + k)
-    ctx.wait()
+    dbatch.wait()
     _hip.DeviceMemory.synchronize()
     elapsed = time.perf_counter() - t0
 

@@ -225,20 +225,26 @@ int mdx_hip_soap_run_noalloc(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, mdx_de
  * in the reference, which rebuilds its grid and graph in each compute_soap
  * call and returns after the call (cpp/src/standalone/soap.cpp:1218-1245):
  * for callers that step through frames (molecular dynamics, trajectory
- * analysis).  The call returns once the frame's graph is built and its
- * expansion queued; the positions have been read by then.  The batch
- * alternates two sets of device buffers, so the graph of one frame is built
- * on a second stream while the previous frame's expansion runs.  Results are
- * bit-identical to the synchronous run.  out_device of a frame is complete
- * after mdx_hip_wait (or after a later synchronous call on the same batch);
- * the caller keeps it alive and unread until then.  A non-finite position
- * returns MDX_INVALID_ARGUMENT ("positions must be finite"). */
+ * analysis).  The call returns once the frame's graph search and expansion
+ * are queued; the positions have been read by then.  The batch alternates
+ * two sets of device buffers, each with its own stream for the graph, so the
+ * graph of one frame is built while the previous frame's search and
+ * expansion run.  A frame's search statistics are read by the next call on
+ * the batch (this one or mdx_hip_batch_wait): a centre that overflowed its
+ * slot has that frame built and expanded again before any later frame's
+ * expansion.  Results are bit-identical to the synchronous run.  A frame's
+ * out_device is complete after mdx_hip_batch_wait on the batch (or after a
+ * later synchronous call on it); the caller keeps the output, the plan and
+ * the cancel flag alive until then, and reads the output only then.  A
+ * non-finite position returns MDX_INVALID_ARGUMENT ("positions must be
+ * finite"); the frames before it are unaffected. */
 int mdx_hip_soap_run_frame(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, mdx_device_batch* batch,
                            const double* positions, void* out_device, int64_t out_pitch_bytes,
                            const volatile int32_t* cancel_flag);
 
-/* Wait for every frame queued on the context by mdx_hip_soap_run_frame. */
-int mdx_hip_wait(mdx_hip_ctx* ctx);
+/* Settle and wait for every frame queued on the batch by
+ * mdx_hip_soap_run_frame. */
+int mdx_hip_batch_wait(mdx_hip_ctx* ctx, mdx_device_batch* batch);
 
 /* Neighbour graph on the device, for parity and the pair-level API.
  * Replaces build_neighbor_graph (cpp/src/common/neighbor.cpp:703-768) as

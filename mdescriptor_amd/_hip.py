@@ -219,7 +219,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
          _i32p],
     ),
-    "mdx_hip_wait": (ctypes.c_int, [ctypes.c_void_p]),
+    "mdx_hip_batch_wait": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
     "mdx_hip_neighbors_build": (
         ctypes.c_int,
         [ctypes.c_void_p, ctypes.POINTER(BatchView), ctypes.c_double, ctypes.c_int32, _i64p],
@@ -317,11 +317,6 @@ class Context:
     def check(self, status: int) -> None:
         if status != MDX_OK:
             _raise_for(status, (self.lib.mdx_hip_last_error(self.handle) or b"").decode())
-
-    def wait(self) -> None:
-        """Wait for the frames queued by :meth:`DeviceBatch.run_frame`."""
-
-        self.check(self.lib.mdx_hip_wait(self.handle))
 
     def close(self) -> None:
         if getattr(self, "handle", None) is not None and self.handle.value:
@@ -532,8 +527,8 @@ class DeviceBatch:
         """One trajectory frame without waiting for it: new positions (a host
         array of shape (atoms, 3), or the device address of atoms * 3 float64
         values) and the descriptors of them into out_device_ptr.  The output
-        is complete after :meth:`Context.wait`; the next frame's graph is
-        built while this frame's expansion runs."""
+        is complete after :meth:`wait`; the next frame's graph is built while
+        this frame's search and expansion run."""
 
         ctx = self.plan.context
         if isinstance(positions, int):
@@ -548,6 +543,12 @@ class DeviceBatch:
         ctx.check(ctx.lib.mdx_hip_soap_run_frame(ctx.handle, self.plan.handle, self.handle, address,
                                                  ctypes.c_void_p(out_device_ptr), int(pitch_bytes), flag))
         del keep
+
+    def wait(self) -> None:
+        """Settle and wait for the frames queued by :meth:`run_frame`."""
+
+        ctx = self.plan.context
+        ctx.check(ctx.lib.mdx_hip_batch_wait(ctx.handle, self.handle))
 
     def close(self) -> None:
         if getattr(self, "handle", None) is not None and self.handle.value:

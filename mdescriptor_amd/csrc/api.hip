@@ -836,9 +836,40 @@ int mdx_hip_batch_upload(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, const mdx_
 
 namespace {
 
-// Wait for the pipelined frames still running on a batch (their expansions
+// The stream on which a pipelined frame of buffer set k builds its graph:
+// one per set, so that the next frame's graph starts while this one's search
+// still runs (the second is the context's copy stream, which the host-batch
+// path uses only inside its own synchronous calls).
+hipStream_t frame_stream(const mdx_hip_ctx* ctx, int k) { return k == 0 ? ctx->graph_stream : ctx->copy_stream; }
+
+// The statistics of the batch's last pipelined frame, read once its search
+// has finished.  A centre that overflowed its slot (the queued expansion then
+// read clamped rows) has the frame built again on the compact layout from the
+// positions still in its set and expanded again into its output, on the main
+// stream behind the expansion that was wrong and before any later one.
+void settle(mdx_hip_ctx* ctx, mdx_device_batch* batch) {
+    const int j = batch->pending;
+    if (j < 0) return;
+    batch->pending = -1;
+    mdx::PreparedBatch& pb = j == 0 ? batch->pb : *batch->pb2;
+    mdx::DeviceGraph& graph = j == 0 ? batch->graph : batch->graph2;
+    mdx::DeviceBuffer& partials = j == 0 ? batch->partials : batch->partials2;
+    const volatile int32_t* cancel = batch->pending_cancel;
+    if (mdx::complete_graph(pb, graph, cancel)) return;
+    hipStream_t s = ctx->stream;
+    MDX_HIP(hipStreamSynchronize(s)); // the first expansion's buffers are replaced
+    MDX_HIP(hipStreamSynchronize(frame_stream(ctx, j)));
+    mdx::build_graph(s, pb, graph, cancel, true, false, true);
+    check_cancel(cancel);
+    mdx::run_soap(s, *batch->pending_plan, pb, graph, batch->pending_out, batch->pending_pitch, partials, cancel,
+                  nullptr, nullptr);
+    MDX_HIP(hipEventRecord(batch->done[j], s));
+}
+
+// Settle the batch's pipelined frames and wait for them (their expansions
 // read its sets), so that a synchronous call may reuse set 0.
-void quiesce(mdx_device_batch* batch) {
+void quiesce(mdx_hip_ctx* ctx, mdx_device_batch* batch) {
+    settle(ctx, batch);
     for (int k = 0; k < 2; ++k) {
         if (batch->queued[k]) {
             MDX_HIP(hipEventSynchronize(batch->done[k]));
@@ -859,7 +890,7 @@ int mdx_hip_batch_set_positions(mdx_hip_ctx* ctx, mdx_device_batch* batch, const
         if (values == 0) return;
         if (positions == nullptr) throw mdx::Error(MDX_INVALID_ARGUMENT, "null positions");
         DeviceScope scope(ctx->device);
-        quiesce(batch);
+        quiesce(ctx, batch);
         if (is_device_memory(positions)) {
             // checked for finiteness by the next run's frame kernels
             MDX_HIP(hipMemcpyAsync(batch->pb.d_positions.ptr, positions, values * sizeof(double),
@@ -912,7 +943,7 @@ int mdx_hip_soap_run(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, mdx_device_bat
         check_device_run(ctx, plan, batch, out_device, out_pitch_bytes);
         check_cancel(cancel_flag);
         DeviceScope scope(ctx->device);
-        quiesce(batch);
+        quiesce(ctx, batch);
         run_pipeline(ctx, *plan, batch->pb, batch->graph, batch->partials, out_device, out_pitch_bytes, cancel_flag,
                      timing);
         ctx->finished.wait(ctx->stream);
@@ -929,7 +960,7 @@ int mdx_hip_soap_run_noalloc(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, mdx_de
         check_device_run(ctx, plan, batch, out_device, out_pitch_bytes);
         check_cancel(cancel_flag);
         DeviceScope scope(ctx->device);
-        quiesce(batch);
+        quiesce(ctx, batch);
         // every piece is carved afresh from the start of the array; the
         // graph's counters are cleared on the stream before each build
         ctx->arena.reset();
@@ -963,7 +994,7 @@ int mdx_hip_soap_run_frame(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, mdx_devi
                                       static_cast<int64_t>(batch->host_numbers.size())};
             pb2->include_boundary = 1;
             mdx::prepare_batch(view, plan->species.data(), plan->S, plan->cutoff, *pb2);
-            mdx::upload_batch(ctx->graph_stream, view, *pb2);
+            mdx::upload_batch(frame_stream(ctx, 1), view, *pb2);
             batch->pb2 = std::move(pb2);
         }
         for (int e = 0; e < 2; ++e) {
@@ -974,12 +1005,13 @@ int mdx_hip_soap_run_frame(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, mdx_devi
         mdx::DeviceGraph& graph = k == 0 ? batch->graph : batch->graph2;
         mdx::DeviceBuffer& partials = k == 0 ? batch->partials : batch->partials2;
         // the set's buffers are rebuilt (and may be reallocated) only after
-        // the expansion that last read them has finished
+        // the expansion that last read them has finished; that frame was
+        // settled by the call after it
         if (batch->queued[k]) {
             MDX_HIP(hipEventSynchronize(batch->done[k]));
             batch->queued[k] = false;
         }
-        hipStream_t gs = ctx->graph_stream, s = ctx->stream;
+        hipStream_t gs = frame_stream(ctx, k), s = ctx->stream;
         if (values > 0) {
             if (is_device_memory(positions)) {
                 // checked for finiteness by the frame kernels below
@@ -995,35 +1027,35 @@ int mdx_hip_soap_run_frame(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, mdx_devi
                                        hipMemcpyHostToDevice, gs));
             }
         }
-        // this frame's graph on the second stream, beside the previous
-        // frame's expansion; its expansion on the main stream behind both
+        // this frame's graph on its set's stream, beside the previous frame's
+        // search and expansion (the call returns from the frame read-back
+        // with the search queued); its expansion on the main stream behind
+        // the graph and the previous frame, which is settled first
         mdx::build_graph(gs, pb, graph, cancel_flag, true, true);
         MDX_HIP(hipEventRecord(batch->ready[k], gs));
+        settle(ctx, batch);
         MDX_HIP(hipStreamWaitEvent(s, batch->ready[k], 0));
         check_cancel(cancel_flag);
         mdx::run_soap(s, *plan, pb, graph, out_device, out_pitch_bytes, partials, cancel_flag, nullptr, nullptr);
-        if (!mdx::complete_graph(pb, graph, cancel_flag)) {
-            // a centre overflowed its slot: the frame again, in order, on the
-            // main stream (its buffers are replaced)
-            MDX_HIP(hipStreamSynchronize(s));
-            MDX_HIP(hipStreamSynchronize(gs));
-            mdx::build_graph(s, pb, graph, cancel_flag, true, false, true);
-            check_cancel(cancel_flag);
-            mdx::run_soap(s, *plan, pb, graph, out_device, out_pitch_bytes, partials, cancel_flag, nullptr, nullptr);
-        }
         MDX_HIP(hipEventRecord(batch->done[k], s));
         batch->queued[k] = true;
+        batch->pending = k;
+        batch->pending_plan = plan;
+        batch->pending_out = out_device;
+        batch->pending_pitch = out_pitch_bytes;
+        batch->pending_cancel = cancel_flag;
         batch->next_set = k ^ 1;
     });
 }
 
-int mdx_hip_wait(mdx_hip_ctx* ctx) {
+int mdx_hip_batch_wait(mdx_hip_ctx* ctx, mdx_device_batch* batch) {
     if (ctx == nullptr) return MDX_INVALID_ARGUMENT;
     std::lock_guard<std::mutex> lock(ctx->mutex);
     return guarded(ctx, [&] {
+        if (batch == nullptr) throw mdx::Error(MDX_INVALID_ARGUMENT, "null batch");
+        if (batch->device != ctx->device) throw mdx::Error(MDX_INVALID_ARGUMENT, "batch belongs to another device");
         DeviceScope scope(ctx->device);
-        MDX_HIP(hipStreamSynchronize(ctx->graph_stream));
-        MDX_HIP(hipStreamSynchronize(ctx->stream));
+        quiesce(ctx, batch);
     });
 }
 

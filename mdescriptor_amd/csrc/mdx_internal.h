@@ -496,7 +496,9 @@ struct mdx_device_batch {
     // Pipelined frames (mdx_hip_soap_run_frame) alternate two sets: set 0 is
     // the one above, set 1 is prepared on the first such run from the host
     // copy of the batch kept here.  A set is rebuilt only after the expansion
-    // that last read it has finished (done[set]).
+    // that last read it has finished (done[set]).  A frame's graph is built on
+    // its set's stream (the context's graph stream for set 0, its copy stream
+    // for set 1).
     std::unique_ptr<mdx::PreparedBatch> pb2;
     mdx::DeviceGraph graph2;
     mdx::DeviceBuffer partials2;
@@ -504,9 +506,17 @@ struct mdx_device_batch {
     std::vector<double> host_positions, host_cells;
     std::vector<int64_t> host_offsets;
     int next_set = 0;
-    hipEvent_t ready[2] = {}; // graph of the set built (second stream)
+    hipEvent_t ready[2] = {}; // graph of the set built (the set's frame stream)
     hipEvent_t done[2] = {};  // expansion of the set finished (main stream)
     bool queued[2] = {};      // done[set] recorded and not yet waited for
+    // The last pipelined frame, whose search statistics are read (and which
+    // is built and expanded again if a centre overflowed its slot) by the next
+    // call on the batch: its set (-1: none), plan, output and cancel flag.
+    int pending = -1;
+    const mdx_soap_plan* pending_plan = nullptr;
+    void* pending_out = nullptr;
+    int64_t pending_pitch = 0;
+    const volatile int32_t* pending_cancel = nullptr;
     ~mdx_device_batch() {
         for (int k = 0; k < 2; ++k) {
             if (queued[k]) (void)hipEventSynchronize(done[k]);

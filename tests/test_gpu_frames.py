@@ -334,7 +334,7 @@ def _pipelined(plan, batch, frames, device_frames=()):
                 resident.batch.run_frame(staged[-1].address, outs[k].address, resident.pitch)
             else:
                 resident.batch.run_frame(positions, outs[k].address, resident.pitch)
-        plan.context.wait()
+        resident.batch.wait()
         shape = (resident.batch.rows, plan.features)
         return [out.to_host(np.empty(shape, plan.dtype)) for out in outs]
     finally:
@@ -418,7 +418,7 @@ def test_pipelined_frame_rejects_non_finite_positions(hip_context):
         with pytest.raises(ValueError, match="positions must be finite"):
             resident.batch.run_frame(memory.address, outs[1].address, resident.pitch)
         resident.batch.run_frame(base, outs[1].address, resident.pitch)
-        plan.context.wait()
+        resident.batch.wait()
         shape = (resident.batch.rows, plan.features)
         first = outs[0].to_host(np.empty(shape, plan.dtype))
         second = outs[1].to_host(np.empty(shape, plan.dtype))
@@ -429,5 +429,30 @@ def test_pipelined_frame_rejects_non_finite_positions(hip_context):
         memory.free()
         for out in outs:
             out.free()
+        resident.close()
+        plan.close()
+
+
+def test_pipelined_frames_share_one_output(hip_context, oracle):
+    """Every frame into the same output buffer, the first frames overflowing
+    their slots: the frame built and expanded again lands before the next
+    frame's expansion, so the buffer ends with the last frame's rows."""
+
+    batch = _two_dense_clusters()
+    plan, basis = _plan(hip_context, OVERFLOW_PARAMS, "off", "float64")
+    base = np.asarray(batch.positions, np.float64)
+    rng = np.random.default_rng(9)
+    resident = _Resident(plan, batch)
+    try:
+        for count in (1, 2, 3):
+            frames = [base + rng.normal(0.0, 0.02, base.shape) for _ in range(count)]
+            for positions in frames:
+                resident.batch.run_frame(positions, resident.out.address, resident.pitch)
+            resident.batch.wait()
+            rows = resident.out.to_host(np.empty((resident.batch.rows, plan.features), plan.dtype))
+            expected = _oracle_soap(oracle, _moved(batch, frames[-1]), OVERFLOW_PARAMS, basis, "off")
+            error = scaled_error(rows, expected)
+            assert error <= F64_GATE, f"{count} frames: scaled error {error:.3e}"
+    finally:
         resident.close()
         plan.close()
