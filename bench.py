@@ -161,8 +161,9 @@ def frame_positions(batch, count: int) -> list[np.ndarray]:
 
 
 def profile_average_us(workload_name: str, kernel: str) -> tuple[float | None, str | None]:
-    """Average duration of `kernel` in the committed rocprofv3 kernel-trace
-    summary of this workload (the ``| name | calls | average us |`` table)."""
+    """Average duration of `kernel` over the synchronous steps in the
+    committed rocprofv3 kernel-trace summary of this workload (the third
+    column of its ``| name | calls | average us (synchronous) | ...`` table)."""
 
     path = ROOT / "profiles" / f"{kernel.split('<')[0]}_{workload_name}_kernel_trace.md"
     if not path.is_file():
