@@ -420,28 +420,36 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
     // centres in LDS (a row per centre would multiply the traffic by the
     // run length).
     const bool outer_fits = (!inner_fits || p.block_forced) && static_cast<double>(pb.atoms) * static_cast<double>(d.F) * 8.0 <= 4294967296.0;
+    // Outer averages of small structures (or of more structures than fill
+    // the device), unweighted and without mu1nu1, take it with a workgroup
+    // per structure: each centre's power spectrum is added into the
+    // structure's float64 row in LDS and the mean written once, with no
+    // partial rows in HBM.
+    const bool outer_lds = p.average == 2 && inner_fits && p.weighted == 0 && p.compression != 2 &&
+                           d.F * static_cast<int64_t>(sizeof(double)) <= kBlockOuterLdsBytes;
     // (inner averages with neighbour weights only as runs of centres: the
     // per-structure modes do not weight)
     const bool block = p.block_waves > 0 &&
-                       (p.average == 0 || (p.average == 2 && outer_fits) ||
+                       (p.average == 0 || (p.average == 2 && (outer_fits || outer_lds)) ||
                         (p.average == 1 && p.compression == 0 && (p.weighted == 0 || !inner_fits))) &&
                        g.row_bound < kQuadMaxRows;
     const bool block_inner = block && p.average == 1 && inner_fits;
     // other inner averages on that kernel: runs of a structure's centres
     // into partial rows, folded, then a launch of one workgroup per structure
     const bool block_runs = block && p.average == 1 && !inner_fits;
-    const bool block_outer = block && p.average == 2;
+    const bool block_outer_lds = block && outer_lds;
+    const bool block_outer = block && p.average == 2 && !outer_lds;
 
     // work items
     std::vector<int64_t>& item_begin_h = pb.item_begin;
     std::vector<int64_t>& struct_items_h = pb.struct_items;
     item_begin_h.clear();
     struct_items_h.clear();
-    int64_t items = block_inner ? pb.structures : pb.atoms;
+    int64_t items = block_inner || block_outer_lds ? pb.structures : pb.atoms;
     if (block_outer) {
         // items are the centres, a structure's partial rows its atoms
         struct_items_h = pb.offsets;
-    } else if (p.average != 0 && !block_inner) {
+    } else if (p.average != 0 && !block_inner && !block_outer_lds) {
         struct_items_h.resize(static_cast<size_t>(pb.structures) + 1);
         for (int64_t s = 0; s < pb.structures; ++s) {
             struct_items_h[static_cast<size_t>(s)] = static_cast<int64_t>(item_begin_h.size());
@@ -466,7 +474,7 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
     double* d_folded = nullptr;
     int64_t* d_fold_items = nullptr;
     std::vector<int64_t>& fold_items_h = pb.fold_items;
-    if (p.average != 0 && !block_inner) {
+    if (p.average != 0 && !block_inner && !block_outer_lds) {
         const size_t inner_width = p.use_mfma ? static_cast<size_t>(mfma_coefficient_rows(p.Sc, p.n, p.compression)) * static_cast<size_t>(p.hpad)
                                               : static_cast<size_t>(d.C);
         const size_t width = block_runs ? static_cast<size_t>(block_partial_width(p.l_max, p.block_ncr))
@@ -588,11 +596,14 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
                 ba.lane_beta = p.d_block_beta.as<double>();
                 ba.ps_offsets = p.d_block_ps.as<int32_t>();
                 ba.S = p.S;
-                ba.out_dtype = block_outer ? 8 : p.out_dtype;
+                ba.out_dtype = block_outer || block_outer_lds ? 8 : p.out_dtype;
                 ba.F = p.features;
                 ba.item_base = base;
                 ba.items = count;
-                ba.struct_offsets = block_inner ? pb.d_offsets.as<int64_t>() : block_runs ? d_item_begin : nullptr;
+                ba.struct_offsets = block_inner || block_outer_lds ? pb.d_offsets.as<int64_t>()
+                                    : block_runs                  ? d_item_begin
+                                                                  : nullptr;
+                ba.outer_lds = block_outer_lds ? p.out_dtype : 0;
                 ba.partial_out = block_runs ? d_partial : nullptr;
                 ba.small_structures = block_inner && largest_structure <= kBlockSmallAtoms ? 1 : 0;
                 ba.summed = p.compression == 2 ? 1 : 0;
@@ -646,7 +657,7 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
             fa.item_base = 0;
             fa.items = pb.structures;
             launch_block_expand(stream, p.l_max, p.block_kg, p.block_ncr, fa, pb.structures);
-        } else if (block_inner) {
+        } else if (block_inner || block_outer_lds) {
             // rows of structures without atoms (the expansion visits none of them)
             bool empty = false;
             for (int64_t st = 0; st < pb.structures && !empty; ++st) {

@@ -16,9 +16,13 @@ namespace mdx {
 // large structures in two launches: runs of a structure's centres leave
 // their summed coefficient registers in partial rows (with or without
 // neighbour weights), then a row per structure from the sum of its partial
-// rows.
+// rows; outer averages of structures a workgroup each, every centre's power
+// spectrum added into the structure's float64 row in LDS and the mean
+// written once.
 constexpr int kBlockRows = 0, kBlockInner = 1, kBlockInnerSmall = 2, kBlockRowsWeighted = 3, kBlockRowsSummed = 4,
-              kBlockInnerRuns = 5, kBlockInnerFinal = 6, kBlockInnerRunsWeighted = 7;
+              kBlockInnerRuns = 5, kBlockInnerFinal = 6, kBlockInnerRunsWeighted = 7, kBlockOuterLds = 8;
+// largest row (features x 8 bytes) the outer mode accumulates in LDS
+constexpr int64_t kBlockOuterLdsBytes = 48 * 1024;
 constexpr int kBlockSmallAtoms = 64;
 
 // Launch arguments (one struct, passed by value).
@@ -60,6 +64,11 @@ struct BlockArgs {
     double* partial_out;
     const double* partial_in;
     const int64_t* part_items;
+    // outer averages in LDS (items = structures, struct_offsets = the
+    // batch's atom offsets, out_dtype 8: the plan's tables are those of
+    // float64 rows): a row per structure, the mean of its centres' power
+    // spectra, written with outer_lds bytes per value (4 or 8; 0: off)
+    int outer_lds;
     void* out;
     int64_t pitch;              // bytes between output rows
 };

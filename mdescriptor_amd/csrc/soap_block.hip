@@ -373,7 +373,7 @@ __device__ __forceinline__ int64_t uniform64(int64_t v) {
 }
 
 template <int LM, int KG, int NCR, int ES, int MODE, int W>
-__device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, const int* s_ps) {
+__device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, const int* s_ps, double* s_acc) {
     using PL = BlockPlan<LM, KG>;
     constexpr int L = PL::L, R = PL::R, P = PL::P, RPL = PL::RPL, NT = PL::NT, GS = PL::GS;
     constexpr int GROUPS = PL::GROUPS;
@@ -433,7 +433,11 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
     // rows of structure averages (the runs' launch sums a run of a structure's
     // centres the same way, into a partial row)
     constexpr bool inner = MODE == kBlockInner || MODE == kBlockInnerSmall || MODE == kBlockInnerRuns ||
-                           MODE == kBlockInnerRunsWeighted;
+                           MODE == kBlockInnerRunsWeighted || MODE == kBlockOuterLds;
+    // outer averages in LDS: a structure's centres one by one, each centre's
+    // power spectrum added into s_acc (F float64 values), its mean written
+    // when the structure ends
+    constexpr bool kOuter = MODE == kBlockOuterLds;
     constexpr bool kRuns = MODE == kBlockInnerRuns || MODE == kBlockInnerRunsWeighted;
     constexpr bool kFinal = MODE == kBlockInnerFinal;
     // this wavefront's registers in a partial row, and the row's width
@@ -718,13 +722,17 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
         char* row = static_cast<char*>(a.out) + row0 * a.pitch;
         const __amdgpu_buffer_rsrc_t rsrc =
             __builtin_amdgcn_make_buffer_rsrc(row, 0, static_cast<int>(F * ES), 0x00020000);
-        // one 4-value store per lane and value of a Gram tile
+        // one 4-value store per lane and value of a Gram tile (outer
+        // averages: added into the structure's row in LDS, each feature by
+        // one lane; the pairs not stored are past the row)
         auto store_tile = [&](const d4& D, const int* fb, const int* fs, int l) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const double v = D[r]; // the coefficients carry sqrt(pi sqrt(8/(2l+1)))
                 const int off = fb[r] + l * fs[r];
-                if constexpr (ES == 4) {
+                if constexpr (kOuter) {
+                    if (off < static_cast<int>(F * ES)) s_acc[off / ES] += v;
+                } else if constexpr (ES == 4) {
                     __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(static_cast<float>(v)), rsrc, off, 0, 0);
                 } else {
                     typedef int i2v __attribute__((ext_vector_type(2)));
@@ -949,10 +957,32 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
         if (ends0) {
             merge(__builtin_amdgcn_readfirstlane(cur));
             cur = -1;
+            // outer averages: the centre's power spectrum into the row in LDS
+            if constexpr (kOuter) row_end(row0, 1.0);
         }
         // ------------------------------------ row end: fold, power spectrum
         if (last0) {
-            if constexpr (kRuns) {
+            if constexpr (kOuter) {
+                // every wavefront's additions are in: the mean to the
+                // structure's row, the LDS row back to zero for the next
+                __syncthreads();
+                const double inv = 1.0 / static_cast<double>(uniform64(a.struct_offsets[row0 + 1]) -
+                                                             uniform64(a.struct_offsets[row0]));
+                char* orow = static_cast<char*>(a.out) + row0 * a.pitch;
+                // (the plan's tables are those of float64 rows; the mean is
+                // written in the output's type, a.outer_lds bytes)
+                const bool f32 = a.outer_lds == 4;
+                for (int64_t f = threadIdx.x; f < F; f += blockDim.x) {
+                    const double v = s_acc[f] * inv;
+                    s_acc[f] = 0.0;
+                    if (f32) {
+                        reinterpret_cast<float*>(orow)[f] = static_cast<float>(v);
+                    } else {
+                        reinterpret_cast<double*>(orow)[f] = v;
+                    }
+                }
+                __syncthreads();
+            } else if constexpr (kRuns) {
                 // the run's summed coefficient registers to its partial row
                 double* part = a.partial_out + row0 * kPartWidth + kPartBase + lane;
                 unroll<NU>([&](auto uc) {
@@ -1008,6 +1038,8 @@ k_soap_block(BlockArgs a) {
     // register against the species-summed one; no more is read
     constexpr int kPsWords = ps_tiles(NCR, MODE == kBlockRowsSummed) * 4 * kWaveThreads;
     __shared__ int s_ps[kPsWords];
+    // outer averages in LDS: the structure's row (F float64), sized at launch
+    extern __shared__ double s_acc[];
     const int tid = threadIdx.x;
     for (int i = tid; i < kPsWords; i += static_cast<int>(blockDim.x)) s_ps[i] = a.ps_offsets[i];
     const int threads = static_cast<int>(blockDim.x);
@@ -1038,18 +1070,21 @@ k_soap_block(BlockArgs a) {
             s_scale[i] = c <= 2 * l ? kScaledHarmonic.s[l][c <= l ? l - c : c - l] * kPsRoot[l] : 0.0;
         }
     }
+    if constexpr (MODE == kBlockOuterLds) {
+        for (int64_t i = tid; i < a.F; i += threads) s_acc[i] = 0.0;
+    }
     __syncthreads();
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWaveThreads);
     if (wave == 0) {
-        block_role<LM, KG, NCR, ES, MODE, 0>(a, lds, s_ps);
+        block_role<LM, KG, NCR, ES, MODE, 0>(a, lds, s_ps, s_acc);
     } else if constexpr (PL::T > 1) {
         if (wave == 1) {
-            block_role<LM, KG, NCR, ES, MODE, (PL::T > 1 ? 1 : 0)>(a, lds, s_ps);
+            block_role<LM, KG, NCR, ES, MODE, (PL::T > 1 ? 1 : 0)>(a, lds, s_ps, s_acc);
         } else if constexpr (PL::T > 2) {
             if (wave == 2) {
-                block_role<LM, KG, NCR, ES, MODE, (PL::T > 2 ? 2 : 0)>(a, lds, s_ps);
+                block_role<LM, KG, NCR, ES, MODE, (PL::T > 2 ? 2 : 0)>(a, lds, s_ps, s_acc);
             } else if constexpr (PL::T > 3) {
-                block_role<LM, KG, NCR, ES, MODE, (PL::T > 3 ? 3 : 0)>(a, lds, s_ps);
+                block_role<LM, KG, NCR, ES, MODE, (PL::T > 3 ? 3 : 0)>(a, lds, s_ps, s_acc);
             }
         }
     }
@@ -1064,7 +1099,10 @@ size_t lds_bytes() {
 template <int LM, int KG, int NCR>
 void launch_shape(hipStream_t stream, const BlockArgs& a, int64_t count) {
     using PL = BlockPlan<LM, KG>;
-    const size_t lds = lds_bytes<LM, KG, NCR>() + ps_tiles(NCR, a.summed != 0) * 4 * kWaveThreads * sizeof(int);
+    // outer averages in LDS: the structure's float64 row beside the tables
+    const size_t row_lds = a.outer_lds != 0 ? static_cast<size_t>(a.F) * sizeof(double) : 0;
+    const size_t lds = lds_bytes<LM, KG, NCR>() + ps_tiles(NCR, a.summed != 0) * 4 * kWaveThreads * sizeof(int) +
+                       row_lds;
     const int64_t resident = std::max<int64_t>(1, std::min<int64_t>(8, (160 * 1024) / std::max<size_t>(lds, 1)));
     const int64_t target = std::max<int64_t>(1, 8 * resident * device_compute_units());
     BlockArgs args = a;
@@ -1075,7 +1113,8 @@ void launch_shape(hipStream_t stream, const BlockArgs& a, int64_t count) {
     args.per_block = std::max<int64_t>(least, (count + target - 1) / target);
     const unsigned grid = static_cast<unsigned>((count + args.per_block - 1) / args.per_block);
     const dim3 threads(PL::T * kWaveThreads);
-    const int mode = a.partial_in != nullptr    ? kBlockInnerFinal
+    const int mode = a.outer_lds != 0            ? kBlockOuterLds
+                     : a.partial_in != nullptr    ? kBlockInnerFinal
                      : a.partial_out != nullptr ? (a.species_w != nullptr ? kBlockInnerRunsWeighted : kBlockInnerRuns)
                      : a.struct_offsets != nullptr ? (a.small_structures ? kBlockInnerSmall : kBlockInner)
                      : a.species_w != nullptr ? kBlockRowsWeighted
@@ -1083,10 +1122,11 @@ void launch_shape(hipStream_t stream, const BlockArgs& a, int64_t count) {
                                               : kBlockRows;
     auto launch = [&](auto m) {
         constexpr int M = decltype(m)::value;
+        const unsigned dyn = M == kBlockOuterLds ? static_cast<unsigned>(row_lds) : 0u;
         if (a.out_dtype == 4) {
-            hipLaunchKernelGGL((k_soap_block<LM, KG, NCR, 4, M>), dim3(grid), threads, 0, stream, args);
+            hipLaunchKernelGGL((k_soap_block<LM, KG, NCR, 4, M>), dim3(grid), threads, dyn, stream, args);
         } else {
-            hipLaunchKernelGGL((k_soap_block<LM, KG, NCR, 8, M>), dim3(grid), threads, 0, stream, args);
+            hipLaunchKernelGGL((k_soap_block<LM, KG, NCR, 8, M>), dim3(grid), threads, dyn, stream, args);
         }
     };
     if (mode == kBlockRows) {
@@ -1103,6 +1143,8 @@ void launch_shape(hipStream_t stream, const BlockArgs& a, int64_t count) {
         launch(std::integral_constant<int, kBlockInnerRunsWeighted>{});
     } else if (mode == kBlockInnerFinal) {
         launch(std::integral_constant<int, kBlockInnerFinal>{});
+    } else if (mode == kBlockOuterLds) {
+        launch(std::integral_constant<int, kBlockOuterLds>{});
     } else {
         launch(std::integral_constant<int, kBlockRowsSummed>{});
     }
@@ -1290,6 +1332,10 @@ void launch_block_expand(hipStream_t stream, int l_max, int kg, int ncr, const B
     if (count <= 0) return;
     const ShapeEntry* e = find_shape(l_max, kg, ncr);
     if (e == nullptr) throw Error(MDX_INTERNAL, "SOAP shape is not compiled for the register-coefficient kernel");
+    if (a.outer_lds != 0 && (a.struct_offsets == nullptr || a.out_dtype != 8 ||
+                             a.F * static_cast<int64_t>(sizeof(double)) > kBlockOuterLdsBytes)) {
+        throw Error(MDX_INTERNAL, "outer average row does not fit the register-coefficient kernel's LDS");
+    }
     e->launch(stream, a, count);
     MDX_HIP(hipGetLastError());
 }

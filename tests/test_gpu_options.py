@@ -149,3 +149,60 @@ def test_public_soap_with_options(hip_context, oracle):
     assert scaled_error(np.asarray(result.values), expected) <= F64_GATE
     assert len(result.labels) == soap.feature_count == expected.shape[1]
     assert result.labels[0].startswith("soap:compression=mu1nu1,")
+
+
+def _with_empty_structure(batch):
+    """The batch with an empty structure inserted after its first one."""
+
+    from types import SimpleNamespace
+
+    offsets = np.asarray(batch.offsets, np.int64)
+    return SimpleNamespace(numbers=batch.numbers, positions=batch.positions,
+                           cells=np.concatenate([batch.cells[:1], np.zeros((1, 3, 3)), batch.cells[1:]]),
+                           pbc=np.concatenate([batch.pbc[:1], np.zeros((1, 3), np.int32), batch.pbc[1:]]),
+                           offsets=np.concatenate([offsets[:2], offsets[1:]]))
+
+
+OUTER_LDS_CASES = {
+    # molecules of configuration 3 (5 species, n 6, l 4)
+    "molecules": (3, None, 6, 4),
+    # the same molecules as four species (F read as O) at configuration 2's n 8, l 6
+    "molecules_hcno": (3, {9: 8}, 8, 6),
+}
+
+
+@pytest.mark.parametrize("case", sorted(OUTER_LDS_CASES))
+@pytest.mark.parametrize("name", ["default", "mu2", "crossover"])
+@pytest.mark.parametrize("dtype", ["float64", "float32"])
+def test_outer_average_in_lds_on_register_coefficient_kernel(hip_context, oracle, case, name, dtype):
+    """Outer averages of many small structures on the register-coefficient
+    kernel: a workgroup per structure adds each centre's power spectrum into
+    the structure's row in LDS and writes the mean; an empty structure gets a
+    zero row."""
+
+    config, remap, n_max, l_max = OUTER_LDS_CASES[case]
+    w = workloads.config(config, "small")
+    p = dict(w.params)
+    batch = _with_empty_structure(w.batch)
+    if remap:
+        numbers = np.asarray(batch.numbers).copy()
+        for old, new in remap.items():
+            numbers[numbers == old] = new
+        batch.numbers = numbers
+        p["species"] = sorted(set(p["species"]) - set(remap))
+    # unweighted compressions (the mode takes no neighbour weights)
+    options = None if name == "default" else {"compression": name}
+    alphas, betas = basis_gto(p["r_cut"], n_max, l_max)
+    plan = _hip.SoapPlan(hip_context, species=p["species"], n_max=n_max, l_max=l_max, r_cut=p["r_cut"], sigma=1.0,
+                         alphas=alphas, betas=betas, average="outer", dtype=dtype, options=options)
+    try:
+        values, timing = plan.compute(batch)
+    finally:
+        plan.close()
+    assert timing["expansion_tiles"] <= -1000
+    expected = oracle.soap(batch, species=p["species"], n_max=n_max, l_max=l_max, r_cut=p["r_cut"], sigma=1.0,
+                           alphas=alphas, betas=betas, average="outer", options=options)
+    assert values.shape == expected.shape
+    assert np.all(values[1] == 0)
+    error = scaled_error(values, expected)
+    assert error <= (F64_GATE if dtype == "float64" else F32_GATE), f"{case} {name} {dtype}: scaled error {error:.3e}"
