@@ -472,6 +472,12 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
     int64_t fold_per_split = 0;
     size_t partial_width = 0;
     double* d_folded = nullptr;
+    // weighted plans on the register-coefficient kernel: each pair row's
+    // weight, computed once before the expansion (k_block_row_weights), after
+    // any partial rows in the scratch buffer
+    const size_t row_w_bytes =
+        block && p.weighted != 0 ? ((g.pair_bin.bytes / sizeof(uint32_t)) * sizeof(double) + 255) & ~size_t(255) : 0;
+    double* d_row_w = nullptr;
     int64_t* d_fold_items = nullptr;
     std::vector<int64_t>& fold_items_h = pb.fold_items;
     if (p.average != 0 && !block_inner && !block_outer_lds) {
@@ -496,8 +502,13 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
         const size_t head = ((item_begin_h.size() + struct_items_h.size() + fold_items_h.size()) * sizeof(int64_t) + 255) &
                             ~size_t(255);
         const size_t partial_bytes = (static_cast<size_t>(items) * width * sizeof(double) + 255) & ~size_t(255);
-        const size_t folded_bytes = static_cast<size_t>(pb.structures) * static_cast<size_t>(fold_splits) * width * sizeof(double);
-        scratch.reserve(head + partial_bytes + folded_bytes);
+        const size_t folded_bytes =
+            (static_cast<size_t>(pb.structures) * static_cast<size_t>(fold_splits) * width * sizeof(double) + 255) &
+            ~size_t(255);
+        scratch.reserve(head + partial_bytes + folded_bytes + row_w_bytes);
+        if (row_w_bytes > 0) {
+            d_row_w = reinterpret_cast<double*>(static_cast<char*>(scratch.ptr) + head + partial_bytes + folded_bytes);
+        }
         d_item_begin = scratch.as<int64_t>();
         d_struct_items = d_item_begin + item_begin_h.size();
         d_fold_items = d_struct_items + struct_items_h.size();
@@ -513,6 +524,10 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
             MDX_HIP(hipMemcpyAsync(d_fold_items, fold_items_h.data(), fold_items_h.size() * sizeof(int64_t),
                                    hipMemcpyHostToDevice, stream));
         }
+    }
+    if (row_w_bytes > 0 && d_row_w == nullptr) {
+        scratch.reserve(row_w_bytes);
+        d_row_w = scratch.as<double>();
     }
     // the partial rows the finalize kernels walk, folded first where
     // structures have many items
@@ -580,6 +595,30 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
         const int tt = mfma_template_tiles(p.tiles);
         BlockArgs block_args{};
         if (events != nullptr) MDX_HIP(hipEventRecord(events[2], stream));
+        if (d_row_w != nullptr) {
+            BlockArgs wa{};
+            wa.positions = pb.d_positions.as<double>();
+            wa.pair_start = g.pair_start.as<int64_t>();
+            wa.counts = g.counts.as<int32_t>();
+            wa.pair_bin = g.pair_bin.as<uint32_t>();
+            wa.bx = g.bin_x.as<double>();
+            wa.by = g.bin_y.as<double>();
+            wa.bz = g.bin_z.as<double>();
+            wa.S = p.S;
+            wa.weighting = p.weighting;
+            wa.has_w0 = p.has_w0;
+            wa.w_r0 = p.w_r0;
+            wa.w_c = p.w_c;
+            wa.w_d = p.w_d;
+            wa.w_m = p.w_m;
+            wa.w_w0 = p.w_w0;
+            wa.species_w = p.d_species_w.as<double>();
+            wa.bin_atom = g.bin_atom.as<int32_t>();
+            wa.bin_image = g.bin_image.as<int32_t>();
+            wa.bin_type = g.bin_type.as<int32_t>();
+            wa.images = pb.d_images.as<ImageDesc>();
+            launch_block_row_weights(stream, wa, pb.atoms, d_row_w);
+        }
         for (int64_t base = 0; base < items; base += slice) {
             if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
             const int64_t count = std::min(slice, items - base);
@@ -620,6 +659,7 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
                     ba.bin_atom = g.bin_atom.as<int32_t>();
                     ba.bin_image = g.bin_image.as<int32_t>();
                     ba.images = pb.d_images.as<ImageDesc>();
+                    ba.row_w = d_row_w;
                 }
                 ba.out = block_outer ? static_cast<void*>(d_partial) : out_device;
                 ba.pitch = block_outer ? static_cast<int64_t>(partial_width * sizeof(double)) : pitch_bytes;

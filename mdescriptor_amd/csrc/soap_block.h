@@ -52,7 +52,10 @@ struct BlockArgs {
     const double* species_w;             // null: no weights
     const int32_t* bin_atom;             // atom of each binned image
     const int32_t* bin_image;            // image of each binned image (w0: the exact self pair)
+    const int32_t* bin_type;             // species of each binned image
     const ImageDesc* images;             // image table (integer shifts)
+    const double* row_w;                 // weighted modes: each pair row's weight, distance function
+                                         // (or w0) times species weight (k_block_row_weights)
     int summed;                          // mu1nu1: spectrum against the species-summed coefficients
     int mu2;                             // mu2: every species' sums into the first species' slots
     // inner averages in two launches: the runs' launch writes partial_out
@@ -93,6 +96,12 @@ bool block_plan_tables(int S, int n, int l_max, int out_dtype, int compression, 
 void launch_block_expand(hipStream_t stream, int l_max, int kg, int ncr, const BlockArgs& a, int64_t count);
 // doubles in one partial row of the runs' launch
 int64_t block_partial_width(int l_max, int ncr);
+// Each pair row's weight for the weighted modes, row_w[row] for the rows
+// of centres [0, centres): the distance function of the neighbour's
+// distance (w0 for the centre's own image under the zero shift) times its
+// species weight (soap_weight, soap.cpp:389-420).  Uses the graph, position,
+// weighting and species-weight fields of a.
+void launch_block_row_weights(hipStream_t stream, const BlockArgs& a, int64_t centres, double* row_w);
 // Zero the rows of the structures without atoms (structure averages; the
 // expansion writes only the rows of structures it visits).
 void launch_block_zero_rows(hipStream_t stream, const int64_t* struct_offsets, int64_t structures, void* out,

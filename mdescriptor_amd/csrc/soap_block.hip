@@ -561,9 +561,10 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
         uint32_t bin;   // bin of the lane's slot row (slot < rows)
         int64_t row;    // output row (centre, or structure)
         int catom;      // species-major: centre (atom) of the lane's slot
+        double w;       // weighted modes: weight of the lane's slot row
     };
     auto next_stage = [&]() -> Stage {
-        Stage s{-1, 0, 0, 0, false, false, 0u, 0, 0};
+        Stage s{-1, 0, 0, 0, false, false, 0u, 0, 0, 0.0};
         if constexpr (kSpeciesMajor) {
             if (sm_base >= sm_total) {
                 if (st_more == 0) {
@@ -624,7 +625,11 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
         s.groups = (n + GS - 1) / GS;
         // pad slots load the chunk's last row (a centre always has its own
         // row, so row 0 of the graph exists for an empty chunk)
-        if constexpr (kHarm) s.bin = a.pair_bin[n > 0 ? st_row + min(lane / 2, n - 1) : 0];
+        if constexpr (kHarm) {
+            const int64_t slot_row = n > 0 ? st_row + min(lane / 2, n - 1) : 0;
+            s.bin = a.pair_bin[slot_row];
+            if constexpr (kWeighted) s.w = a.row_w[slot_row];
+        }
         st_row = uniform64(st_row + n);
         st_left = __builtin_amdgcn_readfirstlane(st_left - n);
         s.ends = st_left == 0 && st_more == 0;
@@ -837,21 +842,12 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
     Stage s1 = next_stage(); // chunk k + 1 (harmonics)
     double px = 0.0, py = 0.0, pz = 0.0;
     double qx = 0.0, qy = 0.0, qz = 0.0; // species-major: the slot's centre
-    int patom = -1;                      // weights with w0: the slot's image's atom, -1 unless the
-                                         // image has the zero shift
     const int jj = lane / 2, comp = lane % 2;
     auto load_positions = [&](const Stage& s) {
         if constexpr (kHarm) {
             px = a.bx[s.bin];
             py = a.by[s.bin];
             pz = a.bz[s.bin];
-            if constexpr (kWeighted) {
-                if (a.has_w0 != 0) {
-                    const ImageDesc& image = a.images[a.bin_image[s.bin]];
-                    const bool zero = image.n[0] == 0 && image.n[1] == 0 && image.n[2] == 0;
-                    patom = zero ? a.bin_atom[s.bin] : -1;
-                }
-            }
             if constexpr (kSpeciesMajor) {
                 qx = a.positions[3 * static_cast<int64_t>(s.catom)];
                 qy = a.positions[3 * static_cast<int64_t>(s.catom) + 1];
@@ -870,15 +866,8 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
             if (comp == 0) s_d2[buf * kNb + jj] = real ? d2 : 0.0;
         }
         double seed = real ? 1.0 : 0.0;
-        if constexpr (kWeighted) {
-            // the neighbour's weight (soap_weight, soap.cpp:389-420); w0 for
-            // the exact self pair, the centre's own atom under the zero shift
-            // (NeighborView::exact_self, neighbor.cpp:683-689)
-            const double r2 = fma(dz, dz, fma(dx, dx, dy * dy));
-            double w = weight_function(a.weighting, a.w_r0, a.w_c, a.w_d, a.w_m, sqrt(r2));
-            if (a.has_w0 != 0 && static_cast<int64_t>(patom) == uniform64(s.centre)) w = a.w_w0;
-            seed = real ? w * a.species_w[__builtin_amdgcn_readfirstlane(s.q)] : 0.0;
-        }
+        // the neighbour's weight, computed per row before the expansion
+        if constexpr (kWeighted) seed = real ? s.w : 0.0;
         harmonic_columns<LM, MLO, MHI>(dx, dy, dz, seed, comp, s_y + buf * PL::YWORDS + jj);
     };
 
@@ -1022,13 +1011,14 @@ __device__ __forceinline__ void block_role(const BlockArgs& a, double* lds, cons
 // or (summed coefficients) the registers
 constexpr int ps_tiles(int ncr, bool summed) { return summed ? ncr : ncr * (ncr + 1) / 2; }
 
-// Five wavefronts per SIMD (96 VGPRs); four for the weighted rows, whose
-// distance function (pow) needs the registers of a fifth, and for mu1nu1,
-// whose summed coefficients stay live beside the registers
+// Five wavefronts per SIMD (96 VGPRs); four for mu1nu1, whose summed
+// coefficients stay live beside the registers, and for outer averages in
+// LDS (their row in LDS allows four workgroups a CU at most; with five the
+// l_max 6 shape spills).  The weighted modes read each row's weight, so
+// they keep five.
 template <int LM, int KG, int NCR, int ES, int MODE>
 __global__ __launch_bounds__(256) __attribute__((
-    amdgpu_waves_per_eu(MODE == kBlockRowsWeighted || MODE == kBlockInnerRunsWeighted || MODE == kBlockRowsSummed ? 4
-                                                                                                           : 5))) void
+    amdgpu_waves_per_eu(MODE == kBlockRowsSummed || MODE == kBlockOuterLds ? 4 : 5))) void
 k_soap_block(BlockArgs a) {
     using PL = BlockPlan<LM, KG>;
     // staging buffers, d2, exp table, padded S_lm table, power-spectrum
@@ -1342,6 +1332,36 @@ void launch_block_expand(hipStream_t stream, int l_max, int kg, int ncr, const B
 
 namespace {
 
+// a wavefront per centre, its rows lane by lane; the distance as the
+// expansion's harmonic staging forms it (image - centre, fma order)
+__global__ __launch_bounds__(256) void k_block_row_weights(BlockArgs a, int64_t centres, double* row_w) {
+    const int lane = threadIdx.x % kWaveThreads;
+    const int64_t waves = static_cast<int64_t>(gridDim.x) * (blockDim.x / kWaveThreads);
+    for (int64_t c = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWaveThreads) + threadIdx.x / kWaveThreads;
+         c < centres; c += waves) {
+        int total = 0;
+        for (int t = 0; t < a.S; ++t) total += a.counts[c * a.S + t];
+        const int64_t row0 = a.pair_start[c];
+        const double cx = a.positions[3 * c], cy = a.positions[3 * c + 1], cz = a.positions[3 * c + 2];
+        for (int r = lane; r < total; r += kWaveThreads) {
+            const int64_t row = row0 + r;
+            const uint32_t b = a.pair_bin[row];
+            const double dx = a.bx[b] - cx, dy = a.by[b] - cy, dz = a.bz[b] - cz;
+            const double r2 = fma(dz, dz, fma(dx, dx, dy * dy));
+            // soap_weight (soap.cpp:389-420); w0 for the exact self pair, the
+            // centre's own atom under the zero shift (NeighborView::exact_self,
+            // neighbor.cpp:683-689)
+            double w = weight_function(a.weighting, a.w_r0, a.w_c, a.w_d, a.w_m, sqrt(r2));
+            if (a.has_w0 != 0) {
+                const ImageDesc& image = a.images[a.bin_image[b]];
+                const bool zero = image.n[0] == 0 && image.n[1] == 0 && image.n[2] == 0;
+                if (zero && static_cast<int64_t>(a.bin_atom[b]) == c) w = a.w_w0;
+            }
+            row_w[row] = w * a.species_w[a.bin_type[b]];
+        }
+    }
+}
+
 // one workgroup per structure without atoms; its row's bytes zeroed
 __global__ void k_block_zero_rows(const int64_t* struct_offsets, int64_t structures, char* out, int64_t pitch,
                                   int64_t row_bytes) {
@@ -1353,6 +1373,14 @@ __global__ void k_block_zero_rows(const int64_t* struct_offsets, int64_t structu
 }
 
 } // namespace
+
+void launch_block_row_weights(hipStream_t stream, const BlockArgs& a, int64_t centres, double* row_w) {
+    if (centres <= 0) return;
+    const unsigned grid =
+        static_cast<unsigned>(std::min<int64_t>((centres + 3) / 4, 32 * static_cast<int64_t>(device_compute_units())));
+    hipLaunchKernelGGL(k_block_row_weights, dim3(grid), dim3(256), 0, stream, a, centres, row_w);
+    MDX_HIP(hipGetLastError());
+}
 
 void launch_block_zero_rows(hipStream_t stream, const int64_t* struct_offsets, int64_t structures, void* out,
                             int64_t pitch, int64_t row_bytes) {
