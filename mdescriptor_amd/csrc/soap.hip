@@ -594,7 +594,8 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
         tab.images = pb.d_images.as<ImageDesc>();
         const int tt = mfma_template_tiles(p.tiles);
         BlockArgs block_args{};
-        if (events != nullptr) MDX_HIP(hipEventRecord(events[2], stream));
+        // (the weight pass counts with the graph's time: the expansion's
+        // events bracket its own launches only)
         if (d_row_w != nullptr) {
             BlockArgs wa{};
             wa.positions = pb.d_positions.as<double>();
@@ -619,6 +620,7 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
             wa.images = pb.d_images.as<ImageDesc>();
             launch_block_row_weights(stream, wa, pb.atoms, d_row_w);
         }
+        if (events != nullptr) MDX_HIP(hipEventRecord(events[2], stream));
         for (int64_t base = 0; base < items; base += slice) {
             if (cancel != nullptr && *cancel != 0) throw Error(MDX_CANCELLED, "descriptor computation was cancelled");
             const int64_t count = std::min(slice, items - base);

@@ -1332,8 +1332,11 @@ void launch_block_expand(hipStream_t stream, int l_max, int kg, int ncr, const B
 
 namespace {
 
-// a wavefront per centre, its rows lane by lane; the distance as the
+// a wavefront per centre, kRowsPerLane of its rows per lane at a time: every
+// row's loads are issued before any weight is formed, so the gathers of
+// the batch of rows are in flight together; the distance as the
 // expansion's harmonic staging forms it (image - centre, fma order)
+constexpr int kRowsPerLane = 4;
 __global__ __launch_bounds__(256) void k_block_row_weights(BlockArgs a, int64_t centres, double* row_w) {
     const int lane = threadIdx.x % kWaveThreads;
     const int64_t waves = static_cast<int64_t>(gridDim.x) * (blockDim.x / kWaveThreads);
@@ -1343,21 +1346,38 @@ __global__ __launch_bounds__(256) void k_block_row_weights(BlockArgs a, int64_t 
         for (int t = 0; t < a.S; ++t) total += a.counts[c * a.S + t];
         const int64_t row0 = a.pair_start[c];
         const double cx = a.positions[3 * c], cy = a.positions[3 * c + 1], cz = a.positions[3 * c + 2];
-        for (int r = lane; r < total; r += kWaveThreads) {
-            const int64_t row = row0 + r;
-            const uint32_t b = a.pair_bin[row];
-            const double dx = a.bx[b] - cx, dy = a.by[b] - cy, dz = a.bz[b] - cz;
-            const double r2 = fma(dz, dz, fma(dx, dx, dy * dy));
-            // soap_weight (soap.cpp:389-420); w0 for the exact self pair, the
-            // centre's own atom under the zero shift (NeighborView::exact_self,
-            // neighbor.cpp:683-689)
-            double w = weight_function(a.weighting, a.w_r0, a.w_c, a.w_d, a.w_m, sqrt(r2));
-            if (a.has_w0 != 0) {
-                const ImageDesc& image = a.images[a.bin_image[b]];
-                const bool zero = image.n[0] == 0 && image.n[1] == 0 && image.n[2] == 0;
-                if (zero && static_cast<int64_t>(a.bin_atom[b]) == c) w = a.w_w0;
+        for (int base = 0; base < total; base += kRowsPerLane * kWaveThreads) {
+            uint32_t bin[kRowsPerLane];
+            double px[kRowsPerLane], py[kRowsPerLane], pz[kRowsPerLane];
+#pragma unroll
+            for (int i = 0; i < kRowsPerLane; ++i) {
+                const int r = base + i * kWaveThreads + lane;
+                bin[i] = r < total ? a.pair_bin[row0 + r] : a.pair_bin[row0];
             }
-            row_w[row] = w * a.species_w[a.bin_type[b]];
+#pragma unroll
+            for (int i = 0; i < kRowsPerLane; ++i) {
+                px[i] = a.bx[bin[i]];
+                py[i] = a.by[bin[i]];
+                pz[i] = a.bz[bin[i]];
+            }
+#pragma unroll
+            for (int i = 0; i < kRowsPerLane; ++i) {
+                const int r = base + i * kWaveThreads + lane;
+                if (r >= total) continue;
+                const uint32_t b = bin[i];
+                const double dx = px[i] - cx, dy = py[i] - cy, dz = pz[i] - cz;
+                const double r2 = fma(dz, dz, fma(dx, dx, dy * dy));
+                // soap_weight (soap.cpp:389-420); w0 for the exact self pair,
+                // the centre's own atom under the zero shift
+                // (NeighborView::exact_self, neighbor.cpp:683-689)
+                double v = weight_function(a.weighting, a.w_r0, a.w_c, a.w_d, a.w_m, sqrt(r2));
+                if (a.has_w0 != 0) {
+                    const ImageDesc& image = a.images[a.bin_image[b]];
+                    const bool zero = image.n[0] == 0 && image.n[1] == 0 && image.n[2] == 0;
+                    if (zero && static_cast<int64_t>(a.bin_atom[b]) == c) v = a.w_w0;
+                }
+                row_w[row0 + r] = v * a.species_w[a.bin_type[b]];
+            }
         }
     }
 }
