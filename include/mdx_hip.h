@@ -109,8 +109,9 @@ typedef struct mdx_soap_params {
 /* Per-stage device times of the last run, from HIP events recorded on the
  * context's stream around each stage. */
 typedef struct mdx_timing {
-    double graph_ms;     /* cell binning + neighbour count/scan/fill (kernel 1); weighted plans on the
-                            register-coefficient kernel: and the per-row weight pass */
+    double graph_ms;     /* cell binning + neighbour count/scan/fill (kernel 1), and what the
+                            expansion needs beside it (item tables; the per-row weight pass of
+                            weighted plans on the register-coefficient kernel) */
     double expansion_ms; /* per-centre expansion + power spectrum + write (kernels 2-4) */
     double finalize_ms;  /* structure-level average reductions (kernel 4), 0 if off */
     double total_ms;     /* first to last event of the device pipeline */
