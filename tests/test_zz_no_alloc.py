@@ -208,3 +208,28 @@ def test_noalloc_slot_overflow_matches_device_run(context):
                 np.testing.assert_array_equal(rows, expected)
         finally:
             plan.close()
+
+
+@pytest.mark.parametrize("average", ["off", "inner"])
+def test_noalloc_weighted_plan_matches_device_run(context, average):
+    """A weighted plan (pow with w0): the per-row weights of the
+    register-coefficient kernel sit in the static array beside the graph and
+    the partial rows."""
+
+    from test_oracle_vs_reference import option_arguments
+
+    work = workloads.config(2, "small")
+    p = work.params
+    alphas, betas = basis_gto(p["r_cut"], p["n_max"], p["l_max"])
+    options = option_arguments("pow_w0", p["species"], p["r_cut"], p["n_max"])
+    plan = _hip.SoapPlan(context, species=p["species"], n_max=p["n_max"], l_max=p["l_max"], r_cut=p["r_cut"],
+                         sigma=1.0, alphas=alphas, betas=betas, average=average, dtype="float64", options=options)
+    try:
+        for batch in (work.batch, _smaller(work.batch)):
+            print(f"weighted {average}: {len(batch.numbers)} atoms", flush=True)
+            expected, reference = _run(context, plan, batch, "mdx_hip_soap_run")
+            rows, timing = _run(context, plan, batch, "mdx_hip_soap_run_noalloc")
+            np.testing.assert_array_equal(rows, expected)
+            assert timing.expansion_tiles == reference.expansion_tiles <= -1000
+    finally:
+        plan.close()
