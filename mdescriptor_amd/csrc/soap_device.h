@@ -326,14 +326,31 @@ __device__ inline void power_spectrum_tiles(const double* s_c, const int* loff, 
 
 constexpr double kPi = 3.141592653589793238462643383279502884;
 
+// x^m: a whole exponent of at most 32 in magnitude by binary powering (at
+// most ten products, for the usual 2 to 12 a few), any other through pow
+__device__ inline double weight_power(double x, double m) {
+    const double whole = rint(m);
+    if (whole != m || fabs(m) > 32.0) return pow(x, m);
+    int e = static_cast<int>(fabs(m));
+    double base = x, result = 1.0;
+    while (e != 0) {
+        if (e & 1) result *= base;
+        e >>= 1;
+        if (e != 0) base *= base;
+    }
+    return m < 0.0 ? 1.0 / result : result;
+}
+
 // Distance function of a neighbour's weight (soap_weight, soap.cpp:389-420):
 // 1 poly, c (1 + 2x^3 - 3x^2)^m for x = r / r0 <= 1, else 0; 2 pow,
 // c / (d + x^m); 3 exp, c / (d + e^-x); 0 none (1).
 __device__ inline double weight_function(int kind, double r0, double c, double d, double m, double distance) {
     if (kind == 0) return 1.0;
     const double ratio = distance / r0;
-    if (kind == 1) return distance > r0 ? 0.0 : c * pow(1.0 + 2.0 * ratio * ratio * ratio - 3.0 * ratio * ratio, m);
-    if (kind == 2) return c / (d + pow(ratio, m));
+    if (kind == 1) {
+        return distance > r0 ? 0.0 : c * weight_power(1.0 + 2.0 * ratio * ratio * ratio - 3.0 * ratio * ratio, m);
+    }
+    if (kind == 2) return c / (d + weight_power(ratio, m));
     return c / (d + exp(-ratio));
 }
 
