@@ -215,7 +215,11 @@ int mdx_hip_soap_run(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, mdx_device_bat
  * batch whose scratch does not fit returns MDX_INVALID_ARGUMENT with a message
  * that names the maximum.  All contexts on one device share its array, which
  * keeps the last call's contents: calls that overlap on one device (through
- * different contexts; one context serialises its own calls) race. */
+ * different contexts; one context serialises its own calls) race.  Frames
+ * still queued on the batch by mdx_hip_soap_run_frame are settled first, as
+ * by mdx_hip_batch_wait, which allocates if one of them overflowed its slot:
+ * call mdx_hip_batch_wait beforehand to keep the call itself free of
+ * allocation. */
 int mdx_hip_soap_run_noalloc(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, mdx_device_batch* batch,
                              void* out_device, int64_t out_pitch_bytes, const volatile int32_t* cancel_flag,
                              mdx_timing* timing);
