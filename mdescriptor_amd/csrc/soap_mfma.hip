@@ -228,27 +228,24 @@ __device__ void polynomial_radial_regs(const double* s_r, double* s_g, const dou
 #pragma unroll
                 for (int u = 0; u < 2; ++u) {
 #pragma unroll
-                    for (int g = 0; g < kPolyGroups; ++g) {
-                        if (g < KG) acc[0][g] = mfma4(a_before[u], bb[u][g], acc[0][g]);
-                    }
+                    for (int g = 0; g < kPolyGroups; ++g) acc[0][g] = mfma4(a_before[u], bb[u][g], acc[0][g]);
                 }
 #pragma unroll
                 for (int l = 1; l < kPolyDegrees; ++l) {
-                    if (l < L) {
+                    // every degree and radial group, without a branch: the
+                    // sums of degrees past L are never stored, and groups
+                    // past KG meet a zero basis
 #pragma unroll
-                        for (int u = 0; u < 2; ++u) {
-                            double value = a_last[u];
-                            if (l >= 2) {
-                                const double next = a_before[u] - a_pref[u] * (4.0 * l - 2.0) * a_last[u];
-                                value = a_centre[u] ? 0.0 : (next > 0.0 ? next : 0.0);
-                                a_before[u] = a_last[u];
-                                a_last[u] = value;
-                            }
-#pragma unroll
-                            for (int g = 0; g < kPolyGroups; ++g) {
-                                if (g < KG) acc[l][g] = mfma4(value, bb[u][g], acc[l][g]);
-                            }
+                    for (int u = 0; u < 2; ++u) {
+                        double value = a_last[u];
+                        if (l >= 2) {
+                            const double next = a_before[u] - a_pref[u] * (4.0 * l - 2.0) * a_last[u];
+                            value = a_centre[u] ? 0.0 : (next > 0.0 ? next : 0.0);
+                            a_before[u] = a_last[u];
+                            a_last[u] = value;
                         }
+#pragma unroll
+                        for (int g = 0; g < kPolyGroups; ++g) acc[l][g] = mfma4(value, bb[u][g], acc[l][g]);
                     }
                 }
             }
