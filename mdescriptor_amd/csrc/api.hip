@@ -1038,7 +1038,9 @@ int mdx_hip_soap_run_frame(mdx_hip_ctx* ctx, const mdx_soap_plan* plan, mdx_devi
         settle(ctx, batch);
         MDX_HIP(hipStreamWaitEvent(s, batch->ready[k], 0));
         check_cancel(cancel_flag);
-        mdx::run_soap(s, *plan, pb, graph, out_device, out_pitch_bytes, partials, cancel_flag, nullptr, nullptr);
+        // (a weighted plan's per-row weight pass goes behind the graph on gs)
+        mdx::run_soap(s, *plan, pb, graph, out_device, out_pitch_bytes, partials, cancel_flag, nullptr, nullptr, 0,
+                      nullptr, gs, batch->ready[k]);
         MDX_HIP(hipEventRecord(batch->done[k], s));
         batch->queued[k] = true;
         batch->pending = k;

@@ -535,8 +535,13 @@ using SliceHook = std::function<void(int64_t first_row, int64_t rows)>;
 // Run the SOAP kernels (2-4) of a plan over a prepared batch whose graph is
 // built; output rows x features in device memory with the given pitch.
 // slice (0: the default) bounds the centres per expansion launch.
+// weight_stream (pipelined frames: the stream that built the graph) takes
+// the per-row weight pass of weighted plans, which then runs beside the
+// previous frame's expansion; weight_ready is recorded behind it and
+// stream waits for it.
 void run_soap(hipStream_t stream, const mdx_soap_plan& plan, PreparedBatch& pb,
               const DeviceGraph& graph, void* out_device, int64_t pitch_bytes, DeviceBuffer& partials,
               const volatile int32_t* cancel, hipEvent_t* events, mdx_timing* timing, int64_t slice = 0,
-              const SliceHook* on_slice = nullptr);
+              const SliceHook* on_slice = nullptr, hipStream_t weight_stream = nullptr,
+              hipEvent_t weight_ready = nullptr);
 } // namespace mdx

@@ -382,7 +382,8 @@ void dispatch_hpt(int hpt, hipStream_t stream, dim3 grid, size_t lds, const mdx_
 
 void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, const DeviceGraph& g,
               void* out_device, int64_t pitch_bytes, DeviceBuffer& partials, const volatile int32_t* cancel,
-              hipEvent_t* events, mdx_timing* timing, int64_t slice_items, const SliceHook* on_slice) {
+              hipEvent_t* events, mdx_timing* timing, int64_t slice_items, const SliceHook* on_slice,
+              hipStream_t weight_stream, hipEvent_t weight_ready) {
     SoapDims d{};
     d.S = p.S;
     d.n = p.n;
@@ -618,7 +619,15 @@ void run_soap(hipStream_t stream, const mdx_soap_plan& p, PreparedBatch& pb, con
             wa.bin_image = g.bin_image.as<int32_t>();
             wa.bin_type = g.bin_type.as<int32_t>();
             wa.images = pb.d_images.as<ImageDesc>();
-            launch_block_row_weights(stream, wa, pb.atoms, d_row_w);
+            if (weight_stream != nullptr && weight_ready != nullptr) {
+                // behind the graph on its own stream (it reads only the
+                // graph, the positions and the plan)
+                launch_block_row_weights(weight_stream, wa, pb.atoms, d_row_w);
+                MDX_HIP(hipEventRecord(weight_ready, weight_stream));
+                MDX_HIP(hipStreamWaitEvent(stream, weight_ready, 0));
+            } else {
+                launch_block_row_weights(stream, wa, pb.atoms, d_row_w);
+            }
         }
         if (events != nullptr) MDX_HIP(hipEventRecord(events[2], stream));
         for (int64_t base = 0; base < items; base += slice) {

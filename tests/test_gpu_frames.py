@@ -379,22 +379,51 @@ def test_pipelined_frames_equal_synchronous_runs(hip_context, oracle, case, aver
         plan.close()
 
 
+WEIGHTED_FRAMES = {"weighting": {"function": "pow", "r0": 2.5, "c": 1.0, "d": 1.0, "m": 2.0, "w0": 0.5}}
+
+
+@pytest.mark.parametrize("case", range(len(FRAME_CASES)), ids=[c[0] for c in FRAME_CASES])
+@pytest.mark.parametrize("average,dtype", [("off", "float64"), ("inner", "float64"), ("off", "float32")])
+def test_pipelined_weighted_frames_equal_synchronous_runs(hip_context, oracle, case, average, dtype):
+    """A weighted plan's frames queued back to back (each frame's per-row
+    weight pass queued behind its graph, beside the previous frame's
+    expansion) give the rows of one synchronous run per frame, bit for bit;
+    the last frame is also checked against the oracle."""
+
+    name, batch, params = FRAME_CASES[case]
+    plan, basis = _plan(hip_context, params, average, dtype, WEIGHTED_FRAMES)
+    base = np.asarray(batch.positions, np.float64)
+    frames = [base, *_frames(batch, 91 + case), base - 0.01]
+    try:
+        expected = _sequential(plan, batch, frames)
+        got = _pipelined(plan, batch, frames, device_frames=(1,))
+        for k, (rows, want) in enumerate(zip(got, expected)):
+            np.testing.assert_array_equal(rows, want, err_msg=f"{name} {average} {dtype} frame {k}")
+        last = _oracle_soap(oracle, _moved(batch, frames[-1]), params, basis, average, WEIGHTED_FRAMES)
+        assert scaled_error(got[-1], last) <= _gate(dtype)
+    finally:
+        plan.close()
+
+
+@pytest.mark.parametrize("options", ["default", "weighted"])
 @pytest.mark.parametrize("average", ["off", "outer"])
-def test_pipelined_frames_with_slot_overflow(hip_context, oracle, average):
+def test_pipelined_frames_with_slot_overflow(hip_context, oracle, average, options):
     """Both buffer sets start with slots smaller than a centre's rows: the
-    first frame on each overflows and is built again inside the call."""
+    first frame on each overflows and is built again inside the call (a
+    weighted plan's weights computed again for the larger slots)."""
 
     batch = _two_dense_clusters()
-    plan, basis = _plan(hip_context, OVERFLOW_PARAMS, average, "float64")
+    chosen = OVERFLOW_PLANS[options]
+    plan, basis = _plan(hip_context, OVERFLOW_PARAMS, average, "float64", chosen)
     base = np.asarray(batch.positions, np.float64)
     rng = np.random.default_rng(5)
     frames = [base + rng.normal(0.0, 0.02, base.shape) for _ in range(4)]
     try:
         got = _pipelined(plan, batch, frames)
         for k, positions in enumerate(frames):
-            expected = _oracle_soap(oracle, _moved(batch, positions), OVERFLOW_PARAMS, basis, average)
+            expected = _oracle_soap(oracle, _moved(batch, positions), OVERFLOW_PARAMS, basis, average, chosen)
             error = scaled_error(got[k], expected)
-            assert error <= F64_GATE, f"{average} frame {k}: scaled error {error:.3e}"
+            assert error <= F64_GATE, f"{average} {options} frame {k}: scaled error {error:.3e}"
     finally:
         plan.close()
 
