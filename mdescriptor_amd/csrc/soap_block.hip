@@ -1369,9 +1369,11 @@ __global__ __launch_bounds__(256) void k_block_row_weights(BlockArgs a, int64_t 
                 const double r2 = fma(dz, dz, fma(dx, dx, dy * dy));
                 // soap_weight (soap.cpp:389-420); w0 for the exact self pair,
                 // the centre's own atom under the zero shift
-                // (NeighborView::exact_self, neighbor.cpp:683-689)
+                // (NeighborView::exact_self, neighbor.cpp:683-689).  Such an
+                // image is the position plus a zero vector, so its r2 is 0
+                // exactly: only rows at r2 == 0 gather the atom and shift
                 double v = weight_function(a.weighting, a.w_r0, a.w_c, a.w_d, a.w_m, sqrt(r2));
-                if (a.has_w0 != 0) {
+                if (a.has_w0 != 0 && r2 == 0.0) {
                     const ImageDesc& image = a.images[a.bin_image[b]];
                     const bool zero = image.n[0] == 0 && image.n[1] == 0 && image.n[2] == 0;
                     if (zero && static_cast<int64_t>(a.bin_atom[b]) == c) v = a.w_w0;
